@@ -1,0 +1,211 @@
+/*
+ * rce_qmm.h -- C ABI of the MI355X (gfx950) GGUF block-quantized matmul
+ * library (librce_qmm.so).
+ *
+ * Drop-in replacement for the quantized-matmul operator of the reference's
+ * compute substrate (openIE-dev/rce, compute/crates/rce-op-qmm).  Plain
+ * pointers and sizes only; no exceptions cross this boundary.  Every entry
+ * point returns an rce_qmm_status; the text of the last failure on the
+ * calling thread is available from rce_qmm_last_error(), the convention of
+ * compute/crates/rce-c/include/rce.h (RceStatus + rce_last_error).
+ *
+ * Numerics.  Three modes:
+ *   RCE_QMM_MODE_EXACT     f32 activations, the reference's own operation
+ *                          order (one binary32 rounding per op, no fused
+ *                          multiply-add in the reference's arithmetic).
+ *                          Bit-identical to rce_op_qmm::mm_1d / mm_batched
+ *                          for finite inputs.
+ *   RCE_QMM_MODE_Q8        activations quantized once per row to Q8 blocks
+ *                          of 32 (nn.rs quantize_block semantics), exact
+ *                          int32 block dot products, then the reference's
+ *                          per-block formula and fold order.  Deterministic;
+ *                          differs from EXACT by the activation rounding.
+ *   RCE_QMM_MODE_F16_MFMA  (matmul / grouped experts) weights dequantized to
+ *                          binary16 tiles and contracted on the matrix cores
+ *                          with f32 accumulation in a fixed order.
+ * Every mode is run-to-run bit-identical: no floating-point atomics, fixed
+ * reduction trees.
+ *
+ * Threading.  A context owns one HIP stream on one device.  Calls on one
+ * context are serialized by the caller (like the reference's per-thread
+ * adapter, rce-tinyllama/src/lib.rs L196-239); use one context per thread.
+ * Host-pointer entry points are synchronous on return.  The *_dev entry
+ * points are asynchronous on the stream they are given (NULL = the
+ * context's stream).
+ */
+#ifndef RCE_QMM_H
+#define RCE_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RCE_QMM_ABI_VERSION 1u
+
+typedef enum rce_qmm_status {
+    RCE_QMM_OK = 0,
+    RCE_QMM_NULL_ARGUMENT = 1,
+    RCE_QMM_BAD_SHAPE = 2,
+    RCE_QMM_UNSUPPORTED_DTYPE = 3,
+    RCE_QMM_NO_DEVICE = 4,
+    RCE_QMM_HIP_ERROR = 5,
+    RCE_QMM_OUT_OF_MEMORY = 6,
+    RCE_QMM_INTERNAL = 7
+} rce_qmm_status;
+
+/* GGUF type tags, as GgufDtype::to_u32 (rce-ingest-gguf/src/parser.rs
+ * L343-378).  The library accepts any u32; rce_qmm_supports() says which
+ * it computes on the GPU. */
+enum {
+    RCE_QMM_F32 = 0,
+    RCE_QMM_F16 = 1,
+    RCE_QMM_Q4_0 = 2,
+    RCE_QMM_Q4_1 = 3,
+    RCE_QMM_Q5_0 = 6,
+    RCE_QMM_Q8_0 = 8,
+    RCE_QMM_Q3_K = 11,
+    RCE_QMM_Q4_K = 12,
+    RCE_QMM_Q5_K = 13,
+    RCE_QMM_Q6_K = 14,
+    RCE_QMM_BF16 = 30
+};
+
+typedef enum rce_qmm_mode {
+    RCE_QMM_MODE_EXACT = 0,
+    RCE_QMM_MODE_Q8 = 1,
+    RCE_QMM_MODE_F16_MFMA = 2
+} rce_qmm_mode;
+
+/* Opaque handles. */
+typedef struct rce_qmm_context rce_qmm_context;
+typedef struct rce_qmm_weight rce_qmm_weight;
+
+/* ---- errors / version ------------------------------------------------ */
+
+/* Text of the last failure on this thread ("" if none).  Mirrors
+ * rce_last_error (compute/crates/rce-c/include/rce.h). */
+const char *rce_qmm_last_error(void);
+const char *rce_qmm_status_str(rce_qmm_status s);
+uint32_t rce_qmm_abi_version(void);
+
+/* ---- context ----------------------------------------------------------- */
+
+/* Bind to HIP device `device`, create the context's stream and scratch.
+ * Replaces MetalQmmContext::new (rce-op-qmm-metal/src/lib.rs L46-52):
+ * no GPU -> RCE_QMM_NO_DEVICE (the caller then stays on the CPU path). */
+rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out);
+void rce_qmm_context_destroy(rce_qmm_context *ctx);
+/* The hipStream_t the context launches on, as void*. */
+rce_qmm_status rce_qmm_context_stream(rce_qmm_context *ctx, void **stream);
+/* Wait for all work on the context's stream. */
+rce_qmm_status rce_qmm_synchronize(rce_qmm_context *ctx);
+
+/* 1 if the GPU computes (dtype, n_cols) in `mode`, else 0.  Same role as
+ * MetalQmmContext::supports (rce-op-qmm-metal/src/lib.rs L127-139) and the
+ * cost()=INFINITY decline of format-specific backends
+ * (rce-placement-adapter/src/lib.rs L253-266). */
+int rce_qmm_supports(uint32_t dtype, size_t n_cols, rce_qmm_mode mode);
+
+/* ---- weights ------------------------------------------------------------ */
+
+/* A device-resident QuantWeight made from GGUF bytes: the weight
+ * [n_rows = N_out, n_cols = K_in], row-major, each row k/QK blocks
+ * (rce-op-qmm/src/lib.rs L60-91 QuantWeight, L123-138 from_owned_bytes).
+ * The bytes are copied to HBM once (the library may store them in a
+ * device layout of the same byte count); the caller keeps its buffer.
+ * len must equal n_rows * row_bytes(dtype, n_cols). */
+rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, size_t n_rows,
+                                         size_t n_cols, const uint8_t *bytes, size_t len,
+                                         rce_qmm_weight **out);
+
+/* QuantWeight::sub_view (rce-op-qmm/src/lib.rs L99-118): a view of
+ * byte_len bytes at byte_offset of `w`'s GGUF bytes, read as
+ * [n_rows, n_cols].  Shares the device copy (no HBM copy).  The view must
+ * start on a row boundary of `w` and keep n_cols (the stacked-expert case
+ * of rce-qwen36-moe/src/lib.rs L216-223 split_experts); Q6_K views must
+ * also start on a multiple of 64 rows.  Other views: RCE_QMM_BAD_SHAPE. */
+rce_qmm_status rce_qmm_weight_sub_view(const rce_qmm_weight *w, size_t byte_offset,
+                                       size_t byte_len, size_t n_rows, size_t n_cols,
+                                       rce_qmm_weight **out);
+
+/* Release a weight or view (the device copy is freed with the last one). */
+void rce_qmm_weight_destroy(rce_qmm_weight *w);
+
+/* dtype, shape and GGUF byte length of a weight (QuantWeight fields). */
+rce_qmm_status rce_qmm_weight_info(const rce_qmm_weight *w, uint32_t *dtype, size_t *n_rows,
+                                   size_t *n_cols, size_t *len);
+
+/* ---- drop-in host-pointer entry points (synchronous, EXACT mode) --------- */
+
+/* rce_op_qmm::mm_1d (rce-op-qmm/src/lib.rs L216-270): out[j] = sum_i a[i]
+ * W[j,i] for a[n_cols] f32, out[n_rows] f32, bit-identical to the
+ * reference's scalar kernels.  Unsupported dtype -> RCE_QMM_UNSUPPORTED_DTYPE
+ * (the reference panics, L268; callers fall back to the CPU path). */
+rce_qmm_status rce_qmm_mm_1d(rce_qmm_context *ctx, const float *a, const rce_qmm_weight *w,
+                             float *out);
+
+/* rce_op_qmm::mm_1d_serial (rce-op-qmm/src/lib.rs L281-304): the same
+ * result as mm_1d (the reference differs only in host threading). */
+rce_qmm_status rce_qmm_mm_1d_serial(rce_qmm_context *ctx, const float *a,
+                                    const rce_qmm_weight *w, float *out);
+
+/* rce_op_qmm::mm_batched (rce-op-qmm/src/lib.rs L967-1023): a [t_rows,
+ * n_cols] -> out [t_rows, n_rows], byte-identical to t_rows calls of mm_1d. */
+rce_qmm_status rce_qmm_mm_batched(rce_qmm_context *ctx, const float *a, size_t t_rows,
+                                  const rce_qmm_weight *w, float *out);
+
+/* QuantWeight::dequant_row (rce-op-qmm/src/lib.rs L150-167 ->
+ * rce-ingest-gguf dequant.rs L115-134): row `row` as n_cols f32 values,
+ * bit-identical to dequantize_to_f32. */
+rce_qmm_status rce_qmm_dequant_row(rce_qmm_context *ctx, const rce_qmm_weight *w, size_t row,
+                                   float *out);
+
+/* ---- device-resident entry points (asynchronous on `stream`) ------------ */
+
+/* mm_batched on device buffers: a_dev [t_rows, n_cols] of a_dtype
+ * (RCE_QMM_F32, or RCE_QMM_F16 whose values are widened exactly to f32 as
+ * the reference's callers do), out_dev [t_rows, n_rows] f32.  No host
+ * synchronization; the library's scratch is owned by the context. */
+rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype,
+                                      size_t t_rows, const rce_qmm_weight *w, float *out_dev,
+                                      rce_qmm_mode mode, void *stream);
+
+/* ---- grouped experts (MoE) ----------------------------------------------- */
+
+/* rce_op_moe::moe_router (rce-op-moe/src/lib.rs L35-73) from given router
+ * logits [n_tokens, n_expert] (host): softmax over all experts (max
+ * subtracted, f32 exp), descending sort (ties: lower index first), top_k,
+ * renormalized when `normalize`.  Writes ids/weights [n_tokens, top_k]. */
+rce_qmm_status rce_qmm_moe_router(const float *logits, size_t n_tokens, size_t n_expert,
+                                  size_t top_k, int normalize, int32_t *ids, float *weights);
+
+/* Grouped-expert FFN on device buffers: for every token t and decision j,
+ * e = ids[t, j]: h = silu(W1[e] x_t), y_j = W2[e] h, and
+ * out_t = sum_j weights[t, j] * y_j in decision order from +0.0
+ * (rce-qwen36-moe/src/lib.rs L667-710 with the router of rce-op-moe;
+ * moe_combine L98-110).  w1[e]: [d_ff, d_model], w2[e]: [d_model, d_ff],
+ * all of one dtype.  x_dev [t_rows, d_model] f32, ids_dev [t_rows, top_k]
+ * i32, weights_dev [t_rows, top_k] f32, out_dev [t_rows, d_model] f32.
+ * Tokens are grouped per expert on the device (stable by expert, then
+ * token, then decision). */
+rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *const *w1,
+                                   const rce_qmm_weight *const *w2, size_t n_expert,
+                                   const float *x_dev, size_t t_rows, const int32_t *ids_dev,
+                                   const float *weights_dev, size_t top_k, float *out_dev,
+                                   rce_qmm_mode mode, void *stream);
+
+/* ---- device memory helpers (for callers without a HIP runtime) ---------- */
+
+rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out);
+rce_qmm_status rce_qmm_dev_free(rce_qmm_context *ctx, void *p);
+rce_qmm_status rce_qmm_memcpy_h2d(rce_qmm_context *ctx, void *dst, const void *src, size_t bytes);
+rce_qmm_status rce_qmm_memcpy_d2h(rce_qmm_context *ctx, void *dst, const void *src, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RCE_QMM_H */

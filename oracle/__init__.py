@@ -1,0 +1,273 @@
+"""CPU restatement of the reference's GGUF quantized-matmul path.
+
+TEST INFRASTRUCTURE ONLY.  This package is the parity checker and the CPU
+baseline; only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import it, and never as the thing measured or
+shipped.  The product (``rce_amd``, ``include/``) does not depend on it.
+
+The C source ``qmm_oracle.c`` restates, in the reference's operation
+order, the kernels of ``compute/crates/rce-op-qmm/src/lib.rs``, the
+dequantizers of ``compute/crates/rce-ingest-gguf/src/dequant.rs``, the
+quantizers and value-form products of
+``compute/crates/rce-vm-backend-cpu/src/ml/{nn,kquant}.rs`` and the MoE
+router/combine of ``compute/crates/rce-op-moe/src/lib.rs``; each C function
+cites the file:line it follows.  The reference itself is Rust and cannot be
+built here, so there is no ``oracle/_ref`` build.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_qmm.so")
+
+# GGUF type tags (rce-ingest-gguf/src/parser.rs L306-341).
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 0, 1, 2, 3, 6, 7, 8
+Q3_K, Q4_K, Q5_K, Q6_K, BF16 = 11, 12, 13, 14, 30
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
+         Q5_0: (32, 22), Q8_0: (32, 34), Q3_K: (256, 110), Q4_K: (256, 144),
+         Q5_K: (256, 176), Q6_K: (256, 210)}
+
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle_qmm.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P, S, U32, I, F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, ctypes.c_float
+        sig = {
+            "orc_f16_to_f32": (F, [ctypes.c_uint16]),
+            "orc_round_to_f16": (F, [F]),
+            "orc_f16_bits": (ctypes.c_uint16, [F]),
+            "orc_block_geometry": (I, [U32, P, P]),
+            "orc_tensor_byte_size": (S, [U32, S]),
+            "orc_quantize_block": (None, [P, I, P, P]),
+            "orc_quantize_q8_0_q4_0": (None, [P, S, I, P]),
+            "orc_quantize_k": (None, [P, U32, P, P, P, P, P]),
+            "orc_pack_k": (None, [P, P, P, F, F, U32, P]),
+            "orc_unpack_k": (None, [P, U32, P, P, P, P, P]),
+            "orc_quantize_tensor_k": (None, [P, S, U32, P]),
+            "orc_dequantize": (I, [P, U32, S, P]),
+            "orc_mm_batched": (I, [P, S, P, U32, S, S, P, I]),
+            "orc_mm_1d": (I, [P, P, U32, S, S, P, I]),
+            "orc_matmul_q": (None, [P, S, S, P, S, P, I, P]),
+            "orc_matmul_k": (None, [P, S, S, P, S, P, P, U32, P]),
+            "orc_quantize_act_q8": (None, [P, S, P, P, P]),
+            "orc_mm_batched_q8": (I, [P, S, P, U32, S, S, P, I]),
+            "orc_block_isums": (I, [P, P, U32, S, S, P]),
+            "orc_silu": (F, [F]),
+            "orc_moe_router": (None, [P, S, S, I, P, P]),
+            "orc_moe_combine": (None, [P, P, S, S, P]),
+            "orc_moe_ffn": (I, [P, S, S, S, P, P, U32, P, P, S, P, I]),
+            "orc_max_threads": (I, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().orc_f16_to_f32(int(h)))
+
+
+def round_to_f16(x: float) -> float:
+    return float(lib().orc_round_to_f16(float(x)))
+
+
+def f16_bits(x: float) -> int:
+    return int(lib().orc_f16_bits(float(x)))
+
+
+def row_bytes(dtype: int, n_cols: int) -> int:
+    qk, bb = BLOCK[dtype]
+    return n_cols // qk * bb
+
+
+def tensor_byte_size(dtype: int, n: int) -> int:
+    return int(lib().orc_tensor_byte_size(dtype, n))
+
+
+def quantize_block(x, q4: bool):
+    x = _c(x, np.float32)
+    assert x.size == 32
+    q = np.zeros(32, np.int32)
+    d = np.zeros(1, np.float32)
+    lib().orc_quantize_block(_p(x), int(q4), _p(q), _p(d))
+    return q, float(d[0])
+
+
+def quantize(w, dtype: int) -> np.ndarray:
+    """GGUF bytes of a flat f32 array (rows of n_cols back to back)."""
+    w = _c(w, np.float32).reshape(-1)
+    out = np.zeros(tensor_byte_size(dtype, w.size), np.uint8)
+    if dtype in (Q8_0, Q4_0):
+        assert w.size % 32 == 0
+        lib().orc_quantize_q8_0_q4_0(_p(w), w.size, int(dtype == Q4_0), _p(out))
+    elif dtype in (Q4_K, Q5_K, Q6_K):
+        assert w.size % 256 == 0
+        lib().orc_quantize_tensor_k(_p(w), w.size, dtype, _p(out))
+    else:
+        raise ValueError(f"no quantizer for dtype {dtype}")
+    return out
+
+
+def quantize_k(x, fmt: int):
+    x = _c(x, np.float32)
+    q = np.zeros(256, np.int32); sc = np.zeros(16, np.int32); mn = np.zeros(8, np.int32)
+    d = np.zeros(1, np.float32); dm = np.zeros(1, np.float32)
+    lib().orc_quantize_k(_p(x), fmt, _p(q), _p(sc), _p(mn), _p(d), _p(dm))
+    nsc = 16 if fmt == Q6_K else 8
+    return q, sc[:nsc].copy(), (mn.copy() if fmt != Q6_K else np.zeros(0, np.int32)), float(d[0]), float(dm[0])
+
+
+def pack_k(q, sc, mn, d, dmin, fmt: int) -> np.ndarray:
+    bb = BLOCK[fmt][1]
+    out = np.zeros(bb, np.uint8)
+    sc16 = np.zeros(16, np.int32); sc16[: len(sc)] = sc
+    mn8 = np.zeros(8, np.int32); mn8[: len(mn)] = mn
+    lib().orc_pack_k(_p(_c(q, np.int32)), _p(sc16), _p(mn8), float(d), float(dmin), fmt, _p(out))
+    return out
+
+
+def unpack_k(b, fmt: int):
+    b = _c(b, np.uint8)
+    q = np.zeros(256, np.int32); sc = np.zeros(16, np.int32); mn = np.zeros(8, np.int32)
+    d = np.zeros(1, np.float32); dm = np.zeros(1, np.float32)
+    lib().orc_unpack_k(_p(b), fmt, _p(q), _p(sc), _p(mn), _p(d), _p(dm))
+    nsc = 16 if fmt == Q6_K else 8
+    return q, sc[:nsc].copy(), (mn.copy() if fmt != Q6_K else np.zeros(0, np.int32)), float(d[0]), float(dm[0])
+
+
+def dequantize(b, dtype: int, n: int) -> np.ndarray:
+    b = _c(b, np.uint8)
+    out = np.zeros(n, np.float32)
+    if lib().orc_dequantize(_p(b), dtype, n, _p(out)) != 0:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return out
+
+
+def mm_batched(a, w_bytes, dtype: int, n_rows: int, n_cols: int, threads: int = 0) -> np.ndarray:
+    """Exact-order reference result: out[t, j] for a [t_rows, n_cols]."""
+    a = _c(a, np.float32)
+    t_rows = a.size // n_cols
+    w_bytes = _c(w_bytes, np.uint8)
+    out = np.zeros((t_rows, n_rows), np.float32)
+    rc = lib().orc_mm_batched(_p(a), t_rows, _p(w_bytes), dtype, n_rows, n_cols, _p(out),
+                              threads or max_threads())
+    if rc:
+        raise ValueError(f"orc_mm_batched rc={rc}")
+    return out
+
+
+def mm_1d(a, w_bytes, dtype: int, n_rows: int, n_cols: int, threads: int = 0) -> np.ndarray:
+    return mm_batched(a, w_bytes, dtype, n_rows, n_cols, threads)[0]
+
+
+def mm_batched_q8(a, w_bytes, dtype: int, n_rows: int, n_cols: int, threads: int = 0) -> np.ndarray:
+    """The Q8-activation path restated on the CPU (same definition as the GPU's)."""
+    a = _c(a, np.float32)
+    t_rows = a.size // n_cols
+    w_bytes = _c(w_bytes, np.uint8)
+    out = np.zeros((t_rows, n_rows), np.float32)
+    rc = lib().orc_mm_batched_q8(_p(a), t_rows, _p(w_bytes), dtype, n_rows, n_cols, _p(out),
+                                 threads or max_threads())
+    if rc:
+        raise ValueError(f"orc_mm_batched_q8 rc={rc}")
+    return out
+
+
+def quantize_act_q8(x):
+    x = _c(x, np.float32)
+    k = x.size
+    xq = np.zeros(k, np.int8); dx = np.zeros(k // 32, np.float32); xs = np.zeros(k // 32, np.int32)
+    lib().orc_quantize_act_q8(_p(x), k, _p(xq), _p(dx), _p(xs))
+    return xq, dx, xs
+
+
+def block_isums(xq, w_bytes, dtype: int, n_rows: int, n_cols: int) -> np.ndarray:
+    out = np.zeros((n_rows, n_cols // 32), np.int32)
+    rc = lib().orc_block_isums(_p(_c(xq, np.int8)), _p(_c(w_bytes, np.uint8)), dtype, n_rows, n_cols, _p(out))
+    if rc:
+        raise ValueError("unsupported")
+    return out
+
+
+def matmul_q(x, q, d, q4: bool) -> np.ndarray:
+    x = _c(x, np.float32); q = _c(q, np.int32); d = _c(d, np.float32)
+    m, k = x.shape; n = q.shape[0]
+    out = np.zeros((m, n), np.float32)
+    lib().orc_matmul_q(_p(x), m, k, _p(q), n, _p(d), int(q4), _p(out))
+    return out
+
+
+def matmul_k(x, q, s, o, fmt: int) -> np.ndarray:
+    x = _c(x, np.float32); q = _c(q, np.int32); s = _c(s, np.float32)
+    o = _c(o if o is not None else np.zeros(1, np.float32), np.float32)
+    m, k = x.shape; n = q.shape[0]
+    out = np.zeros((m, n), np.float32)
+    lib().orc_matmul_k(_p(x), m, k, _p(q), n, _p(s), _p(o), fmt, _p(out))
+    return out
+
+
+def silu(x: float) -> float:
+    return float(lib().orc_silu(float(x)))
+
+
+def moe_router(logits, top_k: int, normalize: bool = True):
+    logits = _c(logits, np.float32)
+    idx = np.zeros(top_k, np.int32); w = np.zeros(top_k, np.float32)
+    lib().orc_moe_router(_p(logits), logits.size, top_k, int(normalize), _p(idx), _p(w))
+    return idx, w
+
+
+def moe_combine(w, ys) -> np.ndarray:
+    w = _c(w, np.float32); ys = _c(ys, np.float32)
+    k, d = ys.shape
+    out = np.zeros(d, np.float32)
+    lib().orc_moe_combine(_p(w), _p(ys), k, d, _p(out))
+    return out
+
+
+def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0) -> np.ndarray:
+    x = _c(x, np.float32)
+    t_rows, d_model = x.shape
+    ids = _c(ids, np.int32); gate_w = _c(gate_w, np.float32)
+    top_k = ids.shape[1]
+    w1 = [_c(b, np.uint8) for b in w1_list]; w2 = [_c(b, np.uint8) for b in w2_list]
+    P1 = (ctypes.c_void_p * len(w1))(*[b.ctypes.data for b in w1])
+    P2 = (ctypes.c_void_p * len(w2))(*[b.ctypes.data for b in w2])
+    out = np.zeros((t_rows, d_model), np.float32)
+    rc = lib().orc_moe_ffn(_p(x), t_rows, d_model, d_ff, ctypes.cast(P1, ctypes.c_void_p),
+                           ctypes.cast(P2, ctypes.c_void_p), dtype, _p(ids), _p(gate_w), top_k,
+                           _p(out), threads or max_threads())
+    if rc:
+        raise ValueError(f"orc_moe_ffn rc={rc}")
+    return out

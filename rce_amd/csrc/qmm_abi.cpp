@@ -1,0 +1,508 @@
+// qmm_abi.cpp -- the extern "C" boundary of librce_qmm.so (include/rce_qmm.h).
+//
+// Owns device memory and streams: a context is one device + one HIP stream +
+// scratch; a weight is a device-resident copy of GGUF bytes in the layout
+// its kernels read (same byte count), shared by its sub-views.  No C++
+// exception crosses the ABI; failures set a thread-local message
+// (rce_qmm_last_error), the convention of compute/crates/rce-c/include/rce.h.
+#include "../../include/rce_qmm.h"
+#include "qmm_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+using namespace rce_qmm;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+rce_qmm_status fail(rce_qmm_status s, const std::string &msg) {
+    g_last_error = msg;
+    return s;
+}
+
+rce_qmm_status hip_fail(hipError_t e, const char *what) {
+    return fail(RCE_QMM_HIP_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                       \
+    do {                                                    \
+        hipError_t e_ = (expr);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr);   \
+    } while (0)
+
+bool block_geometry(uint32_t t, size_t &qk, size_t &bb) {
+    switch (t) {
+    case T_F32: qk = 1; bb = 4; return true;
+    case T_F16: case T_BF16: qk = 1; bb = 2; return true;
+    case T_Q4_0: qk = 32; bb = 18; return true;
+    case T_Q4_1: qk = 32; bb = 20; return true;
+    case T_Q5_0: qk = 32; bb = 22; return true;
+    case T_Q8_0: qk = 32; bb = 34; return true;
+    case T_Q3_K: qk = 256; bb = 110; return true;
+    case T_Q4_K: qk = 256; bb = 144; return true;
+    case T_Q5_K: qk = 256; bb = 176; return true;
+    case T_Q6_K: qk = 256; bb = 210; return true;
+    default: return false;
+    }
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// A device allocation shared by a weight and its views.
+struct DevAlloc {
+    void *p = nullptr;
+    int device = 0;
+    ~DevAlloc() {
+        if (p) {
+            int cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(device);
+            (void)hipFree(p);
+            (void)hipSetDevice(cur);
+        }
+    }
+};
+
+// Grow-only device buffer owned by a context.
+struct Scratch {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+}  // namespace
+
+struct rce_qmm_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Scratch a_in, a_f32, out;
+};
+
+struct rce_qmm_weight {
+    std::shared_ptr<DevAlloc> alloc;
+    DevWeight dw{};
+    size_t host_row_bytes = 0;  // GGUF bytes per row
+    size_t len = 0;             // GGUF byte length of this view
+    int device = 0;
+};
+
+namespace {
+
+rce_qmm_status set_device(int dev) {
+    HIP_TRY(hipSetDevice(dev));
+    return RCE_QMM_OK;
+}
+
+// Make `s` hold at least `bytes`; waits for the context's stream before a
+// reallocation so in-flight kernels never see a freed buffer.
+rce_qmm_status ensure(rce_qmm_context *ctx, Scratch &s, size_t bytes, hipStream_t other) {
+    if (s.cap >= bytes) return RCE_QMM_OK;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (other && other != ctx->stream) HIP_TRY(hipStreamSynchronize(other));
+    if (s.p) HIP_TRY(hipFree(s.p));
+    s.p = nullptr;
+    s.cap = 0;
+    size_t cap = align_up(std::max<size_t>(bytes, 4096), 4096);
+    hipError_t e = hipMalloc(&s.p, cap);
+    if (e != hipSuccess) return fail(RCE_QMM_OUT_OF_MEMORY, std::string("scratch hipMalloc: ") + hipGetErrorString(e));
+    s.cap = cap;
+    return RCE_QMM_OK;
+}
+
+// Host-side relayout of GGUF bytes into the device layout of `dw`.
+void relayout(const uint8_t *src, size_t n_rows, size_t n_cols, uint32_t t, const DevWeight &dw,
+              size_t host_row_bytes, uint8_t *dst) {
+    if (dw.layout == LAYOUT_SPLIT) {
+        const size_t nb = n_cols / 32, qb = t == T_Q8_0 ? 32 : 16, bb = qb + 2;
+        for (size_t r = 0; r < n_rows; r++) {
+            const uint8_t *s = src + r * host_row_bytes;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t b = 0; b < nb; b++) {
+                d[2 * b] = s[b * bb];
+                d[2 * b + 1] = s[b * bb + 1];
+                std::memcpy(d + dw.qs_off + b * qb, s + b * bb + 2, qb);
+            }
+        }
+    } else if (dw.layout == LAYOUT_NATIVE) {
+        for (size_t r = 0; r < n_rows; r++)
+            std::memcpy(dst + r * dw.row_stride, src + r * host_row_bytes, host_row_bytes);
+    } else {  // LAYOUT_IL64, Q6_K
+        const size_t nsb = n_cols / 256;
+        for (size_t r = 0; r < n_rows; r++) {
+            const size_t lane = r & 63;
+            uint8_t *g = dst + (r >> 6) * dw.group_stride;
+            for (size_t sb = 0; sb < nsb; sb++) {
+                const uint8_t *s = src + r * host_row_bytes + sb * 210;
+                uint8_t *d = g + sb * IL64_Q6K_SB;
+                for (size_t c = 0; c < 8; c++) std::memcpy(d + IL64_Q6K_QL + (c * 64 + lane) * 16, s + c * 16, 16);
+                for (size_t c = 0; c < 4; c++) std::memcpy(d + IL64_Q6K_QH + (c * 64 + lane) * 16, s + 128 + c * 16, 16);
+                std::memcpy(d + IL64_Q6K_SC + lane * 16, s + 192, 16);
+                std::memcpy(d + IL64_Q6K_D + lane * 2, s + 208, 2);
+            }
+        }
+    }
+}
+
+rce_qmm_status check_weight_ctx(rce_qmm_context *ctx, const rce_qmm_weight *w) {
+    if (!ctx || !w) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight");
+    if (ctx->device != w->device) return fail(RCE_QMM_BAD_SHAPE, "weight lives on another device than the context");
+    return RCE_QMM_OK;
+}
+
+// Device-side core shared by the host and device entry points.
+rce_qmm_status run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype, size_t t_rows,
+                           const rce_qmm_weight *w, float *out_dev, rce_qmm_mode mode, hipStream_t s) {
+    const DevWeight &dw = w->dw;
+    if (!gpu_supports(dw.dtype, dw.n_cols, (int)mode))
+        return fail(RCE_QMM_UNSUPPORTED_DTYPE, "dtype " + std::to_string(dw.dtype) + " with n_cols " +
+                                                   std::to_string(dw.n_cols) + " has no GPU kernel in mode " +
+                                                   std::to_string((int)mode));
+    if (a_dtype != T_F32 && a_dtype != T_F16) return fail(RCE_QMM_UNSUPPORTED_DTYPE, "activations must be F32 or F16");
+    if (t_rows == 0 || dw.n_rows == 0) return RCE_QMM_OK;
+    const size_t k = dw.n_cols;
+    const float *a32 = static_cast<const float *>(a_dev);
+    rce_qmm_status st;
+    if (a_dtype == T_F16) {
+        if ((st = ensure(ctx, ctx->a_f32, t_rows * k * sizeof(float), s))) return st;
+        HIP_TRY(launch_f16_to_f32(static_cast<const uint16_t *>(a_dev), static_cast<float *>(ctx->a_f32.p), t_rows * k, s));
+        a32 = static_cast<const float *>(ctx->a_f32.p);
+    }
+    if (mode == RCE_QMM_MODE_EXACT) {
+        HIP_TRY(launch_gemv_exact(dw, a32, t_rows, out_dev, s));
+        return RCE_QMM_OK;
+    }
+    if (mode == RCE_QMM_MODE_Q8) {
+        HIP_TRY(launch_gemv_q8(dw, a32, t_rows, out_dev, s));
+        return RCE_QMM_OK;
+    }
+    return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
+}
+
+rce_qmm_status host_batched(rce_qmm_context *ctx, const float *a, size_t t_rows, const rce_qmm_weight *w,
+                            float *out) {
+    rce_qmm_status st = check_weight_ctx(ctx, w);
+    if (st) return st;
+    if (!a || !out) return fail(RCE_QMM_NULL_ARGUMENT, "null activation or output");
+    if ((st = set_device(ctx->device))) return st;
+    const DevWeight &dw = w->dw;
+    if (!gpu_supports(dw.dtype, dw.n_cols, RCE_QMM_MODE_EXACT))
+        return fail(RCE_QMM_UNSUPPORTED_DTYPE, "dtype " + std::to_string(dw.dtype) + " with n_cols " +
+                                                   std::to_string(dw.n_cols) + " has no GPU kernel");
+    if (t_rows == 0 || dw.n_rows == 0) return RCE_QMM_OK;
+    const size_t abytes = t_rows * dw.n_cols * sizeof(float), obytes = t_rows * dw.n_rows * sizeof(float);
+    if ((st = ensure(ctx, ctx->a_in, abytes, nullptr))) return st;
+    if ((st = ensure(ctx, ctx->out, obytes, nullptr))) return st;
+    HIP_TRY(hipMemcpyAsync(ctx->a_in.p, a, abytes, hipMemcpyHostToDevice, ctx->stream));
+    if ((st = run_batched(ctx, ctx->a_in.p, T_F32, t_rows, w, static_cast<float *>(ctx->out.p), RCE_QMM_MODE_EXACT,
+                          ctx->stream)))
+        return st;
+    HIP_TRY(hipMemcpyAsync(out, ctx->out.p, obytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return RCE_QMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *rce_qmm_last_error(void) { return g_last_error.c_str(); }
+
+const char *rce_qmm_status_str(rce_qmm_status s) {
+    switch (s) {
+    case RCE_QMM_OK: return "ok";
+    case RCE_QMM_NULL_ARGUMENT: return "null argument";
+    case RCE_QMM_BAD_SHAPE: return "bad shape";
+    case RCE_QMM_UNSUPPORTED_DTYPE: return "unsupported dtype";
+    case RCE_QMM_NO_DEVICE: return "no device";
+    case RCE_QMM_HIP_ERROR: return "hip error";
+    case RCE_QMM_OUT_OF_MEMORY: return "out of memory";
+    case RCE_QMM_INTERNAL: return "internal error";
+    }
+    return "unknown status";
+}
+
+uint32_t rce_qmm_abi_version(void) { return RCE_QMM_ABI_VERSION; }
+
+rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out) {
+    if (!out) return fail(RCE_QMM_NULL_ARGUMENT, "null out");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(RCE_QMM_NO_DEVICE, "no HIP device");
+    if (device < 0 || device >= n) return fail(RCE_QMM_NO_DEVICE, "device index out of range");
+    HIP_TRY(hipSetDevice(device));
+    hipStream_t s = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    rce_qmm_context *c = new (std::nothrow) rce_qmm_context();
+    if (!c) {
+        (void)hipStreamDestroy(s);
+        return fail(RCE_QMM_OUT_OF_MEMORY, "context allocation");
+    }
+    c->device = device;
+    c->stream = s;
+    *out = c;
+    return RCE_QMM_OK;
+}
+
+void rce_qmm_context_destroy(rce_qmm_context *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out})
+        if (s->p) (void)hipFree(s->p);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+rce_qmm_status rce_qmm_context_stream(rce_qmm_context *ctx, void **stream) {
+    if (!ctx || !stream) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    *stream = ctx->stream;
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_synchronize(rce_qmm_context *ctx) {
+    if (!ctx) return fail(RCE_QMM_NULL_ARGUMENT, "null context");
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return RCE_QMM_OK;
+}
+
+int rce_qmm_supports(uint32_t dtype, size_t n_cols, rce_qmm_mode mode) {
+    return gpu_supports(dtype, n_cols, (int)mode) ? 1 : 0;
+}
+
+rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, size_t n_rows, size_t n_cols,
+                                         const uint8_t *bytes, size_t len, rce_qmm_weight **out) {
+    if (!ctx || !out || (!bytes && len)) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    size_t qk, bb;
+    if (!block_geometry(dtype, qk, bb)) return fail(RCE_QMM_UNSUPPORTED_DTYPE, "unknown dtype " + std::to_string(dtype));
+    if (n_cols == 0 || n_cols % qk)
+        return fail(RCE_QMM_BAD_SHAPE, "n_cols " + std::to_string(n_cols) + " is not a multiple of the block size " +
+                                           std::to_string(qk));
+    const size_t rowb = n_cols / qk * bb;
+    if (len != n_rows * rowb)
+        return fail(RCE_QMM_BAD_SHAPE, "len " + std::to_string(len) + " != n_rows*row_bytes " + std::to_string(n_rows * rowb));
+    if (!gpu_supports(dtype, n_cols, RCE_QMM_MODE_EXACT))
+        return fail(RCE_QMM_UNSUPPORTED_DTYPE, "dtype " + std::to_string(dtype) + " with n_cols " + std::to_string(n_cols) +
+                                                   " has no GPU kernel");
+    rce_qmm_status st = set_device(ctx->device);
+    if (st) return st;
+
+    DevWeight dw{};
+    dw.dtype = dtype;
+    dw.n_rows = n_rows;
+    dw.n_cols = n_cols;
+    size_t total = 0;
+    if (dtype == T_Q4_0 || dtype == T_Q8_0) {
+        const size_t nb = n_cols / 32, qb = dtype == T_Q8_0 ? 32 : 16;
+        dw.layout = LAYOUT_SPLIT;
+        dw.qs_off = align_up(2 * nb, 16);
+        dw.row_stride = dw.qs_off + qb * nb;
+        total = dw.row_stride * n_rows;
+    } else if (dtype == T_Q6_K) {
+        dw.layout = LAYOUT_IL64;
+        dw.group_stride = (n_cols / 256) * IL64_Q6K_SB;
+        total = dw.group_stride * ((n_rows + 63) / 64);
+    } else {
+        dw.layout = LAYOUT_NATIVE;
+        dw.row_stride = align_up(rowb, 16);
+        total = dw.row_stride * n_rows;
+    }
+    std::vector<uint8_t> host;
+    try {
+        host.assign(std::max<size_t>(total, 1), 0);
+    } catch (...) {
+        return fail(RCE_QMM_OUT_OF_MEMORY, "host staging for relayout");
+    }
+    relayout(bytes, n_rows, n_cols, dtype, dw, rowb, host.data());
+    auto alloc = std::make_shared<DevAlloc>();
+    alloc->device = ctx->device;
+    hipError_t e = hipMalloc(&alloc->p, std::max<size_t>(total, 256));
+    if (e != hipSuccess) {
+        alloc->p = nullptr;
+        return fail(RCE_QMM_OUT_OF_MEMORY, std::string("weight hipMalloc: ") + hipGetErrorString(e));
+    }
+    HIP_TRY(hipMemcpyAsync(alloc->p, host.data(), total, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    dw.base = static_cast<const uint8_t *>(alloc->p);
+    rce_qmm_weight *w = new (std::nothrow) rce_qmm_weight();
+    if (!w) return fail(RCE_QMM_OUT_OF_MEMORY, "weight handle");
+    w->alloc = alloc;
+    w->dw = dw;
+    w->host_row_bytes = rowb;
+    w->len = len;
+    w->device = ctx->device;
+    *out = w;
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_weight_sub_view(const rce_qmm_weight *w, size_t byte_offset, size_t byte_len, size_t n_rows,
+                                       size_t n_cols, rce_qmm_weight **out) {
+    if (!w || !out) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (byte_offset + byte_len > w->len)
+        return fail(RCE_QMM_BAD_SHAPE, "sub_view out of bounds: " + std::to_string(byte_offset) + "+" +
+                                           std::to_string(byte_len) + " > " + std::to_string(w->len));
+    if (n_cols != w->dw.n_cols) return fail(RCE_QMM_BAD_SHAPE, "sub_view must keep n_cols");
+    const size_t rb = w->host_row_bytes;
+    if (rb == 0 || byte_offset % rb || byte_len != n_rows * rb)
+        return fail(RCE_QMM_BAD_SHAPE, "sub_view must cover whole rows of the parent");
+    const size_t row0 = byte_offset / rb;
+    DevWeight dw = w->dw;
+    dw.n_rows = n_rows;
+    if (dw.layout == LAYOUT_IL64) {
+        if (row0 % 64) return fail(RCE_QMM_BAD_SHAPE, "Q6_K sub_view must start on a multiple of 64 rows");
+        dw.base += (row0 / 64) * dw.group_stride;
+    } else {
+        dw.base += row0 * dw.row_stride;
+    }
+    rce_qmm_weight *v = new (std::nothrow) rce_qmm_weight();
+    if (!v) return fail(RCE_QMM_OUT_OF_MEMORY, "weight handle");
+    v->alloc = w->alloc;
+    v->dw = dw;
+    v->host_row_bytes = rb;
+    v->len = byte_len;
+    v->device = w->device;
+    *out = v;
+    return RCE_QMM_OK;
+}
+
+void rce_qmm_weight_destroy(rce_qmm_weight *w) { delete w; }
+
+rce_qmm_status rce_qmm_weight_info(const rce_qmm_weight *w, uint32_t *dtype, size_t *n_rows, size_t *n_cols,
+                                   size_t *len) {
+    if (!w) return fail(RCE_QMM_NULL_ARGUMENT, "null weight");
+    if (dtype) *dtype = w->dw.dtype;
+    if (n_rows) *n_rows = w->dw.n_rows;
+    if (n_cols) *n_cols = w->dw.n_cols;
+    if (len) *len = w->len;
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_mm_1d(rce_qmm_context *ctx, const float *a, const rce_qmm_weight *w, float *out) {
+    return host_batched(ctx, a, 1, w, out);
+}
+
+rce_qmm_status rce_qmm_mm_1d_serial(rce_qmm_context *ctx, const float *a, const rce_qmm_weight *w, float *out) {
+    return host_batched(ctx, a, 1, w, out);
+}
+
+rce_qmm_status rce_qmm_mm_batched(rce_qmm_context *ctx, const float *a, size_t t_rows, const rce_qmm_weight *w,
+                                  float *out) {
+    return host_batched(ctx, a, t_rows, w, out);
+}
+
+rce_qmm_status rce_qmm_dequant_row(rce_qmm_context *ctx, const rce_qmm_weight *w, size_t row, float *out) {
+    rce_qmm_status st = check_weight_ctx(ctx, w);
+    if (st) return st;
+    if (!out) return fail(RCE_QMM_NULL_ARGUMENT, "null output");
+    if (row >= w->dw.n_rows) return fail(RCE_QMM_BAD_SHAPE, "row out of range");
+    if ((st = set_device(ctx->device))) return st;
+    const size_t bytes = w->dw.n_cols * sizeof(float);
+    if ((st = ensure(ctx, ctx->out, bytes, nullptr))) return st;
+    HIP_TRY(launch_dequant_row(w->dw, row, static_cast<float *>(ctx->out.p), ctx->stream));
+    HIP_TRY(hipMemcpyAsync(out, ctx->out.p, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype, size_t t_rows,
+                                      const rce_qmm_weight *w, float *out_dev, rce_qmm_mode mode, void *stream) {
+    rce_qmm_status st = check_weight_ctx(ctx, w);
+    if (st) return st;
+    if ((!a_dev || !out_dev) && t_rows) return fail(RCE_QMM_NULL_ARGUMENT, "null device buffer");
+    if ((st = set_device(ctx->device))) return st;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    return run_batched(ctx, a_dev, a_dtype, t_rows, w, out_dev, mode, s);
+}
+
+rce_qmm_status rce_qmm_moe_router(const float *logits, size_t n_tokens, size_t n_expert, size_t top_k,
+                                  int normalize, int32_t *ids, float *weights) {
+    if (!logits || !ids || !weights) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    if (n_expert == 0 || top_k == 0 || top_k > n_expert) return fail(RCE_QMM_BAD_SHAPE, "need 0 < top_k <= n_expert");
+    std::vector<float> probs(n_expert);
+    std::vector<int32_t> order(n_expert);
+    for (size_t t = 0; t < n_tokens; t++) {
+        const float *l = logits + t * n_expert;
+        // rce-op-moe/src/lib.rs L50-55: max-subtracted softmax over all experts.
+        float mx = -INFINITY;
+        for (size_t e = 0; e < n_expert; e++) mx = std::fmax(mx, l[e]);
+        for (size_t e = 0; e < n_expert; e++) probs[e] = std::exp(l[e] - mx);
+        float sum = 0.0f;
+        for (size_t e = 0; e < n_expert; e++) sum += probs[e];
+        if (sum > 0.0f)
+            for (size_t e = 0; e < n_expert; e++) probs[e] /= sum;
+        // L57-62: descending order, keep top_k (ties: lower index first).
+        for (size_t e = 0; e < n_expert; e++) order[e] = (int32_t)e;
+        std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return probs[a] > probs[b]; });
+        float s = 0.0f;
+        for (size_t j = 0; j < top_k; j++) {
+            ids[t * top_k + j] = order[j];
+            weights[t * top_k + j] = probs[order[j]];
+        }
+        // L64-67: renormalize the kept weights.
+        if (normalize) {
+            for (size_t j = 0; j < top_k; j++) s += weights[t * top_k + j];
+            if (s > 0.0f)
+                for (size_t j = 0; j < top_k; j++) weights[t * top_k + j] /= s;
+        }
+    }
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *const *w1,
+                                   const rce_qmm_weight *const *w2, size_t n_expert, const float *x_dev,
+                                   size_t t_rows, const int32_t *ids_dev, const float *weights_dev, size_t top_k,
+                                   float *out_dev, rce_qmm_mode mode, void *stream) {
+    (void)w1; (void)w2; (void)n_expert; (void)x_dev; (void)t_rows; (void)ids_dev; (void)weights_dev;
+    (void)top_k; (void)out_dev; (void)mode; (void)stream;
+    if (!ctx) return fail(RCE_QMM_NULL_ARGUMENT, "null context");
+    return fail(RCE_QMM_UNSUPPORTED_DTYPE, "grouped-expert FFN is not built yet");
+}
+
+rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out) {
+    if (!ctx || !out) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    rce_qmm_status st = set_device(ctx->device);
+    if (st) return st;
+    hipError_t e = hipMalloc(out, std::max<size_t>(bytes, 1));
+    if (e != hipSuccess) return fail(RCE_QMM_OUT_OF_MEMORY, std::string("hipMalloc: ") + hipGetErrorString(e));
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_dev_free(rce_qmm_context *ctx, void *p) {
+    if (!ctx) return fail(RCE_QMM_NULL_ARGUMENT, "null context");
+    if (!p) return RCE_QMM_OK;
+    rce_qmm_status st = set_device(ctx->device);
+    if (st) return st;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(p));
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_memcpy_h2d(rce_qmm_context *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || ((!dst || !src) && bytes)) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    rce_qmm_status st = set_device(ctx->device);
+    if (st) return st;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return RCE_QMM_OK;
+}
+
+rce_qmm_status rce_qmm_memcpy_d2h(rce_qmm_context *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || ((!dst || !src) && bytes)) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    rce_qmm_status st = set_device(ctx->device);
+    if (st) return st;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return RCE_QMM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,84 @@
+"""The C-ABI library loads, exports every symbol include/rce_qmm.h declares,
+and its host-only logic behaves (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rce_amd
+from rce_amd import _lib
+from conftest import ROOT, gpu_available
+
+HEADER = os.path.join(ROOT, "include", "rce_qmm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rce_qmm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), f"{n} missing from {_lib.LIB_PATH}"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures drift from the header"
+
+
+def test_abi_version_and_status_strings():
+    L = _lib.lib()
+    assert L.rce_qmm_abi_version() == 1
+    assert L.rce_qmm_status_str(0) == b"ok"
+    assert L.rce_qmm_status_str(3) == b"unsupported dtype"
+
+
+def test_supports_matrix():
+    G, M = rce_amd.GgufDtype, rce_amd.Mode
+    assert rce_amd.supports(G.Q4_0, 4096) and rce_amd.supports(G.Q8_0, 4096)
+    assert rce_amd.supports(G.Q4K, 4096) and rce_amd.supports(G.Q6K, 2048)
+    assert rce_amd.supports(G.Q4_0, 4096, M.Q8)
+    assert not rce_amd.supports(G.Q4_0, 4100)        # not a block multiple
+    assert not rce_amd.supports(G.Q4K, 4096 + 32)     # K-quants need 256
+    assert not rce_amd.supports(G.Q5K, 4096)          # no kernel yet -> CPU path
+    assert not rce_amd.supports(99, 4096)
+
+
+@pytest.mark.skipif(gpu_available(), reason="checks the no-device path")
+def test_context_without_device_reports_no_device():
+    with pytest.raises(rce_amd.QmmError) as e:
+        rce_amd.Context(0)
+    assert e.value.status == 4
+
+
+def test_null_arguments_are_rejected():
+    L = _lib.lib()
+    assert L.rce_qmm_context_create(0, None) == 1
+    assert L.rce_qmm_mm_1d(None, None, None, None) == 1
+    assert L.rce_qmm_weight_from_bytes(None, 2, 1, 32, None, 18, None) == 1
+    assert b"null" in L.rce_qmm_last_error()
+
+
+def test_moe_router_matches_oracle_bit_for_bit():
+    # Host-side router of the library vs the oracle's restatement of
+    # rce-op-moe moe_router (both take exp from the platform libm).
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((256, 8)).astype(np.float32)
+    ids, w = rce_amd.moe_router(logits, 2, True)
+    for t in range(256):
+        oi, ow = O.moe_router(logits[t], 2, True)
+        assert list(ids[t]) == list(oi)
+        assert np.array_equal(w[t].view(np.uint32), ow.view(np.uint32))
+    ids1, w1 = rce_amd.moe_router(logits[:4], 3, False)
+    for t in range(4):
+        oi, ow = O.moe_router(logits[t], 3, False)
+        assert list(ids1[t]) == list(oi) and np.array_equal(w1[t], ow)
+
+
+def test_moe_router_rejects_bad_top_k():
+    with pytest.raises(rce_amd.QmmError):
+        rce_amd.moe_router(np.zeros((1, 4), np.float32), 5)

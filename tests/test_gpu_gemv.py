@@ -1,0 +1,170 @@
+"""GPU parity of the decode kernels through the C ABI (librce_qmm.so).
+
+EXACT mode must equal the oracle's restatement of rce_op_qmm::mm_1d /
+mm_batched bit for bit; Q8 mode must equal the oracle's restatement of the
+same Q8-activation algorithm bit for bit (the 1e-5 budget is not needed);
+dequant_row must equal dequantize_to_f32 bit for bit."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rce_amd
+from rce_amd import GgufDtype as G, Mode
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make(rng, dt, n, k, sigma=0.02):
+    w = (rng.standard_normal((n, k)) * sigma).astype(F32)
+    return O.quantize(w, dt)
+
+
+def bits(x):
+    return np.ascontiguousarray(x, F32).view(np.uint32)
+
+
+SHAPES = {
+    # (n_rows, n_cols): small, ragged and the configs' shapes
+    O.Q8_0: [(1, 32), (16, 32), (3, 64), (65, 256), (1000, 2048), (4096, 4096)],
+    O.Q4_0: [(1, 32), (6, 128), (77, 1024), (1024, 2048), (11008, 4096), (4096, 14336)],
+    O.Q4_K: [(1, 256), (5, 512), (130, 2048), (2048, 5632), (4096, 4096)],
+    O.Q6_K: [(1, 256), (64, 256), (100, 512), (256, 2048), (32000, 2048)],
+}
+CASES = [(dt, n, k) for dt, shapes in SHAPES.items() for (n, k) in shapes]
+
+
+@pytest.mark.parametrize("dt,n,k", CASES)
+def test_mm_1d_exact_bit_identical(ctx, dt, n, k):
+    note(f"mm_1d exact dtype={dt} n={n} k={k}")
+    rng = np.random.default_rng(1000 + dt * 7 + n + k)
+    b = make(rng, dt, n, k)
+    a = rng.standard_normal(k).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = rce_amd.mm_1d(a, w)
+    want = O.mm_1d(a, b, dt, n, k)
+    assert np.array_equal(bits(got), bits(want)), f"{np.sum(bits(got) != bits(want))} rows differ"
+    serial = rce_amd.mm_1d_serial(a, w)
+    assert np.array_equal(bits(serial), bits(want))
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("t_rows", [2, 8])
+def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
+    n, k = (700, 2048) if dt != O.Q4_0 else (11008, 4096)
+    note(f"mm_batched exact dtype={dt} t={t_rows} n={n} k={k}")
+    rng = np.random.default_rng(2000 + dt + t_rows)
+    b = make(rng, dt, n, k)
+    x = rng.standard_normal((t_rows, k)).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = rce_amd.mm_batched(x, t_rows, w)
+    want = O.mm_batched(x, b, dt, n, k)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def run_dev(ctx, w, x, mode, a_dtype=G.F32):
+    t_rows = x.shape[0]
+    xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    out = rce_amd.DeviceBuffer(ctx, t_rows * w.n_rows * 4)
+    rce_amd.mm_batched_dev(ctx, xa.ptr, a_dtype, t_rows, w, out.ptr, mode)
+    ctx.synchronize()
+    r = out.download(F32, t_rows * w.n_rows).reshape(t_rows, w.n_rows)
+    xa.free(); out.free()
+    return r
+
+
+Q8_CASES = [(O.Q8_0, 4096, 4096), (O.Q4_0, 11008, 4096), (O.Q4_0, 4096, 14336), (O.Q4_K, 4096, 4096),
+            (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256)]
+
+
+@pytest.mark.parametrize("dt,n,k", Q8_CASES)
+@pytest.mark.parametrize("t_rows", [1, 5, 8])
+def test_q8_path_bit_identical_to_its_restatement(ctx, dt, n, k, t_rows):
+    note(f"q8 dtype={dt} n={n} k={k} t={t_rows}")
+    rng = np.random.default_rng(3000 + dt + n + t_rows)
+    b = make(rng, dt, n, k)
+    x = rng.standard_normal((t_rows, k)).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = run_dev(ctx, w, x, Mode.Q8)
+    want = O.mm_batched_q8(x, b, dt, n, k)
+    assert np.array_equal(bits(got), bits(want))
+    # and it is the reference result up to the activation rounding
+    ex = O.mm_batched(x, b, dt, n, k)
+    assert np.max(np.abs(got - ex)) <= 2e-2 * np.max(np.abs(ex))
+
+
+def test_f16_activations_are_widened_exactly(ctx):
+    rng = np.random.default_rng(4000)
+    n, k, t = 512, 4096, 4
+    b = make(rng, O.Q4_K, n, k)
+    x16 = rng.standard_normal((t, k)).astype(np.float16)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_K, n, k)
+    got = run_dev(ctx, w, x16, Mode.EXACT, a_dtype=G.F16)
+    want = O.mm_batched(x16.astype(F32), b, O.Q4_K, n, k)
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q6_K, 130, 512)])
+def test_dequant_row_bit_identical(ctx, dt, n, k):
+    rng = np.random.default_rng(5000 + dt)
+    b = make(rng, dt, n, k)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    rb = O.row_bytes(dt, k)
+    for row in (0, 1, n // 2, n - 1):
+        got = w.dequant_row(row)
+        want = O.dequantize(b[row * rb:(row + 1) * rb], dt, k)
+        assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("dt", [O.Q4_0, O.Q6_K])
+def test_sub_view_addresses_stacked_experts(ctx, dt):
+    # split_experts (rce-qwen36-moe L216-223): sub_view(e*bpe, bpe, rows, cols)
+    rng = np.random.default_rng(6000 + dt)
+    E, rows, k = 4, 128, 512
+    b = make(rng, dt, E * rows, k)
+    stack = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, E * rows, k)
+    bpe = b.size // E
+    a = rng.standard_normal(k).astype(F32)
+    for e in range(E):
+        v = stack.sub_view(e * bpe, bpe, rows, k)
+        got = rce_amd.mm_1d(a, v)
+        want = O.mm_1d(a, b[e * bpe:(e + 1) * bpe], dt, rows, k)
+        assert np.array_equal(bits(got), bits(want))
+    with pytest.raises(rce_amd.QmmError):
+        stack.sub_view(7, bpe, rows, k)            # not on a row boundary
+    with pytest.raises(rce_amd.QmmError):
+        stack.sub_view(0, b.size + 1, E * rows, k)  # out of bounds
+
+
+def test_runs_are_bit_identical(ctx):
+    rng = np.random.default_rng(7000)
+    n, k = 11008, 4096
+    b = make(rng, O.Q4_0, n, k)
+    x = rng.standard_normal((1, k)).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, n, k)
+    for mode in (Mode.EXACT, Mode.Q8):
+        r1 = run_dev(ctx, w, x, mode)
+        r2 = run_dev(ctx, w, x, mode)
+        assert np.array_equal(bits(r1), bits(r2))
+
+
+def test_errors_and_empty_inputs(ctx):
+    rng = np.random.default_rng(8000)
+    b = make(rng, O.Q4_0, 8, 64)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, 8, 64)
+    assert rce_amd.mm_batched(np.zeros((0, 64), F32), 0, w).shape == (0, 8)
+    with pytest.raises(rce_amd.QmmError) as e:
+        rce_amd.QuantWeight.from_owned_bytes(ctx, b[:-1], O.Q4_0, 8, 64)
+    assert e.value.status == 2
+    with pytest.raises(rce_amd.QmmError) as e:
+        rce_amd.QuantWeight.from_owned_bytes(ctx, np.zeros(176, np.uint8), G.Q5K, 1, 256)
+    assert e.value.status == 3
+    with pytest.raises(rce_amd.QmmError):
+        rce_amd.mm_1d(np.zeros(63, F32), w)

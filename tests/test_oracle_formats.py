@@ -1,0 +1,177 @@
+"""Pins the oracle's binary16 conversions, quantizers, packers and
+dequantizers against the reference's own known answers and against what the
+mathematics fixes (IEEE binary16, round trips).  CPU only."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import lcg_uniform
+
+
+# ---- binary16 ----------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive_against_ieee():
+    # Every binary16 pattern widens exactly (half::f16::to_f32; kquant.rs
+    # half_free L411-425); numpy's float16 is IEEE binary16.
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([O.f16_to_f32(int(b)) for b in bits[::7]], np.float32)
+    w = want[::7]
+    nan = np.isnan(w)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), w[~nan].view(np.uint32))
+
+
+def test_round_to_f16_known_answers():
+    # nn.rs blocks_quantize_as_gguf_does L762-765.
+    assert O.round_to_f16(65519.0) == 65504.0
+    assert np.isinf(O.round_to_f16(65520.0))
+    assert O.round_to_f16(2.0 ** -25) == 0.0
+    assert O.round_to_f16(2.0 ** -24) == 2.0 ** -24
+
+
+def test_round_to_f16_matches_ieee_rne():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(0.02),
+        (rng.standard_normal(5000) * 1e-6).astype(np.float32),   # f16 subnormal range
+        (rng.standard_normal(5000) * 3e4).astype(np.float32),
+        np.array([0.5 + 2 ** -12, 1 + 2 ** -11, 1 + 3 * 2 ** -11, -(1 + 2 ** -11)], np.float32),  # ties
+    ])
+    with np.errstate(over="ignore"):  # values past 65504 round to infinity, as round_to_f16 does
+        want = x.astype(np.float16).astype(np.float32)
+    got = np.array([O.round_to_f16(float(v)) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_f16_bits_inverts_widening():
+    rng = np.random.default_rng(2)
+    bits = rng.integers(0, 1 << 16, 4000).astype(np.uint16)
+    vals = bits.view(np.float16).astype(np.float32)
+    ok = np.isfinite(vals)
+    for b, v in zip(bits[ok], vals[ok]):
+        if v == 0.0:
+            continue  # +0/-0 both map to their own sign bit below
+        assert O.f16_bits(float(v)) == int(b)
+    assert O.f16_bits(0.0) == 0 and O.f16_bits(-0.0) == 0x8000
+
+
+# ---- Q8_0 / Q4_0 quantizer (nn.rs quantize_block) ------------------------------
+
+def test_quantize_block_known_answers():
+    # nn.rs L751-761: x = i - 16.
+    x = np.arange(32, dtype=np.float32) - 16
+    q, d = O.quantize_block(x, False)
+    assert d == O.round_to_f16(np.float32(16.0) / np.float32(127.0))
+    assert q[0] == -127
+    assert q[31] == int(np.round(np.float32(15.0) * np.float32(127.0 / 16.0)))
+    q, d = O.quantize_block(x, True)
+    assert d == 2.0 and q[0] == -8 and q.max() == 7
+
+
+def test_q8_0_q4_0_pack_layout_round_trip():
+    # quantize (toy_gpt2.rs L46-58) then dequantize (dequant.rs L360-454)
+    # reproduces q * d position by position: pins the split-nibble order
+    # (first 16 values = low nibbles, next 16 = high nibbles) and the sign of
+    # the Q8_0 bytes.  A ramp makes every position distinct.
+    x = (np.arange(64, dtype=np.float32) - 31.5) * np.float32(0.37)
+    for dt in (O.Q8_0, O.Q4_0):
+        b = O.quantize(x, dt)
+        assert b.size == O.tensor_byte_size(dt, 64)
+        got = O.dequantize(b, dt, 64)
+        want = []
+        for blk in range(2):
+            q, d = O.quantize_block(x[32 * blk:32 * blk + 32], dt == O.Q4_0)
+            want.extend(np.float32(v) * np.float32(d) for v in q)
+        assert np.array_equal(got, np.array(want, np.float32))
+        # and the values are close to x: |x - q d| <= d (Q8_0: d/2 + rounding)
+        assert np.max(np.abs(got - x)) < 0.37 * 64 / 7
+
+
+def test_dequant_q8_0_const_scale():
+    # dequant.rs L748-760: scale 1.0, byte i = (i*2) as i8.
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    b[2:] = (np.arange(32) * 2).astype(np.int8).view(np.uint8)
+    assert np.array_equal(O.dequantize(b, O.Q8_0, 32), (np.arange(32) * 2).astype(np.int8).astype(np.float32))
+
+
+def test_tensor_byte_size_known_answers():
+    # dequant.rs tests L707-735 and quant.rs estimated_bytes_q4_0 (L295).
+    assert O.tensor_byte_size(O.Q4_K, 256) == 144
+    assert O.tensor_byte_size(O.Q4_K, 512) == 288
+    assert O.tensor_byte_size(O.Q4_0, 32) == 18
+    assert O.tensor_byte_size(O.F32, 100) == 400
+    assert O.tensor_byte_size(O.Q6_K, 256) == 210
+    assert O.tensor_byte_size(O.Q8_0, 4096 * 4096) == 17825792
+    assert O.tensor_byte_size(O.Q4_0, 11008 * 4096) == 25362432
+
+
+# ---- K-quants (kquant.rs quantize_k / pack / unpack, GT-10) ---------------------
+
+KFMTS = [(O.Q4_K, 0), (O.Q5_K, 1), (O.Q6_K, 2)]
+
+
+@pytest.mark.parametrize("fmt,disc", KFMTS)
+def test_k_packing_round_trips_and_values_are_close(fmt, disc):
+    # kquant.rs L425-437: x = lcg(7 + f as u64, 256) * 0.7; pack has the
+    # format's byte count; unpack(pack(b)) == b; values within 0.1 of x.
+    x = lcg_uniform(7 + disc, 256, 0.7)
+    q, sc, mn, d, dmin = O.quantize_k(x, fmt)
+    b = O.pack_k(q, sc, mn, d, dmin, fmt)
+    assert b.size == O.BLOCK[fmt][1]
+    q2, sc2, mn2, d2, dmin2 = O.unpack_k(b, fmt)
+    assert np.array_equal(q, q2) and np.array_equal(sc, sc2) and np.array_equal(mn, mn2)
+    assert d == d2 and dmin == dmin2
+    # KBlock::values (kquant.rs L168-172) equals dequantize_to_f32 of the bytes
+    sub = 16 if fmt == O.Q6_K else 32
+    s = np.array([np.float32(d) * np.float32(c) for c in sc], np.float32)
+    if fmt == O.Q6_K:
+        vals = np.array([s[p // sub] * np.float32(q[p]) for p in range(256)], np.float32)
+    else:
+        o = np.array([np.float32(dmin) * np.float32(c) for c in mn], np.float32)
+        vals = np.array([s[p // sub] * np.float32(q[p]) - o[p // sub] for p in range(256)], np.float32)
+    if fmt != O.Q5_K:
+        assert np.array_equal(O.dequantize(b, fmt, 256), vals)
+    assert np.max(np.abs(vals - x)) < 0.1
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q6_K])
+def test_k_quantizer_ranges_and_scales(fmt):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(256) * 0.02).astype(np.float32)
+    q, sc, mn, d, dmin = O.quantize_k(x, fmt)
+    if fmt == O.Q4_K:
+        assert q.min() >= 0 and q.max() <= 15 and sc.max() <= 63 and mn.max() <= 63
+        assert d == O.round_to_f16(d) and dmin == O.round_to_f16(dmin)
+    else:
+        assert q.min() >= -32 and q.max() <= 31 and sc.min() >= -128 and sc.max() <= 127
+    # the element error is within one quantization step of its sub-block
+    b = O.pack_k(q, sc, mn, d, dmin, fmt)
+    err = np.abs(O.dequantize(b, fmt, 256) - x)
+    assert err.max() < 0.02 * 6
+
+
+def test_q4_k_dequant_layout_groups_of_64():
+    # dequant.rs L546-589: group j of 64 = sc1*low nibbles of qs[32j..] -
+    # min1, then sc2*high nibbles - min2 (the layout the comment at L554-557
+    # says an earlier implementation got wrong).  Distinct q per position.
+    q = np.array([(p * 7 + p // 64) % 16 for p in range(256)], np.int32)
+    sc = np.array([1, 2, 3, 4, 5, 6, 7, 63], np.int32)
+    mn = np.array([0, 1, 2, 3, 60, 61, 62, 63], np.int32)
+    b = O.pack_k(q, sc, mn, 0.5, 0.25, O.Q4_K)
+    v = O.dequantize(b, O.Q4_K, 256)
+    want = np.array([np.float32(0.5 * sc[p // 32]) * np.float32(q[p]) - np.float32(0.25 * mn[p // 32])
+                     for p in range(256)], np.float32)
+    assert np.array_equal(v, want)
+
+
+def test_q6_k_dequant_layout_quartets():
+    # dequant.rs L658-701: per half, l in 0..32 produces positions l, l+32,
+    # l+64, l+96 from ql[l], ql[l+32], qh[l]; scale index (l/16) + 2m.
+    q = np.array([((p * 5) % 64) - 32 for p in range(256)], np.int32)
+    sc = np.arange(16, dtype=np.int32) * 3 - 20
+    b = O.pack_k(q, sc, np.zeros(0, np.int32), 0.125, 0.0, O.Q6_K)
+    v = O.dequantize(b, O.Q6_K, 256)
+    want = np.array([np.float32(0.125 * sc[p // 16]) * np.float32(q[p]) for p in range(256)], np.float32)
+    assert np.array_equal(v, want)
