@@ -116,40 +116,6 @@ rce_qmm_status ensure(rce_qmm_context *ctx, Scratch &s, size_t bytes, hipStream_
     return RCE_QMM_OK;
 }
 
-// Host-side relayout of GGUF bytes into the device layout of `dw`.
-void relayout(const uint8_t *src, size_t n_rows, size_t n_cols, uint32_t t, const DevWeight &dw,
-              size_t host_row_bytes, uint8_t *dst) {
-    if (dw.layout == LAYOUT_SPLIT) {
-        const size_t nb = n_cols / 32, qb = t == T_Q8_0 ? 32 : 16, bb = qb + 2;
-        for (size_t r = 0; r < n_rows; r++) {
-            const uint8_t *s = src + r * host_row_bytes;
-            uint8_t *d = dst + r * dw.row_stride;
-            for (size_t b = 0; b < nb; b++) {
-                d[2 * b] = s[b * bb];
-                d[2 * b + 1] = s[b * bb + 1];
-                std::memcpy(d + dw.qs_off + b * qb, s + b * bb + 2, qb);
-            }
-        }
-    } else if (dw.layout == LAYOUT_NATIVE) {
-        for (size_t r = 0; r < n_rows; r++)
-            std::memcpy(dst + r * dw.row_stride, src + r * host_row_bytes, host_row_bytes);
-    } else {  // LAYOUT_IL64, Q6_K
-        const size_t nsb = n_cols / 256;
-        for (size_t r = 0; r < n_rows; r++) {
-            const size_t lane = r & 63;
-            uint8_t *g = dst + (r >> 6) * dw.group_stride;
-            for (size_t sb = 0; sb < nsb; sb++) {
-                const uint8_t *s = src + r * host_row_bytes + sb * 210;
-                uint8_t *d = g + sb * IL64_Q6K_SB;
-                for (size_t c = 0; c < 8; c++) std::memcpy(d + IL64_Q6K_QL + (c * 64 + lane) * 16, s + c * 16, 16);
-                for (size_t c = 0; c < 4; c++) std::memcpy(d + IL64_Q6K_QH + (c * 64 + lane) * 16, s + 128 + c * 16, 16);
-                std::memcpy(d + IL64_Q6K_SC + lane * 16, s + 192, 16);
-                std::memcpy(d + IL64_Q6K_D + lane * 2, s + 208, 2);
-            }
-        }
-    }
-}
-
 rce_qmm_status check_weight_ctx(rce_qmm_context *ctx, const rce_qmm_weight *w) {
     if (!ctx || !w) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight");
     if (ctx->device != w->device) return fail(RCE_QMM_BAD_SHAPE, "weight lives on another device than the context");
@@ -174,15 +140,9 @@ rce_qmm_status run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_d
         HIP_TRY(launch_f16_to_f32(static_cast<const uint16_t *>(a_dev), static_cast<float *>(ctx->a_f32.p), t_rows * k, s));
         a32 = static_cast<const float *>(ctx->a_f32.p);
     }
-    if (mode == RCE_QMM_MODE_EXACT) {
-        HIP_TRY(launch_gemv_exact(dw, a32, t_rows, out_dev, s));
-        return RCE_QMM_OK;
-    }
-    if (mode == RCE_QMM_MODE_Q8) {
-        HIP_TRY(launch_gemv_q8(dw, a32, t_rows, out_dev, s));
-        return RCE_QMM_OK;
-    }
-    return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
+    if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
+    HIP_TRY(launch_gemv(dw, a32, t_rows, out_dev, (int)mode, s));
+    return RCE_QMM_OK;
 }
 
 rce_qmm_status host_batched(rce_qmm_context *ctx, const float *a, size_t t_rows, const rce_qmm_weight *w,
@@ -300,29 +260,14 @@ rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, s
     dw.dtype = dtype;
     dw.n_rows = n_rows;
     dw.n_cols = n_cols;
-    size_t total = 0;
-    if (dtype == T_Q4_0 || dtype == T_Q8_0) {
-        const size_t nb = n_cols / 32, qb = dtype == T_Q8_0 ? 32 : 16;
-        dw.layout = LAYOUT_SPLIT;
-        dw.qs_off = align_up(2 * nb, 16);
-        dw.row_stride = dw.qs_off + qb * nb;
-        total = dw.row_stride * n_rows;
-    } else if (dtype == T_Q6_K) {
-        dw.layout = LAYOUT_IL64;
-        dw.group_stride = (n_cols / 256) * IL64_Q6K_SB;
-        total = dw.group_stride * ((n_rows + 63) / 64);
-    } else {
-        dw.layout = LAYOUT_NATIVE;
-        dw.row_stride = align_up(rowb, 16);
-        total = dw.row_stride * n_rows;
-    }
+    const size_t total = plan_layout(dw);
     std::vector<uint8_t> host;
     try {
         host.assign(std::max<size_t>(total, 1), 0);
     } catch (...) {
         return fail(RCE_QMM_OUT_OF_MEMORY, "host staging for relayout");
     }
-    relayout(bytes, n_rows, n_cols, dtype, dw, rowb, host.data());
+    relayout_host(bytes, dw, host.data());
     auto alloc = std::make_shared<DevAlloc>();
     alloc->device = ctx->device;
     hipError_t e = hipMalloc(&alloc->p, std::max<size_t>(total, 256));
@@ -358,7 +303,7 @@ rce_qmm_status rce_qmm_weight_sub_view(const rce_qmm_weight *w, size_t byte_offs
     const size_t row0 = byte_offset / rb;
     DevWeight dw = w->dw;
     dw.n_rows = n_rows;
-    if (dw.layout == LAYOUT_IL64) {
+    if (dw.layout == LAYOUT_IL64_Q6_K) {
         if (row0 % 64) return fail(RCE_QMM_BAD_SHAPE, "Q6_K sub_view must start on a multiple of 64 rows");
         dw.base += (row0 / 64) * dw.group_stride;
     } else {

@@ -1,27 +1,34 @@
 // qmm_gemv.hip -- decode-shaped kernels of the GGUF quantized-matmul path for
-// gfx950 (CDNA4): exact-order GEMV, Q8-activation GEMV, activation
-// quantization and row dequantization.
+// gfx950 (CDNA4): GEMV / skinny GEMM in the reference's f32 order (EXACT),
+// the Q8-activation GEMV (Q8), and row dequantization.
 //
-// Two work mappings are used:
-//  * activation-stationary ("AS"): each lane owns one column unit (a Q4_0 /
-//    Q8_0 block of 32, or a Q4_K group of 64) of the activation, keeps that
-//    slice in registers and walks rows.  The wave's loads of one row are
-//    contiguous 16-byte chunks.  Each unit's addend of the row sum goes to
-//    LDS and one lane per row then folds the addends in block order, so the
-//    fold is the reference's sequential `sumf += ...` loop.
-//  * lane-per-row ("LPR", Q6_K): the reference's Q6_K row sum is a single
-//    sequential chain over all positions, so one lane runs one row's chain
-//    and the activation is wave-uniform (scalar registers).  The weight is
-//    stored 64-row interleaved so those per-lane loads are still contiguous
-//    across the wave.
+// Work mapping ("activation-stationary").  A row of the weight is U column
+// units (a Q4_0 / Q8_0 block of 32, a Q4_K group of 64, a Q6_K super-block
+// of 256).  Thread `tid` of a block of NT threads owns unit col = tid % U
+// and the rows rsub, rsub + P, ... (rsub = tid / U, P = NT / U) of the
+// block's tile of RT = P * RPL rows, for TB activation rows (tokens).  It
+// keeps its slice of the activations in registers, issues the loads of all
+// RPL rows before doing any arithmetic, and writes one addend per (token,
+// row) -- the reference's per-unit term of the row sum -- to LDS.  After a
+// barrier, one thread per (token, row) folds the U addends in unit order,
+// which is the reference's sequential `sumf += ...` over blocks.  The
+// device layouts (qmm_internal.h) make every wave-wide weight load a
+// contiguous 1 KB read.
 //
-// Exactness (MODE_EXACT): every + - * of the reference is one binary32
-// operation here in the same order.  The product of a Q4_0 value (n - 8)
-// and an activation a is formed as fma(n, a, -8a): -8a is exact and the fma
-// rounds n*a - 8a = (n-8)*a once, which is the reference's rounded product
-// (likewise fma(u, ds, -32 ds) = (u - 32) * ds for Q6_K).  Everything else
-// is compiled with -ffp-contract=off so no other multiply-add is fused.
+// Exactness (EXACT): every + - * of the reference is one binary32 operation
+// in the same order.  Q4_0's product (n - 8) a is formed as fma(n, a, -8a)
+// when a thread has one token (-8a is exact, the fma rounds (n - 8) a once)
+// and as (float)(n) - 8 (exact) times a otherwise.  All other code is built
+// with -ffp-contract=off.  The Q6_K row sum of the reference is one chain
+// over all positions of the row, so Q6_K EXACT runs one row per lane.
+//
+// Q8: the block quantizes its activation rows into LDS once (4 lanes per
+// block of 32: max |x| by two quad exchanges, then quantize_block(x, false)
+// semantics), every thread copies its units' words to registers, and each
+// per-block sub-sum of the reference becomes dx * (exact int32 dot).
 #include "qmm_internal.h"
+
+#include <type_traits>
 
 namespace rce_qmm {
 namespace {
@@ -60,6 +67,12 @@ __device__ __forceinline__ void load_f32x(const float *p, float *v, int n) {
         v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
 }
+
+// Lane exchanges inside a quad of lanes (DPP quad_perm).
+__device__ __forceinline__ int quad_xor1(int x) { return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int quad_xor2(int x) { return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ float quad_xor1f(float x) { return __int_as_float(quad_xor1(__float_as_int(x))); }
+__device__ __forceinline__ float quad_xor2f(float x) { return __int_as_float(quad_xor2(__float_as_int(x))); }
 
 // Byte i (0..11) of a Q4_K super-block's packed scales, the header being the
 // super-block's first 16 bytes (d, dmin, scales[12]).
@@ -101,269 +114,393 @@ __device__ __forceinline__ void k4_scale_min(const uint4 &h, int j, int &sc, int
 }
 
 // ---------------------------------------------------------------------------
-// Column units, exact mode.
+// Raw unit loads (one row, one column unit) from the device layouts.
 // ---------------------------------------------------------------------------
 
-// Q4_0 block (rce-op-qmm/src/lib.rs L496-522): sub over q in 0..16 of
-// (lo_q - 8) a[q] then (hi_q - 8) a[q+16]; addend = scale * sub.
-struct UnitQ4_0Exact {
-    static constexpr int ACT = 32;
-    float av[32], an[32];
-    struct Raw { uint4 q; uint32_t s; };
-    __device__ void load_act(const float *a, int col) {
-        load_f32x(a + 32 * col, av, 32);
-#pragma unroll
-        for (int i = 0; i < 32; i++) an[i] = -8.0f * av[i];
-    }
-    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        const uint8_t *rp = w.base + row * w.row_stride;
-        Raw r;
-        r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * col);
-        r.q = *reinterpret_cast<const uint4 *>(rp + w.qs_off + 16 * (size_t)col);
-        return r;
-    }
-    __device__ float addend(const Raw &r) const {
-        float sub = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t x = wrd(r.q, i);
-            uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
-#define Q40_STEP(J)                                                                 \
-    sub = sub + __builtin_fmaf(ubyte<J>(lo), av[4 * i + J], an[4 * i + J]);           \
-    sub = sub + __builtin_fmaf(ubyte<J>(hi), av[4 * i + J + 16], an[4 * i + J + 16]);
-            Q40_STEP(0) Q40_STEP(1) Q40_STEP(2) Q40_STEP(3)
-#undef Q40_STEP
-        }
-        return h2f(r.s) * sub;
-    }
-};
+struct RawQ4_0 { uint4 q; uint32_t s; };
+struct RawQ8_0 { uint4 q0, q1; uint32_t s; };
+struct RawQ4_K { uint4 h, q0, q1; };
+struct RawQ6_K { uint4 c[13]; uint32_t d; };
 
-// Q8_0 block (rce-op-qmm/src/lib.rs L315-328, L648-670).
-struct UnitQ8_0Exact {
-    static constexpr int ACT = 32;
-    float av[32];
-    struct Raw { uint4 q0, q1; uint32_t s; };
-    __device__ void load_act(const float *a, int col) { load_f32x(a + 32 * col, av, 32); }
-    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        const uint8_t *rp = w.base + row * w.row_stride;
-        Raw r;
-        r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * col);
-        const uint4 *qp = reinterpret_cast<const uint4 *>(rp + w.qs_off + 32 * (size_t)col);
-        r.q0 = qp[0];
-        r.q1 = qp[1];
-        return r;
-    }
-    __device__ float addend(const Raw &r) const {
-        float sub = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
-#pragma unroll
-            for (int j = 0; j < 4; j++) sub = sub + (float)(int8_t)(x >> (8 * j)) * av[4 * i + j];
-        }
-        return h2f(r.s) * sub;
-    }
-};
-
-// Q4_K group g of a super-block (rce-op-qmm/src/lib.rs L354-385, L730-781):
-// va_lo, a_lo, va_hi, a_hi over l in 0..32 from +0.0, then
-// ((d1 va_lo - min1 a_lo) + d2 va_hi) - min2 a_hi.  The activation sums
-// a_lo, a_hi do not depend on the row and are formed once per lane.
-struct UnitQ4_KExact {
-    static constexpr int ACT = 64;
-    float av[64];
-    float a_lo, a_hi;
-    int g;
-    struct Raw { uint4 h, q0, q1; };
-    __device__ void load_act(const float *a, int col) {
-        load_f32x(a + 64 * col, av, 64);
-        g = col & 3;
-        a_lo = 0.0f; a_hi = 0.0f;
-#pragma unroll
-        for (int l = 0; l < 32; l++) { a_lo = a_lo + av[l]; a_hi = a_hi + av[32 + l]; }
-    }
-    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        const uint8_t *sp = w.base + row * w.row_stride + 144 * (size_t)(col >> 2);
-        Raw r;
-        r.h = *reinterpret_cast<const uint4 *>(sp);
-        const uint4 *qp = reinterpret_cast<const uint4 *>(sp + 16 + 32 * (col & 3));
-        r.q0 = qp[0];
-        r.q1 = qp[1];
-        return r;
-    }
-    __device__ float addend(const Raw &r) const {
-        float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
-        int sc1, m1, sc2, m2;
-        k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
-        float d1 = d * (float)sc1, min1 = dmin * (float)m1;
-        float d2 = d * (float)sc2, min2 = dmin * (float)m2;
-        float va_lo = 0.0f, va_hi = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
-            uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
-#define Q4K_STEP(J)                                               \
-    va_lo = va_lo + ubyte<J>(lo) * av[4 * i + J];                 \
-    va_hi = va_hi + ubyte<J>(hi) * av[32 + 4 * i + J];
-            Q4K_STEP(0) Q4K_STEP(1) Q4K_STEP(2) Q4K_STEP(3)
-#undef Q4K_STEP
-        }
-        float t = d1 * va_lo;
-        t = t - min1 * a_lo;
-        t = t + d2 * va_hi;
-        t = t - min2 * a_hi;
-        return t;
-    }
-};
-
-// ---------------------------------------------------------------------------
-// Column units, Q8-activation mode.  TB activation rows (tokens) per pass.
-// Each lane quantizes the activation blocks it owns straight from f32 (no
-// separate quantization pass); the addends are the exact-mode formulas with
-// each block sub-sum replaced by dx * (exact int32 dot of the block).
-// ---------------------------------------------------------------------------
-
-// nn.rs L541-563 quantize_block(x, false) of one block of 32: d = amax/127,
-// id = 1/d (0 when d = 0), q = round half away from zero of x*id, packed
-// four per word; the scale kept is round_to_f16(d) (nn.rs L521-533, the
-// hardware's round-to-nearest-even conversion).  s_lo / s_hi: sums of the
-// first / last 16 values of q.
-__device__ __forceinline__ void quant_block32(const float *p, int *xq8, float &dx, int &s_lo, int &s_hi) {
-    float v[32];
-    load_f32x(p, v, 32);
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) if (amax < fabsf(v[i])) amax = fabsf(v[i]);
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    s_lo = 0;
-    s_hi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) xq8[i] = 0;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const int qi = (int)roundf(v[i] * id);
-        if (i < 16) s_lo += qi; else s_hi += qi;
-        xq8[i >> 2] |= (int)(((uint32_t)qi & 0xFFu) << (8 * (i & 3)));
-    }
-    dx = (float)(_Float16)d;
+__device__ __forceinline__ RawQ4_0 ld_q4_0(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ4_0 r;
+    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    return r;
 }
 
+__device__ __forceinline__ RawQ8_0 ld_q8_0(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ8_0 r;
+    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
+    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    return r;
+}
+
+__device__ __forceinline__ RawQ4_K ld_q4_k(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ4_K r;
+    r.h = *reinterpret_cast<const uint4 *>(rp + 16 * (size_t)(col >> 2));
+    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
+    return r;
+}
+
+// Q6_K super-block sb of row `row` (LAYOUT_IL64_Q6_K: chunk c of rows
+// r..r+63 contiguous, so a wave of 64 rows reads 1 KB per chunk).
+__device__ __forceinline__ void ld_q6_k(const DevWeight &w, size_t row, int sb, RawQ6_K &r) {
+    const uint8_t *sp = w.base + (row >> 6) * w.group_stride + (size_t)sb * IL64_Q6K_SB;
+    const size_t lane = row & 63;
+#pragma unroll
+    for (int j = 0; j < 13; j++) r.c[j] = *reinterpret_cast<const uint4 *>(sp + ((size_t)j * 64 + lane) * 16);
+    r.d = *reinterpret_cast<const uint16_t *>(sp + IL64_Q6K_D + lane * 2);
+}
+
+// The four 6-bit value words (+32 offset, one byte per l) of positions
+// l..l+3 (m = 0), +32 (m = 1), +64 (m = 2), +96 (m = 3) of half o,
+// l = 4 * lq (rce-op-qmm/src/lib.rs L425-454 bit layout: ql = c[0..7],
+// qh = c[8..11]).
+__device__ __forceinline__ void q6_words(const RawQ6_K &b, int o, int lq, uint32_t &u1, uint32_t &u2,
+                                         uint32_t &u3, uint32_t &u4) {
+    const int c = lq >> 2, wi = lq & 3;
+    const uint32_t qa = wrd(b.c[4 * o + c], wi), qb = wrd(b.c[4 * o + 2 + c], wi);
+    const uint32_t qh = wrd(b.c[8 + 2 * o + c], wi);
+    u1 = (qa & NIB) | ((qh & 0x03030303u) << 4);
+    u2 = (qb & NIB) | ((qh & 0x0C0C0C0Cu) << 2);
+    u3 = ((qa >> 4) & NIB) | (qh & 0x30303030u);
+    u4 = ((qb >> 4) & NIB) | ((qh >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ int q6_sc(const uint4 &s, int i) {
+    return (int)(int8_t)((wrd(s, i >> 2) >> (8 * (i & 3))) & 0xFFu);
+}
+
+// ---------------------------------------------------------------------------
+// Q8 activations in LDS: per token t, xq words [k/4], dx [k/32] (the block
+// scale round_to_f16(amax/127)), s16 [k/16] (sums of xq over 16 values).
+// ---------------------------------------------------------------------------
+
+struct ActLds {
+    int *xq;
+    float *dx;
+    int *s16;
+    __device__ ActLds(unsigned char *lds, size_t k, int tb) {
+        xq = reinterpret_cast<int *>(lds);
+        dx = reinterpret_cast<float *>(lds + (size_t)tb * k);
+        s16 = reinterpret_cast<int *>(lds + (size_t)tb * k + (size_t)tb * (k / 32) * 4);
+    }
+};
+
+__host__ __device__ constexpr size_t act_lds_bytes(size_t k, int tb) { return (size_t)tb * (k + k / 8 + k / 4); }
+
+// Round half away from zero (f32::round / C roundf) of |v| <= 2^22, as an
+// integer: v + copysign(pred(0.5), v) in round-to-nearest-even, truncated.
+// Identical to roundf for every finite f32 in that range (checked
+// exhaustively on the CPU, tests/test_round_identity.py); 3 instructions
+// instead of roundf's 6.
+__device__ __forceinline__ int round_half_away(float v) {
+    return (int)(v + __builtin_copysignf(0x1.fffffep-2f, v));
+}
+
+// One task = 8 consecutive activation values of one token; four
+// consecutive tasks (one lane quad) form a block of 32.
+struct QuantTask {
+    float4 v0, v1;
+};
+
+__device__ __forceinline__ void quant_task_load(const float *A, int kq, int t0, int total, int task, QuantTask &q) {
+    // kq = k / 8 tasks per token.  Out-of-range tasks load task 0 (always
+    // valid), so the loads stay unconditional; they come in whole quads
+    // (total is a multiple of 4) and quant_task_finish writes nothing for
+    // them, so their values never reach a valid block.
+    const int tk = task < total ? task : 0;
+    const int t = tk / kq, e = (tk - t * kq) * 8;
+    const float4 *p = reinterpret_cast<const float4 *>(A + (size_t)(t0 + t) * ((size_t)kq * 8) + e);
+    q.v0 = p[0];
+    q.v1 = p[1];
+}
+
+// nn.rs L541-563 quantize_block(x, false) of the quad's block: d = amax/127,
+// id = 1/d (0 when d = 0), q = round half away from zero of x*id; the scale
+// kept is round_to_f16(d) (nn.rs L521-533 = the hardware's RNE conversion).
+// Every lane of the wave must call this (quad exchanges).
+__device__ __forceinline__ void quant_task_finish(const QuantTask &q, size_t k, int total, int task, const ActLds &L) {
+    float v[8] = {q.v0.x, q.v0.y, q.v0.z, q.v0.w, q.v1.x, q.v1.y, q.v1.z, q.v1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, quad_xor1f(amax));
+    amax = fmaxf(amax, quad_xor2f(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int w0 = 0, w1 = 0, s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int qi = round_half_away(v[i] * id);  // |v * id| <= 127
+        s += qi;
+        if (i < 4) w0 |= (int)(((uint32_t)qi & 0xFFu) << (8 * i));
+        else w1 |= (int)(((uint32_t)qi & 0xFFu) << (8 * (i - 4)));
+    }
+    s += quad_xor1(s);  // the sum over this lane's half-block of 16
+    if (task < total) {
+        const size_t e = (size_t)task * 8;  // token-major: t*k + position
+        *reinterpret_cast<int2 *>(L.xq + e / 4) = make_int2(w0, w1);
+        if ((task & 1) == 0) L.s16[e / 16] = s;
+        if ((task & 3) == 0) L.dx[e / 32] = (float)(_Float16)d;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Column units.  TB = tokens per thread.  init_*: the thread's activation
+// slice; addends(raw, out): out[t] = the reference's per-unit term of
+// row sum of token t.
+// ---------------------------------------------------------------------------
+
+// Q4_0 block, EXACT (rce-op-qmm/src/lib.rs L496-522): sub over q in 0..16
+// of (lo_q - 8) a[q] then (hi_q - 8) a[q+16]; addend = scale * sub.
 template <int TB>
-struct UnitQ4_0Q8 {
+struct Q4_0Exact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_0;
+    float av[TB][32];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // Tokens past tv read token 0's slice (no branch: a load inside
+            // a branch is waited for before the branch joins); their sums
+            // are never folded or stored.
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float sub[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) sub[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = wrd(r.q, i);
+            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float nl = (float)((lo >> (8 * j)) & 0xFFu), nh = (float)((hi >> (8 * j)) & 0xFFu);
+                if constexpr (TB == 1) {
+                    sub[0] = sub[0] + __builtin_fmaf(nl, av[0][4 * i + j], -8.0f * av[0][4 * i + j]);
+                    sub[0] = sub[0] + __builtin_fmaf(nh, av[0][4 * i + j + 16], -8.0f * av[0][4 * i + j + 16]);
+                } else {
+                    const float vl = nl - 8.0f, vh = nh - 8.0f;  // exact
+#pragma unroll
+                    for (int t = 0; t < TB; t++) {
+                        sub[t] = sub[t] + vl * av[t][4 * i + j];
+                        sub[t] = sub[t] + vh * av[t][4 * i + j + 16];
+                    }
+                }
+            }
+        }
+        const float scale = h2f(r.s);
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
+    }
+};
+
+// Q8_0 block, EXACT (rce-op-qmm/src/lib.rs L315-328, L648-670).
+template <int TB>
+struct Q8_0Exact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ8_0;
+    float av[TB][32];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q8_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // Tokens past tv read token 0's slice (no branch: a load inside
+            // a branch is waited for before the branch joins); their sums
+            // are never folded or stored.
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float sub[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) sub[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float v = (float)(int8_t)(x >> (8 * j));
+#pragma unroll
+                for (int t = 0; t < TB; t++) sub[t] = sub[t] + v * av[t][4 * i + j];
+            }
+        }
+        const float scale = h2f(r.s);
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
+    }
+};
+
+// Q4_K group g of a super-block, EXACT (rce-op-qmm/src/lib.rs L354-385,
+// L730-781): va_lo, a_lo, va_hi, a_hi over l in 0..32 from +0.0, then
+// ((d1 va_lo - min1 a_lo) + d2 va_hi) - min2 a_hi.  a_lo and a_hi do not
+// depend on the row and are formed once per thread, in the same order.
+template <int TB>
+struct Q4_KExact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_K;
+    float av[TB][64];
+    float a_lo[TB], a_hi[TB];
+    int g;
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_k(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+        g = col & 3;
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // Tokens past tv read token 0's slice (no branch: a load inside
+            // a branch is waited for before the branch joins); their sums
+            // are never folded or stored.
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 64 * (size_t)col, av[t], 64);
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            a_lo[t] = 0.0f;
+            a_hi[t] = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 32; l++) { a_lo[t] = a_lo[t] + av[t][l]; a_hi[t] = a_hi[t] + av[t][32 + l]; }
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        int sc1, m1, sc2, m2;
+        k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
+        const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+        const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+        float va_lo[TB], va_hi[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) { va_lo[t] = 0.0f; va_hi[t] = 0.0f; }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float vl = (float)((lo >> (8 * j)) & 0xFFu), vh = (float)((hi >> (8 * j)) & 0xFFu);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    va_lo[t] = va_lo[t] + vl * av[t][4 * i + j];
+                    va_hi[t] = va_hi[t] + vh * av[t][32 + 4 * i + j];
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            float s = d1 * va_lo[t];
+            s = s - min1 * a_lo[t];
+            s = s + d2 * va_hi[t];
+            s = s - min2 * a_hi[t];
+            out[t] = s;
+        }
+    }
+};
+
+// Q4_0 / Q8_0 block, Q8: sub = dx * isum, addend = scale * sub.
+template <int TB, bool IS_Q4>
+struct Q32Q8 {
+    static constexpr int NTOK = TB;
+    using Raw = typename std::conditional<IS_Q4, RawQ4_0, RawQ8_0>::type;
     int xq[TB][8];
     float dx[TB];
     int xs[TB];
-    struct Raw { uint4 q; uint32_t s; };
-    __device__ void load_act(const float *A, size_t k, int t0, int tv, int col) {
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
+        if constexpr (IS_Q4) return ld_q4_0(w, row, col);
+        else return ld_q8_0(w, row, col);
+    }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
-            if (t < tv) {
-                int lo, hi;
-                quant_block32(A + (t0 + t) * k + 32 * (size_t)col, xq[t], dx[t], lo, hi);
-                xs[t] = lo + hi;
-            }
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 32 * (size_t)col) / 4);
+            const int4 a = p[0], b = p[1];
+            const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) xq[t][i] = ok ? v[i] : 0;
+            dx[t] = ok ? L.dx[tt * (k / 32) + col] : 0.0f;
+            xs[t] = ok ? L.s16[tt * (k / 16) + 2 * col] + L.s16[tt * (k / 16) + 2 * col + 1] : 0;
         }
     }
-    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        const uint8_t *rp = w.base + row * w.row_stride;
-        Raw r;
-        r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * col);
-        r.q = *reinterpret_cast<const uint4 *>(rp + w.qs_off + 16 * (size_t)col);
-        return r;
-    }
     __device__ void addends(const Raw &r, float *out) const {
-        int lo[4], hi[4];
+        const float scale = h2f(r.s);
+        if constexpr (IS_Q4) {
+            int lo[4], hi[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) { lo[i] = (int)(wrd(r.q, i) & NIB); hi[i] = (int)((wrd(r.q, i) >> 4) & NIB); }
-        float scale = h2f(r.s);
+            for (int i = 0; i < 4; i++) { lo[i] = (int)(wrd(r.q, i) & NIB); hi[i] = (int)((wrd(r.q, i) >> 4) & NIB); }
 #pragma unroll
-        for (int t = 0; t < TB; t++) {
-            int acc = 0;
+            for (int t = 0; t < TB; t++) {
+                int acc = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(lo[i], xq[t][i], acc, false);
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(lo[i], xq[t][i], acc, false);
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(hi[i], xq[t][4 + i], acc, false);
-            int isum = acc - 8 * xs[t];
-            float sub = dx[t] * (float)isum;
-            out[t] = scale * sub;
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(hi[i], xq[t][4 + i], acc, false);
+                const float sub = dx[t] * (float)(acc - 8 * xs[t]);
+                out[t] = scale * sub;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                int acc = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4((int)wrd(r.q0, i), xq[t][i], acc, false);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4((int)wrd(r.q1, i), xq[t][4 + i], acc, false);
+                const float sub = dx[t] * (float)acc;
+                out[t] = scale * sub;
+            }
         }
     }
 };
 
+// Q4_K group, Q8: va = dx * isum, a = dx * (sum of xq); then the EXACT
+// group formula.
 template <int TB>
-struct UnitQ8_0Q8 {
-    int xq[TB][8];
-    float dx[TB];
-    struct Raw { uint4 q0, q1; uint32_t s; };
-    __device__ void load_act(const float *A, size_t k, int t0, int tv, int col) {
-#pragma unroll
-        for (int t = 0; t < TB; t++) {
-            if (t < tv) {
-                int lo, hi;
-                quant_block32(A + (t0 + t) * k + 32 * (size_t)col, xq[t], dx[t], lo, hi);
-            }
-        }
-    }
-    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        const uint8_t *rp = w.base + row * w.row_stride;
-        Raw r;
-        r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * col);
-        const uint4 *qp = reinterpret_cast<const uint4 *>(rp + w.qs_off + 32 * (size_t)col);
-        r.q0 = qp[0];
-        r.q1 = qp[1];
-        return r;
-    }
-    __device__ void addends(const Raw &r, float *out) const {
-        float scale = h2f(r.s);
-#pragma unroll
-        for (int t = 0; t < TB; t++) {
-            int acc = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4((int)wrd(r.q0, i), xq[t][i], acc, false);
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4((int)wrd(r.q1, i), xq[t][4 + i], acc, false);
-            float sub = dx[t] * (float)acc;
-            out[t] = scale * sub;
-        }
-    }
-};
-
-template <int TB>
-struct UnitQ4_KQ8 {
+struct Q4_KQ8 {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_K;
     int xl[TB][8], xh[TB][8];
     float dl[TB], dh[TB];
     int sl[TB], sh[TB];
     int g;
-    using Raw = UnitQ4_KExact::Raw;
-    __device__ void load_act(const float *A, size_t k, int t0, int tv, int col) {
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_k(w, row, col); }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
         g = col & 3;
 #pragma unroll
         for (int t = 0; t < TB; t++) {
-            if (t < tv) {
-                // the activation blocks of sub-blocks 2g and 2g+1
-                const float *p = A + (t0 + t) * k + 64 * (size_t)col;
-                int a, b;
-                quant_block32(p, xl[t], dl[t], a, b);
-                sl[t] = a + b;
-                quant_block32(p + 32, xh[t], dh[t], a, b);
-                sh[t] = a + b;
-            }
+            // tokens past tv read token 0's slice and are zeroed (no branch)
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 64 * (size_t)col) / 4);
+            const int4 a = p[0], b = p[1], c = p[2], e = p[3];
+            const int v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) { xl[t][i] = ok ? v[i] : 0; xh[t][i] = ok ? v[8 + i] : 0; }
+            const size_t b32 = tt * (k / 32) + 2 * (size_t)col, b16 = tt * (k / 16) + 4 * (size_t)col;
+            dl[t] = ok ? L.dx[b32] : 0.0f;
+            dh[t] = ok ? L.dx[b32 + 1] : 0.0f;
+            sl[t] = ok ? L.s16[b16] + L.s16[b16 + 1] : 0;
+            sh[t] = ok ? L.s16[b16 + 2] + L.s16[b16 + 3] : 0;
         }
     }
-    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        return UnitQ4_KExact::load(w, row, col);
-    }
     __device__ void addends(const Raw &r, float *out) const {
-        float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
         int sc1, m1, sc2, m2;
         k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
-        float d1 = d * (float)sc1, min1 = dmin * (float)m1;
-        float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+        const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+        const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
         int lo[8], hi[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
             lo[i] = (int)(x & NIB);
             hi[i] = (int)((x >> 4) & NIB);
         }
@@ -375,244 +512,61 @@ struct UnitQ4_KQ8 {
                 il = __builtin_amdgcn_sdot4(lo[i], xl[t][i], il, false);
                 ih = __builtin_amdgcn_sdot4(hi[i], xh[t][i], ih, false);
             }
-            float va_lo = dl[t] * (float)il, a_lo = dl[t] * (float)sl[t];
-            float va_hi = dh[t] * (float)ih, a_hi = dh[t] * (float)sh[t];
-            float tt = d1 * va_lo;
-            tt = tt - min1 * a_lo;
-            tt = tt + d2 * va_hi;
-            tt = tt - min2 * a_hi;
-            out[t] = tt;
+            const float va_lo = dl[t] * (float)il, a_lo = dl[t] * (float)sl[t];
+            const float va_hi = dh[t] * (float)ih, a_hi = dh[t] * (float)sh[t];
+            float s = d1 * va_lo;
+            s = s - min1 * a_lo;
+            s = s + d2 * va_hi;
+            s = s - min2 * a_hi;
+            out[t] = s;
         }
     }
 };
 
-// ---------------------------------------------------------------------------
-// Activation-stationary kernels.
-// Block of NT threads; U column units per row; P = NT / U rows per pass;
-// RT rows per tile (multiple of P); RB rows loaded ahead per lane.
-// LDS: the addends of a tile, [TB][RT][U + 1] floats.
-// ---------------------------------------------------------------------------
-
-constexpr int RB = 4;
-
-template <class Unit, int NT>
-__global__ __launch_bounds__(NT) void k_gemv_exact_as(DevWeight w, const float *__restrict__ A,
-                                                      float *__restrict__ out, int U, int P, int RT,
-                                                      int ntiles) {
-    extern __shared__ float part[];
-    const int tid = threadIdx.x;
-    const int col = tid % U, rsub = tid / U;
-    const bool active = rsub < P;
-    const size_t tok = blockIdx.y;
-    const float *a = A + tok * w.n_cols;
-    float *o = out + tok * w.n_rows;
-    const int ld = U + 1;
-    Unit unit;
-    if (active) unit.load_act(a, col);
-    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const size_t row0 = (size_t)tile * RT;
-        if (active) {
-            for (int r0 = rsub; r0 < RT; r0 += P * RB) {
-                typename Unit::Raw raw[RB];
-#pragma unroll
-                for (int u = 0; u < RB; u++) {
-                    const int r = r0 + u * P;
-                    if (r < RT && row0 + r < w.n_rows) raw[u] = Unit::load(w, row0 + r, col);
-                }
-#pragma unroll
-                for (int u = 0; u < RB; u++) {
-                    const int r = r0 + u * P;
-                    if (r < RT) part[r * ld + col] = row0 + r < w.n_rows ? unit.addend(raw[u]) : 0.0f;
-                }
-            }
-        }
-        __syncthreads();
-        for (int r = tid; r < RT; r += NT) {
-            if (row0 + r < w.n_rows) {
-                float s = 0.0f;
-                for (int c = 0; c < U; c++) s = s + part[r * ld + c];
-                o[row0 + r] = s;
-            }
-        }
-        __syncthreads();
+// Q6_K super-block, Q8: for sub-blocks b of 16 ascending,
+// ssb += (d sc_b) (dx isum_b) from +0.0; the addend is ssb.
+template <int TB>
+struct Q6_KQ8 {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ6_K;
+    int xw[TB][64];
+    float dx[TB][8];
+    int s16[TB][16];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
+        Raw r;
+        ld_q6_k(w, row, col, r);
+        return r;
     }
-}
-
-template <class Unit, int NT, int TB>
-__global__ __launch_bounds__(NT) void k_gemv_q8_as(DevWeight w, const float *__restrict__ A, float *__restrict__ out,
-                                                   int t_rows, int U, int P, int RT, int ntiles) {
-    extern __shared__ float part[];
-    const int tid = threadIdx.x;
-    const int col = tid % U, rsub = tid / U;
-    const bool active = rsub < P;
-    const int t0 = blockIdx.y * TB;
-    const int tv = min(TB, t_rows - t0);
-    const int ld = U + 1;
-    Unit unit;
-    if (active) unit.load_act(A, w.n_cols, t0, tv, col);
-    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const size_t row0 = (size_t)tile * RT;
-        if (active) {
-            for (int r0 = rsub; r0 < RT; r0 += P * RB) {
-                typename Unit::Raw raw[RB];
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
 #pragma unroll
-                for (int u = 0; u < RB; u++) {
-                    const int r = r0 + u * P;
-                    if (r < RT && row0 + r < w.n_rows) raw[u] = Unit::load(w, row0 + r, col);
-                }
+        for (int t = 0; t < TB; t++) {
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 256 * (size_t)col) / 4);
 #pragma unroll
-                for (int u = 0; u < RB; u++) {
-                    const int r = r0 + u * P;
-                    if (r < RT) {
-                        float ad[TB];
-                        if (row0 + r < w.n_rows) {
-                            unit.addends(raw[u], ad);
-                        } else {
-#pragma unroll
-                            for (int t = 0; t < TB; t++) ad[t] = 0.0f;
-                        }
-#pragma unroll
-                        for (int t = 0; t < TB; t++) part[(t * RT + r) * ld + col] = ad[t];
-                    }
-                }
+            for (int i = 0; i < 16; i++) {
+                const int4 v = p[i];
+                xw[t][4 * i] = ok ? v.x : 0; xw[t][4 * i + 1] = ok ? v.y : 0;
+                xw[t][4 * i + 2] = ok ? v.z : 0; xw[t][4 * i + 3] = ok ? v.w : 0;
             }
+#pragma unroll
+            for (int i = 0; i < 8; i++) dx[t][i] = ok ? L.dx[tt * (k / 32) + 8 * (size_t)col + i] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) s16[t][i] = ok ? L.s16[tt * (k / 16) + 16 * (size_t)col + i] : 0;
         }
-        __syncthreads();
-        for (int j = tid; j < tv * RT; j += NT) {
-            const int t = j / RT, r = j % RT;
-            if (row0 + r < w.n_rows) {
-                float s = 0.0f;
-                const float *pp = part + (t * RT + r) * ld;
-                for (int c = 0; c < U; c++) s = s + pp[c];
-                out[(size_t)(t0 + t) * w.n_rows + row0 + r] = s;
-            }
-        }
-        __syncthreads();
     }
-}
-
-// ---------------------------------------------------------------------------
-// Q6_K, lane per row (LAYOUT_IL64).
-// ---------------------------------------------------------------------------
-
-struct Q6Block {
-    uint4 ql[8], qh[4], sc;
-    uint32_t d;
-};
-
-__device__ __forceinline__ void q6_load(const uint8_t *sbp, int lane, Q6Block &b) {
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-        b.ql[c] = *reinterpret_cast<const uint4 *>(sbp + IL64_Q6K_QL + (size_t)(c * 64 + lane) * 16);
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-        b.qh[c] = *reinterpret_cast<const uint4 *>(sbp + IL64_Q6K_QH + (size_t)(c * 64 + lane) * 16);
-    b.sc = *reinterpret_cast<const uint4 *>(sbp + IL64_Q6K_SC + (size_t)lane * 16);
-    b.d = *reinterpret_cast<const uint16_t *>(sbp + IL64_Q6K_D + (size_t)lane * 2);
-}
-
-__device__ __forceinline__ int q6_sc(const uint4 &s, int i) {
-    return (int)(int8_t)((wrd(s, i >> 2) >> (8 * (i & 3))) & 0xFFu);
-}
-
-// The four 6-bit value words (+32 offset, one byte per l) of positions
-// l..l+3 (q1), +32 (q2), +64 (q3), +96 (q4) of half o, l = 4*lq.
-__device__ __forceinline__ void q6_words(const Q6Block &b, int o, int lq, uint32_t &u1, uint32_t &u2,
-                                         uint32_t &u3, uint32_t &u4) {
-    const int c = lq >> 2, wi = lq & 3;
-    const uint32_t qa = wrd(b.ql[4 * o + c], wi), qb = wrd(b.ql[4 * o + 2 + c], wi);
-    const uint32_t qh = wrd(b.qh[2 * o + c], wi);
-    u1 = (qa & NIB) | ((qh & 0x03030303u) << 4);
-    u2 = (qb & NIB) | ((qh & 0x0C0C0C0Cu) << 2);
-    u3 = ((qa >> 4) & NIB) | (qh & 0x30303030u);
-    u4 = ((qb >> 4) & NIB) | ((qh >> 2) & 0x30303030u);
-}
-
-// rce-op-qmm/src/lib.rs L425-454, L1667-1705: per half o, l in 0..32, the
-// positions l, l+32, l+64, l+96 in order: sumf += ((d sc) q) a.
-__global__ __launch_bounds__(256) void k_gemv_exact_q6k(DevWeight w, const float *__restrict__ A,
-                                                        float *__restrict__ out) {
-    const size_t row = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t grp = row >> 6;
-    const int lane = threadIdx.x & 63;
-    if (grp * 64 >= w.n_rows) return;  // wave-uniform
-    const size_t tok = blockIdx.y;
-    const float *a = A + tok * w.n_cols;
-    const uint8_t *gb = w.base + grp * w.group_stride;
-    const int nsb = (int)(w.n_cols / 256);
-    float sumf = 0.0f;
-    for (int sb = 0; sb < nsb; sb++) {
-        Q6Block b;
-        q6_load(gb + (size_t)sb * IL64_Q6K_SB, lane, b);
+    __device__ void addends(const Raw &b, float *out) const {
         const float d = h2f(b.d);
-        const float *as = a + 256 * sb;
+        float ssb[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) ssb[t] = 0.0f;
 #pragma unroll
         for (int o = 0; o < 2; o++) {
+            int acc[TB][8];  // sub-block 8o + 2m + c -> index 2m + c
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const float ds1 = d * (float)q6_sc(b.sc, 8 * o + c), ds2 = d * (float)q6_sc(b.sc, 8 * o + c + 2);
-                const float ds3 = d * (float)q6_sc(b.sc, 8 * o + c + 4), ds4 = d * (float)q6_sc(b.sc, 8 * o + c + 6);
-                const float n1 = -32.0f * ds1, n2 = -32.0f * ds2, n3 = -32.0f * ds3, n4 = -32.0f * ds4;
+            for (int t = 0; t < TB; t++)
 #pragma unroll
-                for (int lq = 4 * c; lq < 4 * c + 4; lq++) {
-                    uint32_t u1, u2, u3, u4;
-                    q6_words(b, o, lq, u1, u2, u3, u4);
-                    const float *al = as + 128 * o + 4 * lq;
-#define Q6_STEP(J)                                                                   \
-    sumf = sumf + __builtin_fmaf(ubyte<J>(u1), ds1, n1) * al[J];                       \
-    sumf = sumf + __builtin_fmaf(ubyte<J>(u2), ds2, n2) * al[J + 32];                  \
-    sumf = sumf + __builtin_fmaf(ubyte<J>(u3), ds3, n3) * al[J + 64];                  \
-    sumf = sumf + __builtin_fmaf(ubyte<J>(u4), ds4, n4) * al[J + 96];
-                    Q6_STEP(0) Q6_STEP(1) Q6_STEP(2) Q6_STEP(3)
-#undef Q6_STEP
-                }
-            }
-        }
-    }
-    if (row < w.n_rows) out[tok * w.n_rows + row] = sumf;
-}
-
-// Q8-activation Q6_K: per super-block, for sub-blocks b of 16 ascending,
-// ssb += (d sc_b) (dx isum_b) from +0.0, then sumf += ssb.  The block first
-// quantizes the activation row into LDS (xq words, dx, half-block sums);
-// every lane then reads the same LDS word (a broadcast).
-__global__ __launch_bounds__(256) void k_gemv_q8_q6k(DevWeight w, const float *__restrict__ A,
-                                                     float *__restrict__ out) {
-    extern __shared__ int lds_q[];
-    const size_t k = w.n_cols;
-    const int nb = (int)(k / 32);
-    int *xq = lds_q;                                          // k/4 words
-    float *dx = reinterpret_cast<float *>(lds_q + k / 4);     // k/32
-    int *xs16 = lds_q + k / 4 + k / 32;                       // k/16
-    const size_t tok = blockIdx.y;
-    for (int b = threadIdx.x; b < nb; b += 256) {
-        int q8[8], lo, hi;
-        float d;
-        quant_block32(A + tok * k + 32 * (size_t)b, q8, d, lo, hi);
-#pragma unroll
-        for (int i = 0; i < 8; i++) xq[8 * b + i] = q8[i];
-        dx[b] = d;
-        xs16[2 * b] = lo;
-        xs16[2 * b + 1] = hi;
-    }
-    __syncthreads();
-    const size_t row = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t grp = row >> 6;
-    const int lane = threadIdx.x & 63;
-    if (grp * 64 >= w.n_rows) return;  // wave-uniform, after the only barrier
-    const uint8_t *gb = w.base + grp * w.group_stride;
-    const int nsb = (int)(k / 256);
-    float sumf = 0.0f;
-    for (int sb = 0; sb < nsb; sb++) {
-        Q6Block b;
-        q6_load(gb + (size_t)sb * IL64_Q6K_SB, lane, b);
-        const float d = h2f(b.d);
-        float ssb = 0.0f;
-#pragma unroll
-        for (int o = 0; o < 2; o++) {
-            int acc[8];  // sub-block 8o + 2m + c -> index 2m + c
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc[i] = 0;
+                for (int i = 0; i < 8; i++) acc[t][i] = 0;
 #pragma unroll
             for (int lq = 0; lq < 8; lq++) {
                 uint32_t u[4];
@@ -620,24 +574,188 @@ __global__ __launch_bounds__(256) void k_gemv_q8_q6k(DevWeight w, const float *_
                 const int c = lq >> 2, wi = lq & 3;
 #pragma unroll
                 for (int m = 0; m < 4; m++) {
-                    // positions 128o + 32m + 16c + 4wi .. +3
-                    const int xw = (256 * sb + 128 * o + 32 * m + 16 * c + 4 * wi) >> 2;
-                    acc[2 * m + c] = __builtin_amdgcn_sdot4((int)u[m], xq[xw], acc[2 * m + c], false);
+#pragma unroll
+                    for (int t = 0; t < TB; t++)
+                        acc[t][2 * m + c] = __builtin_amdgcn_sdot4((int)u[m], xw[t][32 * o + 8 * m + 4 * c + wi],
+                                                                   acc[t][2 * m + c], false);
                 }
             }
 #pragma unroll
             for (int bb = 0; bb < 8; bb++) {
-                const int sbk = 8 * o + bb;              // sub-block within the super-block
-                const int gsub = 16 * sb + sbk;          // sub-block of 16 within the row
-                const int isum = acc[bb] - 32 * xs16[gsub];
-                const float ds = d * (float)q6_sc(b.sc, sbk);
-                const float ab = dx[gsub >> 1] * (float)isum;
-                ssb = ssb + ds * ab;
+                const int sbk = 8 * o + bb;
+                const float ds = d * (float)q6_sc(b.c[12], sbk);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    const int isum = acc[t][bb] - 32 * s16[t][sbk];
+                    const float ab = dx[t][sbk >> 1] * (float)isum;
+                    ssb[t] = ssb[t] + ds * ab;
+                }
             }
         }
-        sumf = sumf + ssb;
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = ssb[t];
     }
-    if (row < w.n_rows) out[tok * w.n_rows + row] = sumf;
+};
+
+// ---------------------------------------------------------------------------
+// The activation-stationary kernel.
+// ---------------------------------------------------------------------------
+
+__host__ __device__ constexpr int fold_ld(int U) { return ((U + 3) & ~3) + 4; }
+
+// Dynamic LDS a block may use (the default per-block limit).
+constexpr size_t LDS_MAX = 64 * 1024;
+
+size_t gemv_lds_bytes(int U, int nt, int rpl, int tb, bool q8, size_t k) {
+    // the tile's addends plus one dummy row written by idle lanes
+    const size_t fold = ((size_t)tb * (size_t)(nt / U) * rpl + 1) * fold_ld(U) * sizeof(float);
+    const size_t act = q8 ? act_lds_bytes(k, tb) : 0;
+    return fold > act ? fold : act;
+}
+
+template <class Unit, int NT, int RPL, bool Q8>
+__global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__restrict__ A, float *__restrict__ out,
+                                                int t_rows, int U) {
+    constexpr int TB = Unit::NTOK;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x;
+    const int P = NT / U;
+    const int col = tid % U, rsub = tid / U;
+    const bool active = rsub < P;
+    const int RT = P * RPL;
+    const size_t row0 = (size_t)blockIdx.x * RT;
+    const int t0 = blockIdx.y * TB;
+    const int tv = min(TB, t_rows - t0);
+    const size_t k = w.n_cols;
+
+    Unit unit;
+    // Phase 1: activation loads first (they are not behind the weights in
+    // the in-order load counter), then every weight load of the thread.
+    // No load sits in a branch (the compiler waits for a load made inside
+    // a branch before the branch joins, which would serialize the rows):
+    // rows past the end, and idle lanes, load a valid row and are dropped.
+    QuantTask qt0, qt1;
+    const int kq = (int)(k / 8);
+    const int qtotal = Q8 ? tv * kq : 0;
+    if constexpr (Q8) {
+        quant_task_load(A, kq, t0, qtotal, tid, qt0);
+        quant_task_load(A, kq, t0, qtotal, tid + NT, qt1);
+    } else {
+        unit.init(A, k, t0, tv, col);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weights'
+    typename Unit::Raw raw[RPL];
+    const int rs = active ? rsub : P - 1;
+#pragma unroll
+    for (int u = 0; u < RPL; u++) {
+        const size_t r = row0 + (size_t)(u * P + rs);
+        raw[u] = Unit::load(w, r < w.n_rows ? r : w.n_rows - 1, col);
+    }
+    // Keep every load above ahead of any arithmetic on loaded data.
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase 2 (Q8): quantize the block's activation rows into LDS.
+    if constexpr (Q8) {
+        ActLds L(lds, k, TB);
+        quant_task_finish(qt0, k, qtotal, tid, L);
+        quant_task_finish(qt1, k, qtotal, tid + NT, L);
+        for (int base = 2 * NT; base < qtotal; base += NT) {
+            QuantTask q;
+            quant_task_load(A, kq, t0, qtotal, base + tid, q);
+            quant_task_finish(q, k, qtotal, base + tid, L);
+        }
+        __syncthreads();
+        if (active) unit.init_q8(L, k, tv, col);
+        __syncthreads();  // the fold below reuses the LDS
+    }
+    // Phase 3: per-unit addends of every (token, row) to LDS.
+    float *part = reinterpret_cast<float *>(lds);
+    const int ld = fold_ld(U);
+#pragma unroll
+    for (int u = 0; u < RPL; u++) {
+        // Every lane computes and stores (idle lanes into a dummy row past
+        // the tile), so no load is sunk into a guarded branch.
+        float ad[TB];
+        unit.addends(raw[u], ad);
+        const int r = u * P + rsub;
+        const bool in = row0 + r < w.n_rows;
+#pragma unroll
+        for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = in ? ad[t] : 0.0f;
+    }
+    __syncthreads();
+    // Phase 4: the reference's fold, one thread per (token, row).
+    for (int j = tid; j < tv * RT; j += NT) {
+        const int t = j / RT, r = j % RT;
+        if (row0 + r < w.n_rows) {
+            const float *pp = part + (t * RT + r) * ld;
+            const float4 *p4 = reinterpret_cast<const float4 *>(pp);
+            float s = 0.0f;
+            const int U4 = U >> 2;
+#pragma unroll 8
+            for (int c = 0; c < U4; c++) {
+                const float4 v = p4[c];
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+            for (int c = U4 * 4; c < U; c++) s = s + pp[c];
+            out[((size_t)t0 + t) * w.n_rows + row0 + r] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K EXACT: one lane per row (the row sum is a single chain).
+// ---------------------------------------------------------------------------
+
+// rce-op-qmm/src/lib.rs L425-454, L1667-1705: per half o, l in 0..32, the
+// positions l, l+32, l+64, l+96 in order: sumf += ((d sc) q) a.
+__device__ __forceinline__ float q6_exact_superblock(const RawQ6_K &b, const float *as, float sumf) {
+    const float d = h2f(b.d);
+#pragma unroll
+    for (int o = 0; o < 2; o++) {
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const float ds1 = d * (float)q6_sc(b.c[12], 8 * o + c), ds2 = d * (float)q6_sc(b.c[12], 8 * o + c + 2);
+            const float ds3 = d * (float)q6_sc(b.c[12], 8 * o + c + 4), ds4 = d * (float)q6_sc(b.c[12], 8 * o + c + 6);
+            const float n1 = -32.0f * ds1, n2 = -32.0f * ds2, n3 = -32.0f * ds3, n4 = -32.0f * ds4;
+#pragma unroll
+            for (int lq = 4 * c; lq < 4 * c + 4; lq++) {
+                uint32_t u1, u2, u3, u4;
+                q6_words(b, o, lq, u1, u2, u3, u4);
+                const float *al = as + 128 * o + 4 * lq;
+#define Q6_STEP(J)                                                                   \
+    sumf = sumf + __builtin_fmaf(ubyte<J>(u1), ds1, n1) * al[J];                       \
+    sumf = sumf + __builtin_fmaf(ubyte<J>(u2), ds2, n2) * al[J + 32];                  \
+    sumf = sumf + __builtin_fmaf(ubyte<J>(u3), ds3, n3) * al[J + 64];                  \
+    sumf = sumf + __builtin_fmaf(ubyte<J>(u4), ds4, n4) * al[J + 96];
+                Q6_STEP(0) Q6_STEP(1) Q6_STEP(2) Q6_STEP(3)
+#undef Q6_STEP
+            }
+        }
+    }
+    return sumf;
+}
+
+__global__ __launch_bounds__(256) void k_gemv_exact_q6k(DevWeight w, const float *__restrict__ A,
+                                                        float *__restrict__ out) {
+    const size_t row = (size_t)blockIdx.x * 256 + threadIdx.x;
+    // Lanes past the end recompute the last row (no branch around loads).
+    const size_t rr = row < w.n_rows ? row : w.n_rows - 1;
+    const int nsb = (int)(w.n_cols / 256);
+    const float *a = A + (size_t)blockIdx.y * w.n_cols;
+    float sumf = 0.0f;
+    RawQ6_K b0, b1;
+    ld_q6_k(w, rr, 0, b0);
+    int sb = 0;
+    for (; sb + 1 < nsb; sb += 2) {
+        ld_q6_k(w, rr, sb + 1, b1);
+        sumf = q6_exact_superblock(b0, a + 256 * sb, sumf);
+        if (sb + 2 < nsb) ld_q6_k(w, rr, sb + 2, b0);
+        sumf = q6_exact_superblock(b1, a + 256 * (sb + 1), sumf);
+    }
+    if (sb < nsb) sumf = q6_exact_superblock(b0, a + 256 * sb, sumf);
+    if (row < w.n_rows) out[(size_t)blockIdx.y * w.n_rows + row] = sumf;
 }
 
 // ---------------------------------------------------------------------------
@@ -661,39 +779,40 @@ __global__ void k_dequant_row(DevWeight w, size_t row, float *__restrict__ out) 
         const int p = (int)(i % 32);
         const float scale = h2f(*reinterpret_cast<const uint16_t *>(rp + 2 * b));
         if (w.dtype == T_Q4_0) {
-            const uint8_t byte = rp[w.qs_off + 16 * b + (p & 15)];
+            const uint8_t byte = rp[w.plane1 + 16 * b + (p & 15)];
             const int n = p < 16 ? (byte & 0x0F) - 8 : ((byte >> 4) & 0x0F) - 8;
             v = (float)n * scale;
         } else {
-            v = (float)(int8_t)rp[w.qs_off + 32 * b + p] * scale;
+            const uint8_t byte = p < 16 ? rp[w.plane1 + 16 * b + p] : rp[w.plane2 + 16 * b + p - 16];
+            v = (float)(int8_t)byte * scale;
         }
     } else if (w.dtype == T_Q4_K) {
-        const uint8_t *sp = w.base + row * w.row_stride + 144 * (i / 256);
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t sb = i / 256;
         const int p = (int)(i % 256), g = p / 64, l = p % 32, hi = (p % 64) >= 32;
-        const uint4 h = *reinterpret_cast<const uint4 *>(sp);
+        const uint4 h = *reinterpret_cast<const uint4 *>(rp + 16 * sb);
         int sc, m;
         k4_scale_min(h, 2 * g + hi, sc, m);
         const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
         const float dd = d * (float)sc, mm = dmin * (float)m;
-        const uint8_t byte = sp[16 + 32 * g + l];
+        const size_t u = 4 * sb + g;
+        const uint8_t byte = l < 16 ? rp[w.plane1 + 16 * u + l] : rp[w.plane2 + 16 * u + l - 16];
         const int n = hi ? ((byte >> 4) & 0x0F) : (byte & 0x0F);
         v = dd * (float)n - mm;
     } else if (w.dtype == T_Q6_K) {
-        const size_t grp = row >> 6;
-        const int lane = (int)(row & 63);
-        const uint8_t *sbp = w.base + grp * w.group_stride + (i / 256) * IL64_Q6K_SB;
+        const uint8_t *sp = w.base + (row >> 6) * w.group_stride + (i / 256) * IL64_Q6K_SB;
+        const size_t lane = row & 63;
         const int p = (int)(i % 256), o = p / 128, r = p % 128, m = r / 32, l = r % 32;
-        // ql byte j of the super-block lives in chunk j/16, byte j%16.
-        auto ql = [&](int j) { return sbp[IL64_Q6K_QL + (size_t)((j >> 4) * 64 + lane) * 16 + (j & 15)]; };
-        auto qh = [&](int j) { return sbp[IL64_Q6K_QH + (size_t)((j >> 4) * 64 + lane) * 16 + (j & 15)]; };
-        const int qhb = qh(32 * o + l);
+        // byte j (0..207) of the super-block's ql/qh/scales is in chunk j/16.
+        auto byte_at = [&](int j) { return sp[((size_t)(j >> 4) * 64 + lane) * 16 + (j & 15)]; };
+        const int qhb = byte_at(128 + 32 * o + l);
         int q;
-        if (m == 0) q = ((ql(64 * o + l) & 0x0F) | ((qhb & 3) << 4)) - 32;
-        else if (m == 1) q = ((ql(64 * o + l + 32) & 0x0F) | (((qhb >> 2) & 3) << 4)) - 32;
-        else if (m == 2) q = ((ql(64 * o + l) >> 4) | (((qhb >> 4) & 3) << 4)) - 32;
-        else q = ((ql(64 * o + l + 32) >> 4) | (((qhb >> 6) & 3) << 4)) - 32;
-        const int sc = (int)(int8_t)sbp[IL64_Q6K_SC + (size_t)lane * 16 + 8 * o + l / 16 + 2 * m];
-        const float d = h2f(*reinterpret_cast<const uint16_t *>(sbp + IL64_Q6K_D + (size_t)lane * 2));
+        if (m == 0) q = ((byte_at(64 * o + l) & 0x0F) | ((qhb & 3) << 4)) - 32;
+        else if (m == 1) q = ((byte_at(64 * o + l + 32) & 0x0F) | (((qhb >> 2) & 3) << 4)) - 32;
+        else if (m == 2) q = ((byte_at(64 * o + l) >> 4) | (((qhb >> 4) & 3) << 4)) - 32;
+        else q = ((byte_at(64 * o + l + 32) >> 4) | (((qhb >> 6) & 3) << 4)) - 32;
+        const int sc = (int)(int8_t)byte_at(192 + 8 * o + l / 16 + 2 * m);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(sp + IL64_Q6K_D + lane * 2));
         const float t = d * (float)sc;
         v = t * (float)q;
     }
@@ -704,76 +823,177 @@ __global__ void k_dequant_row(DevWeight w, size_t row, float *__restrict__ out) 
 // Launch geometry.
 // ---------------------------------------------------------------------------
 
-struct AsGeom { int nt, U, P, RT, ntiles, grid; size_t lds; };
-
-// Threads per block: the smallest of 256/512/1024 holding one row's units.
-// Rows per tile: 2*RB passes per lane (RT = 2*RB*P) keeps a lane's loads in
-// flight while the tile count stays well above the CU count.
-AsGeom as_geom(size_t n_rows, int U, int tb) {
-    AsGeom g{};
-    g.U = U;
-    g.nt = U <= 256 ? 256 : (U <= 512 ? 512 : 1024);
-    g.P = g.nt / U;
-    int passes = tb > 1 ? RB : 2 * RB;
-    g.RT = g.P * passes;
-    g.ntiles = (int)((n_rows + g.RT - 1) / g.RT);
-    g.grid = g.ntiles;
-    g.lds = (size_t)tb * g.RT * (U + 1) * sizeof(float);
-    return g;
+int units_per_row(uint32_t dtype, size_t n_cols) {
+    switch (dtype) {
+    case T_Q4_0: case T_Q8_0: return (int)(n_cols / 32);
+    case T_Q4_K: return (int)(n_cols / 64);
+    case T_Q6_K: return (int)(n_cols / 256);
+    default: return 0;
+    }
 }
 
-template <class Unit>
-hipError_t run_exact_as(const DevWeight &w, int U, const float *a, size_t t_rows, float *out,
-                        hipStream_t s) {
-    AsGeom g = as_geom(w.n_rows, U, 1);
-    dim3 grid(g.grid, (unsigned)t_rows), block(g.nt);
-    if (g.nt == 256)
-        hipLaunchKernelGGL((k_gemv_exact_as<Unit, 256>), grid, block, g.lds, s, w, a, out, g.U, g.P, g.RT, g.ntiles);
-    else if (g.nt == 512)
-        hipLaunchKernelGGL((k_gemv_exact_as<Unit, 512>), grid, block, g.lds, s, w, a, out, g.U, g.P, g.RT, g.ntiles);
-    else
-        hipLaunchKernelGGL((k_gemv_exact_as<Unit, 1024>), grid, block, g.lds, s, w, a, out, g.U, g.P, g.RT, g.ntiles);
+int nt_for(int U) { return U <= 256 ? 256 : (U <= 512 ? 512 : 1024); }
+
+template <class Unit, int NT, int RPL, bool Q8>
+hipError_t launch_as(const DevWeight &w, int U, const float *a, size_t t_rows, float *out, hipStream_t s) {
+    constexpr int TB = Unit::NTOK;
+    const int P = NT / U, RT = P * RPL;
+    if (P < 1) return hipErrorInvalidConfiguration;
+    const size_t lds = gemv_lds_bytes(U, NT, RPL, TB, Q8, w.n_cols);
+    if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
+    dim3 grid((unsigned)((w.n_rows + RT - 1) / RT), (unsigned)((t_rows + TB - 1) / TB)), block(NT);
+    hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8>), grid, block, lds, s, w, a, out, (int)t_rows, U);
     return hipGetLastError();
 }
 
-template <template <int> class Unit, int TB>
-hipError_t run_q8_as_tb(const DevWeight &w, int U, const float *q, size_t t_rows, float *out,
+template <class Unit, bool Q8>
+hipError_t launch_as_nt(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                         hipStream_t s) {
-    AsGeom g = as_geom(w.n_rows, U, TB);
-    dim3 grid(g.grid, (unsigned)((t_rows + TB - 1) / TB)), block(g.nt);
-    int tr = (int)t_rows;
-    if (g.nt == 256)
-        hipLaunchKernelGGL((k_gemv_q8_as<Unit<TB>, 256, TB>), grid, block, g.lds, s, w, q, out, tr, g.U, g.P, g.RT, g.ntiles);
-    else if (g.nt == 512)
-        hipLaunchKernelGGL((k_gemv_q8_as<Unit<TB>, 512, TB>), grid, block, g.lds, s, w, q, out, tr, g.U, g.P, g.RT, g.ntiles);
-    else
-        hipLaunchKernelGGL((k_gemv_q8_as<Unit<TB>, 1024, TB>), grid, block, g.lds, s, w, q, out, tr, g.U, g.P, g.RT, g.ntiles);
-    return hipGetLastError();
+    const int U = units_per_row(w.dtype, w.n_cols);
+#define RCE_RPL(NT)                                                                        \
+    switch (g.rpl) {                                                                       \
+    case 2: return launch_as<Unit, NT, 2, Q8>(w, U, a, t_rows, out, s);                    \
+    case 4: return launch_as<Unit, NT, 4, Q8>(w, U, a, t_rows, out, s);                    \
+    case 8: return launch_as<Unit, NT, 8, Q8>(w, U, a, t_rows, out, s);                    \
+    case 12: return launch_as<Unit, NT, 12, Q8>(w, U, a, t_rows, out, s);                  \
+    case 16: return launch_as<Unit, NT, 16, Q8>(w, U, a, t_rows, out, s);                  \
+    default: return hipErrorInvalidValue;                                                  \
+    }
+    switch (g.nt) {
+    case 256: RCE_RPL(256)
+    case 512: RCE_RPL(512)
+    case 1024: RCE_RPL(1024)
+    default: return hipErrorInvalidValue;
+    }
+#undef RCE_RPL
 }
 
-template <template <int> class Unit, int TBMAX>
-hipError_t run_q8_as(const DevWeight &w, int U, const float *q, size_t t_rows, float *out,
-                     hipStream_t s) {
-    if (t_rows == 1) return run_q8_as_tb<Unit, 1>(w, U, q, t_rows, out, s);
-    if (t_rows <= 4 || TBMAX == 4) return run_q8_as_tb<Unit, 4>(w, U, q, t_rows, out, s);
-    return run_q8_as_tb<Unit, (TBMAX > 4 ? TBMAX : 4)>(w, U, q, t_rows, out, s);
+// MAXTB: the most tokens per thread the unit's registers allow.
+template <template <int> class Unit, bool Q8, int MAXTB>
+hipError_t launch_as_tb(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                        hipStream_t s) {
+    switch (g.tb) {
+    case 1: return launch_as_nt<Unit<1>, Q8>(w, g, a, t_rows, out, s);
+    case 2:
+        if constexpr (MAXTB >= 2) return launch_as_nt<Unit<2>, Q8>(w, g, a, t_rows, out, s);
+        return hipErrorInvalidValue;
+    case 4:
+        if constexpr (MAXTB >= 4) return launch_as_nt<Unit<4>, Q8>(w, g, a, t_rows, out, s);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
 }
+
+template <int TB> using Q4_0Q8 = Q32Q8<TB, true>;
+template <int TB> using Q8_0Q8 = Q32Q8<TB, false>;
 
 }  // namespace
 
 // Column units per row must fit one block of up to 1024 threads.
 bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
-    if (n_cols == 0) return false;
+    if (n_cols == 0 || (mode != 0 && mode != 1)) return false;
+    // Q8 keeps one token's quantized row in LDS (1.375 B per value).
+    if (mode == 1 && act_lds_bytes(n_cols, 1) > LDS_MAX) return false;
     switch (dtype) {
     case T_Q4_0:
     case T_Q8_0:
-        return n_cols % 32 == 0 && n_cols / 32 <= 1024 && (mode == 0 || mode == 1);
+        return n_cols % 32 == 0 && n_cols / 32 <= 1024;
     case T_Q4_K:
-        return n_cols % 256 == 0 && n_cols / 64 <= 1024 && (mode == 0 || mode == 1);
+        return n_cols % 256 == 0 && n_cols / 64 <= 1024;
     case T_Q6_K:
-        return n_cols % 256 == 0 && (mode == 0 || mode == 1);
+        return n_cols % 256 == 0 && n_cols / 256 <= 1024;
     default:
         return false;
+    }
+}
+
+static size_t pad16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+size_t plan_layout(DevWeight &dw) {
+    const size_t n = dw.n_rows, k = dw.n_cols;
+    switch (dw.dtype) {
+    case T_Q4_0:
+        dw.layout = LAYOUT_SPLIT_Q4_0;
+        dw.plane1 = pad16(2 * (k / 32));
+        dw.plane2 = 0;
+        dw.row_stride = dw.plane1 + 16 * (k / 32);
+        return dw.row_stride * n;
+    case T_Q8_0:
+        dw.layout = LAYOUT_SPLIT_Q8_0;
+        dw.plane1 = pad16(2 * (k / 32));
+        dw.plane2 = dw.plane1 + 16 * (k / 32);
+        dw.row_stride = dw.plane2 + 16 * (k / 32);
+        return dw.row_stride * n;
+    case T_Q4_K:
+        dw.layout = LAYOUT_SPLIT_Q4_K;
+        dw.plane1 = 16 * (k / 256);
+        dw.plane2 = dw.plane1 + 16 * (k / 64);
+        dw.row_stride = 144 * (k / 256);
+        return dw.row_stride * n;
+    case T_Q6_K:
+        dw.layout = LAYOUT_IL64_Q6_K;
+        dw.group_stride = (k / 256) * IL64_Q6K_SB;
+        return dw.group_stride * ((n + 63) / 64);
+    default:
+        return 0;
+    }
+}
+
+void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
+    const size_t n = dw.n_rows, k = dw.n_cols;
+    switch (dw.layout) {
+    case LAYOUT_SPLIT_Q4_0:
+    case LAYOUT_SPLIT_Q8_0: {
+        const size_t nb = k / 32, bb = dw.dtype == T_Q8_0 ? 34 : 18;
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * nb * bb;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t b = 0; b < nb; b++) {
+                const uint8_t *blk = s + b * bb;
+                d[2 * b] = blk[0];
+                d[2 * b + 1] = blk[1];
+                for (int i = 0; i < 16; i++) d[dw.plane1 + 16 * b + i] = blk[2 + i];
+                if (dw.dtype == T_Q8_0)
+                    for (int i = 0; i < 16; i++) d[dw.plane2 + 16 * b + i] = blk[18 + i];
+            }
+        }
+        break;
+    }
+    case LAYOUT_SPLIT_Q4_K: {
+        const size_t nsb = k / 256;
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * nsb * 144;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t sb = 0; sb < nsb; sb++) {
+                const uint8_t *blk = s + sb * 144;
+                for (int i = 0; i < 16; i++) d[16 * sb + i] = blk[i];
+                for (int g = 0; g < 4; g++) {
+                    const size_t u = 4 * sb + g;
+                    for (int l = 0; l < 16; l++) d[dw.plane1 + 16 * u + l] = blk[16 + 32 * g + l];
+                    for (int l = 0; l < 16; l++) d[dw.plane2 + 16 * u + l] = blk[16 + 32 * g + 16 + l];
+                }
+            }
+        }
+        break;
+    }
+    case LAYOUT_IL64_Q6_K: {
+        const size_t nsb = k / 256;
+        for (size_t r = 0; r < n; r++) {
+            const size_t lane = r & 63;
+            uint8_t *g = dst + (r >> 6) * dw.group_stride;
+            for (size_t sb = 0; sb < nsb; sb++) {
+                const uint8_t *blk = src + (r * nsb + sb) * 210;
+                uint8_t *d = g + sb * IL64_Q6K_SB;
+                for (size_t j = 0; j < 13; j++)
+                    for (int i = 0; i < 16; i++) d[(j * 64 + lane) * 16 + i] = blk[16 * j + i];
+                d[IL64_Q6K_D + 2 * lane] = blk[208];
+                d[IL64_Q6K_D + 2 * lane + 1] = blk[209];
+            }
+        }
+        break;
+    }
+    default:
+        break;
     }
 }
 
@@ -783,42 +1003,66 @@ hipError_t launch_f16_to_f32(const uint16_t *src, float *dst, size_t n, hipStrea
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_exact(const DevWeight &w, const float *a, size_t t_rows, float *out,
-                             hipStream_t s) {
-    if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
-    switch (w.dtype) {
-    case T_Q4_0: return run_exact_as<UnitQ4_0Exact>(w, (int)(w.n_cols / 32), a, t_rows, out, s);
-    case T_Q8_0: return run_exact_as<UnitQ8_0Exact>(w, (int)(w.n_cols / 32), a, t_rows, out, s);
-    case T_Q4_K: return run_exact_as<UnitQ4_KExact>(w, (int)(w.n_cols / 64), a, t_rows, out, s);
-    case T_Q6_K: {
-        dim3 grid((unsigned)((w.n_rows + 255) / 256), (unsigned)t_rows);
-        hipLaunchKernelGGL(k_gemv_exact_q6k, grid, dim3(256), 0, s, w, a, out);
-        return hipGetLastError();
+// Rows per thread: enough loads in flight per thread to cover HBM latency
+// while keeping about two or more blocks per CU; tokens per block: all of
+// them up to the register budget of the unit.
+GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
+    GemvGeom g;
+    const int U = units_per_row(w.dtype, w.n_cols);
+    g.nt = nt_for(U);
+    const bool q8 = mode == 1;
+    if (w.dtype == T_Q6_K) {
+        g.tb = t_rows >= 2 && (!q8 || act_lds_bytes(w.n_cols, 2) <= LDS_MAX) ? 2 : 1;
+        g.rpl = 2;
+        return g;
     }
-    default: return hipErrorInvalidValue;
+    if (w.dtype == T_Q4_K) g.tb = t_rows >= 4 && q8 ? 4 : (t_rows >= 2 ? 2 : 1);
+    else g.tb = t_rows >= 4 ? 4 : (t_rows >= 2 ? 2 : 1);
+    const bool heavy = g.tb >= 4 || (w.dtype == T_Q4_K && !q8 && g.tb >= 2);  // register-bound units
+    const int P = g.nt / U;
+    // aim for ~3 blocks per CU on a 256-CU part
+    const size_t target_blocks = 768;
+    size_t rows_per_block = (w.n_rows + target_blocks - 1) / target_blocks;
+    int rpl = (int)((rows_per_block + P - 1) / P);
+    g.rpl = rpl <= 2 ? 2 : (rpl <= 4 ? 4 : 8);
+    if (heavy && g.rpl > 4) g.rpl = 4;
+    // shrink rows, then tokens, until the block's LDS fits
+    while (gemv_lds_bytes(U, g.nt, g.rpl, g.tb, q8, w.n_cols) > LDS_MAX) {
+        if (g.rpl > 2) g.rpl /= 2;
+        else if (g.tb > 1) g.tb /= 2;
+        else break;
     }
+    return g;
 }
 
-hipError_t launch_gemv_q8(const DevWeight &w, const float *a, size_t t_rows, float *out,
-                          hipStream_t s) {
+hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float *out, int mode, hipStream_t s,
+                       const GemvGeom *geom) {
     if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
-    switch (w.dtype) {
-    case T_Q4_0: return run_q8_as<UnitQ4_0Q8, 8>(w, (int)(w.n_cols / 32), a, t_rows, out, s);
-    case T_Q8_0: return run_q8_as<UnitQ8_0Q8, 8>(w, (int)(w.n_cols / 32), a, t_rows, out, s);
-    case T_Q4_K: return run_q8_as<UnitQ4_KQ8, 4>(w, (int)(w.n_cols / 64), a, t_rows, out, s);
-    case T_Q6_K: {
-        dim3 grid((unsigned)((w.n_rows + 255) / 256), (unsigned)t_rows);
-        const size_t lds = w.n_cols + (w.n_cols / 32) * 4 + (w.n_cols / 16) * 4;
-        hipLaunchKernelGGL(k_gemv_q8_q6k, grid, dim3(256), lds, s, w, a, out);
-        return hipGetLastError();
+    const GemvGeom g = geom ? *geom : pick_gemv_geom(w, t_rows, mode);
+    if (mode == 0) {
+        switch (w.dtype) {
+        case T_Q4_0: return launch_as_tb<Q4_0Exact, false, 4>(w, g, a, t_rows, out, s);
+        case T_Q8_0: return launch_as_tb<Q8_0Exact, false, 4>(w, g, a, t_rows, out, s);
+        case T_Q4_K: return launch_as_tb<Q4_KExact, false, 2>(w, g, a, t_rows, out, s);
+        case T_Q6_K: {
+            dim3 grid((unsigned)((w.n_rows + 255) / 256), (unsigned)t_rows);
+            hipLaunchKernelGGL(k_gemv_exact_q6k, grid, dim3(256), 0, s, w, a, out);
+            return hipGetLastError();
+        }
+        default: return hipErrorInvalidValue;
+        }
     }
+    switch (w.dtype) {
+    case T_Q4_0: return launch_as_tb<Q4_0Q8, true, 4>(w, g, a, t_rows, out, s);
+    case T_Q8_0: return launch_as_tb<Q8_0Q8, true, 4>(w, g, a, t_rows, out, s);
+    case T_Q4_K: return launch_as_tb<Q4_KQ8, true, 4>(w, g, a, t_rows, out, s);
+    case T_Q6_K: return launch_as_tb<Q6_KQ8, true, 2>(w, g, a, t_rows, out, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_dequant_row, dim3((unsigned)((w.n_cols + 255) / 256)), dim3(256), 0, s, w,
-                       row, out);
+    hipLaunchKernelGGL(k_dequant_row, dim3((unsigned)((w.n_cols + 255) / 256)), dim3(256), 0, s, w, row, out);
     return hipGetLastError();
 }
 

@@ -1,5 +1,5 @@
 // qmm_internal.h -- internal interface between the C ABI (qmm_abi.cpp) and
-// the HIP kernels (qmm_gemv.hip, qmm_mfma.hip).  Not installed; callers use
+// the HIP kernels (qmm_gemv.hip).  Not installed; callers use
 // include/rce_qmm.h.
 #pragma once
 
@@ -16,48 +16,63 @@ enum : uint32_t {
 };
 
 // How a weight's GGUF bytes are arranged in HBM.  Every layout holds the
-// same bytes as the GGUF tensor (plus alignment padding); only their order
-// differs, chosen so that a wave's loads are contiguous 128-bit reads.
+// same bytes as the GGUF tensor plus at most 15 bytes of padding per row
+// (Q6_K: rows padded to a multiple of 64); only their order differs.  Each is chosen so
+// that one load instruction of a wave reads 1 KB of contiguous HBM.
 enum Layout : int {
-    // Row-major rows; inside each row the 2-byte block scales of all blocks
-    // first (padded to 16 bytes), then the blocks' quant bytes.  Q4_0, Q8_0.
-    LAYOUT_SPLIT = 1,
-    // Row-major rows of untouched GGUF blocks.  Q4_K (its 144-byte
-    // super-block is already 16-byte aligned: 16 B of d/dmin/scales + 128 B).
-    LAYOUT_NATIVE = 2,
-    // Groups of 64 rows; per group and super-block the 64 rows' bytes are
-    // interleaved in 16-byte chunks so lane r of a wave reads row r of the
-    // group with contiguous wave-wide loads.  Q6_K (read one row per lane).
-    LAYOUT_IL64 = 3,
+    // Row r at r*row_stride: [block scales, 2 B each, padded to 16]
+    // [16 B of nibbles per block at plane1 + 16 b].
+    LAYOUT_SPLIT_Q4_0 = 1,
+    // Row r: [scales, padded to 16][bytes 0..15 of each block at
+    // plane1 + 16 b][bytes 16..31 of each block at plane2 + 16 b].
+    LAYOUT_SPLIT_Q8_0 = 2,
+    // Row r: [16 B header (d, dmin, 12 scale bytes) per super-block]
+    // [qs bytes l = 0..15 of 64-group u at plane1 + 16 u]
+    // [qs bytes l = 16..31 of group u at plane2 + 16 u].
+    LAYOUT_SPLIT_Q4_K = 3,
+    // Rows in groups of 64; per group and super-block sb (IL64_Q6K_SB
+    // bytes at sb * IL64_Q6K_SB) the 13 16-byte chunks of the super-block's
+    // ql (0..7), qh (8..11) and scales (12) for the 64 rows, chunk j of row
+    // r at (j * 64 + r % 64) * 16, then the rows' 2-byte d values.
+    LAYOUT_IL64_Q6_K = 4,
 };
 
-// Bytes of one Q6_K super-block for a 64-row group in LAYOUT_IL64:
-// ql 8 chunks x 64 rows x 16 B, qh 4 x 64 x 16, scales 64 x 16, d 64 x 2.
-constexpr size_t IL64_Q6K_QL = 0;
-constexpr size_t IL64_Q6K_QH = 8 * 64 * 16;             // 8192
-constexpr size_t IL64_Q6K_SC = IL64_Q6K_QH + 4 * 64 * 16; // 12288
-constexpr size_t IL64_Q6K_D = IL64_Q6K_SC + 64 * 16;      // 13312
-constexpr size_t IL64_Q6K_SB = 64 * 210;                  // 13440
-
 struct DevWeight {
-    const uint8_t *base;  // device address of row 0 (LAYOUT_IL64: of group 0)
+    const uint8_t *base;  // device address of row 0 (IL64: of row group 0)
     uint32_t dtype;
     int layout;
     size_t n_rows, n_cols;
-    size_t row_stride;    // SPLIT / NATIVE: bytes between rows
-    size_t qs_off;        // SPLIT: offset of the quant bytes inside a row
+    size_t row_stride;    // SPLIT: bytes between rows
+    size_t plane1;        // SPLIT: offset of the first 16-B plane in a row
+    size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K: offset of the second plane
     size_t group_stride;  // IL64: bytes between 64-row groups
+};
+
+constexpr size_t IL64_Q6K_D = 13 * 64 * 16;         // 13312: the d values
+constexpr size_t IL64_Q6K_SB = IL64_Q6K_D + 64 * 2;  // 13440 = 64 * 210
+
+// Launch shape of a decode kernel: threads per block, rows per lane, and
+// activation rows (tokens) per block.
+struct GemvGeom {
+    int nt = 0, rpl = 0, tb = 0;
 };
 
 // Kernels available for (dtype, n_cols, mode); mirrors rce_qmm_supports.
 bool gpu_supports(uint32_t dtype, size_t n_cols, int mode);
 
+// Device layout of a weight: fills layout, row_stride, planes and
+// group_stride of `dw` (dtype, n_rows, n_cols already set) and
+// returns the device bytes it needs.
+size_t plan_layout(DevWeight &dw);
+// GGUF bytes (row-major rows of blocks) -> the device layout of `dw`.
+void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst);
+
 hipError_t launch_f16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t s);
-hipError_t launch_gemv_exact(const DevWeight &w, const float *a, size_t t_rows, float *out,
-                             hipStream_t s);
-// Q8-activation path: quantizes the f32 activation rows inside the kernel.
-hipError_t launch_gemv_q8(const DevWeight &w, const float *a, size_t t_rows, float *out,
-                          hipStream_t s);
+// mode 0: the reference's f32 order; mode 1: Q8 activations.  `geom`
+// overrides the shape the library picks (tuning only; nullptr = pick).
+hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float *out, int mode,
+                       hipStream_t s, const GemvGeom *geom = nullptr);
+GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
 
 }  // namespace rce_qmm
