@@ -3,15 +3,18 @@
 Headline (BASELINE.json metric "GEMV HBM GB/s & GEMM TFLOPS per quant
 format, % of MI355X roofline", configs[1]): Q4_0 decode GEMV, weight
 11008x4096 N(0,0.02) quantized to Q4_0, activation batch 1 of 4096 f32
-N(0,1).  A step is one GEMV over device-resident inputs; weights rotate
-over enough copies (> 2 x 256 MB) that each step streams its weight from
-HBM rather than the Infinity Cache.  `value` is algorithmic bytes per step
-(weight bytes + 4 k + 4 n) / time per step.  Other formats/configs are
-reported under "per_format".  The CPU baseline is the oracle (a C
-restatement of the reference's mm_1d, one task per output row over the
-host cores) timed on a bounded sample of the same workload.
+N(0,1), Q8-activation mode.  A step is one GEMV launch over device-resident
+inputs; weights rotate over enough copies (> 2 x 256 MB) that each step
+streams its weight from HBM rather than the Infinity Cache, and the steps
+are replayed from a HIP graph.  `value` is algorithmic bytes per launch
+(GGUF weight bytes + 4 k + 4 n per token) / time per launch, the time
+taken with HIP events on the stream the kernels run on.  Other formats
+and configs are reported under "per_format".  The CPU baseline is the
+oracle (a C restatement of the reference's mm_1d, one task per output row
+over the host cores) timed on a bounded sample of the same workload.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode q8|exact] [--no-cpu] [--quick]
+python bench.py --copy-calibration   # device copies of known size (PMC scaling)
 """
 from __future__ import annotations
 
@@ -19,6 +22,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -28,8 +32,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-MFMA_F16_PEAK_TFLOPS = 2500.0  # dense bf16/fp16
 INFINITY_CACHE = 256 << 20
+HEADLINE_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_11008x4096_q8_traffic.md")
 
 
 def log(msg: str) -> None:
@@ -37,45 +41,44 @@ def log(msg: str) -> None:
 
 
 class Hip:
-    """The few HIP runtime calls the timing needs (events on a stream)."""
+    """The few HIP runtime calls the timing needs (events, graphs, copies)."""
 
     def __init__(self):
-        self.L = ctypes.CDLL("libamdhip64.so.7")
-        for n in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
-                  "hipEventDestroy", "hipDeviceSynchronize"):
-            getattr(self.L, n).restype = ctypes.c_int
-        self.L.hipEventCreate.argtypes = [ctypes.c_void_p]
-        self.L.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        self.L.hipEventSynchronize.argtypes = [ctypes.c_void_p]
-        self.L.hipEventElapsedTime.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
-        self.L.hipEventDestroy.argtypes = [ctypes.c_void_p]
-        for n in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
-                  "hipGraphExecDestroy", "hipGraphDestroy"):
-            getattr(self.L, n).restype = ctypes.c_int
-        self.L.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
-        self.L.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        self.L.hipGraphInstantiate.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                                               ctypes.c_char_p, ctypes.c_size_t]
-        self.L.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        self.L.hipGraphExecDestroy.argtypes = [ctypes.c_void_p]
-        self.L.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+        self.L = ctypes.CDLL("libamdhip64.so")
+        P, S = ctypes.c_void_p, ctypes.c_size_t
+        sig = {
+            "hipEventCreate": [P], "hipEventRecord": [P, P], "hipEventSynchronize": [P],
+            "hipEventElapsedTime": [P, P, P], "hipEventDestroy": [P], "hipDeviceSynchronize": [],
+            "hipStreamBeginCapture": [P, ctypes.c_int], "hipStreamEndCapture": [P, P],
+            "hipGraphInstantiate": [P, P, P, ctypes.c_char_p, S], "hipGraphLaunch": [P, P],
+            "hipGraphExecDestroy": [P], "hipGraphDestroy": [P], "hipMalloc": [P, S], "hipFree": [P],
+            "hipMemcpyAsync": [P, P, S, ctypes.c_int, P], "hipMemset": [P, ctypes.c_int, S],
+        }
+        for n, args in sig.items():
+            fn = getattr(self.L, n)
+            fn.restype = ctypes.c_int
+            fn.argtypes = args
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
 
     def capture(self, stream, body):
         """Record body() (launches on `stream`) into an executable graph, so
         the timed replay is not bound by host launch overhead."""
-        assert self.L.hipStreamBeginCapture(ctypes.c_void_p(stream), 1) == 0  # thread-local mode
+        self.ok(self.L.hipStreamBeginCapture(ctypes.c_void_p(stream), 1), "hipStreamBeginCapture")
         try:
             body()
         finally:
             g = ctypes.c_void_p()
             rc = self.L.hipStreamEndCapture(ctypes.c_void_p(stream), ctypes.byref(g))
-        assert rc == 0, f"hipStreamEndCapture rc={rc}"
+        self.ok(rc, "hipStreamEndCapture")
         ex = ctypes.c_void_p()
-        assert self.L.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0) == 0
+        self.ok(self.L.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0), "hipGraphInstantiate")
         return g, ex
 
     def launch(self, ex, stream):
-        assert self.L.hipGraphLaunch(ex, ctypes.c_void_p(stream)) == 0
+        self.ok(self.L.hipGraphLaunch(ex, ctypes.c_void_p(stream)), "hipGraphLaunch")
 
     def destroy(self, g, ex):
         self.L.hipGraphExecDestroy(ex)
@@ -83,25 +86,33 @@ class Hip:
 
     def event(self):
         e = ctypes.c_void_p()
-        assert self.L.hipEventCreate(ctypes.byref(e)) == 0
+        self.ok(self.L.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
         return e
 
     def record(self, e, stream):
-        assert self.L.hipEventRecord(e, ctypes.c_void_p(stream)) == 0
+        self.ok(self.L.hipEventRecord(e, ctypes.c_void_p(stream)), "hipEventRecord")
 
     def elapsed_ms(self, a, b) -> float:
-        assert self.L.hipEventSynchronize(b) == 0
+        self.ok(self.L.hipEventSynchronize(b), "hipEventSynchronize")
         ms = ctypes.c_float()
-        assert self.L.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        self.ok(self.L.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
         return ms.value
 
-    def sync(self):
-        assert self.L.hipDeviceSynchronize() == 0
-
-
-def gemv_bytes(dt, n, k, t=1):
-    import oracle as O
-    return O.tensor_byte_size(dt, n * k) + 4 * k * t + 4 * n * t
+    def timed_graph(self, stream, body, steps):
+        """Capture `body` (steps launches), replay once untimed, then time one
+        replay with events on `stream`; returns ms per launch."""
+        g, ex = self.capture(stream, body)
+        self.launch(ex, stream)
+        e0, e1 = self.event(), self.event()
+        self.ok(self.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+        self.record(e0, stream)
+        self.launch(ex, stream)
+        self.record(e1, stream)
+        ms = self.elapsed_ms(e0, e1) / steps
+        self.destroy(g, ex)
+        self.L.hipEventDestroy(e0)
+        self.L.hipEventDestroy(e1)
+        return ms
 
 
 def make_weight(seed, dt, n, k):
@@ -109,6 +120,11 @@ def make_weight(seed, dt, n, k):
     rng = np.random.default_rng(seed)
     w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
     return O.quantize(w, dt)
+
+
+def gemv_bytes(dt, n, k, t=1):
+    import oracle as O
+    return O.tensor_byte_size(dt, n * k) + 4 * k * t + 4 * n * t
 
 
 def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
@@ -129,20 +145,13 @@ def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
 
     run(max(1, warmup))  # untimed, eager (also sizes any scratch before capture)
     ctx.synchronize()
-    g, ex = hip.capture(stream, lambda: run(steps))
-    hip.launch(ex, stream)  # untimed replay
+    ms = hip.timed_graph(stream, lambda: run(steps), steps)
     ctx.synchronize()
-    e0, e1 = hip.event(), hip.event()
-    hip.record(e0, stream)
-    hip.launch(ex, stream)
-    hip.record(e1, stream)
-    ms = hip.elapsed_ms(e0, e1) / steps
-    ctx.synchronize()
-    hip.destroy(g, ex)
     res = out.download(np.float32, n * t_rows).reshape(t_rows, n)
     for w in ws:
         w.close()
-    xa.free(); out.free()
+    xa.free()
+    out.free()
     return ms, b, x, res, copies
 
 
@@ -157,8 +166,35 @@ def cpu_baseline(b, x, dt, n, k, budget_s=10.0):
         t0 = time.perf_counter()
         O.mm_batched(x, b, dt, n, k, threads)
         times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return med, threads, len(times)
+    return float(np.median(times)), threads, len(times)
+
+
+def headline_traffic():
+    """HBM bytes per launch of the headline kernel from the committed PMC
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel), or None."""
+    try:
+        text = open(HEADLINE_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(hip, nbytes=256 << 20, reps=8):
+    """Device-to-device copies of a known size: the reference reading for the
+    FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = nbytes)."""
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    hip.ok(hip.L.hipMalloc(ctypes.byref(src), nbytes), "hipMalloc")
+    hip.ok(hip.L.hipMalloc(ctypes.byref(dst), nbytes), "hipMalloc")
+    hip.ok(hip.L.hipMemset(src, 1, nbytes), "hipMemset")
+    hip.ok(hip.L.hipMemset(dst, 0, nbytes), "hipMemset")
+    hip.ok(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    for _ in range(reps):
+        hip.ok(hip.L.hipMemcpyAsync(dst, src, nbytes, 3, None), "hipMemcpyAsync")
+    hip.ok(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    hip.L.hipFree(src)
+    hip.L.hipFree(dst)
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": reps}), flush=True)
 
 
 def main():
@@ -169,16 +205,21 @@ def main():
     ap.add_argument("--mode", choices=["q8", "exact"], default="q8")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only, no per-format sweep")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "run with --gpus 1", file=sys.stderr)
+        print(f"bench.py measures one GPU: every GPU box here has one, and this build has no multi-GPU "
+              f"path (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    hip = Hip()
+    if args.copy_calibration:
+        copy_calibration(hip)
+        return
 
     import oracle as O
     import rce_amd
     from rce_amd import Mode
-    hip = Hip()
     ctx = rce_amd.Context(0)
     mode = Mode.Q8 if args.mode == "q8" else Mode.EXACT
 
@@ -190,10 +231,11 @@ def main():
     gbs = nbytes / (ms * 1e-3) / 1e9
     ref = O.mm_batched(x, b, dt, n, k) if mode == Mode.EXACT else O.mm_batched_q8(x, b, dt, n, k)
     exact_ok = bool(np.array_equal(res.view(np.uint32), ref.view(np.uint32)))
-    log(f"  {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)  parity={exact_ok}")
+    log(f"  {ms * 1e3:.2f} us/launch  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)  "
+        f"bit-identical to the oracle: {exact_ok}")
 
     line = {
-        "metric": "GEMV HBM GB/s (Q4_0 decode, 11008x4096, batch 1)",
+        "metric": "GEMV HBM GB/s (Q4_0 decode 11008x4096, batch 1, Q8 activations)",
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -203,25 +245,27 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 dot (Q8 activations) -> f32" if mode == Mode.Q8 else "f32 (reference order)",
+        "dtype": "int8" if mode == Mode.Q8 else "f32",
         "data": "synthetic: W~N(0,0.02) seeded then GGUF-quantized, x~N(0,1); weights rotated over "
                 f"{copies} HBM copies",
-        "config": {"workload": "configs[1] Q4_0 GEMV 11008x4096 batch 1", "mode": args.mode,
-                   "bytes_per_step": nbytes, "parity_bit_exact": exact_ok},
+        "config": {"workload": "configs[1]: Q4_0 GEMV 11008x4096 batch 1", "mode": args.mode,
+                   "bytes_per_launch": nbytes, "parity_bit_exact": exact_ok},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": headline_traffic() if mode == Mode.Q8 else None},
     }
 
-    # ---- per-format sweep (BASELINE metric is per quant format) ------------------
+    # ---- per-format sweep (the metric is per quant format) -----------------------
     per = {}
     if not args.quick:
         sweep = [
-            ("Q8_0 4096x4096 b1", O.Q8_0, 4096, 4096, 1),
-            ("Q4_0 11008x4096 b1", O.Q4_0, 11008, 4096, 1),
-            ("Q4_0 11008x4096 b8", O.Q4_0, 11008, 4096, 8),
+            ("Q8_0 4096x4096 b1", O.Q8_0, 4096, 4096, 1),      # configs[0] shape
+            ("Q4_0 11008x4096 b1", O.Q4_0, 11008, 4096, 1),    # configs[1]
+            ("Q4_0 11008x4096 b8", O.Q4_0, 11008, 4096, 8),    # configs[1], batch 8
             ("Q4_K 4096x4096 b1", O.Q4_K, 4096, 4096, 1),
-            ("Q4_K 5632x2048 b1", O.Q4_K, 5632, 2048, 1),
-            ("Q6_K 32000x2048 b1", O.Q6_K, 32000, 2048, 1),
+            ("Q4_K 5632x2048 b1", O.Q4_K, 5632, 2048, 1),      # configs[4] FFN shapes
+            ("Q4_K 2048x5632 b1", O.Q4_K, 2048, 5632, 1),
+            ("Q6_K 32000x2048 b1", O.Q6_K, 32000, 2048, 1),    # configs[4] head
         ]
         for name, sdt, sn, sk, st in sweep:
             for m in (Mode.EXACT, Mode.Q8):
@@ -240,7 +284,8 @@ def main():
         med, threads, calls = cpu_baseline(b, x, dt, n, k)
         cpu_gbs = nbytes / med / 1e9
         line["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                                "sample": f"{calls} calls of mm_1d Q4_0 11008x4096 batch 1 (median {med * 1e3:.1f} ms)"}
+                                "sample": f"{calls} calls of mm_1d (f32 activations, reference order) on the "
+                                          f"headline Q4_0 11008x4096 batch-1 workload, median {med * 1e3:.2f} ms"}
         log(f"  cpu {cpu_gbs:.2f} GB/s on {threads} threads")
     ctx.close()
     print(json.dumps(line), flush=True)

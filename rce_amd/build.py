@@ -31,7 +31,7 @@ ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-command-line-argument", f"-I{INCLUDE}", f"-I{CSRC}",
+    "-Wall", "-Wno-unused-command-line-argument", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
 

@@ -1,0 +1,788 @@
+// qmm_gemv_kernels.h -- device code of the decode-shaped kernels of the GGUF
+// quantized-matmul path for gfx950 (CDNA4): GEMV / skinny GEMM in the reference's f32 order (EXACT),
+// the Q8-activation GEMV (Q8), and row dequantization.
+//
+// Work mapping ("activation-stationary").  A row of the weight is U column
+// units (a Q4_0 / Q8_0 block of 32, a Q4_K group of 64, a Q6_K super-block
+// of 256).  Thread `tid` of a block of NT threads owns unit col = tid % U
+// and the rows rsub, rsub + P, ... (rsub = tid / U, P = NT / U) of the
+// block's tile of RT = P * RPL rows, for TB activation rows (tokens).  It
+// keeps its slice of the activations in registers, issues the loads of all
+// RPL rows before doing any arithmetic, and writes one addend per (token,
+// row) -- the reference's per-unit term of the row sum -- to LDS.  After a
+// barrier, one thread per (token, row) folds the U addends in unit order,
+// which is the reference's sequential `sumf += ...` over blocks.  The
+// device layouts (qmm_internal.h) make every wave-wide weight load a
+// contiguous 1 KB read.
+//
+// Exactness (EXACT): every + - * of the reference is one binary32 operation
+// in the same order.  Q4_0's product (n - 8) a is formed as fma(n, a, -8a)
+// when a thread has one token (-8a is exact, the fma rounds (n - 8) a once)
+// and as (float)(n) - 8 (exact) times a otherwise.  All other code is built
+// with -ffp-contract=off.  The Q6_K row sum of the reference is one chain
+// over all positions of the row, so Q6_K EXACT runs one row per lane.
+//
+// Q8: the block quantizes its activation rows into LDS once (4 lanes per
+// block of 32: max |x| by two quad exchanges, then quantize_block(x, false)
+// semantics), every thread copies its units' words to registers, and each
+// per-block sub-sum of the reference becomes dx * (exact int32 dot).
+//
+// This header holds the kernels and launch templates; gemv_<format>.hip
+// instantiate them per weight format (one translation unit each, so they
+// build in parallel) and qmm_gemv.hip holds the host-side planning.
+#pragma once
+
+#include "qmm_internal.h"
+
+#include <cstdlib>
+#include <type_traits>
+
+namespace rce_qmm {
+namespace {
+
+
+constexpr uint32_t NIB = 0x0F0F0F0Fu;
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    _Float16 h;
+    uint16_t b = (uint16_t)bits;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;  // v_cvt_f32_f16: exact, subnormals preserved
+}
+
+// x & m, opaque to the optimizer so that later byte extractions compile to
+// v_cvt_f32_ubyte{0..3} instead of one bitfield extract per nibble.
+__device__ __forceinline__ uint32_t and_opaque(uint32_t x, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(m), "v"(x));
+    return r;
+}
+
+template <int J>
+__device__ __forceinline__ float ubyte(uint32_t x) {
+    return (float)((x >> (8 * J)) & 0xFFu);
+}
+
+__device__ __forceinline__ uint32_t wrd(const uint4 &v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+__device__ __forceinline__ void load_f32x(const float *p, float *v, int n) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int i = 0; i < n / 4; i++) {
+        float4 t = q[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+// Lane exchanges inside a quad of lanes (DPP quad_perm).
+__device__ __forceinline__ int quad_xor1(int x) { return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int quad_xor2(int x) { return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ float quad_xor1f(float x) { return __int_as_float(quad_xor1(__float_as_int(x))); }
+__device__ __forceinline__ float quad_xor2f(float x) { return __int_as_float(quad_xor2(__float_as_int(x))); }
+
+// Byte i (0..11) of a Q4_K super-block's packed scales, the header being the
+// super-block's first 16 bytes (d, dmin, scales[12]).
+__device__ __forceinline__ int k4_sbyte(const uint4 &h, int i) {
+    uint32_t w = i < 4 ? h.y : (i < 8 ? h.z : h.w);
+    return (int)((w >> (8 * (i & 3))) & 0xFFu);
+}
+
+// q4_k_get_scale_min (rce-op-qmm/src/lib.rs L719-728) for the sub-block pair
+// (2g, 2g+1) of group g, with selects instead of indexed byte access (an
+// index that varies per lane would send the header through scratch).
+// Bytes: g<2 reads scales[2g..2g+1] and [2g+4..2g+5]; g>=2 reads
+// scales[2g+4..2g+5] (low/high nibbles) plus the top two bits of
+// scales[2g-4..2g-3] and [2g..2g+1].
+__device__ __forceinline__ void k4_scale_min_pair(const uint4 &h, int g, int &sc1, int &m1, int &sc2,
+                                                  int &m2) {
+    const int sh = 16 * (g & 1);
+    const uint32_t Y = h.y >> sh, Z = h.z >> sh, W = h.w >> sh;  // low 16 bits: the byte pair
+    const uint32_t y0 = Y & 0xFF, y1 = (Y >> 8) & 0xFF, z0 = Z & 0xFF, z1 = (Z >> 8) & 0xFF;
+    const uint32_t w0 = W & 0xFF, w1 = (W >> 8) & 0xFF;
+    if (g < 2) {
+        sc1 = (int)(y0 & 63); sc2 = (int)(y1 & 63);
+        m1 = (int)(z0 & 63); m2 = (int)(z1 & 63);
+    } else {
+        sc1 = (int)((w0 & 0x0F) | ((y0 >> 6) << 4)); sc2 = (int)((w1 & 0x0F) | ((y1 >> 6) << 4));
+        m1 = (int)((w0 >> 4) | ((z0 >> 6) << 4)); m2 = (int)((w1 >> 4) | ((z1 >> 6) << 4));
+    }
+}
+
+// q4_k_get_scale_min (rce-op-qmm/src/lib.rs L719-728), one sub-block j.
+__device__ __forceinline__ void k4_scale_min(const uint4 &h, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = k4_sbyte(h, j) & 63;
+        m = k4_sbyte(h, j + 4) & 63;
+    } else {
+        sc = (k4_sbyte(h, j + 4) & 0x0F) | ((k4_sbyte(h, j - 4) >> 6) << 4);
+        m = (k4_sbyte(h, j + 4) >> 4) | ((k4_sbyte(h, j) >> 6) << 4);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Raw unit loads (one row, one column unit) from the device layouts.
+// ---------------------------------------------------------------------------
+
+struct RawQ4_0 { uint4 q; uint32_t s; };
+struct RawQ8_0 { uint4 q0, q1; uint32_t s; };
+struct RawQ4_K { uint4 h, q0, q1; };
+struct RawQ6_K { uint4 c[13]; uint32_t d; };
+
+__device__ __forceinline__ RawQ4_0 ld_q4_0(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ4_0 r;
+    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    return r;
+}
+
+__device__ __forceinline__ RawQ8_0 ld_q8_0(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ8_0 r;
+    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
+    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    return r;
+}
+
+__device__ __forceinline__ RawQ4_K ld_q4_k(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ4_K r;
+    r.h = *reinterpret_cast<const uint4 *>(rp + 16 * (size_t)(col >> 2));
+    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
+    return r;
+}
+
+// Q6_K super-block sb of row `row` (LAYOUT_IL64_Q6_K: chunk c of rows
+// r..r+63 contiguous, so a wave of 64 rows reads 1 KB per chunk).
+__device__ __forceinline__ void ld_q6_k(const DevWeight &w, size_t row, int sb, RawQ6_K &r) {
+    const uint8_t *sp = w.base + (row >> 6) * w.group_stride + (size_t)sb * IL64_Q6K_SB;
+    const size_t lane = row & 63;
+#pragma unroll
+    for (int j = 0; j < 13; j++) r.c[j] = *reinterpret_cast<const uint4 *>(sp + ((size_t)j * 64 + lane) * 16);
+    r.d = *reinterpret_cast<const uint16_t *>(sp + IL64_Q6K_D + lane * 2);
+}
+
+// The four 6-bit value words (+32 offset, one byte per l) of positions
+// l..l+3 (m = 0), +32 (m = 1), +64 (m = 2), +96 (m = 3) of half o,
+// l = 4 * lq (rce-op-qmm/src/lib.rs L425-454 bit layout: ql = c[0..7],
+// qh = c[8..11]).
+__device__ __forceinline__ void q6_words(const RawQ6_K &b, int o, int lq, uint32_t &u1, uint32_t &u2,
+                                         uint32_t &u3, uint32_t &u4) {
+    const int c = lq >> 2, wi = lq & 3;
+    const uint32_t qa = wrd(b.c[4 * o + c], wi), qb = wrd(b.c[4 * o + 2 + c], wi);
+    const uint32_t qh = wrd(b.c[8 + 2 * o + c], wi);
+    u1 = (qa & NIB) | ((qh & 0x03030303u) << 4);
+    u2 = (qb & NIB) | ((qh & 0x0C0C0C0Cu) << 2);
+    u3 = ((qa >> 4) & NIB) | (qh & 0x30303030u);
+    u4 = ((qb >> 4) & NIB) | ((qh >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ int q6_sc(const uint4 &s, int i) {
+    return (int)(int8_t)((wrd(s, i >> 2) >> (8 * (i & 3))) & 0xFFu);
+}
+
+// ---------------------------------------------------------------------------
+// Q8 activations in LDS: per token t, xq words [k/4], dx [k/32] (the block
+// scale round_to_f16(amax/127)), s16 [k/16] (sums of xq over 16 values).
+// ---------------------------------------------------------------------------
+
+struct ActLds {
+    int *xq;
+    float *dx;
+    int *s16;
+    __device__ ActLds(unsigned char *lds, size_t k, int tb) {
+        xq = reinterpret_cast<int *>(lds);
+        dx = reinterpret_cast<float *>(lds + (size_t)tb * k);
+        s16 = reinterpret_cast<int *>(lds + (size_t)tb * k + (size_t)tb * (k / 32) * 4);
+    }
+};
+
+__host__ __device__ constexpr size_t act_lds_bytes(size_t k, int tb) { return (size_t)tb * (k + k / 8 + k / 4); }
+
+// Round half away from zero (f32::round / C roundf) of |v| <= 2^22, as an
+// integer: v + copysign(pred(0.5), v) in round-to-nearest-even, truncated.
+// Identical to roundf for every finite f32 in that range (checked
+// exhaustively on the CPU, tests/test_round_identity.py); 3 instructions
+// instead of roundf's 6.
+__device__ __forceinline__ int round_half_away(float v) {
+    return (int)(v + __builtin_copysignf(0x1.fffffep-2f, v));
+}
+
+// One task = 8 consecutive activation values of one token; four
+// consecutive tasks (one lane quad) form a block of 32.
+struct QuantTask {
+    float4 v0, v1;
+};
+
+__device__ __forceinline__ void quant_task_load(const float *A, int kq, int t0, int total, int task, QuantTask &q) {
+    // kq = k / 8 tasks per token.  Out-of-range tasks load task 0 (always
+    // valid), so the loads stay unconditional; they come in whole quads
+    // (total is a multiple of 4) and quant_task_finish writes nothing for
+    // them, so their values never reach a valid block.
+    const int tk = task < total ? task : 0;
+    const int t = tk / kq, e = (tk - t * kq) * 8;
+    const float4 *p = reinterpret_cast<const float4 *>(A + (size_t)(t0 + t) * ((size_t)kq * 8) + e);
+    q.v0 = p[0];
+    q.v1 = p[1];
+}
+
+// nn.rs L541-563 quantize_block(x, false) of the quad's block: d = amax/127,
+// id = 1/d (0 when d = 0), q = round half away from zero of x*id; the scale
+// kept is round_to_f16(d) (nn.rs L521-533 = the hardware's RNE conversion).
+// Every lane of the wave must call this (quad exchanges).
+__device__ __forceinline__ void quant_task_finish(const QuantTask &q, size_t k, int total, int task, const ActLds &L) {
+    float v[8] = {q.v0.x, q.v0.y, q.v0.z, q.v0.w, q.v1.x, q.v1.y, q.v1.z, q.v1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, quad_xor1f(amax));
+    amax = fmaxf(amax, quad_xor2f(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int w0 = 0, w1 = 0, s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int qi = round_half_away(v[i] * id);  // |v * id| <= 127
+        s += qi;
+        if (i < 4) w0 |= (int)(((uint32_t)qi & 0xFFu) << (8 * i));
+        else w1 |= (int)(((uint32_t)qi & 0xFFu) << (8 * (i - 4)));
+    }
+    s += quad_xor1(s);  // the sum over this lane's half-block of 16
+    if (task < total) {
+        const size_t e = (size_t)task * 8;  // token-major: t*k + position
+        *reinterpret_cast<int2 *>(L.xq + e / 4) = make_int2(w0, w1);
+        if ((task & 1) == 0) L.s16[e / 16] = s;
+        if ((task & 3) == 0) L.dx[e / 32] = (float)(_Float16)d;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Column units.  TB = tokens per thread.  init_*: the thread's activation
+// slice; addends(raw, out): out[t] = the reference's per-unit term of
+// row sum of token t.
+// ---------------------------------------------------------------------------
+
+// Q4_0 block, EXACT (rce-op-qmm/src/lib.rs L496-522): sub over q in 0..16
+// of (lo_q - 8) a[q] then (hi_q - 8) a[q+16]; addend = scale * sub.
+template <int TB>
+struct Q4_0Exact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_0;
+    float av[TB][32];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // Tokens past tv read token 0's slice (no branch: a load inside
+            // a branch is waited for before the branch joins); their sums
+            // are never folded or stored.
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float sub[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) sub[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = wrd(r.q, i);
+            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float nl = (float)((lo >> (8 * j)) & 0xFFu), nh = (float)((hi >> (8 * j)) & 0xFFu);
+                if constexpr (TB == 1) {
+                    sub[0] = sub[0] + __builtin_fmaf(nl, av[0][4 * i + j], -8.0f * av[0][4 * i + j]);
+                    sub[0] = sub[0] + __builtin_fmaf(nh, av[0][4 * i + j + 16], -8.0f * av[0][4 * i + j + 16]);
+                } else {
+                    const float vl = nl - 8.0f, vh = nh - 8.0f;  // exact
+#pragma unroll
+                    for (int t = 0; t < TB; t++) {
+                        sub[t] = sub[t] + vl * av[t][4 * i + j];
+                        sub[t] = sub[t] + vh * av[t][4 * i + j + 16];
+                    }
+                }
+            }
+        }
+        const float scale = h2f(r.s);
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
+    }
+};
+
+// Q8_0 block, EXACT (rce-op-qmm/src/lib.rs L315-328, L648-670).
+template <int TB>
+struct Q8_0Exact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ8_0;
+    float av[TB][32];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q8_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // Tokens past tv read token 0's slice (no branch: a load inside
+            // a branch is waited for before the branch joins); their sums
+            // are never folded or stored.
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float sub[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) sub[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float v = (float)(int8_t)(x >> (8 * j));
+#pragma unroll
+                for (int t = 0; t < TB; t++) sub[t] = sub[t] + v * av[t][4 * i + j];
+            }
+        }
+        const float scale = h2f(r.s);
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
+    }
+};
+
+// Q4_K group g of a super-block, EXACT (rce-op-qmm/src/lib.rs L354-385,
+// L730-781): va_lo, a_lo, va_hi, a_hi over l in 0..32 from +0.0, then
+// ((d1 va_lo - min1 a_lo) + d2 va_hi) - min2 a_hi.  a_lo and a_hi do not
+// depend on the row and are formed once per thread, in the same order.
+template <int TB>
+struct Q4_KExact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_K;
+    float av[TB][64];
+    float a_lo[TB], a_hi[TB];
+    int g;
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_k(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+        g = col & 3;
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // Tokens past tv read token 0's slice (no branch: a load inside
+            // a branch is waited for before the branch joins); their sums
+            // are never folded or stored.
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 64 * (size_t)col, av[t], 64);
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            a_lo[t] = 0.0f;
+            a_hi[t] = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 32; l++) { a_lo[t] = a_lo[t] + av[t][l]; a_hi[t] = a_hi[t] + av[t][32 + l]; }
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        int sc1, m1, sc2, m2;
+        k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
+        const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+        const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+        float va_lo[TB], va_hi[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) { va_lo[t] = 0.0f; va_hi[t] = 0.0f; }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float vl = (float)((lo >> (8 * j)) & 0xFFu), vh = (float)((hi >> (8 * j)) & 0xFFu);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    va_lo[t] = va_lo[t] + vl * av[t][4 * i + j];
+                    va_hi[t] = va_hi[t] + vh * av[t][32 + 4 * i + j];
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            float s = d1 * va_lo[t];
+            s = s - min1 * a_lo[t];
+            s = s + d2 * va_hi[t];
+            s = s - min2 * a_hi[t];
+            out[t] = s;
+        }
+    }
+};
+
+// Q4_0 / Q8_0 block, Q8: sub = dx * isum, addend = scale * sub.
+template <int TB, bool IS_Q4>
+struct Q32Q8 {
+    static constexpr int NTOK = TB;
+    using Raw = typename std::conditional<IS_Q4, RawQ4_0, RawQ8_0>::type;
+    int xq[TB][8];
+    float dx[TB];
+    int xs[TB];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
+        if constexpr (IS_Q4) return ld_q4_0(w, row, col);
+        else return ld_q8_0(w, row, col);
+    }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 32 * (size_t)col) / 4);
+            const int4 a = p[0], b = p[1];
+            const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) xq[t][i] = ok ? v[i] : 0;
+            dx[t] = ok ? L.dx[tt * (k / 32) + col] : 0.0f;
+            xs[t] = ok ? L.s16[tt * (k / 16) + 2 * col] + L.s16[tt * (k / 16) + 2 * col + 1] : 0;
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        const float scale = h2f(r.s);
+        if constexpr (IS_Q4) {
+            int lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) { lo[i] = (int)(wrd(r.q, i) & NIB); hi[i] = (int)((wrd(r.q, i) >> 4) & NIB); }
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                int acc = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(lo[i], xq[t][i], acc, false);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(hi[i], xq[t][4 + i], acc, false);
+                const float sub = dx[t] * (float)(acc - 8 * xs[t]);
+                out[t] = scale * sub;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                int acc = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4((int)wrd(r.q0, i), xq[t][i], acc, false);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4((int)wrd(r.q1, i), xq[t][4 + i], acc, false);
+                const float sub = dx[t] * (float)acc;
+                out[t] = scale * sub;
+            }
+        }
+    }
+};
+
+// Q4_K group, Q8: va = dx * isum, a = dx * (sum of xq); then the EXACT
+// group formula.
+template <int TB>
+struct Q4_KQ8 {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_K;
+    int xl[TB][8], xh[TB][8];
+    float dl[TB], dh[TB];
+    int sl[TB], sh[TB];
+    int g;
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_k(w, row, col); }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
+        g = col & 3;
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            // tokens past tv read token 0's slice and are zeroed (no branch)
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 64 * (size_t)col) / 4);
+            const int4 a = p[0], b = p[1], c = p[2], e = p[3];
+            const int v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) { xl[t][i] = ok ? v[i] : 0; xh[t][i] = ok ? v[8 + i] : 0; }
+            const size_t b32 = tt * (k / 32) + 2 * (size_t)col, b16 = tt * (k / 16) + 4 * (size_t)col;
+            dl[t] = ok ? L.dx[b32] : 0.0f;
+            dh[t] = ok ? L.dx[b32 + 1] : 0.0f;
+            sl[t] = ok ? L.s16[b16] + L.s16[b16 + 1] : 0;
+            sh[t] = ok ? L.s16[b16 + 2] + L.s16[b16 + 3] : 0;
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        int sc1, m1, sc2, m2;
+        k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
+        const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+        const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+        int lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+            lo[i] = (int)(x & NIB);
+            hi[i] = (int)((x >> 4) & NIB);
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            int il = 0, ih = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                il = __builtin_amdgcn_sdot4(lo[i], xl[t][i], il, false);
+                ih = __builtin_amdgcn_sdot4(hi[i], xh[t][i], ih, false);
+            }
+            const float va_lo = dl[t] * (float)il, a_lo = dl[t] * (float)sl[t];
+            const float va_hi = dh[t] * (float)ih, a_hi = dh[t] * (float)sh[t];
+            float s = d1 * va_lo;
+            s = s - min1 * a_lo;
+            s = s + d2 * va_hi;
+            s = s - min2 * a_hi;
+            out[t] = s;
+        }
+    }
+};
+
+// Q6_K super-block, Q8: for sub-blocks b of 16 ascending,
+// ssb += (d sc_b) (dx isum_b) from +0.0; the addend is ssb.
+template <int TB>
+struct Q6_KQ8 {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ6_K;
+    int xw[TB][64];
+    float dx[TB][8];
+    int s16[TB][16];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
+        Raw r;
+        ld_q6_k(w, row, col, r);
+        return r;
+    }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 256 * (size_t)col) / 4);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int4 v = p[i];
+                xw[t][4 * i] = ok ? v.x : 0; xw[t][4 * i + 1] = ok ? v.y : 0;
+                xw[t][4 * i + 2] = ok ? v.z : 0; xw[t][4 * i + 3] = ok ? v.w : 0;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) dx[t][i] = ok ? L.dx[tt * (k / 32) + 8 * (size_t)col + i] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) s16[t][i] = ok ? L.s16[tt * (k / 16) + 16 * (size_t)col + i] : 0;
+        }
+    }
+    __device__ void addends(const Raw &b, float *out) const {
+        const float d = h2f(b.d);
+        float ssb[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) ssb[t] = 0.0f;
+#pragma unroll
+        for (int o = 0; o < 2; o++) {
+            int acc[TB][8];  // sub-block 8o + 2m + c -> index 2m + c
+#pragma unroll
+            for (int t = 0; t < TB; t++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[t][i] = 0;
+#pragma unroll
+            for (int lq = 0; lq < 8; lq++) {
+                uint32_t u[4];
+                q6_words(b, o, lq, u[0], u[1], u[2], u[3]);
+                const int c = lq >> 2, wi = lq & 3;
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+#pragma unroll
+                    for (int t = 0; t < TB; t++)
+                        acc[t][2 * m + c] = __builtin_amdgcn_sdot4((int)u[m], xw[t][32 * o + 8 * m + 4 * c + wi],
+                                                                   acc[t][2 * m + c], false);
+                }
+            }
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) {
+                const int sbk = 8 * o + bb;
+                const float ds = d * (float)q6_sc(b.c[12], sbk);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    const int isum = acc[t][bb] - 32 * s16[t][sbk];
+                    const float ab = dx[t][sbk >> 1] * (float)isum;
+                    ssb[t] = ssb[t] + ds * ab;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = ssb[t];
+    }
+};
+
+// ---------------------------------------------------------------------------
+// The activation-stationary kernel.
+// ---------------------------------------------------------------------------
+
+__host__ __device__ constexpr int fold_ld(int U) { return ((U + 3) & ~3) + 4; }
+
+// Dynamic LDS a block may use (the default per-block limit).
+constexpr size_t LDS_MAX = 64 * 1024;
+
+inline size_t gemv_lds_bytes(int U, int nt, int rpl, int tb, bool q8, size_t k) {
+    // the tile's addends plus one dummy row written by idle lanes
+    const size_t fold = ((size_t)tb * (size_t)(nt / U) * rpl + 1) * fold_ld(U) * sizeof(float);
+    const size_t act = q8 ? act_lds_bytes(k, tb) : 0;
+    return fold > act ? fold : act;
+}
+
+template <class Unit, int NT, int RPL, bool Q8>
+__global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__restrict__ A, float *__restrict__ out,
+                                                int t_rows, int U) {
+    constexpr int TB = Unit::NTOK;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x;
+    const int P = NT / U;
+    const int col = tid % U, rsub = tid / U;
+    const bool active = rsub < P;
+    const int RT = P * RPL;
+    const size_t row0 = (size_t)blockIdx.x * RT;
+    const int t0 = blockIdx.y * TB;
+    const int tv = min(TB, t_rows - t0);
+    const size_t k = w.n_cols;
+
+    Unit unit;
+    // Phase 1: activation loads first (they are not behind the weights in
+    // the in-order load counter), then every weight load of the thread.
+    // No load sits in a branch (the compiler waits for a load made inside
+    // a branch before the branch joins, which would serialize the rows):
+    // rows past the end, and idle lanes, load a valid row and are dropped.
+    QuantTask qt0, qt1;
+    const int kq = (int)(k / 8);
+    const int qtotal = Q8 ? tv * kq : 0;
+    if constexpr (Q8) {
+        quant_task_load(A, kq, t0, qtotal, tid, qt0);
+        quant_task_load(A, kq, t0, qtotal, tid + NT, qt1);
+    } else {
+        unit.init(A, k, t0, tv, col);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weights'
+    typename Unit::Raw raw[RPL];
+    const int rs = active ? rsub : P - 1;
+#pragma unroll
+    for (int u = 0; u < RPL; u++) {
+        const size_t r = row0 + (size_t)(u * P + rs);
+        raw[u] = Unit::load(w, r < w.n_rows ? r : w.n_rows - 1, col);
+    }
+    // Keep every load above ahead of any arithmetic on loaded data.
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase 2 (Q8): quantize the block's activation rows into LDS.
+    if constexpr (Q8) {
+        ActLds L(lds, k, TB);
+        quant_task_finish(qt0, k, qtotal, tid, L);
+        quant_task_finish(qt1, k, qtotal, tid + NT, L);
+        for (int base = 2 * NT; base < qtotal; base += NT) {
+            QuantTask q;
+            quant_task_load(A, kq, t0, qtotal, base + tid, q);
+            quant_task_finish(q, k, qtotal, base + tid, L);
+        }
+        __syncthreads();
+        if (active) unit.init_q8(L, k, tv, col);
+        __syncthreads();  // the fold below reuses the LDS
+    }
+    // Phase 3: per-unit addends of every (token, row) to LDS.
+    float *part = reinterpret_cast<float *>(lds);
+    const int ld = fold_ld(U);
+#pragma unroll
+    for (int u = 0; u < RPL; u++) {
+        // Every lane computes and stores (idle lanes into a dummy row past
+        // the tile), so no load is sunk into a guarded branch.
+        float ad[TB];
+        unit.addends(raw[u], ad);
+        const int r = u * P + rsub;
+        const bool in = row0 + r < w.n_rows;
+#pragma unroll
+        for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = in ? ad[t] : 0.0f;
+    }
+    __syncthreads();
+    // Phase 4: the reference's fold, one thread per (token, row).
+    for (int j = tid; j < tv * RT; j += NT) {
+        const int t = j / RT, r = j % RT;
+        if (row0 + r < w.n_rows) {
+            const float *pp = part + (t * RT + r) * ld;
+            const float4 *p4 = reinterpret_cast<const float4 *>(pp);
+            float s = 0.0f;
+            const int U4 = U >> 2;
+#pragma unroll 8
+            for (int c = 0; c < U4; c++) {
+                const float4 v = p4[c];
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+            for (int c = U4 * 4; c < U; c++) s = s + pp[c];
+            out[((size_t)t0 + t) * w.n_rows + row0 + r] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launch geometry.
+// ---------------------------------------------------------------------------
+
+inline int units_per_row(uint32_t dtype, size_t n_cols) {
+    switch (dtype) {
+    case T_Q4_0: case T_Q8_0: return (int)(n_cols / 32);
+    case T_Q4_K: return (int)(n_cols / 64);
+    case T_Q6_K: return (int)(n_cols / 256);
+    default: return 0;
+    }
+}
+
+inline int nt_for(int U) { return U <= 256 ? 256 : (U <= 512 ? 512 : 1024); }
+
+template <class Unit, int NT, int RPL, bool Q8>
+hipError_t launch_as(const DevWeight &w, int U, const float *a, size_t t_rows, float *out, hipStream_t s) {
+    constexpr int TB = Unit::NTOK;
+    const int P = NT / U, RT = P * RPL;
+    if (P < 1) return hipErrorInvalidConfiguration;
+    const size_t lds = gemv_lds_bytes(U, NT, RPL, TB, Q8, w.n_cols);
+    if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
+    dim3 grid((unsigned)((w.n_rows + RT - 1) / RT), (unsigned)((t_rows + TB - 1) / TB)), block(NT);
+    hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8>), grid, block, lds, s, w, a, out, (int)t_rows, U);
+    return hipGetLastError();
+}
+
+template <class Unit, bool Q8>
+hipError_t launch_as_nt(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                        hipStream_t s) {
+    const int U = units_per_row(w.dtype, w.n_cols);
+#define RCE_RPL(NT)                                                                        \
+    switch (g.rpl) {                                                                       \
+    case 2: return launch_as<Unit, NT, 2, Q8>(w, U, a, t_rows, out, s);                    \
+    case 4: return launch_as<Unit, NT, 4, Q8>(w, U, a, t_rows, out, s);                    \
+    case 8: return launch_as<Unit, NT, 8, Q8>(w, U, a, t_rows, out, s);                    \
+    case 12: return launch_as<Unit, NT, 12, Q8>(w, U, a, t_rows, out, s);                  \
+    case 16: return launch_as<Unit, NT, 16, Q8>(w, U, a, t_rows, out, s);                  \
+    default: return hipErrorInvalidValue;                                                  \
+    }
+    switch (g.nt) {
+    case 256: RCE_RPL(256)
+    case 512: RCE_RPL(512)
+    case 1024: RCE_RPL(1024)
+    default: return hipErrorInvalidValue;
+    }
+#undef RCE_RPL
+}
+
+// MAXTB: the most tokens per thread the unit's registers allow.
+template <template <int> class Unit, bool Q8, int MAXTB>
+hipError_t launch_as_tb(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                        hipStream_t s) {
+    switch (g.tb) {
+    case 1: return launch_as_nt<Unit<1>, Q8>(w, g, a, t_rows, out, s);
+    case 2:
+        if constexpr (MAXTB >= 2) return launch_as_nt<Unit<2>, Q8>(w, g, a, t_rows, out, s);
+        return hipErrorInvalidValue;
+    case 4:
+        if constexpr (MAXTB >= 4) return launch_as_nt<Unit<4>, Q8>(w, g, a, t_rows, out, s);
+        return hipErrorInvalidValue;
+    case 8:
+        if constexpr (MAXTB >= 8) return launch_as_nt<Unit<8>, Q8>(w, g, a, t_rows, out, s);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int TB> using Q4_0Q8 = Q32Q8<TB, true>;
+template <int TB> using Q8_0Q8 = Q32Q8<TB, false>;
+
+
+}  // namespace
+}  // namespace rce_qmm

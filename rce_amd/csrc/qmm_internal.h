@@ -1,5 +1,5 @@
 // qmm_internal.h -- internal interface between the C ABI (qmm_abi.cpp) and
-// the HIP kernels (qmm_gemv.hip).  Not installed; callers use
+// the HIP kernels (qmm_gemv.hip, gemv_<format>.hip).  Not installed; callers use
 // include/rce_qmm.h.
 #pragma once
 
@@ -73,6 +73,15 @@ hipError_t launch_f16_to_f32(const uint16_t *src, float *dst, size_t n, hipStrea
 hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float *out, int mode,
                        hipStream_t s, const GemvGeom *geom = nullptr);
 GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode);
+// Per-format launchers (gemv_<format>.hip), shape already chosen.
+hipError_t launch_gemv_q4_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q8_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q4_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
 
 }  // namespace rce_qmm
