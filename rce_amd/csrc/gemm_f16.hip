@@ -1,0 +1,566 @@
+// gemm_f16.hip -- prefill-shaped GEMM of the GGUF quantized-matmul path on
+// the CDNA4 matrix cores: out[M, N] = A[M, K] . W[N, K]^T with W in GGUF
+// Q4_K or Q4_0 blocks, dequantized to binary16 MFMA fragments in registers
+// and contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
+//
+// Tiling.  A block of 512 threads owns a 128 x 64 (M x N) output tile, so a
+// 512 x 4096 product is 256 tiles: one per CU.  K runs in chunks of 64 (four
+// MFMA k-steps of 16).  Wave w = 2*kq + t computes k-step kq of every chunk
+// for the 128 x 32 sub-tile of columns 32t.. (4 x 1 MFMA blocks of 32 x 32):
+// per chunk it reads four A fragments from LDS, dequantizes its one W
+// fragment itself from the raw GGUF nibbles in LDS (each W nibble is
+// dequantized by exactly one wave; no B tile is written), and issues four
+// MFMAs.  The four k-step partial sums of each output are added at the end
+// through LDS in a fixed order (deterministic).
+//
+// Balance (measured on MI355X).  Dequantizing one 8-nibble fragment costs
+// ~16 VALU ops, four of them v_pk_fma_f16 at half rate (~80 SIMD cycles);
+// four MFMAs are 128 cycles; a CU's global->LDS path moves ~64 B/cycle.
+// Feeding each fragment to four MFMAs (128 rows) keeps the VALU below the
+// MFMA time; the 18.7 KB of A and W a CU loads per chunk is about the same
+// time again.  LDS offsets are immediates off per-chunk base registers, and
+// the per-sub-block fma scales are computed once per CU per scale group
+// (from the GGUF header) into LDS.
+//
+// Global -> LDS traffic uses gfx950 global_load_lds_dwordx4 (16 bytes per
+// lane, no registers).  Its throughput is set by the 64-byte segments an
+// instruction touches, so every load covers whole segments:
+//   * A: 8 rows x 128 bytes (one chunk of a row) per instruction, stored
+//     XOR-swizzled (16-byte column g of row r at slot g ^ f(r),
+//     f(r) = (r & 7) ^ ((r >> 3) & 1)) so the MFMA fragment reads (32 rows,
+//     one column) are bank-conflict free whether 8 or 16 lanes are served
+//     per LDS cycle;
+//   * W: per scale group (four chunks: one Q4_K super-block, eight Q4_0
+//     blocks) each row's 2 x 64 bytes of nibbles (16-byte pieces rotated by
+//     (row >> 2) & 3) and its 16-byte scale header, loaded three groups
+//     ahead into four group buffers.
+// Pipeline per chunk c (one barrier each): loads of A chunk c + NS - 1 and
+// of part of a W group; LDS reads of chunk c+1's A fragments and chunk
+// c+2's nibbles; dequantization of chunk c+1 interleaved with chunk c's
+// MFMAs.  Every wave issues the same loads per chunk, so a compile-time
+// s_waitcnt vmcnt immediate per chunk position fits all waves.
+//
+// K order.  Any permutation of K inside a chunk is a valid contraction if A
+// and W use the same one.  Lane half h (= lane / 32) of k-step kq holds the
+// nibbles of the 8 bytes 8h..8h+7 of one 16-byte piece (low nibbles for
+// even kq, high for odd); the A fragment is the matching 8 K positions:
+//   Q4_K (64-group q of a super-block; positions 0..31 = low nibbles of qs
+//   bytes 0..31, 32..63 = high; rce-op-qmm/src/lib.rs L354-385): kq 0, 1 =
+//   low, high nibbles of bytes 0..15; kq 2, 3 = bytes 16..31;
+//   Q4_0 (blocks 2q, 2q+1; block positions 0..15 = low nibbles of its 16
+//   bytes, 16..31 = high; L496-522): kq 0, 1 = block 2q, kq 2, 3 = 2q+1.
+//
+// Dequantization (binary16: the "fp16-dequant MFMA" mode).  A nibble n
+// becomes f16(1024 + n) by a byte permute with 0x64, minus 1024 (exact),
+// then one packed f16 fma: Q4_K d1*n + (-min1) with d1 = f16(d*sc),
+// min1 = f16(dmin*m) (the reference's scales, rounded to f16); Q4_0
+// d*n + (-8d), which is d*(n - 8) exact before its single rounding.  The
+// result differs from the reference's f32 order by the f16 rounding of the
+// weights (normwise about 7e-4 at the Q4_K prefill shape; the stated budget
+// is 2e-3) and is deterministic: each output's summation order is fixed.
+#include "qmm_internal.h"
+
+#include <type_traits>
+
+namespace rce_qmm {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int BM = 128, BN = 64, KC = 64, NT = 512;
+constexpr int NS = 6;                            // A stages (chunks), loaded NS - 1 ahead
+constexpr int A_STAGE = BM * KC * 2;             // 16 KB
+constexpr int W_HALF = BN * 64;                  // 4 KB: 64 rows x 4 chunks x 16 B
+constexpr int W_GROUP = 2 * W_HALF + BN * 16;    // + 1 KB of scale headers
+constexpr int NWBUF = 4, GA = 3;                 // W groups loaded GA groups ahead
+constexpr int SC_BUF = BN * 2 * 16;              // [column][set][chunk] of f16 {scale, bias}
+constexpr int OFF_W = NS * A_STAGE;
+constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
+constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
+constexpr int RED_LDS = 8 * 4 * 16 * 64 * 4;     // partial sums: 8 waves x 64 floats x 64 lanes
+constexpr int GEMM_LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
+static_assert(GEMM_LDS + BM * 4 <= 160 * 1024, "LDS budget");
+// W group g must be complete at the barrier of chunk 4g-4 (its headers are
+// read there): its last load (iteration 4(g-GA)+1) precedes the loads of A
+// chunk 4g-3 (iteration 4g-3-(NS-1)).
+static_assert(4 * GA >= NS + 3, "W groups loaded too late for the stage depth");
+// W buffer (g+GA) % NWBUF, refilled from iteration 4g, was last read for
+// chunk 4g-1 (iteration 4g-3).
+static_assert(NWBUF == GA + 1, "W buffer ring");
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    _Float16 h;
+    uint16_t b = (uint16_t)bits;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+__device__ __forceinline__ half2v as_h2(uint32_t u) {
+    half2v h;
+    __builtin_memcpy(&h, &u, 4);
+    return h;
+}
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
+    const half2v h = {lo, hi};
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
+}
+
+// One 16-byte load from global memory straight into LDS at
+// lds_wave + 16 * lane (lds_wave must be the same for the whole wave).
+__device__ __forceinline__ void load_lds16(const void *g, unsigned char *lds_wave) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)g,
+                                     (void __attribute__((address_space(3))) *)lds_wave, 16, 0, 0);
+}
+
+// LDS accesses of the pipelined loop are inline ds_read / ds_write: the
+// compiler counts the global->LDS loads as writes to all of LDS and would
+// wait for every load in flight before each LDS access (the whole
+// pipeline).  Their completion is waited for explicitly instead
+// (wait_lgkm0 below).  OFF is the instruction's immediate byte offset.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <int OFF>
+__device__ __forceinline__ half8 lds_read_frag(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    half8 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read16(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read8(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+__device__ __forceinline__ void lds_write4(uint32_t a, uint32_t v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(a), "v"(v) : "memory");
+}
+// s_waitcnt lgkmcnt(0), then an empty asm that "redefines" each register
+// the reads above filled, so no use of them can move ahead of the wait.
+template <class T>
+__device__ __forceinline__ void pin(T &r) {
+    asm volatile("" : "+v"(r));
+}
+template <class... R>
+__device__ __forceinline__ void wait_lgkm0(R &...r) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    (pin(r), ...);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt not waited for),
+// then a barrier without the memory fence __syncthreads would add (that
+// fence waits for every load in flight, the whole pipeline).
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+    __builtin_amdgcn_s_barrier();
+}
+
+// Four nibbles (one per byte of x, already masked to 0..15) as two f16
+// pairs in byte order: value = s * n + b (packed f16 fma, one rounding),
+// with sb = f16 {s, b}.  Eight VALU ops; two calls make one MFMA fragment.
+__device__ __forceinline__ void dequant4(uint32_t x, uint32_t sb, half2v &lo, half2v &hi) {
+    pin(x);  // empty volatile asm on the input and the outputs: this code stays where it is written
+    const uint32_t K64 = 0x64646464u;
+    const half2v m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v p = as_h2(sb);
+    const half2v sc = __builtin_shufflevector(p, p, 0, 0), bias = __builtin_shufflevector(p, p, 1, 1);
+    // byte pairs (n, 0x64): f16 bits 0x64nn = 1024 + n
+    const uint32_t p0 = __builtin_amdgcn_perm(x, K64, 0x00050004u);
+    const uint32_t p1 = __builtin_amdgcn_perm(x, K64, 0x00070006u);
+    lo = __builtin_elementwise_fma(as_h2(p0) + m1024, sc, bias);
+    hi = __builtin_elementwise_fma(as_h2(p1) + m1024, sc, bias);
+    pin(lo);
+    pin(hi);
+}
+
+__device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
+    return half8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// --- weight formats ----------------------------------------------------------
+// A scale group is four chunks.  Per row it is two 64-byte halves of
+// nibbles and a 16-byte header:
+//   half_off(w, g, hf): byte offset inside a row of half hf of group g;
+//   hdr_off(g): byte offset of group g's 16-byte header;
+//   half_of(q, kq), piece_of(q, kq): the half and 16-byte piece (0..3)
+//     holding k-step kq of chunk q of the group;
+//   acol(kq): the 16-byte A column (0..7 within the chunk) of lane half 0;
+//   sidx(kq): which of a column's two scale sets k-step kq uses;
+//   scale<q>(hdr, si): f16 {scale, bias} of set si for chunk q.
+
+// Q4_K: halves = qs bytes 0..15 (plane 1) and 16..31 (plane 2) of the
+// super-block's four 64-groups; header = d, dmin, 12 scale bytes; scale
+// set 0 / 1 = the low / high nibble sub-block of each 64-group.
+struct Q4K {
+    __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
+        return (hf ? w.plane2 : w.plane1) + 64 * (size_t)g;
+    }
+    __device__ static size_t hdr_off(int g) { return 16 * (size_t)g; }
+    __device__ static int half_of(int, int kq) { return kq >> 1; }
+    __device__ static int piece_of(int q, int) { return q; }
+    __device__ static int acol(int kq) { return (kq & 1) * 4 + (kq >> 1) * 2; }
+    __device__ static int sidx(int kq) { return kq & 1; }
+    // q4_k_get_scale_min (rce-op-qmm/src/lib.rs L719-728) of sub-block
+    // j = 2q + si (q a constant, si = 0 or 1): the 12 scale bytes are header
+    // bytes 4..15 = words y, z, w
+    template <int Q>
+    __device__ static uint32_t scale(const u32x4 &h, int si) {
+        const int sh = 8 * (2 * (Q & 1) + si);  // byte (j & 3) of a word
+        uint32_t sc, m;
+        if constexpr (Q < 2) {  // j < 4
+            sc = (h.y >> sh) & 63;
+            m = (h.z >> sh) & 63;
+        } else {
+            const uint32_t hw = h.w >> sh;
+            sc = (hw & 0x0F) | (((h.y >> sh) >> 6 & 3) << 4);
+            m = (hw >> 4 & 0x0F) | (((h.z >> sh) >> 6 & 3) << 4);
+        }
+        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+        return pack_h2((_Float16)(d * (float)sc), (_Float16)(-(dmin * (float)m)));
+    }
+};
+
+// Q4_0: halves = the 16-byte nibble runs of blocks 8g..8g+3 and 8g+4..8g+7;
+// header = their eight f16 scales; scale set 0 / 1 = block 2q / 2q+1.
+// d * (n - 8) = d*n + (-8d) (-8d exact; the fma rounds once).
+struct Q40 {
+    __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
+        return w.plane1 + 128 * (size_t)g + 64 * hf;
+    }
+    __device__ static size_t hdr_off(int g) { return 16 * (size_t)g; }
+    __device__ static int half_of(int q, int) { return q >> 1; }
+    __device__ static int piece_of(int q, int kq) { return 2 * (q & 1) + (kq >> 1); }
+    __device__ static int acol(int kq) { return 2 * kq; }
+    __device__ static int sidx(int kq) { return kq >> 1; }
+    template <int Q>
+    __device__ static uint32_t scale(const u32x4 &h, int si) {
+        const uint32_t wd = Q == 0 ? h.x : Q == 1 ? h.y : Q == 2 ? h.z : h.w;  // scales 2q, 2q+1
+        const uint16_t bits = (uint16_t)(wd >> (16 * si));
+        _Float16 d;
+        __builtin_memcpy(&d, &bits, 2);
+        return pack_h2(d, (_Float16)(-8.0f * (float)d));
+    }
+};
+
+// Loads issued by iteration `it`, in order: the W load of position it % 4
+// (a row half at position 0, headers at 1, none at 2 and 3), then the two
+// A loads of chunk it + NS - 1.
+__host__ __device__ constexpr int w_loads(int q) { return (q & 3) < 2 ? 1 : 0; }
+// vmcnt immediate for the barrier of chunk position q: the loads a wave
+// issued after chunk c+1's A loads, i.e. those of iterations c+3-NS .. c-1.
+__host__ __device__ constexpr int vm_after(int q) {
+    int n = 0;
+    for (int d = 1; d <= NS - 3; d++) n += 2 + w_loads(q - d);
+    return n;
+}
+
+template <int U>
+using ic = std::integral_constant<int, U>;
+
+template <class Fmt>
+__global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__restrict__ A, const int *__restrict__ gather,
+                                                 size_t M, float *__restrict__ out, int m_tiles) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int arow[BM];
+    const size_t N = w.n_rows, K = w.n_cols;
+    // Blocks are dispatched round-robin over 8 XCDs; consecutive logical
+    // tiles (the m-tiles of one n-tile, sharing W rows) go to one XCD.
+    const int G = gridDim.x, L = blockIdx.x;
+    const int logical = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
+    const int mt = logical % m_tiles, nt = logical / m_tiles;
+    const size_t m0 = (size_t)mt * BM, n0 = (size_t)nt * BN;
+    const int nchunks = (int)(K / KC), ngroups = nchunks / 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = wave & 1, kq = wave >> 1;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    if (tid < BM) {
+        size_t m = m0 + tid;
+        m = m < M ? m : M - 1;  // rows past M load the last row
+        arow[tid] = gather ? gather[m] : (int)m;
+    }
+    __syncthreads();
+
+    // Loads: a uniform base (kernel argument + per-chunk offset) plus this
+    // lane's loop-invariant 32-bit offset (the host checks the ranges).
+    //   A: instruction i covers rows 16*wave + 8i .. +7, 8 lanes per row;
+    //      lane slot p holds column p ^ f(row)
+    uint32_t a_lane[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int ar = 16 * wave + 8 * i + (lane >> 3);
+        const int aswz = (ar & 7) ^ ((ar >> 3) & 1);
+        a_lane[i] = (uint32_t)arow[ar] * (uint32_t)(2 * K) + 16u * (uint32_t)((lane & 7) ^ aswz);
+    }
+    const uint8_t *const abase = reinterpret_cast<const uint8_t *>(A);
+    //   W: wave w loads half w / 4 of rows 16*(w % 4) .. +15, 4 lanes per
+    //      row, slot p holding piece p ^ ((row >> 2) & 3); headers: rows
+    //      8*w + lane for lanes 0..7
+    const int w_hf = wave >> 2;
+    const int wr = 16 * (wave & 3) + (lane >> 2);
+    size_t wrow = n0 + wr;
+    wrow = wrow < N ? wrow : N - 1;  // rows past the end load the last row
+    const uint32_t w_lane = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
+    size_t hrow = n0 + 8 * wave + (lane & 7);
+    hrow = hrow < N ? hrow : N - 1;
+    const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
+    const uint8_t *const wbase = w.base;
+
+    // Loads of (virtual) iteration it: W position it % 4 of group it/4 + GA,
+    // then A chunk it + NS - 1.  Past-the-end groups and chunks reload
+    // group / chunk 0 (keeps every wave's load count fixed).
+    auto issue_w = [&](int it) {
+        const int q = it & 3;
+        if (q >= 2) return;
+        const int g = (it >> 2) + GA;
+        const int gs = g < ngroups ? g : 0;
+        unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
+        if (q == 0) {
+            load_lds16(wbase + Fmt::half_off(w, gs, w_hf) + w_lane, dst + w_hf * W_HALF + (wave & 3) * 1024);
+        } else if (lane < 8) {
+            load_lds16(wbase + Fmt::hdr_off(gs) + h_lane, dst + 2 * W_HALF + wave * 128);
+        }
+    };
+    auto issue_a = [&](int it) {
+        const int c = it + NS - 1;
+        const int cs = c < nchunks ? c : 0;
+        unsigned char *dst = lds + (c % NS) * A_STAGE + wave * 2048;
+#pragma unroll
+        for (int i = 0; i < 2; i++) load_lds16(abase + (size_t)cs * (KC * 2) + a_lane[i], dst + i * 1024);
+    };
+
+    // LDS read addresses of this lane; A row block i is +32 rows (+4096
+    // bytes): immediates.
+    const uint32_t lds0 = lds_addr(lds);
+    const int g0 = Fmt::acol(kq) + h;
+    const uint32_t a_rd = lds0 + (uint32_t)(l32 * 128 + 16 * (g0 ^ ((l32 & 7) ^ ((l32 >> 3) & 1))));
+    const int ncol = 32 * t + l32;  // tile column of this lane
+    uint32_t w_rd[4];               // nibbles of chunk position q, lane half h (group buffer 0)
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
+                                            16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
+    const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((ncol * 2 + Fmt::sidx(kq)) * 16);
+    // Scale producers: thread = column tid % 64, set wave % 2, chunk wave / 2
+    // (set and chunk are wave-uniform).
+    const int p_col = tid & (BN - 1), p_si = wave & 1, p_q = wave >> 1;
+    const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
+    const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_col * 2 + p_si) * 16 + p_q * 4);
+    auto make_scales = [&](const u32x4 &hdr, int g) {
+        uint32_t v;
+        switch (p_q) {
+        case 0: v = Fmt::template scale<0>(hdr, p_si); break;
+        case 1: v = Fmt::template scale<1>(hdr, p_si); break;
+        case 2: v = Fmt::template scale<2>(hdr, p_si); break;
+        default: v = Fmt::template scale<3>(hdr, p_si); break;
+        }
+        lds_write4(sc_wr + (uint32_t)((g & 1) * SC_BUF), v);
+    };
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f32x16{};
+    const int nsh = 4 * (kq & 1);  // low or high nibbles
+    auto nib = [&](uint32_t x) {
+        pin(x);
+        return (x >> nsh) & 0x0F0F0F0Fu;
+    };
+
+    // ---- prologue: virtual iterations -4GA .. -1 (W groups 0 .. GA-1,
+    // A chunks 0 .. NS-2); group 0's scales; chunk 0 dequantized, chunk 1's
+    // nibbles read.
+#pragma unroll
+    for (int it = -4 * GA; it < 0; it++) {
+        issue_w(it);
+        if (it + NS - 1 >= 0) issue_a(it);
+    }
+    wait_vm_barrier<vm_after(3)>();  // as at iteration -1: A chunks 0, 1 and W groups 0, 1 done
+    {
+        u32x4 hdr = lds_read16<0>(hdr_rd);
+        wait_lgkm0(hdr);
+        make_scales(hdr, 0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    half8 a_cur[4], b_cur;
+    u32x2 raw_nxt;
+    u32x4 sc_cur;
+    {
+        a_cur[0] = lds_read_frag<0>(a_rd);
+        a_cur[1] = lds_read_frag<4096>(a_rd);
+        a_cur[2] = lds_read_frag<8192>(a_rd);
+        a_cur[3] = lds_read_frag<12288>(a_rd);
+        u32x2 raw0 = lds_read8<0>(w_rd[0]);
+        raw_nxt = lds_read8<0>(w_rd[1]);
+        sc_cur = lds_read16<0>(sc_rd);
+        wait_lgkm0(a_cur[0], a_cur[1], a_cur[2], a_cur[3], raw0, raw_nxt, sc_cur);
+        half2v h0, h1, h2, h3;
+        dequant4(nib(raw0.x), sc_cur.x, h0, h1);
+        dequant4(nib(raw0.y), sc_cur.x, h2, h3);
+        b_cur = join8(h0, h1, h2, h3);
+    }
+
+    // ---- main loop: one scale group (four chunks) per trip
+    int st_c = 0;  // A stage of chunk 4g
+    for (int g = 0; g < ngroups; g++) {
+        const uint32_t wb_cur = (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
+        const uint32_t wb_nxt = (uint32_t)(((g + 1) & (NWBUF - 1)) * W_GROUP);
+        const uint32_t sc_nxt_rd = sc_rd + (uint32_t)(((g + 1) & 1) * SC_BUF);
+        u32x4 hdr = {0, 0, 0, 0};
+        u32x4 sc_nxt = sc_cur;
+        auto step = [&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const int c = 4 * g + u;
+            wait_vm_barrier<vm_after(u)>();
+            issue_w(c);
+            issue_a(c);
+            if constexpr (u == 1) make_scales(hdr, g + 1);  // headers read at u = 0
+            // LDS reads: A fragments of chunk c+1, nibbles of chunk c+2;
+            // u = 0: the next group's headers (scale producers); u = 2: the
+            // next group's scales
+            int st1 = st_c + u + 1;
+            st1 = st1 >= NS ? st1 - NS : st1;  // stage of chunk c+1
+            const uint32_t sa = a_rd + (uint32_t)(st1 * A_STAGE);
+            half8 a_nxt[4];
+            a_nxt[0] = lds_read_frag<0>(sa);
+            a_nxt[1] = lds_read_frag<4096>(sa);
+            a_nxt[2] = lds_read_frag<8192>(sa);
+            a_nxt[3] = lds_read_frag<12288>(sa);
+            constexpr int q2 = (u + 2) & 3;  // position of chunk c+2 (group g+1 for u >= 2)
+            u32x2 raw_nn = lds_read8<0>(w_rd[q2] + (u >= 2 ? wb_nxt : wb_cur));
+            if constexpr (u == 0) hdr = lds_read16<0>(hdr_rd + wb_nxt);
+            if constexpr (u == 2) sc_nxt = lds_read16<0>(sc_nxt_rd);
+            __builtin_amdgcn_sched_barrier(0);
+            // Chunk c's MFMAs, each followed by a share of chunk c+1's
+            // dequantization (the next group's first chunk for u = 3): the
+            // VALU work runs while the matrix core is busy.  sched_barrier
+            // and the pinned dequant inputs keep this order.
+            constexpr int q1 = (u + 1) & 3;
+            const u32x4 &sv = (u == 3) ? sc_nxt : sc_cur;
+            const uint32_t sb = q1 == 0 ? sv.x : q1 == 1 ? sv.y : q1 == 2 ? sv.z : sv.w;
+            half2v hq[4];
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[0], b_cur, acc[0], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            dequant4(nib(raw_nxt.x), sb, hq[0], hq[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[1], b_cur, acc[1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            dequant4(nib(raw_nxt.y), sb, hq[2], hq[3]);
+            __builtin_amdgcn_sched_barrier(0);
+            acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[2], b_cur, acc[2], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[3], b_cur, acc[3], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkm0(a_nxt[0], a_nxt[1], a_nxt[2], a_nxt[3], raw_nn, hdr, sc_nxt);
+#pragma unroll
+            for (int i = 0; i < 4; i++) a_cur[i] = a_nxt[i];
+            b_cur = join8(hq[0], hq[1], hq[2], hq[3]);
+            raw_nxt = raw_nn;
+        };
+        step(ic<0>{});
+        step(ic<1>{});
+        step(ic<2>{});
+        step(ic<3>{});
+        sc_cur = sc_nxt;
+        st_c += 4;
+        st_c = st_c >= NS ? st_c - NS : st_c;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // drain the padding loads before LDS is reused
+    __syncthreads();
+
+    // Partial sums to LDS: element r of acc[i] in lane l is row
+    // 8(r/4) + 4(l/32) + r%4, column l%32 of that 32 x 32 block.  Layout
+    // [wave][block][r/4][lane][r%4] (conflict-free 16-byte accesses).
+    f32x4 *red = reinterpret_cast<f32x4 *>(lds);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            const f32x4 v = {acc[i][4 * rq], acc[i][4 * rq + 1], acc[i][4 * rq + 2], acc[i][4 * rq + 3]};
+            red[((wave * 4 + i) * 4 + rq) * 64 + lane] = v;
+        }
+    __syncthreads();
+    // Wave (t, kq) finishes row block kq of column half t: k-steps 0, 1, 2, 3
+    // added in order.
+    const size_t col = n0 + ncol;
+#pragma unroll
+    for (int rq = 0; rq < 4; rq++) {
+        f32x4 sum = red[((t * 4 + kq) * 4 + rq) * 64 + lane];
+#pragma unroll
+        for (int k2 = 1; k2 < 4; k2++) sum += red[(((2 * k2 + t) * 4 + kq) * 4 + rq) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const size_t m = m0 + 32 * kq + 8 * rq + 4 * h + e;
+            if (m < M && col < N) out[m * N + col] = sum[e];
+        }
+    }
+}
+
+__global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__ d, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = (_Float16)s[i];
+}
+
+template <class Fmt>
+hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
+    const int m_tiles = (int)((M + BM - 1) / BM), n_tiles = (int)((w.n_rows + BN - 1) / BN);
+    static bool attr_set = false;  // per process; the attribute is per function
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           GEMM_LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_gemm_f16<Fmt>), dim3(m_tiles * n_tiles), dim3(NT), GEMM_LDS, s, w, a, (const int *)nullptr,
+                       M, out, m_tiles);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_supports(uint32_t dtype, size_t n_cols) {
+    if (n_cols >= (size_t)1 << 31 || n_cols == 0) return false;
+    if (dtype == T_Q4_K) return n_cols % 256 == 0;
+    if (dtype == T_Q4_0) return n_cols % 256 == 0;  // whole scale groups of 8 blocks
+    return false;
+}
+
+hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src,
+                       static_cast<_Float16 *>(dst), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s) {
+    if (M == 0 || w.n_rows == 0) return hipSuccess;
+    // the kernel's per-lane load offsets are 32-bit
+    if (M * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
+        return hipErrorInvalidValue;
+    const _Float16 *a = static_cast<const _Float16 *>(a_f16);
+    if (w.dtype == T_Q4_K) return launch_fmt<Q4K>(w, a, M, out, s);
+    if (w.dtype == T_Q4_0) return launch_fmt<Q40>(w, a, M, out, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace rce_qmm

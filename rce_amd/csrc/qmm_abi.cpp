@@ -83,6 +83,7 @@ struct rce_qmm_context {
     int device = 0;
     hipStream_t stream = nullptr;
     Scratch a_in, a_f32, out;
+    Scratch a_f16;  // f32 activations rounded to f16 for the MFMA GEMM
 };
 
 struct rce_qmm_weight {
@@ -122,16 +123,38 @@ rce_qmm_status check_weight_ctx(rce_qmm_context *ctx, const rce_qmm_weight *w) {
     return RCE_QMM_OK;
 }
 
+// Every kernel family: decode kernels (EXACT, Q8) and the MFMA GEMM.
+bool supports_mode(uint32_t dtype, size_t n_cols, int mode) {
+    if (mode == RCE_QMM_MODE_F16_MFMA) return gemm_supports(dtype, n_cols);
+    return gpu_supports(dtype, n_cols, mode);
+}
+
+// The prefill GEMM; f32 activations are rounded to f16 first.
+rce_qmm_status run_gemm(rce_qmm_context *ctx, const void *a_dev, bool a_f16, size_t t_rows, const DevWeight &dw,
+                        float *out_dev, hipStream_t s) {
+    const void *a = a_dev;
+    if (!a_f16) {
+        rce_qmm_status st;
+        const size_t n = t_rows * dw.n_cols;
+        if ((st = ensure(ctx, ctx->a_f16, n * 2, s))) return st;
+        HIP_TRY(launch_f32_to_f16(static_cast<const float *>(a_dev), ctx->a_f16.p, n, s));
+        a = ctx->a_f16.p;
+    }
+    HIP_TRY(launch_gemm_f16(dw, a, t_rows, out_dev, s));
+    return RCE_QMM_OK;
+}
+
 // Device-side core shared by the host and device entry points.
 rce_qmm_status run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype, size_t t_rows,
                            const rce_qmm_weight *w, float *out_dev, rce_qmm_mode mode, hipStream_t s) {
     const DevWeight &dw = w->dw;
-    if (!gpu_supports(dw.dtype, dw.n_cols, (int)mode))
+    if (!supports_mode(dw.dtype, dw.n_cols, (int)mode))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "dtype " + std::to_string(dw.dtype) + " with n_cols " +
                                                    std::to_string(dw.n_cols) + " has no GPU kernel in mode " +
                                                    std::to_string((int)mode));
     if (a_dtype != T_F32 && a_dtype != T_F16) return fail(RCE_QMM_UNSUPPORTED_DTYPE, "activations must be F32 or F16");
     if (t_rows == 0 || dw.n_rows == 0) return RCE_QMM_OK;
+    if (mode == RCE_QMM_MODE_F16_MFMA) return run_gemm(ctx, a_dev, a_dtype == T_F16, t_rows, dw, out_dev, s);
     const size_t k = dw.n_cols;
     const float *a32 = static_cast<const float *>(a_dev);
     rce_qmm_status st;
@@ -215,7 +238,7 @@ void rce_qmm_context_destroy(rce_qmm_context *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out})
+    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16})
         if (s->p) (void)hipFree(s->p);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -235,7 +258,7 @@ rce_qmm_status rce_qmm_synchronize(rce_qmm_context *ctx) {
 }
 
 int rce_qmm_supports(uint32_t dtype, size_t n_cols, rce_qmm_mode mode) {
-    return gpu_supports(dtype, n_cols, (int)mode) ? 1 : 0;
+    return supports_mode(dtype, n_cols, (int)mode) ? 1 : 0;
 }
 
 rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, size_t n_rows, size_t n_cols,

@@ -57,7 +57,7 @@ struct GemvGeom {
     int nt = 0, rpl = 0, tb = 0;
 };
 
-// Kernels available for (dtype, n_cols, mode); mirrors rce_qmm_supports.
+// Decode kernels available for (dtype, n_cols, mode 0 EXACT / 1 Q8).
 bool gpu_supports(uint32_t dtype, size_t n_cols, int mode);
 
 // Device layout of a weight: fills layout, row_stride, planes and
@@ -83,5 +83,12 @@ hipError_t launch_gemv_q4_k(const DevWeight &w, const GemvGeom &g, const float *
 hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
+
+// Prefill GEMM on the matrix cores (gemm_f16.hip): out[M, n_rows] =
+// A[M, n_cols] . W^T, A binary16, W dequantized to binary16 tiles.
+bool gemm_supports(uint32_t dtype, size_t n_cols);
+hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s);
+// f32 activations -> binary16 (round to nearest even) for the GEMM.
+hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t s);
 
 }  // namespace rce_qmm

@@ -1,0 +1,123 @@
+"""GPU parity of the prefill GEMM on the matrix cores (RCE_QMM_MODE_F16_MFMA).
+
+The mode dequantizes Q4_K / Q4_0 weights to binary16 tiles and contracts
+them with f16 MFMA, f32 accumulation.  Two checks per case:
+  * against a numpy restatement of the same f16 weights (f64 products):
+    only accumulation order differs, so normwise error must be ~1e-6 --
+    this catches a wrong fragment layout, K order or scale;
+  * against the oracle's EXACT result (the reference's f32 order,
+    rce-op-qmm mm_batched L967-1023): normwise max|gpu - ref| / max|ref|
+    within 2e-3, the stated budget of the fp16-dequant path.
+Elementwise relative error is not bounded near zero outputs by any f16
+path; the tolerance is normwise, as the reference's own combined
+tolerances are (rce-op-qmm L3462-3475).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import rce_amd
+from rce_amd import GgufDtype as G, Mode
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+F16 = np.float16
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def q4k_f16_weights(b, n, k):
+    """Q4_K bytes -> the f16 weights the kernel forms: f16(f16(d*sc)*q + f16(-dmin*m))
+    (one rounding of the fma), decoded with numpy from the GGUF layout
+    (rce-ingest-gguf dequant.rs L546-589)."""
+    nsb = k // 256
+    blk = b.reshape(n, nsb, 144)
+    d = blk[:, :, 0:2].copy().view(F16)[:, :, 0].astype(F32)
+    dmin = blk[:, :, 2:4].copy().view(F16)[:, :, 0].astype(F32)
+    s = blk[:, :, 4:16].astype(np.int32)
+    sc = np.zeros((n, nsb, 8), np.int32)
+    mn = np.zeros((n, nsb, 8), np.int32)
+    for j in range(8):
+        if j < 4:
+            sc[:, :, j] = s[:, :, j] & 63
+            mn[:, :, j] = s[:, :, j + 4] & 63
+        else:
+            sc[:, :, j] = (s[:, :, j + 4] & 0x0F) | ((s[:, :, j - 4] >> 6) << 4)
+            mn[:, :, j] = (s[:, :, j + 4] >> 4) | ((s[:, :, j] >> 6) << 4)
+    qs = blk[:, :, 16:144].astype(np.int32).reshape(n, nsb, 4, 32)
+    q = np.zeros((n, nsb, 8, 32), np.int32)
+    q[:, :, 0::2, :] = qs & 0x0F
+    q[:, :, 1::2, :] = qs >> 4
+    d1 = (d[:, :, None] * sc.astype(F32)).astype(F16).astype(np.float64)
+    m1 = (-(dmin[:, :, None] * mn.astype(F32))).astype(F16).astype(np.float64)
+    w = (q.astype(np.float64) * d1[:, :, :, None] + m1[:, :, :, None]).astype(F16)
+    return w.reshape(n, k).astype(np.float64)
+
+
+def q40_f16_weights(b, n, k):
+    """Q4_0 bytes -> f16(d * (q - 8)) (rce-ingest-gguf dequant.rs L360-382)."""
+    nb = k // 32
+    blk = b.reshape(n, nb, 18)
+    d = blk[:, :, 0:2].copy().view(F16)[:, :, 0].astype(np.float64)
+    qs = blk[:, :, 2:18].astype(np.int32)
+    q = np.concatenate([(qs & 0x0F) - 8, (qs >> 4) - 8], axis=2).astype(np.float64)
+    return (q * d[:, :, None]).astype(F16).reshape(n, k).astype(np.float64)
+
+
+def run_gemm(ctx, w, x, a_dtype):
+    t = x.shape[0]
+    xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    out = rce_amd.DeviceBuffer(ctx, t * w.n_rows * 4)
+    rce_amd.mm_batched_dev(ctx, xa.ptr, a_dtype, t, w, out.ptr, Mode.F16_MFMA)
+    ctx.synchronize()
+    r = out.download(F32, t * w.n_rows).reshape(t, w.n_rows)
+    xa.free(); out.free()
+    return r
+
+
+def normwise(got, want):
+    return float(np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(want)))
+
+
+CASES = [
+    # (dtype, n_rows, n_cols, tokens): the configs[2] shape, ragged M and N,
+    # short K (split-K off), Q4_0 (the MoE experts' format)
+    (O.Q4_K, 4096, 4096, 512),
+    (O.Q4_K, 384, 1024, 100),
+    (O.Q4_K, 200, 2048, 33),
+    (O.Q4_K, 128, 256, 1),
+    (O.Q4_0, 1024, 4096, 64),
+    (O.Q4_0, 300, 512, 7),
+    (O.Q4_0, 64, 14336, 5),
+]
+
+
+@pytest.mark.parametrize("dt,n,k,t", CASES)
+@pytest.mark.parametrize("a16", [True, False])
+def test_gemm_f16_mfma_parity(ctx, dt, n, k, t, a16):
+    if not a16 and (n, k, t) == (4096, 4096, 512):
+        pytest.skip("f32 activations covered at the smaller shapes")
+    note(f"gemm f16-mfma dtype={dt} n={n} k={k} t={t} a16={a16}")
+    rng = np.random.default_rng(9000 + dt + n + k + t)
+    w32 = (rng.standard_normal((n, k)) * 0.02).astype(F32)
+    b = O.quantize(w32, dt)
+    x = rng.standard_normal((t, k)).astype(F16 if a16 else F32)
+    xv = x.astype(F16).astype(np.float64)  # the kernel's f16 activations
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = run_gemm(ctx, w, x, G.F16 if a16 else G.F32)
+    wf = q4k_f16_weights(b, n, k) if dt == O.Q4_K else q40_f16_weights(b, n, k)
+    same = xv @ wf.T
+    assert normwise(got, same) < 1e-5, "kernel differs from the f16-weight restatement"
+    ref = O.mm_batched(x.astype(F32), b, dt, n, k)  # reference order, f32 activations
+    assert normwise(got, ref) < 2e-3
+    again = run_gemm(ctx, w, x, G.F16 if a16 else G.F32)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not run-to-run deterministic"
+
+
+def test_gemm_supports_matrix():
+    assert rce_amd.supports(G.Q4K, 4096, Mode.F16_MFMA)
+    assert rce_amd.supports(G.Q4_0, 4096, Mode.F16_MFMA)
+    assert not rce_amd.supports(G.Q4_0, 4096 + 64, Mode.F16_MFMA)  # whole groups of 8 blocks
+    assert not rce_amd.supports(G.Q6K, 4096, Mode.F16_MFMA)
