@@ -3,42 +3,39 @@
 // Q4_K or Q4_0 blocks, dequantized to binary16 MFMA fragments in registers
 // and contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
 //
-// Tiling.  A block of 512 threads owns a 128 x 64 (M x N) output tile, so a
-// 512 x 4096 product is 256 tiles: one per CU.  K runs in chunks of 64 (four
-// MFMA k-steps of 16).  Wave w = 2*kq + t computes k-step kq of every chunk
-// for the 128 x 32 sub-tile of columns 32t.. (4 x 1 MFMA blocks of 32 x 32):
-// per chunk it reads four A fragments from LDS, dequantizes its one W
-// fragment itself from the raw GGUF nibbles in LDS (each W nibble is
-// dequantized by exactly one wave; no B tile is written), and issues four
-// MFMAs.  The four k-step partial sums of each output are added at the end
-// through LDS in a fixed order (deterministic).
+// Tiling.  A block owns a 128 x 64 (M x N) output tile, so a 512 x 4096
+// product is 256 tiles: one per CU.  K runs in chunks of 64 (four MFMA
+// k-steps of 16).  The block has ten waves:
+//   * eight compute waves: wave w = 2*kq + t computes k-step kq of every
+//     chunk for the 128 x 32 sub-tile of columns 32t.. (4 x 1 MFMA blocks of
+//     32 x 32): per chunk it reads four A fragments from LDS, dequantizes
+//     its one W fragment itself from the raw GGUF nibbles in LDS (each W
+//     nibble is dequantized by exactly one wave; no B tile is written), and
+//     issues four MFMAs.  The four k-step partial sums of each output are
+//     added at the end through LDS in a fixed order (deterministic);
+//   * two producer waves issue every global -> LDS load and compute the
+//     per-sub-block fma scales from the GGUF headers.  A load instruction
+//     can hold its wave up while the CU's memory pipeline is busy (each
+//     1 KB load occupies it ~20 cycles), so the loads live in waves that do
+//     nothing else and the MFMA/dequantization waves never stall on them.
+// One barrier per chunk.  The producers wait (s_waitcnt vmcnt, one
+// compile-time immediate per chunk position) for the data the compute
+// waves read next before joining it.
 //
-// Balance (measured on MI355X).  Dequantizing one 8-nibble fragment costs
-// ~16 VALU ops, four of them v_pk_fma_f16 at half rate (~80 SIMD cycles);
-// four MFMAs are 128 cycles; a CU's global->LDS path moves ~64 B/cycle.
-// Feeding each fragment to four MFMAs (128 rows) keeps the VALU below the
-// MFMA time; the 18.7 KB of A and W a CU loads per chunk is about the same
-// time again.  LDS offsets are immediates off per-chunk base registers, and
-// the per-sub-block fma scales are computed once per CU per scale group
-// (from the GGUF header) into LDS.
-//
-// Global -> LDS traffic uses gfx950 global_load_lds_dwordx4 (16 bytes per
-// lane, no registers).  Its throughput is set by the 64-byte segments an
-// instruction touches, so every load covers whole segments:
+// Global -> LDS traffic uses buffer_load_dwordx4 ... lds (16 bytes per lane,
+// no registers; a uniform scalar offset per chunk).  Its throughput is set
+// by the 64-byte segments an instruction touches, so every load covers
+// whole segments:
 //   * A: 8 rows x 128 bytes (one chunk of a row) per instruction, stored
 //     XOR-swizzled (16-byte column g of row r at slot g ^ f(r),
 //     f(r) = (r & 7) ^ ((r >> 3) & 1)) so the MFMA fragment reads (32 rows,
 //     one column) are bank-conflict free whether 8 or 16 lanes are served
-//     per LDS cycle;
+//     per LDS cycle; NS - 1 chunks ahead;
 //   * W: per scale group (four chunks: one Q4_K super-block, eight Q4_0
 //     blocks) each row's 2 x 64 bytes of nibbles (16-byte pieces rotated by
-//     (row >> 2) & 3) and its 16-byte scale header, loaded three groups
-//     ahead into four group buffers.
-// Pipeline per chunk c (one barrier each): loads of A chunk c + NS - 1 and
-// of part of a W group; LDS reads of chunk c+1's A fragments and chunk
-// c+2's nibbles; dequantization of chunk c+1 interleaved with chunk c's
-// MFMAs.  Every wave issues the same loads per chunk, so a compile-time
-// s_waitcnt vmcnt immediate per chunk position fits all waves.
+//     (row >> 2) & 3) and its 16-byte scale header, loaded GA groups ahead.
+// The compute waves read chunk c+1's A fragments and chunk c+2's nibbles
+// while chunk c's MFMAs and chunk c+1's dequantization run.
 //
 // K order.  Any permutation of K inside a chunk is a valid contraction if A
 // and W use the same one.  Lane half h (= lane / 32) of k-step kq holds the
@@ -72,12 +69,14 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 64, KC = 64, NT = 512;
+constexpr int BM = 128, BN = 64, KC = 64;
+constexpr int NC = 512;                          // compute threads (8 waves)
+constexpr int NT = NC + 128;                     // + 2 producer waves
 constexpr int NS = 6;                            // A stages (chunks), loaded NS - 1 ahead
 constexpr int A_STAGE = BM * KC * 2;             // 16 KB
 constexpr int W_HALF = BN * 64;                  // 4 KB: 64 rows x 4 chunks x 16 B
 constexpr int W_GROUP = 2 * W_HALF + BN * 16;    // + 1 KB of scale headers
-constexpr int NWBUF = 4, GA = 3;                 // W groups loaded GA groups ahead
+constexpr int NWBUF = 4, GA = 2;                 // W groups loaded GA groups ahead
 constexpr int SC_BUF = BN * 2 * 16;              // [column][set][chunk] of f16 {scale, bias}
 constexpr int OFF_W = NS * A_STAGE;
 constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
@@ -85,13 +84,14 @@ constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
 constexpr int RED_LDS = 8 * 4 * 16 * 64 * 4;     // partial sums: 8 waves x 64 floats x 64 lanes
 constexpr int GEMM_LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
 static_assert(GEMM_LDS + BM * 4 <= 160 * 1024, "LDS budget");
-// W group g must be complete at the barrier of chunk 4g-4 (its headers are
-// read there): its last load (iteration 4(g-GA)+1) precedes the loads of A
-// chunk 4g-3 (iteration 4g-3-(NS-1)).
-static_assert(4 * GA >= NS + 3, "W groups loaded too late for the stage depth");
+// W group g must be complete at the barrier of chunk 4g-3 (its headers are
+// read there for the scales): its last load (iteration 4(g-GA)+1) precedes
+// the loads of A chunk 4g-2 (iteration 4g-2-(NS-1)).
+static_assert(4 * GA >= NS + 2, "W groups loaded too late for the stage depth");
 // W buffer (g+GA) % NWBUF, refilled from iteration 4g, was last read for
-// chunk 4g-1 (iteration 4g-3).
-static_assert(NWBUF == GA + 1, "W buffer ring");
+// chunk 4(g+GA-NWBUF)+3 (iteration 4(g+GA-NWBUF)+1 < 4g).
+static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
+static_assert(NS >= 3, "stage ring");
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     _Float16 h;
@@ -118,6 +118,17 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
 __device__ __forceinline__ void load_lds16(const void *g, unsigned char *lds_wave) {
     __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)g,
                                      (void __attribute__((address_space(3))) *)lds_wave, 16, 0, 0);
+}
+
+// Buffer load of 16 bytes per lane straight into LDS at lds_wave + 16 * lane:
+// byte voff (per lane) + soff (uniform) of the buffer described by r.
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                               unsigned char *lds_wave) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_wave, 16, voff, soff, 0, 0);
+}
+// Raw byte buffer of n bytes (gfx9 descriptor word 3 for untyped access).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *base, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)n, 0x00020000);
 }
 
 // LDS accesses of the pipelined loop are inline ds_read / ds_write: the
@@ -149,8 +160,8 @@ __device__ __forceinline__ u32x2 lds_read8(uint32_t a) {
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
 }
-__device__ __forceinline__ void lds_write4(uint32_t a, uint32_t v) {
-    asm volatile("ds_write_b32 %0, %1" : : "v"(a), "v"(v) : "memory");
+__device__ __forceinline__ void lds_write16(uint32_t a, u32x4 v) {
+    asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
 }
 // s_waitcnt lgkmcnt(0), then an empty asm that "redefines" each register
 // the reads above filled, so no use of them can move ahead of the wait.
@@ -178,7 +189,6 @@ __device__ __forceinline__ void wait_vm_barrier() {
 // pairs in byte order: value = s * n + b (packed f16 fma, one rounding),
 // with sb = f16 {s, b}.  Eight VALU ops; two calls make one MFMA fragment.
 __device__ __forceinline__ void dequant4(uint32_t x, uint32_t sb, half2v &lo, half2v &hi) {
-    pin(x);  // empty volatile asm on the input and the outputs: this code stays where it is written
     const uint32_t K64 = 0x64646464u;
     const half2v m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const half2v p = as_h2(sb);
@@ -188,8 +198,6 @@ __device__ __forceinline__ void dequant4(uint32_t x, uint32_t sb, half2v &lo, ha
     const uint32_t p1 = __builtin_amdgcn_perm(x, K64, 0x00070006u);
     lo = __builtin_elementwise_fma(as_h2(p0) + m1024, sc, bias);
     hi = __builtin_elementwise_fma(as_h2(p1) + m1024, sc, bias);
-    pin(lo);
-    pin(hi);
 }
 
 __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
@@ -261,15 +269,15 @@ struct Q40 {
     }
 };
 
-// Loads issued by iteration `it`, in order: the W load of position it % 4
-// (a row half at position 0, headers at 1, none at 2 and 3), then the two
-// A loads of chunk it + NS - 1.
-__host__ __device__ constexpr int w_loads(int q) { return (q & 3) < 2 ? 1 : 0; }
-// vmcnt immediate for the barrier of chunk position q: the loads a wave
-// issued after chunk c+1's A loads, i.e. those of iterations c+3-NS .. c-1.
+// Producer loads of iteration `it`, in order: the W loads of position
+// it % 4 (row halves at position 0, headers at 1), then the eight A loads
+// of chunk it + NS - 1.
+__host__ __device__ constexpr int w_loads(int q) { return (q & 3) == 0 ? 4 : (q & 3) == 1 ? 1 : 0; }
+// vmcnt immediate for a producer's barrier at chunk position q: the loads
+// it issued after chunk c+1's A loads, i.e. those of iterations c+3-NS .. c-1.
 __host__ __device__ constexpr int vm_after(int q) {
     int n = 0;
-    for (int d = 1; d <= NS - 3; d++) n += 2 + w_loads(q - d);
+    for (int d = 1; d <= NS - 3; d++) n += 8 + w_loads(q - d);
     return n;
 }
 
@@ -278,7 +286,7 @@ using ic = std::integral_constant<int, U>;
 
 template <class Fmt>
 __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__restrict__ A, const int *__restrict__ gather,
-                                                 size_t M, float *__restrict__ out, int m_tiles) {
+                                                 size_t M, uint32_t a_bytes, float *__restrict__ out, int m_tiles) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int arow[BM];
     const size_t N = w.n_rows, K = w.n_cols;
@@ -291,7 +299,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
     const int nchunks = (int)(K / KC), ngroups = nchunks / 4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int t = wave & 1, kq = wave >> 1;
+    const bool producer = wave >= NC / 64;
     const int l32 = lane & 31, h = lane >> 5;
 
     if (tid < BM) {
@@ -300,58 +308,125 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
         arow[tid] = gather ? gather[m] : (int)m;
     }
     __syncthreads();
+    const uint32_t lds0 = lds_addr(lds);
 
-    // Loads: a uniform base (kernel argument + per-chunk offset) plus this
-    // lane's loop-invariant 32-bit offset (the host checks the ranges).
-    //   A: instruction i covers rows 16*wave + 8i .. +7, 8 lanes per row;
-    //      lane slot p holds column p ^ f(row)
-    uint32_t a_lane[2];
+    if (producer) {
+        // ===== producer waves: every global -> LDS load, and the scales.
+        // Loads are a uniform base (kernel argument + per-chunk offset)
+        // plus this lane's loop-invariant 32-bit offset (the host checks
+        // the ranges); issuing them may stall on the memory pipeline, which
+        // holds up only these two waves.
+        const int pw = wave - NC / 64;  // 0, 1
+        const int pt = tid - NC;        // 0 .. 127
+        //   A: rows 64*pw .. +63; instruction i covers rows 64pw + 8i .. +7,
+        //      8 lanes per row; lane slot p holds column p ^ f(row)
+        uint32_t a_lane[8];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int ar = 16 * wave + 8 * i + (lane >> 3);
-        const int aswz = (ar & 7) ^ ((ar >> 3) & 1);
-        a_lane[i] = (uint32_t)arow[ar] * (uint32_t)(2 * K) + 16u * (uint32_t)((lane & 7) ^ aswz);
-    }
-    const uint8_t *const abase = reinterpret_cast<const uint8_t *>(A);
-    //   W: wave w loads half w / 4 of rows 16*(w % 4) .. +15, 4 lanes per
-    //      row, slot p holding piece p ^ ((row >> 2) & 3); headers: rows
-    //      8*w + lane for lanes 0..7
-    const int w_hf = wave >> 2;
-    const int wr = 16 * (wave & 3) + (lane >> 2);
-    size_t wrow = n0 + wr;
-    wrow = wrow < N ? wrow : N - 1;  // rows past the end load the last row
-    const uint32_t w_lane = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
-    size_t hrow = n0 + 8 * wave + (lane & 7);
-    hrow = hrow < N ? hrow : N - 1;
-    const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
-    const uint8_t *const wbase = w.base;
-
-    // Loads of (virtual) iteration it: W position it % 4 of group it/4 + GA,
-    // then A chunk it + NS - 1.  Past-the-end groups and chunks reload
-    // group / chunk 0 (keeps every wave's load count fixed).
-    auto issue_w = [&](int it) {
-        const int q = it & 3;
-        if (q >= 2) return;
-        const int g = (it >> 2) + GA;
-        const int gs = g < ngroups ? g : 0;
-        unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
-        if (q == 0) {
-            load_lds16(wbase + Fmt::half_off(w, gs, w_hf) + w_lane, dst + w_hf * W_HALF + (wave & 3) * 1024);
-        } else if (lane < 8) {
-            load_lds16(wbase + Fmt::hdr_off(gs) + h_lane, dst + 2 * W_HALF + wave * 128);
+        for (int i = 0; i < 8; i++) {
+            const int ar = 64 * pw + 8 * i + (lane >> 3);
+            const int aswz = (ar & 7) ^ ((ar >> 3) & 1);
+            a_lane[i] = (uint32_t)arow[ar] * (uint32_t)(2 * K) + 16u * (uint32_t)((lane & 7) ^ aswz);
         }
-    };
-    auto issue_a = [&](int it) {
-        const int c = it + NS - 1;
-        const int cs = c < nchunks ? c : 0;
-        unsigned char *dst = lds + (c % NS) * A_STAGE + wave * 2048;
+        const __amdgpu_buffer_rsrc_t abuf = byte_buffer(A, a_bytes);
+        //   W: half pw of the group; instruction i covers rows 16i .. +15,
+        //      4 lanes per row, slot p holding piece p ^ ((row >> 2) & 3);
+        //      headers: rows 32*pw + lane for lanes 0..31
+        uint32_t w_lane[4];
 #pragma unroll
-        for (int i = 0; i < 2; i++) load_lds16(abase + (size_t)cs * (KC * 2) + a_lane[i], dst + i * 1024);
-    };
+        for (int i = 0; i < 4; i++) {
+            const int wr = 16 * i + (lane >> 2);
+            size_t wrow = n0 + wr;
+            wrow = wrow < N ? wrow : N - 1;  // rows past the end load the last row
+            w_lane[i] = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
+        }
+        size_t hrow = n0 + 32 * pw + (lane & 31);
+        hrow = hrow < N ? hrow : N - 1;
+        const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
+        const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(w.base, (uint32_t)(N * w.row_stride));
+        const uint32_t a_soff_max = (uint32_t)(nchunks - 1) * (KC * 2);
+        // Loads of (virtual) iteration it: W position it % 4 of group
+        // it/4 + GA (past the end: group 0), then A chunk it + NS - 1 into
+        // stage it % NS (past the end: the last chunk).
+        auto issue = [&](int it) {
+            const int q = it & 3;
+            if (q < 2) {
+                const int g = (it >> 2) + GA, gs = g < ngroups ? g : 0;
+                unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
+                if (q == 0) {
+                    const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
+                } else if (lane < 32) {
+                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * 512);
+                }
+            }
+            const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
+            unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * 8192;
+#pragma unroll
+            for (int i = 0; i < 8; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
+        };
+        // scales of group g: thread = column pt % 64, set pt / 64, chunks 0..3
+        const int p_col = pt & (BN - 1), p_si = pt >> 6;
+        const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
+        const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_col * 2 + p_si) * 16);
+        auto make_scales = [&](int g) {
+            u32x4 hdr = lds_read16<0>(hdr_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP));
+            wait_lgkm0(hdr);
+            const u32x4 v = {Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
+                             Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
+            lds_write16(sc_wr + (uint32_t)((g & 1) * SC_BUF), v);
+        };
 
+        // prologue: virtual iterations -4GA .. -1; group 0's scales
+#pragma unroll
+        for (int it = -4 * GA; it < 0; it++) {
+            if ((it & 3) < 2) {
+                const int q = it & 3, g = (it >> 2) + GA, gs = g < ngroups ? g : 0;
+                unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
+                if (q == 0) {
+                    const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
+                } else if (lane < 32) {
+                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * 512);
+                }
+            }
+            if (it + NS - 1 >= 0) {
+                const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
+                unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * 8192;
+#pragma unroll
+                for (int i = 0; i < 8; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
+            }
+        }
+        wait_vm_barrier<vm_after(3)>();  // barrier P1: A chunks 0, 1 and W groups 0, 1 done
+        make_scales(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // barrier P2: group 0's scales written
+        for (int g = 0; g < ngroups; g++) {
+            auto step = [&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                wait_vm_barrier<vm_after(u)>();
+                issue(4 * g + u);
+                if constexpr (u == 1) {
+                    make_scales(g + 1);  // read by the compute waves from step 2 on
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // written before the next barrier
+                }
+            };
+            step(ic<0>{});
+            step(ic<1>{});
+            step(ic<2>{});
+            step(ic<3>{});
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // drain the padding loads before LDS is reused
+        __syncthreads();                 // barrier E1
+        __syncthreads();                 // barrier E2
+        return;
+    }
+
+    // ===== compute waves: wave w = 2*kq + t
+    const int t = wave & 1, kq = wave >> 1;
     // LDS read addresses of this lane; A row block i is +32 rows (+4096
     // bytes): immediates.
-    const uint32_t lds0 = lds_addr(lds);
     const int g0 = Fmt::acol(kq) + h;
     const uint32_t a_rd = lds0 + (uint32_t)(l32 * 128 + 16 * (g0 ^ ((l32 & 7) ^ ((l32 >> 3) & 1))));
     const int ncol = 32 * t + l32;  // tile column of this lane
@@ -361,47 +436,15 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
         w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
                                             16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
     const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((ncol * 2 + Fmt::sidx(kq)) * 16);
-    // Scale producers: thread = column tid % 64, set wave % 2, chunk wave / 2
-    // (set and chunk are wave-uniform).
-    const int p_col = tid & (BN - 1), p_si = wave & 1, p_q = wave >> 1;
-    const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
-    const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_col * 2 + p_si) * 16 + p_q * 4);
-    auto make_scales = [&](const u32x4 &hdr, int g) {
-        uint32_t v;
-        switch (p_q) {
-        case 0: v = Fmt::template scale<0>(hdr, p_si); break;
-        case 1: v = Fmt::template scale<1>(hdr, p_si); break;
-        case 2: v = Fmt::template scale<2>(hdr, p_si); break;
-        default: v = Fmt::template scale<3>(hdr, p_si); break;
-        }
-        lds_write4(sc_wr + (uint32_t)((g & 1) * SC_BUF), v);
-    };
 
     f32x16 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[i] = f32x16{};
     const int nsh = 4 * (kq & 1);  // low or high nibbles
-    auto nib = [&](uint32_t x) {
-        pin(x);
-        return (x >> nsh) & 0x0F0F0F0Fu;
-    };
+    auto nib = [&](uint32_t x) { return (x >> nsh) & 0x0F0F0F0Fu; };
 
-    // ---- prologue: virtual iterations -4GA .. -1 (W groups 0 .. GA-1,
-    // A chunks 0 .. NS-2); group 0's scales; chunk 0 dequantized, chunk 1's
-    // nibbles read.
-#pragma unroll
-    for (int it = -4 * GA; it < 0; it++) {
-        issue_w(it);
-        if (it + NS - 1 >= 0) issue_a(it);
-    }
-    wait_vm_barrier<vm_after(3)>();  // as at iteration -1: A chunks 0, 1 and W groups 0, 1 done
-    {
-        u32x4 hdr = lds_read16<0>(hdr_rd);
-        wait_lgkm0(hdr);
-        make_scales(hdr, 0);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_s_barrier();  // barrier P1
+    __builtin_amdgcn_s_barrier();  // barrier P2: chunk 0 dequantized, chunk 1's nibbles read
     half8 a_cur[4], b_cur;
     u32x2 raw_nxt;
     u32x4 sc_cur;
@@ -420,58 +463,46 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
         b_cur = join8(h0, h1, h2, h3);
     }
 
-    // ---- main loop: one scale group (four chunks) per trip
-    int st_c = 0;  // A stage of chunk 4g
+    // ---- main loop: one scale group (four chunks) per trip; chunk c's A is
+    // in stage c % NS.
+    int st1 = 1;  // stage of chunk c+1
     for (int g = 0; g < ngroups; g++) {
+        // nibble reads of chunk c+2 (steps 0, 1: this group; 2, 3: the next)
         const uint32_t wb_cur = (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
         const uint32_t wb_nxt = (uint32_t)(((g + 1) & (NWBUF - 1)) * W_GROUP);
         const uint32_t sc_nxt_rd = sc_rd + (uint32_t)(((g + 1) & 1) * SC_BUF);
-        u32x4 hdr = {0, 0, 0, 0};
         u32x4 sc_nxt = sc_cur;
         auto step = [&](auto uc) {
             constexpr int u = decltype(uc)::value;
-            const int c = 4 * g + u;
-            wait_vm_barrier<vm_after(u)>();
-            issue_w(c);
-            issue_a(c);
-            if constexpr (u == 1) make_scales(hdr, g + 1);  // headers read at u = 0
-            // LDS reads: A fragments of chunk c+1, nibbles of chunk c+2;
-            // u = 0: the next group's headers (scale producers); u = 2: the
-            // next group's scales
-            int st1 = st_c + u + 1;
-            st1 = st1 >= NS ? st1 - NS : st1;  // stage of chunk c+1
+            // chunk c+1's A and W are in LDS (the producers waited for them);
+            // every wave is done with the reads of chunk c
+            __builtin_amdgcn_s_barrier();
+            // LDS reads: A fragments of chunk c+1, nibbles of chunk c+2; at
+            // u = 2 the next group's scales (written by the producers at u = 1)
             const uint32_t sa = a_rd + (uint32_t)(st1 * A_STAGE);
+            st1 = st1 == NS - 1 ? 0 : st1 + 1;
             half8 a_nxt[4];
             a_nxt[0] = lds_read_frag<0>(sa);
             a_nxt[1] = lds_read_frag<4096>(sa);
             a_nxt[2] = lds_read_frag<8192>(sa);
             a_nxt[3] = lds_read_frag<12288>(sa);
-            constexpr int q2 = (u + 2) & 3;  // position of chunk c+2 (group g+1 for u >= 2)
-            u32x2 raw_nn = lds_read8<0>(w_rd[q2] + (u >= 2 ? wb_nxt : wb_cur));
-            if constexpr (u == 0) hdr = lds_read16<0>(hdr_rd + wb_nxt);
+            u32x2 raw_nn = lds_read8<0>(w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
             if constexpr (u == 2) sc_nxt = lds_read16<0>(sc_nxt_rd);
             __builtin_amdgcn_sched_barrier(0);
-            // Chunk c's MFMAs, each followed by a share of chunk c+1's
-            // dequantization (the next group's first chunk for u = 3): the
-            // VALU work runs while the matrix core is busy.  sched_barrier
-            // and the pinned dequant inputs keep this order.
+            // Chunk c's MFMAs and chunk c+1's dequantization (the next
+            // group's first chunk for u = 3), independent of each other.
             constexpr int q1 = (u + 1) & 3;
             const u32x4 &sv = (u == 3) ? sc_nxt : sc_cur;
             const uint32_t sb = q1 == 0 ? sv.x : q1 == 1 ? sv.y : q1 == 2 ? sv.z : sv.w;
             half2v hq[4];
             acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[0], b_cur, acc[0], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
             dequant4(nib(raw_nxt.x), sb, hq[0], hq[1]);
-            __builtin_amdgcn_sched_barrier(0);
             acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[1], b_cur, acc[1], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
             dequant4(nib(raw_nxt.y), sb, hq[2], hq[3]);
-            __builtin_amdgcn_sched_barrier(0);
             acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[2], b_cur, acc[2], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
             acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[3], b_cur, acc[3], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            wait_lgkm0(a_nxt[0], a_nxt[1], a_nxt[2], a_nxt[3], raw_nn, hdr, sc_nxt);
+            wait_lgkm0(a_nxt[0], a_nxt[1], a_nxt[2], a_nxt[3], raw_nn, sc_nxt);
 #pragma unroll
             for (int i = 0; i < 4; i++) a_cur[i] = a_nxt[i];
             b_cur = join8(hq[0], hq[1], hq[2], hq[3]);
@@ -482,11 +513,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
         step(ic<2>{});
         step(ic<3>{});
         sc_cur = sc_nxt;
-        st_c += 4;
-        st_c = st_c >= NS ? st_c - NS : st_c;
     }
-    __builtin_amdgcn_s_waitcnt(0);  // drain the padding loads before LDS is reused
-    __syncthreads();
+    __syncthreads();  // barrier E1: the producers have drained their loads
 
     // Partial sums to LDS: element r of acc[i] in lane l is row
     // 8(r/4) + 4(l/32) + r%4, column l%32 of that 32 x 32 block.  Layout
@@ -499,7 +527,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
             const f32x4 v = {acc[i][4 * rq], acc[i][4 * rq + 1], acc[i][4 * rq + 2], acc[i][4 * rq + 3]};
             red[((wave * 4 + i) * 4 + rq) * 64 + lane] = v;
         }
-    __syncthreads();
+    __syncthreads();  // barrier E2
     // Wave (t, kq) finishes row block kq of column half t: k-steps 0, 1, 2, 3
     // added in order.
     const size_t col = n0 + ncol;
@@ -532,7 +560,7 @@ hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *ou
         attr_set = true;
     }
     hipLaunchKernelGGL((k_gemm_f16<Fmt>), dim3(m_tiles * n_tiles), dim3(NT), GEMM_LDS, s, w, a, (const int *)nullptr,
-                       M, out, m_tiles);
+                       M, (uint32_t)(M * w.n_cols * 2), out, m_tiles);
     return hipGetLastError();
 }
 
