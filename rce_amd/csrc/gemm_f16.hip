@@ -284,18 +284,33 @@ __host__ __device__ constexpr int vm_after(int q) {
 template <int U>
 using ic = std::integral_constant<int, U>;
 
+// Plain GEMM: tiles == nullptr, row tile mt covers rows mt*BM .. of M.
+// Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows),
+// multiplied by wtab[e]; tiles at or past n_tiles[0] do nothing.
 template <class Fmt>
-__global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__restrict__ A, const int *__restrict__ gather,
-                                                 size_t M, uint32_t a_bytes, float *__restrict__ out, int m_tiles) {
+__global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16 *__restrict__ A,
+                                                 const int *__restrict__ gather, size_t M, uint32_t a_bytes,
+                                                 float *__restrict__ out, int m_tiles, const MoeTile *__restrict__ tiles,
+                                                 const int *__restrict__ n_tiles, const DevWeight *__restrict__ wtab) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int arow[BM];
-    const size_t N = w.n_rows, K = w.n_cols;
     // Blocks are dispatched round-robin over 8 XCDs; consecutive logical
     // tiles (the m-tiles of one n-tile, sharing W rows) go to one XCD.
     const int G = gridDim.x, L = blockIdx.x;
     const int logical = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
     const int mt = logical % m_tiles, nt = logical / m_tiles;
-    const size_t m0 = (size_t)mt * BM, n0 = (size_t)nt * BN;
+    DevWeight w = w_arg;
+    size_t m0 = (size_t)mt * BM;
+    int rows = (int)(M - m0 < (size_t)BM ? M - m0 : BM);
+    if (tiles) {
+        if (mt >= n_tiles[0]) return;  // the whole block, before any barrier
+        const MoeTile tl = tiles[mt];
+        w = wtab[tl.e];
+        m0 = (size_t)tl.r0;
+        rows = tl.rows;
+    }
+    const size_t N = w.n_rows, K = w.n_cols;
+    const size_t n0 = (size_t)nt * BN;
     const int nchunks = (int)(K / KC), ngroups = nchunks / 4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -303,8 +318,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
     const int l32 = lane & 31, h = lane >> 5;
 
     if (tid < BM) {
-        size_t m = m0 + tid;
-        m = m < M ? m : M - 1;  // rows past M load the last row
+        const size_t m = m0 + (tid < rows ? tid : rows - 1);  // rows past the tile load its last row
         arow[tid] = gather ? gather[m] : (int)m;
     }
     __syncthreads();
@@ -538,8 +552,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w, const _Float16 *__
         for (int k2 = 1; k2 < 4; k2++) sum += red[(((2 * k2 + t) * 4 + kq) * 4 + rq) * 64 + lane];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const size_t m = m0 + 32 * kq + 8 * rq + 4 * h + e;
-            if (m < M && col < N) out[m * N + col] = sum[e];
+            const int m = 32 * kq + 8 * rq + 4 * h + e;
+            if (m < rows && col < N) out[(m0 + m) * N + col] = sum[e];
         }
     }
 }
@@ -560,7 +574,25 @@ hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *ou
         attr_set = true;
     }
     hipLaunchKernelGGL((k_gemm_f16<Fmt>), dim3(m_tiles * n_tiles), dim3(NT), GEMM_LDS, s, w, a, (const int *)nullptr,
-                       M, (uint32_t)(M * w.n_cols * 2), out, m_tiles);
+                       M, (uint32_t)(M * w.n_cols * 2), out, m_tiles, (const MoeTile *)nullptr, (const int *)nullptr,
+                       (const DevWeight *)nullptr);
+    return hipGetLastError();
+}
+
+template <class Fmt>
+hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
+                              const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, float *out,
+                              hipStream_t s) {
+    const int n_tiles = (int)((w.n_rows + BN - 1) / BN);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           GEMM_LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_gemm_f16<Fmt>), dim3(max_tiles * n_tiles), dim3(NT), GEMM_LDS, s, w, a, gather, a_rows,
+                       (uint32_t)(a_rows * w.n_cols * 2), out, max_tiles, tiles, n_tiles_dev, wtab);
     return hipGetLastError();
 }
 
@@ -578,6 +610,19 @@ hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t 
     hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src,
                        static_cast<_Float16 *>(dst), n);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
+                                   const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
+                                   float *out, hipStream_t s) {
+    if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
+    if (a_rows * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
+        return hipErrorInvalidValue;
+    static_assert(GEMM_BM == BM, "tile rows");
+    const _Float16 *a = static_cast<const _Float16 *>(a_f16);
+    if (w.dtype == T_Q4_K) return launch_fmt_grouped<Q4K>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
+    if (w.dtype == T_Q4_0) return launch_fmt_grouped<Q40>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s) {

@@ -84,6 +84,9 @@ struct rce_qmm_context {
     hipStream_t stream = nullptr;
     Scratch a_in, a_f32, out;
     Scratch a_f16;  // f32 activations rounded to f16 for the MFMA GEMM
+    // grouped experts: grouping metadata, expert tables, stage buffers
+    Scratch moe_meta, moe_wtab, moe_x, moe_h, moe_h16, moe_y;
+    std::vector<DevWeight> moe_wtab_host;  // what moe_wtab holds
 };
 
 struct rce_qmm_weight {
@@ -238,7 +241,8 @@ void rce_qmm_context_destroy(rce_qmm_context *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16})
+    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16, &ctx->moe_meta, &ctx->moe_wtab, &ctx->moe_x,
+                       &ctx->moe_h, &ctx->moe_h16, &ctx->moe_y})
         if (s->p) (void)hipFree(s->p);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -430,10 +434,105 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
                                    const rce_qmm_weight *const *w2, size_t n_expert, const float *x_dev,
                                    size_t t_rows, const int32_t *ids_dev, const float *weights_dev, size_t top_k,
                                    float *out_dev, rce_qmm_mode mode, void *stream) {
-    (void)w1; (void)w2; (void)n_expert; (void)x_dev; (void)t_rows; (void)ids_dev; (void)weights_dev;
-    (void)top_k; (void)out_dev; (void)mode; (void)stream;
-    if (!ctx) return fail(RCE_QMM_NULL_ARGUMENT, "null context");
-    return fail(RCE_QMM_UNSUPPORTED_DTYPE, "grouped-expert FFN is not built yet");
+    if (!ctx || !w1 || !w2) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight list");
+    if (n_expert == 0 || n_expert > 4096 || top_k == 0 || top_k > n_expert)
+        return fail(RCE_QMM_BAD_SHAPE, "need 0 < top_k <= n_expert <= 4096");
+    rce_qmm_status st;
+    for (size_t e = 0; e < n_expert; e++) {
+        if ((st = check_weight_ctx(ctx, w1[e])) || (st = check_weight_ctx(ctx, w2[e]))) return st;
+    }
+    const DevWeight &a1 = w1[0]->dw, &a2 = w2[0]->dw;
+    const size_t d_model = a1.n_cols, d_ff = a1.n_rows;
+    if (a2.n_rows != d_model || a2.n_cols != d_ff) return fail(RCE_QMM_BAD_SHAPE, "w2 must be [d_model, d_ff] of w1's d_ff");
+    for (size_t e = 0; e < n_expert; e++) {
+        const DevWeight &b1 = w1[e]->dw, &b2 = w2[e]->dw;
+        if (b1.dtype != a1.dtype || b1.n_rows != d_ff || b1.n_cols != d_model || b1.layout != a1.layout ||
+            b2.dtype != a2.dtype || b2.n_rows != d_model || b2.n_cols != d_ff || b2.layout != a2.layout)
+            return fail(RCE_QMM_BAD_SHAPE, "experts differ in dtype or shape");
+    }
+    if (!supports_mode(a1.dtype, d_model, (int)mode) || !supports_mode(a2.dtype, d_ff, (int)mode))
+        return fail(RCE_QMM_UNSUPPORTED_DTYPE, "the experts' dtype/shape has no GPU kernel in mode " +
+                                                   std::to_string((int)mode));
+    if (t_rows == 0) return RCE_QMM_OK;
+    if (!x_dev || !ids_dev || !weights_dev || !out_dev) return fail(RCE_QMM_NULL_ARGUMENT, "null device buffer");
+    if ((st = set_device(ctx->device))) return st;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+
+    // 1. stable grouping of the (token, decision) pairs by expert
+    const size_t n_pairs = t_rows * top_k;
+    if (n_pairs >= (size_t)1 << 30) return fail(RCE_QMM_BAD_SHAPE, "too many (token, decision) pairs");
+    const int max_tiles = (int)(n_pairs / GEMM_BM + n_expert);
+    const size_t meta_ints = (n_expert + 1) + 2 * n_pairs + 2;
+    const size_t meta_bytes = align_up(meta_ints * 4, 16) + (size_t)max_tiles * sizeof(MoeTile);
+    if ((st = ensure(ctx, ctx->moe_meta, meta_bytes, s))) return st;
+    int *offs = static_cast<int *>(ctx->moe_meta.p);
+    int *slot_of_pair = offs + n_expert + 1;
+    int *tok_of_slot = slot_of_pair + n_pairs;
+    int *n_tiles = tok_of_slot + n_pairs;
+    int *status = n_tiles + 1;
+    MoeTile *tiles = reinterpret_cast<MoeTile *>(static_cast<char *>(ctx->moe_meta.p) + align_up(meta_ints * 4, 16));
+    HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, GEMM_BM, offs, slot_of_pair, tok_of_slot,
+                             tiles, n_tiles, status, s));
+    const int *n_slots = offs + n_expert;  // device count of slots with a valid expert
+
+    // stage buffers: expert outputs in slot order
+    if ((st = ensure(ctx, ctx->moe_h, n_pairs * d_ff * sizeof(float), s))) return st;
+    if ((st = ensure(ctx, ctx->moe_y, n_pairs * d_model * sizeof(float), s))) return st;
+    float *h = static_cast<float *>(ctx->moe_h.p);
+    float *y = static_cast<float *>(ctx->moe_y.p);
+
+    if (mode == RCE_QMM_MODE_F16_MFMA) {
+        // 2. expert tables (uploaded when the expert set changes)
+        std::vector<DevWeight> tab(2 * n_expert);
+        for (size_t e = 0; e < n_expert; e++) {
+            tab[e] = w1[e]->dw;
+            tab[n_expert + e] = w2[e]->dw;
+        }
+        const size_t tab_bytes = tab.size() * sizeof(DevWeight);
+        if (ctx->moe_wtab_host.size() != tab.size() ||
+            std::memcmp(ctx->moe_wtab_host.data(), tab.data(), tab_bytes) != 0) {
+            if ((st = ensure(ctx, ctx->moe_wtab, tab_bytes, s))) return st;
+            HIP_TRY(hipStreamSynchronize(s));  // no kernel still reads the old table
+            HIP_TRY(hipMemcpy(ctx->moe_wtab.p, tab.data(), tab_bytes, hipMemcpyHostToDevice));
+            ctx->moe_wtab_host = tab;
+        }
+        const DevWeight *wtab1 = static_cast<const DevWeight *>(ctx->moe_wtab.p), *wtab2 = wtab1 + n_expert;
+        // 3. x -> f16 once; W1 GEMM on the rows gathered per slot
+        if ((st = ensure(ctx, ctx->moe_x, t_rows * d_model * 2, s))) return st;
+        if ((st = ensure(ctx, ctx->moe_h16, n_pairs * d_ff * 2, s))) return st;
+        HIP_TRY(launch_f32_to_f16(x_dev, ctx->moe_x.p, t_rows * d_model, s));
+        HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, h, s));
+        // 4. silu -> f16; W2 GEMM on the slots themselves
+        HIP_TRY(launch_silu_f16(h, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
+        HIP_TRY(launch_gemm_f16_grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, tiles, n_tiles, max_tiles, y, s));
+    } else {
+        if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
+        // The decode kernels take host row counts: read the grouping back.
+        std::vector<int> hoffs(n_expert + 1), hstatus(1);
+        HIP_TRY(hipMemcpyAsync(hoffs.data(), offs, hoffs.size() * 4, hipMemcpyDeviceToHost, s));
+        HIP_TRY(hipMemcpyAsync(hstatus.data(), status, 4, hipMemcpyDeviceToHost, s));
+        HIP_TRY(hipStreamSynchronize(s));
+        if (hstatus[0]) return fail(RCE_QMM_BAD_SHAPE, "an expert id is out of range");
+        // 2. gather x per slot (f32, the reference's activations)
+        if ((st = ensure(ctx, ctx->moe_x, n_pairs * d_model * sizeof(float), s))) return st;
+        float *xg = static_cast<float *>(ctx->moe_x.p);
+        HIP_TRY(launch_gather_rows(x_dev, tok_of_slot, n_slots, n_pairs, d_model, xg, s));
+        // 3. per expert: h = silu(W1 x), y = W2 h (the reference's per-row products)
+        for (size_t e = 0; e < n_expert; e++) {
+            const size_t r0 = (size_t)hoffs[e], n = (size_t)(hoffs[e + 1] - hoffs[e]);
+            if (n == 0) continue;
+            HIP_TRY(launch_gemv(w1[e]->dw, xg + r0 * d_model, n, h + r0 * d_ff, (int)mode, s));
+        }
+        HIP_TRY(launch_silu_inplace(h, n_slots, n_pairs, d_ff, s));
+        for (size_t e = 0; e < n_expert; e++) {
+            const size_t r0 = (size_t)hoffs[e], n = (size_t)(hoffs[e + 1] - hoffs[e]);
+            if (n == 0) continue;
+            HIP_TRY(launch_gemv(w2[e]->dw, h + r0 * d_ff, n, y + r0 * d_model, (int)mode, s));
+        }
+    }
+    // 5. combine in decision order
+    HIP_TRY(launch_moe_combine(y, slot_of_pair, weights_dev, t_rows, (int)top_k, d_model, out_dev, s));
+    return RCE_QMM_OK;
 }
 
 rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out) {

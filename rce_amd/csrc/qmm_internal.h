@@ -91,4 +91,35 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
 // f32 activations -> binary16 (round to nearest even) for the GEMM.
 hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t s);
 
+// ---- grouped experts (moe.hip, gemm_f16.hip) ----
+// A row tile of the grouped GEMM: expert e, slots r0 .. r0 + rows - 1.
+struct MoeTile {
+    int e, r0, rows, pad;
+};
+constexpr int GEMM_BM = 128;  // rows of a GEMM tile (launch_gemm_f16_grouped's bm)
+// Stable grouping of pairs p = token * top_k + j by expert ids[p]:
+// offs[n_expert + 1], slot_of_pair[n_pairs] (-1: id out of range),
+// tok_of_slot[n_pairs], tiles[n_pairs / bm + n_expert] (bm-row pieces of
+// each expert's slots), n_tiles[1], status[1] (1: an id was out of range).
+hipError_t launch_moe_group(const int32_t *ids, size_t n_pairs, int top_k, int n_expert, int bm, int *offs,
+                            int *slot_of_pair, int *tok_of_slot, MoeTile *tiles, int *n_tiles, int *status,
+                            hipStream_t s);
+// xg[s, :] = x[tok_of_slot[s], :] for s < n_slots (device count)
+hipError_t launch_gather_rows(const float *x, const int *tok_of_slot, const int *n_slots_dev, size_t max_slots,
+                              size_t d, float *xg, hipStream_t s);
+hipError_t launch_silu_inplace(float *h, const int *n_slots_dev, size_t max_slots, size_t d, hipStream_t s);
+// o (binary16) = silu(h)
+hipError_t launch_silu_f16(const float *h, void *o, const int *n_slots_dev, size_t max_slots, size_t d,
+                           hipStream_t s);
+// out[t, :] = sum_j gate_w[t, j] * y[slot_of_pair[t * top_k + j], :], j in order, from +0.0
+hipError_t launch_moe_combine(const float *y, const int *slot_of_pair, const float *gate_w, size_t t_rows, int top_k,
+                              size_t d, float *out, hipStream_t s);
+// Grouped GEMM: for every tile (expert e, slots r0 ..): out[r0 + m, :] =
+// A[gather ? gather[r0 + m] : r0 + m, :] . wtab[e]^T.  `w` gives the dtype
+// and shape shared by all experts; wtab is a device array of DevWeight;
+// a_rows: rows of A (bounds the loads); max_tiles bounds n_tiles_dev[0].
+hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
+                                   const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
+                                   float *out, hipStream_t s);
+
 }  // namespace rce_qmm

@@ -1,0 +1,138 @@
+"""GPU parity of the grouped-expert FFN (rce_qmm_moe_ffn_dev).
+
+Reference semantics (rce-qwen36-moe/src/lib.rs L667-710, rce-op-moe
+L35-110): for every token t and routing decision j, e = ids[t, j],
+h = silu(W1[e] x_t), y_j = W2[e] h, out_t = sum_j w[t, j] * y_j in decision
+order from +0.0.  The oracle restates that loop on the CPU (orc_moe_ffn).
+
+Tolerances: the expert products of EXACT mode are the reference's own f32
+order (bit-exact on their own; tests/test_gpu_gemv.py); the silu between
+them calls the platform exp (the oracle: host libm, the GPU: the device
+expf), which may differ in the last bit, so the MoE output is compared
+normwise at 1e-5.  Q8 mode is compared with the oracle's Q8 restatement per
+expert (same tolerance); F16_MFMA mode with the reference order at the
+fp16-dequant budget, 3e-3 normwise (two f16-rounded products in series).
+Every mode must be run-to-run bit identical (fixed grouping and combine
+order).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import rce_amd
+from rce_amd import GgufDtype as G, Mode
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def make_case(seed, n_expert, d_model, d_ff, t_rows, top_k, dt):
+    rng = np.random.default_rng(seed)
+    w1 = [O.quantize((rng.standard_normal((d_ff, d_model)) * 0.02).astype(F32), dt) for _ in range(n_expert)]
+    w2 = [O.quantize((rng.standard_normal((d_model, d_ff)) * 0.02).astype(F32), dt) for _ in range(n_expert)]
+    x = rng.standard_normal((t_rows, d_model)).astype(F32)
+    logits = rng.standard_normal((t_rows, n_expert)).astype(F32)
+    ids, gw = rce_amd.moe_router(logits, top_k)
+    return w1, w2, x, ids, gw
+
+
+def run_moe(ctx, w1b, w2b, dt, d_model, d_ff, x, ids, gw, mode):
+    t_rows, top_k = ids.shape
+    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, d_ff, d_model) for b in w1b]
+    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, d_model, d_ff) for b in w2b]
+    bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids.astype(np.int32))
+    bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw.astype(F32))
+    bo = rce_amd.DeviceBuffer(ctx, t_rows * d_model * 4)
+    outs = []
+    for _ in range(2):
+        rce_amd.moe_ffn_dev(ctx, W1, W2, bx.ptr, t_rows, bi.ptr, bw.ptr, top_k, bo.ptr, mode)
+        ctx.synchronize()
+        outs.append(bo.download(F32, t_rows * d_model).reshape(t_rows, d_model))
+    for b in (bx, bi, bw, bo):
+        b.free()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "not run-to-run deterministic"
+    return outs[0]
+
+
+def q8_reference(x, w1b, w2b, dt, d_model, d_ff, ids, gw):
+    """The Q8-activation path per (token, decision): the oracle's Q8 products
+    (mm_batched_q8), the oracle's silu, moe_combine."""
+    t_rows, top_k = ids.shape
+    out = np.zeros((t_rows, d_model), F32)
+    for t in range(t_rows):
+        ys = np.zeros((top_k, d_model), F32)
+        for j in range(top_k):
+            e = int(ids[t, j])
+            h = O.mm_batched_q8(x[t:t + 1], w1b[e], dt, d_ff, d_model)[0]
+            h = np.array([O.silu(float(v)) for v in h], F32)
+            ys[j] = O.mm_batched_q8(h[None, :], w2b[e], dt, d_model, d_ff)[0]
+        out[t] = O.moe_combine(gw[t], ys)
+    return out
+
+
+def normwise(got, want):
+    return float(np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(want)))
+
+
+CASES = [
+    # (n_expert, d_model, d_ff, t_rows, top_k, dtype)
+    (4, 512, 1024, 16, 2, O.Q4_0),
+    (8, 256, 512, 3, 2, O.Q4_0),     # most experts get no token
+    (4, 512, 768, 40, 1, O.Q4_0),    # top-1, ragged slots
+    (4, 512, 1024, 24, 2, O.Q4_K),
+]
+
+
+@pytest.mark.parametrize("E,dm,dff,t,k,dt", CASES)
+def test_moe_exact(ctx, E, dm, dff, t, k, dt):
+    note(f"moe exact E={E} d={dm} ff={dff} t={t} k={k} dt={dt}")
+    w1, w2, x, ids, gw = make_case(100 + E + t, E, dm, dff, t, k, dt)
+    got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.EXACT)
+    ref = O.moe_ffn(x, w1, w2, dt, dff, ids, gw)
+    assert normwise(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("E,dm,dff,t,k,dt", CASES[:2])
+def test_moe_q8(ctx, E, dm, dff, t, k, dt):
+    note(f"moe q8 E={E} d={dm} ff={dff} t={t} k={k} dt={dt}")
+    w1, w2, x, ids, gw = make_case(200 + E + t, E, dm, dff, t, k, dt)
+    got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.Q8)
+    ref = q8_reference(x, w1, w2, dt, dm, dff, ids, gw)
+    assert normwise(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("E,dm,dff,t,k,dt", CASES)
+def test_moe_f16_mfma(ctx, E, dm, dff, t, k, dt):
+    note(f"moe f16-mfma E={E} d={dm} ff={dff} t={t} k={k} dt={dt}")
+    w1, w2, x, ids, gw = make_case(300 + E + t, E, dm, dff, t, k, dt)
+    got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.F16_MFMA)
+    ref = O.moe_ffn(x, w1, w2, dt, dff, ids, gw)
+    assert normwise(got, ref) < 3e-3
+
+
+def test_moe_mixtral_shapes(ctx):
+    """configs[3] expert shapes (w1 14336x4096, w2 4096x14336, Q4_0) on two
+    experts and a few tokens: the full-size tiles and long K of both GEMMs."""
+    E, dm, dff, t, k, dt = 2, 4096, 14336, 6, 2, O.Q4_0
+    note(f"moe mixtral-shaped E={E} t={t}")
+    w1, w2, x, ids, gw = make_case(400, E, dm, dff, t, k, dt)
+    ref = O.moe_ffn(x, w1, w2, dt, dff, ids, gw)
+    got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.F16_MFMA)
+    assert normwise(got, ref) < 3e-3
+    got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.EXACT)
+    assert normwise(got, ref) < 1e-5
+
+
+def test_moe_bad_ids(ctx):
+    """An out-of-range expert id is an error in the synchronous modes."""
+    E, dm, dff, t, k, dt = 4, 256, 512, 4, 2, O.Q4_0
+    w1, w2, x, ids, gw = make_case(500, E, dm, dff, t, k, dt)
+    ids = ids.copy()
+    ids[1, 0] = E  # out of range
+    with pytest.raises(rce_amd.QmmError):
+        run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.EXACT)
