@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFS = 2500.0     # MI355X dense fp16 MFMA, TFLOP/s
 INFINITY_CACHE = 256 << 20
 HEADLINE_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_11008x4096_q8_traffic.md")
 
@@ -155,6 +156,82 @@ def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
     return ms, b, x, res, copies
 
 
+def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed):
+    """configs[2]-style prefill GEMM in F16_MFMA mode: A [m, k] f16 resident,
+    weights rotated over HBM copies; returns ms per launch and a normwise
+    check of the first 16 output rows against the oracle's exact order."""
+    import oracle as O
+    import rce_amd
+    b = make_weight(seed, dt, n, k)
+    copies = max(2, min(64, (2 * INFINITY_CACHE) // b.size + 1))
+    ws = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k) for _ in range(copies)]
+    rng = np.random.default_rng(seed + 1)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    out = rce_amd.DeviceBuffer(ctx, 4 * n * m)
+
+    def run(count):
+        for i in range(count):
+            rce_amd.mm_batched_dev(ctx, xa.ptr, rce_amd.GgufDtype.F16, m, ws[i % copies], out.ptr,
+                                   rce_amd.Mode.F16_MFMA)
+
+    run(max(1, warmup))
+    ctx.synchronize()
+    ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
+    ctx.synchronize()
+    res = out.download(np.float32, 16 * n).reshape(16, n)
+    ref = O.mm_batched(x[:16].astype(np.float32), b, dt, n, k)
+    err = float(np.max(np.abs(res.astype(np.float64) - ref)) / np.max(np.abs(ref)))
+    for w in ws:
+        w.close()
+    xa.free()
+    out.free()
+    return ms, err
+
+
+def time_moe(hip, ctx, steps, warmup, seed, mode):
+    """8 Q4_0 experts (w1 14336x4096, w2 4096x14336), 256 tokens,
+    top-2 of N(0,1) router logits; ms per grouped-FFN call (all 8 experts'
+    528 MB stream from HBM each call), the touched weight bytes, and a
+    normwise check of the first 8 tokens against the oracle's moe_ffn."""
+    import oracle as O
+    import rce_amd
+    E, dm, dff, T, K = 8, 4096, 14336, 256, 2
+    rng = np.random.default_rng(seed)
+    w1b, w2b = [], []
+    for _ in range(E):
+        w1b.append(O.quantize(rng.standard_normal((dff, dm), dtype=np.float32) * np.float32(0.02), O.Q4_0))
+        w2b.append(O.quantize(rng.standard_normal((dm, dff), dtype=np.float32) * np.float32(0.02), O.Q4_0))
+    x = rng.standard_normal((T, dm), dtype=np.float32)
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    ids, gw = rce_amd.moe_router(logits, K)
+    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, dff, dm) for b in w1b]
+    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, dm, dff) for b in w2b]
+    bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids)
+    bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw)
+    bo = rce_amd.DeviceBuffer(ctx, T * dm * 4)
+
+    def run(count):
+        for _ in range(count):
+            rce_amd.moe_ffn_dev(ctx, W1, W2, bx.ptr, T, bi.ptr, bw.ptr, K, bo.ptr, mode)
+
+    run(max(1, warmup))  # sizes scratch and uploads the expert tables before capture
+    ctx.synchronize()
+    ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
+    ctx.synchronize()
+    got = bo.download(np.float32, T * dm).reshape(T, dm)[:8]
+    ref = O.moe_ffn(x[:8], w1b, w2b, O.Q4_0, dff, ids[:8], gw[:8])
+    err = float(np.max(np.abs(got.astype(np.float64) - ref)) / np.max(np.abs(ref)))
+    touched = sorted(set(int(e) for e in ids.reshape(-1)))
+    wbytes = sum(w1b[e].size + w2b[e].size for e in touched)
+    for w in W1 + W2:
+        w.close()
+    for bb in (bx, bi, bw, bo):
+        bb.free()
+    return ms, err, wbytes + 2 * T * dm * 4
+
+
 def cpu_baseline(b, x, dt, n, k, budget_s=10.0):
     """Oracle (C restatement of mm_1d, OpenMP over rows) on the same workload."""
     import oracle as O
@@ -276,6 +353,24 @@ def main():
                 key = f"{name} {m.name.lower()}"
                 per[key] = {"us": round(sms * 1e3, 2), "GB/s": round(sg, 1), "hbm_frac": round(sg / HBM_PEAK_GBS, 4)}
                 log(f"  {key}: {sms * 1e3:.2f} us  {sg:.0f} GB/s ({sg / HBM_PEAK_GBS:.1%})")
+        # Q4_K prefill GEMM 512x4096x4096 on f16 MFMA
+        gms, gerr = time_gemm(hip, ctx, O.Q4_K, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
+        gtf = 2.0 * 512 * 4096 * 4096 / (gms * 1e-3) / 1e12
+        per["Q4_K GEMM 512x4096x4096 f16_mfma"] = {
+            "us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4),
+            "normwise_err_vs_oracle": float(f"{gerr:.3g}")}
+        log(f"  Q4_K GEMM 512x4096x4096: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of "
+            f"f16 MFMA peak), normwise err {gerr:.2e}")
+        # grouped MoE, 8 Q4_0 experts, 256 tokens, top-2
+        mms, merr, mbytes = time_moe(hip, ctx, 5, 2, 400, Mode.F16_MFMA)
+        mtf = 120259084288 / (mms * 1e-3) / 1e12
+        mgb = mbytes / (mms * 1e-3) / 1e9
+        per["MoE 8x(14336x4096, 4096x14336) Q4_0 T256 top2 f16_mfma"] = {
+            "us": round(mms * 1e3, 2), "TFLOP/s": round(mtf, 1), "mfma_frac": round(mtf / MFMA_F16_PEAK_TFS, 4),
+            "GB/s": round(mgb, 1), "hbm_frac": round(mgb / HBM_PEAK_GBS, 4),
+            "normwise_err_vs_oracle": float(f"{merr:.3g}")}
+        log(f"  MoE configs[3]: {mms * 1e3:.1f} us  {mtf:.0f} TFLOP/s ({mtf / MFMA_F16_PEAK_TFS:.1%}), "
+            f"{mgb:.0f} GB/s ({mgb / HBM_PEAK_GBS:.1%}), normwise err {merr:.2e}")
     line["per_format"] = per
 
     # ---- CPU baseline (oracle, same workload, bounded sample) ---------------------
