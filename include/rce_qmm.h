@@ -163,6 +163,15 @@ rce_qmm_status rce_qmm_mm_batched(rce_qmm_context *ctx, const float *a, size_t t
 rce_qmm_status rce_qmm_dequant_row(rce_qmm_context *ctx, const rce_qmm_weight *w, size_t row,
                                    float *out);
 
+/* GGUF bytes of f32 weights [n_rows, n_cols] (row-major) by the reference's
+ * quantizers: Q8_0 / Q4_0 by quantize_block (rce-vm-backend-cpu/src/ml/nn.rs
+ * L541-563, packed as spec/checker/tests/support/toy_gpt2.rs L46-58), Q4_K /
+ * Q6_K by quantize_k + pack (kquant.rs L193-346).  len must equal n_rows *
+ * row_bytes(dtype, n_cols).  Host only (no device needed); bit-identical for
+ * any thread count. */
+rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, size_t n_rows, size_t n_cols, uint8_t *dst,
+                                size_t len);
+
 /* ---- device-resident entry points (asynchronous on `stream`) ------------ */
 
 /* mm_batched on device buffers: a_dev [t_rows, n_cols] of a_dtype
@@ -196,6 +205,67 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
                                    const float *x_dev, size_t t_rows, const int32_t *ids_dev,
                                    const float *weights_dev, size_t top_k, float *out_dev,
                                    rce_qmm_mode mode, void *stream);
+
+/* ---- Llama-2 decode step (the TinyLlama caller) -------------------------- */
+
+/* TinyLlamaConfig (rce-tinyllama/src/lib.rs L28-41); d_head = d_model /
+ * n_q_heads there, given explicitly here. */
+typedef struct rce_qmm_llama_config {
+    size_t d_model, vocab, n_layers, n_q_heads, n_kv_heads, d_head, rope_dim, d_ff, context_length;
+    float rope_freq_base, eps;
+} rce_qmm_llama_config;
+
+/* TinyLlamaBlock (rce-tinyllama/src/lib.rs L94-99): host f32 norm weights
+ * [d_model] (copied at creation) and weight handles wq [n_q*d_head,
+ * d_model], wk / wv [n_kv*d_head, d_model], wo [d_model, n_q*d_head],
+ * ffn_gate / ffn_up [d_ff, d_model], ffn_down [d_model, d_ff]. */
+typedef struct rce_qmm_llama_block {
+    const float *attn_norm, *ffn_norm;
+    const rce_qmm_weight *wq, *wk, *wv, *wo, *ffn_gate, *ffn_up, *ffn_down;
+} rce_qmm_llama_block;
+
+/* A device-resident decoder: weights (shared with the handles given, which
+ * may be destroyed afterwards), KV caches of context_length positions and the
+ * decode-step state (TinyLlamaState, L144-155).  Every linear runs on the
+ * decode GEMV kernels in `mode` (EXACT or Q8) -- the qmm_1d calls of
+ * forward_embedding (L303-330) and attn_block (L252-287) -- and the steps
+ * between them (rms_norm, RoPE, attention, silu, residual adds) run on the
+ * device; one step is replayed from a HIP graph.
+ * Numerics: EXACT linears are the reference's bit for bit given their
+ * inputs; rms_norm's sum of squares is a fixed tree instead of a sequential
+ * fold and exp / silu use the device expf, so logits match the reference
+ * to a tolerance, not bitwise.  Run-to-run bit-identical. */
+typedef struct rce_qmm_llama rce_qmm_llama;
+
+rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_config *cfg,
+                                    const rce_qmm_weight *token_embd, const float *output_norm,
+                                    const rce_qmm_weight *lm_head, const rce_qmm_llama_block *blocks,
+                                    rce_qmm_mode mode, rce_qmm_llama **out);
+void rce_qmm_llama_destroy(rce_qmm_llama *m);
+
+/* TinyLlamaRuntime::new_state (L355): position 0, empty caches. */
+rce_qmm_status rce_qmm_llama_reset(rce_qmm_llama *m);
+/* TinyLlamaState::pos: positions decoded since the last reset. */
+rce_qmm_status rce_qmm_llama_pos(const rce_qmm_llama *m, size_t *pos);
+
+/* forward_logits / forward_token (L356, L289-294): logits [vocab] (host)
+ * of token_id at the current position, which then advances.  Synchronous.
+ * token_id outside [0, token_embd rows) or a full cache: RCE_QMM_BAD_SHAPE
+ * (the reference panics), state unchanged. */
+rce_qmm_status rce_qmm_llama_forward_token(rce_qmm_llama *m, int32_t token_id, float *logits);
+/* forward_logits_embed / forward_embedding (L362, L303-330): the same
+ * from a [d_model] input embedding (host).  Synchronous. */
+rce_qmm_status rce_qmm_llama_forward_embedding(rce_qmm_llama *m, const float *embedding, float *logits);
+/* forward_token on device memory, asynchronous on `stream` (NULL = the
+ * context's stream): token id read from token_dev, logits written to
+ * logits_dev [vocab].  A full cache is RCE_QMM_BAD_SHAPE at the call; an
+ * out-of-range token id found on the device is reported by
+ * rce_qmm_llama_check (that step's logits are then undefined). */
+rce_qmm_status rce_qmm_llama_forward_token_dev(rce_qmm_llama *m, const int32_t *token_dev, float *logits_dev,
+                                               void *stream);
+/* Wait for the decoder's work and report (then clear) an error found on the
+ * device since the last check: RCE_QMM_BAD_SHAPE for a token id out of range. */
+rce_qmm_status rce_qmm_llama_check(rce_qmm_llama *m);
 
 /* ---- device memory helpers (for callers without a HIP runtime) ---------- */
 

@@ -10,7 +10,9 @@ order, the kernels of ``compute/crates/rce-op-qmm/src/lib.rs``, the
 dequantizers of ``compute/crates/rce-ingest-gguf/src/dequant.rs``, the
 quantizers and value-form products of
 ``compute/crates/rce-vm-backend-cpu/src/ml/{nn,kquant}.rs`` and the MoE
-router/combine of ``compute/crates/rce-op-moe/src/lib.rs``; each C function
+router/combine of ``compute/crates/rce-op-moe/src/lib.rs`` and the Llama-2
+decode step of ``compute/crates/rce-tinyllama/src/lib.rs`` with the RoPE and
+attention of ``compute/crates/rce-op-attn/src/lib.rs``; each C function
 cites the file:line it follows.  The reference itself is Rust and cannot be
 built here, so there is no ``oracle/_ref`` build.
 """
@@ -73,6 +75,10 @@ def lib() -> ctypes.CDLL:
             "orc_moe_combine": (None, [P, P, S, S, P]),
             "orc_moe_ffn": (I, [P, S, S, S, P, P, U32, P, P, S, P, I]),
             "orc_max_threads": (I, []),
+            "orc_rms_norm": (None, [P, P, S, F, P]),
+            "orc_rope": (None, [P, S, F, S, P]),
+            "orc_attend_head": (None, [P, P, P, S, S, S, S, F, P]),
+            "orc_llama_forward": (I, [P, F, F, I, P, P, P, P, P, P, P, U32, P, P, S, P, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -271,3 +277,89 @@ def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0) -> 
     if rc:
         raise ValueError(f"orc_moe_ffn rc={rc}")
     return out
+
+
+# ---- Llama-2 decode step (rce-tinyllama L158-330, rce-op-attn L107-251) ----
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x = _c(x, np.float32); w = _c(w, np.float32)
+    out = np.zeros_like(x)
+    lib().orc_rms_norm(_p(x), _p(w), x.size, float(eps), _p(out))
+    return out
+
+
+def rope(x, rope_dim: int, base: float, pos: int):
+    """One head rotated in place (returns the new head and the (cos, sin)
+    pairs used, shape [rope_dim // 2, 2])."""
+    x = _c(x, np.float32).copy()
+    cs = np.zeros((rope_dim // 2, 2), np.float32)
+    lib().orc_rope(_p(x), rope_dim, float(base), pos, _p(cs))
+    return x, cs
+
+
+def attend_head(q, k_cache, v_cache, kv_head: int, seq_len: int, kv_dim: int, d_head: int, scale: float):
+    q = _c(q, np.float32); k_cache = _c(k_cache, np.float32); v_cache = _c(v_cache, np.float32)
+    out = np.zeros(d_head, np.float32)
+    lib().orc_attend_head(_p(q), _p(k_cache), _p(v_cache), kv_head, seq_len, kv_dim, d_head, float(scale), _p(out))
+    return out
+
+
+class Llama:
+    """The reference's TinyLlama decode (forward_embedding / forward_token)
+    over GGUF weight bytes: cfg is a dict with d_model, vocab, n_layers,
+    n_q_heads, n_kv_heads, d_head, rope_dim, rope_freq_base, d_ff,
+    context_length, eps.  blocks: per layer a dict with attn_norm, ffn_norm
+    (f32 arrays) and wq, wk, wv, wo, ffn_gate, ffn_up, ffn_down as
+    (bytes, dtype).  token_embd and lm_head: (bytes, dtype).  q8: every
+    linear uses the Q8-activation path instead of mm_1d."""
+
+    LIN = ("wq", "wk", "wv", "wo", "ffn_gate", "ffn_up", "ffn_down")
+
+    def __init__(self, cfg, token_embd, output_norm, lm_head, blocks, q8: bool = False, threads: int = 0):
+        self.cfg = dict(cfg)
+        c = self.cfg
+        self.dims = np.array([c["d_model"], c["vocab"], c["n_layers"], c["n_q_heads"], c["n_kv_heads"],
+                              c["d_head"], c["rope_dim"], c["d_ff"], c["context_length"]], np.uint64)
+        self.token_embd = (_c(token_embd[0], np.uint8), int(token_embd[1]))
+        self.output_norm = _c(output_norm, np.float32)
+        self.lm_head = (_c(lm_head[0], np.uint8), int(lm_head[1]))
+        self.attn_norm = _c(np.stack([b["attn_norm"] for b in blocks]), np.float32)
+        self.ffn_norm = _c(np.stack([b["ffn_norm"] for b in blocks]), np.float32)
+        self._bytes = [_c(b[n][0], np.uint8) for b in blocks for n in self.LIN]
+        self._ptrs = (ctypes.c_void_p * len(self._bytes))(*[b.ctypes.data for b in self._bytes])
+        self._types = np.array([int(b[n][1]) for b in blocks for n in self.LIN], np.uint32)
+        self.q8 = q8
+        self.threads = threads or max_threads()
+        self.reset()
+
+    def reset(self):
+        c = self.cfg
+        kv = c["n_kv_heads"] * c["d_head"]
+        self.k_cache = np.zeros((c["n_layers"], c["context_length"], kv), np.float32)
+        self.v_cache = np.zeros_like(self.k_cache)
+        self.pos = 0
+
+    def embed(self, token_id: int) -> np.ndarray:
+        """QuantWeight::dequant_row (rce-op-qmm L150-167) of token_embd."""
+        b, dt = self.token_embd
+        dm = self.cfg["d_model"]
+        rb = row_bytes(dt, dm)
+        return dequantize(b[token_id * rb:(token_id + 1) * rb], dt, dm)
+
+    def forward_embedding(self, embedding) -> np.ndarray:
+        c = self.cfg
+        e = _c(embedding, np.float32)
+        assert e.size == c["d_model"]
+        logits = np.zeros(c["vocab"], np.float32)
+        rc = lib().orc_llama_forward(
+            _p(self.dims), float(c["rope_freq_base"]), float(c["eps"]), int(self.q8), _p(e),
+            _p(self.attn_norm), _p(self.ffn_norm), ctypes.cast(self._ptrs, ctypes.c_void_p), _p(self._types),
+            _p(self.output_norm), _p(self.lm_head[0]), self.lm_head[1], _p(self.k_cache), _p(self.v_cache),
+            self.pos, _p(logits), self.threads)
+        if rc:
+            raise ValueError(f"orc_llama_forward rc={rc}")
+        self.pos += 1
+        return logits
+
+    def forward_token(self, token_id: int) -> np.ndarray:
+        return self.forward_embedding(self.embed(token_id))

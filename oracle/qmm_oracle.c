@@ -1055,6 +1055,145 @@ EXPORT int orc_moe_ffn(const float *x, size_t t_rows, size_t d_model, size_t d_f
     return rc;
 }
 
+/* ------------------------------------------------------------------ */
+/* Llama-2 decode step (rce-tinyllama, rce-op-attn)                     */
+/* ------------------------------------------------------------------ */
+
+/* rce-tinyllama/src/lib.rs L158-163 `rms_norm`: mean_sq = (sum of v*v,
+ * one sequential fold from +0.0) / n; inv = 1 / sqrt(mean_sq + eps);
+ * out = (v * inv) * w. */
+EXPORT void orc_rms_norm(const float *x, const float *w, size_t n, float eps, float *out) {
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) { float t = x[i] * x[i]; ss += t; }
+    float mean_sq = ss / (float)n;
+    float inv = 1.0f / sqrtf(mean_sq + eps);
+    for (size_t i = 0; i < n; i++) { float t = x[i] * inv; out[i] = t * w[i]; }
+}
+
+/* rce-op-attn/src/lib.rs L115-151 `rope_inplace_scaled` (no frequency
+ * factors): log_base = ln(base); inv_freq_i = 1 / exp(log_base * (2i) /
+ * rope_dim); theta = pos * inv_freq_i; pairs (x[i], x[i + half]) become
+ * (a c - b s, a s + b c).  cos_sin (optional): the 2*half values
+ * (c_0, s_0, c_1, s_1, ...) used, for checking a device table. */
+EXPORT void orc_rope(float *x, size_t rope_dim, float base, size_t pos, float *cos_sin) {
+    size_t half = rope_dim / 2;
+    float log_base = logf(base);
+    for (size_t i = 0; i < half; i++) {
+        float e = log_base * (2.0f * (float)i);
+        e = e / (float)rope_dim;
+        float inv_freq = 1.0f / expf(e);
+        float theta = (float)pos * inv_freq;
+        float s = sinf(theta), c = cosf(theta);
+        if (cos_sin) { cos_sin[2 * i] = c; cos_sin[2 * i + 1] = s; }
+        float a = x[i], b = x[i + half];
+        float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+        x[i] = ac - bs;
+        x[i + half] = as + bc;
+    }
+}
+
+/* rce-op-attn/src/lib.rs L185-251 `fused_attend_head_window` over
+ * [0, seq_len): s_j = dot(q, k_j) * scale (dot = sequential sum of
+ * products, L60-95 on x86); the first key sets out = 0 + 1 * v, l = 1,
+ * m = s; every later key: m' = max(m, s), alpha = exp(m - m'),
+ * beta = exp(s - m'), out = out * alpha + beta * v, l = l * alpha + beta;
+ * finally out *= 1 / l. */
+EXPORT void orc_attend_head(const float *q, const float *k_cache, const float *v_cache, size_t kv_head,
+                            size_t seq_len, size_t kv_dim, size_t d_head, float scale, float *out) {
+    size_t off = kv_head * d_head;
+    float m = -INFINITY, l = 0.0f;
+    for (size_t i = 0; i < d_head; i++) out[i] = 0.0f;
+    for (size_t j = 0; j < seq_len; j++) {
+        const float *k = k_cache + j * kv_dim + off, *v = v_cache + j * kv_dim + off;
+        float dot = 0.0f;
+        for (size_t i = 0; i < d_head; i++) { float t = q[i] * k[i]; dot += t; }
+        float s = dot * scale;
+        float m_new = fmaxf(m, s);
+        if (isinf(m)) {
+            for (size_t i = 0; i < d_head; i++) { float t = 1.0f * v[i]; out[i] += t; }
+            l = 1.0f;
+            m = s;
+        } else {
+            float alpha = expf(m - m_new), beta = expf(s - m_new);
+            for (size_t i = 0; i < d_head; i++) out[i] *= alpha;
+            for (size_t i = 0; i < d_head; i++) { float t = beta * v[i]; out[i] += t; }
+            float la = l * alpha;
+            l = la + beta;
+            m = m_new;
+        }
+    }
+    if (l != 0.0f) {
+        float inv = 1.0f / l;
+        for (size_t i = 0; i < d_head; i++) out[i] *= inv;
+    }
+}
+
+/* One linear of the decoder: mm_1d (q8 = 0) or the Q8-activation path. */
+static int dec_linear(const float *a, const uint8_t *w, uint32_t t, size_t n, size_t k, float *out, int q8,
+                      int threads) {
+    return q8 ? orc_mm_batched_q8(a, 1, w, t, n, k, out, threads) : orc_mm_1d(a, w, t, n, k, out, threads);
+}
+
+/* rce-tinyllama/src/lib.rs L303-330 `forward_embedding` with `attn_block`
+ * (L252-287): one decode step at position `pos` from the input embedding.
+ * dims: d_model, vocab, n_layers, n_q_heads, n_kv_heads, d_head,
+ * rope_dim, d_ff, context_length.  lin: n_layers * 7 weights (GGUF bytes)
+ * in the order wq, wk, wv, wo, ffn_gate, ffn_up, ffn_down, with their
+ * dtypes in lin_dtype.  attn_norm / ffn_norm: [n_layers][d_model].
+ * k_cache / v_cache: [n_layers][context_length][n_kv_heads * d_head]; the
+ * step appends position pos.  logits: [vocab].  Returns 0, or the
+ * failing linear's code, or -10 when pos >= context_length. */
+EXPORT int orc_llama_forward(const size_t *dims, float rope_base, float eps, int q8, const float *embedding,
+                             const float *attn_norm, const float *ffn_norm, const uint8_t *const *lin,
+                             const uint32_t *lin_dtype, const float *output_norm, const uint8_t *lm_head,
+                             uint32_t lm_dtype, float *k_cache, float *v_cache, size_t pos, float *logits,
+                             int threads) {
+    size_t dm = dims[0], vocab = dims[1], nl = dims[2], nq = dims[3], nkv = dims[4], dh = dims[5];
+    size_t rope_dim = dims[6], dff = dims[7], ctx = dims[8];
+    if (pos >= ctx) return -10;
+    size_t qd = nq * dh, kvd = nkv * dh, qpk = nq / nkv;
+    size_t big = dff > qd ? dff : qd;
+    float *x = malloc(dm * 4), *xn = malloc(dm * 4), *q = malloc(qd * 4), *kk = malloc(kvd * 4);
+    float *vv = malloc(kvd * 4), *att = malloc(qd * 4), *o = malloc(dm * 4);
+    float *g = malloc(big * 4), *u = malloc(big * 4), *h = malloc(big * 4);
+    int rc = 0;
+    memcpy(x, embedding, dm * 4);
+    float scale = 1.0f / sqrtf((float)dh);
+    for (size_t il = 0; il < nl && rc == 0; il++) {
+        const uint8_t *const *W = lin + il * 7;
+        const uint32_t *T = lin_dtype + il * 7;
+        float *kc = k_cache + il * ctx * kvd, *vc = v_cache + il * ctx * kvd;
+        orc_rms_norm(x, attn_norm + il * dm, dm, eps, xn);
+        rc = dec_linear(xn, W[0], T[0], qd, dm, q, q8, threads);
+        if (!rc) rc = dec_linear(xn, W[1], T[1], kvd, dm, kk, q8, threads);
+        if (!rc) rc = dec_linear(xn, W[2], T[2], kvd, dm, vv, q8, threads);
+        if (rc) break;
+        for (size_t hh = 0; hh < nq; hh++) orc_rope(q + hh * dh, rope_dim, rope_base, pos, 0);
+        for (size_t hh = 0; hh < nkv; hh++) orc_rope(kk + hh * dh, rope_dim, rope_base, pos, 0);
+        memcpy(kc + pos * kvd, kk, kvd * 4);
+        memcpy(vc + pos * kvd, vv, kvd * 4);
+        for (size_t hh = 0; hh < nq; hh++)
+            orc_attend_head(q + hh * dh, kc, vc, hh / qpk, pos + 1, kvd, dh, scale, att + hh * dh);
+        rc = dec_linear(att, W[3], T[3], dm, qd, o, q8, threads);
+        if (rc) break;
+        for (size_t i = 0; i < dm; i++) x[i] += o[i];
+        orc_rms_norm(x, ffn_norm + il * dm, dm, eps, xn);
+        rc = dec_linear(xn, W[4], T[4], dff, dm, g, q8, threads);
+        if (!rc) rc = dec_linear(xn, W[5], T[5], dff, dm, u, q8, threads);
+        if (rc) break;
+        for (size_t i = 0; i < dff; i++) h[i] = orc_silu(g[i]) * u[i];
+        rc = dec_linear(h, W[6], T[6], dm, dff, o, q8, threads);
+        if (rc) break;
+        for (size_t i = 0; i < dm; i++) x[i] += o[i];
+    }
+    if (!rc) {
+        orc_rms_norm(x, output_norm, dm, eps, xn);
+        rc = dec_linear(xn, lm_head, lm_dtype, vocab, dm, logits, q8, threads);
+    }
+    free(x); free(xn); free(q); free(kk); free(vv); free(att); free(o); free(g); free(u); free(h);
+    return rc;
+}
+
 EXPORT int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -2,9 +2,11 @@
 
 The product is the C-ABI library ``rce_amd/lib/librce_qmm.so`` (HIP kernels
 in ``rce_amd/csrc``, interface ``include/rce_qmm.h``).  ``rce_amd.qmm`` is the
-Python mirror of the reference operator API (``rce-op-qmm``) over that ABI.
+Python mirror of the reference operator API (``rce-op-qmm``) over that ABI;
+``rce_amd.llama`` mirrors the TinyLlama decode runtime (``rce-tinyllama``).
 """
 from .qmm import (  # noqa: F401
     Context, DeviceBuffer, GgufDtype, Mode, QmmError, QuantWeight, block_geometry, mm_1d,
-    mm_1d_serial, mm_batched, mm_batched_dev, moe_ffn_dev, moe_router, row_bytes, supports,
+    mm_1d_serial, mm_batched, mm_batched_dev, moe_ffn_dev, moe_router, quantize, row_bytes, supports,
 )
+from .llama import TinyLlamaBlock, TinyLlamaConfig, TinyLlamaRuntime, TinyLlamaWeights  # noqa: F401,E402

@@ -31,9 +31,18 @@ SIGNATURES = {
     "rce_qmm_mm_1d_serial": (STATUS, [P, P, P, P]),
     "rce_qmm_mm_batched": (STATUS, [P, P, S, P, P]),
     "rce_qmm_dequant_row": (STATUS, [P, P, S, P]),
+    "rce_qmm_quantize": (STATUS, [U32, P, S, S, P, S]),
     "rce_qmm_mm_batched_dev": (STATUS, [P, P, U32, S, P, P, I, P]),
     "rce_qmm_moe_router": (STATUS, [P, S, S, S, I, P, P]),
     "rce_qmm_moe_ffn_dev": (STATUS, [P, P, P, S, P, S, P, P, S, P, I, P]),
+    "rce_qmm_llama_create": (STATUS, [P, P, P, P, P, P, I, P]),
+    "rce_qmm_llama_destroy": (None, [P]),
+    "rce_qmm_llama_reset": (STATUS, [P]),
+    "rce_qmm_llama_pos": (STATUS, [P, P]),
+    "rce_qmm_llama_forward_token": (STATUS, [P, ctypes.c_int32, P]),
+    "rce_qmm_llama_forward_embedding": (STATUS, [P, P, P]),
+    "rce_qmm_llama_forward_token_dev": (STATUS, [P, P, P, P]),
+    "rce_qmm_llama_check": (STATUS, [P]),
     "rce_qmm_dev_alloc": (STATUS, [P, S, P]),
     "rce_qmm_dev_free": (STATUS, [P, P]),
     "rce_qmm_memcpy_h2d": (STATUS, [P, P, P, S]),

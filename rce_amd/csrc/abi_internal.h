@@ -1,0 +1,104 @@
+// abi_internal.h -- what the C-ABI translation units (qmm_abi.cpp,
+// llama.cpp) share: the context and weight objects behind the opaque
+// handles of include/rce_qmm.h, the thread-local last-error text and the
+// device-memory helpers.  Not installed.
+#pragma once
+
+#include "../../include/rce_qmm.h"
+#include "qmm_internal.h"
+
+#include <algorithm>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace rce_qmm_abi {
+
+using namespace rce_qmm;
+
+// Record `msg` as this thread's last error (rce_qmm_last_error) and return s.
+rce_qmm_status fail(rce_qmm_status s, const std::string &msg);
+
+inline rce_qmm_status hip_fail(hipError_t e, const char *what) {
+    return fail(RCE_QMM_HIP_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                       \
+    do {                                                    \
+        hipError_t e_ = (expr);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr);   \
+    } while (0)
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// A device allocation shared by a weight and its views.
+struct DevAlloc {
+    void *p = nullptr;
+    int device = 0;
+    ~DevAlloc() {
+        if (p) {
+            int cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(device);
+            (void)hipFree(p);
+            (void)hipSetDevice(cur);
+        }
+    }
+};
+
+// Grow-only device buffer owned by a context.
+struct Scratch {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+}  // namespace rce_qmm_abi
+
+struct rce_qmm_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    rce_qmm_abi::Scratch a_in, a_f32, out;
+    rce_qmm_abi::Scratch a_f16;  // f32 activations rounded to f16 for the MFMA GEMM
+    // grouped experts: grouping metadata, expert tables, stage buffers
+    rce_qmm_abi::Scratch moe_meta, moe_wtab, moe_x, moe_h, moe_h16, moe_y;
+    std::vector<rce_qmm::DevWeight> moe_wtab_host;  // what moe_wtab holds
+};
+
+struct rce_qmm_weight {
+    std::shared_ptr<rce_qmm_abi::DevAlloc> alloc;
+    rce_qmm::DevWeight dw{};
+    size_t host_row_bytes = 0;  // GGUF bytes per row
+    size_t len = 0;             // GGUF byte length of this view
+    int device = 0;
+};
+
+namespace rce_qmm_abi {
+
+inline rce_qmm_status set_device(int dev) {
+    HIP_TRY(hipSetDevice(dev));
+    return RCE_QMM_OK;
+}
+
+// Make `s` hold at least `bytes`; waits for the context's stream before a
+// reallocation so in-flight kernels never see a freed buffer.
+inline rce_qmm_status ensure(rce_qmm_context *ctx, Scratch &s, size_t bytes, hipStream_t other) {
+    if (s.cap >= bytes) return RCE_QMM_OK;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (other && other != ctx->stream) HIP_TRY(hipStreamSynchronize(other));
+    if (s.p) HIP_TRY(hipFree(s.p));
+    s.p = nullptr;
+    s.cap = 0;
+    size_t cap = align_up(std::max<size_t>(bytes, 4096), 4096);
+    hipError_t e = hipMalloc(&s.p, cap);
+    if (e != hipSuccess) return fail(RCE_QMM_OUT_OF_MEMORY, std::string("scratch hipMalloc: ") + hipGetErrorString(e));
+    s.cap = cap;
+    return RCE_QMM_OK;
+}
+
+inline rce_qmm_status check_weight_ctx(rce_qmm_context *ctx, const rce_qmm_weight *w) {
+    if (!ctx || !w) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight");
+    if (ctx->device != w->device) return fail(RCE_QMM_BAD_SHAPE, "weight lives on another device than the context");
+    return RCE_QMM_OK;
+}
+
+}  // namespace rce_qmm_abi

@@ -1,0 +1,264 @@
+// decoder.hip -- the non-linear steps of the Llama-2 decode step that sit
+// between the quantized matmuls (rce-tinyllama/src/lib.rs L158-330 with
+// rce-op-attn/src/lib.rs L107-251), so that activations stay in HBM for the
+// whole token.  The matmuls themselves are the decode GEMV kernels
+// (qmm_gemv_kernels.h), in their fused forms where the step allows.
+//
+// Numerics (each kernel states its own):
+//   * rms_norm: the sum of squares is a fixed-shape tree (run-to-run
+//     deterministic) where the reference folds sequentially, so the norm's
+//     scale may differ from the reference's in the last bits; every other
+//     operation is the reference's, one rounding each.
+//   * RoPE: the (cos, sin) table is built on the host with the C library's
+//     logf / expf / sinf / cosf in the reference's expression order (the
+//     functions Rust's f32 methods call on Linux), so the rotation is the
+//     reference's bit for bit.
+//   * attention: the reference's key order and recurrence; exp is the
+//     device's expf (last-bit differences from the host libm).
+//   * silu: silu_ref (device expf).
+// This file is built with -ffp-contract=off: no multiply-add contraction.
+#include "qmm_internal.h"
+
+namespace rce_qmm {
+namespace {
+
+constexpr int NORM_NT = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+    // fixed butterfly: the same tree on every call
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+    return v;
+}
+
+// rce-tinyllama/src/lib.rs L158-163: mean_sq = sum(v*v) / n,
+// inv = 1 / sqrt(mean_sq + eps), out = (v * inv) * w.
+__global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w, int n,
+                                                      float eps, float *__restrict__ out, int *pos_next,
+                                                      int *pos_cur, int ctx_len, int *status) {
+    __shared__ float part[NORM_NT / 64];
+    const int t = threadIdx.x;
+    if (pos_next && t == 0) {  // the first kernel of a decode step
+        const int p = pos_next[0];
+        pos_cur[0] = p;
+        pos_next[0] = p + 1;
+        if (p >= ctx_len) status[0] = 2;
+    }
+    float ss = 0.0f;
+    for (int i = t; i < n; i += NORM_NT) {
+        const float sq = x[i] * x[i];
+        ss = ss + sq;
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NORM_NT / 64; i++) tot = tot + part[i];
+    const float mean_sq = tot / (float)n;
+    const float inv = 1.0f / sqrtf(mean_sq + eps);
+    for (int i = t; i < n; i += NORM_NT) {
+        const float v = x[i] * inv;
+        out[i] = v * w[i];
+    }
+}
+
+// One block (one wave) per query head h; kv head g = h / (n_q / n_kv)
+// (rce-tinyllama L262-281).  Steps:
+//  1. q_h and k_g, v_g of this position from the q|k|v projections;
+//     RoPE of q_h and k_g (rce-op-attn L115-151): pairs (i, i + half),
+//     (a, b) -> (a c - b s, a s + b c) with the position's table row.
+//  2. The first query head of each kv group appends k_g, v_g to the caches
+//     at pos (every head of the group uses its own copy of this position's
+//     k and v, so no block waits for another).
+//  3. fused_attend_head_window (rce-op-attn L196-251) over keys 0..pos in
+//     order: s_j = dot(q, k_j) * scale (dot: sequential sum of products);
+//     key 0 sets out = 0 + 1 * v_0, l = 1; key j > 0: m' = max(m, s_j),
+//     alpha = exp(m - m'), beta = exp(s_j - m'), out = out * alpha +
+//     beta * v_j, l = l * alpha + beta; finally out *= 1 / l.  Keys are
+//     staged in chunks of CH through LDS: lane j computes s_j, the running
+//     maxima come from a prefix max over the chunk (max is exact, so these
+//     equal the reference's sequential maxima), and the out / l recurrence
+//     runs in key order with lane = dimension.
+template <int DH>
+__global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv, const float *__restrict__ rope_cs,
+                                                  float *__restrict__ k_cache, float *__restrict__ v_cache,
+                                                  const int *__restrict__ pos_cur, int ctx_len, int n_q, int n_kv,
+                                                  int rope_dim, float scale, float *__restrict__ att) {
+    constexpr int DPL = DH / 64;    // dimensions per lane
+    constexpr int CH = 4096 / DH;   // keys per chunk (64 or 32): 33 KB of LDS staging
+    constexpr int KLD = DH + 1;     // padded key rows: lane j reads row j without bank conflicts
+    __shared__ float qs[DH], ks[DH], vs[DH];
+    __shared__ float kch[CH * KLD];
+    __shared__ float vch[CH * DH];
+    __shared__ float al[CH], be[CH];
+    const int lane = threadIdx.x, h = blockIdx.x;
+    const int pos = pos_cur[0];
+    if (pos < 0 || pos >= ctx_len) return;  // status was set by the step's first kernel
+    const int qpk = n_q / n_kv, g = h / qpk;
+    const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH;
+    for (int i = lane; i < DH; i += 64) {
+        qs[i] = qkv[(size_t)h * DH + i];
+        ks[i] = qkv[qd + (size_t)g * DH + i];
+        vs[i] = qkv[qd + kvd + (size_t)g * DH + i];
+    }
+    __syncthreads();
+    const int half = rope_dim / 2;
+    const float *cs = rope_cs + (size_t)pos * half * 2;
+    for (int i = lane; i < half; i += 64) {
+        const float c = cs[2 * i], s = cs[2 * i + 1];
+        float a = qs[i], b = qs[i + half];
+        float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+        qs[i] = ac - bs;
+        qs[i + half] = as + bc;
+        a = ks[i];
+        b = ks[i + half];
+        ac = a * c; bs = b * s; as = a * s; bc = b * c;
+        ks[i] = ac - bs;
+        ks[i + half] = as + bc;
+    }
+    __syncthreads();
+    if (h % qpk == 0) {
+        float *kd = k_cache + (size_t)pos * kvd + (size_t)g * DH, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
+        for (int i = lane; i < DH; i += 64) {
+            kd[i] = ks[i];
+            vd[i] = vs[i];
+        }
+    }
+    const int seq = pos + 1;
+    float o[DPL];
+#pragma unroll
+    for (int d = 0; d < DPL; d++) o[d] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    for (int c0 = 0; c0 < seq; c0 += CH) {
+        const int n = min(CH, seq - c0);
+        // stage keys and values c0 .. c0 + n - 1 (position pos from this block's own copy)
+        constexpr int R4 = DH / 4;  // float4 pieces per row
+        for (int p = lane; p < n * R4; p += 64) {
+            const int r = p / R4, c4 = p - r * R4, row = c0 + r;
+            float4 kv, vv;
+            if (row == pos) {
+                kv = make_float4(ks[4 * c4], ks[4 * c4 + 1], ks[4 * c4 + 2], ks[4 * c4 + 3]);
+                vv = make_float4(vs[4 * c4], vs[4 * c4 + 1], vs[4 * c4 + 2], vs[4 * c4 + 3]);
+            } else {
+                kv = *reinterpret_cast<const float4 *>(k_cache + (size_t)row * kvd + (size_t)g * DH + 4 * c4);
+                vv = *reinterpret_cast<const float4 *>(v_cache + (size_t)row * kvd + (size_t)g * DH + 4 * c4);
+            }
+            float *kr = kch + r * KLD + 4 * c4;
+            kr[0] = kv.x; kr[1] = kv.y; kr[2] = kv.z; kr[3] = kv.w;
+            *reinterpret_cast<float4 *>(vch + r * DH + 4 * c4) = vv;
+        }
+        __syncthreads();
+        float sc = -INFINITY;
+        if (lane < n) {
+            const float *kr = kch + lane * KLD;
+            float dot = 0.0f;
+#pragma unroll 16
+            for (int i = 0; i < DH; i++) {
+                const float pr = qs[i] * kr[i];
+                dot = dot + pr;
+            }
+            sc = dot * scale;
+        }
+        // running maxima: inclusive prefix max over the chunk, after m
+        // (lanes past n hold -inf and come after every valid lane)
+        float pm = sc;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float t = __shfl_up(pm, off);
+            if (lane >= off) pm = fmaxf(pm, t);
+        }
+        const float m_incl = fmaxf(m, pm);
+        float m_prev = __shfl_up(m_incl, 1);
+        if (lane == 0) m_prev = m;
+        if (lane < n) {
+            al[lane] = expf(m_prev - m_incl);
+            be[lane] = expf(sc - m_incl);
+        }
+        m = __shfl(m_incl, n - 1);
+        __syncthreads();
+        for (int j = 0; j < n; j++) {
+            const float *vr = vch + j * DH;
+            if (c0 + j == 0) {  // the first key: out = 0 + 1 * v, l = 1
+#pragma unroll
+                for (int d = 0; d < DPL; d++) {
+                    const float t = 1.0f * vr[lane + 64 * d];
+                    o[d] = o[d] + t;
+                }
+                l = 1.0f;
+            } else {
+                const float a = al[j], b = be[j];
+#pragma unroll
+                for (int d = 0; d < DPL; d++) {
+                    const float t1 = o[d] * a, t2 = b * vr[lane + 64 * d];
+                    o[d] = t1 + t2;
+                }
+                const float la = l * a;
+                l = la + b;
+            }
+        }
+        __syncthreads();  // the next chunk overwrites the staging buffers
+    }
+    float *out = att + (size_t)h * DH;
+    if (l != 0.0f) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int d = 0; d < DPL; d++) o[d] = o[d] * inv;
+    }
+#pragma unroll
+    for (int d = 0; d < DPL; d++) out[lane + 64 * d] = o[d];
+}
+
+__global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ h, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = silu_ref(g[i]) * u[i];  // rce-tinyllama L320
+}
+
+__global__ void k_add_inplace(float *__restrict__ x, const float *__restrict__ o, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = x[i] + o[i];  // rce-tinyllama L318, L323
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos_next, int *pos_cur,
+                           int ctx_len, int *status, hipStream_t s) {
+    hipLaunchKernelGGL(k_rms_norm, dim3(1), dim3(NORM_NT), 0, s, x, w, (int)n, eps, out, pos_next, pos_cur, ctx_len,
+                       status);
+    return hipGetLastError();
+}
+
+bool attention_supports(int d_head, int rope_dim) {
+    return (d_head == 64 || d_head == 128) && rope_dim >= 0 && rope_dim <= d_head && rope_dim % 2 == 0;
+}
+
+hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache, const int *pos_cur,
+                            int ctx_len, int n_q, int n_kv, int d_head, int rope_dim, float scale, float *att,
+                            hipStream_t s) {
+    if (n_kv <= 0 || n_q % n_kv) return hipErrorInvalidValue;
+    switch (d_head) {
+    case 64:
+        hipLaunchKernelGGL(k_attention<64>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos_cur, ctx_len,
+                           n_q, n_kv, rope_dim, scale, att);
+        break;
+    case 128:
+        hipLaunchKernelGGL(k_attention<128>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos_cur,
+                           ctx_len, n_q, n_kv, rope_dim, scale, att);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float *g, const float *u, float *h, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, h, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_inplace(float *x, const float *o, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_add_inplace, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, o, n);
+    return hipGetLastError();
+}
+
+}  // namespace rce_qmm

@@ -7,4 +7,8 @@ hipError_t launch_gemv_q4_k(const DevWeight &w, const GemvGeom &g, const float *
     if (mode == 0) return launch_as_tb<Q4_KExact, false, 2>(w, g, a, t_rows, out, s);
     return launch_as_tb<Q4_KQ8, true, 4>(w, g, a, t_rows, out, s);
 }
+hipError_t launch_gemv_fx_q4_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s) {
+    if (mode == 0) return launch_as_fx_nt<Q4_KExact<1>, false>(f, g, a, s);
+    return launch_as_fx_nt<Q4_KQ8<1>, true>(f, g, a, s);
+}
 }  // namespace rce_qmm

@@ -69,4 +69,8 @@ hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *
     }
     return launch_as_tb<Q6_KQ8, true, 2>(w, g, a, t_rows, out, s);
 }
+hipError_t launch_gemv_fx_q6_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s) {
+    if (mode == 0) return hipErrorInvalidValue;  // EXACT Q6_K is one lane per row
+    return launch_as_fx_nt<Q6_KQ8<1>, true>(f, g, a, s);
+}
 }  // namespace rce_qmm

@@ -92,30 +92,17 @@ __global__ void k_gather_rows(const float *__restrict__ x, const int *__restrict
     }
 }
 
-// silu (rce-tinyllama/src/lib.rs L164-166, rce-qwen36-moe L459-461): x * sigmoid(x),
-// evaluated like the oracle's restatement (the branch keeps exp's argument
-// non-positive).  The device expf may differ from the host's libm in the
-// last bit.
-__device__ __forceinline__ float silu(float x) {
-    if (x >= 0.0f) {
-        const float e = expf(-x);
-        return x / (1.0f + e);
-    }
-    const float e = expf(x);
-    return (x * e) / (1.0f + e);
-}
-
 __global__ void k_silu_inplace(float *__restrict__ h, const int *__restrict__ n_slots, size_t d) {
     const size_t n = (size_t)n_slots[0] * d;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        h[i] = silu(h[i]);
+        h[i] = silu_ref(h[i]);
 }
 
 __global__ void k_silu_f16(const float *__restrict__ h, _Float16 *__restrict__ o, const int *__restrict__ n_slots,
                            size_t d) {
     const size_t n = (size_t)n_slots[0] * d;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        o[i] = (_Float16)silu(h[i]);
+        o[i] = (_Float16)silu_ref(h[i]);
 }
 
 // moe_combine (rce-op-moe/src/lib.rs L98-110): out[t, :] = sum_j w[t, j] * y[slot(t, j), :],

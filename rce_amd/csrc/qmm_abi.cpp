@@ -5,8 +5,7 @@
 // its kernels read (same byte count), shared by its sub-views.  No C++
 // exception crosses the ABI; failures set a thread-local message
 // (rce_qmm_last_error), the convention of compute/crates/rce-c/include/rce.h.
-#include "../../include/rce_qmm.h"
-#include "qmm_internal.h"
+#include "abi_internal.h"
 
 #include <algorithm>
 #include <cmath>
@@ -19,7 +18,7 @@
 
 using namespace rce_qmm;
 
-namespace {
+namespace rce_qmm_abi {
 
 thread_local std::string g_last_error;
 
@@ -28,15 +27,11 @@ rce_qmm_status fail(rce_qmm_status s, const std::string &msg) {
     return s;
 }
 
-rce_qmm_status hip_fail(hipError_t e, const char *what) {
-    return fail(RCE_QMM_HIP_ERROR, std::string(what) + ": " + hipGetErrorString(e));
-}
+}  // namespace rce_qmm_abi
 
-#define HIP_TRY(expr)                                       \
-    do {                                                    \
-        hipError_t e_ = (expr);                             \
-        if (e_ != hipSuccess) return hip_fail(e_, #expr);   \
-    } while (0)
+using namespace rce_qmm_abi;
+
+namespace {
 
 bool block_geometry(uint32_t t, size_t &qk, size_t &bb) {
     switch (t) {
@@ -52,78 +47,6 @@ bool block_geometry(uint32_t t, size_t &qk, size_t &bb) {
     case T_Q6_K: qk = 256; bb = 210; return true;
     default: return false;
     }
-}
-
-size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-// A device allocation shared by a weight and its views.
-struct DevAlloc {
-    void *p = nullptr;
-    int device = 0;
-    ~DevAlloc() {
-        if (p) {
-            int cur = 0;
-            (void)hipGetDevice(&cur);
-            (void)hipSetDevice(device);
-            (void)hipFree(p);
-            (void)hipSetDevice(cur);
-        }
-    }
-};
-
-// Grow-only device buffer owned by a context.
-struct Scratch {
-    void *p = nullptr;
-    size_t cap = 0;
-};
-
-}  // namespace
-
-struct rce_qmm_context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    Scratch a_in, a_f32, out;
-    Scratch a_f16;  // f32 activations rounded to f16 for the MFMA GEMM
-    // grouped experts: grouping metadata, expert tables, stage buffers
-    Scratch moe_meta, moe_wtab, moe_x, moe_h, moe_h16, moe_y;
-    std::vector<DevWeight> moe_wtab_host;  // what moe_wtab holds
-};
-
-struct rce_qmm_weight {
-    std::shared_ptr<DevAlloc> alloc;
-    DevWeight dw{};
-    size_t host_row_bytes = 0;  // GGUF bytes per row
-    size_t len = 0;             // GGUF byte length of this view
-    int device = 0;
-};
-
-namespace {
-
-rce_qmm_status set_device(int dev) {
-    HIP_TRY(hipSetDevice(dev));
-    return RCE_QMM_OK;
-}
-
-// Make `s` hold at least `bytes`; waits for the context's stream before a
-// reallocation so in-flight kernels never see a freed buffer.
-rce_qmm_status ensure(rce_qmm_context *ctx, Scratch &s, size_t bytes, hipStream_t other) {
-    if (s.cap >= bytes) return RCE_QMM_OK;
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
-    if (other && other != ctx->stream) HIP_TRY(hipStreamSynchronize(other));
-    if (s.p) HIP_TRY(hipFree(s.p));
-    s.p = nullptr;
-    s.cap = 0;
-    size_t cap = align_up(std::max<size_t>(bytes, 4096), 4096);
-    hipError_t e = hipMalloc(&s.p, cap);
-    if (e != hipSuccess) return fail(RCE_QMM_OUT_OF_MEMORY, std::string("scratch hipMalloc: ") + hipGetErrorString(e));
-    s.cap = cap;
-    return RCE_QMM_OK;
-}
-
-rce_qmm_status check_weight_ctx(rce_qmm_context *ctx, const rce_qmm_weight *w) {
-    if (!ctx || !w) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight");
-    if (ctx->device != w->device) return fail(RCE_QMM_BAD_SHAPE, "weight lives on another device than the context");
-    return RCE_QMM_OK;
 }
 
 // Every kernel family: decode kernels (EXACT, Q8) and the MFMA GEMM.

@@ -17,10 +17,8 @@ __global__ void k_f16_to_f32(const uint16_t *__restrict__ s, float *__restrict__
 }
 
 // dequant.rs L360-382 (Q4_0), L438-454 (Q8_0), L546-589 (Q4_K), L658-701
-// (Q6_K): one output value per thread.
-__global__ void k_dequant_row(DevWeight w, size_t row, float *__restrict__ out) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= w.n_cols) return;
+// (Q6_K): value i of row `row`.
+__device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
     float v = 0.0f;
     if (w.dtype == T_Q4_0 || w.dtype == T_Q8_0) {
         const uint8_t *rp = w.base + row * w.row_stride;
@@ -65,7 +63,25 @@ __global__ void k_dequant_row(DevWeight w, size_t row, float *__restrict__ out) 
         const float t = d * (float)sc;
         v = t * (float)q;
     }
-    out[i] = v;
+    return v;
+}
+
+__global__ void k_dequant_row(DevWeight w, size_t row, float *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < w.n_cols) out[i] = dequant_value(w, row, i);
+}
+
+// The row index comes from device memory (a token id of the decode step);
+// an id outside [0, n_rows) sets status[0] = 1 and leaves x unchanged.
+__global__ void k_embed_row(DevWeight w, const int32_t *__restrict__ row_dev, float *__restrict__ x,
+                            int *__restrict__ status) {
+    const int32_t id = row_dev[0];
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id < 0 || (size_t)id >= w.n_rows) {
+        if (i == 0) status[0] = 1;
+        return;
+    }
+    if (i < w.n_cols) x[i] = dequant_value(w, (size_t)id, i);
 }
 
 }  // namespace
@@ -248,6 +264,34 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
     case T_Q6_K: return launch_gemv_q6_k(w, g, a, t_rows, out, mode, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode) {
+    if (!gpu_supports(dtype, n_cols, mode)) return false;
+    if (dtype == T_Q6_K && mode == 0) return false;  // EXACT Q6_K is not the activation-stationary kernel
+    return dtype == T_Q4_0 || dtype == T_Q8_0 || dtype == T_Q4_K || dtype == T_Q6_K;
+}
+
+hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s) {
+    const DevWeight &w = f.w[0];
+    if (mode != 0 && mode != 1) return hipErrorInvalidValue;
+    if (!gemv_fx_supports(w.dtype, w.n_cols, mode)) return hipErrorInvalidValue;
+    for (int i = 1; i < f.nw; i++)
+        if (f.w[i].dtype != w.dtype || f.w[i].n_cols != w.n_cols) return hipErrorInvalidValue;
+    GemvGeom g = pick_gemv_geom(w, 1, mode);
+    if (g.rpl > 8) g.rpl = 8;  // the fused forms exist for 2, 4 and 8 rows per lane
+    switch (w.dtype) {
+    case T_Q4_0: return launch_gemv_fx_q4_0(f, g, a, mode, s);
+    case T_Q8_0: return launch_gemv_fx_q8_0(f, g, a, mode, s);
+    case T_Q4_K: return launch_gemv_fx_q4_k(f, g, a, mode, s);
+    case T_Q6_K: return launch_gemv_fx_q6_k(f, g, a, mode, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_embed_row(const DevWeight &w, const int32_t *row_dev, float *x, int *status, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_row, dim3((unsigned)((w.n_cols + 255) / 256)), dim3(256), 0, s, w, row_dev, x, status);
+    return hipGetLastError();
 }
 
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s) {

@@ -621,9 +621,11 @@ inline size_t gemv_lds_bytes(int U, int nt, int rpl, int tb, bool q8, size_t k) 
     return fold > act ? fold : act;
 }
 
-template <class Unit, int NT, int RPL, bool Q8>
+// FX (qmm_internal.h): 0 = the plain GEMV; FX_SEG, FX_RESIDUAL, FX_SWIGLU =
+// the decode step's fused forms (`fx` is read only by them).
+template <class Unit, int NT, int RPL, bool Q8, int FX>
 __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__restrict__ A, float *__restrict__ out,
-                                                int t_rows, int U) {
+                                                int t_rows, int U, GemvFx fx) {
     constexpr int TB = Unit::NTOK;
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
@@ -631,7 +633,17 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     const int col = tid % U, rsub = tid / U;
     const bool active = rsub < P;
     const int RT = P * RPL;
-    const size_t row0 = (size_t)blockIdx.x * RT;
+    unsigned bx = blockIdx.x;
+    if constexpr (FX == FX_SEG) {  // block-uniform choice of the segment
+        if (bx >= fx.blk3) { w = fx.w3; out = fx.out3; bx -= fx.blk3; }
+        else if (bx >= fx.blk2) { w = fx.w2; out = fx.out2; bx -= fx.blk2; }
+    }
+    // FX_SWIGLU: loads u < RPL / 2 read gate rows, the others the same up
+    // rows; tile rows [0, RTO) are gate rows, [RTO, RT) the matching up rows.
+    constexpr int HALF = RPL / 2;
+    static_assert(FX != FX_SWIGLU || RPL % 2 == 0, "swiglu pairs need an even row count per lane");
+    const int RTO = FX == FX_SWIGLU ? RT / 2 : RT;  // output rows of the block
+    const size_t row0 = (size_t)bx * RTO;
     const int t0 = blockIdx.y * TB;
     const int tv = min(TB, t_rows - t0);
     const size_t k = w.n_cols;
@@ -656,8 +668,9 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     const int rs = active ? rsub : P - 1;
 #pragma unroll
     for (int u = 0; u < RPL; u++) {
-        const size_t r = row0 + (size_t)(u * P + rs);
-        raw[u] = Unit::load(w, r < w.n_rows ? r : w.n_rows - 1, col);
+        const bool up = FX == FX_SWIGLU && u >= HALF;
+        const size_t r = row0 + (size_t)((up ? u - HALF : u) * P + rs);
+        raw[u] = Unit::load(up ? fx.w2 : w, r < w.n_rows ? r : w.n_rows - 1, col);
     }
     // Keep every load above ahead of any arithmetic on loaded data.
     __builtin_amdgcn_sched_barrier(0);
@@ -685,29 +698,41 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
         float ad[TB];
         unit.addends(raw[u], ad);
         const int r = u * P + rsub;
-        const bool in = row0 + r < w.n_rows;
+        const bool up = FX == FX_SWIGLU && u >= HALF;
+        const bool in = row0 + (up ? r - RTO : r) < w.n_rows;
 #pragma unroll
         for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = in ? ad[t] : 0.0f;
     }
     __syncthreads();
-    // Phase 4: the reference's fold, one thread per (token, row).
-    for (int j = tid; j < tv * RT; j += NT) {
-        const int t = j / RT, r = j % RT;
-        if (row0 + r < w.n_rows) {
-            const float *pp = part + (t * RT + r) * ld;
-            const float4 *p4 = reinterpret_cast<const float4 *>(pp);
-            float s = 0.0f;
-            const int U4 = U >> 2;
+    // Phase 4: the reference's fold, one thread per (token, output row).
+    auto fold = [&](int t, int r) {
+        const float *pp = part + (t * RT + r) * ld;
+        const float4 *p4 = reinterpret_cast<const float4 *>(pp);
+        float s = 0.0f;
+        const int U4 = U >> 2;
 #pragma unroll 8
-            for (int c = 0; c < U4; c++) {
-                const float4 v = p4[c];
-                s = s + v.x;
-                s = s + v.y;
-                s = s + v.z;
-                s = s + v.w;
+        for (int c = 0; c < U4; c++) {
+            const float4 v = p4[c];
+            s = s + v.x;
+            s = s + v.y;
+            s = s + v.z;
+            s = s + v.w;
+        }
+        for (int c = U4 * 4; c < U; c++) s = s + pp[c];
+        return s;
+    };
+    for (int j = tid; j < tv * RTO; j += NT) {
+        const int t = j / RTO, r = j % RTO;
+        if (row0 + r < w.n_rows) {
+            const size_t o = ((size_t)t0 + t) * w.n_rows + row0 + r;
+            if constexpr (FX == FX_SWIGLU) {
+                const float g = fold(t, r), u = fold(t, RTO + r);
+                out[o] = silu_ref(g) * u;  // rce-tinyllama L320: h = silu(g) * u
+            } else if constexpr (FX == FX_RESIDUAL) {
+                out[o] = fx.res[o] + fold(t, r);  // rce-tinyllama L318, L323: x += ...
+            } else {
+                out[o] = fold(t, r);
             }
-            for (int c = U4 * 4; c < U; c++) s = s + pp[c];
-            out[((size_t)t0 + t) * w.n_rows + row0 + r] = s;
         }
     }
 }
@@ -735,8 +760,71 @@ hipError_t launch_as(const DevWeight &w, int U, const float *a, size_t t_rows, f
     const size_t lds = gemv_lds_bytes(U, NT, RPL, TB, Q8, w.n_cols);
     if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)((w.n_rows + RT - 1) / RT), (unsigned)((t_rows + TB - 1) / TB)), block(NT);
-    hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8>), grid, block, lds, s, w, a, out, (int)t_rows, U);
+    hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, 0>), grid, block, lds, s, w, a, out, (int)t_rows, U, GemvFx{});
     return hipGetLastError();
+}
+
+// The fused forms (one token).  The caller has checked that the weights
+// share dtype and n_cols (FX_SWIGLU: and n_rows).
+template <class Unit, int NT, int RPL, bool Q8>
+hipError_t launch_as_fx(const FxLaunch &f, int U, const float *a, hipStream_t s) {
+    static_assert(Unit::NTOK == 1, "the fused forms are single-token");
+    const int P = NT / U, RT = P * RPL;
+    if (P < 1) return hipErrorInvalidConfiguration;
+    const size_t lds = gemv_lds_bytes(U, NT, RPL, 1, Q8, f.w[0].n_cols);
+    if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
+    auto nblk = [&](const DevWeight &w, int rows_per_block) {
+        return (unsigned)((w.n_rows + rows_per_block - 1) / rows_per_block);
+    };
+    GemvFx fx{};
+    unsigned blocks = 0;
+    switch (f.kind) {
+    case FX_SEG: {
+        if (f.nw < 1 || f.nw > 3) return hipErrorInvalidValue;
+        blocks = nblk(f.w[0], RT);
+        fx.blk2 = fx.blk3 = ~0u;
+        if (f.nw >= 2) { fx.w2 = f.w[1]; fx.out2 = f.out[1]; fx.blk2 = blocks; blocks += nblk(f.w[1], RT); }
+        if (f.nw >= 3) { fx.w3 = f.w[2]; fx.out3 = f.out[2]; fx.blk3 = blocks; blocks += nblk(f.w[2], RT); }
+        hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SEG>), dim3(blocks), dim3(NT), lds, s, f.w[0], a, f.out[0], 1,
+                           U, fx);
+        break;
+    }
+    case FX_RESIDUAL:
+        fx.res = f.res;
+        hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_RESIDUAL>), dim3(nblk(f.w[0], RT)), dim3(NT), lds, s, f.w[0],
+                           a, f.out[0], 1, U, fx);
+        break;
+    case FX_SWIGLU:
+        if (f.nw != 2 || f.w[1].n_rows != f.w[0].n_rows) return hipErrorInvalidValue;
+        fx.w2 = f.w[1];
+        hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SWIGLU>), dim3(nblk(f.w[0], RT / 2)), dim3(NT), lds, s,
+                           f.w[0], a, f.out[0], 1, U, fx);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Shapes of the fused forms: the plain GEMV's threads per block, rows per
+// lane 2, 4 or 8.
+template <class Unit, bool Q8>
+hipError_t launch_as_fx_nt(const FxLaunch &f, const GemvGeom &g, const float *a, hipStream_t s) {
+    const int U = units_per_row(f.w[0].dtype, f.w[0].n_cols);
+#define RCE_RPL_FX(NT)                                                      \
+    switch (g.rpl) {                                                        \
+    case 2: return launch_as_fx<Unit, NT, 2, Q8>(f, U, a, s);               \
+    case 4: return launch_as_fx<Unit, NT, 4, Q8>(f, U, a, s);               \
+    case 8: return launch_as_fx<Unit, NT, 8, Q8>(f, U, a, s);               \
+    default: return hipErrorInvalidValue;                                   \
+    }
+    switch (g.nt) {
+    case 256: RCE_RPL_FX(256)
+    case 512: RCE_RPL_FX(512)
+    case 1024: RCE_RPL_FX(1024)
+    default: return hipErrorInvalidValue;
+    }
+#undef RCE_RPL_FX
 }
 
 template <class Unit, bool Q8>

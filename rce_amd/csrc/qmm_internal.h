@@ -57,6 +57,78 @@ struct GemvGeom {
     int nt = 0, rpl = 0, tb = 0;
 };
 
+// The reference's silu (rce-tinyllama/src/lib.rs L164-166, rce-qwen36-moe
+// L459-461): x * sigmoid(x) with exp's argument kept non-positive.  The
+// device expf may differ from the host libm's in the last bit.
+__device__ __forceinline__ float silu_ref(float x) {
+    if (x >= 0.0f) {
+        const float e = expf(-x);
+        return x / (1.0f + e);
+    }
+    const float e = expf(x);
+    const float t = x * e;
+    return t / (1.0f + e);
+}
+
+// Fused forms of the single-token decode GEMV, used by the decode step
+// (llama.cpp).  FX_SEG: the grid is split into up to three segments, each a
+// weight of the same format and width with its own output (the q, k and v
+// projections of one input in one launch; one segment = the plain GEMV).
+// FX_RESIDUAL: out[j] = res[j] + row_sum_j, the residual add that follows
+// the attention-output and down projections (res may alias out).
+// FX_SWIGLU: every block computes the same rows of w[0] (gate) and w[1]
+// (up) and writes silu(gate_j) * up_j.
+enum : int { FX_SEG = 1, FX_RESIDUAL = 2, FX_SWIGLU = 3 };
+
+struct GemvFx {
+    DevWeight w2, w3;      // FX_SEG: segments 1 and 2; FX_SWIGLU: w2 = up
+    float *out2, *out3;    // FX_SEG: their outputs
+    unsigned blk2, blk3;   // FX_SEG: first block of segments 1 and 2
+    const float *res;      // FX_RESIDUAL
+};
+
+struct FxLaunch {
+    int kind = FX_SEG;
+    int nw = 1;            // weights used (FX_SEG 1..3, FX_SWIGLU 2, FX_RESIDUAL 1)
+    DevWeight w[3]{};
+    float *out[3]{};
+    const float *res = nullptr;
+};
+
+// Whether the fused forms exist for (dtype, n_cols, mode).
+bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode);
+// One token; all weights of one launch share dtype and n_cols (and, for
+// FX_SWIGLU, n_rows).
+hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s);
+// Per-format launchers of the fused forms (gemv_<format>.hip).
+hipError_t launch_gemv_fx_q4_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q8_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q4_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q6_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+
+// ---- decode step (decoder.hip) ----
+// x = dequant_row(w, *row_dev) (QuantWeight::dequant_row); an id outside
+// [0, n_rows) sets status[0] = 1 and writes nothing.
+hipError_t launch_embed_row(const DevWeight &w, const int32_t *row_dev, float *x, int *status, hipStream_t s);
+// out = rms_norm(x, w, eps) (rce-tinyllama L158-163) over n values.  When
+// pos_next is given, one thread also starts a decode step: pos_cur[0] =
+// pos_next[0], pos_next[0] += 1, and status[0] = 2 if pos_cur >= ctx_len.
+hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos_next,
+                           int *pos_cur, int ctx_len, int *status, hipStream_t s);
+// RoPE of q (n_q heads) and k (n_kv heads) at pos_cur[0], append of k, v to
+// the layer's caches, and per query head the reference's online-softmax
+// attention over positions 0..pos (rce-op-attn L107-151, L185-251).
+// qkv: [q (n_q * d_head) | k (n_kv * d_head) | v (n_kv * d_head)];
+// rope_cs: [ctx_len][rope_dim / 2] (cos, sin) pairs; caches
+// [ctx_len][n_kv * d_head]; att: [n_q * d_head].
+hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache,
+                            const int *pos_cur, int ctx_len, int n_q, int n_kv, int d_head, int rope_dim,
+                            float scale, float *att, hipStream_t s);
+bool attention_supports(int d_head, int rope_dim);
+// h = silu(g) * u, x = x + o: the unfused forms.
+hipError_t launch_swiglu(const float *g, const float *u, float *h, size_t n, hipStream_t s);
+hipError_t launch_add_inplace(float *x, const float *o, size_t n, hipStream_t s);
+
 // Decode kernels available for (dtype, n_cols, mode 0 EXACT / 1 Q8).
 bool gpu_supports(uint32_t dtype, size_t n_cols, int mode);
 

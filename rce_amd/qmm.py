@@ -22,7 +22,7 @@ from ._lib import QmmError, check, lib
 __all__ = [
     "GgufDtype", "Mode", "Context", "QuantWeight", "DeviceBuffer", "QmmError",
     "block_geometry", "row_bytes", "supports", "mm_1d", "mm_1d_serial", "mm_batched",
-    "mm_batched_dev", "moe_router", "moe_ffn_dev",
+    "mm_batched_dev", "moe_router", "moe_ffn_dev", "quantize",
 ]
 
 
@@ -209,6 +209,18 @@ def mm_batched(a, t_rows: int, w: QuantWeight, out: np.ndarray | None = None) ->
     """rce_op_qmm::mm_batched: a [t_rows, n_cols] -> [t_rows, n_rows]."""
     r = _host_call(lib().rce_qmm_mm_batched, w.ctx, a, t_rows, w, out)
     return r.reshape(t_rows, w.n_rows) if out is None else r
+
+
+def quantize(w, dtype) -> np.ndarray:
+    """GGUF bytes of f32 weights [n_rows, n_cols] (rce_qmm_quantize: the
+    reference's quantize_block / quantize_k encoders; host only)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    if w.ndim == 1:
+        w = w.reshape(1, -1)
+    n_rows, n_cols = w.shape
+    out = np.empty(n_rows * row_bytes(dtype, n_cols), np.uint8)
+    check(lib().rce_qmm_quantize(int(dtype), _ptr(w), n_rows, n_cols, _ptr(out), out.size))
+    return out
 
 
 class DeviceBuffer:

@@ -1,0 +1,77 @@
+"""Synthetic Llama-2 decoders for the decode-step tests: random N(0, sigma)
+weights quantized to GGUF bytes by the library's quantizer (checked against
+the oracle's in test_quantize.py), norm weights near 1, and the matching
+oracle model (oracle.Llama) and device runtime (rce_amd.TinyLlamaRuntime)."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+LIN = ("wq", "wk", "wv", "wo", "ffn_gate", "ffn_up", "ffn_down")
+
+
+def tiny_cfg(**kw) -> dict:
+    c = dict(d_model=256, vocab=320, n_layers=2, n_q_heads=4, n_kv_heads=2, d_head=64, rope_dim=64,
+             rope_freq_base=10000.0, d_ff=512, context_length=32, eps=1e-5)
+    c.update(kw)
+    return c
+
+
+def shapes(c: dict) -> dict:
+    qd, kvd = c["n_q_heads"] * c["d_head"], c["n_kv_heads"] * c["d_head"]
+    dm, ff = c["d_model"], c["d_ff"]
+    return {"wq": (qd, dm), "wk": (kvd, dm), "wv": (kvd, dm), "wo": (dm, qd),
+            "ffn_gate": (ff, dm), "ffn_up": (ff, dm), "ffn_down": (dm, ff)}
+
+
+def make_weights(c: dict, seed: int, lin_dtype=O.Q4_K, head_dtype=O.Q6_K, embd_dtype=O.Q4_K,
+                 dtype_of=None, sigma: float = 0.05, unit_norms: bool = False) -> dict:
+    """Host weights: GGUF bytes + dtypes and f32 norms.  dtype_of(layer,
+    name) overrides the linear format per weight."""
+    import rce_amd
+    rng = np.random.default_rng(seed)
+
+    def q(n, k, dt):
+        w = (rng.standard_normal((n, k)) * sigma).astype(np.float32)
+        return rce_amd.quantize(w, dt), dt
+
+    def norm():
+        if unit_norms:
+            return np.ones(c["d_model"], np.float32)
+        return (1.0 + 0.1 * rng.standard_normal(c["d_model"])).astype(np.float32)
+
+    sh = shapes(c)
+    blocks = []
+    for il in range(c["n_layers"]):
+        b = {"attn_norm": norm(), "ffn_norm": norm()}
+        for n in LIN:
+            dt = dtype_of(il, n) if dtype_of else lin_dtype
+            b[n] = q(*sh[n], dt)
+        blocks.append(b)
+    return {"cfg": dict(c), "token_embd": q(c["vocab"], c["d_model"], embd_dtype), "output_norm": norm(),
+            "lm_head": q(c["vocab"], c["d_model"], head_dtype), "blocks": blocks}
+
+
+def oracle_model(W: dict, q8: bool = False) -> O.Llama:
+    return O.Llama(W["cfg"], W["token_embd"], W["output_norm"], W["lm_head"], W["blocks"], q8=q8)
+
+
+def device_model(ctx, W: dict, mode):
+    import rce_amd
+    c = W["cfg"]
+    qw = lambda bd, n, k: rce_amd.QuantWeight.from_owned_bytes(ctx, bd[0], bd[1], n, k)  # noqa: E731
+    sh = shapes(c)
+    blocks = []
+    for b in W["blocks"]:
+        ws = {n: qw(b[n], *sh[n]) for n in LIN}
+        blocks.append(rce_amd.TinyLlamaBlock(b["attn_norm"], b["ffn_norm"], **ws))
+    weights = rce_amd.TinyLlamaWeights(qw(W["token_embd"], c["vocab"], c["d_model"]), W["output_norm"],
+                                       qw(W["lm_head"], c["vocab"], c["d_model"]), blocks)
+    cfg = rce_amd.TinyLlamaConfig(**c)
+    return rce_amd.TinyLlamaRuntime(ctx, cfg, weights, mode)
+
+
+def normwise(got, want) -> float:
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / np.max(np.abs(want)))

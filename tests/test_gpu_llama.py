@@ -1,0 +1,165 @@
+"""GPU parity of the device-resident Llama-2 decode step (rce_qmm_llama_*,
+the TinyLlama caller of the quantized matmuls: rce-tinyllama/src/lib.rs
+L252-330 with rce-op-attn L107-251) against the oracle's restatement
+(oracle.Llama), several positions per case.
+
+Tolerances (normwise max|gpu - ref| / max|ref| over the logits):
+  * EXACT linears: every qmm is the reference's order bit for bit given its
+    input, RoPE is bit-exact (host-built table), but rms_norm's sum of
+    squares is a fixed tree and exp (softmax, silu) is the device expf, so
+    the logits differ by rounding only: 1e-5.
+  * Q8 linears against the oracle's Q8 decoder: the same rounding
+    differences can move an activation across a Q8 rounding boundary, which
+    changes that block's integer by one: 1e-3.
+Also: run-to-run bit identity, the embedding entry point equal to the token
+entry point, reset, the fused and unfused forms (mixed formats), d_head 128,
+errors (token id, full cache), and the TinyLlama shape (2 of its 22 layers,
+full width, 32000-row Q6_K head).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rce_amd
+from rce_amd import Mode
+from llama_case import device_model, make_weights, normwise, oracle_model, tiny_cfg
+
+pytestmark = pytest.mark.gpu
+
+TOKENS = [3, 100, 7, 319, 3, 42, 250, 1]
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def run_pair(ctx, W, mode, tokens, tol):
+    dev = device_model(ctx, W, mode)
+    ref = oracle_model(W, q8=(mode == Mode.Q8))
+    worst = 0.0
+    for pos, t in enumerate(tokens):
+        got = dev.forward_logits(t)
+        want = ref.forward_token(t)
+        err = normwise(got, want)
+        worst = max(worst, err)
+        assert err < tol, f"position {pos}: normwise {err:.3e}"
+    assert dev.pos == len(tokens)
+    note(f"  worst normwise {worst:.3e}")
+    return dev
+
+
+@pytest.mark.parametrize("mode,tol", [(Mode.EXACT, 1e-5), (Mode.Q8, 1e-3)])
+def test_llama_tiny(ctx, mode, tol):
+    note(f"llama tiny mode={mode.name}")
+    W = make_weights(tiny_cfg(), seed=21)
+    dev = run_pair(ctx, W, mode, TOKENS, tol)
+    dev.close()
+
+
+def test_llama_deterministic_and_reset(ctx):
+    note("llama determinism + reset")
+    W = make_weights(tiny_cfg(), seed=22)
+    dev = device_model(ctx, W, Mode.Q8)
+    a = [dev.forward_logits(t) for t in TOKENS[:4]]
+    dev.new_state()
+    assert dev.pos == 0
+    b = [dev.forward_logits(t) for t in TOKENS[:4]]
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    dev.close()
+
+
+def test_llama_embedding_entry(ctx):
+    note("llama forward_embedding == forward_token")
+    W = make_weights(tiny_cfg(), seed=23)
+    d1 = device_model(ctx, W, Mode.EXACT)
+    d2 = device_model(ctx, W, Mode.EXACT)
+    ref = oracle_model(W)
+    for t in TOKENS[:3]:
+        l1 = d1.forward_logits(t)
+        l2 = d2.forward_logits_embed(ref.embed(t))  # dequant_row on the host oracle
+        assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    d1.close(); d2.close()
+
+
+def test_llama_unfused_forms(ctx):
+    """wv in Q8_0 (q|k|v not one launch), ffn_up in Q4_0 (no fused swiglu),
+    ffn_down in Q6_K under EXACT (no fused residual)."""
+    note("llama mixed formats (unfused kernels)")
+    mix = {"wv": O.Q8_0, "ffn_up": O.Q4_0, "ffn_down": O.Q6_K}
+    W = make_weights(tiny_cfg(), seed=24, dtype_of=lambda il, n: mix.get(n, O.Q4_K))
+    run_pair(ctx, W, Mode.EXACT, TOKENS[:5], 1e-5).close()
+    run_pair(ctx, W, Mode.Q8, TOKENS[:5], 1e-3).close()
+
+
+def test_llama_head_dim_128(ctx):
+    note("llama d_head 128, rope_dim 64, GQA 4:1")
+    c = tiny_cfg(d_model=512, n_q_heads=4, n_kv_heads=1, d_head=128, rope_dim=64, d_ff=768,
+                 rope_freq_base=500000.0)
+    W = make_weights(c, seed=25)
+    run_pair(ctx, W, Mode.EXACT, TOKENS[:6], 1e-5).close()
+
+
+def test_llama_long_context(ctx):
+    """More than one key chunk (64 keys) in the attention kernel."""
+    note("llama 70 positions")
+    c = tiny_cfg(n_layers=1, context_length=80)
+    W = make_weights(c, seed=26)
+    toks = [int(t) for t in np.random.default_rng(0).integers(0, c["vocab"], 70)]
+    run_pair(ctx, W, Mode.EXACT, toks, 1e-5).close()
+
+
+def test_llama_errors(ctx):
+    note("llama errors")
+    c = tiny_cfg(n_layers=1, context_length=3)
+    W = make_weights(c, seed=27)
+    dev = device_model(ctx, W, Mode.EXACT)
+    with pytest.raises(rce_amd.QmmError):
+        dev.forward_logits(c["vocab"])  # token id out of range: rejected on the host
+    assert dev.pos == 0
+    for t in (1, 2, 3):
+        dev.forward_logits(t)
+    with pytest.raises(rce_amd.QmmError):
+        dev.forward_logits(4)  # cache full
+    assert dev.pos == 3
+    dev.new_state()
+    # device-side id check of the asynchronous entry point
+    tok = rce_amd.DeviceBuffer.from_numpy(ctx, np.array([c["vocab"] + 5], np.int32))
+    out = rce_amd.DeviceBuffer(ctx, 4 * c["vocab"])
+    dev.forward_token_dev(tok.ptr, out.ptr)
+    with pytest.raises(rce_amd.QmmError):
+        dev.check()
+    dev.check()  # cleared
+    tok.free(); out.free(); dev.close()
+    with pytest.raises(rce_amd.QmmError):
+        device_model(ctx, W, Mode.F16_MFMA)
+
+
+def test_llama_dev_entry_matches_host_entry(ctx):
+    note("llama forward_token_dev == forward_logits")
+    W = make_weights(tiny_cfg(), seed=28)
+    d1 = device_model(ctx, W, Mode.Q8)
+    d2 = device_model(ctx, W, Mode.Q8)
+    tok = rce_amd.DeviceBuffer(ctx, 4)
+    out = rce_amd.DeviceBuffer(ctx, 4 * W["cfg"]["vocab"])
+    for t in TOKENS[:4]:
+        tok.upload(np.array([t], np.int32))
+        d2.forward_token_dev(tok.ptr, out.ptr)
+        d2.check()
+        got = out.download(np.float32, W["cfg"]["vocab"])
+        assert np.array_equal(got.view(np.uint32), d1.forward_logits(t).view(np.uint32))
+    tok.free(); out.free(); d1.close(); d2.close()
+
+
+def test_llama_tinyllama_shape(ctx):
+    """configs[4] widths: d 2048, ffn 5632, 32 q / 4 kv heads, d_head 64,
+    Q4_K linears, Q6_K 32000 x 2048 head (2 of the 22 layers)."""
+    note("llama TinyLlama shape, 2 layers")
+    c = dict(d_model=2048, vocab=32000, n_layers=2, n_q_heads=32, n_kv_heads=4, d_head=64, rope_dim=64,
+             rope_freq_base=10000.0, d_ff=5632, context_length=64, eps=1e-5)
+    W = make_weights(c, seed=29, sigma=0.02)
+    for mode, tol in ((Mode.EXACT, 1e-5), (Mode.Q8, 1e-3)):
+        note(f"  mode={mode.name}")
+        run_pair(ctx, W, mode, [1, 2, 31999, 4], tol).close()
