@@ -117,15 +117,17 @@ class Hip:
 
 
 def make_weight(seed, dt, n, k):
-    import oracle as O
+    """N(0, 0.02) f32 weights (seeded) as GGUF bytes, by the library's
+    quantizer (the reference's encoders)."""
+    import rce_amd
     rng = np.random.default_rng(seed)
-    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-    return O.quantize(w, dt)
+    w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+    return rce_amd.quantize(w, dt)
 
 
 def gemv_bytes(dt, n, k, t=1):
-    import oracle as O
-    return O.tensor_byte_size(dt, n * k) + 4 * k * t + 4 * n * t
+    import rce_amd
+    return n * rce_amd.row_bytes(dt, k) + 4 * k * t + 4 * n * t
 
 
 def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
@@ -158,9 +160,8 @@ def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
 
 def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed):
     """configs[2]-style prefill GEMM in F16_MFMA mode: A [m, k] f16 resident,
-    weights rotated over HBM copies; returns ms per launch and a normwise
-    check of the first 16 output rows against the oracle's exact order."""
-    import oracle as O
+    weights rotated over HBM copies; returns ms per launch and the first 16
+    output rows (checked in the CPU leg)."""
     import rce_amd
     b = make_weight(seed, dt, n, k)
     copies = max(2, min(64, (2 * INFINITY_CACHE) // b.size + 1))
@@ -180,33 +181,32 @@ def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed):
     ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
     ctx.synchronize()
     res = out.download(np.float32, 16 * n).reshape(16, n)
-    ref = O.mm_batched(x[:16].astype(np.float32), b, dt, n, k)
-    err = float(np.max(np.abs(res.astype(np.float64) - ref)) / np.max(np.abs(ref)))
     for w in ws:
         w.close()
     xa.free()
     out.free()
-    return ms, err
+    # the first 16 rows, for the parity check of the CPU leg
+    return ms, {"b": b, "x": x[:16].astype(np.float32), "got": res, "dt": dt, "n": n, "k": k}
 
 
 def time_moe(hip, ctx, steps, warmup, seed, mode):
     """8 Q4_0 experts (w1 14336x4096, w2 4096x14336), 256 tokens,
     top-2 of N(0,1) router logits; ms per grouped-FFN call (all 8 experts'
     528 MB stream from HBM each call), the touched weight bytes, and a
-    normwise check of the first 8 tokens against the oracle's moe_ffn."""
-    import oracle as O
+    sample of the first 8 tokens (checked in the CPU leg)."""
     import rce_amd
+    Q4_0 = rce_amd.GgufDtype.Q4_0
     E, dm, dff, T, K = 8, 4096, 14336, 256, 2
     rng = np.random.default_rng(seed)
     w1b, w2b = [], []
     for _ in range(E):
-        w1b.append(O.quantize(rng.standard_normal((dff, dm), dtype=np.float32) * np.float32(0.02), O.Q4_0))
-        w2b.append(O.quantize(rng.standard_normal((dm, dff), dtype=np.float32) * np.float32(0.02), O.Q4_0))
+        w1b.append(rce_amd.quantize(rng.standard_normal((dff, dm), dtype=np.float32) * np.float32(0.02), Q4_0))
+        w2b.append(rce_amd.quantize(rng.standard_normal((dm, dff), dtype=np.float32) * np.float32(0.02), Q4_0))
     x = rng.standard_normal((T, dm), dtype=np.float32)
     logits = rng.standard_normal((T, E), dtype=np.float32)
     ids, gw = rce_amd.moe_router(logits, K)
-    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, dff, dm) for b in w1b]
-    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, dm, dff) for b in w2b]
+    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, Q4_0, dff, dm) for b in w1b]
+    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, Q4_0, dm, dff) for b in w2b]
     bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
     bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids)
     bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw)
@@ -221,29 +221,133 @@ def time_moe(hip, ctx, steps, warmup, seed, mode):
     ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
     ctx.synchronize()
     got = bo.download(np.float32, T * dm).reshape(T, dm)[:8]
-    ref = O.moe_ffn(x[:8], w1b, w2b, O.Q4_0, dff, ids[:8], gw[:8])
-    err = float(np.max(np.abs(got.astype(np.float64) - ref)) / np.max(np.abs(ref)))
     touched = sorted(set(int(e) for e in ids.reshape(-1)))
     wbytes = sum(w1b[e].size + w2b[e].size for e in touched)
     for w in W1 + W2:
         w.close()
     for bb in (bx, bi, bw, bo):
         bb.free()
-    return ms, err, wbytes + 2 * T * dm * 4
+    sample = {"x": x[:8], "w1": w1b, "w2": w2b, "dff": dff, "ids": ids[:8], "gw": gw[:8], "got": got}
+    return ms, wbytes + 2 * T * dm * 4, sample
 
 
-def cpu_baseline(b, x, dt, n, k, budget_s=10.0):
-    """Oracle (C restatement of mm_1d, OpenMP over rows) on the same workload."""
+LLAMA_CFG = dict(d_model=2048, vocab=32000, n_layers=22, n_q_heads=32, n_kv_heads=4, d_head=64, rope_dim=64,
+                 rope_freq_base=10000.0, d_ff=5632, context_length=2048, eps=1e-5)
+LLAMA_WEIGHT_BYTES = 598_757_376  # 22 x 24,772,608 B of Q4_K linears + the 53,760,000 B Q6_K head
+
+
+def llama_weights(seed):
+    """TinyLlama-shaped random decoder, every weight N(0, 0.02)
+    quantized (Q4_K linears and token_embd, Q6_K head), norms = 1."""
+    import rce_amd
+    G = rce_amd.GgufDtype
+    c = LLAMA_CFG
+    rng = np.random.default_rng(seed)
+    dm, qd, kvd, ff = c["d_model"], c["n_q_heads"] * c["d_head"], c["n_kv_heads"] * c["d_head"], c["d_ff"]
+    shapes = {"wq": (qd, dm), "wk": (kvd, dm), "wv": (kvd, dm), "wo": (dm, qd),
+              "ffn_gate": (ff, dm), "ffn_up": (ff, dm), "ffn_down": (dm, ff)}
+
+    def q(n, k, dt):
+        return rce_amd.quantize(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02), dt), dt
+
+    ones = np.ones(dm, np.float32)
+    blocks = [dict({"attn_norm": ones, "ffn_norm": ones}, **{nm: q(*sh, G.Q4K) for nm, sh in shapes.items()})
+              for _ in range(c["n_layers"])]
+    return {"cfg": dict(c), "token_embd": q(c["vocab"], dm, G.Q4K), "output_norm": ones,
+            "lm_head": q(c["vocab"], dm, G.Q6K), "blocks": blocks, "shapes": shapes}
+
+
+def time_llama(hip, ctx, W, mode, steps, warmup, seed):
+    """Batch-1 decode of `warmup` then `steps` tokens from position 0 through
+    the device-resident decoder (one embed kernel + one graph replay per
+    token, on the context's stream); ms per token over the timed tokens and
+    the first 4 tokens' logits (checked in the CPU leg)."""
+    import rce_amd
+    c = W["cfg"]
+    qw = lambda bd, n, k: rce_amd.QuantWeight.from_owned_bytes(ctx, bd[0], bd[1], n, k)  # noqa: E731
+    blocks = [rce_amd.TinyLlamaBlock(b["attn_norm"], b["ffn_norm"],
+                                     **{nm: qw(b[nm], *W["shapes"][nm]) for nm in W["shapes"]}) for b in W["blocks"]]
+    weights = rce_amd.TinyLlamaWeights(qw(W["token_embd"], c["vocab"], c["d_model"]), W["output_norm"],
+                                       qw(W["lm_head"], c["vocab"], c["d_model"]), blocks)
+    dec = rce_amd.TinyLlamaRuntime(ctx, rce_amd.TinyLlamaConfig(**c), weights, mode)
+    del blocks, weights  # the decoder holds the device weights
+    toks = np.random.default_rng(seed).integers(0, c["vocab"], warmup + steps).astype(np.int32)
+    first = [dec.forward_logits(int(t)) for t in toks[:4]]  # host entry point, also records the graph
+    dec.new_state()
+    tb = rce_amd.DeviceBuffer.from_numpy(ctx, toks)
+    lo = rce_amd.DeviceBuffer(ctx, 4 * c["vocab"])
+    for i in range(warmup):
+        dec.forward_token_dev(tb.ptr + 4 * i, lo.ptr)
+    ctx.synchronize()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, ctx.stream)
+    h0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        dec.forward_token_dev(tb.ptr + 4 * i, lo.ptr)
+    host_ms = (time.perf_counter() - h0) * 1e3 / steps  # submission only
+    hip.record(e1, ctx.stream)
+    ms = hip.elapsed_ms(e0, e1) / steps
+    log(f"  decode: {ms * 1e3:.1f} us/token on the stream, host submission {host_ms * 1e3:.1f} us/token")
+    dec.check()
+    dec.close()
+    tb.free()
+    lo.free()
+    return ms, {"tokens": [int(t) for t in toks[:4]], "got": first}
+
+
+def cpu_leg(line, head, rows, budget_s=10.0):
+    """The CPU baseline and the parity checks (the only part of the bench
+    that uses the oracle, the C restatement of the reference path).
+
+    Baseline: the oracle's mm_1d (OpenMP over rows, the reference's rayon
+    decomposition) timed on the headline workload for about budget_s
+    seconds.  Checks: the headline GEMV result against the oracle's (bit
+    identity), and each per-format row's kept sample against the oracle's
+    reference order (normwise error)."""
     import oracle as O
     threads = O.max_threads()
-    O.mm_batched(x, b, dt, n, k, threads)  # warm
+    b, x, dt, n, k, res, mode = (head[key] for key in ("b", "x", "dt", "n", "k", "res", "mode"))
+    want = O.mm_batched(x, b, dt, n, k, threads)  # also the warm-up
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or len(times) < 3:
         t0 = time.perf_counter()
         O.mm_batched(x, b, dt, n, k, threads)
         times.append(time.perf_counter() - t0)
-    return float(np.median(times)), threads, len(times)
+    med = float(np.median(times))
+    cpu_gbs = gemv_bytes(dt, n, k, 1) / med / 1e9
+    line["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                            "sample": f"{len(times)} calls of mm_1d (f32 activations, reference order) on the "
+                                      f"headline Q4_0 11008x4096 batch-1 workload, median {med * 1e3:.2f} ms"}
+    log(f"  cpu {cpu_gbs:.2f} GB/s on {threads} threads")
+    ref = want if mode == 0 else O.mm_batched_q8(x, b, dt, n, k, threads)
+    line["config"]["parity_bit_exact"] = bool(np.array_equal(res.view(np.uint32), ref.view(np.uint32)))
+    log(f"  headline bit-identical to the oracle: {line['config']['parity_bit_exact']}")
+
+    def normwise(got, want):
+        return float(f"{np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(want)):.3g}")
+
+    per = line["per_format"]
+    if "gemm" in rows:
+        g = rows["gemm"]
+        per[g["key"]]["normwise_err_vs_oracle"] = normwise(g["got"], O.mm_batched(g["x"], g["b"], g["dt"], g["n"], g["k"]))
+    if "moe" in rows:
+        m = rows["moe"]
+        ref = O.moe_ffn(m["x"], m["w1"], m["w2"], O.Q4_0, m["dff"], m["ids"], m["gw"])
+        per[m["key"]]["normwise_err_vs_oracle"] = normwise(m["got"], ref)
+    if "llama" in rows:
+        L = rows["llama"]
+        W = L["W"]
+        om = O.Llama(W["cfg"], W["token_embd"], W["output_norm"], W["lm_head"], W["blocks"], q8=L["q8"], threads=threads)
+        t0 = time.perf_counter()
+        errs = [normwise(got, om.forward_token(t)) for t, got in zip(L["tokens"], L["got"])]
+        cpu_tok_s = len(errs) / (time.perf_counter() - t0)
+        per[L["key"]]["normwise_err_vs_oracle_max"] = max(errs)
+        per[L["key"]]["cpu_baseline_tok_s"] = round(cpu_tok_s, 2)
+        log(f"  decoder: normwise vs oracle {max(errs):.2e} over {len(errs)} tokens; oracle {cpu_tok_s:.2f} tok/s")
+    for key, row in per.items():
+        if "normwise_err_vs_oracle" in row:
+            log(f"  {key}: normwise vs oracle {row['normwise_err_vs_oracle']:.2e}")
 
 
 def headline_traffic():
@@ -281,7 +385,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--mode", choices=["q8", "exact"], default="q8")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--quick", action="store_true", help="headline only, no per-format sweep")
+    ap.add_argument("--quick", action="store_true", help="headline only, no per-format rows")
+    ap.add_argument("--rows", default="sweep,gemm,moe,llama",
+                    help="per-format rows: comma-separated subset of sweep,gemm,moe,llama")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -294,22 +400,20 @@ def main():
         copy_calibration(hip)
         return
 
-    import oracle as O
     import rce_amd
-    from rce_amd import Mode
+    from rce_amd import GgufDtype as G, Mode
     ctx = rce_amd.Context(0)
     mode = Mode.Q8 if args.mode == "q8" else Mode.EXACT
+    rows = set() if args.quick else set(r for r in args.rows.split(",") if r)
 
     # ---- headline: configs[1], Q4_0 11008x4096, batch 1 -------------------------
-    dt, n, k = O.Q4_0, 11008, 4096
+    dt, n, k = G.Q4_0, 11008, 4096
     log(f"headline Q4_0 GEMV {n}x{k} batch 1 mode={args.mode} steps={args.steps} warmup={args.warmup}")
     ms, b, x, res, copies = time_gemv(hip, ctx, dt, n, k, 1, mode, args.steps, args.warmup, 11)
     nbytes = gemv_bytes(dt, n, k, 1)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    ref = O.mm_batched(x, b, dt, n, k) if mode == Mode.EXACT else O.mm_batched_q8(x, b, dt, n, k)
-    exact_ok = bool(np.array_equal(res.view(np.uint32), ref.view(np.uint32)))
-    log(f"  {ms * 1e3:.2f} us/launch  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)  "
-        f"bit-identical to the oracle: {exact_ok}")
+    log(f"  {ms * 1e3:.2f} us/launch  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+    head = {"b": b, "x": x, "dt": int(dt), "n": n, "k": k, "res": res, "mode": int(mode)}
 
     line = {
         "metric": "GEMV HBM GB/s (Q4_0 decode 11008x4096, batch 1, Q8 activations)",
@@ -326,62 +430,70 @@ def main():
         "data": "synthetic: W~N(0,0.02) seeded then GGUF-quantized, x~N(0,1); weights rotated over "
                 f"{copies} HBM copies",
         "config": {"workload": "configs[1]: Q4_0 GEMV 11008x4096 batch 1", "mode": args.mode,
-                   "bytes_per_launch": nbytes, "parity_bit_exact": exact_ok},
+                   "bytes_per_launch": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": headline_traffic() if mode == Mode.Q8 else None},
     }
 
-    # ---- per-format sweep (the metric is per quant format) -----------------------
+    # ---- per-format rows (the metric is per quant format) ------------------------
     per = {}
-    if not args.quick:
+    kept = {}
+    if "sweep" in rows:
         sweep = [
-            ("Q8_0 4096x4096 b1", O.Q8_0, 4096, 4096, 1),      # configs[0] shape
-            ("Q4_0 11008x4096 b1", O.Q4_0, 11008, 4096, 1),    # configs[1]
-            ("Q4_0 11008x4096 b8", O.Q4_0, 11008, 4096, 8),    # configs[1], batch 8
-            ("Q4_K 4096x4096 b1", O.Q4_K, 4096, 4096, 1),
-            ("Q4_K 5632x2048 b1", O.Q4_K, 5632, 2048, 1),      # configs[4] FFN shapes
-            ("Q4_K 2048x5632 b1", O.Q4_K, 2048, 5632, 1),
-            ("Q6_K 32000x2048 b1", O.Q6_K, 32000, 2048, 1),    # configs[4] head
+            ("Q8_0 4096x4096 b1", G.Q8_0, 4096, 4096, 1),      # configs[0] shape
+            ("Q4_0 11008x4096 b1", G.Q4_0, 11008, 4096, 1),    # configs[1]
+            ("Q4_0 11008x4096 b8", G.Q4_0, 11008, 4096, 8),    # configs[1], batch 8
+            ("Q4_K 4096x4096 b1", G.Q4K, 4096, 4096, 1),
+            ("Q4_K 5632x2048 b1", G.Q4K, 5632, 2048, 1),       # configs[4] FFN shapes
+            ("Q4_K 2048x5632 b1", G.Q4K, 2048, 5632, 1),
+            ("Q6_K 32000x2048 b1", G.Q6K, 32000, 2048, 1),     # configs[4] head
         ]
         for name, sdt, sn, sk, st in sweep:
             for m in (Mode.EXACT, Mode.Q8):
                 steps = max(20, args.steps // 2)
-                sms, sb, sx, sres, _ = time_gemv(hip, ctx, sdt, sn, sk, st, m, steps, 5, 100 + sdt)
+                sms, _, _, _, _ = time_gemv(hip, ctx, sdt, sn, sk, st, m, steps, 5, 100 + int(sdt))
                 sbytes = gemv_bytes(sdt, sn, sk, st)
                 sg = sbytes / (sms * 1e-3) / 1e9
                 key = f"{name} {m.name.lower()}"
                 per[key] = {"us": round(sms * 1e3, 2), "GB/s": round(sg, 1), "hbm_frac": round(sg / HBM_PEAK_GBS, 4)}
                 log(f"  {key}: {sms * 1e3:.2f} us  {sg:.0f} GB/s ({sg / HBM_PEAK_GBS:.1%})")
-        # Q4_K prefill GEMM 512x4096x4096 on f16 MFMA
-        gms, gerr = time_gemm(hip, ctx, O.Q4_K, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
+    if "gemm" in rows:  # configs[2]: Q4_K prefill GEMM 512x4096x4096 on f16 MFMA
+        gms, gs = time_gemm(hip, ctx, G.Q4K, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
         gtf = 2.0 * 512 * 4096 * 4096 / (gms * 1e-3) / 1e12
-        per["Q4_K GEMM 512x4096x4096 f16_mfma"] = {
-            "us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4),
-            "normwise_err_vs_oracle": float(f"{gerr:.3g}")}
-        log(f"  Q4_K GEMM 512x4096x4096: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of "
-            f"f16 MFMA peak), normwise err {gerr:.2e}")
-        # grouped MoE, 8 Q4_0 experts, 256 tokens, top-2
-        mms, merr, mbytes = time_moe(hip, ctx, 5, 2, 400, Mode.F16_MFMA)
+        key = "Q4_K GEMM 512x4096x4096 f16_mfma"
+        per[key] = {"us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4)}
+        kept["gemm"] = dict(gs, key=key)
+        log(f"  {key}: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of f16 MFMA peak)")
+    if "moe" in rows:  # configs[3]: grouped MoE, 8 Q4_0 experts, 256 tokens, top-2
+        mms, mbytes, msample = time_moe(hip, ctx, 5, 2, 400, Mode.F16_MFMA)
         mtf = 120259084288 / (mms * 1e-3) / 1e12
         mgb = mbytes / (mms * 1e-3) / 1e9
-        per["MoE 8x(14336x4096, 4096x14336) Q4_0 T256 top2 f16_mfma"] = {
-            "us": round(mms * 1e3, 2), "TFLOP/s": round(mtf, 1), "mfma_frac": round(mtf / MFMA_F16_PEAK_TFS, 4),
-            "GB/s": round(mgb, 1), "hbm_frac": round(mgb / HBM_PEAK_GBS, 4),
-            "normwise_err_vs_oracle": float(f"{merr:.3g}")}
+        key = "MoE 8x(14336x4096, 4096x14336) Q4_0 T256 top2 f16_mfma"
+        per[key] = {"us": round(mms * 1e3, 2), "TFLOP/s": round(mtf, 1), "mfma_frac": round(mtf / MFMA_F16_PEAK_TFS, 4),
+                    "GB/s": round(mgb, 1), "hbm_frac": round(mgb / HBM_PEAK_GBS, 4)}
+        kept["moe"] = dict(msample, key=key)
         log(f"  MoE configs[3]: {mms * 1e3:.1f} us  {mtf:.0f} TFLOP/s ({mtf / MFMA_F16_PEAK_TFS:.1%}), "
-            f"{mgb:.0f} GB/s ({mgb / HBM_PEAK_GBS:.1%}), normwise err {merr:.2e}")
+            f"{mgb:.0f} GB/s ({mgb / HBM_PEAK_GBS:.1%})")
+    if "llama" in rows:  # configs[4]: TinyLlama-shaped decode, batch 1
+        log("  building the configs[4] decoder (22 layers, Q4_K + Q6_K head)")
+        W = llama_weights(500)
+        lsteps, lwarm = 128, 16
+        lms, lsample = time_llama(hip, ctx, W, mode, lsteps, lwarm, 501)
+        lgb = LLAMA_WEIGHT_BYTES / (lms * 1e-3) / 1e9
+        key = f"TinyLlama-shape decode 22L Q4_K/Q6_K b1 {args.mode}"
+        per[key] = {"us_per_token": round(lms * 1e3, 2), "tok/s": round(1e3 / lms, 1),
+                    "weight_GB/s": round(lgb, 1), "hbm_frac": round(lgb / HBM_PEAK_GBS, 4),
+                    "positions": f"{lwarm}..{lwarm + lsteps - 1}", "weight_bytes_per_token": LLAMA_WEIGHT_BYTES}
+        kept["llama"] = dict(lsample, key=key, W=W, q8=(mode == Mode.Q8))
+        log(f"  {key}: {lms * 1e3:.1f} us/token  {1e3 / lms:.0f} tok/s  weights {lgb:.0f} GB/s "
+            f"({lgb / HBM_PEAK_GBS:.1%} of HBM peak; floor {LLAMA_WEIGHT_BYTES / 8e12 * 1e6:.1f} us)")
     line["per_format"] = per
 
-    # ---- CPU baseline (oracle, same workload, bounded sample) ---------------------
+    # ---- CPU baseline + parity checks (oracle) -------------------------------------
     if not args.no_cpu:
-        log("cpu baseline: oracle mm_1d on the headline workload (~10 s sample)")
-        med, threads, calls = cpu_baseline(b, x, dt, n, k)
-        cpu_gbs = nbytes / med / 1e9
-        line["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                                "sample": f"{calls} calls of mm_1d (f32 activations, reference order) on the "
-                                          f"headline Q4_0 11008x4096 batch-1 workload, median {med * 1e3:.2f} ms"}
-        log(f"  cpu {cpu_gbs:.2f} GB/s on {threads} threads")
+        log("cpu leg: oracle mm_1d on the headline workload (~10 s sample) and parity checks")
+        cpu_leg(line, head, kept)
     ctx.close()
     print(json.dumps(line), flush=True)
 

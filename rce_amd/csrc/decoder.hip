@@ -34,15 +34,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 // rce-tinyllama/src/lib.rs L158-163: mean_sq = sum(v*v) / n,
 // inv = 1 / sqrt(mean_sq + eps), out = (v * inv) * w.
 __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w, int n,
-                                                      float eps, float *__restrict__ out, int *pos_next,
-                                                      int *pos_cur, int ctx_len, int *status) {
+                                                      float eps, float *__restrict__ out, int *pos, int ctx_len,
+                                                      int *status) {
     __shared__ float part[NORM_NT / 64];
     const int t = threadIdx.x;
-    if (pos_next && t == 0) {  // the first kernel of a decode step
-        const int p = pos_next[0];
-        pos_cur[0] = p;
-        pos_next[0] = p + 1;
+    if (pos && t == 0) {  // the last norm of a decode step advances the position
+        const int p = pos[0];
         if (p >= ctx_len) status[0] = 2;
+        pos[0] = p + 1;
     }
     float ss = 0.0f;
     for (int i = t; i < n; i += NORM_NT) {
@@ -76,25 +75,24 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
 //     key 0 sets out = 0 + 1 * v_0, l = 1; key j > 0: m' = max(m, s_j),
 //     alpha = exp(m - m'), beta = exp(s_j - m'), out = out * alpha +
 //     beta * v_j, l = l * alpha + beta; finally out *= 1 / l.  Keys are
-//     staged in chunks of CH through LDS: lane j computes s_j, the running
-//     maxima come from a prefix max over the chunk (max is exact, so these
-//     equal the reference's sequential maxima), and the out / l recurrence
-//     runs in key order with lane = dimension.
+//     taken in chunks of CH: lane j loads key row j of the chunk and computes
+//     s_j, every lane loads its dimensions of the chunk's value rows (all
+//     loads of a chunk are issued together), the running maxima come from a
+//     prefix max over the chunk (max is exact, so these equal the
+//     reference's sequential maxima), and the out / l recurrence runs in key
+//     order with lane = dimension.
 template <int DH>
 __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv, const float *__restrict__ rope_cs,
                                                   float *__restrict__ k_cache, float *__restrict__ v_cache,
-                                                  const int *__restrict__ pos_cur, int ctx_len, int n_q, int n_kv,
+                                                  const int *__restrict__ pos_p, int ctx_len, int n_q, int n_kv,
                                                   int rope_dim, float scale, float *__restrict__ att) {
     constexpr int DPL = DH / 64;    // dimensions per lane
-    constexpr int CH = 4096 / DH;   // keys per chunk (64 or 32): 33 KB of LDS staging
-    constexpr int KLD = DH + 1;     // padded key rows: lane j reads row j without bank conflicts
+    constexpr int CH = 4096 / DH;   // keys per chunk (64 or 32)
+    constexpr int R4 = DH / 4;      // float4 pieces of a row
     __shared__ float qs[DH], ks[DH], vs[DH];
-    __shared__ float kch[CH * KLD];
-    __shared__ float vch[CH * DH];
-    __shared__ float al[CH], be[CH];
     const int lane = threadIdx.x, h = blockIdx.x;
-    const int pos = pos_cur[0];
-    if (pos < 0 || pos >= ctx_len) return;  // status was set by the step's first kernel
+    const int pos = pos_p[0];
+    if (pos < 0 || pos >= ctx_len) return;  // the step's last kernel reports it
     const int qpk = n_q / n_kv, g = h / qpk;
     const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH;
     for (int i = lane; i < DH; i += 64) {
@@ -118,6 +116,7 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
         ks[i + half] = as + bc;
     }
     __syncthreads();
+    const float *kbase = k_cache + (size_t)g * DH, *vbase = v_cache + (size_t)g * DH;
     if (h % qpk == 0) {
         float *kd = k_cache + (size_t)pos * kvd + (size_t)g * DH, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
         for (int i = lane; i < DH; i += 64) {
@@ -125,6 +124,10 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
             vd[i] = vs[i];
         }
     }
+    // q in registers (every lane needs all of it for its key's dot)
+    float q[DH];
+#pragma unroll
+    for (int i = 0; i < DH; i++) q[i] = qs[i];
     const int seq = pos + 1;
     float o[DPL];
 #pragma unroll
@@ -132,30 +135,50 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
     float m = -INFINITY, l = 0.0f;
     for (int c0 = 0; c0 < seq; c0 += CH) {
         const int n = min(CH, seq - c0);
-        // stage keys and values c0 .. c0 + n - 1 (position pos from this block's own copy)
-        constexpr int R4 = DH / 4;  // float4 pieces per row
-        for (int p = lane; p < n * R4; p += 64) {
-            const int r = p / R4, c4 = p - r * R4, row = c0 + r;
-            float4 kv, vv;
-            if (row == pos) {
-                kv = make_float4(ks[4 * c4], ks[4 * c4 + 1], ks[4 * c4 + 2], ks[4 * c4 + 3]);
-                vv = make_float4(vs[4 * c4], vs[4 * c4 + 1], vs[4 * c4 + 2], vs[4 * c4 + 3]);
-            } else {
-                kv = *reinterpret_cast<const float4 *>(k_cache + (size_t)row * kvd + (size_t)g * DH + 4 * c4);
-                vv = *reinterpret_cast<const float4 *>(v_cache + (size_t)row * kvd + (size_t)g * DH + 4 * c4);
-            }
-            float *kr = kch + r * KLD + 4 * c4;
-            kr[0] = kv.x; kr[1] = kv.y; kr[2] = kv.z; kr[3] = kv.w;
-            *reinterpret_cast<float4 *>(vch + r * DH + 4 * c4) = vv;
+        // Positions before pos come from the caches (written by earlier
+        // steps); position pos from this block's own k / v.  Loads are
+        // unconditional (rows at or past pos read row 0, always in range,
+        // and are not used) so that all of them are in flight together.
+        const int kr = c0 + lane;
+        float4 kv[R4];
+        {
+            const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(kr < pos ? kr : 0) * kvd);
+#pragma unroll
+            for (int i = 0; i < R4; i++) kv[i] = kp[i];
         }
-        __syncthreads();
+        float vv[CH][DPL];
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int r = c0 + j;
+            const float *vp = vbase + (size_t)(r < pos ? r : 0) * kvd;
+#pragma unroll
+            for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
+        }
+        if (kr == pos) {  // this lane's key is the current position
+#pragma unroll
+            for (int i = 0; i < R4; i++) kv[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
+        }
+        if (pos - c0 < CH) {  // the chunk holds the current position: its value row from vs
+            const int jp = pos - c0;
+#pragma unroll
+            for (int j = 0; j < CH; j++)
+                if (j == jp) {
+#pragma unroll
+                    for (int d = 0; d < DPL; d++) vv[j][d] = vs[lane + 64 * d];
+                }
+        }
         float sc = -INFINITY;
         if (lane < n) {
-            const float *kr = kch + lane * KLD;
             float dot = 0.0f;
-#pragma unroll 16
-            for (int i = 0; i < DH; i++) {
-                const float pr = qs[i] * kr[i];
+#pragma unroll
+            for (int i = 0; i < R4; i++) {
+                float pr = q[4 * i] * kv[i].x;
+                dot = dot + pr;
+                pr = q[4 * i + 1] * kv[i].y;
+                dot = dot + pr;
+                pr = q[4 * i + 2] * kv[i].z;
+                dot = dot + pr;
+                pr = q[4 * i + 3] * kv[i].w;
                 dot = dot + pr;
             }
             sc = dot * scale;
@@ -171,33 +194,33 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
         const float m_incl = fmaxf(m, pm);
         float m_prev = __shfl_up(m_incl, 1);
         if (lane == 0) m_prev = m;
-        if (lane < n) {
-            al[lane] = expf(m_prev - m_incl);
-            be[lane] = expf(sc - m_incl);
-        }
+        const float alpha = lane < n ? expf(m_prev - m_incl) : 1.0f;
+        const float beta = lane < n ? expf(sc - m_incl) : 0.0f;
         m = __shfl(m_incl, n - 1);
-        __syncthreads();
-        for (int j = 0; j < n; j++) {
-            const float *vr = vch + j * DH;
-            if (c0 + j == 0) {  // the first key: out = 0 + 1 * v, l = 1
+        // the recurrence in key order; key j's factors broadcast from lane j
 #pragma unroll
-                for (int d = 0; d < DPL; d++) {
-                    const float t = 1.0f * vr[lane + 64 * d];
-                    o[d] = o[d] + t;
-                }
-                l = 1.0f;
-            } else {
-                const float a = al[j], b = be[j];
+        for (int j = 0; j < CH; j++) {
+            if (j < n) {
+                const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), j));
+                const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, beta), j));
+                if (c0 + j == 0) {  // the first key: out = 0 + 1 * v, l = 1
 #pragma unroll
-                for (int d = 0; d < DPL; d++) {
-                    const float t1 = o[d] * a, t2 = b * vr[lane + 64 * d];
-                    o[d] = t1 + t2;
+                    for (int d = 0; d < DPL; d++) {
+                        const float t = 1.0f * vv[j][d];
+                        o[d] = o[d] + t;
+                    }
+                    l = 1.0f;
+                } else {
+#pragma unroll
+                    for (int d = 0; d < DPL; d++) {
+                        const float t1 = o[d] * a, t2 = b * vv[j][d];
+                        o[d] = t1 + t2;
+                    }
+                    const float la = l * a;
+                    l = la + b;
                 }
-                const float la = l * a;
-                l = la + b;
             }
         }
-        __syncthreads();  // the next chunk overwrites the staging buffers
     }
     float *out = att + (size_t)h * DH;
     if (l != 0.0f) {
@@ -221,10 +244,9 @@ __global__ void k_add_inplace(float *__restrict__ x, const float *__restrict__ o
 
 }  // namespace
 
-hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos_next, int *pos_cur,
-                           int ctx_len, int *status, hipStream_t s) {
-    hipLaunchKernelGGL(k_rms_norm, dim3(1), dim3(NORM_NT), 0, s, x, w, (int)n, eps, out, pos_next, pos_cur, ctx_len,
-                       status);
+hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos, int ctx_len,
+                           int *status, hipStream_t s) {
+    hipLaunchKernelGGL(k_rms_norm, dim3(1), dim3(NORM_NT), 0, s, x, w, (int)n, eps, out, pos, ctx_len, status);
     return hipGetLastError();
 }
 
@@ -232,17 +254,17 @@ bool attention_supports(int d_head, int rope_dim) {
     return (d_head == 64 || d_head == 128) && rope_dim >= 0 && rope_dim <= d_head && rope_dim % 2 == 0;
 }
 
-hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache, const int *pos_cur,
+hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache, const int *pos,
                             int ctx_len, int n_q, int n_kv, int d_head, int rope_dim, float scale, float *att,
                             hipStream_t s) {
     if (n_kv <= 0 || n_q % n_kv) return hipErrorInvalidValue;
     switch (d_head) {
     case 64:
-        hipLaunchKernelGGL(k_attention<64>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos_cur, ctx_len,
+        hipLaunchKernelGGL(k_attention<64>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos, ctx_len,
                            n_q, n_kv, rope_dim, scale, att);
         break;
     case 128:
-        hipLaunchKernelGGL(k_attention<128>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos_cur,
+        hipLaunchKernelGGL(k_attention<128>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos,
                            ctx_len, n_q, n_kv, rope_dim, scale, att);
         break;
     default:

@@ -7,20 +7,23 @@
 // Kernels of one step (L layers):
 //   [embed row]            outside the graph, token input only
 //   per layer:
-//     rms_norm(x, attn_norm) -> xn      (the first one also advances pos)
-//     q | k | v = W{q,k,v} xn           one FX_SEG launch when the three
-//                                       weights share format and width
+//     q | k | v = W{q,k,v} rms_norm(x)  one FX_SEG | FX_NORM launch when the
+//                                       three weights share format and width
 //     attention                         RoPE, cache append, softmax . V
 //     x = x + Wo att                    FX_RESIDUAL
-//     rms_norm(x, ffn_norm) -> xn
-//     h = silu(Wg xn) * (Wu xn)         FX_SWIGLU when gate and up share format
+//     h = silu(Wg n) * (Wu n),          FX_SWIGLU | FX_NORM when gate and up
+//         n = rms_norm(x)               share format
 //     x = x + Wd h                      FX_RESIDUAL
-//   rms_norm(x, output_norm) -> xn; logits = lm_head xn
-// Linears whose format has no fused form run as plain GEMVs followed by the
+//   rms_norm(x, output_norm) -> xn      also advances the position
+//   logits = lm_head xn
+// Every kernel of a step reads the position from pos (device memory), so
+// the recorded graph replays for any position.  Linears whose format has no
+// fused form run as a separate rms_norm and plain GEMVs followed by the
 // unfused add / swiglu kernels.
 #include "abi_internal.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -36,21 +39,24 @@ struct rce_qmm_llama {
     struct Layer {
         DevWeight wq, wk, wv, wo, gate, up, down;
         bool qkv_seg = false, wo_res = false, ffn_swiglu = false, down_res = false;
+        bool qkv_norm = false, ffn_norm = false;  // the fused forms also form rms_norm
     };
     std::vector<Layer> layers;
     // device memory (one allocation)
     void *mem = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *g = nullptr, *u = nullptr,
           *o = nullptr, *logits = nullptr, *norms = nullptr, *rope_cs = nullptr, *kc = nullptr, *vc = nullptr;
-    int *pos_next = nullptr, *pos_cur = nullptr, *status = nullptr, *token = nullptr;
+    int *pos_dev = nullptr, *status = nullptr, *token = nullptr;
     // pinned host staging
     int32_t *h_token = nullptr;
     int *h_status = nullptr;
     float *h_logits = nullptr;
-    size_t pos = 0;  // host mirror of pos_next
+    size_t pos = 0;  // host mirror of pos_dev
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     float *graph_logits = nullptr;  // where the captured graph writes logits
+    bool eager = false;  // RCE_QMM_LLAMA_GRAPH=0: launch the step's kernels one by one (tools that
+                         // cannot follow graph replays)
 
     size_t qd() const { return cfg.n_q_heads * cfg.d_head; }
     size_t kvd() const { return cfg.n_kv_heads * cfg.d_head; }
@@ -93,30 +99,28 @@ rce_qmm_status enqueue_body(rce_qmm_llama *m, float *logits, hipStream_t s) {
     const size_t dm = c.d_model, qd = m->qd(), kvd = m->kvd();
     const int ctx_len = (int)c.context_length;
     const float scale = 1.0f / std::sqrt((float)c.d_head);  // rce-tinyllama L269
-    bool first = true;
-    auto norm = [&](const float *w) {
-        hipError_t e = launch_rms_norm(m->x, w, dm, c.eps, m->xn, first ? m->pos_next : nullptr, m->pos_cur, ctx_len,
-                                       m->status, s);
-        first = false;
-        return e;
+    auto norm = [&](const float *w, int *pos) {
+        return launch_rms_norm(m->x, w, dm, c.eps, m->xn, pos, ctx_len, m->status, s);
     };
     for (size_t il = 0; il < c.n_layers; il++) {
         const rce_qmm_llama::Layer &L = m->layers[il];
         float *kc = m->kc + il * m->cache_layer(), *vc = m->vc + il * m->cache_layer();
-        HIP_TRY(norm(m->attn_norm(il)));
+        if (!L.qkv_norm) HIP_TRY(norm(m->attn_norm(il), nullptr));
         if (L.qkv_seg) {
             FxLaunch f;
-            f.kind = FX_SEG;
+            f.kind = L.qkv_norm ? (FX_SEG | FX_NORM) : FX_SEG;
             f.nw = 3;
             f.w[0] = L.wq; f.w[1] = L.wk; f.w[2] = L.wv;
             f.out[0] = m->qkv; f.out[1] = m->qkv + qd; f.out[2] = m->qkv + qd + kvd;
-            HIP_TRY(launch_gemv_fx(f, m->xn, m->mode, s));
+            f.norm_w = m->attn_norm(il);
+            f.eps = c.eps;
+            HIP_TRY(launch_gemv_fx(f, L.qkv_norm ? m->x : m->xn, m->mode, s));
         } else {
             HIP_TRY(launch_gemv(L.wq, m->xn, 1, m->qkv, m->mode, s));
             HIP_TRY(launch_gemv(L.wk, m->xn, 1, m->qkv + qd, m->mode, s));
             HIP_TRY(launch_gemv(L.wv, m->xn, 1, m->qkv + qd + kvd, m->mode, s));
         }
-        HIP_TRY(launch_attention(m->qkv, m->rope_cs, kc, vc, m->pos_cur, ctx_len, (int)c.n_q_heads, (int)c.n_kv_heads,
+        HIP_TRY(launch_attention(m->qkv, m->rope_cs, kc, vc, m->pos_dev, ctx_len, (int)c.n_q_heads, (int)c.n_kv_heads,
                                  (int)c.d_head, (int)c.rope_dim, scale, m->att, s));
         if (L.wo_res) {
             FxLaunch f;
@@ -129,14 +133,16 @@ rce_qmm_status enqueue_body(rce_qmm_llama *m, float *logits, hipStream_t s) {
             HIP_TRY(launch_gemv(L.wo, m->att, 1, m->o, m->mode, s));
             HIP_TRY(launch_add_inplace(m->x, m->o, dm, s));
         }
-        HIP_TRY(norm(m->ffn_norm(il)));
+        if (!L.ffn_norm) HIP_TRY(norm(m->ffn_norm(il), nullptr));
         if (L.ffn_swiglu) {
             FxLaunch f;
-            f.kind = FX_SWIGLU;
+            f.kind = L.ffn_norm ? (FX_SWIGLU | FX_NORM) : FX_SWIGLU;
             f.nw = 2;
             f.w[0] = L.gate; f.w[1] = L.up;
             f.out[0] = m->h;
-            HIP_TRY(launch_gemv_fx(f, m->xn, m->mode, s));
+            f.norm_w = m->ffn_norm(il);
+            f.eps = c.eps;
+            HIP_TRY(launch_gemv_fx(f, L.ffn_norm ? m->x : m->xn, m->mode, s));
         } else {
             HIP_TRY(launch_gemv(L.gate, m->xn, 1, m->g, m->mode, s));
             HIP_TRY(launch_gemv(L.up, m->xn, 1, m->u, m->mode, s));
@@ -154,7 +160,7 @@ rce_qmm_status enqueue_body(rce_qmm_llama *m, float *logits, hipStream_t s) {
             HIP_TRY(launch_add_inplace(m->x, m->o, dm, s));
         }
     }
-    HIP_TRY(norm(m->out_norm()));
+    HIP_TRY(norm(m->out_norm(), m->pos_dev));  // the step's last reader of pos advances it
     HIP_TRY(launch_gemv(m->head, m->xn, 1, logits, m->mode, s));
     return RCE_QMM_OK;
 }
@@ -187,9 +193,14 @@ rce_qmm_status graph_for(rce_qmm_llama *m, float *logits, hipStream_t s) {
 rce_qmm_status run_step(rce_qmm_llama *m, float *logits, hipStream_t s) {
     if (m->pos >= m->cfg.context_length)
         return fail(RCE_QMM_BAD_SHAPE, "the KV cache is full (context_length " + std::to_string(m->cfg.context_length) + ")");
-    rce_qmm_status st = graph_for(m, logits, s);
-    if (st) return st;
-    HIP_TRY(hipGraphLaunch(m->exec, s));
+    if (m->eager) {
+        rce_qmm_status st = enqueue_body(m, logits, s);
+        if (st) return st;
+    } else {
+        rce_qmm_status st = graph_for(m, logits, s);
+        if (st) return st;
+        HIP_TRY(hipGraphLaunch(m->exec, s));
+    }
     m->pos++;
     return RCE_QMM_OK;
 }
@@ -259,6 +270,7 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     m->ctx = ctx;
     m->cfg = c;
     m->mode = md;
+    if (const char *g = std::getenv("RCE_QMM_LLAMA_GRAPH")) m->eager = g[0] == '0';
     auto keep = [&](const rce_qmm_weight *w) { m->keep.push_back(w->alloc); return w->dw; };
     m->embd = keep(token_embd);
     m->head = keep(lm_head);
@@ -268,8 +280,12 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
         L.wq = keep(b.wq); L.wk = keep(b.wk); L.wv = keep(b.wv); L.wo = keep(b.wo);
         L.gate = keep(b.ffn_gate); L.up = keep(b.ffn_up); L.down = keep(b.ffn_down);
         L.qkv_seg = fx_ok(L.wq, md) && L.wk.dtype == L.wq.dtype && L.wv.dtype == L.wq.dtype;
+        L.qkv_norm = L.qkv_seg && gemv_fx_supports(L.wq.dtype, L.wq.n_cols, md, true) &&
+                     std::getenv("RCE_QMM_LLAMA_NORM_KERNEL") == nullptr;
         L.wo_res = fx_ok(L.wo, md);
         L.ffn_swiglu = fx_ok(L.gate, md) && L.up.dtype == L.gate.dtype;
+        L.ffn_norm = L.ffn_swiglu && gemv_fx_supports(L.gate.dtype, L.gate.n_cols, md, true) &&
+                     std::getenv("RCE_QMM_LLAMA_NORM_KERNEL") == nullptr;
         L.down_res = fx_ok(L.down, md);
         m->layers.push_back(L);
     }
@@ -286,7 +302,7 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
         total = align_up(total + n_f[i] * sizeof(float), 256);
     }
     off[13] = total;
-    total += 256;  // ints: pos_next, pos_cur, status, token
+    total += 256;  // ints: pos, status, token
     hipError_t e = hipMalloc(&m->mem, total);
     if (e != hipSuccess) {
         m->mem = nullptr;
@@ -298,10 +314,9 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
                     &m->norms, &m->rope_cs, &m->kc, &m->vc};
     for (int i = 0; i < 13; i++) *fp[i] = reinterpret_cast<float *>(base + off[i]);
     int *ints = reinterpret_cast<int *>(base + off[13]);
-    m->pos_next = ints;
-    m->pos_cur = ints + 1;
-    m->status = ints + 2;
-    m->token = ints + 3;
+    m->pos_dev = ints;
+    m->status = ints + 1;
+    m->token = ints + 2;
     auto cleanup = [&](rce_qmm_status s2) {
         rce_qmm_llama_destroy(m);
         return s2;
@@ -362,7 +377,7 @@ rce_qmm_status rce_qmm_llama_reset(rce_qmm_llama *m) {
     rce_qmm_status st = set_device(m->ctx->device);
     if (st) return st;
     hipStream_t s = m->ctx->stream;
-    HIP_TRY(hipMemsetAsync(m->pos_next, 0, 3 * sizeof(int), s));  // pos_next, pos_cur, status
+    HIP_TRY(hipMemsetAsync(m->pos_dev, 0, 2 * sizeof(int), s));  // pos, status
     HIP_TRY(hipStreamSynchronize(s));
     m->pos = 0;
     return RCE_QMM_OK;

@@ -216,7 +216,31 @@ __device__ __forceinline__ int round_half_away(float v) {
 // consecutive tasks (one lane quad) form a block of 32.
 struct QuantTask {
     float4 v0, v1;
+    float4 g0, g1;  // FX_NORM: the norm weights of the same 8 positions
 };
+
+// FX_NORM: the norm weights of the task's positions (out-of-range tasks read
+// task 0's, like quant_task_load).
+__device__ __forceinline__ void quant_task_load_g(const float *gw, int kq, int total, int task, QuantTask &q) {
+    const int tk = task < total ? task : 0;
+    const int e = (tk % kq) * 8;
+    const float4 *p = reinterpret_cast<const float4 *>(gw + e);
+    q.g0 = p[0];
+    q.g1 = p[1];
+}
+
+// Sequential sum of the squares of the task's 8 values (0 for a task past
+// the end): one task's share of rms_norm's sum of squares.
+__device__ __forceinline__ float quant_task_ssq(const QuantTask &q, bool valid) {
+    const float v[8] = {q.v0.x, q.v0.y, q.v0.z, q.v0.w, q.v1.x, q.v1.y, q.v1.z, q.v1.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float sq = v[i] * v[i];
+        s = s + sq;
+    }
+    return valid ? s : 0.0f;
+}
 
 __device__ __forceinline__ void quant_task_load(const float *A, int kq, int t0, int total, int task, QuantTask &q) {
     // kq = k / 8 tasks per token.  Out-of-range tasks load task 0 (always
@@ -234,8 +258,19 @@ __device__ __forceinline__ void quant_task_load(const float *A, int kq, int t0, 
 // id = 1/d (0 when d = 0), q = round half away from zero of x*id; the scale
 // kept is round_to_f16(d) (nn.rs L521-533 = the hardware's RNE conversion).
 // Every lane of the wave must call this (quad exchanges).
-__device__ __forceinline__ void quant_task_finish(const QuantTask &q, size_t k, int total, int task, const ActLds &L) {
+// NORM: the values are first normalized, (x * inv) * g (rms_norm's order).
+template <bool NORM = false>
+__device__ __forceinline__ void quant_task_finish(const QuantTask &q, size_t k, int total, int task, const ActLds &L,
+                                                  float inv = 0.0f) {
     float v[8] = {q.v0.x, q.v0.y, q.v0.z, q.v0.w, q.v1.x, q.v1.y, q.v1.z, q.v1.w};
+    if constexpr (NORM) {
+        const float g[8] = {q.g0.x, q.g0.y, q.g0.z, q.g0.w, q.g1.x, q.g1.y, q.g1.z, q.g1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float t = v[i] * inv;
+            v[i] = t * g[i];
+        }
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
@@ -311,6 +346,13 @@ struct Q4_0Exact {
 #pragma unroll
         for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
     }
+    // FX_NORM: the slice becomes (x * inv) * g (one token).
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float g[32];
+        load_f32x(gw + 32 * (size_t)col, g, 32);
+#pragma unroll
+        for (int l = 0; l < 32; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
+    }
 };
 
 // Q8_0 block, EXACT (rce-op-qmm/src/lib.rs L315-328, L648-670).
@@ -346,6 +388,12 @@ struct Q8_0Exact {
         const float scale = h2f(r.s);
 #pragma unroll
         for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
+    }
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float g[32];
+        load_f32x(gw + 32 * (size_t)col, g, 32);
+#pragma unroll
+        for (int l = 0; l < 32; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
     }
 };
 
@@ -409,6 +457,17 @@ struct Q4_KExact {
             s = s - min2 * a_hi[t];
             out[t] = s;
         }
+    }
+    // FX_NORM: the slice becomes (x * inv) * g and its sums are re-formed.
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float g[64];
+        load_f32x(gw + 64 * (size_t)col, g, 64);
+#pragma unroll
+        for (int l = 0; l < 64; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
+        a_lo[0] = 0.0f;
+        a_hi[0] = 0.0f;
+#pragma unroll
+        for (int l = 0; l < 32; l++) { a_lo[0] = a_lo[0] + av[0][l]; a_hi[0] = a_hi[0] + av[0][32 + l]; }
     }
 };
 
@@ -627,6 +686,9 @@ template <class Unit, int NT, int RPL, bool Q8, int FX>
 __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__restrict__ A, float *__restrict__ out,
                                                 int t_rows, int U, GemvFx fx) {
     constexpr int TB = Unit::NTOK;
+    constexpr int KIND = FX & 7;
+    constexpr bool NORM = (FX & FX_NORM) != 0;
+    static_assert(!NORM || TB == 1, "the normalizing forms are single-token");
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
     const int P = NT / U;
@@ -634,15 +696,15 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     const bool active = rsub < P;
     const int RT = P * RPL;
     unsigned bx = blockIdx.x;
-    if constexpr (FX == FX_SEG) {  // block-uniform choice of the segment
+    if constexpr (KIND == FX_SEG) {  // block-uniform choice of the segment
         if (bx >= fx.blk3) { w = fx.w3; out = fx.out3; bx -= fx.blk3; }
         else if (bx >= fx.blk2) { w = fx.w2; out = fx.out2; bx -= fx.blk2; }
     }
     // FX_SWIGLU: loads u < RPL / 2 read gate rows, the others the same up
     // rows; tile rows [0, RTO) are gate rows, [RTO, RT) the matching up rows.
     constexpr int HALF = RPL / 2;
-    static_assert(FX != FX_SWIGLU || RPL % 2 == 0, "swiglu pairs need an even row count per lane");
-    const int RTO = FX == FX_SWIGLU ? RT / 2 : RT;  // output rows of the block
+    static_assert(KIND != FX_SWIGLU || RPL % 2 == 0, "swiglu pairs need an even row count per lane");
+    const int RTO = KIND == FX_SWIGLU ? RT / 2 : RT;  // output rows of the block
     const size_t row0 = (size_t)bx * RTO;
     const int t0 = blockIdx.y * TB;
     const int tv = min(TB, t_rows - t0);
@@ -656,29 +718,51 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     // rows past the end, and idle lanes, load a valid row and are dropped.
     QuantTask qt0, qt1;
     const int kq = (int)(k / 8);
-    const int qtotal = Q8 ? tv * kq : 0;
-    if constexpr (Q8) {
+    // Q8: the block's quantization tasks; FX_NORM: the tasks of the sum of
+    // squares (the host guarantees kq <= 2 NT, so qt0 and qt1 cover the row)
+    const int qtotal = (Q8 || NORM) ? tv * kq : 0;
+    if constexpr (Q8 || NORM) {
         quant_task_load(A, kq, t0, qtotal, tid, qt0);
         quant_task_load(A, kq, t0, qtotal, tid + NT, qt1);
-    } else {
-        unit.init(A, k, t0, tv, col);
     }
+    if constexpr (Q8 && NORM) {
+        quant_task_load_g(fx.norm_w, kq, qtotal, tid, qt0);
+        quant_task_load_g(fx.norm_w, kq, qtotal, tid + NT, qt1);
+    }
+    if constexpr (!Q8) unit.init(A, k, t0, tv, col);
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weights'
     typename Unit::Raw raw[RPL];
     const int rs = active ? rsub : P - 1;
 #pragma unroll
     for (int u = 0; u < RPL; u++) {
-        const bool up = FX == FX_SWIGLU && u >= HALF;
+        const bool up = KIND == FX_SWIGLU && u >= HALF;
         const size_t r = row0 + (size_t)((up ? u - HALF : u) * P + rs);
         raw[u] = Unit::load(up ? fx.w2 : w, r < w.n_rows ? r : w.n_rows - 1, col);
     }
     // Keep every load above ahead of any arithmetic on loaded data.
     __builtin_amdgcn_sched_barrier(0);
+    // FX_NORM: rms_norm's scale from the whole row, while the weights load.
+    float inv = 0.0f;
+    if constexpr (NORM) {
+        __shared__ float red[NT / 64];
+        float ss = quant_task_ssq(qt0, tid < qtotal);
+        ss = ss + quant_task_ssq(qt1, tid + NT < qtotal);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NT / 64; i++) tot = tot + red[i];
+        const float mean_sq = tot / (float)k;
+        inv = 1.0f / sqrtf(mean_sq + fx.eps);
+        if constexpr (!Q8) unit.normalize(fx.norm_w, col, inv);
+    }
     // Phase 2 (Q8): quantize the block's activation rows into LDS.
     if constexpr (Q8) {
         ActLds L(lds, k, TB);
-        quant_task_finish(qt0, k, qtotal, tid, L);
-        quant_task_finish(qt1, k, qtotal, tid + NT, L);
+        quant_task_finish<NORM>(qt0, k, qtotal, tid, L, inv);
+        quant_task_finish<NORM>(qt1, k, qtotal, tid + NT, L, inv);
         for (int base = 2 * NT; base < qtotal; base += NT) {
             QuantTask q;
             quant_task_load(A, kq, t0, qtotal, base + tid, q);
@@ -698,7 +782,7 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
         float ad[TB];
         unit.addends(raw[u], ad);
         const int r = u * P + rsub;
-        const bool up = FX == FX_SWIGLU && u >= HALF;
+        const bool up = KIND == FX_SWIGLU && u >= HALF;
         const bool in = row0 + (up ? r - RTO : r) < w.n_rows;
 #pragma unroll
         for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = in ? ad[t] : 0.0f;
@@ -725,10 +809,10 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
         const int t = j / RTO, r = j % RTO;
         if (row0 + r < w.n_rows) {
             const size_t o = ((size_t)t0 + t) * w.n_rows + row0 + r;
-            if constexpr (FX == FX_SWIGLU) {
+            if constexpr (KIND == FX_SWIGLU) {
                 const float g = fold(t, r), u = fold(t, RTO + r);
                 out[o] = silu_ref(g) * u;  // rce-tinyllama L320: h = silu(g) * u
-            } else if constexpr (FX == FX_RESIDUAL) {
+            } else if constexpr (KIND == FX_RESIDUAL) {
                 out[o] = fx.res[o] + fold(t, r);  // rce-tinyllama L318, L323: x += ...
             } else {
                 out[o] = fold(t, r);
@@ -777,28 +861,44 @@ hipError_t launch_as_fx(const FxLaunch &f, int U, const float *a, hipStream_t s)
         return (unsigned)((w.n_rows + rows_per_block - 1) / rows_per_block);
     };
     GemvFx fx{};
+    fx.norm_w = f.norm_w;
+    fx.eps = f.eps;
+    if ((f.kind & FX_NORM) && (f.w[0].n_cols / 8 > (size_t)(2 * NT) || !f.norm_w)) return hipErrorInvalidValue;
     unsigned blocks = 0;
-    switch (f.kind) {
+    switch (f.kind & 7) {
     case FX_SEG: {
         if (f.nw < 1 || f.nw > 3) return hipErrorInvalidValue;
         blocks = nblk(f.w[0], RT);
         fx.blk2 = fx.blk3 = ~0u;
         if (f.nw >= 2) { fx.w2 = f.w[1]; fx.out2 = f.out[1]; fx.blk2 = blocks; blocks += nblk(f.w[1], RT); }
         if (f.nw >= 3) { fx.w3 = f.w[2]; fx.out3 = f.out[2]; fx.blk3 = blocks; blocks += nblk(f.w[2], RT); }
-        hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SEG>), dim3(blocks), dim3(NT), lds, s, f.w[0], a, f.out[0], 1,
-                           U, fx);
+        if (f.kind & FX_NORM)
+            hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SEG | FX_NORM>), dim3(blocks), dim3(NT), lds, s, f.w[0], a,
+                               f.out[0], 1, U, fx);
+        else
+            hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SEG>), dim3(blocks), dim3(NT), lds, s, f.w[0], a,
+                               f.out[0], 1, U, fx);
         break;
     }
     case FX_RESIDUAL:
+        if (f.kind & FX_NORM) return hipErrorInvalidValue;
         fx.res = f.res;
         hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_RESIDUAL>), dim3(nblk(f.w[0], RT)), dim3(NT), lds, s, f.w[0],
                            a, f.out[0], 1, U, fx);
         break;
     case FX_SWIGLU:
-        if (f.nw != 2 || f.w[1].n_rows != f.w[0].n_rows) return hipErrorInvalidValue;
-        fx.w2 = f.w[1];
-        hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SWIGLU>), dim3(nblk(f.w[0], RT / 2)), dim3(NT), lds, s,
-                           f.w[0], a, f.out[0], 1, U, fx);
+        if constexpr (RPL % 2 != 0) {
+            return hipErrorInvalidValue;  // gate and up rows come in pairs
+        } else {
+            if (f.nw != 2 || f.w[1].n_rows != f.w[0].n_rows) return hipErrorInvalidValue;
+            fx.w2 = f.w[1];
+            if (f.kind & FX_NORM)
+                hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SWIGLU | FX_NORM>), dim3(nblk(f.w[0], RT / 2)),
+                                   dim3(NT), lds, s, f.w[0], a, f.out[0], 1, U, fx);
+            else
+                hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, Q8, FX_SWIGLU>), dim3(nblk(f.w[0], RT / 2)), dim3(NT), lds,
+                                   s, f.w[0], a, f.out[0], 1, U, fx);
+        }
         break;
     default:
         return hipErrorInvalidValue;
@@ -807,12 +907,13 @@ hipError_t launch_as_fx(const FxLaunch &f, int U, const float *a, hipStream_t s)
 }
 
 // Shapes of the fused forms: the plain GEMV's threads per block, rows per
-// lane 2, 4 or 8.
+// lane 1, 2, 4 or 8 (FX_SWIGLU: even).
 template <class Unit, bool Q8>
 hipError_t launch_as_fx_nt(const FxLaunch &f, const GemvGeom &g, const float *a, hipStream_t s) {
     const int U = units_per_row(f.w[0].dtype, f.w[0].n_cols);
 #define RCE_RPL_FX(NT)                                                      \
     switch (g.rpl) {                                                        \
+    case 1: return launch_as_fx<Unit, NT, 1, Q8>(f, U, a, s);               \
     case 2: return launch_as_fx<Unit, NT, 2, Q8>(f, U, a, s);               \
     case 4: return launch_as_fx<Unit, NT, 4, Q8>(f, U, a, s);               \
     case 8: return launch_as_fx<Unit, NT, 8, Q8>(f, U, a, s);               \

@@ -77,26 +77,36 @@ __device__ __forceinline__ float silu_ref(float x) {
 // FX_RESIDUAL: out[j] = res[j] + row_sum_j, the residual add that follows
 // the attention-output and down projections (res may alias out).
 // FX_SWIGLU: every block computes the same rows of w[0] (gate) and w[1]
-// (up) and writes silu(gate_j) * up_j.
-enum : int { FX_SEG = 1, FX_RESIDUAL = 2, FX_SWIGLU = 3 };
+// (up) and writes silu(gate_j) * up_j.  FX_NORM (with FX_SEG or
+// FX_SWIGLU): the input is the residual stream x and every block forms
+// rms_norm(x, norm_w, eps) itself (rce-tinyllama L158-163) before the
+// products: the sum of squares over tasks of 8 consecutive values (one
+// sequential fold per task, tasks t and t + NT on thread t, then a fixed
+// tree over the block), inv = 1 / sqrt(sum / n + eps), value (x * inv) * w.
+enum : int { FX_SEG = 1, FX_RESIDUAL = 2, FX_SWIGLU = 3, FX_NORM = 8 };
 
 struct GemvFx {
     DevWeight w2, w3;      // FX_SEG: segments 1 and 2; FX_SWIGLU: w2 = up
     float *out2, *out3;    // FX_SEG: their outputs
     unsigned blk2, blk3;   // FX_SEG: first block of segments 1 and 2
     const float *res;      // FX_RESIDUAL
+    const float *norm_w;   // FX_NORM
+    float eps;             // FX_NORM
 };
 
 struct FxLaunch {
-    int kind = FX_SEG;
+    int kind = FX_SEG;     // FX_SEG, FX_RESIDUAL, FX_SWIGLU, optionally | FX_NORM
     int nw = 1;            // weights used (FX_SEG 1..3, FX_SWIGLU 2, FX_RESIDUAL 1)
     DevWeight w[3]{};
     float *out[3]{};
     const float *res = nullptr;
+    const float *norm_w = nullptr;
+    float eps = 0.0f;
 };
 
-// Whether the fused forms exist for (dtype, n_cols, mode).
-bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode);
+// Whether the fused forms exist for (dtype, n_cols, mode); with_norm: also
+// with FX_NORM (the input row must be at most 16 values per thread).
+bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode, bool with_norm = false);
 // One token; all weights of one launch share dtype and n_cols (and, for
 // FX_SWIGLU, n_rows).
 hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s);
@@ -111,18 +121,19 @@ hipError_t launch_gemv_fx_q6_k(const FxLaunch &f, const GemvGeom &g, const float
 // [0, n_rows) sets status[0] = 1 and writes nothing.
 hipError_t launch_embed_row(const DevWeight &w, const int32_t *row_dev, float *x, int *status, hipStream_t s);
 // out = rms_norm(x, w, eps) (rce-tinyllama L158-163) over n values.  When
-// pos_next is given, one thread also starts a decode step: pos_cur[0] =
-// pos_next[0], pos_next[0] += 1, and status[0] = 2 if pos_cur >= ctx_len.
-hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos_next,
-                           int *pos_cur, int ctx_len, int *status, hipStream_t s);
-// RoPE of q (n_q heads) and k (n_kv heads) at pos_cur[0], append of k, v to
+// pos is given, one thread also ends a decode step: status[0] = 2 if
+// pos[0] >= ctx_len, then pos[0] += 1 (no other kernel of the step may
+// follow that reads pos).
+hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos, int ctx_len,
+                           int *status, hipStream_t s);
+// RoPE of q (n_q heads) and k (n_kv heads) at position pos[0], append of k, v to
 // the layer's caches, and per query head the reference's online-softmax
 // attention over positions 0..pos (rce-op-attn L107-151, L185-251).
 // qkv: [q (n_q * d_head) | k (n_kv * d_head) | v (n_kv * d_head)];
 // rope_cs: [ctx_len][rope_dim / 2] (cos, sin) pairs; caches
 // [ctx_len][n_kv * d_head]; att: [n_q * d_head].
 hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache,
-                            const int *pos_cur, int ctx_len, int n_q, int n_kv, int d_head, int rope_dim,
+                            const int *pos, int ctx_len, int n_q, int n_kv, int d_head, int rope_dim,
                             float scale, float *att, hipStream_t s);
 bool attention_supports(int d_head, int rope_dim);
 // h = silu(g) * u, x = x + o: the unfused forms.

@@ -163,3 +163,22 @@ def test_llama_tinyllama_shape(ctx):
     for mode, tol in ((Mode.EXACT, 1e-5), (Mode.Q8, 1e-3)):
         note(f"  mode={mode.name}")
         run_pair(ctx, W, mode, [1, 2, 31999, 4], tol).close()
+
+
+def test_llama_separate_norm_and_eager_paths(ctx, monkeypatch):
+    """RCE_QMM_LLAMA_NORM_KERNEL: rms_norm as its own kernel before the
+    fused q|k|v and gate/up launches (instead of inside them); and
+    RCE_QMM_LLAMA_GRAPH=0: the step's kernels launched one by one instead
+    of replayed from the graph, bit-identical to the replay."""
+    note("llama separate norm kernel + eager launches")
+    W = make_weights(tiny_cfg(), seed=30)
+    monkeypatch.setenv("RCE_QMM_LLAMA_NORM_KERNEL", "1")
+    run_pair(ctx, W, Mode.EXACT, TOKENS[:4], 1e-5).close()
+    monkeypatch.delenv("RCE_QMM_LLAMA_NORM_KERNEL")
+    graph = device_model(ctx, W, Mode.Q8)
+    monkeypatch.setenv("RCE_QMM_LLAMA_GRAPH", "0")
+    eager = device_model(ctx, W, Mode.Q8)
+    for t in TOKENS[:4]:
+        a, b = graph.forward_logits(t), eager.forward_logits(t)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    graph.close(); eager.close()
