@@ -89,20 +89,52 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
     constexpr int DPL = DH / 64;    // dimensions per lane
     constexpr int CH = 4096 / DH;   // keys per chunk (64 or 32)
     constexpr int R4 = DH / 4;      // float4 pieces of a row
-    __shared__ float qs[DH], ks[DH], vs[DH];
+    __shared__ float qs[DH], ks[DH], cs[DH];
     const int lane = threadIdx.x, h = blockIdx.x;
     const int pos = pos_p[0];
     if (pos < 0 || pos >= ctx_len) return;  // the step's last kernel reports it
     const int qpk = n_q / n_kv, g = h / qpk;
     const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH;
-    for (int i = lane; i < DH; i += 64) {
-        qs[i] = qkv[(size_t)h * DH + i];
-        ks[i] = qkv[qd + (size_t)g * DH + i];
-        vs[i] = qkv[qd + kvd + (size_t)g * DH + i];
+    const int half = rope_dim / 2;
+    const float *kbase = k_cache + (size_t)g * DH, *vbase = v_cache + (size_t)g * DH;
+
+    // One round of loads: this position's q, k, v, the RoPE row, and the
+    // first chunk of cached keys / values.  Cache rows at or past pos read
+    // row 0 (always in range) and are replaced or unused, so every load is
+    // unconditional and all are in flight together.
+    float qr[DPL], kr[DPL], vcur[DPL], csr[DPL];
+#pragma unroll
+    for (int d = 0; d < DPL; d++) {
+        const int i = lane + 64 * d;
+        qr[d] = qkv[(size_t)h * DH + i];
+        kr[d] = qkv[qd + (size_t)g * DH + i];
+        vcur[d] = qkv[qd + kvd + (size_t)g * DH + i];
+        csr[d] = i < 2 * half ? rope_cs[(size_t)pos * half * 2 + i] : 0.0f;
+    }
+    float4 kv[R4];
+    float vv[CH][DPL];
+    auto load_chunk = [&](int c0) {
+        const int r = c0 + lane;
+        const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(r < pos ? r : 0) * kvd);
+#pragma unroll
+        for (int i = 0; i < R4; i++) kv[i] = kp[i];
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int rj = c0 + j;
+            const float *vp = vbase + (size_t)(rj < pos ? rj : 0) * kvd;
+#pragma unroll
+            for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
+        }
+    };
+    load_chunk(0);
+#pragma unroll
+    for (int d = 0; d < DPL; d++) {
+        qs[lane + 64 * d] = qr[d];
+        ks[lane + 64 * d] = kr[d];
+        cs[lane + 64 * d] = csr[d];
     }
     __syncthreads();
-    const int half = rope_dim / 2;
-    const float *cs = rope_cs + (size_t)pos * half * 2;
+    // RoPE (rce-op-attn L115-151): pairs (i, i + half) -> (a c - b s, a s + b c)
     for (int i = lane; i < half; i += 64) {
         const float c = cs[2 * i], s = cs[2 * i + 1];
         float a = qs[i], b = qs[i + half];
@@ -116,12 +148,12 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
         ks[i + half] = as + bc;
     }
     __syncthreads();
-    const float *kbase = k_cache + (size_t)g * DH, *vbase = v_cache + (size_t)g * DH;
-    if (h % qpk == 0) {
+    if (h % qpk == 0) {  // append this position to the layer's caches
         float *kd = k_cache + (size_t)pos * kvd + (size_t)g * DH, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
-        for (int i = lane; i < DH; i += 64) {
-            kd[i] = ks[i];
-            vd[i] = vs[i];
+#pragma unroll
+        for (int d = 0; d < DPL; d++) {
+            kd[lane + 64 * d] = ks[lane + 64 * d];
+            vd[lane + 64 * d] = vcur[d];
         }
     }
     // q in registers (every lane needs all of it for its key's dot)
@@ -134,37 +166,19 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
     for (int d = 0; d < DPL; d++) o[d] = 0.0f;
     float m = -INFINITY, l = 0.0f;
     for (int c0 = 0; c0 < seq; c0 += CH) {
+        if (c0 > 0) load_chunk(c0);
         const int n = min(CH, seq - c0);
-        // Positions before pos come from the caches (written by earlier
-        // steps); position pos from this block's own k / v.  Loads are
-        // unconditional (rows at or past pos read row 0, always in range,
-        // and are not used) so that all of them are in flight together.
-        const int kr = c0 + lane;
-        float4 kv[R4];
-        {
-            const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(kr < pos ? kr : 0) * kvd);
-#pragma unroll
-            for (int i = 0; i < R4; i++) kv[i] = kp[i];
-        }
-        float vv[CH][DPL];
-#pragma unroll
-        for (int j = 0; j < CH; j++) {
-            const int r = c0 + j;
-            const float *vp = vbase + (size_t)(r < pos ? r : 0) * kvd;
-#pragma unroll
-            for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
-        }
-        if (kr == pos) {  // this lane's key is the current position
+        if (c0 + lane == pos) {  // this lane's key is the current position
 #pragma unroll
             for (int i = 0; i < R4; i++) kv[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
         }
-        if (pos - c0 < CH) {  // the chunk holds the current position: its value row from vs
+        if (pos - c0 < CH) {  // the chunk holds the current position: its value row
             const int jp = pos - c0;
 #pragma unroll
             for (int j = 0; j < CH; j++)
                 if (j == jp) {
 #pragma unroll
-                    for (int d = 0; d < DPL; d++) vv[j][d] = vs[lane + 64 * d];
+                    for (int d = 0; d < DPL; d++) vv[j][d] = vcur[d];
                 }
         }
         float sc = -INFINITY;

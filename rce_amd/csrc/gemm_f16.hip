@@ -3,16 +3,20 @@
 // Q4_K or Q4_0 blocks, dequantized to binary16 MFMA fragments in registers
 // and contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
 //
-// Tiling.  A block owns a 128 x 64 (M x N) output tile, so a 512 x 4096
-// product is 256 tiles: one per CU.  K runs in chunks of 64 (four MFMA
-// k-steps of 16).  The block has ten waves:
+// Tiling.  A block owns a BM x BN (M x N) output tile of 8192 outputs:
+// 128 x 64 or 64 x 128 (Tile<BM>), so a 512 x 4096 product is 256 tiles,
+// one per CU.  The 64 x 128 tile moves a third less data into LDS per flop
+// (8 KB of activations + 4.5 KB of weights per chunk instead of 16 + 2.25)
+// and has no empty rows when an expert of the grouped mode gets 64 tokens.
+// K runs in chunks of 64 (four MFMA k-steps of 16).  The block has ten waves:
 //   * eight compute waves: wave w = 2*kq + t computes k-step kq of every
-//     chunk for the 128 x 32 sub-tile of columns 32t.. (4 x 1 MFMA blocks of
-//     32 x 32): per chunk it reads four A fragments from LDS, dequantizes
-//     its one W fragment itself from the raw GGUF nibbles in LDS (each W
-//     nibble is dequantized by exactly one wave; no B tile is written), and
-//     issues four MFMAs.  The four k-step partial sums of each output are
-//     added at the end through LDS in a fixed order (deterministic);
+//     chunk for the BM x BN/2 sub-tile of columns BN/2 * t.. (RB x CB MFMA
+//     blocks of 32 x 32, four in all): per chunk it reads RB A fragments
+//     from LDS, dequantizes its CB W fragments itself from the raw GGUF
+//     nibbles in LDS (each W nibble is dequantized by exactly one wave; no
+//     B tile is written), and issues four MFMAs.  The four k-step partial
+//     sums of each output are added at the end through LDS in a fixed order
+//     (deterministic);
 //   * two producer waves issue every global -> LDS load and compute the
 //     per-sub-block fma scales from the GGUF headers.  A load instruction
 //     can hold its wave up while the CU's memory pipeline is busy (each
@@ -69,21 +73,11 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 64, KC = 64;
+constexpr int KC = 64;                           // K per chunk (four MFMA k-steps of 16)
 constexpr int NC = 512;                          // compute threads (8 waves)
 constexpr int NT = NC + 128;                     // + 2 producer waves
 constexpr int NS = 6;                            // A stages (chunks), loaded NS - 1 ahead
-constexpr int A_STAGE = BM * KC * 2;             // 16 KB
-constexpr int W_HALF = BN * 64;                  // 4 KB: 64 rows x 4 chunks x 16 B
-constexpr int W_GROUP = 2 * W_HALF + BN * 16;    // + 1 KB of scale headers
 constexpr int NWBUF = 4, GA = 2;                 // W groups loaded GA groups ahead
-constexpr int SC_BUF = BN * 2 * 16;              // [column][set][chunk] of f16 {scale, bias}
-constexpr int OFF_W = NS * A_STAGE;
-constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
-constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
-constexpr int RED_LDS = 8 * 4 * 16 * 64 * 4;     // partial sums: 8 waves x 64 floats x 64 lanes
-constexpr int GEMM_LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
-static_assert(GEMM_LDS + BM * 4 <= 160 * 1024, "LDS budget");
 // W group g must be complete at the barrier of chunk 4g-3 (its headers are
 // read there for the scales): its last load (iteration 4(g-GA)+1) precedes
 // the loads of A chunk 4g-2 (iteration 4g-2-(NS-1)).
@@ -92,6 +86,39 @@ static_assert(4 * GA >= NS + 2, "W groups loaded too late for the stage depth");
 // chunk 4(g+GA-NWBUF)+3 (iteration 4(g+GA-NWBUF)+1 < 4g).
 static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 static_assert(NS >= 3, "stage ring");
+
+// Output tile BM x BN with BM * BN = 8192: 128 x 64 or 64 x 128.  Compute
+// wave w = 2*kq + t holds RB x CB MFMA blocks of 32 x 32 (rows 32*rb,
+// columns BN/2 * t + 32*cb): four MFMAs per chunk either way.
+template <int BM_>
+struct Tile {
+    static constexpr int BM = BM_, BN = 8192 / BM_;
+    static constexpr int RB = BM / 32, CB = BN / 64;
+    static constexpr int A_STAGE = BM * KC * 2;           // 16 KB / 8 KB
+    static constexpr int A_LOADS = BM / 16;               // per producer per chunk (1 KB each)
+    static constexpr int W_HALF = BN * 64;                // rows x 4 chunks x 16 B
+    static constexpr int W_LOADS = BN / 16;               // per producer per group (its half)
+    static constexpr int W_GROUP = 2 * W_HALF + BN * 16;  // + the scale headers
+    static constexpr int SC_BUF = BN * 2 * 16;            // [column][set][chunk] of f16 {scale, bias}
+    static constexpr int OFF_W = NS * A_STAGE;
+    static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
+    static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
+    static constexpr int RED_LDS = 8 * RB * CB * 16 * 64 * 4;  // partial sums of every wave
+    static constexpr int LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
+    static_assert(LDS + BM * 4 <= 160 * 1024, "LDS budget");
+    static_assert(RB * CB == 4, "four MFMA blocks per compute wave; eight output blocks, one finished per wave");
+    // Producer loads of iteration `it`, in order: the W loads of position
+    // it % 4 (row halves at position 0, headers at 1), then the A loads of
+    // chunk it + NS - 1.
+    static constexpr int w_loads(int q) { return (q & 3) == 0 ? W_LOADS : (q & 3) == 1 ? 1 : 0; }
+    // vmcnt immediate for a producer's barrier at chunk position q: the
+    // loads it issued after chunk c+1's A loads (iterations c+3-NS .. c-1).
+    static constexpr int vm_after(int q) {
+        int n = 0;
+        for (int d = 1; d <= NS - 3; d++) n += A_LOADS + w_loads(q - d);
+        return n;
+    }
+};
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     _Float16 h;
@@ -269,17 +296,6 @@ struct Q40 {
     }
 };
 
-// Producer loads of iteration `it`, in order: the W loads of position
-// it % 4 (row halves at position 0, headers at 1), then the eight A loads
-// of chunk it + NS - 1.
-__host__ __device__ constexpr int w_loads(int q) { return (q & 3) == 0 ? 4 : (q & 3) == 1 ? 1 : 0; }
-// vmcnt immediate for a producer's barrier at chunk position q: the loads
-// it issued after chunk c+1's A loads, i.e. those of iterations c+3-NS .. c-1.
-__host__ __device__ constexpr int vm_after(int q) {
-    int n = 0;
-    for (int d = 1; d <= NS - 3; d++) n += 8 + w_loads(q - d);
-    return n;
-}
 
 template <int U>
 using ic = std::integral_constant<int, U>;
@@ -287,11 +303,15 @@ using ic = std::integral_constant<int, U>;
 // Plain GEMM: tiles == nullptr, row tile mt covers rows mt*BM .. of M.
 // Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows),
 // multiplied by wtab[e]; tiles at or past n_tiles[0] do nothing.
-template <class Fmt>
+template <class Fmt, int BM_>
 __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16 *__restrict__ A,
                                                  const int *__restrict__ gather, size_t M, uint32_t a_bytes,
                                                  float *__restrict__ out, int m_tiles, const MoeTile *__restrict__ tiles,
                                                  const int *__restrict__ n_tiles, const DevWeight *__restrict__ wtab) {
+    using T = Tile<BM_>;
+    constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB;
+    constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP, SC_BUF = T::SC_BUF;
+    constexpr int OFF_W = T::OFF_W, OFF_SC = T::OFF_SC;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int arow[BM];
     // Blocks are dispatched round-robin over 8 XCDs; consecutive logical
@@ -332,28 +352,29 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         // holds up only these two waves.
         const int pw = wave - NC / 64;  // 0, 1
         const int pt = tid - NC;        // 0 .. 127
-        //   A: rows 64*pw .. +63; instruction i covers rows 64pw + 8i .. +7,
-        //      8 lanes per row; lane slot p holds column p ^ f(row)
-        uint32_t a_lane[8];
+        //   A: rows BM/2*pw .. +BM/2-1; instruction i covers rows
+        //      BM/2*pw + 8i .. +7, 8 lanes per row; lane slot p holds
+        //      column p ^ f(row)
+        uint32_t a_lane[T::A_LOADS];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int ar = 64 * pw + 8 * i + (lane >> 3);
+        for (int i = 0; i < T::A_LOADS; i++) {
+            const int ar = BM / 2 * pw + 8 * i + (lane >> 3);
             const int aswz = (ar & 7) ^ ((ar >> 3) & 1);
             a_lane[i] = (uint32_t)arow[ar] * (uint32_t)(2 * K) + 16u * (uint32_t)((lane & 7) ^ aswz);
         }
         const __amdgpu_buffer_rsrc_t abuf = byte_buffer(A, a_bytes);
         //   W: half pw of the group; instruction i covers rows 16i .. +15,
         //      4 lanes per row, slot p holding piece p ^ ((row >> 2) & 3);
-        //      headers: rows 32*pw + lane for lanes 0..31
-        uint32_t w_lane[4];
+        //      headers: rows BN/2*pw + lane for lanes 0..BN/2-1
+        uint32_t w_lane[T::W_LOADS];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < T::W_LOADS; i++) {
             const int wr = 16 * i + (lane >> 2);
             size_t wrow = n0 + wr;
             wrow = wrow < N ? wrow : N - 1;  // rows past the end load the last row
             w_lane[i] = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
         }
-        size_t hrow = n0 + 32 * pw + (lane & 31);
+        size_t hrow = n0 + BN / 2 * pw + (lane & (BN / 2 - 1));
         hrow = hrow < N ? hrow : N - 1;
         const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
         const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(w.base, (uint32_t)(N * w.row_stride));
@@ -369,26 +390,31 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 if (q == 0) {
                     const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
-                } else if (lane < 32) {
-                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * 512);
+                    for (int i = 0; i < T::W_LOADS; i++)
+                        buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
+                } else if (lane < BN / 2) {
+                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * (BN / 2) * 16);
                 }
             }
             const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
-            unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * 8192;
+            unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * (A_STAGE / 2);
 #pragma unroll
-            for (int i = 0; i < 8; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
+            for (int i = 0; i < T::A_LOADS; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
         };
-        // scales of group g: thread = column pt % 64, set pt / 64, chunks 0..3
-        const int p_col = pt & (BN - 1), p_si = pt >> 6;
-        const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
-        const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_col * 2 + p_si) * 16);
+        // scales of group g: the (column, set) pairs pt, pt + 128, ... (set =
+        // pair / BN), chunks 0..3 each
         auto make_scales = [&](int g) {
-            u32x4 hdr = lds_read16<0>(hdr_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP));
-            wait_lgkm0(hdr);
-            const u32x4 v = {Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
-                             Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
-            lds_write16(sc_wr + (uint32_t)((g & 1) * SC_BUF), v);
+#pragma unroll
+            for (int pr = pt; pr < 2 * BN; pr += 128) {
+                const int p_col = pr & (BN - 1), p_si = pr / BN;
+                const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
+                const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_col * 2 + p_si) * 16);
+                u32x4 hdr = lds_read16<0>(hdr_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP));
+                wait_lgkm0(hdr);
+                const u32x4 v = {Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
+                                 Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
+                lds_write16(sc_wr + (uint32_t)((g & 1) * SC_BUF), v);
+            }
         };
 
         // prologue: virtual iterations -4GA .. -1; group 0's scales
@@ -400,26 +426,27 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 if (q == 0) {
                     const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
-                } else if (lane < 32) {
-                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * 512);
+                    for (int i = 0; i < T::W_LOADS; i++)
+                        buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
+                } else if (lane < BN / 2) {
+                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * (BN / 2) * 16);
                 }
             }
             if (it + NS - 1 >= 0) {
                 const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
-                unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * 8192;
+                unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * (A_STAGE / 2);
 #pragma unroll
-                for (int i = 0; i < 8; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
+                for (int i = 0; i < T::A_LOADS; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
             }
         }
-        wait_vm_barrier<vm_after(3)>();  // barrier P1: A chunks 0, 1 and W groups 0, 1 done
+        wait_vm_barrier<T::vm_after(3)>();  // barrier P1: A chunks 0, 1 and W groups 0, 1 done
         make_scales(0);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();  // barrier P2: group 0's scales written
         for (int g = 0; g < ngroups; g++) {
             auto step = [&](auto uc) {
                 constexpr int u = decltype(uc)::value;
-                wait_vm_barrier<vm_after(u)>();
+                wait_vm_barrier<T::vm_after(u)>();
                 issue(4 * g + u);
                 if constexpr (u == 1) {
                     make_scales(g + 1);  // read by the compute waves from step 2 on
@@ -439,42 +466,72 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 
     // ===== compute waves: wave w = 2*kq + t
     const int t = wave & 1, kq = wave >> 1;
-    // LDS read addresses of this lane; A row block i is +32 rows (+4096
-    // bytes): immediates.
+    // LDS read addresses of this lane; A row block rb is +32 rows (+4096
+    // bytes), W column block cb +32 rows of nibbles (+2048 bytes) and +32
+    // columns of scales (+1024 bytes): immediates.
     const int g0 = Fmt::acol(kq) + h;
     const uint32_t a_rd = lds0 + (uint32_t)(l32 * 128 + 16 * (g0 ^ ((l32 & 7) ^ ((l32 >> 3) & 1))));
-    const int ncol = 32 * t + l32;  // tile column of this lane
-    uint32_t w_rd[4];               // nibbles of chunk position q, lane half h (group buffer 0)
+    const int ncol = BN / 2 * t + l32;  // tile column of this lane in column block 0
+    uint32_t w_rd[4];                   // nibbles of chunk position q, lane half h (group buffer 0)
 #pragma unroll
     for (int q = 0; q < 4; q++)
         w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
                                             16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
     const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((ncol * 2 + Fmt::sidx(kq)) * 16);
 
-    f32x16 acc[4];
+    f32x16 acc[RB * CB];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = f32x16{};
+    for (int i = 0; i < RB * CB; i++) acc[i] = f32x16{};
     const int nsh = 4 * (kq & 1);  // low or high nibbles
     auto nib = [&](uint32_t x) { return (x >> nsh) & 0x0F0F0F0Fu; };
+    auto read_a = [&](half8 *a, uint32_t addr) {
+        a[0] = lds_read_frag<0>(addr);
+        if constexpr (RB > 1) a[1] = lds_read_frag<4096>(addr);
+        if constexpr (RB > 2) {
+            a[2] = lds_read_frag<8192>(addr);
+            a[3] = lds_read_frag<12288>(addr);
+        }
+    };
+    auto read_w = [&](u32x2 *r, uint32_t addr) {
+        r[0] = lds_read8<0>(addr);
+        if constexpr (CB > 1) r[1] = lds_read8<2048>(addr);
+    };
+    auto read_sc = [&](u32x4 *v, uint32_t addr) {
+        v[0] = lds_read16<0>(addr);
+        if constexpr (CB > 1) v[1] = lds_read16<1024>(addr);
+    };
+    auto wait_reads = [&](half8 *a, u32x2 *r, u32x4 *v) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < RB; i++) pin(a[i]);
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            pin(r[i]);
+            pin(v[i]);
+        }
+    };
 
     __builtin_amdgcn_s_barrier();  // barrier P1
     __builtin_amdgcn_s_barrier();  // barrier P2: chunk 0 dequantized, chunk 1's nibbles read
-    half8 a_cur[4], b_cur;
-    u32x2 raw_nxt;
-    u32x4 sc_cur;
+    half8 a_cur[RB], b_cur[CB];
+    u32x2 raw_nxt[CB];
+    u32x4 sc_cur[CB];
     {
-        a_cur[0] = lds_read_frag<0>(a_rd);
-        a_cur[1] = lds_read_frag<4096>(a_rd);
-        a_cur[2] = lds_read_frag<8192>(a_rd);
-        a_cur[3] = lds_read_frag<12288>(a_rd);
-        u32x2 raw0 = lds_read8<0>(w_rd[0]);
-        raw_nxt = lds_read8<0>(w_rd[1]);
-        sc_cur = lds_read16<0>(sc_rd);
-        wait_lgkm0(a_cur[0], a_cur[1], a_cur[2], a_cur[3], raw0, raw_nxt, sc_cur);
-        half2v h0, h1, h2, h3;
-        dequant4(nib(raw0.x), sc_cur.x, h0, h1);
-        dequant4(nib(raw0.y), sc_cur.x, h2, h3);
-        b_cur = join8(h0, h1, h2, h3);
+        u32x2 raw0[CB];
+        read_a(a_cur, a_rd);
+        read_w(raw0, w_rd[0]);
+        read_w(raw_nxt, w_rd[1]);
+        read_sc(sc_cur, sc_rd);
+        wait_reads(a_cur, raw0, sc_cur);
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) pin(raw_nxt[cb]);
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {
+            half2v h0, h1, h2, h3;
+            dequant4(nib(raw0[cb].x), sc_cur[cb].x, h0, h1);
+            dequant4(nib(raw0[cb].y), sc_cur[cb].x, h2, h3);
+            b_cur[cb] = join8(h0, h1, h2, h3);
+        }
     }
 
     // ---- main loop: one scale group (four chunks) per trip; chunk c's A is
@@ -485,7 +542,9 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         const uint32_t wb_cur = (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
         const uint32_t wb_nxt = (uint32_t)(((g + 1) & (NWBUF - 1)) * W_GROUP);
         const uint32_t sc_nxt_rd = sc_rd + (uint32_t)(((g + 1) & 1) * SC_BUF);
-        u32x4 sc_nxt = sc_cur;
+        u32x4 sc_nxt[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) sc_nxt[cb] = sc_cur[cb];
         auto step = [&](auto uc) {
             constexpr int u = decltype(uc)::value;
             // chunk c+1's A and W are in LDS (the producers waited for them);
@@ -495,38 +554,43 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             // u = 2 the next group's scales (written by the producers at u = 1)
             const uint32_t sa = a_rd + (uint32_t)(st1 * A_STAGE);
             st1 = st1 == NS - 1 ? 0 : st1 + 1;
-            half8 a_nxt[4];
-            a_nxt[0] = lds_read_frag<0>(sa);
-            a_nxt[1] = lds_read_frag<4096>(sa);
-            a_nxt[2] = lds_read_frag<8192>(sa);
-            a_nxt[3] = lds_read_frag<12288>(sa);
-            u32x2 raw_nn = lds_read8<0>(w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
-            if constexpr (u == 2) sc_nxt = lds_read16<0>(sc_nxt_rd);
+            half8 a_nxt[RB];
+            u32x2 raw_nn[CB];
+            read_a(a_nxt, sa);
+            read_w(raw_nn, w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
+            if constexpr (u == 2) read_sc(sc_nxt, sc_nxt_rd);
             __builtin_amdgcn_sched_barrier(0);
             // Chunk c's MFMAs and chunk c+1's dequantization (the next
             // group's first chunk for u = 3), independent of each other.
             constexpr int q1 = (u + 1) & 3;
-            const u32x4 &sv = (u == 3) ? sc_nxt : sc_cur;
-            const uint32_t sb = q1 == 0 ? sv.x : q1 == 1 ? sv.y : q1 == 2 ? sv.z : sv.w;
-            half2v hq[4];
-            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[0], b_cur, acc[0], 0, 0, 0);
-            dequant4(nib(raw_nxt.x), sb, hq[0], hq[1]);
-            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[1], b_cur, acc[1], 0, 0, 0);
-            dequant4(nib(raw_nxt.y), sb, hq[2], hq[3]);
-            acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[2], b_cur, acc[2], 0, 0, 0);
-            acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[3], b_cur, acc[3], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            wait_lgkm0(a_nxt[0], a_nxt[1], a_nxt[2], a_nxt[3], raw_nn, sc_nxt);
+            half2v hq[CB][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) a_cur[i] = a_nxt[i];
-            b_cur = join8(hq[0], hq[1], hq[2], hq[3]);
-            raw_nxt = raw_nn;
+            for (int cb = 0; cb < CB; cb++) {
+                const u32x4 &sv = (u == 3) ? sc_nxt[cb] : sc_cur[cb];
+                const uint32_t sb = q1 == 0 ? sv.x : q1 == 1 ? sv.y : q1 == 2 ? sv.z : sv.w;
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
+                    acc[rb * CB + cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[rb], b_cur[cb], acc[rb * CB + cb], 0, 0, 0);
+                    if (rb == 0) dequant4(nib(raw_nxt[cb].x), sb, hq[cb][0], hq[cb][1]);
+                    if (rb == 1) dequant4(nib(raw_nxt[cb].y), sb, hq[cb][2], hq[cb][3]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            wait_reads(a_nxt, raw_nn, sc_nxt);
+#pragma unroll
+            for (int i = 0; i < RB; i++) a_cur[i] = a_nxt[i];
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) {
+                b_cur[cb] = join8(hq[cb][0], hq[cb][1], hq[cb][2], hq[cb][3]);
+                raw_nxt[cb] = raw_nn[cb];
+            }
         };
         step(ic<0>{});
         step(ic<1>{});
         step(ic<2>{});
         step(ic<3>{});
-        sc_cur = sc_nxt;
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) sc_cur[cb] = sc_nxt[cb];
     }
     __syncthreads();  // barrier E1: the producers have drained their loads
 
@@ -535,24 +599,27 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // [wave][block][r/4][lane][r%4] (conflict-free 16-byte accesses).
     f32x4 *red = reinterpret_cast<f32x4 *>(lds);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < RB * CB; i++)
 #pragma unroll
         for (int rq = 0; rq < 4; rq++) {
             const f32x4 v = {acc[i][4 * rq], acc[i][4 * rq + 1], acc[i][4 * rq + 2], acc[i][4 * rq + 3]};
             red[((wave * 4 + i) * 4 + rq) * 64 + lane] = v;
         }
     __syncthreads();  // barrier E2
-    // Wave (t, kq) finishes row block kq of column half t: k-steps 0, 1, 2, 3
-    // added in order.
-    const size_t col = n0 + ncol;
+    // Wave w finishes output block w (row block w / 2CB, column block
+    // w % 2CB, i.e. column half ot, block ocb of that half): the partials of
+    // the waves 2*kq + ot, k-steps 0, 1, 2, 3 added in order.
+    const int orb = wave / (2 * CB), occ = wave % (2 * CB), ot = occ / CB, ocb = occ % CB;
+    const int oi = orb * CB + ocb;
+    const size_t col = n0 + (size_t)(BN / 2 * ot + 32 * ocb + l32);
 #pragma unroll
     for (int rq = 0; rq < 4; rq++) {
-        f32x4 sum = red[((t * 4 + kq) * 4 + rq) * 64 + lane];
+        f32x4 sum = red[((ot * 4 + oi) * 4 + rq) * 64 + lane];
 #pragma unroll
-        for (int k2 = 1; k2 < 4; k2++) sum += red[(((2 * k2 + t) * 4 + kq) * 4 + rq) * 64 + lane];
+        for (int k2 = 1; k2 < 4; k2++) sum += red[(((2 * k2 + ot) * 4 + oi) * 4 + rq) * 64 + lane];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int m = 32 * kq + 8 * rq + 4 * h + e;
+            const int m = 32 * orb + 8 * rq + 4 * h + e;
             if (m < rows && col < N) out[(m0 + m) * N + col] = sum[e];
         }
     }
@@ -563,35 +630,39 @@ __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__
     if (i < n) d[i] = (_Float16)s[i];
 }
 
-template <class Fmt>
-hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
-    const int m_tiles = (int)((M + BM - 1) / BM), n_tiles = (int)((w.n_rows + BN - 1) / BN);
+template <class Fmt, int BM>
+hipError_t set_lds_attr() {
     static bool attr_set = false;  // per process; the attribute is per function
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           GEMM_LDS);
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt, BM>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Tile<BM>::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_gemm_f16<Fmt>), dim3(m_tiles * n_tiles), dim3(NT), GEMM_LDS, s, w, a, (const int *)nullptr,
+    return hipSuccess;
+}
+
+template <class Fmt, int BM>
+hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
+    using T = Tile<BM>;
+    const int m_tiles = (int)((M + T::BM - 1) / T::BM), n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
+    hipError_t e = set_lds_attr<Fmt, BM>();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM>), dim3(m_tiles * n_tiles), dim3(NT), T::LDS, s, w, a, (const int *)nullptr,
                        M, (uint32_t)(M * w.n_cols * 2), out, m_tiles, (const MoeTile *)nullptr, (const int *)nullptr,
                        (const DevWeight *)nullptr);
     return hipGetLastError();
 }
 
-template <class Fmt>
+template <class Fmt, int BM>
 hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
                               const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, float *out,
                               hipStream_t s) {
-    const int n_tiles = (int)((w.n_rows + BN - 1) / BN);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           GEMM_LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
-    hipLaunchKernelGGL((k_gemm_f16<Fmt>), dim3(max_tiles * n_tiles), dim3(NT), GEMM_LDS, s, w, a, gather, a_rows,
+    using T = Tile<BM>;
+    const int n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
+    hipError_t e = set_lds_attr<Fmt, BM>();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM>), dim3(max_tiles * n_tiles), dim3(NT), T::LDS, s, w, a, gather, a_rows,
                        (uint32_t)(a_rows * w.n_cols * 2), out, max_tiles, tiles, n_tiles_dev, wtab);
     return hipGetLastError();
 }
@@ -612,27 +683,37 @@ hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t 
     return hipGetLastError();
 }
 
+int gemm_tile_rows(size_t rows_hint) { return rows_hint <= 96 ? 64 : 128; }
+
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
-                                   float *out, hipStream_t s) {
+                                   int bm, float *out, hipStream_t s) {
     if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
     if (a_rows * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
         return hipErrorInvalidValue;
-    static_assert(GEMM_BM == BM, "tile rows");
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
-    if (w.dtype == T_Q4_K) return launch_fmt_grouped<Q4K>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
-    if (w.dtype == T_Q4_0) return launch_fmt_grouped<Q40>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
+    const bool q4k = w.dtype == T_Q4_K;
+    if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
+    if (bm == 64)
+        return q4k ? launch_fmt_grouped<Q4K, 64>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s)
+                   : launch_fmt_grouped<Q40, 64>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
+    if (bm == 128)
+        return q4k ? launch_fmt_grouped<Q4K, 128>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s)
+                   : launch_fmt_grouped<Q40, 128>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s) {
+hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s, int bm) {
     if (M == 0 || w.n_rows == 0) return hipSuccess;
     // the kernel's per-lane load offsets are 32-bit
     if (M * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
         return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
-    if (w.dtype == T_Q4_K) return launch_fmt<Q4K>(w, a, M, out, s);
-    if (w.dtype == T_Q4_0) return launch_fmt<Q40>(w, a, M, out, s);
+    const bool q4k = w.dtype == T_Q4_K;
+    if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
+    if (bm == 0) bm = gemm_tile_rows(M);
+    if (bm == 64) return q4k ? launch_fmt<Q4K, 64>(w, a, M, out, s) : launch_fmt<Q40, 64>(w, a, M, out, s);
+    if (bm == 128) return q4k ? launch_fmt<Q4K, 128>(w, a, M, out, s) : launch_fmt<Q40, 128>(w, a, M, out, s);
     return hipErrorInvalidValue;
 }
 

@@ -384,7 +384,9 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
     // 1. stable grouping of the (token, decision) pairs by expert
     const size_t n_pairs = t_rows * top_k;
     if (n_pairs >= (size_t)1 << 30) return fail(RCE_QMM_BAD_SHAPE, "too many (token, decision) pairs");
-    const int max_tiles = (int)(n_pairs / GEMM_BM + n_expert);
+    // tile rows of the grouped GEMM for the average rows per expert
+    const int bm = gemm_tile_rows((n_pairs + n_expert - 1) / n_expert);
+    const int max_tiles = (int)(n_pairs / bm + n_expert);
     const size_t meta_ints = (n_expert + 1) + 2 * n_pairs + 2;
     const size_t meta_bytes = align_up(meta_ints * 4, 16) + (size_t)max_tiles * sizeof(MoeTile);
     if ((st = ensure(ctx, ctx->moe_meta, meta_bytes, s))) return st;
@@ -394,7 +396,7 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
     int *n_tiles = tok_of_slot + n_pairs;
     int *status = n_tiles + 1;
     MoeTile *tiles = reinterpret_cast<MoeTile *>(static_cast<char *>(ctx->moe_meta.p) + align_up(meta_ints * 4, 16));
-    HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, GEMM_BM, offs, slot_of_pair, tok_of_slot,
+    HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, bm, offs, slot_of_pair, tok_of_slot,
                              tiles, n_tiles, status, s));
     const int *n_slots = offs + n_expert;  // device count of slots with a valid expert
 
@@ -424,10 +426,10 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
         if ((st = ensure(ctx, ctx->moe_x, t_rows * d_model * 2, s))) return st;
         if ((st = ensure(ctx, ctx->moe_h16, n_pairs * d_ff * 2, s))) return st;
         HIP_TRY(launch_f32_to_f16(x_dev, ctx->moe_x.p, t_rows * d_model, s));
-        HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, h, s));
+        HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm, h, s));
         // 4. silu -> f16; W2 GEMM on the slots themselves
         HIP_TRY(launch_silu_f16(h, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
-        HIP_TRY(launch_gemm_f16_grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, tiles, n_tiles, max_tiles, y, s));
+        HIP_TRY(launch_gemm_f16_grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, tiles, n_tiles, max_tiles, bm, y, s));
     } else {
         if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
         // The decode kernels take host row counts: read the grouping back.

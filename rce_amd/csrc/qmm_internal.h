@@ -170,7 +170,11 @@ hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStr
 // Prefill GEMM on the matrix cores (gemm_f16.hip): out[M, n_rows] =
 // A[M, n_cols] . W^T, A binary16, W dequantized to binary16 tiles.
 bool gemm_supports(uint32_t dtype, size_t n_cols);
-hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s);
+// bm: output tile rows, 64 (tile 64 x 128) or 128 (128 x 64); 0 = by M.
+hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s, int bm = 0);
+// The tile rows the GEMM uses for about `rows_hint` rows per tile column
+// (the grouped mode: rows per expert).
+int gemm_tile_rows(size_t rows_hint);
 // f32 activations -> binary16 (round to nearest even) for the GEMM.
 hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t s);
 
@@ -179,7 +183,6 @@ hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t 
 struct MoeTile {
     int e, r0, rows, pad;
 };
-constexpr int GEMM_BM = 128;  // rows of a GEMM tile (launch_gemm_f16_grouped's bm)
 // Stable grouping of pairs p = token * top_k + j by expert ids[p]:
 // offs[n_expert + 1], slot_of_pair[n_pairs] (-1: id out of range),
 // tok_of_slot[n_pairs], tiles[n_pairs / bm + n_expert] (bm-row pieces of
@@ -203,6 +206,6 @@ hipError_t launch_moe_combine(const float *y, const int *slot_of_pair, const flo
 // a_rows: rows of A (bounds the loads); max_tiles bounds n_tiles_dev[0].
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
-                                   float *out, hipStream_t s);
+                                   int bm, float *out, hipStream_t s);
 
 }  // namespace rce_qmm
