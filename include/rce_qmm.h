@@ -206,6 +206,21 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
                                    const float *weights_dev, size_t top_k, float *out_dev,
                                    rce_qmm_mode mode, void *stream);
 
+/* The SwiGLU experts of rce-qwen36-moe (moe_ffn_forward's routed part,
+ * src/lib.rs L667-703): for every token t and decision j, e = ids[t, j]:
+ * g = gate[e] x_t, u = up[e] x_t, h = silu(g) * u, y_j = down[e] h
+ * (swiglu_expert_serial, L667-676), out_t = sum_j weights[t, j] * y_j in
+ * decision order from +0.0 (L698-703).  gate[e], up[e]: [d_ff, d_model],
+ * down[e]: [d_model, d_ff], all of one dtype; buffers and grouping as
+ * rce_qmm_moe_ffn_dev.  The shared expert and its sigmoid gate (L704-709)
+ * stay with the caller (for instance one more call with n_expert = 1 and
+ * the per-token gate as the weight). */
+rce_qmm_status rce_qmm_moe_swiglu_dev(rce_qmm_context *ctx, const rce_qmm_weight *const *gate,
+                                      const rce_qmm_weight *const *up, const rce_qmm_weight *const *down,
+                                      size_t n_expert, const float *x_dev, size_t t_rows,
+                                      const int32_t *ids_dev, const float *weights_dev, size_t top_k,
+                                      float *out_dev, rce_qmm_mode mode, void *stream);
+
 /* ---- Llama-2 decode step (the TinyLlama caller) -------------------------- */
 
 /* TinyLlamaConfig (rce-tinyllama/src/lib.rs L28-41); d_head = d_model /

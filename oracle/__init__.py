@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
             "orc_moe_combine": (None, [P, P, S, S, P]),
             "orc_moe_ffn": (I, [P, S, S, S, P, P, U32, P, P, S, P, I]),
             "orc_max_threads": (I, []),
+            "orc_moe_swiglu_ffn": (I, [P, S, S, S, P, P, P, U32, P, P, S, P, I]),
             "orc_rms_norm": (None, [P, P, S, F, P]),
             "orc_rope": (None, [P, S, F, S, P]),
             "orc_attend_head": (None, [P, P, P, S, S, S, S, F, P]),
@@ -276,6 +277,22 @@ def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0) -> 
                            _p(out), threads or max_threads())
     if rc:
         raise ValueError(f"orc_moe_ffn rc={rc}")
+    return out
+
+
+def moe_swiglu_ffn(x, gate_list, up_list, down_list, dtype, d_ff, ids, gate_w, threads: int = 0) -> np.ndarray:
+    """rce-qwen36-moe's routed SwiGLU experts (orc_moe_swiglu_ffn)."""
+    x = _c(x, np.float32)
+    t_rows, d_model = x.shape
+    ids = _c(ids, np.int32); gate_w = _c(gate_w, np.float32)
+    top_k = ids.shape[1]
+    keep = [[_c(b, np.uint8) for b in L] for L in (gate_list, up_list, down_list)]
+    ptrs = [(ctypes.c_void_p * len(L))(*[b.ctypes.data for b in L]) for L in keep]
+    out = np.zeros((t_rows, d_model), np.float32)
+    rc = lib().orc_moe_swiglu_ffn(_p(x), t_rows, d_model, d_ff, *[ctypes.cast(p, ctypes.c_void_p) for p in ptrs],
+                                  dtype, _p(ids), _p(gate_w), top_k, _p(out), threads or max_threads())
+    if rc:
+        raise ValueError(f"orc_moe_swiglu_ffn rc={rc}")
     return out
 
 

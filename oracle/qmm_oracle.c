@@ -1194,6 +1194,32 @@ EXPORT int orc_llama_forward(const size_t *dims, float rope_base, float eps, int
     return rc;
 }
 
+/* rce-qwen36-moe/src/lib.rs L667-703, the routed part of moe_ffn_forward:
+ * per token t and decision j, e = ids[t*top_k + j]: g = mm_1d(x_t, gate[e]),
+ * u = mm_1d(x_t, up[e]), h[i] = silu(g[i]) * u[i] (swiglu_expert_serial),
+ * y_j = mm_1d(h, down[e]); out_t = sum_j w_j * y_j from +0.0 in decision
+ * order (L698-703, = moe_combine). */
+EXPORT int orc_moe_swiglu_ffn(const float *x, size_t t_rows, size_t d_model, size_t d_ff,
+                              const uint8_t *const *gate, const uint8_t *const *up, const uint8_t *const *down,
+                              uint32_t t, const int32_t *ids, const float *gate_w, size_t top_k, float *out,
+                              int threads) {
+    float *g = (float *)malloc(d_ff * sizeof(float)), *u = (float *)malloc(d_ff * sizeof(float));
+    float *ys = (float *)malloc(top_k * d_model * sizeof(float));
+    int rc = 0;
+    for (size_t tr = 0; tr < t_rows && rc == 0; tr++) {
+        for (size_t j = 0; j < top_k && rc == 0; j++) {
+            int e = ids[tr * top_k + j];
+            rc = orc_mm_1d(x + tr * d_model, gate[e], t, d_ff, d_model, g, threads);
+            if (!rc) rc = orc_mm_1d(x + tr * d_model, up[e], t, d_ff, d_model, u, threads);
+            for (size_t i = 0; i < d_ff; i++) g[i] = orc_silu(g[i]) * u[i];
+            if (!rc) rc = orc_mm_1d(g, down[e], t, d_model, d_ff, ys + j * d_model, threads);
+        }
+        orc_moe_combine(gate_w + tr * top_k, ys, top_k, d_model, out + tr * d_model);
+    }
+    free(g); free(u); free(ys);
+    return rc;
+}
+
 EXPORT int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

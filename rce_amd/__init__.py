@@ -7,6 +7,7 @@ Python mirror of the reference operator API (``rce-op-qmm``) over that ABI;
 """
 from .qmm import (  # noqa: F401
     Context, DeviceBuffer, GgufDtype, Mode, QmmError, QuantWeight, block_geometry, mm_1d,
-    mm_1d_serial, mm_batched, mm_batched_dev, moe_ffn_dev, moe_router, quantize, row_bytes, supports,
+    mm_1d_serial, mm_batched, mm_batched_dev, moe_ffn_dev, moe_router, moe_swiglu_dev, quantize, row_bytes,
+    supports,
 )
 from .llama import TinyLlamaBlock, TinyLlamaConfig, TinyLlamaRuntime, TinyLlamaWeights  # noqa: F401,E402

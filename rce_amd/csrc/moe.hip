@@ -105,6 +105,22 @@ __global__ void k_silu_f16(const float *__restrict__ h, _Float16 *__restrict__ o
         o[i] = (_Float16)silu_ref(h[i]);
 }
 
+// SwiGLU experts (rce-qwen36-moe/src/lib.rs L667-676 swiglu_expert_serial):
+// h = silu(g) * u per slot, in place (f32) or into binary16 for the MFMA GEMM.
+__global__ void k_swiglu_slots(float *__restrict__ g, const float *__restrict__ u, const int *__restrict__ n_slots,
+                               size_t d) {
+    const size_t n = (size_t)n_slots[0] * d;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        g[i] = silu_ref(g[i]) * u[i];
+}
+
+__global__ void k_swiglu_slots_f16(const float *__restrict__ g, const float *__restrict__ u, _Float16 *__restrict__ o,
+                                   const int *__restrict__ n_slots, size_t d) {
+    const size_t n = (size_t)n_slots[0] * d;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        o[i] = (_Float16)(silu_ref(g[i]) * u[i]);
+}
+
 // moe_combine (rce-op-moe/src/lib.rs L98-110): out[t, :] = sum_j w[t, j] * y[slot(t, j), :],
 // j in decision order, from +0.0; a pair without a slot contributes nothing.
 __global__ void k_moe_combine(const float *__restrict__ y, const int *__restrict__ slot_of_pair,
@@ -155,6 +171,19 @@ hipError_t launch_silu_f16(const float *h, void *o, const int *n_slots_dev, size
                            hipStream_t s) {
     hipLaunchKernelGGL(k_silu_f16, dim3(grid_1d(max_slots * d, 256)), dim3(256), 0, s, h, static_cast<_Float16 *>(o),
                        n_slots_dev, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_slots(float *g, const float *u, const int *n_slots_dev, size_t max_slots, size_t d,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(k_swiglu_slots, dim3(grid_1d(max_slots * d, 256)), dim3(256), 0, s, g, u, n_slots_dev, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_slots_f16(const float *g, const float *u, void *o, const int *n_slots_dev, size_t max_slots,
+                                   size_t d, hipStream_t s) {
+    hipLaunchKernelGGL(k_swiglu_slots_f16, dim3(grid_1d(max_slots * d, 256)), dim3(256), 0, s, g, u,
+                       static_cast<_Float16 *>(o), n_slots_dev, d);
     return hipGetLastError();
 }
 

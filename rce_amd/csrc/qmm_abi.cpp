@@ -165,7 +165,7 @@ void rce_qmm_context_destroy(rce_qmm_context *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16, &ctx->moe_meta, &ctx->moe_wtab, &ctx->moe_x,
-                       &ctx->moe_h, &ctx->moe_h16, &ctx->moe_y})
+                       &ctx->moe_h, &ctx->moe_h16, &ctx->moe_y, &ctx->moe_u})
         if (s->p) (void)hipFree(s->p);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -353,16 +353,24 @@ rce_qmm_status rce_qmm_moe_router(const float *logits, size_t n_tokens, size_t n
     return RCE_QMM_OK;
 }
 
-rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *const *w1,
-                                   const rce_qmm_weight *const *w2, size_t n_expert, const float *x_dev,
-                                   size_t t_rows, const int32_t *ids_dev, const float *weights_dev, size_t top_k,
-                                   float *out_dev, rce_qmm_mode mode, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// The grouped experts: h = silu(W1 x) (w3 == nullptr, the benchmark's
+// two-matrix expert) or h = silu(W1 x) * (W3 x) (SwiGLU: W1 = gate, W3 =
+// up), y = W2 h, out = the decision-order combine.
+rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, const rce_qmm_weight *const *w3,
+                       const rce_qmm_weight *const *w2, size_t n_expert, const float *x_dev, size_t t_rows,
+                       const int32_t *ids_dev, const float *weights_dev, size_t top_k, float *out_dev,
+                       rce_qmm_mode mode, void *stream) {
     if (!ctx || !w1 || !w2) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight list");
     if (n_expert == 0 || n_expert > 4096 || top_k == 0 || top_k > n_expert)
         return fail(RCE_QMM_BAD_SHAPE, "need 0 < top_k <= n_expert <= 4096");
     rce_qmm_status st;
     for (size_t e = 0; e < n_expert; e++) {
         if ((st = check_weight_ctx(ctx, w1[e])) || (st = check_weight_ctx(ctx, w2[e]))) return st;
+        if (w3 && (st = check_weight_ctx(ctx, w3[e]))) return st;
     }
     const DevWeight &a1 = w1[0]->dw, &a2 = w2[0]->dw;
     const size_t d_model = a1.n_cols, d_ff = a1.n_rows;
@@ -372,6 +380,11 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
         if (b1.dtype != a1.dtype || b1.n_rows != d_ff || b1.n_cols != d_model || b1.layout != a1.layout ||
             b2.dtype != a2.dtype || b2.n_rows != d_model || b2.n_cols != d_ff || b2.layout != a2.layout)
             return fail(RCE_QMM_BAD_SHAPE, "experts differ in dtype or shape");
+        if (w3) {
+            const DevWeight &b3 = w3[e]->dw;
+            if (b3.dtype != a1.dtype || b3.n_rows != d_ff || b3.n_cols != d_model || b3.layout != a1.layout)
+                return fail(RCE_QMM_BAD_SHAPE, "up matrices must match the gate matrices in dtype and shape");
+        }
     }
     if (!supports_mode(a1.dtype, d_model, (int)mode) || !supports_mode(a2.dtype, d_ff, (int)mode))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "the experts' dtype/shape has no GPU kernel in mode " +
@@ -405,13 +418,19 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
     if ((st = ensure(ctx, ctx->moe_y, n_pairs * d_model * sizeof(float), s))) return st;
     float *h = static_cast<float *>(ctx->moe_h.p);
     float *y = static_cast<float *>(ctx->moe_y.p);
+    float *u = nullptr;  // SwiGLU: the up products
+    if (w3) {
+        if ((st = ensure(ctx, ctx->moe_u, n_pairs * d_ff * sizeof(float), s))) return st;
+        u = static_cast<float *>(ctx->moe_u.p);
+    }
 
     if (mode == RCE_QMM_MODE_F16_MFMA) {
         // 2. expert tables (uploaded when the expert set changes)
-        std::vector<DevWeight> tab(2 * n_expert);
+        std::vector<DevWeight> tab((w3 ? 3 : 2) * n_expert);
         for (size_t e = 0; e < n_expert; e++) {
             tab[e] = w1[e]->dw;
             tab[n_expert + e] = w2[e]->dw;
+            if (w3) tab[2 * n_expert + e] = w3[e]->dw;
         }
         const size_t tab_bytes = tab.size() * sizeof(DevWeight);
         if (ctx->moe_wtab_host.size() != tab.size() ||
@@ -422,13 +441,20 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
             ctx->moe_wtab_host = tab;
         }
         const DevWeight *wtab1 = static_cast<const DevWeight *>(ctx->moe_wtab.p), *wtab2 = wtab1 + n_expert;
+        const DevWeight *wtab3 = wtab1 + 2 * n_expert;
         // 3. x -> f16 once; W1 GEMM on the rows gathered per slot
         if ((st = ensure(ctx, ctx->moe_x, t_rows * d_model * 2, s))) return st;
         if ((st = ensure(ctx, ctx->moe_h16, n_pairs * d_ff * 2, s))) return st;
         HIP_TRY(launch_f32_to_f16(x_dev, ctx->moe_x.p, t_rows * d_model, s));
         HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm, h, s));
-        // 4. silu -> f16; W2 GEMM on the slots themselves
-        HIP_TRY(launch_silu_f16(h, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
+        // 4. silu (times the up products) -> f16; W2 GEMM on the slots themselves
+        if (w3) {
+            HIP_TRY(launch_gemm_f16_grouped(a1, wtab3, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm,
+                                            u, s));
+            HIP_TRY(launch_swiglu_slots_f16(h, u, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
+        } else {
+            HIP_TRY(launch_silu_f16(h, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
+        }
         HIP_TRY(launch_gemm_f16_grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, tiles, n_tiles, max_tiles, bm, y, s));
     } else {
         if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
@@ -442,13 +468,15 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
         if ((st = ensure(ctx, ctx->moe_x, n_pairs * d_model * sizeof(float), s))) return st;
         float *xg = static_cast<float *>(ctx->moe_x.p);
         HIP_TRY(launch_gather_rows(x_dev, tok_of_slot, n_slots, n_pairs, d_model, xg, s));
-        // 3. per expert: h = silu(W1 x), y = W2 h (the reference's per-row products)
+        // 3. per expert: h = silu(W1 x) [* (W3 x)], y = W2 h (the reference's per-row products)
         for (size_t e = 0; e < n_expert; e++) {
             const size_t r0 = (size_t)hoffs[e], n = (size_t)(hoffs[e + 1] - hoffs[e]);
             if (n == 0) continue;
             HIP_TRY(launch_gemv(w1[e]->dw, xg + r0 * d_model, n, h + r0 * d_ff, (int)mode, s));
+            if (w3) HIP_TRY(launch_gemv(w3[e]->dw, xg + r0 * d_model, n, u + r0 * d_ff, (int)mode, s));
         }
-        HIP_TRY(launch_silu_inplace(h, n_slots, n_pairs, d_ff, s));
+        if (w3) HIP_TRY(launch_swiglu_slots(h, u, n_slots, n_pairs, d_ff, s));
+        else HIP_TRY(launch_silu_inplace(h, n_slots, n_pairs, d_ff, s));
         for (size_t e = 0; e < n_expert; e++) {
             const size_t r0 = (size_t)hoffs[e], n = (size_t)(hoffs[e + 1] - hoffs[e]);
             if (n == 0) continue;
@@ -458,6 +486,26 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
     // 5. combine in decision order
     HIP_TRY(launch_moe_combine(y, slot_of_pair, weights_dev, t_rows, (int)top_k, d_model, out_dev, s));
     return RCE_QMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *const *w1,
+                                   const rce_qmm_weight *const *w2, size_t n_expert, const float *x_dev,
+                                   size_t t_rows, const int32_t *ids_dev, const float *weights_dev, size_t top_k,
+                                   float *out_dev, rce_qmm_mode mode, void *stream) {
+    return moe_run(ctx, w1, nullptr, w2, n_expert, x_dev, t_rows, ids_dev, weights_dev, top_k, out_dev, mode, stream);
+}
+
+rce_qmm_status rce_qmm_moe_swiglu_dev(rce_qmm_context *ctx, const rce_qmm_weight *const *gate,
+                                      const rce_qmm_weight *const *up, const rce_qmm_weight *const *down,
+                                      size_t n_expert, const float *x_dev, size_t t_rows, const int32_t *ids_dev,
+                                      const float *weights_dev, size_t top_k, float *out_dev, rce_qmm_mode mode,
+                                      void *stream) {
+    if (!up) return fail(RCE_QMM_NULL_ARGUMENT, "null up-projection list");
+    return moe_run(ctx, gate, up, down, n_expert, x_dev, t_rows, ids_dev, weights_dev, top_k, out_dev, mode, stream);
 }
 
 rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out) {

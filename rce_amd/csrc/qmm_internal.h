@@ -197,6 +197,12 @@ hipError_t launch_silu_inplace(float *h, const int *n_slots_dev, size_t max_slot
 // o (binary16) = silu(h)
 hipError_t launch_silu_f16(const float *h, void *o, const int *n_slots_dev, size_t max_slots, size_t d,
                            hipStream_t s);
+// SwiGLU experts: g = silu(g) * u over the first n_slots (device count) slots,
+// in place, or as binary16 into o.
+hipError_t launch_swiglu_slots(float *g, const float *u, const int *n_slots_dev, size_t max_slots, size_t d,
+                               hipStream_t s);
+hipError_t launch_swiglu_slots_f16(const float *g, const float *u, void *o, const int *n_slots_dev, size_t max_slots,
+                                   size_t d, hipStream_t s);
 // out[t, :] = sum_j gate_w[t, j] * y[slot_of_pair[t * top_k + j], :], j in order, from +0.0
 hipError_t launch_moe_combine(const float *y, const int *slot_of_pair, const float *gate_w, size_t t_rows, int top_k,
                               size_t d, float *out, hipStream_t s);

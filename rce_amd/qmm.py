@@ -22,7 +22,7 @@ from ._lib import QmmError, check, lib
 __all__ = [
     "GgufDtype", "Mode", "Context", "QuantWeight", "DeviceBuffer", "QmmError",
     "block_geometry", "row_bytes", "supports", "mm_1d", "mm_1d_serial", "mm_batched",
-    "mm_batched_dev", "moe_router", "moe_ffn_dev", "quantize",
+    "mm_batched_dev", "moe_router", "moe_ffn_dev", "moe_swiglu_dev", "quantize",
 ]
 
 
@@ -296,3 +296,19 @@ def moe_ffn_dev(ctx: Context, w1: list[QuantWeight], w2: list[QuantWeight], x_de
                                     n, ctypes.c_void_p(x_dev), t_rows, ctypes.c_void_p(ids_dev),
                                     ctypes.c_void_p(weights_dev), top_k, ctypes.c_void_p(out_dev), int(mode),
                                     ctypes.c_void_p(stream) if stream else None))
+
+
+def moe_swiglu_dev(ctx: Context, gate: list[QuantWeight], up: list[QuantWeight], down: list[QuantWeight], x_dev: int,
+                   t_rows: int, ids_dev: int, weights_dev: int, top_k: int, out_dev: int,
+                   mode: Mode = Mode.F16_MFMA, stream: int | None = None) -> None:
+    """SwiGLU grouped experts (rce_qmm_moe_swiglu_dev): rce-qwen36-moe's
+    routed experts down . (silu(gate . x) * (up . x)), combined in decision
+    order."""
+    n = len(gate)
+    arr = lambda ws: (ctypes.c_void_p * n)(*[w.handle.value for w in ws])  # noqa: E731
+    G, U, D = arr(gate), arr(up), arr(down)
+    check(lib().rce_qmm_moe_swiglu_dev(ctx.handle, ctypes.cast(G, ctypes.c_void_p), ctypes.cast(U, ctypes.c_void_p),
+                                       ctypes.cast(D, ctypes.c_void_p), n, ctypes.c_void_p(x_dev), t_rows,
+                                       ctypes.c_void_p(ids_dev), ctypes.c_void_p(weights_dev), top_k,
+                                       ctypes.c_void_p(out_dev), int(mode),
+                                       ctypes.c_void_p(stream) if stream else None))

@@ -136,3 +136,43 @@ def test_moe_bad_ids(ctx):
     ids[1, 0] = E  # out of range
     with pytest.raises(rce_amd.QmmError):
         run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.EXACT)
+
+
+# ---- SwiGLU experts (rce-qwen36-moe's form) ---------------------------------
+
+def run_swiglu(ctx, gb, ub, db, dt, d_model, d_ff, x, ids, gw, mode):
+    t_rows, top_k = ids.shape
+    G = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, d_ff, d_model) for b in gb]
+    U = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, d_ff, d_model) for b in ub]
+    D = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, d_model, d_ff) for b in db]
+    bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids.astype(np.int32))
+    bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw.astype(F32))
+    bo = rce_amd.DeviceBuffer(ctx, t_rows * d_model * 4)
+    outs = []
+    for _ in range(2):
+        rce_amd.moe_swiglu_dev(ctx, G, U, D, bx.ptr, t_rows, bi.ptr, bw.ptr, top_k, bo.ptr, mode)
+        ctx.synchronize()
+        outs.append(bo.download(F32, t_rows * d_model).reshape(t_rows, d_model))
+    for b in (bx, bi, bw, bo):
+        b.free()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "not run-to-run deterministic"
+    return outs[0]
+
+
+@pytest.mark.parametrize("mode,tol", [(Mode.EXACT, 1e-5), (Mode.F16_MFMA, 3e-3)])
+@pytest.mark.parametrize("E,dm,dff,t,k,dt", [(4, 512, 1024, 16, 2, O.Q4_0), (6, 256, 512, 9, 3, O.Q4_K)])
+def test_moe_swiglu(ctx, mode, tol, E, dm, dff, t, k, dt):
+    """rce_qmm_moe_swiglu_dev against the oracle's swiglu_expert_serial +
+    combine (orc_moe_swiglu_ffn); tolerances as the two-matrix form."""
+    note(f"moe swiglu mode={mode.name} E={E} d={dm} ff={dff} t={t} k={k} dt={dt}")
+    rng = np.random.default_rng(600 + E + t)
+    mk = lambda n, kk: O.quantize((rng.standard_normal((n, kk)) * 0.02).astype(F32), dt)  # noqa: E731
+    gb = [mk(dff, dm) for _ in range(E)]
+    ub = [mk(dff, dm) for _ in range(E)]
+    db = [mk(dm, dff) for _ in range(E)]
+    x = rng.standard_normal((t, dm)).astype(F32)
+    ids, gw = rce_amd.moe_router(rng.standard_normal((t, E)).astype(F32), k)
+    got = run_swiglu(ctx, gb, ub, db, dt, dm, dff, x, ids, gw, mode)
+    ref = O.moe_swiglu_ffn(x, gb, ub, db, dt, dff, ids, gw)
+    assert normwise(got, ref) < tol

@@ -332,3 +332,31 @@ def test_silu_branches():
         e = np.exp(np.float64(-x)) if x >= 0 else np.exp(np.float64(x))
         want = x / (1 + e) if x >= 0 else x * e / (1 + e)
         assert abs(O.silu(x) - want) <= 1e-6 * max(1.0, abs(want))
+
+
+def test_moe_swiglu_ffn_independent():
+    """orc_moe_swiglu_ffn (rce-qwen36-moe L667-703) against an f64 numpy
+    restatement over the dequantized experts: silu on the gate product,
+    times the up product, down, combined in decision order.  Swapping gate
+    and up, or dropping the up factor, is far outside the bound."""
+    rng = np.random.default_rng(77)
+    E, dm, dff, T, K = 3, 64, 96, 5, 2
+    dt = O.Q8_0
+    mk = lambda n, k: O.quantize((rng.standard_normal((n, k)) * 0.05).astype(np.float32), dt)  # noqa: E731
+    gate = [mk(dff, dm) for _ in range(E)]
+    up = [mk(dff, dm) for _ in range(E)]
+    down = [mk(dm, dff) for _ in range(E)]
+    x = rng.standard_normal((T, dm)).astype(np.float32)
+    ids = np.array([[0, 2], [1, 0], [2, 1], [2, 0], [1, 2]], np.int32)
+    gw = rng.random((T, K)).astype(np.float32)
+    got = O.moe_swiglu_ffn(x, gate, up, down, dt, dff, ids, gw)
+    deq = lambda b, n, k: O.dequantize(b, dt, n * k).reshape(n, k).astype(np.float64)  # noqa: E731
+    want = np.zeros((T, dm))
+    for t in range(T):
+        for j in range(K):
+            e = ids[t, j]
+            g = deq(gate[e], dff, dm) @ x[t]
+            u = deq(up[e], dff, dm) @ x[t]
+            h = g / (1 + np.exp(-g)) * u
+            want[t] += gw[t, j] * (deq(down[e], dm, dff) @ h)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
