@@ -275,7 +275,7 @@ bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode, bool with_norm) {
     return !with_norm || n_cols / 8 <= (size_t)(2 * nt_for(units_per_row(dtype, n_cols)));
 }
 
-hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s) {
+hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s, const GemvGeom *geom) {
     const DevWeight &w = f.w[0];
     if (mode != 0 && mode != 1) return hipErrorInvalidValue;
     if (!gemv_fx_supports(w.dtype, w.n_cols, mode, (f.kind & FX_NORM) != 0)) return hipErrorInvalidValue;
@@ -283,15 +283,20 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
         if (f.w[i].dtype != w.dtype || f.w[i].n_cols != w.n_cols) return hipErrorInvalidValue;
     GemvGeom g = pick_gemv_geom(w, 1, mode);
     if (g.rpl > 8) g.rpl = 8;  // the fused forms exist for 1, 2, 4 and 8 rows per lane
-    // at least one block per CU where the rows allow (the decode step's
-    // projections are small: 2048-2560 rows); gate/up pairs need an even count
+    // Rows per lane, measured on the decode step's shapes (2048-11264 rows):
+    // the plain forms want at least one block per CU; the normalizing forms
+    // repeat rms_norm's prologue in every block, so they take the most rows
+    // per lane that still leave 128 blocks.  Gate/up pairs need an even count.
     size_t rows = 0;
     for (int i = 0; i < f.nw; i++) rows += f.w[i].n_rows;
     if ((f.kind & 7) == FX_SWIGLU) rows = w.n_rows;
     const int P = g.nt / units_per_row(w.dtype, w.n_cols);
     const int min_rpl = (f.kind & 7) == FX_SWIGLU ? 2 : 1;
     const size_t per_rpl = (f.kind & 7) == FX_SWIGLU ? (size_t)P / 2 : (size_t)P;  // output rows per block per rpl
-    while (g.rpl > min_rpl && (rows + per_rpl * g.rpl - 1) / (per_rpl * g.rpl) < 256) g.rpl /= 2;
+    const size_t min_blocks = (f.kind & FX_NORM) ? 128 : 256;
+    if (f.kind & FX_NORM) g.rpl = 8;
+    while (g.rpl > min_rpl && (rows + per_rpl * g.rpl - 1) / (per_rpl * g.rpl) < min_blocks) g.rpl /= 2;
+    if (geom) g = *geom;
     switch (w.dtype) {
     case T_Q4_0: return launch_gemv_fx_q4_0(f, g, a, mode, s);
     case T_Q8_0: return launch_gemv_fx_q8_0(f, g, a, mode, s);

@@ -109,7 +109,9 @@ struct FxLaunch {
 bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode, bool with_norm = false);
 // One token; all weights of one launch share dtype and n_cols (and, for
 // FX_SWIGLU, n_rows).
-hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s);
+// `geom` overrides the launch shape (tuning only; nullptr = pick).
+hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream_t s,
+                          const GemvGeom *geom = nullptr);
 // Per-format launchers of the fused forms (gemv_<format>.hip).
 hipError_t launch_gemv_fx_q4_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q8_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
