@@ -13,8 +13,10 @@
 //     logf / expf / sinf / cosf in the reference's expression order (the
 //     functions Rust's f32 methods call on Linux), so the rotation is the
 //     reference's bit for bit.
-//   * attention: the reference's key order and recurrence; exp is the
-//     device's expf (last-bit differences from the host libm).
+//   * attention: the reference's key order and recurrence within each of
+//     four parallel runs of keys (up to 64 keys: one run, exactly the
+//     reference's order); longer contexts merge the runs in a fixed order;
+//     exp is the device's expf (last-bit differences from the host libm).
 //   * silu: silu_ref (device expf).
 // This file is built with -ffp-contract=off: no multiply-add contraction.
 #include "qmm_internal.h"
@@ -62,58 +64,56 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
     }
 }
 
-// One block (one wave) per query head h; kv head g = h / (n_q / n_kv)
-// (rce-tinyllama L262-281).  Steps:
-//  1. q_h and k_g, v_g of this position from the q|k|v projections;
-//     RoPE of q_h and k_g (rce-op-attn L115-151): pairs (i, i + half),
-//     (a, b) -> (a c - b s, a s + b c) with the position's table row.
-//  2. The first query head of each kv group appends k_g, v_g to the caches
-//     at pos (every head of the group uses its own copy of this position's
-//     k and v, so no block waits for another).
-//  3. fused_attend_head_window (rce-op-attn L196-251) over keys 0..pos in
-//     order: s_j = dot(q, k_j) * scale (dot: sequential sum of products);
-//     key 0 sets out = 0 + 1 * v_0, l = 1; key j > 0: m' = max(m, s_j),
-//     alpha = exp(m - m'), beta = exp(s_j - m'), out = out * alpha +
-//     beta * v_j, l = l * alpha + beta; finally out *= 1 / l.  Keys are
-//     taken in chunks of CH: lane j loads key row j of the chunk and computes
-//     s_j, every lane loads its dimensions of the chunk's value rows (all
-//     loads of a chunk are issued together), the running maxima come from a
-//     prefix max over the chunk (max is exact, so these equal the
-//     reference's sequential maxima), and the out / l recurrence runs in key
-//     order with lane = dimension.
+// Attention of one decode step: one block of NW waves per query head h;
+// kv head g = h / (n_q / n_kv) (rce-tinyllama L262-281).  Keys are cut into
+// splits of CH (64 for d_head 64, 32 for 128); wave w takes the contiguous
+// run of splits [w*ns/NW, (w+1)*ns/NW) of the ns the context needs.
+//  1. The block loads this position's q_h, k_g, v_g and the RoPE row into
+//     LDS and rotates q_h and k_g (rce-op-attn L115-151): pairs
+//     (i, i + half) -> (a c - b s, a s + b c).  The block of the first
+//     query head of each kv group appends k_g, v_g to the caches (every
+//     block uses its own copy of this position's k and v, so no block waits
+//     for another).
+//  2. Each wave runs fused_attend_head_window's recurrence (rce-op-attn
+//     L196-251) over its keys in order, one split at a time with all of a
+//     split's loads in flight together: lane j scores key j (sequential
+//     dot, times scale), the running maxima come from an exact prefix max,
+//     then out = out * alpha + beta * v_j and l = l * alpha + beta key by
+//     key with lane = dimension (a wave's first key gives out = v, l = 1, as
+//     the reference's first key does).
+//  3. One split (pos < CH): out *= 1 / l -- the reference's order exactly.
+//     Several: the waves' (m, l, out) are merged in wave order through LDS
+//     (M = max m_w; out = sum_w exp(m_w - M) out_w, l = sum_w exp(m_w - M)
+//     l_w; out *= 1 / l), a fixed order, so runs are bit-identical.
+constexpr int ATT_NW = 4;  // waves per head: one per SIMD, so no register spills
+
 template <int DH>
-__global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv, const float *__restrict__ rope_cs,
-                                                  float *__restrict__ k_cache, float *__restrict__ v_cache,
-                                                  const int *__restrict__ pos_p, int ctx_len, int n_q, int n_kv,
-                                                  int rope_dim, float scale, float *__restrict__ att) {
+__global__ __launch_bounds__(64 * ATT_NW) void k_attention(const float *__restrict__ qkv,
+                                                           const float *__restrict__ rope_cs,
+                                                           float *__restrict__ k_cache, float *__restrict__ v_cache,
+                                                           const int *__restrict__ pos_p, int ctx_len, int n_q,
+                                                           int n_kv, int rope_dim, float scale,
+                                                           float *__restrict__ att) {
     constexpr int DPL = DH / 64;    // dimensions per lane
-    constexpr int CH = 4096 / DH;   // keys per chunk (64 or 32)
+    constexpr int CH = 4096 / DH;   // keys per split (64 or 32)
     constexpr int R4 = DH / 4;      // float4 pieces of a row
-    __shared__ float qs[DH], ks[DH], cs[DH];
-    const int lane = threadIdx.x, h = blockIdx.x;
+    __shared__ float qs[DH], ks[DH], vs[DH], cs[DH];
+    __shared__ float mo[ATT_NW][DH + 2];  // each wave's out[DH], m, l
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
     const int pos = pos_p[0];
     if (pos < 0 || pos >= ctx_len) return;  // the step's last kernel reports it
+    const int seq = pos + 1, ns = (seq + CH - 1) / CH;
+    const int s_lo = wave * ns / ATT_NW, s_hi = (wave + 1) * ns / ATT_NW;  // this wave's splits
     const int qpk = n_q / n_kv, g = h / qpk;
     const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH;
     const int half = rope_dim / 2;
     const float *kbase = k_cache + (size_t)g * DH, *vbase = v_cache + (size_t)g * DH;
 
-    // One round of loads: this position's q, k, v, the RoPE row, and the
-    // first chunk of cached keys / values.  Cache rows at or past pos read
-    // row 0 (always in range) and are replaced or unused, so every load is
-    // unconditional and all are in flight together.
-    float qr[DPL], kr[DPL], vcur[DPL], csr[DPL];
-#pragma unroll
-    for (int d = 0; d < DPL; d++) {
-        const int i = lane + 64 * d;
-        qr[d] = qkv[(size_t)h * DH + i];
-        kr[d] = qkv[qd + (size_t)g * DH + i];
-        vcur[d] = qkv[qd + kvd + (size_t)g * DH + i];
-        csr[d] = i < 2 * half ? rope_cs[(size_t)pos * half * 2 + i] : 0.0f;
-    }
     float4 kv[R4];
     float vv[CH][DPL];
-    auto load_chunk = [&](int c0) {
+    // A split's cached keys / values, every load unconditional: rows at or
+    // past pos read row 0 (always in range; replaced or unused).
+    auto load_split = [&](int c0) {
         const int r = c0 + lane;
         const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(r < pos ? r : 0) * kvd);
 #pragma unroll
@@ -126,16 +126,17 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
             for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
         }
     };
-    load_chunk(0);
-#pragma unroll
-    for (int d = 0; d < DPL; d++) {
-        qs[lane + 64 * d] = qr[d];
-        ks[lane + 64 * d] = kr[d];
-        cs[lane + 64 * d] = csr[d];
+    // one round of loads: this position's vectors (spread over the block)
+    // and the wave's first split
+    for (int i = tid; i < DH; i += 64 * ATT_NW) {
+        qs[i] = qkv[(size_t)h * DH + i];
+        ks[i] = qkv[qd + (size_t)g * DH + i];
+        vs[i] = qkv[qd + kvd + (size_t)g * DH + i];
+        cs[i] = i < 2 * half ? rope_cs[(size_t)pos * half * 2 + i] : 0.0f;
     }
+    if (s_lo < s_hi) load_split(s_lo * CH);
     __syncthreads();
-    // RoPE (rce-op-attn L115-151): pairs (i, i + half) -> (a c - b s, a s + b c)
-    for (int i = lane; i < half; i += 64) {
+    for (int i = tid; i < half; i += 64 * ATT_NW) {
         const float c = cs[2 * i], s = cs[2 * i + 1];
         float a = qs[i], b = qs[i + half];
         float ac = a * c, bs = b * s, as = a * s, bc = b * c;
@@ -148,102 +149,133 @@ __global__ __launch_bounds__(64) void k_attention(const float *__restrict__ qkv,
         ks[i + half] = as + bc;
     }
     __syncthreads();
-    if (h % qpk == 0) {  // append this position to the layer's caches
+    if (h % qpk == 0 && wave == 0) {  // append this position to the layer's caches
         float *kd = k_cache + (size_t)pos * kvd + (size_t)g * DH, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
 #pragma unroll
         for (int d = 0; d < DPL; d++) {
             kd[lane + 64 * d] = ks[lane + 64 * d];
-            vd[lane + 64 * d] = vcur[d];
+            vd[lane + 64 * d] = vs[lane + 64 * d];
         }
     }
-    // q in registers (every lane needs all of it for its key's dot)
-    float q[DH];
-#pragma unroll
-    for (int i = 0; i < DH; i++) q[i] = qs[i];
-    const int seq = pos + 1;
     float o[DPL];
 #pragma unroll
     for (int d = 0; d < DPL; d++) o[d] = 0.0f;
     float m = -INFINITY, l = 0.0f;
-    for (int c0 = 0; c0 < seq; c0 += CH) {
-        if (c0 > 0) load_chunk(c0);
-        const int n = min(CH, seq - c0);
-        if (c0 + lane == pos) {  // this lane's key is the current position
+    if (s_lo < s_hi) {
+        float q[DH];  // every lane needs all of q for its key's dot
 #pragma unroll
-            for (int i = 0; i < R4; i++) kv[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
-        }
-        if (pos - c0 < CH) {  // the chunk holds the current position: its value row
-            const int jp = pos - c0;
+        for (int i = 0; i < DH; i++) q[i] = qs[i];
+        for (int sp = s_lo; sp < s_hi; sp++) {
+            const int c0 = sp * CH, n = min(CH, seq - c0);
+            if (sp > s_lo) load_split(c0);
+            if (c0 + lane == pos) {  // this lane's key is the current position
 #pragma unroll
-            for (int j = 0; j < CH; j++)
-                if (j == jp) {
-#pragma unroll
-                    for (int d = 0; d < DPL; d++) vv[j][d] = vcur[d];
-                }
-        }
-        float sc = -INFINITY;
-        if (lane < n) {
-            float dot = 0.0f;
-#pragma unroll
-            for (int i = 0; i < R4; i++) {
-                float pr = q[4 * i] * kv[i].x;
-                dot = dot + pr;
-                pr = q[4 * i + 1] * kv[i].y;
-                dot = dot + pr;
-                pr = q[4 * i + 2] * kv[i].z;
-                dot = dot + pr;
-                pr = q[4 * i + 3] * kv[i].w;
-                dot = dot + pr;
+                for (int i = 0; i < R4; i++) kv[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
             }
-            sc = dot * scale;
-        }
-        // running maxima: inclusive prefix max over the chunk, after m
-        // (lanes past n hold -inf and come after every valid lane)
-        float pm = sc;
+            if (pos - c0 < CH) {  // the split holds the current position: its value row
+                const int jp = pos - c0;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float t = __shfl_up(pm, off);
-            if (lane >= off) pm = fmaxf(pm, t);
-        }
-        const float m_incl = fmaxf(m, pm);
-        float m_prev = __shfl_up(m_incl, 1);
-        if (lane == 0) m_prev = m;
-        const float alpha = lane < n ? expf(m_prev - m_incl) : 1.0f;
-        const float beta = lane < n ? expf(sc - m_incl) : 0.0f;
-        m = __shfl(m_incl, n - 1);
-        // the recurrence in key order; key j's factors broadcast from lane j
+                for (int j = 0; j < CH; j++)
+                    if (j == jp) {
 #pragma unroll
-        for (int j = 0; j < CH; j++) {
-            if (j < n) {
-                const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), j));
-                const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, beta), j));
-                if (c0 + j == 0) {  // the first key: out = 0 + 1 * v, l = 1
-#pragma unroll
-                    for (int d = 0; d < DPL; d++) {
-                        const float t = 1.0f * vv[j][d];
-                        o[d] = o[d] + t;
+                        for (int d = 0; d < DPL; d++) vv[j][d] = vs[lane + 64 * d];
                     }
-                    l = 1.0f;
-                } else {
+            }
+            float sc = -INFINITY;
+            if (lane < n) {
+                float dot = 0.0f;
 #pragma unroll
-                    for (int d = 0; d < DPL; d++) {
-                        const float t1 = o[d] * a, t2 = b * vv[j][d];
-                        o[d] = t1 + t2;
+                for (int i = 0; i < R4; i++) {
+                    float pr = q[4 * i] * kv[i].x;
+                    dot = dot + pr;
+                    pr = q[4 * i + 1] * kv[i].y;
+                    dot = dot + pr;
+                    pr = q[4 * i + 2] * kv[i].z;
+                    dot = dot + pr;
+                    pr = q[4 * i + 3] * kv[i].w;
+                    dot = dot + pr;
+                }
+                sc = dot * scale;
+            }
+            // running maxima: inclusive prefix max over the split, after m
+            // (lanes past n hold -inf and come after every valid lane)
+            float pm = sc;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float t = __shfl_up(pm, off);
+                if (lane >= off) pm = fmaxf(pm, t);
+            }
+            const float m_incl = fmaxf(m, pm);
+            float m_prev = __shfl_up(m_incl, 1);
+            if (lane == 0) m_prev = m;
+            // a wave's first key: exp(-inf) = 0 and exp(0) = 1, so out = v, l = 1
+            const float alpha = lane < n ? expf(m_prev - m_incl) : 1.0f;
+            const float beta = lane < n ? expf(sc - m_incl) : 0.0f;
+            m = __shfl(m_incl, n - 1);
+            // the recurrence in key order; key j's factors broadcast from lane j
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                if (j < n) {
+                    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), j));
+                    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, beta), j));
+                    if (c0 + j == 0) {  // the reference's first key: out = 0 + 1 * v, l = 1
+#pragma unroll
+                        for (int d = 0; d < DPL; d++) {
+                            const float t = 1.0f * vv[j][d];
+                            o[d] = o[d] + t;
+                        }
+                        l = 1.0f;
+                    } else {
+#pragma unroll
+                        for (int d = 0; d < DPL; d++) {
+                            const float t1 = o[d] * a, t2 = b * vv[j][d];
+                            o[d] = t1 + t2;
+                        }
+                        const float la = l * a;
+                        l = la + b;
                     }
-                    const float la = l * a;
-                    l = la + b;
                 }
             }
         }
     }
     float *out = att + (size_t)h * DH;
-    if (l != 0.0f) {
-        const float inv = 1.0f / l;
+    if (ns == 1) {  // the single wave that had the keys finishes as the reference does
+        if (s_lo < s_hi) {
+            const float inv = 1.0f / l;
 #pragma unroll
-        for (int d = 0; d < DPL; d++) o[d] = o[d] * inv;
+            for (int d = 0; d < DPL; d++) out[lane + 64 * d] = o[d] * inv;
+        }
+        return;
     }
 #pragma unroll
-    for (int d = 0; d < DPL; d++) out[lane + 64 * d] = o[d];
+    for (int d = 0; d < DPL; d++) mo[wave][lane + 64 * d] = o[d];
+    if (lane == 0) {
+        mo[wave][DH] = s_lo < s_hi ? m : -INFINITY;
+        mo[wave][DH + 1] = l;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < ATT_NW; w++) M = fmaxf(M, mo[w][DH]);
+    float acc[DPL], lacc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DPL; d++) acc[d] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_NW; w++) {
+        if (mo[w][DH] == -INFINITY) continue;  // a wave without keys
+        const float wt = expf(mo[w][DH] - M);
+#pragma unroll
+        for (int d = 0; d < DPL; d++) {
+            const float t = wt * mo[w][lane + 64 * d];
+            acc[d] = acc[d] + t;
+        }
+        const float lw = wt * mo[w][DH + 1];
+        lacc = lacc + lw;
+    }
+    const float inv = 1.0f / lacc;
+#pragma unroll
+    for (int d = 0; d < DPL; d++) out[lane + 64 * d] = acc[d] * inv;
 }
 
 __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ h, size_t n) {
@@ -274,11 +306,11 @@ hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cac
     if (n_kv <= 0 || n_q % n_kv) return hipErrorInvalidValue;
     switch (d_head) {
     case 64:
-        hipLaunchKernelGGL(k_attention<64>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos, ctx_len,
-                           n_q, n_kv, rope_dim, scale, att);
+        hipLaunchKernelGGL(k_attention<64>, dim3(n_q), dim3(64 * ATT_NW), 0, s, qkv, rope_cs, k_cache, v_cache, pos,
+                           ctx_len, n_q, n_kv, rope_dim, scale, att);
         break;
     case 128:
-        hipLaunchKernelGGL(k_attention<128>, dim3(n_q), dim3(64), 0, s, qkv, rope_cs, k_cache, v_cache, pos,
+        hipLaunchKernelGGL(k_attention<128>, dim3(n_q), dim3(64 * ATT_NW), 0, s, qkv, rope_cs, k_cache, v_cache, pos,
                            ctx_len, n_q, n_kv, rope_dim, scale, att);
         break;
     default:

@@ -296,13 +296,15 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     const size_t n_f[] = {dm, dm, qd + 2 * kvd, qd, c.d_ff, c.d_ff, c.d_ff, std::max(dm, big), c.vocab,
                           (2 * c.n_layers + 1) * dm, c.context_length * std::max<size_t>(half, 1) * 2,
                           c.n_layers * c.context_length * kvd, c.n_layers * c.context_length * kvd};
-    size_t off[14], total = 0;
-    for (int i = 0; i < 13; i++) {
+    constexpr int NF = sizeof(n_f) / sizeof(n_f[0]);
+    size_t off[NF + 1], total = 0;
+    for (int i = 0; i < NF; i++) {
         off[i] = total;
         total = align_up(total + n_f[i] * sizeof(float), 256);
     }
-    off[13] = total;
-    total += 256;  // ints: pos, status, token
+    off[NF] = total;
+    const size_t int_bytes = 256;  // pos, status, token
+    total += int_bytes;
     hipError_t e = hipMalloc(&m->mem, total);
     if (e != hipSuccess) {
         m->mem = nullptr;
@@ -312,8 +314,9 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     char *base = static_cast<char *>(m->mem);
     float **fp[] = {&m->x, &m->xn, &m->qkv, &m->att, &m->h, &m->g, &m->u, &m->o, &m->logits,
                     &m->norms, &m->rope_cs, &m->kc, &m->vc};
-    for (int i = 0; i < 13; i++) *fp[i] = reinterpret_cast<float *>(base + off[i]);
-    int *ints = reinterpret_cast<int *>(base + off[13]);
+    static_assert(sizeof(fp) / sizeof(fp[0]) == NF, "one pointer per buffer");
+    for (int i = 0; i < NF; i++) *fp[i] = reinterpret_cast<float *>(base + off[i]);
+    int *ints = reinterpret_cast<int *>(base + off[NF]);
     m->pos_dev = ints;
     m->status = ints + 1;
     m->token = ints + 2;
@@ -354,7 +357,7 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     hipStream_t s = ctx->stream;
     if ((e = hipMemcpyAsync(m->norms, norms.data(), norms.size() * sizeof(float), hipMemcpyHostToDevice, s)) ||
         (e = hipMemcpyAsync(m->rope_cs, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, s)) ||
-        (e = hipMemsetAsync(ints, 0, 256, s)) || (e = hipStreamSynchronize(s)))
+        (e = hipMemsetAsync(ints, 0, int_bytes, s)) || (e = hipStreamSynchronize(s)))
         return cleanup(hip_fail(e, "decoder upload"));
     *out = m;
     return RCE_QMM_OK;

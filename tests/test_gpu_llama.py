@@ -95,19 +95,22 @@ def test_llama_unfused_forms(ctx):
 
 
 def test_llama_head_dim_128(ctx):
-    note("llama d_head 128, rope_dim 64, GQA 4:1")
+    """d_head 128: key splits of 32, so 40 positions merge two splits."""
+    note("llama d_head 128, rope_dim 64, GQA 4:1, 40 positions")
     c = tiny_cfg(d_model=512, n_q_heads=4, n_kv_heads=1, d_head=128, rope_dim=64, d_ff=768,
-                 rope_freq_base=500000.0)
+                 rope_freq_base=500000.0, context_length=48)
     W = make_weights(c, seed=25)
-    run_pair(ctx, W, Mode.EXACT, TOKENS[:6], 1e-5).close()
+    toks = [int(t) for t in np.random.default_rng(1).integers(0, c["vocab"], 40)]
+    run_pair(ctx, W, Mode.EXACT, toks, 1e-5).close()
 
 
 def test_llama_long_context(ctx):
-    """More than one key chunk (64 keys) in the attention kernel."""
-    note("llama 70 positions")
-    c = tiny_cfg(n_layers=1, context_length=80)
+    """Up to three key splits of 64 merged by the last-arriving block
+    (positions 64.. use the merge; the first 64 the reference's order)."""
+    note("llama 150 positions")
+    c = tiny_cfg(n_layers=1, context_length=160)
     W = make_weights(c, seed=26)
-    toks = [int(t) for t in np.random.default_rng(0).integers(0, c["vocab"], 70)]
+    toks = [int(t) for t in np.random.default_rng(0).integers(0, c["vocab"], 150)]
     run_pair(ctx, W, Mode.EXACT, toks, 1e-5).close()
 
 
