@@ -303,11 +303,14 @@ using ic = std::integral_constant<int, U>;
 // Plain GEMM: tiles == nullptr, row tile mt covers rows mt*BM .. of M.
 // Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows),
 // multiplied by wtab[e]; tiles at or past n_tiles[0] do nothing.
-template <class Fmt, int BM_>
+// EPI (GemmEpilogue) is what the block stores for an output element o with
+// f32 sum v: v (f32 out); binary16 silu(v); binary16 silu(aux[o]) * v.
+template <class Fmt, int BM_, int EPI>
 __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16 *__restrict__ A,
                                                  const int *__restrict__ gather, size_t M, uint32_t a_bytes,
-                                                 float *__restrict__ out, int m_tiles, const MoeTile *__restrict__ tiles,
-                                                 const int *__restrict__ n_tiles, const DevWeight *__restrict__ wtab) {
+                                                 void *__restrict__ out_v, const float *__restrict__ aux, int m_tiles,
+                                                 const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
+                                                 const DevWeight *__restrict__ wtab) {
     using T = Tile<BM_>;
     constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB;
     constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP, SC_BUF = T::SC_BUF;
@@ -620,7 +623,17 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int m = 32 * orb + 8 * rq + 4 * h + e;
-            if (m < rows && col < N) out[(m0 + m) * N + col] = sum[e];
+            if (m < rows && col < N) {
+                const size_t o = (m0 + m) * N + col;
+                if constexpr (EPI == GEPI_F32) {
+                    static_cast<float *>(out_v)[o] = sum[e];
+                } else if constexpr (EPI == GEPI_SILU_F16) {  // rce-qwen36-moe/src/lib.rs L459-461
+                    static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_ref(sum[e]);
+                } else {  // silu(g) * u, rce-qwen36-moe/src/lib.rs L667-676
+                    const float hv = silu_ref(aux[o]) * sum[e];
+                    static_cast<_Float16 *>(out_v)[o] = (_Float16)hv;
+                }
+            }
         }
     }
 }
@@ -630,12 +643,12 @@ __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__
     if (i < n) d[i] = (_Float16)s[i];
 }
 
-template <class Fmt, int BM>
+template <class Fmt, int BM, int EPI>
 hipError_t set_lds_attr() {
     static bool attr_set = false;  // per process; the attribute is per function
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt, BM>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Tile<BM>::LDS);
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt, BM, EPI>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, Tile<BM>::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
@@ -646,25 +659,44 @@ template <class Fmt, int BM>
 hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
     using T = Tile<BM>;
     const int m_tiles = (int)((M + T::BM - 1) / T::BM), n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
-    hipError_t e = set_lds_attr<Fmt, BM>();
+    hipError_t e = set_lds_attr<Fmt, BM, GEPI_F32>();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM>), dim3(m_tiles * n_tiles), dim3(NT), T::LDS, s, w, a, (const int *)nullptr,
-                       M, (uint32_t)(M * w.n_cols * 2), out, m_tiles, (const MoeTile *)nullptr, (const int *)nullptr,
-                       (const DevWeight *)nullptr);
+    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM, GEPI_F32>), dim3(m_tiles * n_tiles), dim3(NT), T::LDS, s, w, a,
+                       (const int *)nullptr, M, (uint32_t)(M * w.n_cols * 2), (void *)out, (const float *)nullptr,
+                       m_tiles, (const MoeTile *)nullptr, (const int *)nullptr, (const DevWeight *)nullptr);
+    return hipGetLastError();
+}
+
+template <class Fmt, int BM, int EPI>
+hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
+                              const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, void *out,
+                              const float *aux, hipStream_t s) {
+    using T = Tile<BM>;
+    const int n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
+    hipError_t e = set_lds_attr<Fmt, BM, EPI>();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM, EPI>), dim3(max_tiles * n_tiles), dim3(NT), T::LDS, s, w, a, gather, a_rows,
+                       (uint32_t)(a_rows * w.n_cols * 2), out, aux, max_tiles, tiles, n_tiles_dev, wtab);
     return hipGetLastError();
 }
 
 template <class Fmt, int BM>
-hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
-                              const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, float *out,
-                              hipStream_t s) {
-    using T = Tile<BM>;
-    const int n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
-    hipError_t e = set_lds_attr<Fmt, BM>();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM>), dim3(max_tiles * n_tiles), dim3(NT), T::LDS, s, w, a, gather, a_rows,
-                       (uint32_t)(a_rows * w.n_cols * 2), out, max_tiles, tiles, n_tiles_dev, wtab);
-    return hipGetLastError();
+hipError_t launch_grouped_epi(int epi, const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
+                              const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, void *out,
+                              const float *aux, hipStream_t s) {
+    switch (epi) {
+    case GEPI_F32:
+        return launch_fmt_grouped<Fmt, BM, GEPI_F32>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case GEPI_SILU_F16:
+        return launch_fmt_grouped<Fmt, BM, GEPI_SILU_F16>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out,
+                                                          aux, s);
+    case GEPI_SWIGLU_F16:
+        if (!aux) return hipErrorInvalidValue;
+        return launch_fmt_grouped<Fmt, BM, GEPI_SWIGLU_F16>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles,
+                                                            out, aux, s);
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
@@ -687,7 +719,7 @@ int gemm_tile_rows(size_t rows_hint) { return rows_hint <= 96 ? 64 : 128; }
 
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
-                                   int bm, float *out, hipStream_t s) {
+                                   int bm, int epi, void *out, const float *aux, hipStream_t s) {
     if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
     if (a_rows * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
         return hipErrorInvalidValue;
@@ -695,11 +727,12 @@ hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, co
     const bool q4k = w.dtype == T_Q4_K;
     if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
     if (bm == 64)
-        return q4k ? launch_fmt_grouped<Q4K, 64>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s)
-                   : launch_fmt_grouped<Q40, 64>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
+        return q4k ? launch_grouped_epi<Q4K, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
+                   : launch_grouped_epi<Q40, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     if (bm == 128)
-        return q4k ? launch_fmt_grouped<Q4K, 128>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s)
-                   : launch_fmt_grouped<Q40, 128>(w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, s);
+        return q4k ? launch_grouped_epi<Q4K, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
+                   : launch_grouped_epi<Q40, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux,
+                                                  s);
     return hipErrorInvalidValue;
 }
 

@@ -409,20 +409,10 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
     int *n_tiles = tok_of_slot + n_pairs;
     int *status = n_tiles + 1;
     MoeTile *tiles = reinterpret_cast<MoeTile *>(static_cast<char *>(ctx->moe_meta.p) + align_up(meta_ints * 4, 16));
-    HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, bm, offs, slot_of_pair, tok_of_slot,
-                             tiles, n_tiles, status, s));
     const int *n_slots = offs + n_expert;  // device count of slots with a valid expert
-
-    // stage buffers: expert outputs in slot order
-    if ((st = ensure(ctx, ctx->moe_h, n_pairs * d_ff * sizeof(float), s))) return st;
+    // expert outputs in slot order
     if ((st = ensure(ctx, ctx->moe_y, n_pairs * d_model * sizeof(float), s))) return st;
-    float *h = static_cast<float *>(ctx->moe_h.p);
     float *y = static_cast<float *>(ctx->moe_y.p);
-    float *u = nullptr;  // SwiGLU: the up products
-    if (w3) {
-        if ((st = ensure(ctx, ctx->moe_u, n_pairs * d_ff * sizeof(float), s))) return st;
-        u = static_cast<float *>(ctx->moe_u.p);
-    }
 
     if (mode == RCE_QMM_MODE_F16_MFMA) {
         // 2. expert tables (uploaded when the expert set changes)
@@ -442,22 +432,38 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
         }
         const DevWeight *wtab1 = static_cast<const DevWeight *>(ctx->moe_wtab.p), *wtab2 = wtab1 + n_expert;
         const DevWeight *wtab3 = wtab1 + 2 * n_expert;
-        // 3. x -> f16 once; W1 GEMM on the rows gathered per slot
+        // 3. the grouping, and x -> f16 in the same launch; W1 GEMM on the
+        // rows gathered per slot, storing f16 silu(W1 x) (SwiGLU: the gate
+        // products in f32, then the up GEMM stores f16 silu(g) * u)
         if ((st = ensure(ctx, ctx->moe_x, t_rows * d_model * 2, s))) return st;
         if ((st = ensure(ctx, ctx->moe_h16, n_pairs * d_ff * 2, s))) return st;
-        HIP_TRY(launch_f32_to_f16(x_dev, ctx->moe_x.p, t_rows * d_model, s));
-        HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm, h, s));
-        // 4. silu (times the up products) -> f16; W2 GEMM on the slots themselves
+        HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, bm, offs, slot_of_pair, tok_of_slot,
+                                 tiles, n_tiles, status, x_dev, ctx->moe_x.p, t_rows * d_model, s));
         if (w3) {
+            if ((st = ensure(ctx, ctx->moe_h, n_pairs * d_ff * sizeof(float), s))) return st;
+            float *g = static_cast<float *>(ctx->moe_h.p);
+            HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm,
+                                            GEPI_F32, g, nullptr, s));
             HIP_TRY(launch_gemm_f16_grouped(a1, wtab3, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm,
-                                            u, s));
-            HIP_TRY(launch_swiglu_slots_f16(h, u, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
+                                            GEPI_SWIGLU_F16, ctx->moe_h16.p, g, s));
         } else {
-            HIP_TRY(launch_silu_f16(h, ctx->moe_h16.p, n_slots, n_pairs, d_ff, s));
+            HIP_TRY(launch_gemm_f16_grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, tiles, n_tiles, max_tiles, bm,
+                                            GEPI_SILU_F16, ctx->moe_h16.p, nullptr, s));
         }
-        HIP_TRY(launch_gemm_f16_grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, tiles, n_tiles, max_tiles, bm, y, s));
+        // 4. W2 GEMM on the slots themselves
+        HIP_TRY(launch_gemm_f16_grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, tiles, n_tiles, max_tiles, bm,
+                                        GEPI_F32, y, nullptr, s));
     } else {
         if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
+        HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, bm, offs, slot_of_pair, tok_of_slot,
+                                 tiles, n_tiles, status, nullptr, nullptr, 0, s));
+        if ((st = ensure(ctx, ctx->moe_h, n_pairs * d_ff * sizeof(float), s))) return st;
+        float *h = static_cast<float *>(ctx->moe_h.p);
+        float *u = nullptr;  // SwiGLU: the up products
+        if (w3) {
+            if ((st = ensure(ctx, ctx->moe_u, n_pairs * d_ff * sizeof(float), s))) return st;
+            u = static_cast<float *>(ctx->moe_u.p);
+        }
         // The decode kernels take host row counts: read the grouping back.
         std::vector<int> hoffs(n_expert + 1), hstatus(1);
         HIP_TRY(hipMemcpyAsync(hoffs.data(), offs, hoffs.size() * 4, hipMemcpyDeviceToHost, s));

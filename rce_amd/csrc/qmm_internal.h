@@ -189,31 +189,33 @@ struct MoeTile {
 // offs[n_expert + 1], slot_of_pair[n_pairs] (-1: id out of range),
 // tok_of_slot[n_pairs], tiles[n_pairs / bm + n_expert] (bm-row pieces of
 // each expert's slots), n_tiles[1], status[1] (1: an id was out of range).
+// With x16 non-null the same launch also writes x16[i] = binary16(x[i]),
+// i < n_x.
 hipError_t launch_moe_group(const int32_t *ids, size_t n_pairs, int top_k, int n_expert, int bm, int *offs,
                             int *slot_of_pair, int *tok_of_slot, MoeTile *tiles, int *n_tiles, int *status,
-                            hipStream_t s);
+                            const float *x, void *x16, size_t n_x, hipStream_t s);
 // xg[s, :] = x[tok_of_slot[s], :] for s < n_slots (device count)
 hipError_t launch_gather_rows(const float *x, const int *tok_of_slot, const int *n_slots_dev, size_t max_slots,
                               size_t d, float *xg, hipStream_t s);
 hipError_t launch_silu_inplace(float *h, const int *n_slots_dev, size_t max_slots, size_t d, hipStream_t s);
-// o (binary16) = silu(h)
-hipError_t launch_silu_f16(const float *h, void *o, const int *n_slots_dev, size_t max_slots, size_t d,
-                           hipStream_t s);
 // SwiGLU experts: g = silu(g) * u over the first n_slots (device count) slots,
-// in place, or as binary16 into o.
+// in place.
 hipError_t launch_swiglu_slots(float *g, const float *u, const int *n_slots_dev, size_t max_slots, size_t d,
                                hipStream_t s);
-hipError_t launch_swiglu_slots_f16(const float *g, const float *u, void *o, const int *n_slots_dev, size_t max_slots,
-                                   size_t d, hipStream_t s);
 // out[t, :] = sum_j gate_w[t, j] * y[slot_of_pair[t * top_k + j], :], j in order, from +0.0
 hipError_t launch_moe_combine(const float *y, const int *slot_of_pair, const float *gate_w, size_t t_rows, int top_k,
                               size_t d, float *out, hipStream_t s);
+// What the grouped GEMM stores for output element o with f32 sum v:
+// v (f32 out), binary16 silu(v), or binary16 silu(aux[o]) * v (aux: the
+// f32 gate products of the same slots, SwiGLU).
+enum GemmEpilogue { GEPI_F32 = 0, GEPI_SILU_F16 = 1, GEPI_SWIGLU_F16 = 2 };
 // Grouped GEMM: for every tile (expert e, slots r0 ..): out[r0 + m, :] =
-// A[gather ? gather[r0 + m] : r0 + m, :] . wtab[e]^T.  `w` gives the dtype
-// and shape shared by all experts; wtab is a device array of DevWeight;
-// a_rows: rows of A (bounds the loads); max_tiles bounds n_tiles_dev[0].
+// epi(A[gather ? gather[r0 + m] : r0 + m, :] . wtab[e]^T).  `w` gives the
+// dtype and shape shared by all experts; wtab is a device array of
+// DevWeight; a_rows: rows of A (bounds the loads); max_tiles bounds
+// n_tiles_dev[0].
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
-                                   int bm, float *out, hipStream_t s);
+                                   int bm, int epi, void *out, const float *aux, hipStream_t s);
 
 }  // namespace rce_qmm

@@ -85,6 +85,8 @@ CASES = [
     (8, 256, 512, 3, 2, O.Q4_0),     # most experts get no token
     (4, 512, 768, 40, 1, O.Q4_0),    # top-1, ragged slots
     (4, 512, 1024, 24, 2, O.Q4_K),
+    (40, 256, 512, 50, 3, O.Q4_0),   # more experts than the single-scan grouping takes
+    (32, 256, 512, 300, 2, O.Q4_K),  # its largest expert count, several pairs per thread
 ]
 
 
