@@ -97,6 +97,9 @@ uint32_t rce_qmm_abi_version(void);
  * Replaces MetalQmmContext::new (rce-op-qmm-metal/src/lib.rs L46-52):
  * no GPU -> RCE_QMM_NO_DEVICE (the caller then stays on the CPU path). */
 rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out);
+/* Releases the caller's hold on the context.  Decoders made on it
+ * (rce_qmm_llama_create) hold it too: it is freed when the last of them is
+ * destroyed, so destroying the context first is safe. */
 void rce_qmm_context_destroy(rce_qmm_context *ctx);
 /* The hipStream_t the context launches on, as void*. */
 rce_qmm_status rce_qmm_context_stream(rce_qmm_context *ctx, void **stream);

@@ -8,6 +8,7 @@
 #include "qmm_internal.h"
 
 #include <algorithm>
+#include <atomic>
 #include <memory>
 #include <string>
 #include <vector>
@@ -57,6 +58,10 @@ struct Scratch {
 struct rce_qmm_context {
     int device = 0;
     hipStream_t stream = nullptr;
+    // Holders: the caller (until rce_qmm_context_destroy) and every decoder
+    // made on the context (until rce_qmm_llama_destroy); the last release
+    // frees it, so a decoder destroyed after its context stays valid.
+    std::atomic<int> refs{1};
     rce_qmm_abi::Scratch a_in, a_f32, out;
     rce_qmm_abi::Scratch a_f16;  // f32 activations rounded to f16 for the MFMA GEMM
     // grouped experts: grouping metadata, expert tables, stage buffers
@@ -73,6 +78,9 @@ struct rce_qmm_weight {
 };
 
 namespace rce_qmm_abi {
+
+// Drop one holder of the context (see rce_qmm_context::refs).
+void context_release(rce_qmm_context *ctx);
 
 inline rce_qmm_status set_device(int dev) {
     HIP_TRY(hipSetDevice(dev));

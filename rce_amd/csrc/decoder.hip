@@ -13,9 +13,9 @@
 //     logf / expf / sinf / cosf in the reference's expression order (the
 //     functions Rust's f32 methods call on Linux), so the rotation is the
 //     reference's bit for bit.
-//   * attention: the reference's key order and recurrence within each of
-//     four parallel runs of keys (up to 64 keys: one run, exactly the
-//     reference's order); longer contexts merge the runs in a fixed order;
+//   * attention: the reference's softmax-weighted sum of the values,
+//     evaluated with fixed-shape parallel reductions instead of its
+//     key-by-key recurrence (f32 reassociation; one key gives v exactly);
 //     exp is the device's expf (last-bit differences from the host libm).
 //   * silu: silu_ref (device expf).
 // This file is built with -ffp-contract=off: no multiply-add contraction.
@@ -65,55 +65,79 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
 }
 
 // Attention of one decode step: one block of NW waves per query head h;
-// kv head g = h / (n_q / n_kv) (rce-tinyllama L262-281).  Keys are cut into
-// splits of CH (64 for d_head 64, 32 for 128); wave w takes the contiguous
-// run of splits [w*ns/NW, (w+1)*ns/NW) of the ns the context needs.
-//  1. The block loads this position's q_h, k_g, v_g and the RoPE row into
-//     LDS and rotates q_h and k_g (rce-op-attn L115-151): pairs
-//     (i, i + half) -> (a c - b s, a s + b c).  The block of the first
-//     query head of each kv group appends k_g, v_g to the caches (every
-//     block uses its own copy of this position's k and v, so no block waits
-//     for another).
-//  2. Each wave runs fused_attend_head_window's recurrence (rce-op-attn
-//     L196-251) over its keys in order, one split at a time with all of a
-//     split's loads in flight together: lane j scores key j (sequential
-//     dot, times scale), the running maxima come from an exact prefix max,
-//     then out = out * alpha + beta * v_j and l = l * alpha + beta key by
-//     key with lane = dimension (a wave's first key gives out = v, l = 1, as
-//     the reference's first key does).
-//  3. One split (pos < CH): out *= 1 / l -- the reference's order exactly.
-//     Several: the waves' (m, l, out) are merged in wave order through LDS
-//     (M = max m_w; out = sum_w exp(m_w - M) out_w, l = sum_w exp(m_w - M)
-//     l_w; out *= 1 / l), a fixed order, so runs are bit-identical.
-constexpr int ATT_NW = 4;  // waves per head: one per SIMD, so no register spills
+// kv head g = h / (n_q / n_kv) (rce-tinyllama L262-281).
+//  1. The block loads this position's q_h, k_g, v_g into LDS (issued before
+//     the position is read: they do not depend on it), then the RoPE row,
+//     and rotates q_h and k_g (rce-op-attn L115-151): pairs (i, i + half) ->
+//     (a c - b s, a s + b c).  The block of the first query head of each kv
+//     group appends k_g, v_g to the caches (every block uses its own copy of
+//     this position's k and v, so no block waits for another).
+//  2. Wave w takes the keys [w*seq/NW, (w+1)*seq/NW) in runs of CH (64 for
+//     d_head 64, 32 for 128), all of a run's loads in flight together: lane
+//     j scores key j (the reference's sequential dot, times scale); the
+//     run's maximum and the sum of p_j = exp(s_j - m) are wave reductions
+//     of fixed shape; out[d] = sum_j p_j v_j[d] (lane = d, four partial sums
+//     added in a fixed order).  A wave's runs merge by rescaling with
+//     exp(m_old - m_new).
+//  3. The waves' (m, l, out) merge in wave order through LDS (M = max m_w;
+//     out = sum_w exp(m_w - M) out_w, l = sum_w exp(m_w - M) l_w), then
+//     out *= 1 / l.
+// This is the softmax-weighted sum that fused_attend_head_window
+// (rce-op-attn L196-251) folds key by key with its online recurrence,
+// evaluated in parallel: every reduction has a fixed shape (run-to-run
+// bit-identical), and the result differs from the reference's by f32
+// reassociation only (one key: out = v exactly, as the reference's first
+// key gives).
+// Waves per head: one per SIMD.  A run keeps a key row, a value column and
+// q in registers (about 200 for d_head 64), so the kernel asks for one wave
+// per SIMD and the whole register file: a launch has n_q blocks at most.
+constexpr int ATT_NW = 4;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
 
 template <int DH>
-__global__ __launch_bounds__(64 * ATT_NW) void k_attention(const float *__restrict__ qkv,
+__global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attention(const float *__restrict__ qkv,
                                                            const float *__restrict__ rope_cs,
                                                            float *__restrict__ k_cache, float *__restrict__ v_cache,
                                                            const int *__restrict__ pos_p, int ctx_len, int n_q,
                                                            int n_kv, int rope_dim, float scale,
                                                            float *__restrict__ att) {
     constexpr int DPL = DH / 64;    // dimensions per lane
-    constexpr int CH = 4096 / DH;   // keys per split (64 or 32)
+    constexpr int CH = 4096 / DH;   // keys per run (64 or 32)
     constexpr int R4 = DH / 4;      // float4 pieces of a row
     __shared__ float qs[DH], ks[DH], vs[DH], cs[DH];
     __shared__ float mo[ATT_NW][DH + 2];  // each wave's out[DH], m, l
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
-    const int pos = pos_p[0];
-    if (pos < 0 || pos >= ctx_len) return;  // the step's last kernel reports it
-    const int seq = pos + 1, ns = (seq + CH - 1) / CH;
-    const int s_lo = wave * ns / ATT_NW, s_hi = (wave + 1) * ns / ATT_NW;  // this wave's splits
+    // the wave index in a scalar register: the run bounds below are then
+    // wave-uniform and their branches scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = blockIdx.x;
     const int qpk = n_q / n_kv, g = h / qpk;
     const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH;
-    const int half = rope_dim / 2;
+    for (int i = tid; i < DH; i += 64 * ATT_NW) {  // independent of the position
+        qs[i] = qkv[(size_t)h * DH + i];
+        ks[i] = qkv[qd + (size_t)g * DH + i];
+        vs[i] = qkv[qd + kvd + (size_t)g * DH + i];
+    }
+    const int pos = pos_p[0];
+    if (pos < 0 || pos >= ctx_len) return;  // the whole block; the step's last kernel reports it
+    const int seq = pos + 1, half = rope_dim / 2;
+    for (int i = tid; i < 2 * half; i += 64 * ATT_NW) cs[i] = rope_cs[(size_t)pos * half * 2 + i];
+    const int j0 = (int)((long)wave * seq / ATT_NW), j1 = (int)((long)(wave + 1) * seq / ATT_NW);
     const float *kbase = k_cache + (size_t)g * DH, *vbase = v_cache + (size_t)g * DH;
 
     float4 kv[R4];
     float vv[CH][DPL];
-    // A split's cached keys / values, every load unconditional: rows at or
-    // past pos read row 0 (always in range; replaced or unused).
-    auto load_split = [&](int c0) {
+    float vcur[DPL];  // this position's value column (not in the cache yet)
+#pragma unroll
+    for (int d = 0; d < DPL; d++) vcur[d] = qkv[qd + kvd + (size_t)g * DH + lane + 64 * d];
+    // A run's cached keys / values, every load unconditional: rows at or
+    // past pos read row 0 (always in range).  Value rows past pos become 0
+    // and row pos this position's values, so every value row is finite;
+    // key rows at or past pos are unused (the current key comes from LDS).
+    auto load_run = [&](int c0) {
         const int r = c0 + lane;
         const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(r < pos ? r : 0) * kvd);
 #pragma unroll
@@ -123,18 +147,13 @@ __global__ __launch_bounds__(64 * ATT_NW) void k_attention(const float *__restri
             const int rj = c0 + j;
             const float *vp = vbase + (size_t)(rj < pos ? rj : 0) * kvd;
 #pragma unroll
-            for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
+            for (int d = 0; d < DPL; d++) {
+                const float x = vp[lane + 64 * d];
+                vv[j][d] = rj < pos ? x : (rj == pos ? vcur[d] : 0.0f);
+            }
         }
     };
-    // one round of loads: this position's vectors (spread over the block)
-    // and the wave's first split
-    for (int i = tid; i < DH; i += 64 * ATT_NW) {
-        qs[i] = qkv[(size_t)h * DH + i];
-        ks[i] = qkv[qd + (size_t)g * DH + i];
-        vs[i] = qkv[qd + kvd + (size_t)g * DH + i];
-        cs[i] = i < 2 * half ? rope_cs[(size_t)pos * half * 2 + i] : 0.0f;
-    }
-    if (s_lo < s_hi) load_split(s_lo * CH);
+    if (j0 < j1) load_run(j0);
     __syncthreads();
     for (int i = tid; i < half; i += 64 * ATT_NW) {
         const float c = cs[2 * i], s = cs[2 * i + 1];
@@ -161,25 +180,16 @@ __global__ __launch_bounds__(64 * ATT_NW) void k_attention(const float *__restri
 #pragma unroll
     for (int d = 0; d < DPL; d++) o[d] = 0.0f;
     float m = -INFINITY, l = 0.0f;
-    if (s_lo < s_hi) {
+    if (j0 < j1) {
         float q[DH];  // every lane needs all of q for its key's dot
 #pragma unroll
         for (int i = 0; i < DH; i++) q[i] = qs[i];
-        for (int sp = s_lo; sp < s_hi; sp++) {
-            const int c0 = sp * CH, n = min(CH, seq - c0);
-            if (sp > s_lo) load_split(c0);
+        for (int c0 = j0; c0 < j1; c0 += CH) {
+            const int n = min(CH, j1 - c0);
+            if (c0 > j0) load_run(c0);
             if (c0 + lane == pos) {  // this lane's key is the current position
 #pragma unroll
                 for (int i = 0; i < R4; i++) kv[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
-            }
-            if (pos - c0 < CH) {  // the split holds the current position: its value row
-                const int jp = pos - c0;
-#pragma unroll
-                for (int j = 0; j < CH; j++)
-                    if (j == jp) {
-#pragma unroll
-                        for (int d = 0; d < DPL; d++) vv[j][d] = vs[lane + 64 * d];
-                    }
             }
             float sc = -INFINITY;
             if (lane < n) {
@@ -197,60 +207,46 @@ __global__ __launch_bounds__(64 * ATT_NW) void k_attention(const float *__restri
                 }
                 sc = dot * scale;
             }
-            // running maxima: inclusive prefix max over the split, after m
-            // (lanes past n hold -inf and come after every valid lane)
-            float pm = sc;
+            const float m_new = fmaxf(m, wave_max(sc));  // finite: the run has a key
+            const float corr = expf(m - m_new);           // 0 for the wave's first run
+            const float p = lane < n ? expf(sc - m_new) : 0.0f;
+            const float lc = l * corr;
+            l = lc + wave_sum(p);
+            float a[4][DPL];
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float t = __shfl_up(pm, off);
-                if (lane >= off) pm = fmaxf(pm, t);
-            }
-            const float m_incl = fmaxf(m, pm);
-            float m_prev = __shfl_up(m_incl, 1);
-            if (lane == 0) m_prev = m;
-            // a wave's first key: exp(-inf) = 0 and exp(0) = 1, so out = v, l = 1
-            const float alpha = lane < n ? expf(m_prev - m_incl) : 1.0f;
-            const float beta = lane < n ? expf(sc - m_incl) : 0.0f;
-            m = __shfl(m_incl, n - 1);
-            // the recurrence in key order; key j's factors broadcast from lane j
+            for (int k = 0; k < 4; k++)
 #pragma unroll
-            for (int j = 0; j < CH; j++) {
-                if (j < n) {
-                    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), j));
-                    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, beta), j));
-                    if (c0 + j == 0) {  // the reference's first key: out = 0 + 1 * v, l = 1
+                for (int d = 0; d < DPL; d++) a[k][d] = 0.0f;
+            // p = 0 and finite value rows past the run's keys: whole groups of
+            // four.  A constant trip count with a uniform test per group (not
+            // a break), so the loop unrolls and vv stays in registers.
 #pragma unroll
-                        for (int d = 0; d < DPL; d++) {
-                            const float t = 1.0f * vv[j][d];
-                            o[d] = o[d] + t;
-                        }
-                        l = 1.0f;
-                    } else {
+            for (int j = 0; j < CH; j += 4) {
+                if (j >= n) continue;
 #pragma unroll
-                        for (int d = 0; d < DPL; d++) {
-                            const float t1 = o[d] * a, t2 = b * vv[j][d];
-                            o[d] = t1 + t2;
-                        }
-                        const float la = l * a;
-                        l = la + b;
+                for (int k = 0; k < 4; k++) {
+                    const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), j + k));
+#pragma unroll
+                    for (int d = 0; d < DPL; d++) {
+                        const float t = pj * vv[j + k][d];
+                        a[k][d] = a[k][d] + t;
                     }
                 }
             }
+#pragma unroll
+            for (int d = 0; d < DPL; d++) {
+                const float s01 = a[0][d] + a[1][d], s23 = a[2][d] + a[3][d];
+                const float sv = s01 + s23, oc = o[d] * corr;
+                o[d] = oc + sv;
+            }
+            m = m_new;
         }
     }
     float *out = att + (size_t)h * DH;
-    if (ns == 1) {  // the single wave that had the keys finishes as the reference does
-        if (s_lo < s_hi) {
-            const float inv = 1.0f / l;
-#pragma unroll
-            for (int d = 0; d < DPL; d++) out[lane + 64 * d] = o[d] * inv;
-        }
-        return;
-    }
 #pragma unroll
     for (int d = 0; d < DPL; d++) mo[wave][lane + 64 * d] = o[d];
     if (lane == 0) {
-        mo[wave][DH] = s_lo < s_hi ? m : -INFINITY;
+        mo[wave][DH] = m;  // -inf: a wave without keys
         mo[wave][DH + 1] = l;
     }
     __syncthreads();

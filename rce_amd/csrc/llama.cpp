@@ -14,8 +14,9 @@
 //     h = silu(Wg n) * (Wu n),          FX_SWIGLU | FX_NORM when gate and up
 //         n = rms_norm(x)               share format
 //     x = x + Wd h                      FX_RESIDUAL
-//   rms_norm(x, output_norm) -> xn      also advances the position
-//   logits = lm_head xn
+//   logits = lm_head rms_norm(x, output_norm)   one FX_SEG | FX_NORM launch
+//                                       that also advances the position (or
+//                                       a separate rms_norm that does)
 // Every kernel of a step reads the position from pos (device memory), so
 // the recorded graph replays for any position.  Linears whose format has no
 // fused form run as a separate rms_norm and plain GEMVs followed by the
@@ -41,6 +42,7 @@ struct rce_qmm_llama {
         bool qkv_seg = false, wo_res = false, ffn_swiglu = false, down_res = false;
         bool qkv_norm = false, ffn_norm = false;  // the fused forms also form rms_norm
     };
+    bool head_norm = false;  // the head GEMV forms the output rms_norm and advances the position
     std::vector<Layer> layers;
     // device memory (one allocation)
     void *mem = nullptr;
@@ -92,6 +94,16 @@ rce_qmm_status check_linear(const char *name, size_t il, const rce_qmm_weight *w
 }
 
 bool fx_ok(const DevWeight &w, int mode) { return gemv_fx_supports(w.dtype, w.n_cols, mode); }
+
+// Unwritten KV-cache rows hold quiet NaNs (at creation and after a reset),
+// so a kernel that lets a row past the position into a result shows it
+// as NaN instead of depending on what the memory held.
+hipError_t poison_caches(rce_qmm_llama *m, hipStream_t s) {
+    const size_t n = m->cfg.n_layers * m->cache_layer();
+    hipError_t e = hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(m->kc), 0x7fc00000, n, s);
+    if (e == hipSuccess) e = hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(m->vc), 0x7fc00000, n, s);
+    return e;
+}
 
 // The step's kernels after the input embedding is in x.
 rce_qmm_status enqueue_body(rce_qmm_llama *m, float *logits, hipStream_t s) {
@@ -160,8 +172,21 @@ rce_qmm_status enqueue_body(rce_qmm_llama *m, float *logits, hipStream_t s) {
             HIP_TRY(launch_add_inplace(m->x, m->o, dm, s));
         }
     }
-    HIP_TRY(norm(m->out_norm(), m->pos_dev));  // the step's last reader of pos advances it
-    HIP_TRY(launch_gemv(m->head, m->xn, 1, logits, m->mode, s));
+    if (m->head_norm) {  // the step's last kernel advances the position
+        FxLaunch f;
+        f.kind = FX_SEG | FX_NORM;
+        f.w[0] = m->head;
+        f.out[0] = logits;
+        f.norm_w = m->out_norm();
+        f.eps = c.eps;
+        f.pos = m->pos_dev;
+        f.status = m->status;
+        f.ctx_len = ctx_len;
+        HIP_TRY(launch_gemv_fx(f, m->x, m->mode, s));
+    } else {
+        HIP_TRY(norm(m->out_norm(), m->pos_dev));  // the step's last reader of pos advances it
+        HIP_TRY(launch_gemv(m->head, m->xn, 1, logits, m->mode, s));
+    }
     return RCE_QMM_OK;
 }
 
@@ -268,12 +293,15 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     rce_qmm_llama *m = new (std::nothrow) rce_qmm_llama();
     if (!m) return fail(RCE_QMM_OUT_OF_MEMORY, "decoder object");
     m->ctx = ctx;
+    ctx->refs.fetch_add(1);  // released by rce_qmm_llama_destroy
     m->cfg = c;
     m->mode = md;
     if (const char *g = std::getenv("RCE_QMM_LLAMA_GRAPH")) m->eager = g[0] == '0';
     auto keep = [&](const rce_qmm_weight *w) { m->keep.push_back(w->alloc); return w->dw; };
     m->embd = keep(token_embd);
     m->head = keep(lm_head);
+    m->head_norm = gemv_fx_supports(m->head.dtype, m->head.n_cols, md, true) &&
+                   std::getenv("RCE_QMM_LLAMA_NORM_KERNEL") == nullptr;
     for (size_t il = 0; il < c.n_layers; il++) {
         const rce_qmm_llama_block &b = blocks[il];
         rce_qmm_llama::Layer L;
@@ -357,7 +385,7 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     hipStream_t s = ctx->stream;
     if ((e = hipMemcpyAsync(m->norms, norms.data(), norms.size() * sizeof(float), hipMemcpyHostToDevice, s)) ||
         (e = hipMemcpyAsync(m->rope_cs, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, s)) ||
-        (e = hipMemsetAsync(ints, 0, int_bytes, s)) || (e = hipStreamSynchronize(s)))
+        (e = poison_caches(m, s)) || (e = hipMemsetAsync(ints, 0, int_bytes, s)) || (e = hipStreamSynchronize(s)))
         return cleanup(hip_fail(e, "decoder upload"));
     *out = m;
     return RCE_QMM_OK;
@@ -372,7 +400,9 @@ void rce_qmm_llama_destroy(rce_qmm_llama *m) {
     if (m->h_token) (void)hipHostFree(m->h_token);
     if (m->h_status) (void)hipHostFree(m->h_status);
     if (m->h_logits) (void)hipHostFree(m->h_logits);
+    rce_qmm_context *ctx = m->ctx;
     delete m;
+    context_release(ctx);
 }
 
 rce_qmm_status rce_qmm_llama_reset(rce_qmm_llama *m) {
@@ -380,6 +410,7 @@ rce_qmm_status rce_qmm_llama_reset(rce_qmm_llama *m) {
     rce_qmm_status st = set_device(m->ctx->device);
     if (st) return st;
     hipStream_t s = m->ctx->stream;
+    HIP_TRY(poison_caches(m, s));
     HIP_TRY(hipMemsetAsync(m->pos_dev, 0, 2 * sizeof(int), s));  // pos, status
     HIP_TRY(hipStreamSynchronize(s));
     m->pos = 0;

@@ -161,7 +161,13 @@ rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out) {
 }
 
 void rce_qmm_context_destroy(rce_qmm_context *ctx) {
-    if (!ctx) return;
+    if (ctx) context_release(ctx);
+}
+
+}  // extern "C"
+
+void rce_qmm_abi::context_release(rce_qmm_context *ctx) {
+    if (ctx->refs.fetch_sub(1) != 1) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16, &ctx->moe_meta, &ctx->moe_wtab, &ctx->moe_x,
@@ -170,6 +176,8 @@ void rce_qmm_context_destroy(rce_qmm_context *ctx) {
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
+
+extern "C" {
 
 rce_qmm_status rce_qmm_context_stream(rce_qmm_context *ctx, void **stream) {
     if (!ctx || !stream) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");

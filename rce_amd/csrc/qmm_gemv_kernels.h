@@ -697,6 +697,11 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     const int RT = P * RPL;
     unsigned bx = blockIdx.x;
     if constexpr (KIND == FX_SEG) {  // block-uniform choice of the segment
+        if (fx.pos && bx == 0 && tid == 0) {  // the step's last kernel: advance the position
+            const int p = fx.pos[0];
+            if (p >= fx.ctx_len) fx.status[0] = 2;
+            fx.pos[0] = p + 1;
+        }
         if (bx >= fx.blk3) { w = fx.w3; out = fx.out3; bx -= fx.blk3; }
         else if (bx >= fx.blk2) { w = fx.w2; out = fx.out2; bx -= fx.blk2; }
     }
@@ -863,6 +868,10 @@ hipError_t launch_as_fx(const FxLaunch &f, int U, const float *a, hipStream_t s)
     GemvFx fx{};
     fx.norm_w = f.norm_w;
     fx.eps = f.eps;
+    if (f.pos && ((f.kind & 7) != FX_SEG || !f.status)) return hipErrorInvalidValue;
+    fx.pos = f.pos;
+    fx.status = f.status;
+    fx.ctx_len = f.ctx_len;
     if ((f.kind & FX_NORM) && (f.w[0].n_cols / 8 > (size_t)(2 * NT) || !f.norm_w)) return hipErrorInvalidValue;
     unsigned blocks = 0;
     switch (f.kind & 7) {

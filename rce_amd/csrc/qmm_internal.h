@@ -92,6 +92,9 @@ struct GemvFx {
     const float *res;      // FX_RESIDUAL
     const float *norm_w;   // FX_NORM
     float eps;             // FX_NORM
+    int *pos;              // FX_SEG, non-null: ends a decode step (see FxLaunch)
+    int *status;
+    int ctx_len;
 };
 
 struct FxLaunch {
@@ -102,6 +105,12 @@ struct FxLaunch {
     const float *res = nullptr;
     const float *norm_w = nullptr;
     float eps = 0.0f;
+    // FX_SEG: when pos is given, one thread also ends a decode step, as
+    // launch_rms_norm does with pos (status[0] = 2 if pos[0] >= ctx_len,
+    // then pos[0] += 1); no other kernel of the step may follow that reads pos.
+    int *pos = nullptr;
+    int *status = nullptr;
+    int ctx_len = 0;
 };
 
 // Whether the fused forms exist for (dtype, n_cols, mode); with_norm: also

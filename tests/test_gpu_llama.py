@@ -95,7 +95,7 @@ def test_llama_unfused_forms(ctx):
 
 
 def test_llama_head_dim_128(ctx):
-    """d_head 128: key splits of 32, so 40 positions merge two splits."""
+    """d_head 128: runs of 32 keys per wave."""
     note("llama d_head 128, rope_dim 64, GQA 4:1, 40 positions")
     c = tiny_cfg(d_model=512, n_q_heads=4, n_kv_heads=1, d_head=128, rope_dim=64, d_ff=768,
                  rope_freq_base=500000.0, context_length=48)
@@ -105,8 +105,8 @@ def test_llama_head_dim_128(ctx):
 
 
 def test_llama_long_context(ctx):
-    """Up to three key splits of 64 merged by the last-arriving block
-    (positions 64.. use the merge; the first 64 the reference's order)."""
+    """150 positions: each wave's keys span several 64-key runs (merged by
+    rescaling), and the four waves' results merge in LDS."""
     note("llama 150 positions")
     c = tiny_cfg(n_layers=1, context_length=160)
     W = make_weights(c, seed=26)
@@ -185,3 +185,17 @@ def test_llama_separate_norm_and_eager_paths(ctx, monkeypatch):
         a, b = graph.forward_logits(t), eager.forward_logits(t)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     graph.close(); eager.close()
+
+
+def test_llama_outlives_its_context():
+    """A decoder destroyed after its context (as pytest's kept tracebacks do
+    at exit): the decoder holds the context until it is destroyed."""
+    note("llama destroyed after its context")
+    c2 = rce_amd.Context(0)
+    W = make_weights(tiny_cfg(n_layers=1), seed=31)
+    dev = device_model(c2, W, Mode.EXACT)
+    first = dev.forward_logits(5)
+    c2.close()
+    again = dev.forward_logits(6)  # the context is still held by the decoder
+    assert np.all(np.isfinite(first)) and np.all(np.isfinite(again))
+    dev.close()
