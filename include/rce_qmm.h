@@ -43,7 +43,9 @@
 extern "C" {
 #endif
 
-#define RCE_QMM_ABI_VERSION 1u
+/* 2: GGUF files (rce_qmm_gguf_*, rce_qmm_weight_from_gguf) and the
+ * NOT_FOUND / PARSE_ERROR / IO_ERROR statuses, added to version 1. */
+#define RCE_QMM_ABI_VERSION 2u
 
 typedef enum rce_qmm_status {
     RCE_QMM_OK = 0,
@@ -53,7 +55,10 @@ typedef enum rce_qmm_status {
     RCE_QMM_NO_DEVICE = 4,
     RCE_QMM_HIP_ERROR = 5,
     RCE_QMM_OUT_OF_MEMORY = 6,
-    RCE_QMM_INTERNAL = 7
+    RCE_QMM_INTERNAL = 7,
+    RCE_QMM_NOT_FOUND = 8,    /* a tensor or metadata key the file does not hold */
+    RCE_QMM_PARSE_ERROR = 9,  /* not a GGUF v2/v3 file, or a malformed one */
+    RCE_QMM_IO_ERROR = 10     /* the file could not be opened or mapped */
 } rce_qmm_status;
 
 /* GGUF type tags, as GgufDtype::to_u32 (rce-ingest-gguf/src/parser.rs
@@ -284,6 +289,55 @@ rce_qmm_status rce_qmm_llama_forward_token_dev(rce_qmm_llama *m, const int32_t *
 /* Wait for the decoder's work and report (then clear) an error found on the
  * device since the last check: RCE_QMM_BAD_SHAPE for a token id out of range. */
 rce_qmm_status rce_qmm_llama_check(rce_qmm_llama *m);
+
+/* ---- GGUF files (rce-ingest-gguf) ---------------------------------------- */
+
+/* A parsed GGUF v2/v3 file: header, metadata and tensor infos
+ * (GgufFile, parser.rs L431-446).  Strings and value bytes handed out
+ * below stay valid until rce_qmm_gguf_close. */
+typedef struct rce_qmm_gguf rce_qmm_gguf;
+
+/* GgufFile::parse (parser.rs L446-551) over the caller's bytes, which must
+ * outlive the handle.  Never reads tensor data.  RCE_QMM_PARSE_ERROR with
+ * the reference's error text for a bad magic, a version outside 2..=3, a
+ * truncated file, invalid UTF-8, an unknown value type or more than 8
+ * dimensions. */
+rce_qmm_status rce_qmm_gguf_parse(const uint8_t *bytes, size_t len, rce_qmm_gguf **out);
+/* mmap_load_sequential + GgufFile::parse (mmap.rs, parser.rs L446): the
+ * file is mapped read-only for the handle's lifetime; RCE_QMM_IO_ERROR
+ * when it cannot be opened or mapped. */
+rce_qmm_status rce_qmm_gguf_open(const char *path, rce_qmm_gguf **out);
+void rce_qmm_gguf_close(rce_qmm_gguf *g);
+/* version, tensor and metadata counts, data_offset (absolute start of the
+ * tensor data: the end of the infos padded to alignment) and alignment
+ * (general.alignment if U32/U64, else 32) (GgufFile fields, L431-445). */
+rce_qmm_status rce_qmm_gguf_header(const rce_qmm_gguf *g, uint32_t *version, size_t *n_tensors, size_t *n_metadata,
+                                   uint64_t *data_offset, uint64_t *alignment);
+/* Metadata entry i (GgufMetadata): key, value type tag (GGUF_TYPE_*,
+ * parser.rs L187-199) and the value's bytes as encoded in the file (little
+ * endian; strings and arrays with their length prefixes). */
+rce_qmm_status rce_qmm_gguf_metadata(const rce_qmm_gguf *g, size_t i, const char **key, uint32_t *type,
+                                     const uint8_t **value, size_t *value_len);
+/* The first metadata entry with this key (get_metadata, L553);
+ * RCE_QMM_NOT_FOUND if none. */
+rce_qmm_status rce_qmm_gguf_find_metadata(const rce_qmm_gguf *g, const char *key, size_t *index);
+/* Tensor info i (GgufTensorInfo, L404-418): name, dims (ne0 first; dims
+ * must hold 8), GGUF dtype tag, offset relative to data_offset, and its
+ * size in the file (tensor_byte_size, dequant.rs L18-60; 0 for dtypes
+ * with no size rule; tag 42 sized as STQ1_0 in hunyuan-dense files). */
+rce_qmm_status rce_qmm_gguf_tensor(const rce_qmm_gguf *g, size_t i, const char **name, uint32_t *ndim, uint64_t *dims,
+                                   uint32_t *dtype, uint64_t *offset, uint64_t *nbytes);
+rce_qmm_status rce_qmm_gguf_find_tensor(const rce_qmm_gguf *g, const char *name, size_t *index);
+/* QuantWeight::from_gguf (rce-op-qmm/src/lib.rs L173-209): the tensor
+ * `name` as a device-resident weight of the declared [n_rows, n_cols]
+ * (n_rows * n_cols must equal the tensor's element count, and its bytes
+ * must lie inside the file), then as rce_qmm_weight_from_bytes.  The
+ * handle can be closed afterwards: the weight holds its own device copy. */
+rce_qmm_status rce_qmm_weight_from_gguf(rce_qmm_context *ctx, const rce_qmm_gguf *g, const char *name, size_t n_rows,
+                                        size_t n_cols, rce_qmm_weight **out);
+/* read_tensor_f32 (dequant.rs L85-112) for F32, F16 and BF16 tensors (norm
+ * weights): n must equal the element count. */
+rce_qmm_status rce_qmm_gguf_read_f32(const rce_qmm_gguf *g, const char *name, float *out, size_t n);
 
 /* ---- device memory helpers (for callers without a HIP runtime) ---------- */
 

@@ -44,6 +44,16 @@ SIGNATURES = {
     "rce_qmm_llama_forward_embedding": (STATUS, [P, P, P]),
     "rce_qmm_llama_forward_token_dev": (STATUS, [P, P, P, P]),
     "rce_qmm_llama_check": (STATUS, [P]),
+    "rce_qmm_gguf_parse": (STATUS, [P, S, P]),
+    "rce_qmm_gguf_open": (STATUS, [ctypes.c_char_p, P]),
+    "rce_qmm_gguf_close": (None, [P]),
+    "rce_qmm_gguf_header": (STATUS, [P, P, P, P, P, P]),
+    "rce_qmm_gguf_metadata": (STATUS, [P, S, P, P, P, P]),
+    "rce_qmm_gguf_find_metadata": (STATUS, [P, ctypes.c_char_p, P]),
+    "rce_qmm_gguf_tensor": (STATUS, [P, S, P, P, P, P, P, P]),
+    "rce_qmm_gguf_find_tensor": (STATUS, [P, ctypes.c_char_p, P]),
+    "rce_qmm_weight_from_gguf": (STATUS, [P, P, ctypes.c_char_p, S, S, P]),
+    "rce_qmm_gguf_read_f32": (STATUS, [P, ctypes.c_char_p, P, S]),
     "rce_qmm_dev_alloc": (STATUS, [P, S, P]),
     "rce_qmm_dev_free": (STATUS, [P, P]),
     "rce_qmm_memcpy_h2d": (STATUS, [P, P, P, S]),

@@ -133,6 +133,9 @@ const char *rce_qmm_status_str(rce_qmm_status s) {
     case RCE_QMM_HIP_ERROR: return "hip error";
     case RCE_QMM_OUT_OF_MEMORY: return "out of memory";
     case RCE_QMM_INTERNAL: return "internal error";
+    case RCE_QMM_NOT_FOUND: return "not found";
+    case RCE_QMM_PARSE_ERROR: return "parse error";
+    case RCE_QMM_IO_ERROR: return "i/o error";
     }
     return "unknown status";
 }

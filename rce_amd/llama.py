@@ -21,7 +21,7 @@ import numpy as np
 from ._lib import check, lib
 from .qmm import Context, Mode, QmmError, QuantWeight
 
-__all__ = ["TinyLlamaConfig", "TinyLlamaBlock", "TinyLlamaWeights", "TinyLlamaRuntime"]
+__all__ = ["TinyLlamaConfig", "TinyLlamaBlock", "TinyLlamaWeights", "TinyLlamaRuntime", "load_weights"]
 
 
 @dataclass
@@ -37,6 +37,46 @@ class TinyLlamaConfig:
     d_ff: int
     context_length: int
     eps: float
+
+    @classmethod
+    def from_gguf(cls, gguf) -> "TinyLlamaConfig":
+        """TinyLlamaConfig::from_gguf (rce-tinyllama/src/lib.rs L44-89): the
+        llama.* metadata of a GgufFile (rce_amd.gguf), with the reference's
+        defaults and fallbacks; QmmError(BAD_SHAPE) naming a missing key."""
+        arch = gguf.get_string("general.architecture")
+        if arch is None:
+            raise QmmError(2, "missing general.architecture")
+        if arch != "llama":
+            raise QmmError(2, f"expected llama, got {arch}")
+        u32 = lambda k: gguf.get_u32(f"llama.{k}")  # noqa: E731
+        f32 = lambda k: gguf.get_f32(f"llama.{k}")  # noqa: E731
+
+        def need(k):
+            v = u32(k)
+            if v is None:
+                raise QmmError(2, k)
+            return v
+
+        d_model = need("embedding_length")
+        vocab = u32("vocab_size")
+        if vocab is None:  # the token embedding's second dimension
+            t = gguf.tensor("token_embd.weight")
+            vocab = t.dims[1] if t is not None and len(t.dims) > 1 else None
+        if vocab is None:
+            raise QmmError(2, "vocab_size")
+        n_layers = need("block_count")
+        n_q = need("attention.head_count")
+        n_kv = u32("attention.head_count_kv")
+        n_kv = n_q if n_kv is None else n_kv
+        d_head = d_model // n_q
+        rope_dim = u32("rope.dimension_count")
+        rope_base = f32("rope.freq_base")
+        ctx_len = u32("context_length")
+        eps = f32("attention.layer_norm_rms_epsilon")
+        return cls(d_model=d_model, vocab=vocab, n_layers=n_layers, n_q_heads=n_q, n_kv_heads=n_kv, d_head=d_head,
+                   rope_dim=d_head if rope_dim is None else rope_dim,
+                   rope_freq_base=10000.0 if rope_base is None else rope_base, d_ff=need("feed_forward_length"),
+                   context_length=2048 if ctx_len is None else ctx_len, eps=1e-5 if eps is None else eps)
 
     def n_embd_q(self) -> int:
         return self.n_q_heads * self.d_head
@@ -64,6 +104,40 @@ class TinyLlamaWeights:
     output_norm: np.ndarray
     lm_head: QuantWeight  # separate output.weight (not tied)
     blocks: list
+
+
+def load_weights(ctx: Context, gguf, cfg: TinyLlamaConfig) -> TinyLlamaWeights:
+    """load_weights (rce-tinyllama/src/lib.rs L108-145): every linear as a
+    device-resident QuantWeight (QuantWeight::from_gguf), the norms read as
+    f32 (read_tensor_f32); errors name the tensor."""
+    def qw(name, n_rows, n_cols):
+        try:
+            return QuantWeight.from_gguf(ctx, gguf, name, n_rows, n_cols)
+        except QmmError as e:
+            raise QmmError(e.status, f"{name}: {e}") from None
+
+    def f32n(name):
+        try:
+            return gguf.read_tensor_f32(name)
+        except QmmError as e:
+            raise QmmError(e.status, f"{name}: {e}") from None
+
+    token_embd = qw("token_embd.weight", cfg.vocab, cfg.d_model)
+    output_norm = f32n("output_norm.weight")
+    lm_head = qw("output.weight", cfg.vocab, cfg.d_model)
+    blocks = []
+    for il in range(cfg.n_layers):
+        bn = f"blk.{il}"
+        blocks.append(TinyLlamaBlock(
+            attn_norm=f32n(f"{bn}.attn_norm.weight"), ffn_norm=f32n(f"{bn}.ffn_norm.weight"),
+            wq=qw(f"{bn}.attn_q.weight", cfg.n_embd_q(), cfg.d_model),
+            wk=qw(f"{bn}.attn_k.weight", cfg.n_embd_kv(), cfg.d_model),
+            wv=qw(f"{bn}.attn_v.weight", cfg.n_embd_kv(), cfg.d_model),
+            wo=qw(f"{bn}.attn_output.weight", cfg.d_model, cfg.n_embd_q()),
+            ffn_gate=qw(f"{bn}.ffn_gate.weight", cfg.d_ff, cfg.d_model),
+            ffn_up=qw(f"{bn}.ffn_up.weight", cfg.d_ff, cfg.d_model),
+            ffn_down=qw(f"{bn}.ffn_down.weight", cfg.d_model, cfg.d_ff)))
+    return TinyLlamaWeights(token_embd=token_embd, output_norm=output_norm, lm_head=lm_head, blocks=blocks)
 
 
 class _Cfg(ctypes.Structure):
@@ -108,6 +182,17 @@ class TinyLlamaRuntime:
                                          weights.lm_head.handle, ctypes.cast(blocks, ctypes.c_void_p), int(self.mode),
                                          ctypes.byref(h)))
         self._h = h
+
+    @classmethod
+    def load(cls, ctx: Context, path, mode: Mode = Mode.EXACT) -> "TinyLlamaRuntime":
+        """TinyLlamaRuntime::load (rce-tinyllama/src/lib.rs L339-354): map and
+        parse the GGUF file, read the config and upload every weight once;
+        the file is closed again when the weights are on the device."""
+        from .gguf import GgufFile
+        with GgufFile.open(path) as g:
+            cfg = TinyLlamaConfig.from_gguf(g)
+            weights = load_weights(ctx, g, cfg)
+        return cls(ctx, cfg, weights, mode)
 
     @property
     def handle(self) -> ctypes.c_void_p:

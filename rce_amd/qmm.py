@@ -152,6 +152,16 @@ class QuantWeight:
                                               ctypes.byref(h)))
         return cls(ctx, h)
 
+    @classmethod
+    def from_gguf(cls, ctx: Context, gguf, name: str, n_rows: int, n_cols: int) -> "QuantWeight":
+        """QuantWeight::from_gguf (L173-209): tensor `name` of a GgufFile
+        (rce_amd.gguf) as a device-resident weight of the declared
+        [n_rows, n_cols] (n_rows * n_cols must be its element count)."""
+        h = ctypes.c_void_p()
+        check(lib().rce_qmm_weight_from_gguf(ctx.handle, gguf.handle, name.encode("utf-8"), n_rows, n_cols,
+                                             ctypes.byref(h)))
+        return cls(ctx, h)
+
     def sub_view(self, byte_offset: int, byte_len: int, n_rows: int, n_cols: int) -> "QuantWeight":
         """QuantWeight::sub_view (L99-118): shares the device copy."""
         h = ctypes.c_void_p()

@@ -32,9 +32,12 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     L = _lib.lib()
-    assert L.rce_qmm_abi_version() == 1
+    assert L.rce_qmm_abi_version() == 2
     assert L.rce_qmm_status_str(0) == b"ok"
     assert L.rce_qmm_status_str(3) == b"unsupported dtype"
+    assert L.rce_qmm_status_str(8) == b"not found"
+    assert L.rce_qmm_status_str(9) == b"parse error"
+    assert L.rce_qmm_status_str(10) == b"i/o error"
 
 
 def test_supports_matrix():
