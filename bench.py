@@ -447,6 +447,7 @@ def main():
             ("Q4_K 4096x4096 b1", G.Q4K, 4096, 4096, 1),
             ("Q4_K 5632x2048 b1", G.Q4K, 5632, 2048, 1),       # configs[4] FFN shapes
             ("Q4_K 2048x5632 b1", G.Q4K, 2048, 5632, 1),
+            ("Q5_K 4096x4096 b1", G.Q5K, 4096, 4096, 1),       # Q5_K_M models' linears
             ("Q6_K 32000x2048 b1", G.Q6K, 32000, 2048, 1),     # configs[4] head
         ]
         for name, sdt, sn, sk, st in sweep:

@@ -174,7 +174,7 @@ rce_qmm_status rce_qmm_dequant_row(rce_qmm_context *ctx, const rce_qmm_weight *w
 /* GGUF bytes of f32 weights [n_rows, n_cols] (row-major) by the reference's
  * quantizers: Q8_0 / Q4_0 by quantize_block (rce-vm-backend-cpu/src/ml/nn.rs
  * L541-563, packed as spec/checker/tests/support/toy_gpt2.rs L46-58), Q4_K /
- * Q6_K by quantize_k + pack (kquant.rs L193-346).  len must equal n_rows *
+ * Q5_K / Q6_K by quantize_k + pack (kquant.rs L193-346).  len must equal n_rows *
  * row_bytes(dtype, n_cols).  Host only (no device needed); bit-identical for
  * any thread count. */
 rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, size_t n_rows, size_t n_cols, uint8_t *dst,

@@ -860,8 +860,9 @@ EXPORT void orc_matmul_k(const float *x, size_t m, size_t k, const int32_t *q, s
  * 16 for Q6_K) is replaced by dx * (exact integer dot of the block); the
  * rest of each row formula and its fold order are the reference's:
  *   Q8_0, Q4_0 : sub = dx * isum;            sumf += scale * sub
- *   Q4_K       : va = dx * isum, a = dx * xsum (xsum = sum of xq);
+ *   Q4_K, Q5_K : va = dx * isum, a = dx * xsum (xsum = sum of xq);
  *                sumf += d1*va_lo - min1*a_lo + d2*va_hi - min2*a_hi
+ *                (Q5_K: the 5-bit values of lib.rs L388-422)
  *   Q6_K       : per super-block, ssb = sum over sub-blocks of 16 b ascending
  *                of (d*sc_b) * (dx * isum_b) from +0.0; sumf += ssb
  */
@@ -894,9 +895,11 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
             float sub = dx[ib] * (float)isum;
             sumf += rd_f16(s) * sub;
         }
-    } else if (t == T_Q4_K) {
+    } else if (t == T_Q4_K || t == T_Q5_K) {
+        const int q5 = t == T_Q5_K;
+        const size_t bb = q5 ? 176 : 144, qs_off = q5 ? 48 : 16;
         for (size_t ib = 0; ib < k / 256; ib++) {
-            const uint8_t *s = r + ib * 144;
+            const uint8_t *s = r + ib * bb;
             float d = rd_f16(s), dmin = rd_f16(s + 2);
             for (int g = 0; g < 4; g++) {
                 int sc1, m1, sc2, m2;
@@ -908,9 +911,14 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
                 const int8_t *xl = xq + b_lo * 32, *xh = xq + b_hi * 32;
                 int32_t il = 0, ih = 0, sl = 0, sh = 0;
                 for (int l = 0; l < 32; l++) {
-                    uint8_t byte = s[16 + g * 32 + l];
-                    il += (byte & 0x0F) * xl[l]; sl += xl[l];
-                    ih += (byte >> 4) * xh[l]; sh += xh[l];
+                    uint8_t byte = s[qs_off + g * 32 + l];
+                    int h1 = 0, h2 = 0;
+                    if (q5) {
+                        h1 = ((s[16 + l] >> (2 * g)) & 1) << 4;
+                        h2 = ((s[16 + l] >> (2 * g + 1)) & 1) << 4;
+                    }
+                    il += ((byte & 0x0F) | h1) * xl[l]; sl += xl[l];
+                    ih += ((byte >> 4) | h2) * xh[l]; sh += xh[l];
                 }
                 float va_lo = dx[b_lo] * (float)il, a_lo = dx[b_lo] * (float)sl;
                 float va_hi = dx[b_hi] * (float)ih, a_hi = dx[b_hi] * (float)sh;
@@ -946,7 +954,7 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
 EXPORT int orc_mm_batched_q8(const float *a, size_t t_rows, const uint8_t *w, uint32_t t,
                              size_t n_rows, size_t n_cols, float *out, int threads) {
     uint32_t qk, bb;
-    if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q4_K && t != T_Q6_K) return -1;
+    if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q4_K && t != T_Q5_K && t != T_Q6_K) return -1;
     if (orc_block_geometry(t, &qk, &bb) || n_cols % qk) return -2;
     size_t row_bytes = n_cols / qk * bb;
     int8_t *xq = (int8_t *)malloc(n_cols);

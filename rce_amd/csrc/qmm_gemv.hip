@@ -46,6 +46,21 @@ __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
         const uint8_t byte = l < 16 ? rp[w.plane1 + 16 * u + l] : rp[w.plane2 + 16 * u + l - 16];
         const int n = hi ? ((byte >> 4) & 0x0F) : (byte & 0x0F);
         v = dd * (float)n - mm;
+    } else if (w.dtype == T_Q5_K) {  // dequant.rs L606-655
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t sb = i / 256;
+        const int p = (int)(i % 256), g = p / 64, l = p % 32, hi = (p % 64) >= 32;
+        const uint4 h = *reinterpret_cast<const uint4 *>(rp + 16 * sb);
+        int sc, m;
+        k4_scale_min(h, 2 * g + hi, sc, m);
+        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+        const float dd = d * (float)sc, mm = dmin * (float)m;
+        const size_t u = 4 * sb + g;
+        const uint8_t byte = l < 16 ? rp[w.plane1 + 16 * u + l] : rp[w.plane2 + 16 * u + l - 16];
+        const uint2 hb = *reinterpret_cast<const uint2 *>(rp + w.plane3 + 8 * u);
+        const uint32_t h5 = ((hi ? hb.y : hb.x) >> l) & 1u;
+        const int n = (int)((hi ? ((byte >> 4) & 0x0F) : (byte & 0x0F)) + 16 * h5);
+        v = dd * (float)n - mm;
     } else if (w.dtype == T_Q6_K) {
         const uint8_t *sp = w.base + (row >> 6) * w.group_stride + (i / 256) * IL64_Q6K_SB;
         const size_t lane = row & 63;
@@ -96,6 +111,7 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
     case T_Q8_0:
         return n_cols % 32 == 0 && n_cols / 32 <= 1024;
     case T_Q4_K:
+    case T_Q5_K:
         return n_cols % 256 == 0 && n_cols / 64 <= 1024;
     case T_Q6_K:
         return n_cols % 256 == 0 && n_cols / 256 <= 1024;
@@ -126,6 +142,13 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane1 = 16 * (k / 256);
         dw.plane2 = dw.plane1 + 16 * (k / 64);
         dw.row_stride = 144 * (k / 256);
+        return dw.row_stride * n;
+    case T_Q5_K:  // 16 + 4 * (16 + 16 + 8) = 176 B per super-block, as in the file
+        dw.layout = LAYOUT_SPLIT_Q5_K;
+        dw.plane1 = 16 * (k / 256);
+        dw.plane2 = dw.plane1 + 16 * (k / 64);
+        dw.plane3 = dw.plane2 + 16 * (k / 64);
+        dw.row_stride = 176 * (k / 256);
         return dw.row_stride * n;
     case T_Q6_K:
         dw.layout = LAYOUT_IL64_Q6_K;
@@ -173,6 +196,29 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
         }
         break;
     }
+    case LAYOUT_SPLIT_Q5_K: {  // block: d, dmin, scales[12], qh[32], qs[128]
+        const size_t nsb = k / 256;
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * nsb * 176;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t sb = 0; sb < nsb; sb++) {
+                const uint8_t *blk = s + sb * 176, *qh = blk + 16, *qs = blk + 48;
+                for (int i = 0; i < 16; i++) d[16 * sb + i] = blk[i];
+                for (int g = 0; g < 4; g++) {
+                    const size_t u = 4 * sb + g;
+                    for (int l = 0; l < 16; l++) d[dw.plane1 + 16 * u + l] = qs[32 * g + l];
+                    for (int l = 0; l < 16; l++) d[dw.plane2 + 16 * u + l] = qs[32 * g + 16 + l];
+                    uint64_t bits = 0;  // group g reads qh bits 2g (low half) and 2g+1 (high half)
+                    for (int l = 0; l < 32; l++) {
+                        bits |= (uint64_t)((qh[l] >> (2 * g)) & 1) << l;
+                        bits |= (uint64_t)((qh[l] >> (2 * g + 1)) & 1) << (32 + l);
+                    }
+                    for (int b = 0; b < 8; b++) d[dw.plane3 + 8 * u + b] = (uint8_t)(bits >> (8 * b));
+                }
+            }
+        }
+        break;
+    }
     case LAYOUT_IL64_Q6_K: {
         const size_t nsb = k / 256;
         for (size_t r = 0; r < n; r++) {
@@ -206,6 +252,7 @@ static size_t unit_bytes(uint32_t dtype) {
     case T_Q4_0: return 18;
     case T_Q8_0: return 34;
     case T_Q4_K: return 36;
+    case T_Q5_K: return 44;
     case T_Q6_K: return 210;
     default: return 0;
     }
@@ -225,7 +272,8 @@ GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
     g.nt = nt_for(U);
     const bool q8 = mode == 1;
     const int P = g.nt / U;
-    int tbmax = q8 ? (w.dtype == T_Q6_K ? 2 : (w.dtype == T_Q4_K ? 4 : 8)) : (w.dtype == T_Q4_K ? 2 : 4);
+    const bool k4 = w.dtype == T_Q4_K || w.dtype == T_Q5_K;  // 64-value units
+    int tbmax = q8 ? (w.dtype == T_Q6_K ? 2 : (k4 ? 4 : 8)) : (k4 ? 2 : 4);
     if (w.dtype == T_Q6_K && !q8) tbmax = 1;
     g.tb = 1;
     while (g.tb * 2 <= tbmax && (size_t)g.tb * 2 <= t_rows) g.tb *= 2;
@@ -240,7 +288,7 @@ GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
             if (std::abs(o - want) < std::abs(g.rpl - want)) g.rpl = o;
         // at least one block per CU
         while (g.rpl > 2 && (w.n_rows + (size_t)P * g.rpl - 1) / ((size_t)P * g.rpl) < 256) g.rpl = g.rpl == 16 ? 12 : (g.rpl == 12 ? 8 : g.rpl / 2);
-        const bool heavy = (q8 && g.tb >= 4) || (!q8 && (g.tb >= 4 || (w.dtype == T_Q4_K && g.tb >= 2)));
+        const bool heavy = (q8 && g.tb >= 4) || (!q8 && (g.tb >= 4 || (k4 && g.tb >= 2)));
         if (heavy && g.rpl > 4) g.rpl = 4;
     }
     // shrink rows, then tokens, until the block's LDS fits
@@ -261,6 +309,7 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
     case T_Q4_0: return launch_gemv_q4_0(w, g, a, t_rows, out, mode, s);
     case T_Q8_0: return launch_gemv_q8_0(w, g, a, t_rows, out, mode, s);
     case T_Q4_K: return launch_gemv_q4_k(w, g, a, t_rows, out, mode, s);
+    case T_Q5_K: return launch_gemv_q5_k(w, g, a, t_rows, out, mode, s);
     case T_Q6_K: return launch_gemv_q6_k(w, g, a, t_rows, out, mode, s);
     default: return hipErrorInvalidValue;
     }
@@ -269,7 +318,7 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
 bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode, bool with_norm) {
     if (!gpu_supports(dtype, n_cols, mode)) return false;
     if (dtype == T_Q6_K && mode == 0) return false;  // EXACT Q6_K is not the activation-stationary kernel
-    if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q6_K) return false;
+    if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q5_K && dtype != T_Q6_K) return false;
     // the normalizing forms hold the row's sum-of-squares tasks (8 values
     // each) in two per thread
     return !with_norm || n_cols / 8 <= (size_t)(2 * nt_for(units_per_row(dtype, n_cols)));
@@ -301,6 +350,7 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
     case T_Q4_0: return launch_gemv_fx_q4_0(f, g, a, mode, s);
     case T_Q8_0: return launch_gemv_fx_q8_0(f, g, a, mode, s);
     case T_Q4_K: return launch_gemv_fx_q4_k(f, g, a, mode, s);
+    case T_Q5_K: return launch_gemv_fx_q5_k(f, g, a, mode, s);
     case T_Q6_K: return launch_gemv_fx_q6_k(f, g, a, mode, s);
     default: return hipErrorInvalidValue;
     }

@@ -129,6 +129,7 @@ struct RawQ4_0 { uint4 q; uint32_t s; };
 struct RawQ8_0 { uint4 q0, q1; uint32_t s; };
 struct RawQ4_K { uint4 h, q0, q1; };
 struct RawQ6_K { uint4 c[13]; uint32_t d; };
+struct RawQ5_K { uint4 h, q0, q1; uint2 hb; };
 
 __device__ __forceinline__ RawQ4_0 ld_q4_0(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
@@ -154,6 +155,30 @@ __device__ __forceinline__ RawQ4_K ld_q4_k(const DevWeight &w, size_t row, int c
     r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
     r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
     return r;
+}
+
+__device__ __forceinline__ RawQ5_K ld_q5_k(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ5_K r;
+    r.h = *reinterpret_cast<const uint4 *>(rp + 16 * (size_t)(col >> 2));
+    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
+    r.hb = *reinterpret_cast<const uint2 *>(rp + w.plane3 + 8 * (size_t)col);
+    return r;
+}
+
+// Four bits b0..b3 of t (t < 16) to bit 4 of bytes 0..3: t * 0x00204081
+// puts copies of t at bits 0, 7, 14 and 21 (no overlap, so no carries),
+// and bit j of t then sits at bit 8j; shifted to 8j + 4.
+__device__ __forceinline__ uint32_t spread4_bit4(uint32_t t) { return ((t * 0x00204081u) & 0x01010101u) << 4; }
+
+// The 5-bit values of positions 4i..4i+3 of Q5_K group halves, one per
+// byte: nibbles of qs word x (low or high) with the 5th bits from hb.
+__device__ __forceinline__ uint32_t q5_lo(uint32_t x, uint32_t hb_lo, int i) {
+    return (x & NIB) | spread4_bit4((hb_lo >> (4 * i)) & 0xFu);
+}
+__device__ __forceinline__ uint32_t q5_hi(uint32_t x, uint32_t hb_hi, int i) {
+    return ((x >> 4) & NIB) | spread4_bit4((hb_hi >> (4 * i)) & 0xFu);
 }
 
 // Q6_K super-block sb of row `row` (LAYOUT_IL64_Q6_K: chunk c of rows
@@ -471,6 +496,73 @@ struct Q4_KExact {
     }
 };
 
+// Q5_K group, EXACT (rce-op-qmm/src/lib.rs L388-422, L783-838): Q4_K's
+// group formula with the 5-bit values (nibble | h << 4).
+template <int TB>
+struct Q5_KExact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ5_K;
+    float av[TB][64];
+    float a_lo[TB], a_hi[TB];
+    int g;
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q5_k(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+        g = col & 3;
+#pragma unroll
+        for (int t = 0; t < TB; t++)  // tokens past tv read token 0's slice (never folded)
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 64 * (size_t)col, av[t], 64);
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            a_lo[t] = 0.0f;
+            a_hi[t] = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 32; l++) { a_lo[t] = a_lo[t] + av[t][l]; a_hi[t] = a_hi[t] + av[t][32 + l]; }
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        int sc1, m1, sc2, m2;
+        k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
+        const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+        const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+        float va_lo[TB], va_hi[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) { va_lo[t] = 0.0f; va_hi[t] = 0.0f; }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+            const uint32_t lo = q5_lo(x, r.hb.x, i), hi = q5_hi(x, r.hb.y, i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float vl = (float)((lo >> (8 * j)) & 0xFFu), vh = (float)((hi >> (8 * j)) & 0xFFu);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    va_lo[t] = va_lo[t] + vl * av[t][4 * i + j];
+                    va_hi[t] = va_hi[t] + vh * av[t][32 + 4 * i + j];
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            float s = d1 * va_lo[t];
+            s = s - min1 * a_lo[t];
+            s = s + d2 * va_hi[t];
+            s = s - min2 * a_hi[t];
+            out[t] = s;
+        }
+    }
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float gv[64];
+        load_f32x(gw + 64 * (size_t)col, gv, 64);
+#pragma unroll
+        for (int l = 0; l < 64; l++) { const float t = av[0][l] * inv; av[0][l] = t * gv[l]; }
+        a_lo[0] = 0.0f;
+        a_hi[0] = 0.0f;
+#pragma unroll
+        for (int l = 0; l < 32; l++) { a_lo[0] = a_lo[0] + av[0][l]; a_hi[0] = a_hi[0] + av[0][32 + l]; }
+    }
+};
+
 // Q4_0 / Q8_0 block, Q8: sub = dx * isum, addend = scale * sub.
 template <int TB, bool IS_Q4>
 struct Q32Q8 {
@@ -570,6 +662,66 @@ struct Q4_KQ8 {
             const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
             lo[i] = (int)(x & NIB);
             hi[i] = (int)((x >> 4) & NIB);
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            int il = 0, ih = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                il = __builtin_amdgcn_sdot4(lo[i], xl[t][i], il, false);
+                ih = __builtin_amdgcn_sdot4(hi[i], xh[t][i], ih, false);
+            }
+            const float va_lo = dl[t] * (float)il, a_lo = dl[t] * (float)sl[t];
+            const float va_hi = dh[t] * (float)ih, a_hi = dh[t] * (float)sh[t];
+            float s = d1 * va_lo;
+            s = s - min1 * a_lo;
+            s = s + d2 * va_hi;
+            s = s - min2 * a_hi;
+            out[t] = s;
+        }
+    }
+};
+
+// Q5_K group, Q8: Q4_KQ8 with the 5-bit values (0..31, so sdot4 applies).
+template <int TB>
+struct Q5_KQ8 {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ5_K;
+    int xl[TB][8], xh[TB][8];
+    float dl[TB], dh[TB];
+    int sl[TB], sh[TB];
+    int g;
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q5_k(w, row, col); }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
+        g = col & 3;
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 64 * (size_t)col) / 4);
+            const int4 a = p[0], b = p[1], c = p[2], e = p[3];
+            const int v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) { xl[t][i] = ok ? v[i] : 0; xh[t][i] = ok ? v[8 + i] : 0; }
+            const size_t b32 = tt * (k / 32) + 2 * (size_t)col, b16 = tt * (k / 16) + 4 * (size_t)col;
+            dl[t] = ok ? L.dx[b32] : 0.0f;
+            dh[t] = ok ? L.dx[b32 + 1] : 0.0f;
+            sl[t] = ok ? L.s16[b16] + L.s16[b16 + 1] : 0;
+            sh[t] = ok ? L.s16[b16 + 2] + L.s16[b16 + 3] : 0;
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        int sc1, m1, sc2, m2;
+        k4_scale_min_pair(r.h, g, sc1, m1, sc2, m2);
+        const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+        const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+        int lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+            lo[i] = (int)q5_lo(x, r.hb.x, i);
+            hi[i] = (int)q5_hi(x, r.hb.y, i);
         }
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -833,7 +985,7 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
 inline int units_per_row(uint32_t dtype, size_t n_cols) {
     switch (dtype) {
     case T_Q4_0: case T_Q8_0: return (int)(n_cols / 32);
-    case T_Q4_K: return (int)(n_cols / 64);
+    case T_Q4_K: case T_Q5_K: return (int)(n_cols / 64);
     case T_Q6_K: return (int)(n_cols / 256);
     default: return 0;
     }

@@ -35,6 +35,11 @@ enum Layout : int {
     // ql (0..7), qh (8..11) and scales (12) for the 64 rows, chunk j of row
     // r at (j * 64 + r % 64) * 16, then the rows' 2-byte d values.
     LAYOUT_IL64_Q6_K = 4,
+    // Q5_K: LAYOUT_SPLIT_Q4_K's header and two qs planes, plus at plane3 +
+    // 8 u one 8-byte word per 64-group u: bit l (l < 32) = the 5th bit of
+    // position l, bit 32 + l = that of position 32 + l (the two qh bits of
+    // the group, 2g and 2g + 1, of qh byte l).
+    LAYOUT_SPLIT_Q5_K = 5,
 };
 
 struct DevWeight {
@@ -44,7 +49,8 @@ struct DevWeight {
     size_t n_rows, n_cols;
     size_t row_stride;    // SPLIT: bytes between rows
     size_t plane1;        // SPLIT: offset of the first 16-B plane in a row
-    size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K: offset of the second plane
+    size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K / SPLIT_Q5_K: offset of the second plane
+    size_t plane3;        // SPLIT_Q5_K: offset of the high-bit words
     size_t group_stride;  // IL64: bytes between 64-row groups
 };
 
@@ -125,6 +131,7 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
 hipError_t launch_gemv_fx_q4_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q8_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q4_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q5_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q6_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 
 // ---- decode step (decoder.hip) ----
@@ -173,6 +180,8 @@ hipError_t launch_gemv_q4_0(const DevWeight &w, const GemvGeom &g, const float *
 hipError_t launch_gemv_q8_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_gemv_q4_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q5_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);

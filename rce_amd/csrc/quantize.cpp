@@ -6,7 +6,7 @@
 //     packed as spec/checker/tests/support/toy_gpt2.rs L46-58 does: f16
 //     scale, then int8 values (Q8_0) or nibbles (lo = q[t] + 8, hi =
 //     q[t + 16] + 8) (Q4_0).
-//   Q4_K, Q6_K: quantize_k (rce-vm-backend-cpu/src/ml/kquant.rs L193-245)
+//   Q4_K, Q5_K, Q6_K: quantize_k (rce-vm-backend-cpu/src/ml/kquant.rs L193-245)
 //     and pack (L284-346).
 // Scales are rounded with round_to_f16 (nn.rs L521-533): IEEE binary16
 // round-to-nearest-even, overflow to infinity -- exactly the compiler's
@@ -68,7 +68,9 @@ void encode_q32(const float *x, bool q4, uint8_t *out) {
 }
 
 // One super-block of 256 -> 144 bytes (Q4_K).
-void encode_q4_k(const float *x, uint8_t *out) {
+// Q4_K (nmax 15) and Q5_K (nmax 31, plus the qh plane of 5th bits).
+void encode_q45_k(const float *x, uint8_t *out, bool q5) {
+    const float nmax = q5 ? 31.0f : 15.0f;
     float w[8], v[8];
     for (int b = 0; b < 8; b++) {
         float lo = 0.0f, hi = -INFINITY;
@@ -78,7 +80,7 @@ void encode_q4_k(const float *x, uint8_t *out) {
             if (t > hi) hi = t;
         }
         const float span = hi - lo;
-        w[b] = span / 15.0f;
+        w[b] = span / nmax;
         v[b] = -lo;
     }
     float bw = 0.0f, bv = 0.0f;
@@ -104,11 +106,22 @@ void encode_q4_k(const float *x, uint8_t *out) {
     for (int p = 0; p < 256; p++) {
         const float sb = d * (float)sc[p / 32], ob = dmin * (float)mn[p / 32];
         const float num = x[p] + ob;
-        q[p] = sb != 0.0f ? clamp_i(round_i(num / sb), 0, 15) : 0;
+        q[p] = sb != 0.0f ? clamp_i(round_i(num / sb), 0, (int)nmax) : 0;
+    }
+    uint8_t *qs = out + 16;
+    if (q5) {  // qh[l] bit 2g: position 64g + l, bit 2g+1: 64g + 32 + l (kquant.rs L310-318)
+        uint8_t *qh = out + 16;
+        for (int l = 0; l < 32; l++) qh[l] = 0;
+        for (int g = 0; g < 4; g++)
+            for (int l = 0; l < 32; l++) {
+                qh[l] = (uint8_t)(qh[l] | (((q[64 * g + l] >> 4) & 1) << (2 * g)));
+                qh[l] = (uint8_t)(qh[l] | (((q[64 * g + 32 + l] >> 4) & 1) << (2 * g + 1)));
+            }
+        qs = out + 48;
     }
     for (int g = 0; g < 4; g++)
         for (int l = 0; l < 32; l++)
-            out[16 + 32 * g + l] = (uint8_t)((q[64 * g + l] & 15) | ((q[64 * g + 32 + l] & 15) << 4));
+            qs[32 * g + l] = (uint8_t)((q[64 * g + l] & 15) | ((q[64 * g + 32 + l] & 15) << 4));
 }
 
 // One super-block of 256 -> 210 bytes (Q6_K).
@@ -158,6 +171,7 @@ extern "C" rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, siz
     case T_Q8_0: qk = 32; bb = 34; break;
     case T_Q4_0: qk = 32; bb = 18; break;
     case T_Q4_K: qk = 256; bb = 144; break;
+    case T_Q5_K: qk = 256; bb = 176; break;
     case T_Q6_K: qk = 256; bb = 210; break;
     default: return fail(RCE_QMM_UNSUPPORTED_DTYPE, "no quantizer for dtype " + std::to_string(dtype));
     }
@@ -172,7 +186,8 @@ extern "C" rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, siz
                 switch (dtype) {
                 case T_Q8_0: encode_q32(x, false, o); break;
                 case T_Q4_0: encode_q32(x, true, o); break;
-                case T_Q4_K: encode_q4_k(x, o); break;
+                case T_Q4_K: encode_q45_k(x, o, false); break;
+                case T_Q5_K: encode_q45_k(x, o, true); break;
                 default: encode_q6_k(x, o); break;
                 }
             }

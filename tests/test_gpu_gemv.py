@@ -36,6 +36,7 @@ SHAPES = {
     O.Q8_0: [(1, 32), (16, 32), (3, 64), (65, 256), (1000, 2048), (4096, 4096)],
     O.Q4_0: [(1, 32), (6, 128), (77, 1024), (1024, 2048), (11008, 4096), (4096, 14336)],
     O.Q4_K: [(1, 256), (5, 512), (130, 2048), (2048, 5632), (4096, 4096)],
+    O.Q5_K: [(1, 256), (7, 512), (129, 2048), (2048, 5632), (4096, 4096)],
     O.Q6_K: [(1, 256), (64, 256), (100, 512), (256, 2048), (32000, 2048)],
 }
 CASES = [(dt, n, k) for dt, shapes in SHAPES.items() for (n, k) in shapes]
@@ -55,7 +56,7 @@ def test_mm_1d_exact_bit_identical(ctx, dt, n, k):
     assert np.array_equal(bits(serial), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K])
 @pytest.mark.parametrize("t_rows", [2, 8])
 def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
     n, k = (700, 2048) if dt != O.Q4_0 else (11008, 4096)
@@ -81,7 +82,8 @@ def run_dev(ctx, w, x, mode, a_dtype=G.F32):
 
 
 Q8_CASES = [(O.Q8_0, 4096, 4096), (O.Q4_0, 11008, 4096), (O.Q4_0, 4096, 14336), (O.Q4_K, 4096, 4096),
-            (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256)]
+            (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256),
+            (O.Q5_K, 4096, 4096), (O.Q5_K, 2048, 5632), (O.Q5_K, 9, 256)]
 
 
 @pytest.mark.parametrize("dt,n,k", Q8_CASES)
@@ -111,7 +113,8 @@ def test_f16_activations_are_widened_exactly(ctx):
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q6_K, 130, 512)])
+@pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q5_K, 35, 1024),
+                                    (O.Q6_K, 130, 512)])
 def test_dequant_row_bit_identical(ctx, dt, n, k):
     rng = np.random.default_rng(5000 + dt)
     b = make(rng, dt, n, k)
@@ -164,7 +167,7 @@ def test_errors_and_empty_inputs(ctx):
         rce_amd.QuantWeight.from_owned_bytes(ctx, b[:-1], O.Q4_0, 8, 64)
     assert e.value.status == 2
     with pytest.raises(rce_amd.QmmError) as e:
-        rce_amd.QuantWeight.from_owned_bytes(ctx, np.zeros(176, np.uint8), G.Q5K, 1, 256)
+        rce_amd.QuantWeight.from_owned_bytes(ctx, np.zeros(110, np.uint8), G.Q3K, 1, 256)  # no kernel
     assert e.value.status == 3
     with pytest.raises(rce_amd.QmmError):
         rce_amd.mm_1d(np.zeros(63, F32), w)

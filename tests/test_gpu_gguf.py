@@ -20,7 +20,7 @@ def note(msg):
     print(msg, flush=True)
 
 
-FORMATS = [(O.Q4_0, 96, 512), (O.Q8_0, 64, 256), (O.Q4_K, 80, 512), (O.Q6_K, 48, 256)]
+FORMATS = [(O.Q4_0, 96, 512), (O.Q8_0, 64, 256), (O.Q4_K, 80, 512), (O.Q5_K, 40, 512), (O.Q6_K, 48, 256)]
 
 
 @pytest.mark.parametrize("align", [32, 64])

@@ -94,6 +94,15 @@ def test_llama_unfused_forms(ctx):
     run_pair(ctx, W, Mode.Q8, TOKENS[:5], 1e-3).close()
 
 
+def test_llama_q5_k_linears(ctx):
+    """Q5_K linears with a Q6_K head (a Q5_K_M-style model): the fused
+    q|k|v, gate/up and residual forms run on the Q5_K units."""
+    note("llama Q5_K linears")
+    W = make_weights(tiny_cfg(), seed=32, lin_dtype=O.Q5_K)
+    run_pair(ctx, W, Mode.EXACT, TOKENS[:5], 1e-5).close()
+    run_pair(ctx, W, Mode.Q8, TOKENS[:5], 1e-3).close()
+
+
 def test_llama_head_dim_128(ctx):
     """d_head 128: runs of 32 keys per wave."""
     note("llama d_head 128, rope_dim 64, GQA 4:1, 40 positions")

@@ -46,7 +46,7 @@ def np_mm_q8_0_q4_0(a, b, dt, n, k):
 
 
 def np_mm_k(a, b, fmt, n, k):
-    """dot_row_q4_k / dot_row_q6_k order from unpacked super-blocks."""
+    """dot_row_q4_k / dot_row_q5_k / dot_row_q6_k order from unpacked super-blocks."""
     nsb = k // 256
     bb = O.BLOCK[fmt][1]
     Q = np.zeros((n, k), np.int64)
@@ -88,7 +88,7 @@ def rand_weight(rng, dt, n, k, sigma=0.02):
     return w, O.quantize(w, dt)
 
 
-FORMATS = [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K]
+FORMATS = [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K]
 
 
 @pytest.mark.parametrize("dt", FORMATS)
@@ -259,7 +259,7 @@ def test_q8_path_equals_numpy_restatement(dt):
             for s in range(nsb):
                 q, sc, mn, d, dmin = O.unpack_k(b[(j * nsb + s) * bb:(j * nsb + s + 1) * bb], dt)
                 xs = xq[256 * s:256 * s + 256]
-                if dt == O.Q4_K:
+                if dt in (O.Q4_K, O.Q5_K):
                     for g in range(4):
                         bl, bh = 8 * s + 2 * g, 8 * s + 2 * g + 1
                         il = int((q[64 * g:64 * g + 32] * xs[64 * g:64 * g + 32]).sum())

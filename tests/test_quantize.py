@@ -11,8 +11,8 @@ import rce_amd
 F32 = np.float32
 
 
-@pytest.mark.parametrize("dt,k", [(O.Q8_0, 4096), (O.Q4_0, 4096), (O.Q4_K, 2048), (O.Q6_K, 2048),
-                                  (O.Q4_0, 32), (O.Q4_K, 256)])
+@pytest.mark.parametrize("dt,k", [(O.Q8_0, 4096), (O.Q4_0, 4096), (O.Q4_K, 2048), (O.Q5_K, 2048), (O.Q6_K, 2048),
+                                  (O.Q4_0, 32), (O.Q4_K, 256), (O.Q5_K, 256)])
 def test_quantize_matches_oracle(dt, k):
     rng = np.random.default_rng(dt * 1000 + k)
     for n, sigma in ((1, 1.0), (37, 0.02), (200, 3.0)):
@@ -20,7 +20,7 @@ def test_quantize_matches_oracle(dt, k):
         assert np.array_equal(rce_amd.quantize(w, dt), O.quantize(w, dt)), (dt, k, n, sigma)
 
 
-@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K])
 def test_quantize_edge_blocks(dt):
     """Zero blocks (d = 0 branches), constant blocks, the reference's known
     answer input x = i - 16 (nn.rs L751-765), ties and large magnitudes."""
@@ -47,4 +47,4 @@ def test_quantize_errors():
     with pytest.raises(rce_amd.QmmError):
         rce_amd.quantize(np.zeros((1, 100), F32), O.Q4_0)  # not a block multiple
     with pytest.raises(rce_amd.QmmError):
-        rce_amd.quantize(np.zeros((1, 256), F32), O.Q5_K)  # no encoder
+        rce_amd.quantize(np.zeros((1, 256), F32), O.Q3_K)  # no encoder
