@@ -859,7 +859,9 @@ EXPORT void orc_matmul_k(const float *x, size_t m, size_t k, const int32_t *q, s
  * sub-sum (the reference's `sub`, `va`, `a` sums over a block of 32, or of
  * 16 for Q6_K) is replaced by dx * (exact integer dot of the block); the
  * rest of each row formula and its fold order are the reference's:
- *   Q8_0, Q4_0 : sub = dx * isum;            sumf += scale * sub
+ *   Q8_0, Q4_0, Q5_0 : sub = dx * isum;      sumf += scale * sub
+ *   Q4_1       : va = dx * isum, a = dx * xsum (isum over the raw
+ *                nibbles 0..15); sumf += scale * va + min * a
  *   Q4_K, Q5_K : va = dx * isum, a = dx * xsum (xsum = sum of xq);
  *                sumf += d1*va_lo - min1*a_lo + d2*va_hi - min2*a_hi
  *                (Q5_K: the 5-bit values of lib.rs L388-422)
@@ -878,22 +880,42 @@ EXPORT void orc_quantize_act_q8(const float *x, size_t k, int8_t *xq, float *dx,
 
 static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const uint8_t *r, size_t k) {
     float sumf = 0.0f;
-    if (t == T_Q8_0 || t == T_Q4_0) {
-        size_t bb = t == T_Q8_0 ? 34 : 18;
+    if (t == T_Q8_0 || t == T_Q4_0 || t == T_Q5_0) {
+        size_t bb = t == T_Q8_0 ? 34 : (t == T_Q4_0 ? 18 : 22);
         for (size_t ib = 0; ib < k / 32; ib++) {
             const uint8_t *s = r + ib * bb;
             const int8_t *xb = xq + ib * 32;
             int32_t isum = 0;
             if (t == T_Q8_0) {
                 for (int q = 0; q < 32; q++) isum += (int32_t)(int8_t)s[2 + q] * xb[q];
-            } else {
+            } else if (t == T_Q4_0) {
                 for (int q = 0; q < 16; q++) {
                     isum += ((s[2 + q] & 0x0F) - 8) * xb[q];
                     isum += ((s[2 + q] >> 4) - 8) * xb[q + 16];
                 }
+            } else {  /* Q5_0: the 5-bit values of lib.rs L525-561 */
+                uint32_t qh = (uint32_t)s[2] | ((uint32_t)s[3] << 8) | ((uint32_t)s[4] << 16) | ((uint32_t)s[5] << 24);
+                for (int q = 0; q < 16; q++) {
+                    isum += ((int)((s[6 + q] & 0x0F) | (((qh >> q) & 1) << 4)) - 16) * xb[q];
+                    isum += ((int)((s[6 + q] >> 4) | (((qh >> (q + 16)) & 1) << 4)) - 16) * xb[q + 16];
+                }
             }
             float sub = dx[ib] * (float)isum;
             sumf += rd_f16(s) * sub;
+        }
+    } else if (t == T_Q4_1) {
+        for (size_t ib = 0; ib < k / 32; ib++) {
+            const uint8_t *s = r + ib * 20;
+            const int8_t *xb = xq + ib * 32;
+            int32_t isum = 0, xs = 0;
+            for (int q = 0; q < 16; q++) {
+                isum += (s[4 + q] & 0x0F) * xb[q] + (s[4 + q] >> 4) * xb[q + 16];
+                xs += xb[q] + xb[q + 16];
+            }
+            float va = dx[ib] * (float)isum, a = dx[ib] * (float)xs;
+            float tt = rd_f16(s) * va;
+            tt = tt + rd_f16(s + 2) * a;
+            sumf += tt;
         }
     } else if (t == T_Q4_K || t == T_Q5_K) {
         const int q5 = t == T_Q5_K;
@@ -954,7 +976,8 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
 EXPORT int orc_mm_batched_q8(const float *a, size_t t_rows, const uint8_t *w, uint32_t t,
                              size_t n_rows, size_t n_cols, float *out, int threads) {
     uint32_t qk, bb;
-    if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q4_K && t != T_Q5_K && t != T_Q6_K) return -1;
+    if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q5_0 && t != T_Q4_1 && t != T_Q4_K && t != T_Q5_K && t != T_Q6_K)
+        return -1;
     if (orc_block_geometry(t, &qk, &bb) || n_cols % qk) return -2;
     size_t row_bytes = n_cols / qk * bb;
     int8_t *xq = (int8_t *)malloc(n_cols);

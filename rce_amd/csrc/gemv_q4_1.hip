@@ -1,0 +1,14 @@
+// gemv_q4_1.hip -- the Q4_1 decode kernels (EXACT and Q8).
+#include "qmm_gemv_kernels.h"
+
+namespace rce_qmm {
+hipError_t launch_gemv_q4_1(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out, int mode,
+                            hipStream_t s) {
+    if (mode == 0) return launch_as_tb<Q4_1Exact, false, 4>(w, g, a, t_rows, out, s);
+    return launch_as_tb<Q4_1Q8, true, 8>(w, g, a, t_rows, out, s);
+}
+hipError_t launch_gemv_fx_q4_1(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s) {
+    if (mode == 0) return launch_as_fx_nt<Q4_1Exact<1>, false>(f, g, a, s);
+    return launch_as_fx_nt<Q4_1Q8<1>, true>(f, g, a, s);
+}
+}  // namespace rce_qmm

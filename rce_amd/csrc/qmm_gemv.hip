@@ -16,8 +16,8 @@ __global__ void k_f16_to_f32(const uint16_t *__restrict__ s, float *__restrict__
     if (i < n) d[i] = h2f(s[i]);
 }
 
-// dequant.rs L360-382 (Q4_0), L438-454 (Q8_0), L546-589 (Q4_K), L658-701
-// (Q6_K): value i of row `row`.
+// dequant.rs L360-382 (Q4_0), L385-433 (Q4_1, Q5_0), L438-454 (Q8_0),
+// L546-589 (Q4_K), L606-655 (Q5_K), L658-701 (Q6_K): value i of row `row`.
 __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
     float v = 0.0f;
     if (w.dtype == T_Q4_0 || w.dtype == T_Q8_0) {
@@ -32,6 +32,21 @@ __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
         } else {
             const uint8_t byte = p < 16 ? rp[w.plane1 + 16 * b + p] : rp[w.plane2 + 16 * b + p - 16];
             v = (float)(int8_t)byte * scale;
+        }
+    } else if (w.dtype == T_Q5_0 || w.dtype == T_Q4_1) {  // dequant.rs L385-433
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t b = i / 32;
+        const int p = (int)(i % 32);
+        const uint8_t byte = rp[w.plane1 + 16 * b + (p & 15)];
+        const int nib = p < 16 ? (byte & 0x0F) : (byte >> 4);
+        if (w.dtype == T_Q5_0) {
+            const float scale = h2f(*reinterpret_cast<const uint16_t *>(rp + 2 * b));
+            const uint32_t qh = *reinterpret_cast<const uint32_t *>(rp + w.plane2 + 4 * b);
+            v = (float)((nib | (int)(((qh >> p) & 1u) << 4)) - 16) * scale;
+        } else {
+            const uint32_t sm = *reinterpret_cast<const uint32_t *>(rp + 4 * b);
+            const float t = (float)nib * h2f(sm & 0xFFFFu);
+            v = t + h2f(sm >> 16);
         }
     } else if (w.dtype == T_Q4_K) {
         const uint8_t *rp = w.base + row * w.row_stride;
@@ -109,6 +124,8 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
     switch (dtype) {
     case T_Q4_0:
     case T_Q8_0:
+    case T_Q5_0:
+    case T_Q4_1:
         return n_cols % 32 == 0 && n_cols / 32 <= 1024;
     case T_Q4_K:
     case T_Q5_K:
@@ -150,6 +167,18 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane3 = dw.plane2 + 16 * (k / 64);
         dw.row_stride = 176 * (k / 256);
         return dw.row_stride * n;
+    case T_Q5_0:
+        dw.layout = LAYOUT_SPLIT_Q5_0;
+        dw.plane1 = pad16(2 * (k / 32));
+        dw.plane2 = dw.plane1 + 16 * (k / 32);
+        dw.row_stride = pad16(dw.plane2 + 4 * (k / 32));
+        return dw.row_stride * n;
+    case T_Q4_1:
+        dw.layout = LAYOUT_SPLIT_Q4_1;
+        dw.plane1 = pad16(4 * (k / 32));
+        dw.plane2 = 0;
+        dw.row_stride = dw.plane1 + 16 * (k / 32);
+        return dw.row_stride * n;
     case T_Q6_K:
         dw.layout = LAYOUT_IL64_Q6_K;
         dw.group_stride = (k / 256) * IL64_Q6K_SB;
@@ -175,6 +204,27 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
                 for (int i = 0; i < 16; i++) d[dw.plane1 + 16 * b + i] = blk[2 + i];
                 if (dw.dtype == T_Q8_0)
                     for (int i = 0; i < 16; i++) d[dw.plane2 + 16 * b + i] = blk[18 + i];
+            }
+        }
+        break;
+    }
+    case LAYOUT_SPLIT_Q5_0:  // block: d, qh[4], qs[16]
+    case LAYOUT_SPLIT_Q4_1: {  // block: d, m, qs[16]
+        const bool q5 = dw.layout == LAYOUT_SPLIT_Q5_0;
+        const size_t nb = k / 32, bb = q5 ? 22 : 20;
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * nb * bb;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t b = 0; b < nb; b++) {
+                const uint8_t *blk = s + b * bb;
+                if (q5) {
+                    d[2 * b] = blk[0];
+                    d[2 * b + 1] = blk[1];
+                    for (int i = 0; i < 4; i++) d[dw.plane2 + 4 * b + i] = blk[2 + i];
+                } else {
+                    for (int i = 0; i < 4; i++) d[4 * b + i] = blk[i];
+                }
+                for (int i = 0; i < 16; i++) d[dw.plane1 + 16 * b + i] = blk[bb - 16 + i];
             }
         }
         break;
@@ -251,6 +301,8 @@ static size_t unit_bytes(uint32_t dtype) {
     switch (dtype) {
     case T_Q4_0: return 18;
     case T_Q8_0: return 34;
+    case T_Q5_0: return 22;
+    case T_Q4_1: return 20;
     case T_Q4_K: return 36;
     case T_Q5_K: return 44;
     case T_Q6_K: return 210;
@@ -311,6 +363,8 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
     case T_Q4_K: return launch_gemv_q4_k(w, g, a, t_rows, out, mode, s);
     case T_Q5_K: return launch_gemv_q5_k(w, g, a, t_rows, out, mode, s);
     case T_Q6_K: return launch_gemv_q6_k(w, g, a, t_rows, out, mode, s);
+    case T_Q5_0: return launch_gemv_q5_0(w, g, a, t_rows, out, mode, s);
+    case T_Q4_1: return launch_gemv_q4_1(w, g, a, t_rows, out, mode, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -318,7 +372,9 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
 bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode, bool with_norm) {
     if (!gpu_supports(dtype, n_cols, mode)) return false;
     if (dtype == T_Q6_K && mode == 0) return false;  // EXACT Q6_K is not the activation-stationary kernel
-    if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q5_K && dtype != T_Q6_K) return false;
+    if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q5_K && dtype != T_Q6_K &&
+        dtype != T_Q5_0 && dtype != T_Q4_1)
+        return false;
     // the normalizing forms hold the row's sum-of-squares tasks (8 values
     // each) in two per thread
     return !with_norm || n_cols / 8 <= (size_t)(2 * nt_for(units_per_row(dtype, n_cols)));
@@ -352,6 +408,8 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
     case T_Q4_K: return launch_gemv_fx_q4_k(f, g, a, mode, s);
     case T_Q5_K: return launch_gemv_fx_q5_k(f, g, a, mode, s);
     case T_Q6_K: return launch_gemv_fx_q6_k(f, g, a, mode, s);
+    case T_Q5_0: return launch_gemv_fx_q5_0(f, g, a, mode, s);
+    case T_Q4_1: return launch_gemv_fx_q4_1(f, g, a, mode, s);
     default: return hipErrorInvalidValue;
     }
 }

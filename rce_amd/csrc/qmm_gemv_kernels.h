@@ -130,6 +130,8 @@ struct RawQ8_0 { uint4 q0, q1; uint32_t s; };
 struct RawQ4_K { uint4 h, q0, q1; };
 struct RawQ6_K { uint4 c[13]; uint32_t d; };
 struct RawQ5_K { uint4 h, q0, q1; uint2 hb; };
+struct RawQ5_0 { uint4 q; uint32_t s, h; };
+struct RawQ4_1 { uint4 q; uint32_t sm; };
 
 __device__ __forceinline__ RawQ4_0 ld_q4_0(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
@@ -164,6 +166,23 @@ __device__ __forceinline__ RawQ5_K ld_q5_k(const DevWeight &w, size_t row, int c
     r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
     r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
     r.hb = *reinterpret_cast<const uint2 *>(rp + w.plane3 + 8 * (size_t)col);
+    return r;
+}
+
+__device__ __forceinline__ RawQ5_0 ld_q5_0(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ5_0 r;
+    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    r.h = *reinterpret_cast<const uint32_t *>(rp + w.plane2 + 4 * (size_t)col);
+    return r;
+}
+
+__device__ __forceinline__ RawQ4_1 ld_q4_1(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ4_1 r;
+    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
+    r.sm = *reinterpret_cast<const uint32_t *>(rp + 4 * (size_t)col);
     return r;
 }
 
@@ -422,6 +441,117 @@ struct Q8_0Exact {
     }
 };
 
+// Q5_0 block, EXACT (rce-op-qmm/src/lib.rs L331-352, L525-561): Q4_0's
+// order with 5-bit values: position j (< 16: low nibble of qs byte j,
+// else high nibble of byte j - 16) takes bit j of qh as its fifth bit, and
+// the value is that minus 16.
+template <int TB>
+struct Q5_0Exact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ5_0;
+    float av[TB][32];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q5_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++)
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float sub[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) sub[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = wrd(r.q, i);
+            const uint32_t lo = and_opaque(x, NIB) | spread4_bit4((r.h >> (4 * i)) & 0xFu);
+            const uint32_t hi = and_opaque(x >> 4, NIB) | spread4_bit4((r.h >> (16 + 4 * i)) & 0xFu);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float nl = (float)((lo >> (8 * j)) & 0xFFu), nh = (float)((hi >> (8 * j)) & 0xFFu);
+                if constexpr (TB == 1) {  // (n - 16) a as fma(n, a, -16a): one rounding, like the product
+                    sub[0] = sub[0] + __builtin_fmaf(nl, av[0][4 * i + j], -16.0f * av[0][4 * i + j]);
+                    sub[0] = sub[0] + __builtin_fmaf(nh, av[0][4 * i + j + 16], -16.0f * av[0][4 * i + j + 16]);
+                } else {
+                    const float vl = nl - 16.0f, vh = nh - 16.0f;  // exact
+#pragma unroll
+                    for (int t = 0; t < TB; t++) {
+                        sub[t] = sub[t] + vl * av[t][4 * i + j];
+                        sub[t] = sub[t] + vh * av[t][4 * i + j + 16];
+                    }
+                }
+            }
+        }
+        const float scale = h2f(r.s);
+#pragma unroll
+        for (int t = 0; t < TB; t++) out[t] = scale * sub[t];
+    }
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float g[32];
+        load_f32x(gw + 32 * (size_t)col, g, 32);
+#pragma unroll
+        for (int l = 0; l < 32; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
+    }
+};
+
+// Q4_1 block, EXACT (rce-op-qmm/src/lib.rs L615-645): va over q in 0..16
+// of (v0 a[q] + v1 a[q+16]) and asum of (a[q] + a[q+16]), both from +0.0;
+// addend = scale va + min asum.  asum does not depend on the row and is
+// formed once per thread, in the same order.
+template <int TB>
+struct Q4_1Exact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ4_1;
+    float av[TB][32];
+    float as[TB];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_1(w, row, col); }
+    __device__ void sums() {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            as[t] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) as[t] = as[t] + (av[t][q] + av[t][q + 16]);
+        }
+    }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++)
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+        sums();
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float va[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) va[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = wrd(r.q, i);
+            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float nl = (float)((lo >> (8 * j)) & 0xFFu), nh = (float)((hi >> (8 * j)) & 0xFFu);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    const float p = nl * av[t][4 * i + j], q = nh * av[t][4 * i + j + 16];
+                    va[t] = va[t] + (p + q);
+                }
+            }
+        }
+        const float scale = h2f(r.sm & 0xFFFFu), mn = h2f(r.sm >> 16);
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const float u = scale * va[t], v = mn * as[t];
+            out[t] = u + v;
+        }
+    }
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float g[32];
+        load_f32x(gw + 32 * (size_t)col, g, 32);
+#pragma unroll
+        for (int l = 0; l < 32; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
+        sums();
+    }
+};
+
 // Q4_K group g of a super-block, EXACT (rce-op-qmm/src/lib.rs L354-385,
 // L730-781): va_lo, a_lo, va_hi, a_hi over l in 0..32 from +0.0, then
 // ((d1 va_lo - min1 a_lo) + d2 va_hi) - min2 a_hi.  a_lo and a_hi do not
@@ -563,16 +693,29 @@ struct Q5_KExact {
     }
 };
 
-// Q4_0 / Q8_0 block, Q8: sub = dx * isum, addend = scale * sub.
-template <int TB, bool IS_Q4>
+// Blocks of 32, Q8.  Q4_0 / Q8_0 / Q5_0: sub = dx * isum, addend =
+// scale * sub (the offsets 8 and 16 enter isum as -8 xs, -16 xs, with xs
+// the sum of the block's xq).  Q4_1: va = dx * isum over the raw nibbles,
+// a = dx * xs, addend = scale va + min a.
+enum Blk32 { B32_Q8_0, B32_Q4_0, B32_Q5_0, B32_Q4_1 };
+template <int KIND> struct Blk32Raw;
+template <> struct Blk32Raw<B32_Q8_0> { using T = RawQ8_0; };
+template <> struct Blk32Raw<B32_Q4_0> { using T = RawQ4_0; };
+template <> struct Blk32Raw<B32_Q5_0> { using T = RawQ5_0; };
+template <> struct Blk32Raw<B32_Q4_1> { using T = RawQ4_1; };
+
+template <int TB, int KIND>
 struct Q32Q8 {
     static constexpr int NTOK = TB;
-    using Raw = typename std::conditional<IS_Q4, RawQ4_0, RawQ8_0>::type;
+    static constexpr bool IS_Q4 = KIND == B32_Q4_0;
+    using Raw = typename Blk32Raw<KIND>::T;
     int xq[TB][8];
     float dx[TB];
     int xs[TB];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) {
-        if constexpr (IS_Q4) return ld_q4_0(w, row, col);
+        if constexpr (KIND == B32_Q4_0) return ld_q4_0(w, row, col);
+        else if constexpr (KIND == B32_Q5_0) return ld_q5_0(w, row, col);
+        else if constexpr (KIND == B32_Q4_1) return ld_q4_1(w, row, col);
         else return ld_q8_0(w, row, col);
     }
     __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
@@ -590,8 +733,35 @@ struct Q32Q8 {
         }
     }
     __device__ void addends(const Raw &r, float *out) const {
-        const float scale = h2f(r.s);
-        if constexpr (IS_Q4) {
+        if constexpr (KIND == B32_Q5_0 || KIND == B32_Q4_1) {
+            int lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (int)(wrd(r.q, i) & NIB);
+                hi[i] = (int)((wrd(r.q, i) >> 4) & NIB);
+                if constexpr (KIND == B32_Q5_0) {
+                    lo[i] |= (int)spread4_bit4((r.h >> (4 * i)) & 0xFu);
+                    hi[i] |= (int)spread4_bit4((r.h >> (16 + 4 * i)) & 0xFu);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                int acc = 0;  // the 5-bit values are 0..31: positive as signed bytes
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(lo[i], xq[t][i], acc, false);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_sdot4(hi[i], xq[t][4 + i], acc, false);
+                if constexpr (KIND == B32_Q5_0) {
+                    const float sub = dx[t] * (float)(acc - 16 * xs[t]);
+                    out[t] = h2f(r.s) * sub;
+                } else {
+                    const float va = dx[t] * (float)acc, a = dx[t] * (float)xs[t];
+                    const float u = h2f(r.sm & 0xFFFFu) * va, v = h2f(r.sm >> 16) * a;
+                    out[t] = u + v;
+                }
+            }
+        } else if constexpr (IS_Q4) {
+            const float scale = h2f(r.s);
             int lo[4], hi[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) { lo[i] = (int)(wrd(r.q, i) & NIB); hi[i] = (int)((wrd(r.q, i) >> 4) & NIB); }
@@ -606,6 +776,7 @@ struct Q32Q8 {
                 out[t] = scale * sub;
             }
         } else {
+            const float scale = h2f(r.s);
 #pragma unroll
             for (int t = 0; t < TB; t++) {
                 int acc = 0;
@@ -984,7 +1155,7 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
 
 inline int units_per_row(uint32_t dtype, size_t n_cols) {
     switch (dtype) {
-    case T_Q4_0: case T_Q8_0: return (int)(n_cols / 32);
+    case T_Q4_0: case T_Q8_0: case T_Q5_0: case T_Q4_1: return (int)(n_cols / 32);
     case T_Q4_K: case T_Q5_K: return (int)(n_cols / 64);
     case T_Q6_K: return (int)(n_cols / 256);
     default: return 0;
@@ -1130,8 +1301,10 @@ hipError_t launch_as_tb(const DevWeight &w, const GemvGeom &g, const float *a, s
     }
 }
 
-template <int TB> using Q4_0Q8 = Q32Q8<TB, true>;
-template <int TB> using Q8_0Q8 = Q32Q8<TB, false>;
+template <int TB> using Q4_0Q8 = Q32Q8<TB, B32_Q4_0>;
+template <int TB> using Q8_0Q8 = Q32Q8<TB, B32_Q8_0>;
+template <int TB> using Q5_0Q8 = Q32Q8<TB, B32_Q5_0>;
+template <int TB> using Q4_1Q8 = Q32Q8<TB, B32_Q4_1>;
 
 
 }  // namespace

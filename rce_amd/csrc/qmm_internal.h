@@ -40,6 +40,12 @@ enum Layout : int {
     // position l, bit 32 + l = that of position 32 + l (the two qh bits of
     // the group, 2g and 2g + 1, of qh byte l).
     LAYOUT_SPLIT_Q5_K = 5,
+    // Q5_0: LAYOUT_SPLIT_Q4_0's scales and nibble plane, plus the blocks'
+    // 4-byte qh words at plane2 + 4 b; rows padded to 16 B.
+    LAYOUT_SPLIT_Q5_0 = 6,
+    // Q4_1: the blocks' (d, m) f16 pairs as 4-byte words, padded to 16,
+    // then the 16 B of nibbles per block at plane1 + 16 b.
+    LAYOUT_SPLIT_Q4_1 = 7,
 };
 
 struct DevWeight {
@@ -49,7 +55,7 @@ struct DevWeight {
     size_t n_rows, n_cols;
     size_t row_stride;    // SPLIT: bytes between rows
     size_t plane1;        // SPLIT: offset of the first 16-B plane in a row
-    size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K / SPLIT_Q5_K: offset of the second plane
+    size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K / SPLIT_Q5_K / SPLIT_Q5_0: offset of the second plane
     size_t plane3;        // SPLIT_Q5_K: offset of the high-bit words
     size_t group_stride;  // IL64: bytes between 64-row groups
 };
@@ -133,6 +139,8 @@ hipError_t launch_gemv_fx_q8_0(const FxLaunch &f, const GemvGeom &g, const float
 hipError_t launch_gemv_fx_q4_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q5_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q6_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q5_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q4_1(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 
 // ---- decode step (decoder.hip) ----
 // x = dequant_row(w, *row_dev) (QuantWeight::dequant_row); an id outside
@@ -184,6 +192,10 @@ hipError_t launch_gemv_q4_k(const DevWeight &w, const GemvGeom &g, const float *
 hipError_t launch_gemv_q5_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q5_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q4_1(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
 

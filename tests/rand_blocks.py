@@ -1,0 +1,18 @@
+"""Random GGUF blocks for formats the reference ships no quantizer for
+(Q5_0, Q4_1): random qs/qh bytes (every bit pattern) with f16 scales of
+magnitude dmax/32..dmax of both signs, and for Q4_1 mins in (-2 dmax, 2 dmax)."""
+import numpy as np
+
+import oracle as O
+
+
+def rand_blocks(rng, dt, n, k, dmax=2.0 ** -4):
+    nb = k // 32
+    bb = O.BLOCK[dt][1]
+    b = rng.integers(0, 256, size=(n * nb, bb), dtype=np.uint8)
+    d = (rng.uniform(dmax / 32, dmax, n * nb) * rng.choice([-1.0, 1.0], n * nb)).astype(np.float16)
+    b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    if dt == O.Q4_1:
+        m = rng.uniform(-2 * dmax, 2 * dmax, n * nb).astype(np.float16)
+        b[:, 2:4] = m.view(np.uint8).reshape(-1, 2)
+    return b.reshape(-1)

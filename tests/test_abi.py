@@ -48,7 +48,8 @@ def test_supports_matrix():
     assert not rce_amd.supports(G.Q4_0, 4100)        # not a block multiple
     assert not rce_amd.supports(G.Q4K, 4096 + 32)     # K-quants need 256
     assert rce_amd.supports(G.Q5K, 4096) and rce_amd.supports(G.Q5K, 4096, M.Q8)
-    assert not rce_amd.supports(G.Q3K, 4096)          # no kernel yet -> CPU path
+    assert rce_amd.supports(G.Q5_0, 96) and rce_amd.supports(G.Q4_1, 4096, M.Q8)
+    assert not rce_amd.supports(G.Q3K, 4096)          # no kernel yet: reported unsupported
     assert not rce_amd.supports(99, 4096)
 
 

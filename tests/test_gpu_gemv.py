@@ -12,6 +12,7 @@ import pytest
 import oracle as O
 import rce_amd
 from rce_amd import GgufDtype as G, Mode
+from rand_blocks import rand_blocks
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
@@ -23,6 +24,8 @@ def note(msg):
 
 
 def make(rng, dt, n, k, sigma=0.02):
+    if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks
+        return rand_blocks(rng, dt, n, k)
     w = (rng.standard_normal((n, k)) * sigma).astype(F32)
     return O.quantize(w, dt)
 
@@ -38,6 +41,8 @@ SHAPES = {
     O.Q4_K: [(1, 256), (5, 512), (130, 2048), (2048, 5632), (4096, 4096)],
     O.Q5_K: [(1, 256), (7, 512), (129, 2048), (2048, 5632), (4096, 4096)],
     O.Q6_K: [(1, 256), (64, 256), (100, 512), (256, 2048), (32000, 2048)],
+    O.Q5_0: [(1, 32), (5, 96), (77, 1024), (1024, 2048), (4096, 4096)],
+    O.Q4_1: [(1, 32), (9, 160), (65, 1024), (2048, 2048), (4096, 4096)],
 }
 CASES = [(dt, n, k) for dt, shapes in SHAPES.items() for (n, k) in shapes]
 
@@ -56,7 +61,7 @@ def test_mm_1d_exact_bit_identical(ctx, dt, n, k):
     assert np.array_equal(bits(serial), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K])
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1])
 @pytest.mark.parametrize("t_rows", [2, 8])
 def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
     n, k = (700, 2048) if dt != O.Q4_0 else (11008, 4096)
@@ -83,7 +88,8 @@ def run_dev(ctx, w, x, mode, a_dtype=G.F32):
 
 Q8_CASES = [(O.Q8_0, 4096, 4096), (O.Q4_0, 11008, 4096), (O.Q4_0, 4096, 14336), (O.Q4_K, 4096, 4096),
             (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256),
-            (O.Q5_K, 4096, 4096), (O.Q5_K, 2048, 5632), (O.Q5_K, 9, 256)]
+            (O.Q5_K, 4096, 4096), (O.Q5_K, 2048, 5632), (O.Q5_K, 9, 256), (O.Q5_0, 4096, 4096), (O.Q5_0, 13, 96),
+            (O.Q4_1, 4096, 4096), (O.Q4_1, 11, 160)]
 
 
 @pytest.mark.parametrize("dt,n,k", Q8_CASES)
@@ -114,7 +120,7 @@ def test_f16_activations_are_widened_exactly(ctx):
 
 
 @pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q5_K, 35, 1024),
-                                    (O.Q6_K, 130, 512)])
+                                    (O.Q6_K, 130, 512), (O.Q5_0, 21, 96), (O.Q4_1, 19, 160)])
 def test_dequant_row_bit_identical(ctx, dt, n, k):
     rng = np.random.default_rng(5000 + dt)
     b = make(rng, dt, n, k)
@@ -126,7 +132,7 @@ def test_dequant_row_bit_identical(ctx, dt, n, k):
         assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q4_0, O.Q6_K])
+@pytest.mark.parametrize("dt", [O.Q4_0, O.Q6_K, O.Q5_0])
 def test_sub_view_addresses_stacked_experts(ctx, dt):
     # split_experts (rce-qwen36-moe L216-223): sub_view(e*bpe, bpe, rows, cols)
     rng = np.random.default_rng(6000 + dt)
