@@ -862,6 +862,9 @@ EXPORT void orc_matmul_k(const float *x, size_t m, size_t k, const int32_t *q, s
  *   Q8_0, Q4_0, Q5_0 : sub = dx * isum;      sumf += scale * sub
  *   Q4_1       : va = dx * isum, a = dx * xsum (isum over the raw
  *                nibbles 0..15); sumf += scale * va + min * a
+ *   Q3_K       : per 32 values (outer, j) of lib.rs L840-928, the two
+ *                halves of 16 get s1 = dx * isum1, s2 = dx * isum2;
+ *                sumf += dl1 * s1 + dl2 * s2
  *   Q4_K, Q5_K : va = dx * isum, a = dx * xsum (xsum = sum of xq);
  *                sumf += d1*va_lo - min1*a_lo + d2*va_hi - min2*a_hi
  *                (Q5_K: the 5-bit values of lib.rs L388-422)
@@ -951,6 +954,30 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
                 sumf += tt;
             }
         }
+    } else if (t == T_Q3_K) {
+        for (size_t ib = 0; ib < k / 256; ib++) {
+            const uint8_t *s = r + ib * 110, *hmask = s, *qs = s + 32;
+            float d_all = rd_f16(s + 108);
+            int8_t scales[16];
+            q3k_scales(s + 96, scales);
+            for (int outer = 0; outer < 2; outer++)
+                for (int jj = 0; jj < 4; jj++) {
+                    const int is = 8 * outer + 2 * jj, shift = 2 * jj;
+                    const uint8_t m = (uint8_t)(1u << (4 * outer + jj));
+                    const size_t b = ib * 8 + (size_t)(4 * outer + jj);  /* the block of 32 */
+                    const int8_t *xb = xq + b * 32;
+                    int32_t i1 = 0, i2 = 0;
+                    for (int l = 0; l < 16; l++) {
+                        i1 += (((qs[32 * outer + l] >> shift) & 3) - ((hmask[l] & m) ? 0 : 4)) * xb[l];
+                        i2 += (((qs[32 * outer + 16 + l] >> shift) & 3) - ((hmask[16 + l] & m) ? 0 : 4)) * xb[16 + l];
+                    }
+                    float dl1 = d_all * (float)(scales[is] - 32), dl2 = d_all * (float)(scales[is + 1] - 32);
+                    float s1 = dx[b] * (float)i1, s2 = dx[b] * (float)i2;
+                    float tt = dl1 * s1;
+                    tt = tt + dl2 * s2;
+                    sumf += tt;
+                }
+        }
     } else if (t == T_Q6_K) {
         for (size_t ib = 0; ib < k / 256; ib++) {
             const uint8_t *s = r + ib * 210;
@@ -976,7 +1003,8 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
 EXPORT int orc_mm_batched_q8(const float *a, size_t t_rows, const uint8_t *w, uint32_t t,
                              size_t n_rows, size_t n_cols, float *out, int threads) {
     uint32_t qk, bb;
-    if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q5_0 && t != T_Q4_1 && t != T_Q4_K && t != T_Q5_K && t != T_Q6_K)
+    if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q5_0 && t != T_Q4_1 && t != T_Q3_K && t != T_Q4_K && t != T_Q5_K &&
+        t != T_Q6_K)
         return -1;
     if (orc_block_geometry(t, &qk, &bb) || n_cols % qk) return -2;
     size_t row_bytes = n_cols / qk * bb;

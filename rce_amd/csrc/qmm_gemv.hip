@@ -17,7 +17,8 @@ __global__ void k_f16_to_f32(const uint16_t *__restrict__ s, float *__restrict__
 }
 
 // dequant.rs L360-382 (Q4_0), L385-433 (Q4_1, Q5_0), L438-454 (Q8_0),
-// L546-589 (Q4_K), L606-655 (Q5_K), L658-701 (Q6_K): value i of row `row`.
+// L468-543 (Q3_K), L546-589 (Q4_K), L606-655 (Q5_K), L658-701 (Q6_K): value
+// i of row `row`.
 __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
     float v = 0.0f;
     if (w.dtype == T_Q4_0 || w.dtype == T_Q8_0) {
@@ -48,6 +49,17 @@ __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
             const float t = (float)nib * h2f(sm & 0xFFFFu);
             v = t + h2f(sm >> 16);
         }
+    } else if (w.dtype == T_Q3_K) {  // dl * (float)q with q = low - (high ? 0 : 4)
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t u = i / 32;
+        const int p = (int)(i % 32), h = p / 16, q = p % 16;
+        const uint32_t lw = *reinterpret_cast<const uint32_t *>(rp + w.plane1 + 8 * u + 4 * h);
+        const uint32_t hw = *reinterpret_cast<const uint32_t *>(rp + w.plane2 + 4 * u);
+        const int8_t sc = *reinterpret_cast<const int8_t *>(rp + w.plane3 + 2 * u + h);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 2 * (u / 8)));
+        const int low = (int)((lw >> (8 * (q % 4) + 2 * (q / 4))) & 3u), high = (int)((hw >> p) & 1u);
+        const float dl = d * (float)sc;
+        v = dl * (float)(low - (high ? 0 : 4));
     } else if (w.dtype == T_Q4_K) {
         const uint8_t *rp = w.base + row * w.row_stride;
         const size_t sb = i / 256;
@@ -130,6 +142,8 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
     case T_Q4_K:
     case T_Q5_K:
         return n_cols % 256 == 0 && n_cols / 64 <= 1024;
+    case T_Q3_K:
+        return n_cols % 256 == 0 && n_cols / 32 <= 1024;
     case T_Q6_K:
         return n_cols % 256 == 0 && n_cols / 256 <= 1024;
     default:
@@ -179,6 +193,13 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane2 = 0;
         dw.row_stride = dw.plane1 + 16 * (k / 32);
         return dw.row_stride * n;
+    case T_Q3_K:
+        dw.layout = LAYOUT_SPLIT_Q3_K;
+        dw.plane1 = pad16(2 * (k / 256));
+        dw.plane2 = dw.plane1 + 8 * (k / 32);
+        dw.plane3 = dw.plane2 + 4 * (k / 32);
+        dw.row_stride = pad16(dw.plane3 + 2 * (k / 32));
+        return dw.row_stride * n;
     case T_Q6_K:
         dw.layout = LAYOUT_IL64_Q6_K;
         dw.group_stride = (k / 256) * IL64_Q6K_SB;
@@ -225,6 +246,41 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
                     for (int i = 0; i < 4; i++) d[4 * b + i] = blk[i];
                 }
                 for (int i = 0; i < 16; i++) d[dw.plane1 + 16 * b + i] = blk[bb - 16 + i];
+            }
+        }
+        break;
+    }
+    case LAYOUT_SPLIT_Q3_K: {  // block: hmask[32], qs[64], scales[12], d
+        const size_t nsb = k / 256;
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * nsb * 110;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t sb = 0; sb < nsb; sb++) {
+                const uint8_t *blk = s + sb * 110, *hmask = blk, *qs = blk + 32, *sp = blk + 96;
+                d[2 * sb] = blk[108];
+                d[2 * sb + 1] = blk[109];
+                int sc[16];  // the 6-bit scales (dequant.rs L486-504)
+                for (int g = 0; g < 16; g++)
+                    sc[g] = ((g < 8 ? sp[g] & 0xF : sp[g - 8] >> 4) | (((sp[8 + g % 4] >> (2 * (g / 4))) & 3) << 4));
+                for (int o = 0; o < 2; o++)
+                    for (int j = 0; j < 4; j++) {
+                        const size_t u = 8 * sb + 4 * o + j;
+                        uint32_t lw[2] = {0, 0}, hw = 0;
+                        for (int h = 0; h < 2; h++)
+                            for (int q = 0; q < 16; q++) {
+                                const uint32_t low = (qs[32 * o + 16 * h + q] >> (2 * j)) & 3u;
+                                const uint32_t high = (hmask[16 * h + q] >> (4 * o + j)) & 1u;
+                                lw[h] |= low << (8 * (q % 4) + 2 * (q / 4));
+                                hw |= high << (16 * h + q);
+                            }
+                        for (int b = 0; b < 4; b++) {
+                            d[dw.plane1 + 8 * u + b] = (uint8_t)(lw[0] >> (8 * b));
+                            d[dw.plane1 + 8 * u + 4 + b] = (uint8_t)(lw[1] >> (8 * b));
+                            d[dw.plane2 + 4 * u + b] = (uint8_t)(hw >> (8 * b));
+                        }
+                        d[dw.plane3 + 2 * u] = (uint8_t)(int8_t)(sc[2 * (4 * o + j)] - 32);
+                        d[dw.plane3 + 2 * u + 1] = (uint8_t)(int8_t)(sc[2 * (4 * o + j) + 1] - 32);
+                    }
             }
         }
         break;
@@ -303,6 +359,7 @@ static size_t unit_bytes(uint32_t dtype) {
     case T_Q8_0: return 34;
     case T_Q5_0: return 22;
     case T_Q4_1: return 20;
+    case T_Q3_K: return 14;  // 13.75: an eighth of the 110 B super-block
     case T_Q4_K: return 36;
     case T_Q5_K: return 44;
     case T_Q6_K: return 210;
@@ -365,6 +422,7 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
     case T_Q6_K: return launch_gemv_q6_k(w, g, a, t_rows, out, mode, s);
     case T_Q5_0: return launch_gemv_q5_0(w, g, a, t_rows, out, mode, s);
     case T_Q4_1: return launch_gemv_q4_1(w, g, a, t_rows, out, mode, s);
+    case T_Q3_K: return launch_gemv_q3_k(w, g, a, t_rows, out, mode, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -373,7 +431,7 @@ bool gemv_fx_supports(uint32_t dtype, size_t n_cols, int mode, bool with_norm) {
     if (!gpu_supports(dtype, n_cols, mode)) return false;
     if (dtype == T_Q6_K && mode == 0) return false;  // EXACT Q6_K is not the activation-stationary kernel
     if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q5_K && dtype != T_Q6_K &&
-        dtype != T_Q5_0 && dtype != T_Q4_1)
+        dtype != T_Q5_0 && dtype != T_Q4_1 && dtype != T_Q3_K)
         return false;
     // the normalizing forms hold the row's sum-of-squares tasks (8 values
     // each) in two per thread
@@ -410,6 +468,7 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
     case T_Q6_K: return launch_gemv_fx_q6_k(f, g, a, mode, s);
     case T_Q5_0: return launch_gemv_fx_q5_0(f, g, a, mode, s);
     case T_Q4_1: return launch_gemv_fx_q4_1(f, g, a, mode, s);
+    case T_Q3_K: return launch_gemv_fx_q3_k(f, g, a, mode, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -132,6 +132,7 @@ struct RawQ6_K { uint4 c[13]; uint32_t d; };
 struct RawQ5_K { uint4 h, q0, q1; uint2 hb; };
 struct RawQ5_0 { uint4 q; uint32_t s, h; };
 struct RawQ4_1 { uint4 q; uint32_t sm; };
+struct RawQ3_K { uint2 q; uint32_t h; uint32_t sd; };  // sd: scales (bytes 0, 1), d (bits 16..31)
 
 __device__ __forceinline__ RawQ4_0 ld_q4_0(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
@@ -184,6 +185,27 @@ __device__ __forceinline__ RawQ4_1 ld_q4_1(const DevWeight &w, size_t row, int c
     r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
     r.sm = *reinterpret_cast<const uint32_t *>(rp + 4 * (size_t)col);
     return r;
+}
+
+__device__ __forceinline__ RawQ3_K ld_q3_k(const DevWeight &w, size_t row, int col) {
+    const uint8_t *rp = w.base + row * w.row_stride;
+    RawQ3_K r;
+    r.q = *reinterpret_cast<const uint2 *>(rp + w.plane1 + 8 * (size_t)col);
+    r.h = *reinterpret_cast<const uint32_t *>(rp + w.plane2 + 4 * (size_t)col);
+    const uint32_t sc = *reinterpret_cast<const uint16_t *>(rp + w.plane3 + 2 * (size_t)col);
+    const uint32_t d = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)(col >> 3));
+    r.sd = sc | (d << 16);
+    return r;
+}
+
+// Four bits b0..b3 of t (t < 16) to bit 2 of bytes 0..3 (see spread4_bit4).
+__device__ __forceinline__ uint32_t spread4_bit2(uint32_t t) { return ((t * 0x00204081u) & 0x01010101u) << 2; }
+
+// The 3-bit values (low | high << 2, the reference's value + 4) of
+// positions 16 h + 4 i .. + 3 of a Q3_K unit, one per byte.
+__device__ __forceinline__ uint32_t q3_vals(const RawQ3_K &r, int h, int i) {
+    const uint32_t w = h ? r.q.y : r.q.x;
+    return ((w >> (2 * i)) & 0x03030303u) | spread4_bit2((r.h >> (16 * h + 4 * i)) & 0xFu);
 }
 
 // Four bits b0..b3 of t (t < 16) to bit 4 of bytes 0..3: t * 0x00204081
@@ -552,6 +574,61 @@ struct Q4_1Exact {
     }
 };
 
+// Q3_K unit (outer o, j) of a super-block, EXACT (rce-op-qmm/src/lib.rs
+// L840-928): s1 over l < 16 of q a[l], s2 over l < 16 of q a[16 + l], both
+// from +0.0 with q = (low | high << 2) - 4; addend = dl1 s1 + dl2 s2 with
+// dl = d * (scale - 32).
+template <int TB>
+struct Q3_KExact {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ3_K;
+    float av[TB][32];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q3_k(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++)
+            load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float s1[TB], s2[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) { s1[t] = 0.0f; s2[t] = 0.0f; }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v1 = q3_vals(r, 0, i), v2 = q3_vals(r, 1, i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float n1 = (float)((v1 >> (8 * j)) & 0xFFu), n2 = (float)((v2 >> (8 * j)) & 0xFFu);
+                const int p = 4 * i + j;
+                if constexpr (TB == 1) {  // (n - 4) a as fma(n, a, -4a): one rounding, like the product
+                    s1[0] = s1[0] + __builtin_fmaf(n1, av[0][p], -4.0f * av[0][p]);
+                    s2[0] = s2[0] + __builtin_fmaf(n2, av[0][16 + p], -4.0f * av[0][16 + p]);
+                } else {
+                    const float q1 = n1 - 4.0f, q2 = n2 - 4.0f;  // exact
+#pragma unroll
+                    for (int t = 0; t < TB; t++) {
+                        s1[t] = s1[t] + q1 * av[t][p];
+                        s2[t] = s2[t] + q2 * av[t][16 + p];
+                    }
+                }
+            }
+        }
+        const float d = h2f(r.sd >> 16);
+        const float dl1 = d * (float)(int8_t)(r.sd & 0xFFu), dl2 = d * (float)(int8_t)((r.sd >> 8) & 0xFFu);
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const float u = dl1 * s1[t], v = dl2 * s2[t];
+            out[t] = u + v;
+        }
+    }
+    __device__ void normalize(const float *gw, int col, float inv) {
+        float g[32];
+        load_f32x(gw + 32 * (size_t)col, g, 32);
+#pragma unroll
+        for (int l = 0; l < 32; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
+    }
+};
+
 // Q4_K group g of a super-block, EXACT (rce-op-qmm/src/lib.rs L354-385,
 // L730-781): va_lo, a_lo, va_hi, a_hi over l in 0..32 from +0.0, then
 // ((d1 va_lo - min1 a_lo) + d2 va_hi) - min2 a_hi.  a_lo and a_hi do not
@@ -787,6 +864,52 @@ struct Q32Q8 {
                 const float sub = dx[t] * (float)acc;
                 out[t] = scale * sub;
             }
+        }
+    }
+};
+
+// Q3_K unit, Q8: s1 = dx * isum1, s2 = dx * isum2 over the two halves of
+// 16 (isum = dot of the 3-bit values with xq, minus 4 times the half's xq
+// sum); addend = dl1 s1 + dl2 s2.
+template <int TB>
+struct Q3_KQ8 {
+    static constexpr int NTOK = TB;
+    using Raw = RawQ3_K;
+    int xq[TB][8];
+    float dx[TB];
+    int xs1[TB], xs2[TB];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q3_k(w, row, col); }
+    __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const bool ok = t < tv;
+            const size_t tt = ok ? (size_t)t : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(L.xq + (tt * k + 32 * (size_t)col) / 4);
+            const int4 a = p[0], b = p[1];
+            const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) xq[t][i] = ok ? v[i] : 0;
+            dx[t] = ok ? L.dx[tt * (k / 32) + col] : 0.0f;
+            xs1[t] = ok ? L.s16[tt * (k / 16) + 2 * col] : 0;
+            xs2[t] = ok ? L.s16[tt * (k / 16) + 2 * col + 1] : 0;
+        }
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        int v1[4], v2[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) { v1[i] = (int)q3_vals(r, 0, i); v2[i] = (int)q3_vals(r, 1, i); }
+        const float d = h2f(r.sd >> 16);
+        const float dl1 = d * (float)(int8_t)(r.sd & 0xFFu), dl2 = d * (float)(int8_t)((r.sd >> 8) & 0xFFu);
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            int a1 = 0, a2 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) a1 = __builtin_amdgcn_sdot4(v1[i], xq[t][i], a1, false);
+#pragma unroll
+            for (int i = 0; i < 4; i++) a2 = __builtin_amdgcn_sdot4(v2[i], xq[t][4 + i], a2, false);
+            const float s1 = dx[t] * (float)(a1 - 4 * xs1[t]), s2 = dx[t] * (float)(a2 - 4 * xs2[t]);
+            const float u = dl1 * s1, v = dl2 * s2;
+            out[t] = u + v;
         }
     }
 };
@@ -1155,7 +1278,7 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
 
 inline int units_per_row(uint32_t dtype, size_t n_cols) {
     switch (dtype) {
-    case T_Q4_0: case T_Q8_0: case T_Q5_0: case T_Q4_1: return (int)(n_cols / 32);
+    case T_Q4_0: case T_Q8_0: case T_Q5_0: case T_Q4_1: case T_Q3_K: return (int)(n_cols / 32);
     case T_Q4_K: case T_Q5_K: return (int)(n_cols / 64);
     case T_Q6_K: return (int)(n_cols / 256);
     default: return 0;

@@ -46,6 +46,14 @@ enum Layout : int {
     // Q4_1: the blocks' (d, m) f16 pairs as 4-byte words, padded to 16,
     // then the 16 B of nibbles per block at plane1 + 16 b.
     LAYOUT_SPLIT_Q4_1 = 7,
+    // Q3_K, per row: the super-blocks' f16 d, padded to 16; then per unit
+    // u of 32 values (u = 8 sb + 4 o + j, the reference's (outer, j) loop)
+    // at plane1 + 8 u two words of 2-bit low parts (word h holds positions
+    // 16 h + q, q < 16, at bits 8 (q % 4) + 2 (q / 4)), at plane2 + 4 u the
+    // 32 high bits (bit p = position p), at plane3 + 2 u the unit's two
+    // 16-value scales as signed bytes (the 6-bit scale minus 32); rows
+    // padded to 16 B.
+    LAYOUT_SPLIT_Q3_K = 8,
 };
 
 struct DevWeight {
@@ -56,7 +64,7 @@ struct DevWeight {
     size_t row_stride;    // SPLIT: bytes between rows
     size_t plane1;        // SPLIT: offset of the first 16-B plane in a row
     size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K / SPLIT_Q5_K / SPLIT_Q5_0: offset of the second plane
-    size_t plane3;        // SPLIT_Q5_K: offset of the high-bit words
+    size_t plane3;        // SPLIT_Q5_K: offset of the high-bit words; SPLIT_Q3_K: of the scales
     size_t group_stride;  // IL64: bytes between 64-row groups
 };
 
@@ -141,6 +149,7 @@ hipError_t launch_gemv_fx_q5_k(const FxLaunch &f, const GemvGeom &g, const float
 hipError_t launch_gemv_fx_q6_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q5_0(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 hipError_t launch_gemv_fx_q4_1(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
+hipError_t launch_gemv_fx_q3_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 
 // ---- decode step (decoder.hip) ----
 // x = dequant_row(w, *row_dev) (QuantWeight::dequant_row); an id outside
@@ -196,6 +205,8 @@ hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *
 hipError_t launch_gemv_q5_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_gemv_q4_1(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                            int mode, hipStream_t s);
+hipError_t launch_gemv_q3_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
 

@@ -33,9 +33,9 @@ def make_weights(c: dict, seed: int, lin_dtype=O.Q4_K, head_dtype=O.Q6_K, embd_d
     rng = np.random.default_rng(seed)
 
     def q(n, k, dt):
-        if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks of about sigma
+        if dt in (O.Q5_0, O.Q4_1, O.Q3_K):  # no quantizer in the reference: random blocks of about sigma
             from rand_blocks import rand_blocks
-            return rand_blocks(rng, dt, n, k, dmax=sigma / 8), dt
+            return rand_blocks(rng, dt, n, k, dmax=sigma / (32 if dt == O.Q3_K else 8)), dt
         w = (rng.standard_normal((n, k)) * sigma).astype(np.float32)
         return rce_amd.quantize(w, dt), dt
 

@@ -1,12 +1,19 @@
 """Random GGUF blocks for formats the reference ships no quantizer for
-(Q5_0, Q4_1): random qs/qh bytes (every bit pattern) with f16 scales of
-magnitude dmax/32..dmax of both signs, and for Q4_1 mins in (-2 dmax, 2 dmax)."""
+(Q5_0, Q4_1, Q3_K): random qs/qh/hmask/scale bytes (every bit pattern) with
+f16 scales of magnitude dmax/32..dmax of both signs, and for Q4_1 mins in
+(-2 dmax, 2 dmax).  Q3_K's super-block scale d sits at bytes 108..109."""
 import numpy as np
 
 import oracle as O
 
 
 def rand_blocks(rng, dt, n, k, dmax=2.0 ** -4):
+    if dt == O.Q3_K:
+        nsb = k // 256
+        b = rng.integers(0, 256, size=(n * nsb, 110), dtype=np.uint8)
+        d = (rng.uniform(dmax / 32, dmax, n * nsb) * rng.choice([-1.0, 1.0], n * nsb)).astype(np.float16)
+        b[:, 108:110] = d.view(np.uint8).reshape(-1, 2)
+        return b.reshape(-1)
     nb = k // 32
     bb = O.BLOCK[dt][1]
     b = rng.integers(0, 256, size=(n * nb, bb), dtype=np.uint8)

@@ -49,7 +49,9 @@ def test_supports_matrix():
     assert not rce_amd.supports(G.Q4K, 4096 + 32)     # K-quants need 256
     assert rce_amd.supports(G.Q5K, 4096) and rce_amd.supports(G.Q5K, 4096, M.Q8)
     assert rce_amd.supports(G.Q5_0, 96) and rce_amd.supports(G.Q4_1, 4096, M.Q8)
-    assert not rce_amd.supports(G.Q3K, 4096)          # no kernel yet: reported unsupported
+    assert rce_amd.supports(G.Q3K, 4096) and rce_amd.supports(G.Q3K, 512, M.Q8)
+    assert not rce_amd.supports(G.Q3K, 4096 + 32)     # K-quants need 256
+    assert not rce_amd.supports(G.Q2K, 4096)          # not in mm_1d's table either: reported unsupported
     assert not rce_amd.supports(99, 4096)
 
 

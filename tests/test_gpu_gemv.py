@@ -24,7 +24,7 @@ def note(msg):
 
 
 def make(rng, dt, n, k, sigma=0.02):
-    if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks
+    if dt in (O.Q5_0, O.Q4_1, O.Q3_K):  # no quantizer in the reference: random blocks
         return rand_blocks(rng, dt, n, k)
     w = (rng.standard_normal((n, k)) * sigma).astype(F32)
     return O.quantize(w, dt)
@@ -43,6 +43,7 @@ SHAPES = {
     O.Q6_K: [(1, 256), (64, 256), (100, 512), (256, 2048), (32000, 2048)],
     O.Q5_0: [(1, 32), (5, 96), (77, 1024), (1024, 2048), (4096, 4096)],
     O.Q4_1: [(1, 32), (9, 160), (65, 1024), (2048, 2048), (4096, 4096)],
+    O.Q3_K: [(1, 256), (6, 512), (99, 1024), (2048, 2048), (4096, 4096)],
 }
 CASES = [(dt, n, k) for dt, shapes in SHAPES.items() for (n, k) in shapes]
 
@@ -61,7 +62,7 @@ def test_mm_1d_exact_bit_identical(ctx, dt, n, k):
     assert np.array_equal(bits(serial), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1])
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1, O.Q3_K])
 @pytest.mark.parametrize("t_rows", [2, 8])
 def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
     n, k = (700, 2048) if dt != O.Q4_0 else (11008, 4096)
@@ -89,7 +90,7 @@ def run_dev(ctx, w, x, mode, a_dtype=G.F32):
 Q8_CASES = [(O.Q8_0, 4096, 4096), (O.Q4_0, 11008, 4096), (O.Q4_0, 4096, 14336), (O.Q4_K, 4096, 4096),
             (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256),
             (O.Q5_K, 4096, 4096), (O.Q5_K, 2048, 5632), (O.Q5_K, 9, 256), (O.Q5_0, 4096, 4096), (O.Q5_0, 13, 96),
-            (O.Q4_1, 4096, 4096), (O.Q4_1, 11, 160)]
+            (O.Q4_1, 4096, 4096), (O.Q4_1, 11, 160), (O.Q3_K, 4096, 4096), (O.Q3_K, 5, 256)]
 
 
 @pytest.mark.parametrize("dt,n,k", Q8_CASES)
@@ -120,7 +121,7 @@ def test_f16_activations_are_widened_exactly(ctx):
 
 
 @pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q5_K, 35, 1024),
-                                    (O.Q6_K, 130, 512), (O.Q5_0, 21, 96), (O.Q4_1, 19, 160)])
+                                    (O.Q6_K, 130, 512), (O.Q5_0, 21, 96), (O.Q4_1, 19, 160), (O.Q3_K, 17, 512)])
 def test_dequant_row_bit_identical(ctx, dt, n, k):
     rng = np.random.default_rng(5000 + dt)
     b = make(rng, dt, n, k)
@@ -173,7 +174,7 @@ def test_errors_and_empty_inputs(ctx):
         rce_amd.QuantWeight.from_owned_bytes(ctx, b[:-1], O.Q4_0, 8, 64)
     assert e.value.status == 2
     with pytest.raises(rce_amd.QmmError) as e:
-        rce_amd.QuantWeight.from_owned_bytes(ctx, np.zeros(110, np.uint8), G.Q3K, 1, 256)  # no kernel
+        rce_amd.QuantWeight.from_owned_bytes(ctx, np.zeros(84, np.uint8), G.Q2K, 1, 256)  # not in mm_1d either
     assert e.value.status == 3
     with pytest.raises(rce_amd.QmmError):
         rce_amd.mm_1d(np.zeros(63, F32), w)

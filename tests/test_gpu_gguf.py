@@ -12,6 +12,7 @@ import rce_amd
 from rce_amd import GgufFile, Mode, QmmError, QuantWeight
 from gguf_writer import STRING, U32, build_gguf, llama_gguf
 from llama_case import device_model, make_weights, tiny_cfg
+from rand_blocks import rand_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -20,7 +21,8 @@ def note(msg):
     print(msg, flush=True)
 
 
-FORMATS = [(O.Q4_0, 96, 512), (O.Q8_0, 64, 256), (O.Q4_K, 80, 512), (O.Q5_K, 40, 512), (O.Q6_K, 48, 256)]
+FORMATS = [(O.Q4_0, 96, 512), (O.Q8_0, 64, 256), (O.Q4_K, 80, 512), (O.Q5_K, 40, 512), (O.Q6_K, 48, 256),
+           (O.Q5_0, 24, 96), (O.Q4_1, 24, 160), (O.Q3_K, 24, 512)]
 
 
 @pytest.mark.parametrize("align", [32, 64])
@@ -29,7 +31,8 @@ def test_weight_from_gguf_matches_bytes(ctx, align):
     rng = np.random.default_rng(50 + align)
     tens, keep = [], []
     for dt, n, k in FORMATS:
-        b = rce_amd.quantize((rng.standard_normal((n, k)) * 0.05).astype(np.float32), dt)
+        b = (rand_blocks(rng, dt, n, k) if dt in (O.Q5_0, O.Q4_1, O.Q3_K)
+             else rce_amd.quantize((rng.standard_normal((n, k)) * 0.05).astype(np.float32), dt))
         tens.append((f"w.{int(dt)}", (k, n), int(dt), bytes(b)))
         keep.append((dt, n, k, b))
     meta = [("general.alignment", U32, align)] if align != 32 else []

@@ -103,10 +103,10 @@ def test_llama_q5_k_linears(ctx):
     run_pair(ctx, W, Mode.Q8, TOKENS[:5], 1e-3).close()
 
 
-@pytest.mark.parametrize("dt", [O.Q5_0, O.Q4_1])
+@pytest.mark.parametrize("dt", [O.Q5_0, O.Q4_1, O.Q3_K])
 def test_llama_block32_linears(ctx, dt):
-    """Q5_0 / Q4_1 linears (random blocks): the fused q|k|v, gate/up and
-    residual forms on the 32-value units.  (Seed 39 with Q5_0 is a case
+    """Q5_0 / Q4_1 / Q3_K linears (random blocks): the fused q|k|v, gate/up
+    and residual forms on the 32-value units.  (Seed 39 with Q5_0 is a case
     where the oracle's own Q8 decoder moves by 1e-2 at position 2 when eps
     changes by 1e-4 relative: an activation sits on a Q8 rounding boundary,
     and the device's rounding differences move it across.  The seeds here
