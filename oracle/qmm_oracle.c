@@ -999,10 +999,13 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
 }
 
 /* Q8-activation mm_batched: each activation row quantized, then the row
- * formulas above.  Returns -1 for a dtype without a Q8 path. */
+ * formulas above.  The whole-element formats (F32, F16, BF16) take no
+ * quantized activations: their Q8 mode is the reference order.  Returns -1
+ * for a dtype without a Q8 path. */
 EXPORT int orc_mm_batched_q8(const float *a, size_t t_rows, const uint8_t *w, uint32_t t,
                              size_t n_rows, size_t n_cols, float *out, int threads) {
     uint32_t qk, bb;
+    if (t == T_F32 || t == T_F16 || t == T_BF16) return orc_mm_batched(a, t_rows, w, t, n_rows, n_cols, out, threads);
     if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q5_0 && t != T_Q4_1 && t != T_Q3_K && t != T_Q4_K && t != T_Q5_K &&
         t != T_Q6_K)
         return -1;

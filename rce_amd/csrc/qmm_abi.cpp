@@ -264,8 +264,8 @@ rce_qmm_status rce_qmm_weight_sub_view(const rce_qmm_weight *w, size_t byte_offs
     const size_t row0 = byte_offset / rb;
     DevWeight dw = w->dw;
     dw.n_rows = n_rows;
-    if (dw.layout == LAYOUT_IL64_Q6_K) {
-        if (row0 % 64) return fail(RCE_QMM_BAD_SHAPE, "Q6_K sub_view must start on a multiple of 64 rows");
+    if (dw.layout == LAYOUT_IL64_Q6_K || dw.layout == LAYOUT_IL64_ROWS) {
+        if (row0 % 64) return fail(RCE_QMM_BAD_SHAPE, "Q6_K / F32 / F16 / BF16 sub_view must start on a multiple of 64 rows");
         dw.base += (row0 / 64) * dw.group_stride;
     } else {
         dw.base += row0 * dw.row_stride;

@@ -4,6 +4,9 @@
 // f16 widening and row dequantization kernels.
 #include "qmm_gemv_kernels.h"
 
+#include <algorithm>
+#include <cstring>
+
 namespace rce_qmm {
 namespace {
 
@@ -49,6 +52,12 @@ __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
             const float t = (float)nib * h2f(sm & 0xFFFFu);
             v = t + h2f(sm >> 16);
         }
+    } else if (is_whole_element(w.dtype)) {  // dequant.rs L343-356: the value itself
+        const size_t es = w.dtype == T_F32 ? 4 : 2, o = i * es;
+        const uint8_t *p = w.base + (row >> 6) * w.group_stride + ((o / 16) * 64 + (row & 63)) * 16 + o % 16;
+        if (w.dtype == T_F32) v = *reinterpret_cast<const float *>(p);
+        else if (w.dtype == T_F16) v = h2f(*reinterpret_cast<const uint16_t *>(p));
+        else v = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t *>(p) << 16);
     } else if (w.dtype == T_Q3_K) {  // dl * (float)q with q = low - (high ? 0 : 4)
         const uint8_t *rp = w.base + row * w.row_stride;
         const size_t u = i / 32;
@@ -144,6 +153,10 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
         return n_cols % 256 == 0 && n_cols / 64 <= 1024;
     case T_Q3_K:
         return n_cols % 256 == 0 && n_cols / 32 <= 1024;
+    case T_F32:
+    case T_F16:
+    case T_BF16:
+        return n_cols <= ((size_t)1 << 26);
     case T_Q6_K:
         return n_cols % 256 == 0 && n_cols / 256 <= 1024;
     default:
@@ -200,6 +213,12 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane3 = dw.plane2 + 4 * (k / 32);
         dw.row_stride = pad16(dw.plane3 + 2 * (k / 32));
         return dw.row_stride * n;
+    case T_F32:
+    case T_F16:
+    case T_BF16:
+        dw.layout = LAYOUT_IL64_ROWS;
+        dw.group_stride = ((k * (dw.dtype == T_F32 ? 4 : 2) + 15) / 16) * 1024;
+        return dw.group_stride * ((n + 63) / 64);
     case T_Q6_K:
         dw.layout = LAYOUT_IL64_Q6_K;
         dw.group_stride = (k / 256) * IL64_Q6K_SB;
@@ -325,6 +344,16 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
         }
         break;
     }
+    case LAYOUT_IL64_ROWS: {
+        const size_t rb = k * (dw.dtype == T_F32 ? 4 : 2);
+        for (size_t r = 0; r < n; r++) {
+            uint8_t *g = dst + (r >> 6) * dw.group_stride + (r & 63) * 16;
+            const uint8_t *s = src + r * rb;
+            for (size_t c = 0; c * 16 < rb; c++)
+                std::memcpy(g + c * 1024, s + c * 16, std::min<size_t>(16, rb - c * 16));
+        }
+        break;
+    }
     case LAYOUT_IL64_Q6_K: {
         const size_t nsb = k / 256;
         for (size_t r = 0; r < n; r++) {
@@ -413,6 +442,7 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
                        const GemvGeom *geom) {
     if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
     if (mode != 0 && mode != 1) return hipErrorInvalidValue;
+    if (is_whole_element(w.dtype)) return launch_gemv_chain(w, a, t_rows, out, s);
     const GemvGeom g = geom ? *geom : pick_gemv_geom(w, t_rows, mode);
     switch (w.dtype) {
     case T_Q4_0: return launch_gemv_q4_0(w, g, a, t_rows, out, mode, s);

@@ -54,6 +54,10 @@ enum Layout : int {
     // 16-value scales as signed bytes (the 6-bit scale minus 32); rows
     // padded to 16 B.
     LAYOUT_SPLIT_Q3_K = 8,
+    // F32 / F16 / BF16: rows in groups of 64, each row cut into 16-byte
+    // chunks (the last one zero-padded); chunk c of row r at
+    // (c * 64 + r % 64) * 16 within the group's group_stride bytes.
+    LAYOUT_IL64_ROWS = 9,
 };
 
 struct DevWeight {
@@ -209,6 +213,10 @@ hipError_t launch_gemv_q4_1(const DevWeight &w, const GemvGeom &g, const float *
 hipError_t launch_gemv_q3_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
+// F32 / F16 / BF16 (gemv_chain.hip): the reference's one chain per row, in
+// both modes (there is no Q8 form of a whole-element weight).
+hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s);
+__host__ __device__ inline bool is_whole_element(uint32_t dtype) { return dtype == T_F32 || dtype == T_F16 || dtype == T_BF16; }
 
 // Prefill GEMM on the matrix cores (gemm_f16.hip): out[M, n_rows] =
 // A[M, n_cols] . W^T, A binary16, W dequantized to binary16 tiles.

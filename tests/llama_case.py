@@ -33,6 +33,9 @@ def make_weights(c: dict, seed: int, lin_dtype=O.Q4_K, head_dtype=O.Q6_K, embd_d
     rng = np.random.default_rng(seed)
 
     def q(n, k, dt):
+        if dt in (O.F32, O.F16, O.BF16):
+            from rand_blocks import float_bytes
+            return float_bytes(rng, dt, n, k, sigma), dt
         if dt in (O.Q5_0, O.Q4_1, O.Q3_K):  # no quantizer in the reference: random blocks of about sigma
             from rand_blocks import rand_blocks
             return rand_blocks(rng, dt, n, k, dmax=sigma / (32 if dt == O.Q3_K else 8)), dt

@@ -23,3 +23,14 @@ def rand_blocks(rng, dt, n, k, dmax=2.0 ** -4):
         m = rng.uniform(-2 * dmax, 2 * dmax, n * nb).astype(np.float16)
         b[:, 2:4] = m.view(np.uint8).reshape(-1, 2)
     return b.reshape(-1)
+
+
+def float_bytes(rng, dt, n, k, sigma=0.05):
+    """F32 / F16 / BF16 weight bytes of N(0, sigma^2) values (bf16 by
+    truncating the f32 bits)."""
+    w = (rng.standard_normal((n, k)) * sigma).astype(np.float32)
+    if dt == O.F32:
+        return w.view(np.uint8).reshape(-1)
+    if dt == O.F16:
+        return w.astype(np.float16).view(np.uint8).reshape(-1)
+    return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)

@@ -12,7 +12,7 @@ import pytest
 import oracle as O
 import rce_amd
 from rce_amd import GgufDtype as G, Mode
-from rand_blocks import rand_blocks
+from rand_blocks import float_bytes, rand_blocks
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
@@ -26,6 +26,8 @@ def note(msg):
 def make(rng, dt, n, k, sigma=0.02):
     if dt in (O.Q5_0, O.Q4_1, O.Q3_K):  # no quantizer in the reference: random blocks
         return rand_blocks(rng, dt, n, k)
+    if dt in (O.F32, O.F16, O.BF16):
+        return float_bytes(rng, dt, n, k, sigma)
     w = (rng.standard_normal((n, k)) * sigma).astype(F32)
     return O.quantize(w, dt)
 
@@ -44,6 +46,9 @@ SHAPES = {
     O.Q5_0: [(1, 32), (5, 96), (77, 1024), (1024, 2048), (4096, 4096)],
     O.Q4_1: [(1, 32), (9, 160), (65, 1024), (2048, 2048), (4096, 4096)],
     O.Q3_K: [(1, 256), (6, 512), (99, 1024), (2048, 2048), (4096, 4096)],
+    O.F16: [(1, 1), (5, 7), (64, 256), (65, 1000), (2048, 2048), (32000, 2048)],
+    O.BF16: [(1, 8), (3, 100), (130, 2048), (4096, 4096)],
+    O.F32: [(1, 4), (70, 333), (2048, 2048)],
 }
 CASES = [(dt, n, k) for dt, shapes in SHAPES.items() for (n, k) in shapes]
 
@@ -62,7 +67,7 @@ def test_mm_1d_exact_bit_identical(ctx, dt, n, k):
     assert np.array_equal(bits(serial), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1, O.Q3_K])
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1, O.Q3_K, O.F16, O.BF16, O.F32])
 @pytest.mark.parametrize("t_rows", [2, 8])
 def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
     n, k = (700, 2048) if dt != O.Q4_0 else (11008, 4096)
@@ -90,7 +95,8 @@ def run_dev(ctx, w, x, mode, a_dtype=G.F32):
 Q8_CASES = [(O.Q8_0, 4096, 4096), (O.Q4_0, 11008, 4096), (O.Q4_0, 4096, 14336), (O.Q4_K, 4096, 4096),
             (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256),
             (O.Q5_K, 4096, 4096), (O.Q5_K, 2048, 5632), (O.Q5_K, 9, 256), (O.Q5_0, 4096, 4096), (O.Q5_0, 13, 96),
-            (O.Q4_1, 4096, 4096), (O.Q4_1, 11, 160), (O.Q3_K, 4096, 4096), (O.Q3_K, 5, 256)]
+            (O.Q4_1, 4096, 4096), (O.Q4_1, 11, 160), (O.Q3_K, 4096, 4096), (O.Q3_K, 5, 256), (O.F16, 2048, 2048),
+            (O.BF16, 70, 96)]
 
 
 @pytest.mark.parametrize("dt,n,k", Q8_CASES)
@@ -121,7 +127,8 @@ def test_f16_activations_are_widened_exactly(ctx):
 
 
 @pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q5_K, 35, 1024),
-                                    (O.Q6_K, 130, 512), (O.Q5_0, 21, 96), (O.Q4_1, 19, 160), (O.Q3_K, 17, 512)])
+                                    (O.Q6_K, 130, 512), (O.Q5_0, 21, 96), (O.Q4_1, 19, 160), (O.Q3_K, 17, 512),
+                                    (O.F16, 70, 300), (O.BF16, 65, 64), (O.F32, 3, 5)])
 def test_dequant_row_bit_identical(ctx, dt, n, k):
     rng = np.random.default_rng(5000 + dt)
     b = make(rng, dt, n, k)
@@ -133,7 +140,7 @@ def test_dequant_row_bit_identical(ctx, dt, n, k):
         assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q4_0, O.Q6_K, O.Q5_0])
+@pytest.mark.parametrize("dt", [O.Q4_0, O.Q6_K, O.Q5_0, O.F16])
 def test_sub_view_addresses_stacked_experts(ctx, dt):
     # split_experts (rce-qwen36-moe L216-223): sub_view(e*bpe, bpe, rows, cols)
     rng = np.random.default_rng(6000 + dt)

@@ -12,7 +12,7 @@ import rce_amd
 from rce_amd import GgufFile, Mode, QmmError, QuantWeight
 from gguf_writer import STRING, U32, build_gguf, llama_gguf
 from llama_case import device_model, make_weights, tiny_cfg
-from rand_blocks import rand_blocks
+from rand_blocks import float_bytes, rand_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -22,7 +22,8 @@ def note(msg):
 
 
 FORMATS = [(O.Q4_0, 96, 512), (O.Q8_0, 64, 256), (O.Q4_K, 80, 512), (O.Q5_K, 40, 512), (O.Q6_K, 48, 256),
-           (O.Q5_0, 24, 96), (O.Q4_1, 24, 160), (O.Q3_K, 24, 512)]
+           (O.Q5_0, 24, 96), (O.Q4_1, 24, 160), (O.Q3_K, 24, 512), (O.F16, 70, 100), (O.BF16, 64, 64),
+           (O.F32, 3, 16)]
 
 
 @pytest.mark.parametrize("align", [32, 64])
@@ -32,6 +33,7 @@ def test_weight_from_gguf_matches_bytes(ctx, align):
     tens, keep = [], []
     for dt, n, k in FORMATS:
         b = (rand_blocks(rng, dt, n, k) if dt in (O.Q5_0, O.Q4_1, O.Q3_K)
+             else float_bytes(rng, dt, n, k) if dt in (O.F32, O.F16, O.BF16)
              else rce_amd.quantize((rng.standard_normal((n, k)) * 0.05).astype(np.float32), dt))
         tens.append((f"w.{int(dt)}", (k, n), int(dt), bytes(b)))
         keep.append((dt, n, k, b))
@@ -52,7 +54,7 @@ def test_weight_from_gguf_matches_bytes(ctx, align):
 def test_weight_from_gguf_errors(ctx):
     note("weight_from_gguf errors")
     b = rce_amd.quantize(np.ones((8, 64), np.float32), O.Q4_0)
-    raw = build_gguf([], [("w", (64, 8), int(O.Q4_0), bytes(b)), ("f", (4,), 0, bytes(16))])
+    raw = build_gguf([], [("w", (64, 8), int(O.Q4_0), bytes(b)), ("f", (256,), 10, bytes(84))])
     f = GgufFile.parse(raw)
     with pytest.raises(QmmError) as e:
         QuantWeight.from_gguf(ctx, f, "w", 4, 64)  # declared 256 elements, the tensor has 512
@@ -61,9 +63,9 @@ def test_weight_from_gguf_errors(ctx):
         QuantWeight.from_gguf(ctx, f, "nope", 8, 64)
     assert e.value.status == 8
     with pytest.raises(QmmError) as e:
-        QuantWeight.from_gguf(ctx, f, "f", 1, 4)  # F32: no quantized-matmul kernel
+        QuantWeight.from_gguf(ctx, f, "f", 1, 256)  # Q2_K: not in mm_1d's table
     assert e.value.status == 3
-    short = GgufFile.parse(raw[:len(raw) - 40])  # the first tensor's bytes run past the end
+    short = GgufFile.parse(raw[:len(raw) - 130])  # the first tensor's bytes run past the end
     with pytest.raises(QmmError) as e:
         QuantWeight.from_gguf(ctx, short, "w", 8, 64)
     assert e.value.status == 2 and "out of bounds" in str(e.value)

@@ -117,6 +117,16 @@ def test_llama_block32_linears(ctx, dt):
     run_pair(ctx, W, Mode.Q8, TOKENS[:5], 1e-3).close()
 
 
+def test_llama_float_head_and_embedding(ctx):
+    """An F16 head (one chain per row, not a fused form: the output
+    rms_norm runs on its own) and a BF16 embedding table; Q8 mode keeps the
+    reference order for the float weights."""
+    note("llama F16 head, BF16 embedding")
+    W = make_weights(tiny_cfg(), seed=34, head_dtype=O.F16, embd_dtype=O.BF16)
+    run_pair(ctx, W, Mode.EXACT, TOKENS[:5], 1e-5).close()
+    run_pair(ctx, W, Mode.Q8, TOKENS[:5], 1e-3).close()
+
+
 def test_llama_head_dim_128(ctx):
     """d_head 128: runs of 32 keys per wave."""
     note("llama d_head 128, rope_dim 64, GQA 4:1, 40 positions")
