@@ -116,12 +116,44 @@ class Hip:
         return ms
 
 
+# F32, F16, BF16, I2_S, Q1_0, Q2_0, STQ1_0: no Q8 form, the same kernel in both modes
+FLOAT_DTYPES = (0, 1, 30, 36, 41, 42, 0x8000002A)
+
+
 def make_weight(seed, dt, n, k):
-    """N(0, 0.02) f32 weights (seeded) as GGUF bytes, by the library's
-    quantizer (the reference's encoders)."""
+    """N(0, 0.02) f32 weights (seeded) as GGUF bytes: by the library's
+    quantizer (the reference's encoders) where it has one, as the values
+    themselves for F32 / F16 / BF16, and as random blocks (random bit
+    fields, f16 scales of about 0.002) for Q5_0 / Q4_1 / Q3_K, which the
+    reference ships no encoder for."""
     import rce_amd
     rng = np.random.default_rng(seed)
+    if int(dt) in (36, 41, 42, 0x8000002A):  # multiply-free formats: random codes, scales about 0.02
+        qk, bb = {36: (128, 32), 41: (128, 18), 42: (128, 34), 0x8000002A: (256, 42)}[int(dt)]
+        b = rng.integers(0, 256, size=n * (k // qk) * bb + (4 if int(dt) == 36 else 0), dtype=np.uint8)
+        if int(dt) == 36:
+            b[-4:] = np.frombuffer(np.float32(0.02).tobytes(), np.uint8)
+        else:
+            bl = b.reshape(-1, bb)
+            at = 40 if int(dt) == 0x8000002A else 0
+            bl[:, at:at + 2] = np.frombuffer(np.float16(0.02).tobytes(), np.uint8)
+        return b
+    if int(dt) in (3, 6, 11):
+        qk, bb = (256, 110) if int(dt) == 11 else (32, 20 if int(dt) == 3 else 22)
+        b = rng.integers(0, 256, size=(n * (k // qk), bb), dtype=np.uint8)
+        d = rng.uniform(0.0005, 0.004, b.shape[0]).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        if int(dt) == 11:
+            b[:, 108:110] = d
+        else:
+            b[:, 0:2] = d
+        return b.reshape(-1)
     w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+    if int(dt) == 0:
+        return w.view(np.uint8).reshape(-1)
+    if int(dt) == 1:
+        return w.astype(np.float16).view(np.uint8).reshape(-1)
+    if int(dt) == 30:
+        return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
     return rce_amd.quantize(w, dt)
 
 
@@ -449,9 +481,18 @@ def main():
             ("Q4_K 2048x5632 b1", G.Q4K, 2048, 5632, 1),
             ("Q5_K 4096x4096 b1", G.Q5K, 4096, 4096, 1),       # Q5_K_M models' linears
             ("Q6_K 32000x2048 b1", G.Q6K, 32000, 2048, 1),     # configs[4] head
+            ("Q5_0 4096x4096 b1", G.Q5_0, 4096, 4096, 1),
+            ("Q4_1 4096x4096 b1", G.Q4_1, 4096, 4096, 1),
+            ("Q3_K 4096x4096 b1", G.Q3K, 4096, 4096, 1),
+            ("F16 2048x2048 b1", G.F16, 2048, 2048, 1),
+            ("F16 32000x2048 b1", G.F16, 32000, 2048, 1),      # an F16 head
+            ("Q1_0 2048x2048 b1", G.Q1_0, 2048, 2048, 1),
+            ("Q2_0 2048x2048 b1", G.Q2_0, 2048, 2048, 1),
+            ("STQ1_0 2048x2048 b1", G.STQ1_0, 2048, 2048, 1),
+            ("I2_S 6912x2560 b1", G.I2S, 6912, 2560, 1),       # BitNet b1.58 2B FFN up
         ]
         for name, sdt, sn, sk, st in sweep:
-            for m in (Mode.EXACT, Mode.Q8):
+            for m in ((Mode.EXACT,) if int(sdt) in FLOAT_DTYPES else (Mode.EXACT, Mode.Q8)):
                 steps = max(20, args.steps // 2)
                 sms, _, _, _, _ = time_gemv(hip, ctx, sdt, sn, sk, st, m, steps, 5, 100 + int(sdt))
                 sbytes = gemv_bytes(sdt, sn, sk, st)

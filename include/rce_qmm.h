@@ -119,17 +119,25 @@ int rce_qmm_supports(uint32_t dtype, size_t n_cols, rce_qmm_mode mode);
 
 /* ---- weights ------------------------------------------------------------ */
 
+/* dtype arguments are GGUF type tags (parser.rs L306-378), except that
+ * STQ1_0, which shares tag 42 with Q2_0 in files (hunyuan-dense files read
+ * it as STQ1_0, parser.rs L529-541), is named RCE_QMM_DTYPE_STQ1_0 here.
+ * I2_S weights are the ceil(n_rows * n_cols / 4) code bytes followed by the
+ * tensor's one f32 scale. */
+#define RCE_QMM_DTYPE_STQ1_0 0x8000002Au
+
 /* A device-resident QuantWeight made from GGUF bytes: the weight
  * [n_rows = N_out, n_cols = K_in], row-major, each row k/QK blocks
  * (rce-op-qmm/src/lib.rs L60-91 QuantWeight, L123-138 from_owned_bytes).
  * The bytes are copied to HBM once (the library may store them in a
  * device layout of the same byte count); the caller keeps its buffer.
- * len must equal n_rows * row_bytes(dtype, n_cols). */
+ * len must equal n_rows * row_bytes(dtype, n_cols) (I2_S: plus its 4-byte scale). */
 rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, size_t n_rows,
                                          size_t n_cols, const uint8_t *bytes, size_t len,
                                          rce_qmm_weight **out);
 
-/* QuantWeight::sub_view (rce-op-qmm/src/lib.rs L99-118): a view of
+/* QuantWeight::sub_view (rce-op-qmm/src/lib.rs L99-118) (not for I2_S: its
+ * scale belongs to the whole tensor): a view of
  * byte_len bytes at byte_offset of `w`'s GGUF bytes, read as
  * [n_rows, n_cols].  Shares the device copy (no HBM copy).  The view must
  * start on a row boundary of `w` and keep n_cols (the stacked-expert case

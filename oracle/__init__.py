@@ -30,9 +30,12 @@ _LIB_PATH = os.path.join(_HERE, "liboracle_qmm.so")
 # GGUF type tags (rce-ingest-gguf/src/parser.rs L306-341).
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 0, 1, 2, 3, 6, 7, 8
 Q3_K, Q4_K, Q5_K, Q6_K, BF16 = 11, 12, 13, 14, 30
+I2_S, Q1_0, Q2_0 = 36, 41, 42
+STQ1_0 = 0x8000002A  # file tag 42 (shared with Q2_0) read as STQ1_0: this build's name for it
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20),
          Q5_0: (32, 22), Q8_0: (32, 34), Q3_K: (256, 110), Q4_K: (256, 144),
-         Q5_K: (256, 176), Q6_K: (256, 210)}
+         Q5_K: (256, 176), Q6_K: (256, 210), I2_S: (128, 32), Q1_0: (128, 18), Q2_0: (128, 34),
+         STQ1_0: (256, 42)}
 
 _lib = None
 

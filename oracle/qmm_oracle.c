@@ -46,8 +46,11 @@
 enum {
     T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7,
     T_Q8_0 = 8, T_Q8_1 = 9, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12,
-    T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30
+    T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30, T_I2_S = 36, T_Q1_0 = 41, T_Q2_0 = 42
 };
+/* STQ1_0 shares the file tag 42 with Q2_0 (parser.rs L376-377); this build
+ * names it tag 42 with bit 31 set. */
+#define T_STQ1_0 0x8000002Au
 
 static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -122,6 +125,10 @@ EXPORT int orc_block_geometry(uint32_t t, uint32_t *block, uint32_t *bytes) {
     case T_Q4_K: qk = 256; bb = 144; break;
     case T_Q5_K: qk = 256; bb = 176; break;
     case T_Q6_K: qk = 256; bb = 210; break;
+    case T_I2_S: qk = 128; bb = 32; break;  /* plus one f32 scale per tensor */
+    case T_Q1_0: qk = 128; bb = 18; break;
+    case T_Q2_0: qk = 128; bb = 34; break;
+    case T_STQ1_0: qk = 256; bb = 42; break;
     default: return -1;
     }
     *block = qk; *bytes = bb;
@@ -130,6 +137,7 @@ EXPORT int orc_block_geometry(uint32_t t, uint32_t *block, uint32_t *bytes) {
 
 EXPORT size_t orc_tensor_byte_size(uint32_t t, size_t n) {
     uint32_t qk, bb;
+    if (t == T_I2_S) return (n + 3) / 4 + 4;  /* dequant.rs L45-48: 2-bit codes + the f32 scale */
     if (orc_block_geometry(t, &qk, &bb)) return 0;
     return (n + qk - 1) / qk * bb;
 }
@@ -494,6 +502,57 @@ static void dq_q6_k(const uint8_t *x, size_t nb, float *out) {
     }
 }
 
+/* dequant.rs L141-148 STQ1_0_CODEBOOK: (sign << 4 | code) -> four 2-bit
+ * lanes (lane p at bits 2p; 0 = -1, 1 = 0, 2 = +1).  A table of the
+ * format, the same in every implementation. */
+static const uint8_t STQ1_CB[32] = {
+    0xA9, 0x89, 0x29, 0x09, 0xA6, 0x86, 0x26, 0x06, 0x9A, 0x92, 0x1A, 0x12, 0x6A, 0x62, 0x4A, 0x42,
+    0x01, 0x21, 0x81, 0xA1, 0x04, 0x24, 0x84, 0xA4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68};
+EXPORT uint8_t orc_stq1_0_codebook(int i) { return STQ1_CB[i & 31]; }
+
+/* dequant.rs L222-256 dequant_i2_s: byte gp of block b holds positions
+ * 128 b + {gp, 32 + gp, 64 + gp, 96 + gp} at bits 7:6, 5:4, 3:2, 1:0;
+ * w = scale * map2bit[code], map2bit = {-1, 0, +1, 0}; the f32 scale
+ * follows the ceil(n / 4) code bytes. */
+static void dq_i2_s(const uint8_t *x, size_t n, float *out) {
+    static const float MAP[4] = {-1.0f, 0.0f, 1.0f, 0.0f};
+    float scale; memcpy(&scale, x + (n + 3) / 4, 4);
+    for (size_t b = 0; b < (n + 127) / 128; b++)
+        for (int gp = 0; gp < 32; gp++) {
+            uint8_t byte = x[b * 32 + gp];
+            for (int c = 0; c < 4; c++) {
+                size_t i = b * 128 + (size_t)(32 * c + gp);
+                if (i < n) out[i] = scale * MAP[(byte >> (6 - 2 * c)) & 3];
+            }
+        }
+}
+/* dequant.rs L272-299 dequant_q1_0: bit j of qs (LSB first) -> +d, else -d. */
+static void dq_q1_0(const uint8_t *x, size_t nb, float *out) {
+    for (size_t b = 0; b < nb; b++, x += 18, out += 128) {
+        float d = rd_f16(x), nd = -d;
+        for (int j = 0; j < 128; j++) out[j] = ((x[2 + j / 8] >> (j % 8)) & 1) ? d : nd;
+    }
+}
+/* dequant.rs L317-340 dequant_q2_0: q = 2-bit lane j % 4 of qs[j / 4]; (q - 1) * d. */
+static void dq_q2_0(const uint8_t *x, size_t nb, float *out) {
+    for (size_t b = 0; b < nb; b++, x += 34, out += 128) {
+        float d = rd_f16(x);
+        for (int j = 0; j < 128; j++) out[j] = (float)(((x[2 + j / 4] >> ((j % 4) * 2)) & 3) - 1) * d;
+    }
+}
+/* dequant.rs L162-196 dequant_stq1_0: group g of 4: code = nibble g & 1 of
+ * qs[g / 2], sign = bit g % 8 of sign[g / 8], lanes from the codebook. */
+static void dq_stq1_0(const uint8_t *x, size_t nb, float *out) {
+    for (size_t b = 0; b < nb; b++, x += 42, out += 256) {
+        float d = rd_f16(x + 40);
+        for (int g = 0; g < 64; g++) {
+            int code = (x[g / 2] >> (4 * (g & 1))) & 0xF, sg = (x[32 + g / 8] >> (g % 8)) & 1;
+            uint8_t qp = STQ1_CB[(sg << 4) | code];
+            for (int p = 0; p < 4; p++) out[4 * g + p] = (float)(((qp >> (2 * p)) & 3) - 1) * d;
+        }
+    }
+}
+
 /* dequant.rs L115-134 `dequantize_to_f32` for whole blocks (n a multiple
  * of the block size).  Returns 0, or -1 for an unsupported type. */
 EXPORT int orc_dequantize(const uint8_t *bytes, uint32_t t, size_t n, float *out) {
@@ -509,6 +568,10 @@ EXPORT int orc_dequantize(const uint8_t *bytes, uint32_t t, size_t n, float *out
     case T_Q4_K: dq_q4_k(bytes, n / 256, out); return 0;
     case T_Q5_K: dq_q5_k(bytes, n / 256, out); return 0;
     case T_Q6_K: dq_q6_k(bytes, n / 256, out); return 0;
+    case T_I2_S: dq_i2_s(bytes, n, out); return 0;
+    case T_Q1_0: dq_q1_0(bytes, n / 128, out); return 0;
+    case T_Q2_0: dq_q2_0(bytes, n / 128, out); return 0;
+    case T_STQ1_0: dq_stq1_0(bytes, n / 256, out); return 0;
     default: return -1;
     }
 }
@@ -728,6 +791,77 @@ static float row_q6_k(const float *a, const uint8_t *r, size_t k) {
     return sumf;
 }
 
+/* lib.rs L1716-1760 mm_1d_q1_0: per block of 128, pos / neg over j
+ * ascending (bit j set: pos += a, else neg += a); sumf += d * (pos - neg). */
+static float row_q1_0(const float *a, const uint8_t *r, size_t k) {
+    float sumf = 0.0f;
+    for (size_t b = 0; b < k / 128; b++) {
+        const uint8_t *s = r + b * 18;
+        float d = rd_f16(s), pos = 0.0f, neg = 0.0f;
+        for (int j = 0; j < 128; j++) {
+            float av = a[b * 128 + j];
+            if ((s[2 + j / 8] >> (j % 8)) & 1) pos += av; else neg += av;
+        }
+        sumf += d * (pos - neg);
+    }
+    return sumf;
+}
+/* lib.rs L1766-1815 mm_1d_q2_0: code 0 -> neg, 2 -> pos, 3 -> plus2, 1 ->
+ * nothing; sumf += d * ((pos - neg) + 2 * plus2). */
+static float row_q2_0(const float *a, const uint8_t *r, size_t k) {
+    float sumf = 0.0f;
+    for (size_t b = 0; b < k / 128; b++) {
+        const uint8_t *s = r + b * 34;
+        float d = rd_f16(s), pos = 0.0f, neg = 0.0f, plus2 = 0.0f;
+        for (int j = 0; j < 128; j++) {
+            int code = (s[2 + j / 4] >> ((j % 4) * 2)) & 3;
+            float av = a[b * 128 + j];
+            if (code == 0) neg += av; else if (code == 2) pos += av; else if (code == 3) plus2 += av;
+        }
+        float t = pos - neg;
+        t = t + 2.0f * plus2;
+        sumf += d * t;
+    }
+    return sumf;
+}
+/* lib.rs L1821-1875 mm_1d_stq1_0: lane value 2 -> pos, 0 -> neg; sumf +=
+ * d * (pos - neg) per super-block of 256. */
+static float row_stq1_0(const float *a, const uint8_t *r, size_t k) {
+    float sumf = 0.0f;
+    for (size_t b = 0; b < k / 256; b++) {
+        const uint8_t *s = r + b * 42;
+        float d = rd_f16(s + 40), pos = 0.0f, neg = 0.0f;
+        for (int g = 0; g < 64; g++) {
+            int code = (s[g / 2] >> (4 * (g & 1))) & 0xF, sg = (s[32 + g / 8] >> (g % 8)) & 1;
+            uint8_t qp = STQ1_CB[(sg << 4) | code];
+            for (int p = 0; p < 4; p++) {
+                int q = (qp >> (2 * p)) & 3;
+                float av = a[b * 256 + 4 * g + p];
+                if (q == 2) pos += av; else if (q == 0) neg += av;
+            }
+        }
+        sumf += d * (pos - neg);
+    }
+    return sumf;
+}
+/* lib.rs L1478-1537 mm_1d_i2_s: pos / neg over the whole row, byte gp of
+ * each block of 128 in order, its codes for positions gp, 32 + gp, 64 + gp,
+ * 96 + gp (bits 7:6, 5:4, 3:2, 1:0); code 2 -> pos, 0 -> neg; the row is
+ * scale * (pos - neg) with the tensor's one f32 scale. */
+static float row_i2_s(const float *a, const uint8_t *r, size_t k, float scale) {
+    float pos = 0.0f, neg = 0.0f;
+    for (size_t b = 0; b < k / 128; b++)
+        for (int gp = 0; gp < 32; gp++) {
+            uint8_t byte = r[b * 32 + gp];
+            for (int c = 0; c < 4; c++) {
+                int code = (byte >> (6 - 2 * c)) & 3;
+                float av = a[b * 128 + (size_t)(32 * c + gp)];
+                if (code == 2) pos += av; else if (code == 0) neg += av;
+            }
+        }
+    return scale * (pos - neg);
+}
+
 typedef float (*row_fn)(const float *, const uint8_t *, size_t);
 
 static row_fn pick_row(uint32_t t, uint32_t *qk, uint32_t *bb) {
@@ -744,6 +878,9 @@ static row_fn pick_row(uint32_t t, uint32_t *qk, uint32_t *bb) {
     case T_Q4_K: return row_q4_k;
     case T_Q5_K: return row_q5_k;
     case T_Q6_K: return row_q6_k;
+    case T_Q1_0: return row_q1_0;
+    case T_Q2_0: return row_q2_0;
+    case T_STQ1_0: return row_stq1_0;
     default: return 0;
     }
 }
@@ -757,11 +894,21 @@ static row_fn pick_row(uint32_t t, uint32_t *qk, uint32_t *bb) {
 EXPORT int orc_mm_batched(const float *a, size_t t_rows, const uint8_t *w, uint32_t t,
                           size_t n_rows, size_t n_cols, float *out, int threads) {
     uint32_t qk, bb;
+    if (threads < 1) threads = 1;
+    if (t == T_I2_S) {
+        if (n_cols % 128) return -2;
+        float scale; memcpy(&scale, w + n_rows * (n_cols / 4), 4);
+        for (size_t tr = 0; tr < t_rows; tr++) {
+#pragma omp parallel for schedule(dynamic, 16) num_threads(threads)
+            for (size_t j = 0; j < n_rows; j++)
+                out[tr * n_rows + j] = row_i2_s(a + tr * n_cols, w + j * (n_cols / 4), n_cols, scale);
+        }
+        return 0;
+    }
     row_fn f = pick_row(t, &qk, &bb);
     if (!f) return -1;
     if (n_cols % qk) return -2;
     size_t row_bytes = n_cols / qk * bb;
-    if (threads < 1) threads = 1;
     for (size_t tr = 0; tr < t_rows; tr++) {
         const float *at = a + tr * n_cols;
         float *ot = out + tr * n_rows;
@@ -999,13 +1146,15 @@ static float row_q8_path(uint32_t t, const int8_t *xq, const float *dx, const ui
 }
 
 /* Q8-activation mm_batched: each activation row quantized, then the row
- * formulas above.  The whole-element formats (F32, F16, BF16) take no
- * quantized activations: their Q8 mode is the reference order.  Returns -1
+ * formulas above.  The whole-element formats (F32, F16, BF16) and the
+ * multiply-free ternary ones (I2_S, Q1_0, Q2_0, STQ1_0) take no quantized
+ * activations: their Q8 mode is the reference order.  Returns -1
  * for a dtype without a Q8 path. */
 EXPORT int orc_mm_batched_q8(const float *a, size_t t_rows, const uint8_t *w, uint32_t t,
                              size_t n_rows, size_t n_cols, float *out, int threads) {
     uint32_t qk, bb;
-    if (t == T_F32 || t == T_F16 || t == T_BF16) return orc_mm_batched(a, t_rows, w, t, n_rows, n_cols, out, threads);
+    if (t == T_F32 || t == T_F16 || t == T_BF16 || t == T_I2_S || t == T_Q1_0 || t == T_Q2_0 || t == T_STQ1_0)
+        return orc_mm_batched(a, t_rows, w, t, n_rows, n_cols, out, threads);
     if (t != T_Q8_0 && t != T_Q4_0 && t != T_Q5_0 && t != T_Q4_1 && t != T_Q3_K && t != T_Q4_K && t != T_Q5_K &&
         t != T_Q6_K)
         return -1;

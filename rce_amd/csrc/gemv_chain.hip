@@ -1,7 +1,8 @@
-// gemv_chain.hip -- the whole-element formats F32, F16 and BF16.  The
-// reference's row sum is one chain over every position of the row
+// gemv_chain.hip -- the whole-element formats F32, F16 and BF16, and I2_S.
+// The reference's row sum is one chain over every position of the row
 // (rce-op-qmm/src/lib.rs L458-490: acc += a[i] * w[i], i ascending, from
-// +0.0), so each lane owns one row and walks it in that order.  Rows sit in
+// +0.0; I2_S, L1478-1537: two chains pos / neg over the whole row), so each
+// lane owns one row and walks it in that order.  Rows sit in
 // the 64-row interleave of LAYOUT_IL64_ROWS: chunk c (16 B) of the 64 rows
 // of a group is one contiguous 1 KB wave load.  With one wave per 64 rows
 // the launch has few waves, so each wave keeps CHAIN_D chunks (16 KB) in
@@ -86,6 +87,63 @@ __global__ __launch_bounds__(64) void k_gemv_chain(DevWeight w, const float *__r
     if (row < w.n_rows) out[t * w.n_rows + row] = acc;
 }
 
+// I2_S (lib.rs L1478-1537): byte gp of each block of 128 in order, its four
+// codes for positions gp, 32 + gp, 64 + gp, 96 + gp (bits 7:6, 5:4, 3:2,
+// 1:0); code 2: pos += a, code 0: neg += a.  Chunk c (16 code bytes) is
+// bytes 16 (c % 2) .. + 15 of block c / 2.  A chain step adds the
+// activation or +0.0, which leaves a chain (never -0.0: it starts at +0.0)
+// unchanged.  The row is scale * (pos - neg) with the tensor's scale.
+__global__ __launch_bounds__(64) void k_gemv_chain_i2s(DevWeight w, const float *__restrict__ A,
+                                                       float *__restrict__ out) {
+    const int lane = threadIdx.x;
+    const size_t grp = blockIdx.x, t = blockIdx.y;
+    const size_t k = w.n_cols;
+    const float *a = A + t * k;
+    const uint4 *src = reinterpret_cast<const uint4 *>(w.base + grp * w.group_stride) + lane;
+    const int nc = (int)(k / 64);
+    const int ns = (nc + CHAIN_D - 1) / CHAIN_D;
+    float pos = 0.0f, neg = 0.0f;
+    uint4 b0[CHAIN_D], b1[CHAIN_D];
+    auto load = [&](uint4 *b, int s) {
+#pragma unroll
+        for (int i = 0; i < CHAIN_D; i++) {
+            const int c = s * CHAIN_D + i;
+            b[i] = src[(size_t)(c < nc ? c : 0) * 64];
+        }
+    };
+    auto consume = [&](const uint4 *b, int s) {
+#pragma unroll
+        for (int i = 0; i < CHAIN_D; i++) {
+            const int c = s * CHAIN_D + i;
+            if (c < nc) {
+                const float *ab = a + (size_t)(c >> 1) * 128 + 16 * (c & 1);
+#pragma unroll
+                for (int g = 0; g < 16; g++) {
+                    const uint32_t byte = (wrd(b[i], g >> 2) >> (8 * (g & 3))) & 0xFFu;
+#pragma unroll
+                    for (int slot = 0; slot < 4; slot++) {
+                        const uint32_t code = (byte >> (6 - 2 * slot)) & 3u;
+                        const uint32_t av = __float_as_uint(ab[32 * slot + g]);
+                        pos = pos + __uint_as_float(code == 2 ? av : 0u);
+                        neg = neg + __uint_as_float(code == 0 ? av : 0u);
+                    }
+                }
+            }
+        }
+    };
+    load(b0, 0);
+    for (int s = 0; s < ns; s += 2) {
+        load(b1, s + 1);
+        consume(b0, s);
+        load(b0, s + 2);
+        consume(b1, s + 1);
+    }
+    const size_t row = grp * 64 + lane;
+    const float scale = *reinterpret_cast<const float *>(w.aux);
+    const float d = pos - neg;
+    if (row < w.n_rows) out[t * w.n_rows + row] = scale * d;
+}
+
 }  // namespace
 
 hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
@@ -96,6 +154,7 @@ hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, 
     case T_F32: hipLaunchKernelGGL(k_gemv_chain<T_F32>, grid, dim3(64), 0, s, w, a, out); break;
     case T_F16: hipLaunchKernelGGL(k_gemv_chain<T_F16>, grid, dim3(64), 0, s, w, a, out); break;
     case T_BF16: hipLaunchKernelGGL(k_gemv_chain<T_BF16>, grid, dim3(64), 0, s, w, a, out); break;
+    case T_I2_S: hipLaunchKernelGGL(k_gemv_chain_i2s, grid, dim3(64), 0, s, w, a, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

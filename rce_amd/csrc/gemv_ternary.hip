@@ -1,0 +1,139 @@
+// gemv_ternary.hip -- the multiply-free block formats Q1_0, Q2_0 (blocks of
+// 128) and STQ1_0 (super-blocks of 256), one token per thread.  The
+// reference keeps per-block chains of activation sums (pos: weights +1,
+// neg: weights -1, Q2_0 also plus2: weights +2) in position order and adds
+// d * (pos - neg [+ 2 plus2]) per block (rce-op-qmm/src/lib.rs
+// L1716-1875), so a unit is one whole block.  A chain step adds the
+// activation or +0.0 (the activation's bits masked to zero): the chains
+// start at +0.0 and a sum of two floats is -0.0 only if both are, so
+// adding +0.0 leaves every chain value unchanged, and the result equals
+// the reference's conditional adds bit for bit.  There is no Q8 form:
+// both modes run these kernels.
+#include "qmm_gemv_kernels.h"
+
+namespace rce_qmm {
+namespace {
+
+// a if (mask == all ones), else +0.0
+__device__ __forceinline__ float keep(float a, uint32_t mask) { return __uint_as_float(__float_as_uint(a) & mask); }
+
+// Q1_0 block (lib.rs L1716-1760): bit j of the 16 code bytes (LSB first)
+// is position j; set: pos += a, clear: neg += a.
+template <int TB>
+struct Q1_0Unit {
+    static_assert(TB == 1, "one token per thread");
+    static constexpr int NTOK = 1;
+    using Raw = RawQ4_0;  // 16 code bytes + the f16 d, Q4_0's layout
+    float av[128];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int, int col) {
+        load_f32x(A + (size_t)t0 * k + 128 * (size_t)col, av, 128);
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float pos = 0.0f, neg = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = wrd(r.q, i);
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                const uint32_t m = (uint32_t)((int32_t)(x << (31 - j)) >> 31);  // bit j as a mask
+                pos = pos + keep(av[32 * i + j], m);
+                neg = neg + keep(av[32 * i + j], ~m);
+            }
+        }
+        const float t = pos - neg;
+        out[0] = h2f(r.s) * t;
+    }
+};
+
+// Q2_0 block (lib.rs L1766-1815): 2-bit lane j % 4 of byte j / 4 is
+// position j; code 0: neg += a, 2: pos += a, 3: plus2 += a, 1: nothing;
+// addend d * ((pos - neg) + 2 plus2).
+template <int TB>
+struct Q2_0Unit {
+    static_assert(TB == 1, "one token per thread");
+    static constexpr int NTOK = 1;
+    using Raw = RawQ8_0;  // 32 code bytes in two planes + the f16 d, Q8_0's layout
+    float av[128];
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q8_0(w, row, col); }
+    __device__ void init(const float *A, size_t k, int t0, int, int col) {
+        load_f32x(A + (size_t)t0 * k + 128 * (size_t)col, av, 128);
+    }
+    __device__ void addends(const Raw &r, float *out) const {
+        float pos = 0.0f, neg = 0.0f, p2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
+#pragma unroll
+            for (int l = 0; l < 16; l++) {
+                const uint32_t c = (x >> (2 * l)) & 3u;
+                const float a = av[16 * i + l];
+                neg = neg + keep(a, c == 0 ? ~0u : 0u);
+                pos = pos + keep(a, c == 2 ? ~0u : 0u);
+                p2 = p2 + keep(a, c == 3 ? ~0u : 0u);
+            }
+        }
+        float t = pos - neg;
+        const float u = 2.0f * p2;
+        t = t + u;
+        out[0] = h2f(r.s) * t;
+    }
+};
+
+// STQ1_0 super-block (lib.rs L1821-1875) with its codebook expanded at
+// upload: lane code 2: pos += a, 0: neg += a.  The unit's 256 activations
+// are read from global memory (L1) 16 at a time rather than held.
+struct RawSTQ1_0 { uint4 c[4]; uint32_t d; };
+template <int TB>
+struct STQ1_0Unit {
+    static_assert(TB == 1, "one token per thread");
+    static constexpr int NTOK = 1;
+    using Raw = RawSTQ1_0;
+    const float *ap;
+    __device__ static Raw load(const DevWeight &w, size_t row, int col) {
+        const uint8_t *rp = w.base + row * w.row_stride;
+        Raw r;
+        const uint4 *p = reinterpret_cast<const uint4 *>(rp + w.plane1 + 64 * (size_t)col);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.c[i] = p[i];
+        r.d = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+        return r;
+    }
+    __device__ void init(const float *A, size_t k, int t0, int, int col) { ap = A + (size_t)t0 * k + 256 * (size_t)col; }
+    __device__ void addends(const Raw &r, float *out) const {
+        float pos = 0.0f, neg = 0.0f;
+#pragma unroll 1
+        for (int seg = 0; seg < 4; seg++) {  // positions 64 seg .. 64 seg + 63: 16 code bytes, 64 activations
+            const uint4 cw = seg == 0 ? r.c[0] : (seg == 1 ? r.c[1] : (seg == 2 ? r.c[2] : r.c[3]));
+            float a[64];
+            load_f32x(ap + 64 * seg, a, 64);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t x = wrd(cw, i);
+#pragma unroll
+                for (int l = 0; l < 16; l++) {
+                    const uint32_t c = (x >> (2 * l)) & 3u;
+                    pos = pos + keep(a[16 * i + l], c == 2 ? ~0u : 0u);
+                    neg = neg + keep(a[16 * i + l], c == 0 ? ~0u : 0u);
+                }
+            }
+        }
+        const float t = pos - neg;
+        out[0] = h2f(r.d) * t;
+    }
+};
+
+}  // namespace
+
+hipError_t launch_gemv_ternary(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                               hipStream_t s) {
+    if (g.tb != 1) return hipErrorInvalidValue;
+    switch (w.dtype) {
+    case T_Q1_0: return launch_as_tb<Q1_0Unit, false, 1>(w, g, a, t_rows, out, s);
+    case T_Q2_0: return launch_as_tb<Q2_0Unit, false, 1>(w, g, a, t_rows, out, s);
+    case T_STQ1_0: return launch_as_tb<STQ1_0Unit, false, 1>(w, g, a, t_rows, out, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace rce_qmm

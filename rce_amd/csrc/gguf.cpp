@@ -29,6 +29,7 @@ struct rce_qmm_gguf {
     void *map = nullptr;  // owned mapping (rce_qmm_gguf_open)
     size_t map_len = 0;
     uint32_t version = 0;
+    bool tag42_stq1 = false;  // hunyuan-dense: tag 42 is STQ1_0 (parser.rs L529-541)
     struct Meta {
         std::string key;
         uint32_t type = 0;
@@ -239,6 +240,7 @@ rce_qmm_status parse_into(rce_qmm_gguf *g) {
             const uint8_t *v = g->data + m.val_off + 8;
             hunyuan = hunyuan || (m.val_len - 8 == 13 && std::memcmp(v, "hunyuan-dense", 13) == 0);
         }
+    g->tag42_stq1 = hunyuan;
     for (uint64_t i = 0; i < n_tensors; i++) {
         rce_qmm_gguf::Tensor t;
         if (!c.str(&t.name) || !c.u32(t.ndim)) return perr(c.err);
@@ -465,7 +467,8 @@ rce_qmm_status rce_qmm_weight_from_gguf(rce_qmm_context *ctx, const rce_qmm_gguf
     size_t n;
     rce_qmm_status st = tensor_span(g, *t, p, n);
     if (st) return st;
-    return rce_qmm_weight_from_bytes(ctx, t->dtype, n_rows, n_cols, p, n, out);
+    const uint32_t dt = (t->dtype == 42 && g->tag42_stq1) ? RCE_QMM_DTYPE_STQ1_0 : t->dtype;
+    return rce_qmm_weight_from_bytes(ctx, dt, n_rows, n_cols, p, n, out);
 }
 
 rce_qmm_status rce_qmm_gguf_read_f32(const rce_qmm_gguf *g, const char *name, float *out, size_t n) {

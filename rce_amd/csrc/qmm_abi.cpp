@@ -45,6 +45,10 @@ bool block_geometry(uint32_t t, size_t &qk, size_t &bb) {
     case T_Q4_K: qk = 256; bb = 144; return true;
     case T_Q5_K: qk = 256; bb = 176; return true;
     case T_Q6_K: qk = 256; bb = 210; return true;
+    case T_I2_S: qk = 128; bb = 32; return true;  // plus the tensor's f32 scale
+    case T_Q1_0: qk = 128; bb = 18; return true;
+    case T_Q2_0: qk = 128; bb = 34; return true;
+    case T_STQ1_0: qk = 256; bb = 42; return true;
     default: return false;
     }
 }
@@ -209,8 +213,10 @@ rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, s
         return fail(RCE_QMM_BAD_SHAPE, "n_cols " + std::to_string(n_cols) + " is not a multiple of the block size " +
                                            std::to_string(qk));
     const size_t rowb = n_cols / qk * bb;
-    if (len != n_rows * rowb)
-        return fail(RCE_QMM_BAD_SHAPE, "len " + std::to_string(len) + " != n_rows*row_bytes " + std::to_string(n_rows * rowb));
+    const size_t want_len = n_rows * rowb + (dtype == T_I2_S ? 4 : 0);  // I2_S: codes, then one f32 scale
+    if (len != want_len)
+        return fail(RCE_QMM_BAD_SHAPE, "len " + std::to_string(len) + " != " + std::to_string(want_len) +
+                                           (dtype == T_I2_S ? " (n_rows*row_bytes + the f32 scale)" : " (n_rows*row_bytes)"));
     if (!gpu_supports(dtype, n_cols, RCE_QMM_MODE_EXACT))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "dtype " + std::to_string(dtype) + " with n_cols " + std::to_string(n_cols) +
                                                    " has no GPU kernel");
@@ -239,6 +245,7 @@ rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, s
     HIP_TRY(hipMemcpyAsync(alloc->p, host.data(), total, hipMemcpyHostToDevice, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     dw.base = static_cast<const uint8_t *>(alloc->p);
+    if (dtype == T_I2_S) dw.aux = dw.base + dw.plane1;
     rce_qmm_weight *w = new (std::nothrow) rce_qmm_weight();
     if (!w) return fail(RCE_QMM_OUT_OF_MEMORY, "weight handle");
     w->alloc = alloc;
@@ -262,6 +269,8 @@ rce_qmm_status rce_qmm_weight_sub_view(const rce_qmm_weight *w, size_t byte_offs
     if (rb == 0 || byte_offset % rb || byte_len != n_rows * rb)
         return fail(RCE_QMM_BAD_SHAPE, "sub_view must cover whole rows of the parent");
     const size_t row0 = byte_offset / rb;
+    if (w->dw.dtype == T_I2_S)  // one scale per tensor, after all rows
+        return fail(RCE_QMM_BAD_SHAPE, "I2_S has one scale per tensor: no sub_view");
     DevWeight dw = w->dw;
     dw.n_rows = n_rows;
     if (dw.layout == LAYOUT_IL64_Q6_K || dw.layout == LAYOUT_IL64_ROWS) {

@@ -52,6 +52,33 @@ __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
             const float t = (float)nib * h2f(sm & 0xFFFFu);
             v = t + h2f(sm >> 16);
         }
+    } else if (w.dtype == T_Q1_0) {  // dequant.rs L272-299: bit set -> +d, else -d
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t b = i / 128;
+        const int j = (int)(i % 128);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 2 * b));
+        v = ((rp[w.plane1 + 16 * b + j / 8] >> (j % 8)) & 1) ? d : -d;
+    } else if (w.dtype == T_Q2_0) {  // dequant.rs L317-340: (q - 1) * d
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t b = i / 128;
+        const int j = (int)(i % 128), byte = j / 4;
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 2 * b));
+        const uint8_t x = byte < 16 ? rp[w.plane1 + 16 * b + byte] : rp[w.plane2 + 16 * b + byte - 16];
+        v = (float)((int)((x >> (2 * (j % 4))) & 3) - 1) * d;
+    } else if (w.dtype == T_STQ1_0) {  // dequant.rs L162-196, codes expanded at upload
+        const uint8_t *rp = w.base + row * w.row_stride;
+        const size_t b = i / 256;
+        const int p = (int)(i % 256);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 2 * b));
+        v = (float)((int)((rp[w.plane1 + 64 * b + p / 4] >> (2 * (p % 4))) & 3) - 1) * d;
+    } else if (w.dtype == T_I2_S) {  // dequant.rs L222-256: scale * map2bit[code]
+        const size_t blk = i / 128;
+        const int within = (int)(i % 128), slot = within / 32, gp = within % 32;
+        const size_t byte = 32 * blk + gp;
+        const uint8_t x = *(w.base + (row >> 6) * w.group_stride + ((byte / 16) * 64 + (row & 63)) * 16 + byte % 16);
+        const int code = (x >> (6 - 2 * slot)) & 3;
+        const float m = code == 0 ? -1.0f : (code == 2 ? 1.0f : 0.0f);
+        v = *reinterpret_cast<const float *>(w.aux) * m;
     } else if (is_whole_element(w.dtype)) {  // dequant.rs L343-356: the value itself
         const size_t es = w.dtype == T_F32 ? 4 : 2, o = i * es;
         const uint8_t *p = w.base + (row >> 6) * w.group_stride + ((o / 16) * 64 + (row & 63)) * 16 + o % 16;
@@ -157,6 +184,13 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
     case T_F16:
     case T_BF16:
         return n_cols <= ((size_t)1 << 26);
+    case T_I2_S:
+        return n_cols % 128 == 0 && n_cols <= ((size_t)1 << 26);
+    case T_Q1_0:  // 128 activations per thread: blocks of 256 threads only
+    case T_Q2_0:
+        return n_cols % 128 == 0 && n_cols / 128 <= 256;
+    case T_STQ1_0:
+        return n_cols % 256 == 0 && n_cols / 256 <= 256;
     case T_Q6_K:
         return n_cols % 256 == 0 && n_cols / 256 <= 1024;
     default:
@@ -213,6 +247,28 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane3 = dw.plane2 + 4 * (k / 32);
         dw.row_stride = pad16(dw.plane3 + 2 * (k / 32));
         return dw.row_stride * n;
+    case T_Q1_0:  // 2 + 16 bytes per block of 128: Q4_0's split layout
+        dw.layout = LAYOUT_SPLIT_Q4_0;
+        dw.plane1 = pad16(2 * (k / 128));
+        dw.plane2 = 0;
+        dw.row_stride = dw.plane1 + 16 * (k / 128);
+        return dw.row_stride * n;
+    case T_Q2_0:  // 2 + 32 bytes per block of 128: Q8_0's split layout
+        dw.layout = LAYOUT_SPLIT_Q8_0;
+        dw.plane1 = pad16(2 * (k / 128));
+        dw.plane2 = dw.plane1 + 16 * (k / 128);
+        dw.row_stride = dw.plane2 + 16 * (k / 128);
+        return dw.row_stride * n;
+    case T_STQ1_0:
+        dw.layout = LAYOUT_SPLIT_STQ1_0;
+        dw.plane1 = pad16(2 * (k / 256));
+        dw.row_stride = dw.plane1 + 64 * (k / 256);
+        return dw.row_stride * n;
+    case T_I2_S:  // the codes in the 64-row interleave, then the tensor's f32 scale
+        dw.layout = LAYOUT_IL64_ROWS;
+        dw.group_stride = ((k / 4 + 15) / 16) * 1024;
+        dw.plane1 = dw.group_stride * ((n + 63) / 64);
+        return dw.plane1 + 16;
     case T_F32:
     case T_F16:
     case T_BF16:
@@ -232,8 +288,9 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
     const size_t n = dw.n_rows, k = dw.n_cols;
     switch (dw.layout) {
     case LAYOUT_SPLIT_Q4_0:
-    case LAYOUT_SPLIT_Q8_0: {
-        const size_t nb = k / 32, bb = dw.dtype == T_Q8_0 ? 34 : 18;
+    case LAYOUT_SPLIT_Q8_0: {  // also Q1_0 (as Q4_0) and Q2_0 (as Q8_0), blocks of 128
+        const size_t qk = (dw.dtype == T_Q1_0 || dw.dtype == T_Q2_0) ? 128 : 32;
+        const size_t nb = k / qk, bb = dw.layout == LAYOUT_SPLIT_Q8_0 ? 34 : 18;
         for (size_t r = 0; r < n; r++) {
             const uint8_t *s = src + r * nb * bb;
             uint8_t *d = dst + r * dw.row_stride;
@@ -242,7 +299,7 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
                 d[2 * b] = blk[0];
                 d[2 * b + 1] = blk[1];
                 for (int i = 0; i < 16; i++) d[dw.plane1 + 16 * b + i] = blk[2 + i];
-                if (dw.dtype == T_Q8_0)
+                if (dw.layout == LAYOUT_SPLIT_Q8_0)
                     for (int i = 0; i < 16; i++) d[dw.plane2 + 16 * b + i] = blk[18 + i];
             }
         }
@@ -344,8 +401,29 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
         }
         break;
     }
+    case LAYOUT_SPLIT_STQ1_0: {  // block: qs[32], sign[8], d; codebook dequant.rs L141-148
+        static const uint8_t CB[32] = {0xA9, 0x89, 0x29, 0x09, 0xA6, 0x86, 0x26, 0x06, 0x9A, 0x92, 0x1A,
+                                       0x12, 0x6A, 0x62, 0x4A, 0x42, 0x01, 0x21, 0x81, 0xA1, 0x04, 0x24,
+                                       0x84, 0xA4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68};
+        const size_t nsb = k / 256;
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * nsb * 42;
+            uint8_t *d = dst + r * dw.row_stride;
+            for (size_t sb = 0; sb < nsb; sb++) {
+                const uint8_t *blk = s + sb * 42;
+                d[2 * sb] = blk[40];
+                d[2 * sb + 1] = blk[41];
+                for (int g = 0; g < 64; g++) {
+                    const int code = (blk[g / 2] >> (4 * (g & 1))) & 0xF, sg = (blk[32 + g / 8] >> (g % 8)) & 1;
+                    d[dw.plane1 + 64 * sb + g] = CB[(sg << 4) | code];  // group g = byte g: lanes 4g..4g+3
+                }
+            }
+        }
+        break;
+    }
     case LAYOUT_IL64_ROWS: {
-        const size_t rb = k * (dw.dtype == T_F32 ? 4 : 2);
+        const size_t rb = dw.dtype == T_I2_S ? k / 4 : k * (dw.dtype == T_F32 ? 4 : 2);
+        if (dw.dtype == T_I2_S) std::memcpy(dst + dw.plane1, src + n * rb, 4);  // the tensor's scale
         for (size_t r = 0; r < n; r++) {
             uint8_t *g = dst + (r >> 6) * dw.group_stride + (r & 63) * 16;
             const uint8_t *s = src + r * rb;
@@ -389,6 +467,9 @@ static size_t unit_bytes(uint32_t dtype) {
     case T_Q5_0: return 22;
     case T_Q4_1: return 20;
     case T_Q3_K: return 14;  // 13.75: an eighth of the 110 B super-block
+    case T_Q1_0: return 18;
+    case T_Q2_0: return 34;
+    case T_STQ1_0: return 42;
     case T_Q4_K: return 36;
     case T_Q5_K: return 44;
     case T_Q6_K: return 210;
@@ -412,7 +493,7 @@ GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
     const int P = g.nt / U;
     const bool k4 = w.dtype == T_Q4_K || w.dtype == T_Q5_K;  // 64-value units
     int tbmax = q8 ? (w.dtype == T_Q6_K ? 2 : (k4 ? 4 : 8)) : (k4 ? 2 : 4);
-    if (w.dtype == T_Q6_K && !q8) tbmax = 1;
+    if ((w.dtype == T_Q6_K && !q8) || is_ternary_block(w.dtype)) tbmax = 1;
     g.tb = 1;
     while (g.tb * 2 <= tbmax && (size_t)g.tb * 2 <= t_rows) g.tb *= 2;
     if (w.dtype == T_Q6_K) {
@@ -428,6 +509,7 @@ GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
         while (g.rpl > 2 && (w.n_rows + (size_t)P * g.rpl - 1) / ((size_t)P * g.rpl) < 256) g.rpl = g.rpl == 16 ? 12 : (g.rpl == 12 ? 8 : g.rpl / 2);
         const bool heavy = (q8 && g.tb >= 4) || (!q8 && (g.tb >= 4 || (k4 && g.tb >= 2)));
         if (heavy && g.rpl > 4) g.rpl = 4;
+        if (is_ternary_block(w.dtype) && g.rpl > 4) g.rpl = 4;  // 128 activations or 256-lane codes per row
     }
     // shrink rows, then tokens, until the block's LDS fits
     while (gemv_lds_bytes(U, g.nt, g.rpl, g.tb, q8, w.n_cols) > LDS_MAX) {
@@ -442,8 +524,9 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
                        const GemvGeom *geom) {
     if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
     if (mode != 0 && mode != 1) return hipErrorInvalidValue;
-    if (is_whole_element(w.dtype)) return launch_gemv_chain(w, a, t_rows, out, s);
-    const GemvGeom g = geom ? *geom : pick_gemv_geom(w, t_rows, mode);
+    if (is_row_chain(w.dtype)) return launch_gemv_chain(w, a, t_rows, out, s);
+    const GemvGeom g = geom ? *geom : pick_gemv_geom(w, t_rows, is_ternary_block(w.dtype) ? 0 : mode);
+    if (is_ternary_block(w.dtype)) return launch_gemv_ternary(w, g, a, t_rows, out, s);
     switch (w.dtype) {
     case T_Q4_0: return launch_gemv_q4_0(w, g, a, t_rows, out, mode, s);
     case T_Q8_0: return launch_gemv_q8_0(w, g, a, t_rows, out, mode, s);

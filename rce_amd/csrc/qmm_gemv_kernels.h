@@ -1279,6 +1279,8 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
 inline int units_per_row(uint32_t dtype, size_t n_cols) {
     switch (dtype) {
     case T_Q4_0: case T_Q8_0: case T_Q5_0: case T_Q4_1: case T_Q3_K: return (int)(n_cols / 32);
+    case T_Q1_0: case T_Q2_0: return (int)(n_cols / 128);
+    case T_STQ1_0: return (int)(n_cols / 256);
     case T_Q4_K: case T_Q5_K: return (int)(n_cols / 64);
     case T_Q6_K: return (int)(n_cols / 256);
     default: return 0;

@@ -12,7 +12,10 @@ namespace rce_qmm {
 // GGUF type tags (rce-ingest-gguf/src/parser.rs L306-341).
 enum : uint32_t {
     T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q8_0 = 8,
-    T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30
+    T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30, T_I2_S = 36, T_Q1_0 = 41, T_Q2_0 = 42,
+    // STQ1_0 shares the file tag 42 with Q2_0 (parser.rs L376-377): the ABI
+    // names it tag 42 with bit 31 set (RCE_QMM_DTYPE_STQ1_0).
+    T_STQ1_0 = 0x8000002Au
 };
 
 // How a weight's GGUF bytes are arranged in HBM.  Every layout holds the
@@ -58,6 +61,13 @@ enum Layout : int {
     // chunks (the last one zero-padded); chunk c of row r at
     // (c * 64 + r % 64) * 16 within the group's group_stride bytes.
     LAYOUT_IL64_ROWS = 9,
+    // STQ1_0: the super-blocks' f16 d, padded to 16, then per super-block
+    // u the 256 lane codes its codebook gives (64 B at plane1 + 64 u:
+    // position p at bits 2 (p % 4) of byte p / 4; 0 = -1, 1 = 0, 2 = +1).
+    // Q1_0 uses LAYOUT_SPLIT_Q4_0 (2-byte d + 16 bytes per block of 128)
+    // and Q2_0 LAYOUT_SPLIT_Q8_0 (2-byte d + 32 bytes); I2_S uses
+    // LAYOUT_IL64_ROWS with its f32 scale at plane1 (pointed to by aux).
+    LAYOUT_SPLIT_STQ1_0 = 10,
 };
 
 struct DevWeight {
@@ -70,6 +80,7 @@ struct DevWeight {
     size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K / SPLIT_Q5_K / SPLIT_Q5_0: offset of the second plane
     size_t plane3;        // SPLIT_Q5_K: offset of the high-bit words; SPLIT_Q3_K: of the scales
     size_t group_stride;  // IL64: bytes between 64-row groups
+    const uint8_t *aux;   // I2_S: device address of the tensor's f32 scale
 };
 
 constexpr size_t IL64_Q6K_D = 13 * 64 * 16;         // 13312: the d values
@@ -213,10 +224,19 @@ hipError_t launch_gemv_q4_1(const DevWeight &w, const GemvGeom &g, const float *
 hipError_t launch_gemv_q3_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
                             int mode, hipStream_t s);
 hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStream_t s);
-// F32 / F16 / BF16 (gemv_chain.hip): the reference's one chain per row, in
-// both modes (there is no Q8 form of a whole-element weight).
+// F32 / F16 / BF16 and I2_S (gemv_chain.hip): the reference's one chain
+// (I2_S: two chains) per row, in both modes (there is no Q8 form of these
+// weights).
 hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s);
 __host__ __device__ inline bool is_whole_element(uint32_t dtype) { return dtype == T_F32 || dtype == T_F16 || dtype == T_BF16; }
+__host__ __device__ inline bool is_row_chain(uint32_t dtype) { return is_whole_element(dtype) || dtype == T_I2_S; }
+// Multiply-free block formats (gemv_ternary.hip): Q1_0, Q2_0, STQ1_0, one
+// token per thread, the same kernel in both modes.
+__host__ __device__ inline bool is_ternary_block(uint32_t dtype) {
+    return dtype == T_Q1_0 || dtype == T_Q2_0 || dtype == T_STQ1_0;
+}
+hipError_t launch_gemv_ternary(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                               hipStream_t s);
 
 // Prefill GEMM on the matrix cores (gemm_f16.hip): out[M, n_rows] =
 // A[M, n_cols] . W^T, A binary16, W dequantized to binary16 tiles.

@@ -42,13 +42,19 @@ class GgufDtype(enum.IntEnum):
     Q5K = 13
     Q6K = 14
     BF16 = 30
+    I2S = 36      # BitNet b1.58 (parser.rs L336)
+    Q1_0 = 41     # PrismML Bonsai
+    Q2_0 = 42     # PrismML Ternary-Bonsai
+    # Tencent STQ1_0 shares file tag 42 with Q2_0 (parser.rs L376-377);
+    # the library names it tag 42 with bit 31 set (RCE_QMM_DTYPE_STQ1_0).
+    STQ1_0 = 0x8000002A
 
     @classmethod
     def from_u32(cls, v: int) -> "GgufDtype":
         return cls(v)
 
     def to_u32(self) -> int:
-        return int(self)
+        return 42 if self is GgufDtype.STQ1_0 else int(self)
 
 
 class Mode(enum.IntEnum):
@@ -64,6 +70,8 @@ _GEOMETRY = {
     GgufDtype.Q5_1: (32, 24), GgufDtype.Q8_0: (32, 34), GgufDtype.Q8_1: (32, 36),
     GgufDtype.Q2K: (256, 84), GgufDtype.Q3K: (256, 110), GgufDtype.Q4K: (256, 144),
     GgufDtype.Q5K: (256, 176), GgufDtype.Q6K: (256, 210),
+    GgufDtype.I2S: (128, 32),  # plus one f32 scale per tensor
+    GgufDtype.Q1_0: (128, 18), GgufDtype.Q2_0: (128, 34), GgufDtype.STQ1_0: (256, 42),
 }
 
 

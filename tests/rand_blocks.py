@@ -34,3 +34,21 @@ def float_bytes(rng, dt, n, k, sigma=0.05):
     if dt == O.F16:
         return w.astype(np.float16).view(np.uint8).reshape(-1)
     return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
+
+
+def rand_ternary(rng, dt, n, k, dmax=2.0 ** -4):
+    """Random Q1_0 / Q2_0 / STQ1_0 blocks (random code bytes, f16 scale of
+    dmax/32..dmax), or an I2_S tensor (random codes, then one f32 scale)."""
+    if dt == O.I2_S:
+        b = rng.integers(0, 256, size=n * k // 4 + 4, dtype=np.uint8)
+        b[-4:] = np.frombuffer(np.float32(rng.uniform(dmax / 32, dmax)).tobytes(), np.uint8)
+        return b
+    qk, bb = O.BLOCK[dt]
+    nb = n * (k // qk)
+    b = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    d = rng.uniform(dmax / 32, dmax, nb).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    if dt == O.STQ1_0:
+        b[:, 40:42] = d
+    else:
+        b[:, 0:2] = d
+    return b.reshape(-1)

@@ -52,6 +52,10 @@ def test_supports_matrix():
     assert rce_amd.supports(G.Q3K, 4096) and rce_amd.supports(G.Q3K, 512, M.Q8)
     assert not rce_amd.supports(G.Q3K, 4096 + 32)     # K-quants need 256
     assert not rce_amd.supports(G.Q2K, 4096)          # not in mm_1d's table either: reported unsupported
+    for dt, k in ((G.Q1_0, 2048), (G.Q2_0, 2048), (G.STQ1_0, 2560), (G.I2S, 2560), (G.F16, 7), (G.BF16, 100)):
+        assert rce_amd.supports(dt, k) and rce_amd.supports(dt, k, M.Q8)
+    assert not rce_amd.supports(G.Q1_0, 2048 + 32) and not rce_amd.supports(G.I2S, 2560 + 64)
+    assert G.STQ1_0.to_u32() == 42 and G.from_u32(42) is G.Q2_0
     assert not rce_amd.supports(99, 4096)
 
 

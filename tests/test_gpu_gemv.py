@@ -12,7 +12,7 @@ import pytest
 import oracle as O
 import rce_amd
 from rce_amd import GgufDtype as G, Mode
-from rand_blocks import float_bytes, rand_blocks
+from rand_blocks import float_bytes, rand_blocks, rand_ternary
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
@@ -28,6 +28,8 @@ def make(rng, dt, n, k, sigma=0.02):
         return rand_blocks(rng, dt, n, k)
     if dt in (O.F32, O.F16, O.BF16):
         return float_bytes(rng, dt, n, k, sigma)
+    if dt in (O.Q1_0, O.Q2_0, O.STQ1_0, O.I2_S):  # multiply-free formats: random codes
+        return rand_ternary(rng, dt, n, k)
     w = (rng.standard_normal((n, k)) * sigma).astype(F32)
     return O.quantize(w, dt)
 
@@ -49,6 +51,10 @@ SHAPES = {
     O.F16: [(1, 1), (5, 7), (64, 256), (65, 1000), (2048, 2048), (32000, 2048)],
     O.BF16: [(1, 8), (3, 100), (130, 2048), (4096, 4096)],
     O.F32: [(1, 4), (70, 333), (2048, 2048)],
+    O.Q1_0: [(1, 128), (7, 384), (130, 2048), (2048, 2048), (4096, 4096)],
+    O.Q2_0: [(1, 128), (9, 256), (65, 2048), (2048, 2048), (4096, 4096)],
+    O.STQ1_0: [(1, 256), (5, 512), (100, 2048), (2048, 2048), (4096, 4096)],
+    O.I2_S: [(1, 128), (3, 256), (64, 640), (129, 2048), (2560, 2560), (6912, 2560)],
 }
 CASES = [(dt, n, k) for dt, shapes in SHAPES.items() for (n, k) in shapes]
 
@@ -67,7 +73,8 @@ def test_mm_1d_exact_bit_identical(ctx, dt, n, k):
     assert np.array_equal(bits(serial), bits(want))
 
 
-@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1, O.Q3_K, O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q5_0, O.Q4_1, O.Q3_K, O.F16, O.BF16, O.F32,
+                                O.Q1_0, O.Q2_0, O.STQ1_0, O.I2_S])
 @pytest.mark.parametrize("t_rows", [2, 8])
 def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
     n, k = (700, 2048) if dt != O.Q4_0 else (11008, 4096)
@@ -96,7 +103,7 @@ Q8_CASES = [(O.Q8_0, 4096, 4096), (O.Q4_0, 11008, 4096), (O.Q4_0, 4096, 14336), 
             (O.Q4_K, 2048, 5632), (O.Q6_K, 32000, 2048), (O.Q4_0, 33, 64), (O.Q4_K, 7, 256), (O.Q6_K, 70, 256),
             (O.Q5_K, 4096, 4096), (O.Q5_K, 2048, 5632), (O.Q5_K, 9, 256), (O.Q5_0, 4096, 4096), (O.Q5_0, 13, 96),
             (O.Q4_1, 4096, 4096), (O.Q4_1, 11, 160), (O.Q3_K, 4096, 4096), (O.Q3_K, 5, 256), (O.F16, 2048, 2048),
-            (O.BF16, 70, 96)]
+            (O.BF16, 70, 96), (O.Q1_0, 300, 2048), (O.Q2_0, 33, 512), (O.STQ1_0, 70, 1024), (O.I2_S, 200, 2560)]
 
 
 @pytest.mark.parametrize("dt,n,k", Q8_CASES)
@@ -128,7 +135,8 @@ def test_f16_activations_are_widened_exactly(ctx):
 
 @pytest.mark.parametrize("dt,n,k", [(O.Q8_0, 40, 256), (O.Q4_0, 70, 512), (O.Q4_K, 33, 1024), (O.Q5_K, 35, 1024),
                                     (O.Q6_K, 130, 512), (O.Q5_0, 21, 96), (O.Q4_1, 19, 160), (O.Q3_K, 17, 512),
-                                    (O.F16, 70, 300), (O.BF16, 65, 64), (O.F32, 3, 5)])
+                                    (O.F16, 70, 300), (O.BF16, 65, 64), (O.F32, 3, 5), (O.Q1_0, 9, 256),
+                                    (O.Q2_0, 10, 384), (O.STQ1_0, 11, 512), (O.I2_S, 12, 384)])
 def test_dequant_row_bit_identical(ctx, dt, n, k):
     rng = np.random.default_rng(5000 + dt)
     b = make(rng, dt, n, k)
@@ -136,7 +144,10 @@ def test_dequant_row_bit_identical(ctx, dt, n, k):
     rb = O.row_bytes(dt, k)
     for row in (0, 1, n // 2, n - 1):
         got = w.dequant_row(row)
-        want = O.dequantize(b[row * rb:(row + 1) * rb], dt, k)
+        rowb = b[row * rb:(row + 1) * rb]
+        if dt == O.I2_S:  # the row's codes and the tensor's scale
+            rowb = np.concatenate([rowb, b[-4:]])
+        want = O.dequantize(rowb, dt, k)
         assert np.array_equal(bits(got), bits(want))
 
 

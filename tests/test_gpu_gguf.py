@@ -12,7 +12,7 @@ import rce_amd
 from rce_amd import GgufFile, Mode, QmmError, QuantWeight
 from gguf_writer import STRING, U32, build_gguf, llama_gguf
 from llama_case import device_model, make_weights, tiny_cfg
-from rand_blocks import float_bytes, rand_blocks
+from rand_blocks import float_bytes, rand_blocks, rand_ternary
 
 pytestmark = pytest.mark.gpu
 
@@ -23,7 +23,7 @@ def note(msg):
 
 FORMATS = [(O.Q4_0, 96, 512), (O.Q8_0, 64, 256), (O.Q4_K, 80, 512), (O.Q5_K, 40, 512), (O.Q6_K, 48, 256),
            (O.Q5_0, 24, 96), (O.Q4_1, 24, 160), (O.Q3_K, 24, 512), (O.F16, 70, 100), (O.BF16, 64, 64),
-           (O.F32, 3, 16)]
+           (O.F32, 3, 16), (O.Q1_0, 20, 256), (O.Q2_0, 20, 384), (O.I2_S, 20, 256)]
 
 
 @pytest.mark.parametrize("align", [32, 64])
@@ -33,6 +33,7 @@ def test_weight_from_gguf_matches_bytes(ctx, align):
     tens, keep = [], []
     for dt, n, k in FORMATS:
         b = (rand_blocks(rng, dt, n, k) if dt in (O.Q5_0, O.Q4_1, O.Q3_K)
+             else rand_ternary(rng, dt, n, k) if dt in (O.Q1_0, O.Q2_0, O.I2_S)
              else float_bytes(rng, dt, n, k) if dt in (O.F32, O.F16, O.BF16)
              else rce_amd.quantize((rng.standard_normal((n, k)) * 0.05).astype(np.float32), dt))
         tens.append((f"w.{int(dt)}", (k, n), int(dt), bytes(b)))
@@ -48,6 +49,26 @@ def test_weight_from_gguf_matches_bytes(ctx, align):
         assert np.array_equal(wf.dequant_row(n - 1), wb.dequant_row(n - 1))
         wf.close()
         wb.close()
+    f.close()
+
+
+@pytest.mark.parametrize("arch", ["hunyuan-dense", "llama"])
+def test_tag_42_follows_the_architecture(ctx, arch):
+    """Tag 42 is STQ1_0 in hunyuan-dense files and Q2_0 otherwise
+    (parser.rs L529-541); the file sizes it accordingly and the weight
+    computes in that format."""
+    note(f"tag 42 in a {arch} file")
+    rng = np.random.default_rng(54)
+    dt = O.STQ1_0 if arch == "hunyuan-dense" else O.Q2_0
+    n, k = 40, 512
+    b = rand_ternary(rng, dt, n, k)
+    f = GgufFile.parse(build_gguf([("general.architecture", STRING, arch)], [("w", (k, n), 42, bytes(b))]))
+    assert f.tensor("w").nbytes == b.size and f.tensor("w").dtype == 42
+    w = QuantWeight.from_gguf(ctx, f, "w", n, k)
+    assert w.dtype == dt
+    a = rng.standard_normal(k).astype(np.float32)
+    assert np.array_equal(rce_amd.mm_1d(a, w).view(np.uint32), O.mm_1d(a, b, dt, n, k).view(np.uint32))
+    w.close()
     f.close()
 
 
