@@ -298,6 +298,31 @@ rce_qmm_status rce_qmm_llama_forward_token_dev(rce_qmm_llama *m, const int32_t *
  * device since the last check: RCE_QMM_BAD_SHAPE for a token id out of range. */
 rce_qmm_status rce_qmm_llama_check(rce_qmm_llama *m);
 
+/* ---- the "hip:op-qmm" priced backend (rce-placement-adapter) ------------- */
+
+/* The adapter's qmm dtype ids (QMM_DTYPE_*, rce-placement-adapter/src/lib.rs
+ * L80-90: 1 Q8_0, 2 Q4_K, 3 Q5_K, 4 Q6_K, 5 Q4_0, 6 Q5_0, 7 Q4_1, 8 Q1_0,
+ * 9 Q2_0, 10 Q3_K) as GGUF tags; 0 for QMM_DTYPE_UNKNOWN (0) and any other id. */
+uint32_t rce_qmm_dtype_for_qmm_id(size_t qmm_dtype_id);
+
+/* The library's analytical prior (basis est) for the ("qmm", "hip:op-qmm")
+ * cost cell, in the units of LinearCoeffs (rce-placement L231-242): pJ per
+ * FLOP, pJ per byte, pJ per call.  Replaces nothing in the reference; it is
+ * the cell default_qmm_cost_table (adapter L163-182) inserts for MetalQmm. */
+void rce_qmm_hip_cost_prior(double *a_pj_per_flop, double *b_pj_per_byte, double *c_pj_overhead);
+
+/* HipQmm::cost (the PricedBackend::cost of CpuQmm / MetalQmm, adapter
+ * L214-266) for op "qmm": a_shape = [k], w_shape = [n_rows, n_cols,
+ * weight_bytes, dtype_id].  *picojoules = +inf when the GPU declines (short
+ * shapes, an id without a tag, no kernel for (tag, n_cols)): pick_priced
+ * then routes the call to CpuQmm.  Else a * flops + b * bytes + c with
+ * qmm_1d_flops_bytes (L141-145): flops = 2 n k, bytes = weight_bytes + 4 k
+ * + 4 n.  The coefficients are the cell's (the caller's CostTable may have
+ * calibrated them). */
+rce_qmm_status rce_qmm_hip_cost(const size_t *a_shape, size_t a_len, const size_t *w_shape, size_t w_len,
+                                double a_pj_per_flop, double b_pj_per_byte, double c_pj_overhead,
+                                double *picojoules);
+
 /* ---- GGUF files (rce-ingest-gguf) ---------------------------------------- */
 
 /* A parsed GGUF v2/v3 file: header, metadata and tensor infos

@@ -54,6 +54,9 @@ SIGNATURES = {
     "rce_qmm_gguf_find_tensor": (STATUS, [P, ctypes.c_char_p, P]),
     "rce_qmm_weight_from_gguf": (STATUS, [P, P, ctypes.c_char_p, S, S, P]),
     "rce_qmm_gguf_read_f32": (STATUS, [P, ctypes.c_char_p, P, S]),
+    "rce_qmm_dtype_for_qmm_id": (U32, [S]),
+    "rce_qmm_hip_cost_prior": (None, [P, P, P]),
+    "rce_qmm_hip_cost": (STATUS, [P, S, P, S, ctypes.c_double, ctypes.c_double, ctypes.c_double, P]),
     "rce_qmm_dev_alloc": (STATUS, [P, S, P]),
     "rce_qmm_dev_free": (STATUS, [P, P]),
     "rce_qmm_memcpy_h2d": (STATUS, [P, P, P, S]),
