@@ -8,13 +8,31 @@
 // the launch has few waves, so each wave keeps CHAIN_D chunks (16 KB) in
 // flight: the loads of stage s + 1 are issued before the chain consumes
 // stage s.  Loads past the row's last chunk read chunk 0 (always valid) and
-// are not consumed, so no load sits in a branch.
+// are not consumed, so no load sits in a branch.  The token's activations
+// are first copied to LDS (k <= CHAIN_MAX_K), where every lane reads the
+// same address (a broadcast) instead of holding them in scalar registers.
 #include "qmm_gemv_kernels.h"
 
 namespace rce_qmm {
 namespace {
 
 constexpr int CHAIN_D = 16;  // chunks per stage
+constexpr int I2S_D = 4;     // I2_S: chunks of 64 codes per stage (fully unrolled)
+
+// Copy the token's k activations to LDS (I2_S: position 128 b + 32 s + gp
+// to 128 b + 4 gp + s, so the four positions of one code byte are adjacent).
+template <bool I2S>
+__device__ __forceinline__ void stage_activations(const float *__restrict__ a, size_t k, float *act) {
+    for (size_t i = threadIdx.x; i < k; i += 64) {
+        size_t d = i;
+        if constexpr (I2S) {
+            const size_t r = i % 128;
+            d = i - r + 4 * (r % 32) + r / 32;
+        }
+        act[d] = a[i];
+    }
+    __syncthreads();
+}
 
 template <int DT>
 struct ChainFmt {
@@ -42,7 +60,9 @@ __global__ __launch_bounds__(64) void k_gemv_chain(DevWeight w, const float *__r
     const int lane = threadIdx.x;
     const size_t grp = blockIdx.x, t = blockIdx.y;
     const size_t k = w.n_cols;
-    const float *a = A + t * k;
+    extern __shared__ float act[];
+    stage_activations<false>(A + t * k, k, act);
+    const float *a = act;
     const uint4 *src = reinterpret_cast<const uint4 *>(w.base + grp * w.group_stride) + lane;
     const int nc = (int)((k + E - 1) / E);  // chunks holding values
     const int nfull = (int)(k / E);
@@ -62,9 +82,15 @@ __global__ __launch_bounds__(64) void k_gemv_chain(DevWeight w, const float *__r
             const int c = s * CHAIN_D + i;
             const float *ac = a + (size_t)c * E;
             if (c < nfull) {
+                float av[E];
+#pragma unroll
+                for (int q = 0; q < E / 4; q++) {  // 16-byte broadcast reads
+                    const float4 v = reinterpret_cast<const float4 *>(ac)[q];
+                    av[4 * q] = v.x; av[4 * q + 1] = v.y; av[4 * q + 2] = v.z; av[4 * q + 3] = v.w;
+                }
 #pragma unroll
                 for (int e = 0; e < E; e++) {
-                    const float p = ac[e] * chunk_value<DT>(b[i], e);
+                    const float p = av[e] * chunk_value<DT>(b[i], e);
                     acc = acc + p;
                 }
             } else if (c < nc) {  // the row's last, partial chunk
@@ -98,32 +124,36 @@ __global__ __launch_bounds__(64) void k_gemv_chain_i2s(DevWeight w, const float 
     const int lane = threadIdx.x;
     const size_t grp = blockIdx.x, t = blockIdx.y;
     const size_t k = w.n_cols;
-    const float *a = A + t * k;
+    extern __shared__ float act[];
+    stage_activations<true>(A + t * k, k, act);
     const uint4 *src = reinterpret_cast<const uint4 *>(w.base + grp * w.group_stride) + lane;
     const int nc = (int)(k / 64);
-    const int ns = (nc + CHAIN_D - 1) / CHAIN_D;
+    const int ns = (nc + I2S_D - 1) / I2S_D;
     float pos = 0.0f, neg = 0.0f;
-    uint4 b0[CHAIN_D], b1[CHAIN_D];
+    uint4 b0[I2S_D], b1[I2S_D];
     auto load = [&](uint4 *b, int s) {
 #pragma unroll
-        for (int i = 0; i < CHAIN_D; i++) {
-            const int c = s * CHAIN_D + i;
+        for (int i = 0; i < I2S_D; i++) {
+            const int c = s * I2S_D + i;
             b[i] = src[(size_t)(c < nc ? c : 0) * 64];
         }
     };
     auto consume = [&](const uint4 *b, int s) {
 #pragma unroll
-        for (int i = 0; i < CHAIN_D; i++) {
-            const int c = s * CHAIN_D + i;
+        for (int i = 0; i < I2S_D; i++) {
+            const int c = s * I2S_D + i;
             if (c < nc) {
-                const float *ab = a + (size_t)(c >> 1) * 128 + 16 * (c & 1);
+                // LDS holds block c / 2 with the four positions of code byte gp at 4 gp
+                const float4 *ab = reinterpret_cast<const float4 *>(act + (size_t)(c >> 1) * 128) + 16 * (c & 1);
 #pragma unroll
                 for (int g = 0; g < 16; g++) {
                     const uint32_t byte = (wrd(b[i], g >> 2) >> (8 * (g & 3))) & 0xFFu;
+                    const float4 a4 = ab[g];
+                    const float av4[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                     for (int slot = 0; slot < 4; slot++) {
                         const uint32_t code = (byte >> (6 - 2 * slot)) & 3u;
-                        const uint32_t av = __float_as_uint(ab[32 * slot + g]);
+                        const uint32_t av = __float_as_uint(av4[slot]);
                         pos = pos + __uint_as_float(code == 2 ? av : 0u);
                         neg = neg + __uint_as_float(code == 0 ? av : 0u);
                     }
@@ -149,12 +179,14 @@ __global__ __launch_bounds__(64) void k_gemv_chain_i2s(DevWeight w, const float 
 hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
     if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
     if (w.layout != LAYOUT_IL64_ROWS || t_rows > 65535) return hipErrorInvalidValue;
+    if (w.n_cols > CHAIN_MAX_K) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((w.n_rows + 63) / 64), (unsigned)t_rows);
+    const size_t lds = w.n_cols * sizeof(float);
     switch (w.dtype) {
-    case T_F32: hipLaunchKernelGGL(k_gemv_chain<T_F32>, grid, dim3(64), 0, s, w, a, out); break;
-    case T_F16: hipLaunchKernelGGL(k_gemv_chain<T_F16>, grid, dim3(64), 0, s, w, a, out); break;
-    case T_BF16: hipLaunchKernelGGL(k_gemv_chain<T_BF16>, grid, dim3(64), 0, s, w, a, out); break;
-    case T_I2_S: hipLaunchKernelGGL(k_gemv_chain_i2s, grid, dim3(64), 0, s, w, a, out); break;
+    case T_F32: hipLaunchKernelGGL(k_gemv_chain<T_F32>, grid, dim3(64), lds, s, w, a, out); break;
+    case T_F16: hipLaunchKernelGGL(k_gemv_chain<T_F16>, grid, dim3(64), lds, s, w, a, out); break;
+    case T_BF16: hipLaunchKernelGGL(k_gemv_chain<T_BF16>, grid, dim3(64), lds, s, w, a, out); break;
+    case T_I2_S: hipLaunchKernelGGL(k_gemv_chain_i2s, grid, dim3(64), lds, s, w, a, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -102,9 +102,9 @@ struct STQ1_0Unit {
     __device__ void init(const float *A, size_t k, int t0, int, int col) { ap = A + (size_t)t0 * k + 256 * (size_t)col; }
     __device__ void addends(const Raw &r, float *out) const {
         float pos = 0.0f, neg = 0.0f;
-#pragma unroll 1
+#pragma unroll
         for (int seg = 0; seg < 4; seg++) {  // positions 64 seg .. 64 seg + 63: 16 code bytes, 64 activations
-            const uint4 cw = seg == 0 ? r.c[0] : (seg == 1 ? r.c[1] : (seg == 2 ? r.c[2] : r.c[3]));
+            const uint4 cw = r.c[seg];
             float a[64];
             load_f32x(ap + 64 * seg, a, 64);
 #pragma unroll
@@ -117,6 +117,7 @@ struct STQ1_0Unit {
                     neg = neg + keep(a[16 * i + l], c == 0 ? ~0u : 0u);
                 }
             }
+            asm volatile("" ::: "memory");  // one segment's 64 activations live at a time (no reuse across rows)
         }
         const float t = pos - neg;
         out[0] = h2f(r.d) * t;
@@ -125,13 +126,35 @@ struct STQ1_0Unit {
 
 }  // namespace
 
-hipError_t launch_gemv_ternary(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+namespace {
+// These units are compute-heavy (a chain step per value, 128 or 256 steps
+// per unit) and light on bytes, so the launch maximizes (unit, row) pairs
+// in flight: the smallest block that holds a row's units, one row per lane
+// (two once there are more than 2048 blocks), one token per thread.
+template <class Unit>
+hipError_t launch_ternary(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
+    const int U = units_per_row(w.dtype, w.n_cols);
+    if (U < 1 || U > 256) return hipErrorInvalidValue;
+    const int nt = U <= 64 ? 64 : (U <= 128 ? 128 : 256);
+    const size_t blocks = (w.n_rows + (size_t)(nt / U) - 1) / (size_t)(nt / U);
+    const bool two = blocks > 2048;
+    switch (nt) {
+    case 64: return two ? launch_as<Unit, 64, 2, false>(w, U, a, t_rows, out, s)
+                        : launch_as<Unit, 64, 1, false>(w, U, a, t_rows, out, s);
+    case 128: return two ? launch_as<Unit, 128, 2, false>(w, U, a, t_rows, out, s)
+                         : launch_as<Unit, 128, 1, false>(w, U, a, t_rows, out, s);
+    default: return two ? launch_as<Unit, 256, 2, false>(w, U, a, t_rows, out, s)
+                        : launch_as<Unit, 256, 1, false>(w, U, a, t_rows, out, s);
+    }
+}
+}  // namespace
+
+hipError_t launch_gemv_ternary(const DevWeight &w, const GemvGeom &, const float *a, size_t t_rows, float *out,
                                hipStream_t s) {
-    if (g.tb != 1) return hipErrorInvalidValue;
     switch (w.dtype) {
-    case T_Q1_0: return launch_as_tb<Q1_0Unit, false, 1>(w, g, a, t_rows, out, s);
-    case T_Q2_0: return launch_as_tb<Q2_0Unit, false, 1>(w, g, a, t_rows, out, s);
-    case T_STQ1_0: return launch_as_tb<STQ1_0Unit, false, 1>(w, g, a, t_rows, out, s);
+    case T_Q1_0: return launch_ternary<Q1_0Unit<1>>(w, a, t_rows, out, s);
+    case T_Q2_0: return launch_ternary<Q2_0Unit<1>>(w, a, t_rows, out, s);
+    case T_STQ1_0: return launch_ternary<STQ1_0Unit<1>>(w, a, t_rows, out, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -183,9 +183,9 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
     case T_F32:
     case T_F16:
     case T_BF16:
-        return n_cols <= ((size_t)1 << 26);
+        return n_cols <= CHAIN_MAX_K;
     case T_I2_S:
-        return n_cols % 128 == 0 && n_cols <= ((size_t)1 << 26);
+        return n_cols % 128 == 0 && n_cols <= CHAIN_MAX_K;
     case T_Q1_0:  // 128 activations per thread: blocks of 256 threads only
     case T_Q2_0:
         return n_cols % 128 == 0 && n_cols / 128 <= 256;

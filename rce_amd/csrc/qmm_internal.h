@@ -228,6 +228,7 @@ hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStr
 // (I2_S: two chains) per row, in both modes (there is no Q8 form of these
 // weights).
 hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s);
+constexpr size_t CHAIN_MAX_K = 16384;  // the row-chain kernels stage a token's activations in 64 KB of LDS
 __host__ __device__ inline bool is_whole_element(uint32_t dtype) { return dtype == T_F32 || dtype == T_F16 || dtype == T_BF16; }
 __host__ __device__ inline bool is_row_chain(uint32_t dtype) { return is_whole_element(dtype) || dtype == T_I2_S; }
 // Multiply-free block formats (gemv_ternary.hip): Q1_0, Q2_0, STQ1_0, one
