@@ -182,8 +182,10 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode) {
         return n_cols % 256 == 0 && n_cols / 32 <= 1024;
     case T_F32:
     case T_F16:
-    case T_BF16:
-        return n_cols <= CHAIN_MAX_K;
+    case T_BF16: {  // the row's values padded to whole stages must fit the LDS staging
+        const size_t es = dtype == T_F32 ? 4 : 2, chunks = (n_cols * es + 15) / 16;
+        return ((chunks + CHAIN_STAGE - 1) / CHAIN_STAGE) * CHAIN_STAGE * (16 / es) <= CHAIN_MAX_K;
+    }
     case T_I2_S:
         return n_cols % 128 == 0 && n_cols <= CHAIN_MAX_K;
     case T_Q1_0:  // 128 activations per thread: blocks of 256 threads only
@@ -273,7 +275,8 @@ size_t plan_layout(DevWeight &dw) {
     case T_F16:
     case T_BF16:
         dw.layout = LAYOUT_IL64_ROWS;
-        dw.group_stride = ((k * (dw.dtype == T_F32 ? 4 : 2) + 15) / 16) * 1024;
+        dw.group_stride = (((k * (dw.dtype == T_F32 ? 4 : 2) + 15) / 16 + CHAIN_STAGE - 1) / CHAIN_STAGE) *
+                          CHAIN_STAGE * 1024;
         return dw.group_stride * ((n + 63) / 64);
     case T_Q6_K:
         dw.layout = LAYOUT_IL64_Q6_K;

@@ -58,8 +58,9 @@ enum Layout : int {
     // padded to 16 B.
     LAYOUT_SPLIT_Q3_K = 8,
     // F32 / F16 / BF16: rows in groups of 64, each row cut into 16-byte
-    // chunks (the last one zero-padded); chunk c of row r at
-    // (c * 64 + r % 64) * 16 within the group's group_stride bytes.
+    // chunks, zero-padded to a multiple of CHAIN_STAGE chunks; chunk c of
+    // row r at (c * 64 + r % 64) * 16 within the group's group_stride bytes.
+    // (I2_S: the same without the stage padding.)
     LAYOUT_IL64_ROWS = 9,
     // STQ1_0: the super-blocks' f16 d, padded to 16, then per super-block
     // u the 256 lane codes its codebook gives (64 B at plane1 + 64 u:
@@ -229,6 +230,7 @@ hipError_t launch_dequant_row(const DevWeight &w, size_t row, float *out, hipStr
 // weights).
 hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s);
 constexpr size_t CHAIN_MAX_K = 16384;  // the row-chain kernels stage a token's activations in 64 KB of LDS
+constexpr size_t CHAIN_STAGE = 12;     // F32 / F16 / BF16 rows are padded to whole stages of 12 zero chunks
 __host__ __device__ inline bool is_whole_element(uint32_t dtype) { return dtype == T_F32 || dtype == T_F16 || dtype == T_BF16; }
 __host__ __device__ inline bool is_row_chain(uint32_t dtype) { return is_whole_element(dtype) || dtype == T_I2_S; }
 // Multiply-free block formats (gemv_ternary.hip): Q1_0, Q2_0, STQ1_0, one
