@@ -64,6 +64,7 @@ struct rce_qmm_context {
     std::atomic<int> refs{1};
     rce_qmm_abi::Scratch a_in, a_f32, out;
     rce_qmm_abi::Scratch a_f16;  // f32 activations rounded to f16 for the MFMA GEMM
+    rce_qmm_abi::Scratch act_q;  // several tokens' Q8 activations, quantized once per launch
     // grouped experts: grouping metadata, expert tables, stage buffers
     rce_qmm_abi::Scratch moe_meta, moe_wtab, moe_x, moe_h, moe_h16, moe_y, moe_u;
     std::vector<rce_qmm::DevWeight> moe_wtab_host;  // what moe_wtab holds

@@ -94,6 +94,11 @@ rce_qmm_status run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_d
         a32 = static_cast<const float *>(ctx->a_f32.p);
     }
     if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
+    if (mode == RCE_QMM_MODE_Q8 && gemv_q8_pre_supports(dw.dtype, k, t_rows)) {
+        if ((st = ensure(ctx, ctx->act_q, t_rows * (k + k / 8 + k / 4), s))) return st;  // xq, dx, s16
+        HIP_TRY(launch_gemv_q8_pre(dw, a32, t_rows, out_dev, ctx->act_q.p, s));
+        return RCE_QMM_OK;
+    }
     HIP_TRY(launch_gemv(dw, a32, t_rows, out_dev, (int)mode, s));
     return RCE_QMM_OK;
 }
@@ -177,7 +182,7 @@ void rce_qmm_abi::context_release(rce_qmm_context *ctx) {
     if (ctx->refs.fetch_sub(1) != 1) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16, &ctx->moe_meta, &ctx->moe_wtab, &ctx->moe_x,
+    for (Scratch *s : {&ctx->a_in, &ctx->a_f32, &ctx->out, &ctx->a_f16, &ctx->act_q, &ctx->moe_meta, &ctx->moe_wtab, &ctx->moe_x,
                        &ctx->moe_h, &ctx->moe_h16, &ctx->moe_y, &ctx->moe_u})
         if (s->p) (void)hipFree(s->p);
     (void)hipStreamDestroy(ctx->stream);

@@ -162,6 +162,17 @@ __global__ void k_embed_row(DevWeight w, const int32_t *__restrict__ row_dev, fl
     if (i < w.n_cols) x[i] = dequant_value(w, (size_t)id, i);
 }
 
+// The Q8 activations of `total` / (k / 8) tokens, quantized once into
+// `ws` in the layout ActLds gives a block of that many tokens.
+__global__ __launch_bounds__(256) void k_quantize_act(const float *__restrict__ A, size_t k, int total,
+                                                      unsigned char *__restrict__ ws, int T) {
+    const int task = blockIdx.x * 256 + threadIdx.x;
+    QuantTask q;
+    quant_task_load(A, (int)(k / 8), 0, total, task, q);
+    ActLds L(ws, k, T);
+    quant_task_finish<false>(q, k, total, task, L);
+}
+
 }  // namespace
 
 // Column units per row must fit one block of up to 1024 threads.
@@ -585,6 +596,41 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
     case T_Q5_0: return launch_gemv_fx_q5_0(f, g, a, mode, s);
     case T_Q4_1: return launch_gemv_fx_q4_1(f, g, a, mode, s);
     case T_Q3_K: return launch_gemv_fx_q3_k(f, g, a, mode, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+bool gemv_q8_pre_supports(uint32_t dtype, size_t n_cols, size_t t_rows) {
+    if (t_rows < 2 || t_rows > 65535 * 8 || !gpu_supports(dtype, n_cols, 1)) return false;
+    if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q5_K && dtype != T_Q6_K) return false;
+    return nt_for(units_per_row(dtype, n_cols)) == 256;
+}
+
+hipError_t launch_gemv_q8_pre(const DevWeight &w, const float *a, size_t t_rows, float *out, void *ws,
+                              hipStream_t s) {
+    if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
+    if (!gemv_q8_pre_supports(w.dtype, w.n_cols, t_rows)) return launch_gemv(w, a, t_rows, out, 1, s);
+    GemvGeom g = pick_gemv_geom(w, t_rows, 1);
+    if (g.nt != 256 || g.tb < 2) return launch_gemv(w, a, t_rows, out, 1, s);
+    // the blocks no longer hold the activations in LDS: more rows per lane,
+    // as long as the fold's LDS fits
+    const size_t k = w.n_cols;
+    const int U = units_per_row(w.dtype, k);
+    g.rpl = 8;
+    while (g.rpl > 2 && gemv_lds_bytes(U, 256, g.rpl, g.tb, false, k) > LDS_MAX) g.rpl /= 2;
+    if (gemv_lds_bytes(U, 256, g.rpl, g.tb, false, k) > LDS_MAX) return launch_gemv(w, a, t_rows, out, 1, s);
+    const int total = (int)(t_rows * (k / 8));
+    unsigned char *q = static_cast<unsigned char *>(ws);
+    hipLaunchKernelGGL(k_quantize_act, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a, k, total, q,
+                       (int)t_rows);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (w.dtype) {
+    case T_Q4_0: return launch_as_preq_tb<Q4_0Q8, 8>(w, g, a, t_rows, out, q, s);
+    case T_Q8_0: return launch_as_preq_tb<Q8_0Q8, 8>(w, g, a, t_rows, out, q, s);
+    case T_Q4_K: return launch_as_preq_tb<Q4_KQ8, 4>(w, g, a, t_rows, out, q, s);
+    case T_Q5_K: return launch_as_preq_tb<Q5_KQ8, 4>(w, g, a, t_rows, out, q, s);
+    case T_Q6_K: return launch_as_preq_tb<Q6_KQ8, 2>(w, g, a, t_rows, out, q, s);
     default: return hipErrorInvalidValue;
     }
 }

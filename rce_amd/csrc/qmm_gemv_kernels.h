@@ -1134,6 +1134,8 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     constexpr int TB = Unit::NTOK;
     constexpr int KIND = FX & 7;
     constexpr bool NORM = (FX & FX_NORM) != 0;
+    constexpr bool PREQ = (FX & FX_PREQ) != 0;
+    static_assert(!PREQ || (Q8 && KIND == 0 && !NORM), "pre-quantized activations: plain Q8 launches");
     static_assert(!NORM || TB == 1, "the normalizing forms are single-token");
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
@@ -1171,8 +1173,8 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     const int kq = (int)(k / 8);
     // Q8: the block's quantization tasks; FX_NORM: the tasks of the sum of
     // squares (the host guarantees kq <= 2 NT, so qt0 and qt1 cover the row)
-    const int qtotal = (Q8 || NORM) ? tv * kq : 0;
-    if constexpr (Q8 || NORM) {
+    const int qtotal = ((Q8 && !PREQ) || NORM) ? tv * kq : 0;
+    if constexpr ((Q8 && !PREQ) || NORM) {
         quant_task_load(A, kq, t0, qtotal, tid, qt0);
         quant_task_load(A, kq, t0, qtotal, tid + NT, qt1);
     }
@@ -1209,8 +1211,16 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
         inv = 1.0f / sqrtf(mean_sq + fx.eps);
         if constexpr (!Q8) unit.normalize(fx.norm_w, col, inv);
     }
-    // Phase 2 (Q8): quantize the block's activation rows into LDS.
-    if constexpr (Q8) {
+    // Phase 2 (Q8): quantize the block's activation rows into LDS (or, with
+    // FX_PREQ, read the block's tokens from the pre-quantized buffer).
+    if constexpr (PREQ) {
+        const size_t T = (size_t)fx.preq_t;
+        ActLds L(const_cast<unsigned char *>(fx.preq), k, (int)T);
+        L.xq += (size_t)t0 * k / 4;
+        L.dx += (size_t)t0 * (k / 32);
+        L.s16 += (size_t)t0 * (k / 16);
+        if (active) unit.init_q8(L, k, tv, col);
+    } else if constexpr (Q8) {
         ActLds L(lds, k, TB);
         quant_task_finish<NORM>(qt0, k, qtotal, tid, L, inv);
         quant_task_finish<NORM>(qt1, k, qtotal, tid + NT, L, inv);
@@ -1405,6 +1415,49 @@ hipError_t launch_as_nt(const DevWeight &w, const GemvGeom &g, const float *a, s
     default: return hipErrorInvalidValue;
     }
 #undef RCE_RPL
+}
+
+// Plain Q8 launches on pre-quantized activations (FX_PREQ): no activation
+// LDS, 256 threads, 2 / 4 / 8 rows per lane, 2 / 4 / 8 tokens per thread.
+template <class Unit, int RPL>
+hipError_t launch_as_preq(const DevWeight &w, int U, const float *a, size_t t_rows, float *out,
+                          const unsigned char *preq, hipStream_t s) {
+    constexpr int NT = 256, TB = Unit::NTOK;
+    const int P = NT / U, RT = P * RPL;
+    if (P < 1) return hipErrorInvalidConfiguration;
+    const size_t lds = gemv_lds_bytes(U, NT, RPL, TB, false, w.n_cols);
+    if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
+    GemvFx fx{};
+    fx.preq = preq;
+    fx.preq_t = (int)t_rows;
+    dim3 grid((unsigned)((w.n_rows + RT - 1) / RT), (unsigned)((t_rows + TB - 1) / TB)), block(NT);
+    hipLaunchKernelGGL((k_gemv_as<Unit, NT, RPL, true, FX_PREQ>), grid, block, lds, s, w, a, out, (int)t_rows, U, fx);
+    return hipGetLastError();
+}
+
+template <template <int> class Unit, int MAXTB>
+hipError_t launch_as_preq_tb(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
+                             const unsigned char *preq, hipStream_t s) {
+    const int U = units_per_row(w.dtype, w.n_cols);
+    if (g.nt != 256) return hipErrorInvalidValue;
+#define RCE_PQ(TB)                                                                   \
+    switch (g.rpl) {                                                                 \
+    case 2: return launch_as_preq<Unit<TB>, 2>(w, U, a, t_rows, out, preq, s);       \
+    case 4: return launch_as_preq<Unit<TB>, 4>(w, U, a, t_rows, out, preq, s);       \
+    case 8: return launch_as_preq<Unit<TB>, 8>(w, U, a, t_rows, out, preq, s);       \
+    default: return hipErrorInvalidValue;                                            \
+    }
+    switch (g.tb) {
+    case 2: RCE_PQ(2)
+    case 4:
+        if constexpr (MAXTB >= 4) { RCE_PQ(4) }
+        return hipErrorInvalidValue;
+    case 8:
+        if constexpr (MAXTB >= 8) { RCE_PQ(8) }
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+#undef RCE_PQ
 }
 
 // MAXTB: the most tokens per thread the unit's registers allow.

@@ -120,11 +120,16 @@ __device__ __forceinline__ float silu_ref(float x) {
 // sequential fold per task, tasks t and t + NT on thread t, then a fixed
 // tree over the block), inv = 1 / sqrt(sum / n + eps), value (x * inv) * w.
 enum : int { FX_SEG = 1, FX_RESIDUAL = 2, FX_SWIGLU = 3, FX_NORM = 8 };
+// Plain launches only: the Q8 activations were quantized beforehand into
+// GemvFx::preq (launch_gemv_q8_pre); blocks read their tokens' slices.
+constexpr int FX_PREQ = 16;
 
 struct GemvFx {
     DevWeight w2, w3;      // FX_SEG: segments 1 and 2; FX_SWIGLU: w2 = up
     float *out2, *out3;    // FX_SEG: their outputs
     unsigned blk2, blk3;   // FX_SEG: first block of segments 1 and 2
+    const unsigned char *preq;  // FX_PREQ: the quantized activations of all preq_t tokens
+    int preq_t;
     const float *res;      // FX_RESIDUAL
     const float *norm_w;   // FX_NORM
     float eps;             // FX_NORM
@@ -206,6 +211,13 @@ hipError_t launch_f16_to_f32(const uint16_t *src, float *dst, size_t n, hipStrea
 // overrides the shape the library picks (tuning only; nullptr = pick).
 hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float *out, int mode,
                        hipStream_t s, const GemvGeom *geom = nullptr);
+// Q8 with several tokens: the activations are quantized once into `ws`
+// (act_lds_bytes(n_cols, t_rows) bytes, 16-byte aligned) by one small
+// kernel instead of by every block; the results are the same bits.  Falls
+// back to launch_gemv where the pre-quantized form has no kernel.
+hipError_t launch_gemv_q8_pre(const DevWeight &w, const float *a, size_t t_rows, float *out, void *ws,
+                              hipStream_t s);
+bool gemv_q8_pre_supports(uint32_t dtype, size_t n_cols, size_t t_rows);
 GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode);
 // Per-format launchers (gemv_<format>.hip), shape already chosen.
 hipError_t launch_gemv_q4_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,
