@@ -164,9 +164,9 @@ __global__ void k_embed_row(DevWeight w, const int32_t *__restrict__ row_dev, fl
 
 // The Q8 activations of `total` / (k / 8) tokens, quantized once into
 // `ws` in the layout ActLds gives a block of that many tokens.
-__global__ __launch_bounds__(256) void k_quantize_act(const float *__restrict__ A, size_t k, int total,
-                                                      unsigned char *__restrict__ ws, int T) {
-    const int task = blockIdx.x * 256 + threadIdx.x;
+__global__ __launch_bounds__(64) void k_quantize_act(const float *__restrict__ A, size_t k, int total,
+                                                     unsigned char *__restrict__ ws, int T) {
+    const int task = blockIdx.x * 64 + threadIdx.x;
     QuantTask q;
     quant_task_load(A, (int)(k / 8), 0, total, task, q);
     ActLds L(ws, k, T);
@@ -612,16 +612,20 @@ hipError_t launch_gemv_q8_pre(const DevWeight &w, const float *a, size_t t_rows,
     if (!gemv_q8_pre_supports(w.dtype, w.n_cols, t_rows)) return launch_gemv(w, a, t_rows, out, 1, s);
     GemvGeom g = pick_gemv_geom(w, t_rows, 1);
     if (g.nt != 256 || g.tb < 2) return launch_gemv(w, a, t_rows, out, 1, s);
+    if (g.tb > 4) g.tb = 4;  // more token groups re-read the weight, mostly from the Infinity Cache
     // the blocks no longer hold the activations in LDS: more rows per lane,
     // as long as the fold's LDS fits
     const size_t k = w.n_cols;
     const int U = units_per_row(w.dtype, k);
-    g.rpl = 8;
+    // (every block reads its tokens' slices of the workspace: fewer, taller
+    // blocks read less of it)
+    g.rpl = 16;
+    while (g.rpl > 2 && (w.n_rows + (size_t)(256 / U) * g.rpl - 1) / ((size_t)(256 / U) * g.rpl) < 256) g.rpl /= 2;
     while (g.rpl > 2 && gemv_lds_bytes(U, 256, g.rpl, g.tb, false, k) > LDS_MAX) g.rpl /= 2;
     if (gemv_lds_bytes(U, 256, g.rpl, g.tb, false, k) > LDS_MAX) return launch_gemv(w, a, t_rows, out, 1, s);
     const int total = (int)(t_rows * (k / 8));
     unsigned char *q = static_cast<unsigned char *>(ws);
-    hipLaunchKernelGGL(k_quantize_act, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a, k, total, q,
+    hipLaunchKernelGGL(k_quantize_act, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, a, k, total, q,
                        (int)t_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -1418,7 +1418,7 @@ hipError_t launch_as_nt(const DevWeight &w, const GemvGeom &g, const float *a, s
 }
 
 // Plain Q8 launches on pre-quantized activations (FX_PREQ): no activation
-// LDS, 256 threads, 2 / 4 / 8 rows per lane, 2 / 4 / 8 tokens per thread.
+// LDS, 256 threads, 2 / 4 / 8 / 16 rows per lane, 2 / 4 / 8 tokens per thread.
 template <class Unit, int RPL>
 hipError_t launch_as_preq(const DevWeight &w, int U, const float *a, size_t t_rows, float *out,
                           const unsigned char *preq, hipStream_t s) {
@@ -1445,6 +1445,7 @@ hipError_t launch_as_preq_tb(const DevWeight &w, const GemvGeom &g, const float 
     case 2: return launch_as_preq<Unit<TB>, 2>(w, U, a, t_rows, out, preq, s);       \
     case 4: return launch_as_preq<Unit<TB>, 4>(w, U, a, t_rows, out, preq, s);       \
     case 8: return launch_as_preq<Unit<TB>, 8>(w, U, a, t_rows, out, preq, s);       \
+    case 16: return launch_as_preq<Unit<TB>, 16>(w, U, a, t_rows, out, preq, s);     \
     default: return hipErrorInvalidValue;                                            \
     }
     switch (g.tb) {
