@@ -193,7 +193,9 @@ rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, size_t n_rows,
 /* mm_batched on device buffers: a_dev [t_rows, n_cols] of a_dtype
  * (RCE_QMM_F32, or RCE_QMM_F16 whose values are widened exactly to f32 as
  * the reference's callers do), out_dev [t_rows, n_rows] f32.  No host
- * synchronization; the library's scratch is owned by the context. */
+ * synchronization; the library's scratch is owned by the context, so calls
+ * on one context must not overlap on different streams (one context per
+ * stream). */
 rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype,
                                       size_t t_rows, const rce_qmm_weight *w, float *out_dev,
                                       rce_qmm_mode mode, void *stream);
