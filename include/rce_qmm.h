@@ -325,6 +325,17 @@ rce_qmm_status rce_qmm_hip_cost(const size_t *a_shape, size_t a_len, const size_
                                 double a_pj_per_flop, double b_pj_per_byte, double c_pj_overhead,
                                 double *picojoules);
 
+/* The GPU's accumulated energy in microjoules (ROCm SMI's energy counter,
+ * opened at first use), and the reading's timestamp in ns: what an
+ * EnergyMeter (adapter L48-74) for HIP dispatches brackets a call with, as
+ * SubstrateEnergyMeter does with RAPL (substrate_meter.rs L104-130); its
+ * basis is `reported`.  `device` is ROCm SMI's index (the HIP index on a
+ * one-GPU node).  On MI355X the counter advances once a second (15.3 uJ
+ * units): a window shorter than that reads 0, as the reference's meter
+ * expects of tiny dispatches; calibrate over windows of seconds.
+ * RCE_QMM_NOT_FOUND where no counter can be read. */
+rce_qmm_status rce_qmm_energy_read(int device, uint64_t *microjoules, uint64_t *timestamp_ns);
+
 /* ---- GGUF files (rce-ingest-gguf) ---------------------------------------- */
 
 /* A parsed GGUF v2/v3 file: header, metadata and tensor infos

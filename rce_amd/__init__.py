@@ -13,4 +13,5 @@ from .qmm import (  # noqa: F401
 )
 from .llama import TinyLlamaBlock, TinyLlamaConfig, TinyLlamaRuntime, TinyLlamaWeights, load_weights  # noqa: F401,E402
 from .gguf import GgufFile, GgufMetadata, GgufTensorInfo, GgufValue, split_experts  # noqa: F401,E402
-from .placement import HipQmm, HostQuantWeight, LinearCoeffs, hip_cost_prior, pick_priced, qmm_dtype_id  # noqa: F401,E402
+from .placement import (GpuEnergyMeter, HipQmm, HostQuantWeight, LinearCoeffs, hip_cost_prior,  # noqa: F401,E402
+                        pick_priced, qmm_dtype_id)

@@ -126,6 +126,51 @@ class HipQmm:
         self._dev.clear()
 
 
+class GpuEnergyMeter:
+    """EnergyMeter (adapter L48-74) over the GPU's energy counter
+    (rce_qmm_energy_read), the MI355X counterpart of SubstrateEnergyMeter
+    (substrate_meter.rs L60-130): start() snapshots the counter under a
+    token, end(token) returns the picojoules since, basis "reported".
+    The counter advances once a second on MI355X, so windows shorter than
+    that read 0 (the reference's meter expects that of tiny dispatches).
+    ``open`` returns None where no counter can be read."""
+
+    def __init__(self, device: int):
+        self.device = device
+        self._windows: dict = {}
+        self._next = 0
+
+    @classmethod
+    def open(cls, device: int = 0) -> "GpuEnergyMeter | None":
+        m = cls(device)
+        return m if m._read() is not None else None
+
+    def _read(self):
+        uj = ctypes.c_uint64()
+        return uj.value if lib().rce_qmm_energy_read(self.device, ctypes.byref(uj), None) == 0 else None
+
+    def basis(self) -> str:
+        return "reported"
+
+    def start(self):
+        uj = self._read()
+        if uj is None:
+            return None
+        self._next += 1
+        self._windows[self._next] = uj
+        return self._next
+
+    def end(self, token):
+        prior = self._windows.pop(token, None)
+        now = self._read()
+        if prior is None or now is None:
+            return None
+        return max(0, now - prior) * 1_000_000  # uJ -> pJ
+
+    def windows_open(self) -> int:
+        return len(self._windows)
+
+
 def pick_priced(backends, op: str, shapes):
     """rce-vm-scheduler pick_priced (L98-115): the first backend with the
     strictly lowest cost among those that handle `op`; None if none does."""
