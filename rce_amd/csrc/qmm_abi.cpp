@@ -499,19 +499,32 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
         if ((st = ensure(ctx, ctx->moe_x, n_pairs * d_model * sizeof(float), s))) return st;
         float *xg = static_cast<float *>(ctx->moe_x.p);
         HIP_TRY(launch_gather_rows(x_dev, tok_of_slot, n_slots, n_pairs, d_model, xg, s));
-        // 3. per expert: h = silu(W1 x) [* (W3 x)], y = W2 h (the reference's per-row products)
+        // 3. per expert: h = silu(W1 x) [* (W3 x)], y = W2 h (the reference's per-row products).
+        // Q8 with several tokens quantizes each launch's activations once
+        // (launch_gemv_q8_pre; the launches are ordered on the stream, so
+        // they share one workspace).
+        size_t n_max = 0;
+        for (size_t e = 0; e < n_expert; e++) n_max = std::max<size_t>(n_max, (size_t)(hoffs[e + 1] - hoffs[e]));
+        const size_t kmax = std::max(d_model, d_ff);
+        if (mode == RCE_QMM_MODE_Q8 && n_max >= 2)
+            if ((st = ensure(ctx, ctx->act_q, n_max * (kmax + kmax / 8 + kmax / 4), s))) return st;
+        auto gemv = [&](const DevWeight &dw, const float *a, size_t n, float *o) {
+            if (mode == RCE_QMM_MODE_Q8 && gemv_q8_pre_supports(dw.dtype, dw.n_cols, n))
+                return launch_gemv_q8_pre(dw, a, n, o, ctx->act_q.p, s);
+            return launch_gemv(dw, a, n, o, (int)mode, s);
+        };
         for (size_t e = 0; e < n_expert; e++) {
             const size_t r0 = (size_t)hoffs[e], n = (size_t)(hoffs[e + 1] - hoffs[e]);
             if (n == 0) continue;
-            HIP_TRY(launch_gemv(w1[e]->dw, xg + r0 * d_model, n, h + r0 * d_ff, (int)mode, s));
-            if (w3) HIP_TRY(launch_gemv(w3[e]->dw, xg + r0 * d_model, n, u + r0 * d_ff, (int)mode, s));
+            HIP_TRY(gemv(w1[e]->dw, xg + r0 * d_model, n, h + r0 * d_ff));
+            if (w3) HIP_TRY(gemv(w3[e]->dw, xg + r0 * d_model, n, u + r0 * d_ff));
         }
         if (w3) HIP_TRY(launch_swiglu_slots(h, u, n_slots, n_pairs, d_ff, s));
         else HIP_TRY(launch_silu_inplace(h, n_slots, n_pairs, d_ff, s));
         for (size_t e = 0; e < n_expert; e++) {
             const size_t r0 = (size_t)hoffs[e], n = (size_t)(hoffs[e + 1] - hoffs[e]);
             if (n == 0) continue;
-            HIP_TRY(launch_gemv(w2[e]->dw, h + r0 * d_ff, n, y + r0 * d_model, (int)mode, s));
+            HIP_TRY(gemv(w2[e]->dw, h + r0 * d_ff, n, y + r0 * d_model));
         }
     }
     // 5. combine in decision order
