@@ -421,6 +421,8 @@ def main():
     ap.add_argument("--rows", default="sweep,gemm,moe,llama",
                     help="per-format rows: comma-separated subset of sweep,gemm,moe,llama")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--sweep-only", default="",
+                    help="run only the sweep rows whose name contains this text (e.g. 'b8'; profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every GPU box here has one, and this build has no multi-GPU "
@@ -491,6 +493,7 @@ def main():
             ("STQ1_0 2048x2048 b1", G.STQ1_0, 2048, 2048, 1),
             ("I2_S 6912x2560 b1", G.I2S, 6912, 2560, 1),       # BitNet b1.58 2B FFN up
         ]
+        sweep = [r for r in sweep if args.sweep_only in r[0]]
         for name, sdt, sn, sk, st in sweep:
             for m in ((Mode.EXACT,) if int(sdt) in FLOAT_DTYPES else (Mode.EXACT, Mode.Q8)):
                 steps = max(20, args.steps // 2)
