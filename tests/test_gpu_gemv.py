@@ -196,3 +196,26 @@ def test_errors_and_empty_inputs(ctx):
     assert e.value.status == 3
     with pytest.raises(rce_amd.QmmError):
         rce_amd.mm_1d(np.zeros(63, F32), w)
+
+
+# The largest K each kernel family takes (rce_qmm_supports): 1024 column
+# units per row (blocks of 1024 threads), the ternary blocks' 256 units,
+# and the row chains' LDS staging (F16: 16 KB values padded to stages).
+MAX_K = [(O.Q4_0, 48, 32768), (O.Q8_0, 40, 32768), (O.Q5_0, 24, 32768), (O.Q4_K, 24, 65536),
+         (O.Q6_K, 70, 65536), (O.Q3_K, 16, 32768), (O.F16, 80, 16320), (O.Q1_0, 24, 32768),
+         (O.STQ1_0, 16, 65536), (O.I2_S, 70, 16384)]
+
+
+@pytest.mark.parametrize("dt,n,k", MAX_K)
+def test_largest_k(ctx, dt, n, k):
+    note(f"largest k: dtype={dt} n={n} k={k}")
+    assert rce_amd.supports(dt, k)
+    rng = np.random.default_rng(9000 + (dt & 0xFF))
+    b = make(rng, dt, n, k)
+    a = rng.standard_normal(k).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    assert np.array_equal(bits(rce_amd.mm_1d(a, w)), bits(O.mm_1d(a, b, dt, n, k)))
+    if rce_amd.supports(dt, k, Mode.Q8):
+        x = rng.standard_normal((3, k)).astype(F32)
+        assert np.array_equal(bits(run_dev(ctx, w, x, Mode.Q8)), bits(O.mm_batched_q8(x, b, dt, n, k)))
+    w.close()
