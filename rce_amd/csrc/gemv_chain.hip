@@ -95,7 +95,17 @@ __global__ __launch_bounds__(64) void k_gemv_chain(DevWeight w, const float *__r
             }
 #pragma unroll
             for (int e = 0; e < E; e++) {
-                const float p = av[e] * chunk_value<DT>(b[i], e);
+                float p;
+                if constexpr (DT == T_F16) {
+                    // fma(w, a, +0.0) on the widened f16 is one v_fma_mix_f32
+                    // (no separate convert): the product rounded once, as
+                    // v_mul_f32 rounds it.  A zero product is +0.0 here where
+                    // the multiply may give -0.0; either adds the same to a
+                    // chain that starts at +0.0 and is never -0.0.
+                    p = __builtin_fmaf(chunk_value<DT>(b[i], e), av[e], 0.0f);
+                } else {
+                    p = av[e] * chunk_value<DT>(b[i], e);
+                }
                 acc = acc + p;
             }
         }
