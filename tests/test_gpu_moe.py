@@ -128,6 +128,13 @@ def test_moe_mixtral_shapes(ctx):
     assert normwise(got, ref) < 3e-3
     got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.EXACT)
     assert normwise(got, ref) < 1e-5
+    # Q8: each expert's six tokens through the pre-quantized multi-token
+    # GEMV (K 4096, then 14336).  The device silu's last-bit differences can
+    # move one hidden activation across a Q8 rounding boundary (one block's
+    # integer by one) among 14336 per token: 1e-3, as the decoder's Q8 test.
+    note("  mode=Q8")
+    got = run_moe(ctx, w1, w2, dt, dm, dff, x, ids, gw, Mode.Q8)
+    assert normwise(got, q8_reference(x, w1, w2, dt, dm, dff, ids, gw)) < 1e-3
 
 
 def test_moe_bad_ids(ctx):
