@@ -134,9 +134,13 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
     for (int d = 0; d < DPL; d++) vcur[d] = qkv[qd + kvd + (size_t)g * DH + lane + 64 * d];
     // A run's cached keys / values, every load unconditional: rows at or
-    // past pos read row 0 (always in range).  Value rows past pos become 0
-    // and row pos this position's values, so every value row is finite;
-    // key rows at or past pos are unused (the current key comes from LDS).
+    // past pos read row 0 (always in range); key rows at or past pos are
+    // unused (the current key comes from LDS).  The loaded value rows are
+    // replaced where they are consumed (value_at): row pos by this
+    // position's values, rows past pos by 0, so every value row used is
+    // finite.  Doing that here instead would put a branch after each load
+    // whose untaken side waits for the load, and the run's loads would no
+    // longer be in flight together.
     auto load_run = [&](int c0) {
         const int r = c0 + lane;
         const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(r < pos ? r : 0) * kvd);
@@ -147,11 +151,11 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
             const int rj = c0 + j;
             const float *vp = vbase + (size_t)(rj < pos ? rj : 0) * kvd;
 #pragma unroll
-            for (int d = 0; d < DPL; d++) {
-                const float x = vp[lane + 64 * d];
-                vv[j][d] = rj < pos ? x : (rj == pos ? vcur[d] : 0.0f);
-            }
+            for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
         }
+    };
+    auto value_at = [&](int rj, int j, int d) {
+        return rj < pos ? vv[j][d] : (rj == pos ? vcur[d] : 0.0f);
     };
     if (j0 < j1) load_run(j0);
     __syncthreads();
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
                     const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), j + k));
 #pragma unroll
                     for (int d = 0; d < DPL; d++) {
-                        const float t = pj * vv[j + k][d];
+                        const float t = pj * value_at(c0 + j + k, j + k, d);
                         a[k][d] = a[k][d] + t;
                     }
                 }
