@@ -200,6 +200,23 @@ rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, u
                                       size_t t_rows, const rce_qmm_weight *w, float *out_dev,
                                       rce_qmm_mode mode, void *stream);
 
+/* No counterpart in the reference.  rce_qmm_mm_batched_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): the same arguments,
+ * kernels and bits, and no hipMalloc / hipFree / allocating library call.
+ * The scratch the call needs -- 4 t_rows n_cols bytes to widen F16
+ * activations (EXACT, Q8), 1.375 t_rows n_cols bytes for several tokens'
+ * Q8 activations (Q8, t_rows >= 2), 2 t_rows n_cols bytes to round F32
+ * activations to f16 (F16_MFMA), each rounded up to 256 -- comes from a
+ * fixed device array of RCE_QMM_NOALLOC_SCRATCH_BYTES that each GPU the
+ * library runs on holds until the process ends; a call that needs more
+ * returns RCE_QMM_BAD_SHAPE.  All calls on one GPU share that array:
+ * calls that overlap on one GPU (other streams, other contexts) race. */
+#define RCE_QMM_NOALLOC_SCRATCH_BYTES (16u << 20)
+rce_qmm_status rce_qmm_mm_batched_dev_noalloc(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype,
+                                              size_t t_rows, const rce_qmm_weight *w, float *out_dev,
+                                              rce_qmm_mode mode, void *stream);
+
 /* ---- grouped experts (MoE) ----------------------------------------------- */
 
 /* rce_op_moe::moe_router (rce-op-moe/src/lib.rs L35-73) from given router

@@ -33,6 +33,7 @@ SIGNATURES = {
     "rce_qmm_dequant_row": (STATUS, [P, P, S, P]),
     "rce_qmm_quantize": (STATUS, [U32, P, S, S, P, S]),
     "rce_qmm_mm_batched_dev": (STATUS, [P, P, U32, S, P, P, I, P]),
+    "rce_qmm_mm_batched_dev_noalloc": (STATUS, [P, P, U32, S, P, P, I, P]),
     "rce_qmm_moe_router": (STATUS, [P, S, S, S, I, P, P]),
     "rce_qmm_moe_ffn_dev": (STATUS, [P, P, P, S, P, S, P, P, S, P, I, P]),
     "rce_qmm_moe_swiglu_dev": (STATUS, [P, P, P, P, S, P, S, P, P, S, P, I, P]),

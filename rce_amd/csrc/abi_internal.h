@@ -104,6 +104,19 @@ inline rce_qmm_status ensure(rce_qmm_context *ctx, Scratch &s, size_t bytes, hip
     return RCE_QMM_OK;
 }
 
+// mm_batched_dev's device-side core (qmm_abi.cpp).  fixed == nullptr: the
+// scratch comes from the context's grow-only buffers; else from the
+// fixed_cap bytes at `fixed`, with no allocation (RCE_QMM_BAD_SHAPE when
+// the call needs more than batched_scratch_bytes allows).
+rce_qmm_status run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype, size_t t_rows,
+                           const rce_qmm_weight *w, float *out_dev, rce_qmm_mode mode, hipStream_t s, void *fixed,
+                           size_t fixed_cap);
+// Scratch bytes run_batched needs for these arguments.
+size_t batched_scratch_bytes(const DevWeight &dw, uint32_t a_dtype, size_t t_rows, rce_qmm_mode mode);
+// Resolve the device address of the no-allocation entry point's fixed
+// scratch on `device` (the current device), once per device (noalloc.hip).
+rce_qmm_status noalloc_setup(int device);
+
 inline rce_qmm_status check_weight_ctx(rce_qmm_context *ctx, const rce_qmm_weight *w) {
     if (!ctx || !w) return fail(RCE_QMM_NULL_ARGUMENT, "null context or weight");
     if (ctx->device != w->device) return fail(RCE_QMM_BAD_SHAPE, "weight lives on another device than the context");

@@ -59,49 +59,108 @@ bool supports_mode(uint32_t dtype, size_t n_cols, int mode) {
     return gpu_supports(dtype, n_cols, mode);
 }
 
-// The prefill GEMM; f32 activations are rounded to f16 first.
-rce_qmm_status run_gemm(rce_qmm_context *ctx, const void *a_dev, bool a_f16, size_t t_rows, const DevWeight &dw,
-                        float *out_dev, hipStream_t s) {
+// Scratch pointers of one mm_batched_dev call: each is null when the
+// call's (a_dtype, mode, shape) does not need it.
+struct BatchedScratch {
+    float *a_f32 = nullptr;       // F16 activations widened to f32 (EXACT, Q8)
+    unsigned char *act_q = nullptr;  // Q8 activations of several tokens, quantized once
+    void *a_f16 = nullptr;        // F32 activations rounded to f16 (F16_MFMA)
+};
+
+}  // namespace
+
+// The scratch bytes mm_batched_dev needs for these arguments (the parts
+// BatchedScratch names, each rounded up to 256 bytes), given a supported
+// (dtype, n_cols, mode).
+size_t rce_qmm_abi::batched_scratch_bytes(const DevWeight &dw, uint32_t a_dtype, size_t t_rows, rce_qmm_mode mode) {
+    const size_t k = dw.n_cols;
+    if (t_rows == 0 || dw.n_rows == 0) return 0;
+    if (mode == RCE_QMM_MODE_F16_MFMA) return a_dtype == T_F16 ? 0 : align_up(t_rows * k * 2, 256);
+    size_t b = 0;
+    if (a_dtype == T_F16) b += align_up(t_rows * k * sizeof(float), 256);
+    if (mode == RCE_QMM_MODE_Q8 && gemv_q8_pre_supports(dw.dtype, k, t_rows)) b += align_up(t_rows * (k + k / 8 + k / 4), 256);
+    return b;
+}
+
+namespace {
+
+// The prefill GEMM; f32 activations are rounded to f16 first (into sc.a_f16).
+rce_qmm_status run_gemm(const void *a_dev, bool a_f16, size_t t_rows, const DevWeight &dw, float *out_dev,
+                        const BatchedScratch &sc, hipStream_t s) {
     const void *a = a_dev;
     if (!a_f16) {
-        rce_qmm_status st;
-        const size_t n = t_rows * dw.n_cols;
-        if ((st = ensure(ctx, ctx->a_f16, n * 2, s))) return st;
-        HIP_TRY(launch_f32_to_f16(static_cast<const float *>(a_dev), ctx->a_f16.p, n, s));
-        a = ctx->a_f16.p;
+        HIP_TRY(launch_f32_to_f16(static_cast<const float *>(a_dev), sc.a_f16, t_rows * dw.n_cols, s));
+        a = sc.a_f16;
     }
     HIP_TRY(launch_gemm_f16(dw, a, t_rows, out_dev, s));
     return RCE_QMM_OK;
 }
 
-// Device-side core shared by the host and device entry points.
-rce_qmm_status run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype, size_t t_rows,
-                           const rce_qmm_weight *w, float *out_dev, rce_qmm_mode mode, hipStream_t s) {
+}  // namespace
+
+// Device-side core shared by the host and device entry points.  fixed ==
+// nullptr: the scratch comes from the context's grow-only buffers (which
+// may allocate); else from the fixed_cap bytes at fixed (no allocation;
+// RCE_QMM_BAD_SHAPE when the call needs more).
+rce_qmm_status rce_qmm_abi::run_batched(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype, size_t t_rows,
+                                        const rce_qmm_weight *w, float *out_dev, rce_qmm_mode mode, hipStream_t s,
+                                        void *fixed, size_t fixed_cap) {
     const DevWeight &dw = w->dw;
     if (!supports_mode(dw.dtype, dw.n_cols, (int)mode))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "dtype " + std::to_string(dw.dtype) + " with n_cols " +
                                                    std::to_string(dw.n_cols) + " has no GPU kernel in mode " +
                                                    std::to_string((int)mode));
     if (a_dtype != T_F32 && a_dtype != T_F16) return fail(RCE_QMM_UNSUPPORTED_DTYPE, "activations must be F32 or F16");
+    if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8 && mode != RCE_QMM_MODE_F16_MFMA)
+        return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
     if (t_rows == 0 || dw.n_rows == 0) return RCE_QMM_OK;
-    if (mode == RCE_QMM_MODE_F16_MFMA) return run_gemm(ctx, a_dev, a_dtype == T_F16, t_rows, dw, out_dev, s);
     const size_t k = dw.n_cols;
-    const float *a32 = static_cast<const float *>(a_dev);
+    const bool mfma = mode == RCE_QMM_MODE_F16_MFMA;
+    const bool widen = !mfma && a_dtype == T_F16;
+    const bool preq = mode == RCE_QMM_MODE_Q8 && gemv_q8_pre_supports(dw.dtype, k, t_rows);
+    const size_t f32_b = widen ? t_rows * k * sizeof(float) : 0;
+    const size_t q8_b = preq ? t_rows * (k + k / 8 + k / 4) : 0;  // xq, dx, s16
+    const size_t f16_b = mfma && a_dtype == T_F32 ? t_rows * k * 2 : 0;
+    BatchedScratch sc;
     rce_qmm_status st;
-    if (a_dtype == T_F16) {
-        if ((st = ensure(ctx, ctx->a_f32, t_rows * k * sizeof(float), s))) return st;
-        HIP_TRY(launch_f16_to_f32(static_cast<const uint16_t *>(a_dev), static_cast<float *>(ctx->a_f32.p), t_rows * k, s));
-        a32 = static_cast<const float *>(ctx->a_f32.p);
+    if (fixed) {
+        const size_t need = batched_scratch_bytes(dw, a_dtype, t_rows, mode);
+        if (need > fixed_cap)
+            return fail(RCE_QMM_BAD_SHAPE, "the call needs " + std::to_string(need) + " bytes of scratch; the fixed scratch holds " +
+                                               std::to_string(fixed_cap));
+        unsigned char *p = static_cast<unsigned char *>(fixed);
+        if (f32_b) { sc.a_f32 = reinterpret_cast<float *>(p); p += align_up(f32_b, 256); }
+        if (q8_b) { sc.act_q = p; p += align_up(q8_b, 256); }
+        if (f16_b) { sc.a_f16 = p; p += align_up(f16_b, 256); }
+    } else {
+        if (f32_b) {
+            if ((st = ensure(ctx, ctx->a_f32, f32_b, s))) return st;
+            sc.a_f32 = static_cast<float *>(ctx->a_f32.p);
+        }
+        if (q8_b) {
+            if ((st = ensure(ctx, ctx->act_q, q8_b, s))) return st;
+            sc.act_q = static_cast<unsigned char *>(ctx->act_q.p);
+        }
+        if (f16_b) {
+            if ((st = ensure(ctx, ctx->a_f16, f16_b, s))) return st;
+            sc.a_f16 = ctx->a_f16.p;
+        }
     }
-    if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
-    if (mode == RCE_QMM_MODE_Q8 && gemv_q8_pre_supports(dw.dtype, k, t_rows)) {
-        if ((st = ensure(ctx, ctx->act_q, t_rows * (k + k / 8 + k / 4), s))) return st;  // xq, dx, s16
-        HIP_TRY(launch_gemv_q8_pre(dw, a32, t_rows, out_dev, ctx->act_q.p, s));
+    if (mfma) return run_gemm(a_dev, a_dtype == T_F16, t_rows, dw, out_dev, sc, s);
+    const float *a32 = static_cast<const float *>(a_dev);
+    if (widen) {
+        HIP_TRY(launch_f16_to_f32(static_cast<const uint16_t *>(a_dev), sc.a_f32, t_rows * k, s));
+        a32 = sc.a_f32;
+    }
+    if (preq) {
+        HIP_TRY(launch_gemv_q8_pre(dw, a32, t_rows, out_dev, sc.act_q, s));
         return RCE_QMM_OK;
     }
     HIP_TRY(launch_gemv(dw, a32, t_rows, out_dev, (int)mode, s));
     return RCE_QMM_OK;
 }
+
+namespace {
 
 rce_qmm_status host_batched(rce_qmm_context *ctx, const float *a, size_t t_rows, const rce_qmm_weight *w,
                             float *out) {
@@ -119,7 +178,7 @@ rce_qmm_status host_batched(rce_qmm_context *ctx, const float *a, size_t t_rows,
     if ((st = ensure(ctx, ctx->out, obytes, nullptr))) return st;
     HIP_TRY(hipMemcpyAsync(ctx->a_in.p, a, abytes, hipMemcpyHostToDevice, ctx->stream));
     if ((st = run_batched(ctx, ctx->a_in.p, T_F32, t_rows, w, static_cast<float *>(ctx->out.p), RCE_QMM_MODE_EXACT,
-                          ctx->stream)))
+                          ctx->stream, nullptr, 0)))
         return st;
     HIP_TRY(hipMemcpyAsync(out, ctx->out.p, obytes, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -159,6 +218,8 @@ rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out) {
     if (e != hipSuccess || n == 0) return fail(RCE_QMM_NO_DEVICE, "no HIP device");
     if (device < 0 || device >= n) return fail(RCE_QMM_NO_DEVICE, "device index out of range");
     HIP_TRY(hipSetDevice(device));
+    rce_qmm_status st = noalloc_setup(device);
+    if (st) return st;
     hipStream_t s = nullptr;
     HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     rce_qmm_context *c = new (std::nothrow) rce_qmm_context();
@@ -341,7 +402,7 @@ rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, u
     if ((!a_dev || !out_dev) && t_rows) return fail(RCE_QMM_NULL_ARGUMENT, "null device buffer");
     if ((st = set_device(ctx->device))) return st;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
-    return run_batched(ctx, a_dev, a_dtype, t_rows, w, out_dev, mode, s);
+    return run_batched(ctx, a_dev, a_dtype, t_rows, w, out_dev, mode, s, nullptr, 0);
 }
 
 rce_qmm_status rce_qmm_moe_router(const float *logits, size_t n_tokens, size_t n_expert, size_t top_k,

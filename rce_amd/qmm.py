@@ -291,6 +291,18 @@ def mm_batched_dev(ctx: Context, a_dev: int, a_dtype, t_rows: int, w: QuantWeigh
                                        ctypes.c_void_p(stream) if stream else None))
 
 
+def mm_batched_dev_noalloc(ctx: Context, a_dev: int, a_dtype, t_rows: int, w: QuantWeight, out_dev: int,
+                           mode: Mode = Mode.EXACT, stream: int | None = None) -> None:
+    """mm_batched_dev with its scratch in the library's fixed per-GPU array
+    (rce_qmm_mm_batched_dev_noalloc): no device allocation."""
+    check(lib().rce_qmm_mm_batched_dev_noalloc(ctx.handle, ctypes.c_void_p(a_dev), int(a_dtype), t_rows, w.handle,
+                                               ctypes.c_void_p(out_dev), int(mode),
+                                               ctypes.c_void_p(stream) if stream else None))
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # RCE_QMM_NOALLOC_SCRATCH_BYTES
+
+
 def moe_router(logits, top_k: int, normalize: bool = True):
     """rce_op_moe::moe_router from logits [n_tokens, n_expert]."""
     lg = np.ascontiguousarray(logits, dtype=np.float32)
