@@ -76,13 +76,18 @@ def lib() -> ctypes.CDLL:
             "orc_silu": (F, [F]),
             "orc_moe_router": (None, [P, S, S, I, P, P]),
             "orc_moe_combine": (None, [P, P, S, S, P]),
-            "orc_moe_ffn": (I, [P, S, S, S, P, P, U32, P, P, S, P, I]),
+            "orc_moe_ffn": (I, [P, S, S, S, P, P, U32, P, P, S, P, I, I]),
             "orc_max_threads": (I, []),
             "orc_moe_swiglu_ffn": (I, [P, S, S, S, P, P, P, U32, P, P, S, P, I]),
             "orc_rms_norm": (None, [P, P, S, F, P]),
             "orc_rope": (None, [P, S, F, S, P]),
             "orc_attend_head": (None, [P, P, P, S, S, S, S, F, P]),
-            "orc_llama_forward": (I, [P, F, F, I, P, P, P, P, P, P, P, U32, P, P, S, P, I]),
+            "orc_llama_forward": (I, [P, F, F, I, P, P, P, P, P, P, P, U32, P, P, S, P, I, P, P]),
+            "orc_exp_dev": (F, [F]),
+            "orc_exp_dev_max_ulp": (ctypes.c_double, [U32, U32, P, I]),
+            "orc_silu_dev": (F, [F]),
+            "orc_rms_norm_dev": (None, [P, P, S, F, I, P]),
+            "orc_attend_head_dev": (None, [P, P, P, S, S, S, S, F, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -266,7 +271,11 @@ def moe_combine(w, ys) -> np.ndarray:
     return out
 
 
-def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0) -> np.ndarray:
+def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0, q8: bool = False,
+            silu_dev: bool = False) -> np.ndarray:
+    """The grouped-expert FFN per (token, decision) in the reference's order;
+    q8: the Q8-activation products; silu_dev: silu with exp_dev (the
+    device's order)."""
     x = _c(x, np.float32)
     t_rows, d_model = x.shape
     ids = _c(ids, np.int32); gate_w = _c(gate_w, np.float32)
@@ -277,7 +286,7 @@ def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0) -> 
     out = np.zeros((t_rows, d_model), np.float32)
     rc = lib().orc_moe_ffn(_p(x), t_rows, d_model, d_ff, ctypes.cast(P1, ctypes.c_void_p),
                            ctypes.cast(P2, ctypes.c_void_p), dtype, _p(ids), _p(gate_w), top_k,
-                           _p(out), threads or max_threads())
+                           _p(out), threads or max_threads(), int(silu_dev) | (2 * int(q8)))
     if rc:
         raise ValueError(f"orc_moe_ffn rc={rc}")
     return out
@@ -300,6 +309,41 @@ def moe_swiglu_ffn(x, gate_list, up_list, down_list, dtype, d_ff, ids, gate_w, t
 
 
 # ---- Llama-2 decode step (rce-tinyllama L158-330, rce-op-attn L107-251) ----
+
+def exp_dev(x: float) -> float:
+    """The device library's exp (Cody-Waite reduction, Taylor degree 7)."""
+    return float(lib().orc_exp_dev(float(x)))
+
+
+def exp_dev_max_ulp(lo_bits: int, hi_bits: int, threads: int = 0):
+    """Largest ulp error of exp_dev against the correctly rounded exp over
+    the floats with bits in [lo_bits, hi_bits]; returns (ulps, worst input)."""
+    wb = ctypes.c_uint32(0)
+    u = lib().orc_exp_dev_max_ulp(lo_bits, hi_bits, ctypes.byref(wb), threads)
+    return float(u), float(np.array([wb.value], np.uint32).view(np.float32)[0])
+
+
+def silu_dev(x: float) -> float:
+    return float(lib().orc_silu_dev(float(x)))
+
+
+def rms_norm_dev(x, w, eps: float, nt: int) -> np.ndarray:
+    """rms_norm with the device's sum-of-squares tree (nt > 0: the fused
+    form's tasks of 8 over nt threads; nt < 0: the separate kernel's)."""
+    x = _c(x, np.float32); w = _c(w, np.float32)
+    out = np.zeros_like(x)
+    lib().orc_rms_norm_dev(_p(x), _p(w), x.size, float(eps), int(nt), _p(out))
+    return out
+
+
+def attend_head_dev(q, k_cache, v_cache, kv_head: int, seq_len: int, kv_dim: int, d_head: int, scale: float):
+    """One head's attention in the device's parallel order."""
+    q = _c(q, np.float32); k_cache = _c(k_cache, np.float32); v_cache = _c(v_cache, np.float32)
+    out = np.zeros(d_head, np.float32)
+    lib().orc_attend_head_dev(_p(q), _p(k_cache), _p(v_cache), kv_head, seq_len, kv_dim, d_head, float(scale),
+                              _p(out))
+    return out
+
 
 def rms_norm(x, w, eps: float) -> np.ndarray:
     x = _c(x, np.float32); w = _c(w, np.float32)
@@ -331,11 +375,15 @@ class Llama:
     context_length, eps.  blocks: per layer a dict with attn_norm, ffn_norm
     (f32 arrays) and wq, wk, wv, wo, ffn_gate, ffn_up, ffn_down as
     (bytes, dtype).  token_embd and lm_head: (bytes, dtype).  q8: every
-    linear uses the Q8-activation path instead of mm_1d."""
+    linear uses the Q8-activation path instead of mm_1d.  device_order:
+    None (the reference's order) or (nt_layers, nt_head), the GPU decode
+    step's own orders (rms_norm_dev with those thread layouts,
+    attend_head_dev, silu_dev)."""
 
     LIN = ("wq", "wk", "wv", "wo", "ffn_gate", "ffn_up", "ffn_down")
 
-    def __init__(self, cfg, token_embd, output_norm, lm_head, blocks, q8: bool = False, threads: int = 0):
+    def __init__(self, cfg, token_embd, output_norm, lm_head, blocks, q8: bool = False, threads: int = 0,
+                 device_order=None):
         self.cfg = dict(cfg)
         c = self.cfg
         self.dims = np.array([c["d_model"], c["vocab"], c["n_layers"], c["n_q_heads"], c["n_kv_heads"],
@@ -350,6 +398,7 @@ class Llama:
         self._types = np.array([int(b[n][1]) for b in blocks for n in self.LIN], np.uint32)
         self.q8 = q8
         self.threads = threads or max_threads()
+        self.dev_order = None if device_order is None else np.array(device_order, np.int32)
         self.reset()
 
     def reset(self):
@@ -366,20 +415,24 @@ class Llama:
         rb = row_bytes(dt, dm)
         return dequantize(b[token_id * rb:(token_id + 1) * rb], dt, dm)
 
-    def forward_embedding(self, embedding) -> np.ndarray:
+    def forward_embedding(self, embedding, trace: bool = False):
+        """Logits of one step; with trace, also the residual stream entering
+        each layer and leaving the last ([n_layers + 1, d_model])."""
         c = self.cfg
         e = _c(embedding, np.float32)
         assert e.size == c["d_model"]
         logits = np.zeros(c["vocab"], np.float32)
+        xt = np.zeros((c["n_layers"] + 1, c["d_model"]), np.float32) if trace else None
         rc = lib().orc_llama_forward(
             _p(self.dims), float(c["rope_freq_base"]), float(c["eps"]), int(self.q8), _p(e),
             _p(self.attn_norm), _p(self.ffn_norm), ctypes.cast(self._ptrs, ctypes.c_void_p), _p(self._types),
             _p(self.output_norm), _p(self.lm_head[0]), self.lm_head[1], _p(self.k_cache), _p(self.v_cache),
-            self.pos, _p(logits), self.threads)
+            self.pos, _p(logits), self.threads, _p(xt) if trace else None,
+            _p(self.dev_order) if self.dev_order is not None else None)
         if rc:
             raise ValueError(f"orc_llama_forward rc={rc}")
         self.pos += 1
-        return logits
+        return (logits, xt) if trace else logits
 
-    def forward_token(self, token_id: int) -> np.ndarray:
-        return self.forward_embedding(self.embed(token_id))
+    def forward_token(self, token_id: int, trace: bool = False):
+        return self.forward_embedding(self.embed(token_id), trace)

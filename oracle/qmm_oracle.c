@@ -1246,19 +1246,28 @@ EXPORT void orc_moe_combine(const float *w, const float *ys, size_t top_k, size_
  * decision j (rce-qwen36-moe L667-710 with the config's two matrices):
  * h = silu(mm_1d(x_t, w1[e])); y_j = mm_1d(h, w2[e]); out_t = moe_combine.
  * w1_bytes/w2_bytes: arrays of n_expert pointers to GGUF bytes. */
+EXPORT float orc_silu_dev(float x);
+
+/* how: 0 = the reference (mm_1d products, silu with the platform exp);
+ * bit 0: silu with orc_exp_dev (the device's order, test instrumentation);
+ * bit 1: the Q8-activation products (orc_mm_batched_q8) instead of mm_1d. */
 EXPORT int orc_moe_ffn(const float *x, size_t t_rows, size_t d_model, size_t d_ff,
                        const uint8_t *const *w1_bytes, const uint8_t *const *w2_bytes, uint32_t t,
                        const int32_t *ids, const float *gate_w, size_t top_k, float *out,
-                       int threads) {
+                       int threads, int how) {
     float *h = (float *)malloc(d_ff * sizeof(float));
     float *ys = (float *)malloc(top_k * d_model * sizeof(float));
     int rc = 0;
+    const int q8 = (how & 2) != 0;
     for (size_t tr = 0; tr < t_rows && rc == 0; tr++) {
         for (size_t j = 0; j < top_k && rc == 0; j++) {
             int e = ids[tr * top_k + j];
-            rc = orc_mm_1d(x + tr * d_model, w1_bytes[e], t, d_ff, d_model, h, threads);
-            for (size_t i = 0; i < d_ff; i++) h[i] = orc_silu(h[i]);
-            if (!rc) rc = orc_mm_1d(h, w2_bytes[e], t, d_model, d_ff, ys + j * d_model, threads);
+            rc = q8 ? orc_mm_batched_q8(x + tr * d_model, 1, w1_bytes[e], t, d_ff, d_model, h, threads)
+                    : orc_mm_1d(x + tr * d_model, w1_bytes[e], t, d_ff, d_model, h, threads);
+            for (size_t i = 0; i < d_ff; i++) h[i] = (how & 1) ? orc_silu_dev(h[i]) : orc_silu(h[i]);
+            if (!rc)
+                rc = q8 ? orc_mm_batched_q8(h, 1, w2_bytes[e], t, d_model, d_ff, ys + j * d_model, threads)
+                        : orc_mm_1d(h, w2_bytes[e], t, d_model, d_ff, ys + j * d_model, threads);
         }
         orc_moe_combine(gate_w + tr * top_k, ys, top_k, d_model, out + tr * d_model);
     }
@@ -1339,6 +1348,217 @@ EXPORT void orc_attend_head(const float *q, const float *k_cache, const float *v
     }
 }
 
+/* ---- the GPU decode step's own orders (test instrumentation) -------------
+ * Where the device's decode step documents an order of its own instead of
+ * the reference's -- the sum of squares of rms_norm as a fixed tree, the
+ * attention softmax as fixed-shape parallel reductions, exp as the
+ * library's exp -- these functions restate that order, so the device can be
+ * checked bit for bit against it (orc_llama_forward with dev_order).  The
+ * reference-order functions above stay the parity definition against the
+ * reference; these are judged by their own checks (tests/test_oracle_decoder.py:
+ * orc_exp_dev's error bound over every float of its range, the trees and
+ * the parallel attention against the reference order within rounding). */
+
+/* exp as the device library computes it: x = n ln2 + r with n =
+ * rint(x log2e) and r = (x - n ln2_hi) - n ln2_lo (Cody & Waite's split of
+ * ln 2, W. J. Cody and W. Waite, Software Manual for the Elementary
+ * Functions, 1980), exp(r) by its Taylor series to degree 7 in Horner form
+ * with fused multiply-adds, then the two exact scalings by 2^(n/2) and
+ * 2^(n - n/2).  0 below -104 (and for -inf), +inf above 88.75, NaN kept. */
+EXPORT float orc_exp_dev(float x) {
+    if (!(x > -104.0f)) return x != x ? x : 0.0f;
+    if (x > 88.75f) return INFINITY;
+    const float n = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62e4p-1f, x);
+    r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0x1p-1f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n, e1 = ni / 2, e2 = ni - e1;
+    union { uint32_t u; float f; } s1, s2;
+    s1.u = (uint32_t)(e1 + 127) << 23;
+    s2.u = (uint32_t)(e2 + 127) << 23;
+    return (p * s1.f) * s2.f;
+}
+
+/* Largest error of orc_exp_dev in units in the last place of the correctly
+ * rounded exp (exp in double, rounded to float) over every float whose bits
+ * lie in [lo_bits, hi_bits] (as unsigned; one sign), and the input where it
+ * occurs.  Results that are 0 or infinite on either side count as exact
+ * when both agree. */
+EXPORT double orc_exp_dev_max_ulp(uint32_t lo_bits, uint32_t hi_bits, uint32_t *worst_bits, int threads) {
+    double worst = 0.0;
+    uint32_t wb = lo_bits;
+#ifdef _OPENMP
+#pragma omp parallel num_threads(threads > 0 ? threads : omp_get_max_threads())
+#endif
+    {
+        double lw = 0.0;
+        uint32_t lb = lo_bits;
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t b = (int64_t)lo_bits; b <= (int64_t)hi_bits; b++) {
+            union { uint32_t u; float f; } v;
+            v.u = (uint32_t)b;
+            const float got = orc_exp_dev(v.f);
+            const float want = (float)exp((double)v.f);
+            if (got == want) continue;
+            double ulp;
+            if (want == 0.0f || isinf(want) || isinf(got)) {
+                ulp = 1e30;  /* one side 0 or infinite, the other not */
+                if (want == 0.0f && !isinf(got)) ulp = (double)got / 0x1p-149;  /* subnormal steps */
+            } else {
+                int e;
+                frexpf(want, &e);
+                double u = ldexp(1.0, (e - 24 < -149 ? -149 : e - 24));
+                ulp = fabs((double)got - (double)want) / u;
+            }
+            if (ulp > lw) { lw = ulp; lb = v.u; }
+        }
+#ifdef _OPENMP
+#pragma omp critical
+#endif
+        {
+            if (lw > worst) { worst = lw; wb = lb; }
+        }
+    }
+    if (worst_bits) *worst_bits = wb;
+    return worst;
+}
+
+/* silu (rce-tinyllama L164-166) with orc_exp_dev in place of exp. */
+EXPORT float orc_silu_dev(float x) {
+    if (x >= 0.0f) { float e = orc_exp_dev(-x); return x / (1.0f + e); }
+    float e = orc_exp_dev(x);
+    float t = x * e;
+    return t / (1.0f + e);
+}
+
+/* The wave-wide butterfly sum of the device (lane i adds lane i ^ off for
+ * off = 32, 16, ..., 1; every lane ends with the same value). */
+static float dev_wave_sum(float v[64]) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        float t[64];
+        for (int i = 0; i < 64; i++) t[i] = v[i] + v[i ^ off];
+        memcpy(v, t, sizeof t);
+    }
+    return v[0];
+}
+
+/* rms_norm with the device's sum of squares.  nt > 0: the form fused into
+ * the GEMV kernels -- thread t of nt holds tasks t and t + nt of 8
+ * consecutive values (a sequential sum of squares each; a task past the end
+ * adds 0), then the butterfly per wave of 64 threads, then the waves' sums
+ * in wave order from 0.  nt < 0: the separate kernel of -nt threads --
+ * thread t sums the squares of x[t], x[t - nt], ... in order, then the
+ * same butterfly and wave order.  The rest is the reference's: mean_sq =
+ * sum / n, inv = 1 / sqrt(mean_sq + eps), out = (x * inv) * w. */
+EXPORT void orc_rms_norm_dev(const float *x, const float *w, size_t n, float eps, int nt, float *out) {
+    const int threads = nt > 0 ? nt : -nt;
+    float *ss = (float *)calloc((size_t)threads, sizeof(float));
+    for (int t = 0; t < threads; t++) {
+        float s = 0.0f;
+        if (nt > 0) {
+            for (int h = 0; h < 2; h++) {
+                const size_t task = (size_t)t + (size_t)h * (size_t)threads;
+                float q = 0.0f;
+                if (task < n / 8)
+                    for (int i = 0; i < 8; i++) { float sq = x[8 * task + i] * x[8 * task + i]; q = q + sq; }
+                s = h == 0 ? q : s + q;
+            }
+        } else {
+            for (size_t i = (size_t)t; i < n; i += (size_t)threads) { float sq = x[i] * x[i]; s = s + sq; }
+        }
+        ss[t] = s;
+    }
+    float tot = 0.0f;
+    for (int wv = 0; wv < threads / 64; wv++) tot = tot + dev_wave_sum(ss + 64 * wv);
+    free(ss);
+    float mean_sq = tot / (float)n;
+    float inv = 1.0f / sqrtf(mean_sq + eps);
+    for (size_t i = 0; i < n; i++) { float t = x[i] * inv; out[i] = t * w[i]; }
+}
+
+/* One query head's attention as the device evaluates it (seq_len keys of
+ * the caches, this position's row included): four waves take the keys
+ * [w seq / 4, (w + 1) seq / 4) in runs of 4096 / d_head; in a run, key j's
+ * score is the sequential dot q . k_j times scale, m_new = max(m, the
+ * run's scores), p_j = exp(s_j - m_new), l = l exp(m - m_new) + (butterfly
+ * sum of the p_j over 64 lanes), and per dimension four partial sums a_k
+ * over the run's keys j = k mod 4 in order, o = o exp(m - m_new) + ((a_0 +
+ * a_1) + (a_2 + a_3)); then the waves with keys merge in wave order with
+ * weights exp(m_w - M), M the largest m_w, and out = acc * (1 / l). */
+EXPORT void orc_attend_head_dev(const float *q, const float *k_cache, const float *v_cache, size_t kv_head,
+                                size_t seq_len, size_t kv_dim, size_t d_head, float scale, float *out) {
+    enum { NW = 4 };
+    const size_t off = kv_head * d_head, ch = 4096 / d_head;
+    float wm[NW], wl[NW];
+    float *wo = (float *)calloc(NW * d_head, sizeof(float));
+    float *a = (float *)calloc(4 * d_head, sizeof(float));
+    for (int wv = 0; wv < NW; wv++) {
+        const size_t j0 = (size_t)wv * seq_len / NW, j1 = (size_t)(wv + 1) * seq_len / NW;
+        float m = -INFINITY, l = 0.0f;
+        float *o = wo + wv * d_head;
+        for (size_t c0 = j0; c0 < j1; c0 += ch) {
+            const size_t n = j1 - c0 < ch ? j1 - c0 : ch;
+            float sc[64], p[64];
+            float mx = -INFINITY;
+            for (size_t j = 0; j < 64; j++) {
+                sc[j] = -INFINITY;
+                if (j < n) {
+                    const float *k = k_cache + (c0 + j) * kv_dim + off;
+                    float dot = 0.0f;
+                    for (size_t i = 0; i < d_head; i++) { float t = q[i] * k[i]; dot = dot + t; }
+                    sc[j] = dot * scale;
+                }
+                mx = fmaxf(mx, sc[j]);
+            }
+            const float m_new = fmaxf(m, mx);
+            const float corr = orc_exp_dev(m - m_new);
+            for (size_t j = 0; j < 64; j++) p[j] = j < n ? orc_exp_dev(sc[j] - m_new) : 0.0f;
+            const float lc = l * corr;
+            float pp[64];
+            memcpy(pp, p, sizeof pp);
+            l = lc + dev_wave_sum(pp);
+            memset(a, 0, 4 * d_head * sizeof(float));
+            for (size_t j = 0; j < n; j++) {
+                const float *v = v_cache + (c0 + j) * kv_dim + off;
+                float *ak = a + (j % 4) * d_head;
+                for (size_t d = 0; d < d_head; d++) { float t = p[j] * v[d]; ak[d] = ak[d] + t; }
+            }
+            for (size_t d = 0; d < d_head; d++) {
+                const float s01 = a[d] + a[d_head + d], s23 = a[2 * d_head + d] + a[3 * d_head + d];
+                const float sv = s01 + s23, oc = o[d] * corr;
+                o[d] = oc + sv;
+            }
+            m = m_new;
+        }
+        wm[wv] = m;
+        wl[wv] = l;
+    }
+    float M = -INFINITY;
+    for (int wv = 0; wv < NW; wv++) M = fmaxf(M, wm[wv]);
+    float lacc = 0.0f;
+    for (size_t d = 0; d < d_head; d++) out[d] = 0.0f;
+    for (int wv = 0; wv < NW; wv++) {
+        if (wm[wv] == -INFINITY) continue;
+        const float wt = orc_exp_dev(wm[wv] - M);
+        for (size_t d = 0; d < d_head; d++) { float t = wt * wo[wv * d_head + d]; out[d] = out[d] + t; }
+        const float lw = wt * wl[wv];
+        lacc = lacc + lw;
+    }
+    const float inv = 1.0f / lacc;
+    for (size_t d = 0; d < d_head; d++) out[d] = out[d] * inv;
+    free(wo);
+    free(a);
+}
+
 /* One linear of the decoder: mm_1d (q8 = 0) or the Q8-activation path. */
 static int dec_linear(const float *a, const uint8_t *w, uint32_t t, size_t n, size_t k, float *out, int q8,
                       int threads) {
@@ -1352,13 +1572,19 @@ static int dec_linear(const float *a, const uint8_t *w, uint32_t t, size_t n, si
  * in the order wq, wk, wv, wo, ffn_gate, ffn_up, ffn_down, with their
  * dtypes in lin_dtype.  attn_norm / ffn_norm: [n_layers][d_model].
  * k_cache / v_cache: [n_layers][context_length][n_kv_heads * d_head]; the
- * step appends position pos.  logits: [vocab].  Returns 0, or the
- * failing linear's code, or -10 when pos >= context_length. */
+ * step appends position pos.  logits: [vocab].  dev_order (may be NULL:
+ * the reference's order): {nt_layers, nt_head}, the device's orders --
+ * orc_rms_norm_dev with nt_layers for the layers' norms and nt_head for
+ * the output norm, orc_attend_head_dev, orc_silu_dev.  x_trace (may be NULL):
+ * [n_layers + 1][d_model], the residual stream entering each layer and,
+ * last, leaving the final one (test instrumentation: it changes nothing
+ * else).  Returns 0, or the failing linear's code, or -10 when pos >=
+ * context_length. */
 EXPORT int orc_llama_forward(const size_t *dims, float rope_base, float eps, int q8, const float *embedding,
                              const float *attn_norm, const float *ffn_norm, const uint8_t *const *lin,
                              const uint32_t *lin_dtype, const float *output_norm, const uint8_t *lm_head,
                              uint32_t lm_dtype, float *k_cache, float *v_cache, size_t pos, float *logits,
-                             int threads) {
+                             int threads, float *x_trace, const int *dev_order) {
     size_t dm = dims[0], vocab = dims[1], nl = dims[2], nq = dims[3], nkv = dims[4], dh = dims[5];
     size_t rope_dim = dims[6], dff = dims[7], ctx = dims[8];
     if (pos >= ctx) return -10;
@@ -1374,7 +1600,9 @@ EXPORT int orc_llama_forward(const size_t *dims, float rope_base, float eps, int
         const uint8_t *const *W = lin + il * 7;
         const uint32_t *T = lin_dtype + il * 7;
         float *kc = k_cache + il * ctx * kvd, *vc = v_cache + il * ctx * kvd;
-        orc_rms_norm(x, attn_norm + il * dm, dm, eps, xn);
+        if (x_trace) memcpy(x_trace + il * dm, x, dm * 4);
+        if (dev_order) orc_rms_norm_dev(x, attn_norm + il * dm, dm, eps, dev_order[0], xn);
+        else orc_rms_norm(x, attn_norm + il * dm, dm, eps, xn);
         rc = dec_linear(xn, W[0], T[0], qd, dm, q, q8, threads);
         if (!rc) rc = dec_linear(xn, W[1], T[1], kvd, dm, kk, q8, threads);
         if (!rc) rc = dec_linear(xn, W[2], T[2], kvd, dm, vv, q8, threads);
@@ -1383,22 +1611,27 @@ EXPORT int orc_llama_forward(const size_t *dims, float rope_base, float eps, int
         for (size_t hh = 0; hh < nkv; hh++) orc_rope(kk + hh * dh, rope_dim, rope_base, pos, 0);
         memcpy(kc + pos * kvd, kk, kvd * 4);
         memcpy(vc + pos * kvd, vv, kvd * 4);
-        for (size_t hh = 0; hh < nq; hh++)
-            orc_attend_head(q + hh * dh, kc, vc, hh / qpk, pos + 1, kvd, dh, scale, att + hh * dh);
+        for (size_t hh = 0; hh < nq; hh++) {
+            if (dev_order) orc_attend_head_dev(q + hh * dh, kc, vc, hh / qpk, pos + 1, kvd, dh, scale, att + hh * dh);
+            else orc_attend_head(q + hh * dh, kc, vc, hh / qpk, pos + 1, kvd, dh, scale, att + hh * dh);
+        }
         rc = dec_linear(att, W[3], T[3], dm, qd, o, q8, threads);
         if (rc) break;
         for (size_t i = 0; i < dm; i++) x[i] += o[i];
-        orc_rms_norm(x, ffn_norm + il * dm, dm, eps, xn);
+        if (dev_order) orc_rms_norm_dev(x, ffn_norm + il * dm, dm, eps, dev_order[0], xn);
+        else orc_rms_norm(x, ffn_norm + il * dm, dm, eps, xn);
         rc = dec_linear(xn, W[4], T[4], dff, dm, g, q8, threads);
         if (!rc) rc = dec_linear(xn, W[5], T[5], dff, dm, u, q8, threads);
         if (rc) break;
-        for (size_t i = 0; i < dff; i++) h[i] = orc_silu(g[i]) * u[i];
+        for (size_t i = 0; i < dff; i++) h[i] = (dev_order ? orc_silu_dev(g[i]) : orc_silu(g[i])) * u[i];
         rc = dec_linear(h, W[6], T[6], dm, dff, o, q8, threads);
         if (rc) break;
         for (size_t i = 0; i < dm; i++) x[i] += o[i];
     }
     if (!rc) {
-        orc_rms_norm(x, output_norm, dm, eps, xn);
+        if (x_trace) memcpy(x_trace + nl * dm, x, dm * 4);
+        if (dev_order) orc_rms_norm_dev(x, output_norm, dm, eps, dev_order[1], xn);
+        else orc_rms_norm(x, output_norm, dm, eps, xn);
         rc = dec_linear(xn, lm_head, lm_dtype, vocab, dm, logits, q8, threads);
     }
     free(x); free(xn); free(q); free(kk); free(vv); free(att); free(o); free(g); free(u); free(h);

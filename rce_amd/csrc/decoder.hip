@@ -16,8 +16,8 @@
 //   * attention: the reference's softmax-weighted sum of the values,
 //     evaluated with fixed-shape parallel reductions instead of its
 //     key-by-key recurrence (f32 reassociation; one key gives v exactly);
-//     exp is the device's expf (last-bit differences from the host libm).
-//   * silu: silu_ref (device expf).
+//     exp is the library's rce_exp (last-bit differences from the host libm).
+//   * silu: silu_ref (rce_exp).
 // This file is built with -ffp-contract=off: no multiply-add contraction.
 #include "qmm_internal.h"
 
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
                 sc = dot * scale;
             }
             const float m_new = fmaxf(m, wave_max(sc));  // finite: the run has a key
-            const float corr = expf(m - m_new);           // 0 for the wave's first run
-            const float p = lane < n ? expf(sc - m_new) : 0.0f;
+            const float corr = rce_exp(m - m_new);           // 0 for the wave's first run
+            const float p = lane < n ? rce_exp(sc - m_new) : 0.0f;
             const float lc = l * corr;
             l = lc + wave_sum(p);
             float a[4][DPL];
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
     for (int w = 0; w < ATT_NW; w++) {
         if (mo[w][DH] == -INFINITY) continue;  // a wave without keys
-        const float wt = expf(mo[w][DH] - M);
+        const float wt = rce_exp(mo[w][DH] - M);
 #pragma unroll
         for (int d = 0; d < DPL; d++) {
             const float t = wt * mo[w][lane + 64 * d];

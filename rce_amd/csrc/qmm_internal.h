@@ -93,15 +93,43 @@ struct GemvGeom {
     int nt = 0, rpl = 0, tb = 0;
 };
 
+// The library's exp: x = n ln2 + r with n = rint(x log2e) and r = (x -
+// n ln2_hi) - n ln2_lo (Cody & Waite's two-part ln 2, W. J. Cody and W.
+// Waite, Software Manual for the Elementary Functions, 1980), exp(r) by its
+// Taylor series to degree 7 in Horner form with fused multiply-adds, then
+// two exact scalings by 2^(n/2) and 2^(n - n/2).  Within 1 ulp of the
+// correctly rounded exp over every float in [-104, 88.75]; 0 below (and
+// for -inf), +inf above, NaN kept.  A fixed sequence of IEEE operations,
+// so a host restatement gives the same bits (the reference's f32::exp is
+// the platform libm, which differs from any device exp in the last bit).
+__device__ __forceinline__ float rce_exp(float x) {
+    if (!(x > -104.0f)) return x != x ? x : 0.0f;
+    if (x > 88.75f) return __builtin_inff();
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0x1p-1f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = (int)n, e1 = ni / 2, e2 = ni - e1;
+    const float s1 = __uint_as_float((uint32_t)(e1 + 127) << 23), s2 = __uint_as_float((uint32_t)(e2 + 127) << 23);
+    return (p * s1) * s2;
+}
+
 // The reference's silu (rce-tinyllama/src/lib.rs L164-166, rce-qwen36-moe
-// L459-461): x * sigmoid(x) with exp's argument kept non-positive.  The
-// device expf may differ from the host libm's in the last bit.
+// L459-461): x * sigmoid(x) with exp's argument kept non-positive, exp
+// being rce_exp.
 __device__ __forceinline__ float silu_ref(float x) {
     if (x >= 0.0f) {
-        const float e = expf(-x);
+        const float e = rce_exp(-x);
         return x / (1.0f + e);
     }
-    const float e = expf(x);
+    const float e = rce_exp(x);
     const float t = x * e;
     return t / (1.0f + e);
 }

@@ -78,6 +78,51 @@ def device_model(ctx, W: dict, mode):
     return rce_amd.TinyLlamaRuntime(ctx, cfg, weights, mode)
 
 
+# Formats whose decode GEMV has the fused forms (rms_norm inside the GEMV);
+# Q6_K only in Q8 mode (its EXACT kernel is a row chain).
+_FX = {O.Q4_0: 32, O.Q8_0: 32, O.Q5_0: 32, O.Q4_1: 32, O.Q3_K: 32, O.Q4_K: 64, O.Q5_K: 64, O.Q6_K: 256}
+
+
+def _fused_nt(dt, n_cols, q8):
+    """Threads of the fused GEMV whose blocks form rms_norm (None: no fused
+    norm for this weight): 256 / 512 / 1024 by the row's column units."""
+    if dt not in _FX or (dt == O.Q6_K and not q8):
+        return None
+    u = n_cols // _FX[dt]
+    nt = 256 if u <= 256 else (512 if u <= 512 else 1024)
+    return nt if n_cols // 8 <= 2 * nt else None
+
+
+def device_order(W: dict, q8: bool, separate_norms: bool = False):
+    """(nt_layers, nt_head) of oracle.Llama's device-order mode for the
+    device decoder of W: the fused forms' thread count where the decoder
+    forms rms_norm inside the q|k|v, gate/up and head GEMVs, -256 where it
+    runs the separate norm kernel.  None where the layers' norms do not all
+    take one form (mixed linear formats)."""
+    dm = W["cfg"]["d_model"]
+    forms = set()
+    for b in W["blocks"]:
+        qkv = {b[n][1] for n in ("wq", "wk", "wv")}
+        gu = {b[n][1] for n in ("ffn_gate", "ffn_up")}
+        for grp in (qkv, gu):
+            nt = _fused_nt(next(iter(grp)), dm, q8) if len(grp) == 1 else None
+            forms.add(-256 if separate_norms or nt is None else nt)
+    if len(forms) != 1:
+        return None
+    nt_head = _fused_nt(W["lm_head"][1], dm, q8)
+    return forms.pop(), (-256 if separate_norms or nt_head is None else nt_head)
+
+
+def oracle_model_dev(W: dict, q8: bool = False, separate_norms: bool = False):
+    """The oracle's decoder in the device's own orders (bit-identical
+    target), or None where device_order has no single form."""
+    order = device_order(W, q8, separate_norms)
+    if order is None:
+        return None
+    return O.Llama(W["cfg"], W["token_embd"], W["output_norm"], W["lm_head"], W["blocks"], q8=q8,
+                   device_order=order)
+
+
 def normwise(got, want) -> float:
     want = np.asarray(want, np.float64)
     return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / np.max(np.abs(want)))

@@ -1,0 +1,222 @@
+"""GPU parity at the full workloads of configs[3] and configs[4].
+
+the TinyLlama-shaped decoder (22 layers, d 2048, ffn 5632, 32 q /
+4 kv heads, d_head 64, Q4_K linears and token_embd, Q6_K 32000 x 2048 head,
+norms = 1, every weight N(0, 0.02) quantized by the reference's encoders),
+batch-1 decode over 72 positions, so attention runs past one 64-key run.
+  * Both modes against the oracle's decoder in the device's own orders
+    (oracle.Llama with device_order: rms_norm's tree, the parallel
+    attention, the library's exp; the linears in the reference's order, or
+    the Q8 path): bit for bit at every position of all 22 layers.  A defect
+    anywhere in the step changes bits.
+  * EXACT against the reference's order (rce-tinyllama/src/lib.rs L252-330,
+    rce-op-attn L107-251) at every position: 1e-5 normwise (the norm's
+    tree and the exp differ from the reference in the last bits).
+  * Q8 against the reference's order is not a fixed tolerance: a last-bit
+    difference moves one activation across a Q8 rounding boundary now and
+    then, and from there the runs' roundings decorrelate.  The oracle's own
+    Q8 decoder with every norm weight moved by one ulp drifts as far (about
+    1e-2 .. 5e-2 normwise at 22 layers); the test reports both and bounds
+    the device's by the Q8 noise level, TOL_Q8_FULL.
+
+8 Q4_0 experts (w1 14336 x 4096, w2 4096 x 14336), 256 tokens
+N(0, 1), top-2 of N(0, 1) router logits (rce-qwen36-moe/src/lib.rs L667-710,
+rce-op-moe L35-110).  The device runs all 256 tokens in each mode; a fixed
+sample of 16 tokens that covers every expert is compared with the oracle:
+EXACT and Q8 bit for bit with the oracle's restatement in the device's order
+(silu with the library's exp; Q8: the Q8-activation products), EXACT also
+within 1e-5 of the reference (libm exp), F16_MFMA within 3e-3 of the
+reference order.  Every mode must be run-to-run bit-identical over the
+whole output.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rce_amd
+from rce_amd import Mode
+from llama_case import LIN, make_weights, normwise, shapes
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+TL_CFG = dict(d_model=2048, vocab=32000, n_layers=22, n_q_heads=32, n_kv_heads=4, d_head=64, rope_dim=64,
+              rope_freq_base=10000.0, d_ff=5632, context_length=80, eps=1e-5)
+N_POS = 72
+TOL_EXACT = 1e-5
+TOL_Q8_FULL = 1e-1   # 22 layers against the reference order: the Q8 activation-rounding noise, not ulps
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def tl(ctx):
+    """The configs[4] weights on the host and, once, on the device."""
+    note("configs[4] weights: 22 layers, Q4_K linears, Q6_K head (quantizing)")
+    W = make_weights(TL_CFG, seed=500, sigma=0.02, unit_norms=True)
+    sh = shapes(TL_CFG)
+    qw = lambda bd, n, k: rce_amd.QuantWeight.from_owned_bytes(ctx, bd[0], bd[1], n, k)  # noqa: E731
+    dev = {"token_embd": qw(W["token_embd"], TL_CFG["vocab"], TL_CFG["d_model"]),
+           "lm_head": qw(W["lm_head"], TL_CFG["vocab"], TL_CFG["d_model"]),
+           "blocks": [{n: qw(b[n], *sh[n]) for n in LIN} for b in W["blocks"]]}
+    toks = [int(t) for t in np.random.default_rng(501).integers(0, TL_CFG["vocab"], N_POS)]
+    yield W, dev, toks
+    for b in dev["blocks"]:
+        for w in b.values():
+            w.close()
+    dev["token_embd"].close()
+    dev["lm_head"].close()
+
+
+def device_decoder(ctx, W, dev, mode, layers):
+    """A device decoder over the uploaded weights of `layers` (indices)."""
+    c = dict(TL_CFG, n_layers=len(layers))
+    blocks = [rce_amd.TinyLlamaBlock(W["blocks"][i]["attn_norm"], W["blocks"][i]["ffn_norm"], **dev["blocks"][i])
+              for i in layers]
+    weights = rce_amd.TinyLlamaWeights(dev["token_embd"], W["output_norm"], dev["lm_head"], blocks)
+    return rce_amd.TinyLlamaRuntime(ctx, rce_amd.TinyLlamaConfig(**c), weights, mode)
+
+
+def oracle_decoder(W, q8, layers, bump_norms=False, device_order=None):
+    c = dict(TL_CFG, n_layers=len(layers))
+    blocks = [W["blocks"][i] for i in layers]
+    if bump_norms:  # every norm weight one ulp up: a last-bit perturbation of every layer
+        up = lambda v: np.nextafter(v, np.float32(np.inf))  # noqa: E731
+        blocks = [dict(b, attn_norm=up(b["attn_norm"]), ffn_norm=up(b["ffn_norm"])) for b in blocks]
+    return O.Llama(c, W["token_embd"], W["output_norm"], W["lm_head"], blocks, q8=q8, device_order=device_order)
+
+
+def bits(x):
+    return np.ascontiguousarray(x, F32).view(np.uint32)
+
+
+def test_tinyllama_22_layers_exact(ctx, tl):
+    W, dev, toks = tl
+    note(f"configs[4] EXACT, 22 layers, {N_POS} positions")
+    d = device_decoder(ctx, W, dev, Mode.EXACT, range(22))
+    ref = oracle_decoder(W, False, range(22))
+    same = oracle_decoder(W, False, range(22), device_order=(256, -256))  # fused layer norms, separate head norm
+    errs = []
+    for pos, t in enumerate(toks):
+        got = d.forward_logits(t)
+        errs.append(normwise(got, ref.forward_token(t)))
+        assert errs[-1] < TOL_EXACT, f"position {pos}: normwise {errs[-1]:.3e}"
+        assert np.array_equal(bits(got), bits(same.forward_token(t))), f"position {pos}: not the device-order bits"
+    note(f"  bit-identical to the device-order oracle; vs the reference order normwise max {max(errs):.3e}")
+    d.close()
+
+
+def test_tinyllama_22_layers_q8(ctx, tl):
+    W, dev, toks = tl
+    note(f"configs[4] Q8, 22 layers, {N_POS} positions")
+    d = device_decoder(ctx, W, dev, Mode.Q8, range(22))
+    same = oracle_decoder(W, True, range(22), device_order=(256, 256))  # every norm fused
+    ref = oracle_decoder(W, True, range(22))
+    bumped = oracle_decoder(W, True, range(22), bump_norms=True)
+    dev_err, self_err = [], []
+    for pos, t in enumerate(toks):
+        got = d.forward_logits(t)
+        assert np.array_equal(bits(got), bits(same.forward_token(t))), f"position {pos}: not the device-order bits"
+        want = ref.forward_token(t)
+        dev_err.append(normwise(got, want))
+        self_err.append(normwise(bumped.forward_token(t), want))
+    d.close()
+    note(f"  bit-identical to the device-order oracle at all {N_POS} positions; vs the reference order: "
+         f"max {max(dev_err):.3e} median {np.median(dev_err):.3e}; the oracle against itself with norms +1 ulp: "
+         f"max {max(self_err):.3e} median {np.median(self_err):.3e}")
+    assert max(dev_err) < TOL_Q8_FULL
+
+
+# ---- grouped experts ---------------------------------------------
+
+MOE_E, MOE_DM, MOE_DFF, MOE_T, MOE_K = 8, 4096, 14336, 256, 2
+
+
+@pytest.fixture(scope="module")
+def moe(ctx):
+    note("configs[3] experts: 8 x (14336x4096, 4096x14336) Q4_0 (quantizing)")
+    rng = np.random.default_rng(400)
+    q = lambda n, k: rce_amd.quantize(rng.standard_normal((n, k), dtype=F32) * F32(0.02), O.Q4_0)  # noqa: E731
+    w1b = [q(MOE_DFF, MOE_DM) for _ in range(MOE_E)]
+    w2b = [q(MOE_DM, MOE_DFF) for _ in range(MOE_E)]
+    x = rng.standard_normal((MOE_T, MOE_DM), dtype=F32)
+    ids, gw = rce_amd.moe_router(rng.standard_normal((MOE_T, MOE_E), dtype=F32), MOE_K)
+    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, MOE_DFF, MOE_DM) for b in w1b]
+    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, MOE_DM, MOE_DFF) for b in w2b]
+    # 16 sample tokens: the first token of each expert (in token order), then
+    # the lowest-numbered remaining tokens
+    sample = []
+    for e in range(MOE_E):
+        t = int(np.nonzero((ids == e).any(axis=1))[0][0])
+        if t not in sample:
+            sample.append(t)
+    for t in range(MOE_T):
+        if len(sample) >= 16:
+            break
+        if t not in sample:
+            sample.append(t)
+    sample = sorted(sample)
+    assert set(int(e) for e in ids[sample].reshape(-1)) == set(range(MOE_E))
+    yield w1b, w2b, x, ids, gw, W1, W2, sample
+    for w in W1 + W2:
+        w.close()
+
+
+def run_full_moe(ctx, W1, W2, x, ids, gw, mode):
+    bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids.astype(np.int32))
+    bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw.astype(F32))
+    bo = rce_amd.DeviceBuffer(ctx, MOE_T * MOE_DM * 4)
+    outs = []
+    for _ in range(2):
+        rce_amd.moe_ffn_dev(ctx, W1, W2, bx.ptr, MOE_T, bi.ptr, bw.ptr, MOE_K, bo.ptr, mode)
+        ctx.synchronize()
+        outs.append(bo.download(F32, MOE_T * MOE_DM).reshape(MOE_T, MOE_DM))
+    for b in (bx, bi, bw, bo):
+        b.free()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "not run-to-run deterministic"
+    assert np.all(np.isfinite(outs[0]))
+    return outs[0]
+
+
+@pytest.fixture(scope="module")
+def moe_ref(moe):
+    w1b, w2b, x, ids, gw, _, _, sample = moe
+    note(f"  oracle moe_ffn on tokens {sample}")
+    return O.moe_ffn(x[sample], w1b, w2b, O.Q4_0, MOE_DFF, ids[sample], gw[sample])
+
+
+def test_moe_full_f16_mfma(ctx, moe, moe_ref):
+    _, _, x, ids, gw, W1, W2, sample = moe
+    note("configs[3] F16_MFMA, 8 experts x 256 tokens top-2")
+    got = run_full_moe(ctx, W1, W2, x, ids, gw, Mode.F16_MFMA)
+    err = normwise(got[sample], moe_ref)
+    note(f"  normwise {err:.3e} over the sample")
+    assert err < 3e-3
+
+
+def test_moe_full_exact(ctx, moe, moe_ref):
+    w1b, w2b, x, ids, gw, W1, W2, sample = moe
+    note("configs[3] EXACT, 8 experts x 256 tokens top-2")
+    got = run_full_moe(ctx, W1, W2, x, ids, gw, Mode.EXACT)
+    err = normwise(got[sample], moe_ref)
+    note(f"  normwise {err:.3e} over the sample")
+    assert err < 1e-5
+    same = O.moe_ffn(x[sample], w1b, w2b, O.Q4_0, MOE_DFF, ids[sample], gw[sample], silu_dev=True)
+    assert np.array_equal(got[sample].view(np.uint32), same.view(np.uint32))
+
+
+def test_moe_full_q8(ctx, moe):
+    w1b, w2b, x, ids, gw, W1, W2, sample = moe
+    note("configs[3] Q8, 8 experts x 256 tokens top-2")
+    got = run_full_moe(ctx, W1, W2, x, ids, gw, Mode.Q8)
+    same = O.moe_ffn(x[sample], w1b, w2b, O.Q4_0, MOE_DFF, ids[sample], gw[sample], q8=True, silu_dev=True)
+    assert np.array_equal(got[sample].view(np.uint32), same.view(np.uint32))
+    ref = O.moe_ffn(x[sample], w1b, w2b, O.Q4_0, MOE_DFF, ids[sample], gw[sample])
+    note(f"  bit-identical to the oracle's Q8 path over the sample; vs the reference order normwise "
+         f"{normwise(got[sample], ref):.3e}")

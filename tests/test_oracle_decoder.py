@@ -197,3 +197,96 @@ def test_llama_cache_full():
     m.forward_token(2)
     with pytest.raises(ValueError):
         m.forward_token(3)
+
+
+# ---- the device's own orders (orc_exp_dev, orc_silu_dev, orc_rms_norm_dev,
+# orc_attend_head_dev): what the GPU decode step is compared with bit for bit
+
+def _bits(x: float) -> int:
+    return int(np.array([x], F32).view(np.uint32)[0])
+
+
+def test_exp_dev_within_one_ulp_everywhere():
+    """Every float in [-104, 88.75]: within 1 ulp of the correctly rounded
+    exp (double exp rounded to float), subnormal results included.  A wrong
+    coefficient, a dropped Taylor term or a wrong ln 2 split fails this."""
+    pos_ulp, _ = O.exp_dev_max_ulp(0, _bits(88.75))
+    neg_ulp, _ = O.exp_dev_max_ulp(_bits(-0.0), _bits(-104.0))
+    assert pos_ulp <= 1.0 and neg_ulp <= 1.0
+
+
+def test_exp_dev_special_values():
+    assert O.exp_dev(0.0) == 1.0 and O.exp_dev(-0.0) == 1.0
+    assert O.exp_dev(float("-inf")) == 0.0 and O.exp_dev(-104.5) == 0.0
+    assert O.exp_dev(89.0) == float("inf") and O.exp_dev(float("inf")) == float("inf")
+    assert math.isnan(O.exp_dev(float("nan")))
+    assert O.exp_dev(1.0) == float(np.float32(math.e))
+
+
+def test_silu_dev_close_to_silu():
+    for x in np.linspace(-90, 90, 2001).astype(F32):
+        a, b = O.silu_dev(float(x)), O.silu(float(x))
+        assert abs(a - b) <= 4 * np.spacing(F32(abs(b))) + 1e-44, (x, a, b)
+
+
+@pytest.mark.parametrize("n,nt", [(2048, 256), (4096, 256), (256, 256), (2048, -256), (5632, -256), (300, -256),
+                                  (8192, 512)])
+def test_rms_norm_dev_is_the_same_sum(n, nt):
+    """Squares that are small integers sum exactly in any order, so the
+    device's trees must give the reference's bits: a dropped, doubled or
+    misplaced term (a task past its end, a wave skipped) fails.  Random
+    values: within rounding of the sequential sum."""
+    rng = np.random.default_rng(n + nt)
+    if nt > 0 and n // 8 > 2 * nt:
+        pytest.skip("the fused form covers at most 2 nt tasks")
+    w = rng.standard_normal(n).astype(F32)
+    x = rng.integers(-7, 8, n).astype(F32)
+    assert np.array_equal(O.rms_norm_dev(x, w, 1e-5, nt).view(np.uint32), O.rms_norm(x, w, 1e-5).view(np.uint32))
+    x = rng.standard_normal(n).astype(F32)
+    a, b = O.rms_norm_dev(x, w, 1e-5, nt), O.rms_norm(x, w, 1e-5)
+    assert np.max(np.abs(a - b)) <= 2e-6 * np.max(np.abs(b))
+
+
+@pytest.mark.parametrize("seq", [1, 2, 3, 4, 5, 63, 64, 65, 200, 257, 300])
+@pytest.mark.parametrize("d_head", [64, 128])
+def test_attend_head_dev_is_the_same_softmax(seq, d_head):
+    """Equal scores make every p_j = 1 exactly; with small integer values
+    every partial sum is exact, so the parallel order must give the mean of
+    the values exactly as the reference's recurrence does (a key dropped or
+    counted twice, a wrong run bound or a lost wave fails).  Random inputs:
+    within 1e-6 of the reference's order.  Seq lengths cover waves without
+    keys (seq < 4), one partial run, several runs per wave, and the
+    32-key runs of d_head 128."""
+    rng = np.random.default_rng(seq * 7 + d_head)
+    kvd = 2 * d_head
+    q = np.zeros(d_head, F32)
+    k = rng.standard_normal((seq, kvd)).astype(F32)
+    v = rng.integers(-8, 9, (seq, kvd)).astype(F32)
+    ref = O.attend_head(q, k, v, 1, seq, kvd, d_head, 0.125)
+    got = O.attend_head_dev(q, k, v, 1, seq, kvd, d_head, 0.125)
+    if seq & (seq - 1) == 0:  # 1 / seq exact
+        assert np.array_equal(got, v[:, d_head:].mean(axis=0).astype(F32))
+    assert np.max(np.abs(got - ref)) <= 1e-6 * max(1.0, np.max(np.abs(ref)))
+    q = rng.standard_normal(d_head).astype(F32)
+    v = rng.standard_normal((seq, kvd)).astype(F32)
+    ref = O.attend_head(q, k, v, 1, seq, kvd, d_head, 0.125)
+    got = O.attend_head_dev(q, k, v, 1, seq, kvd, d_head, 0.125)
+    assert np.max(np.abs(got - ref)) <= 1e-6 * np.max(np.abs(ref))
+
+
+def test_llama_device_order_close_to_reference_order():
+    """The whole step in the device's orders stays within rounding of the
+    reference's orders (EXACT linears), and the trace is the residual stream
+    the step really adds to."""
+    W = make_weights(tiny_cfg(), seed=61)
+    a = oracle_model(W)
+    b = O.Llama(W["cfg"], W["token_embd"], W["output_norm"], W["lm_head"], W["blocks"], device_order=(256, -256))
+    for t in (3, 100, 7, 319, 3):
+        la, xa = a.forward_token(t, trace=True)
+        lb = b.forward_token(t)
+        assert normwise(lb, la) < 1e-5
+    # the trace's last row is what the output norm and head see
+    head_in = O.rms_norm(xa[-1], W["output_norm"], W["cfg"]["eps"])
+    bb, dt = W["lm_head"]
+    assert np.array_equal(O.mm_1d(head_in, bb, dt, W["cfg"]["vocab"], W["cfg"]["d_model"]).view(np.uint32),
+                          la.view(np.uint32))
