@@ -175,3 +175,104 @@ def test_q6_k_dequant_layout_quartets():
     v = O.dequantize(b, O.Q6_K, 256)
     want = np.array([np.float32(0.125 * sc[p // 16]) * np.float32(q[p]) for p in range(256)], np.float32)
     assert np.array_equal(v, want)
+
+
+# ---- GT-10 known answers (spec/book/08-steps-loops-concurrency.md L761-790,
+# kquant.rs L193-245), derived by hand from the rule's text.  Each block is
+# built so that one plausible mistake changes a named integer: round half to
+# even instead of half away from zero, lo = the least value instead of
+# min(0, least), a missing clamp of sc / m / q, the last instead of the first
+# value of largest magnitude (Q6_K).
+
+def _kat_q4k_ties_all_positive():
+    """Q4_K, no negative value.  Sub-block 0: 59.0625, 9.84375, 1.96875, then
+    zeros: hi - lo = 59.0625, w0 = 3.9375, d = f16(3.9375 / 63) = 0.0625,
+    sc0 = 63, s0 = 3.9375, q = 59.0625 / s0 = 15, 9.84375 / s0 = 2.5 -> 3,
+    1.96875 / s0 = 0.5 -> 1 (half to even: 2 and 0).  Sub-block 1: 9.84375
+    then zeros: w1 = 0.65625, w1 / d = 10.5 -> sc1 = 11 (even: 10), s1 =
+    0.6875, q = 14.318 -> 14.  Sub-block 2: 32 times 0.9375 (all positive):
+    lo = min(0, 0.9375) = 0, w2 = 0.0625, sc2 = 1, q = 15 (lo = 0.9375 would
+    give w2 = 0, sc2 = 0, q = 0).  All v_b = 0: dmin = 0, every m = 0."""
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[2], x[32] = 59.0625, 9.84375, 1.96875, 9.84375
+    x[64:96] = 0.9375
+    q = np.zeros(256, np.int32)
+    q[0], q[1], q[2], q[32] = 15, 3, 1, 14
+    q[64:96] = 15
+    return x, q, [63, 11, 1, 0, 0, 0, 0, 0], [0] * 8, 0.0625, 0.0
+
+
+def _kat_q4k_min_tie():
+    """Q4_K with mins.  Sub-block 0: -7.875, 6.890625, then zeros: lo =
+    -7.875, hi - lo = 14.765625, w0 = 0.984375 -> d = f16(0.984375 / 63) =
+    2^-6, sc0 = 63, s0 = 0.984375; v0 = 7.875 -> dmin = f16(7.875 / 63) =
+    0.125, m0 = 63, o0 = 7.875: q = 0 / s0 = 0, 14.765625 / s0 = 15, zeros
+    7.875 / s0 = 8.  Sub-block 1: -2.5625, then zeros: w1 = 2.5625 / 15 ->
+    w1 / d = 10.93 -> sc1 = 11, s1 = 0.171875; v1 / dmin = 20.5 -> m1 = 21
+    (even: 20), o1 = 2.625: q = 0.0625 / s1 = 0.36 -> 0, zeros 2.625 / s1
+    = 15.27 -> 15."""
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[32] = -7.875, 6.890625, -2.5625
+    q = np.zeros(256, np.int32)
+    q[1] = 15
+    q[2:32] = 8
+    q[33:64] = 15
+    return x, q, [63, 11, 0, 0, 0, 0, 0, 0], [63, 21, 0, 0, 0, 0, 0, 0], 2.0 ** -6, 0.125
+
+
+def _kat_q4k_clamps():
+    """Q4_K of tiny values, where binary16 subnormal rounding makes the
+    scales small.  Sub-block 0: 1323 * 2^-24, then zeros: w0 = 88.2 * 2^-24,
+    d = f16(1.4 * 2^-24) = 2^-24, round(w0 / d) = 88 -> sc0 = 63 (clamp),
+    s0 = 63 * 2^-24, q = 1323 / 63 = 21 -> 15 (clamp).  Sub-block 1:
+    -88 * 2^-24, then zeros: v1 = 88 * 2^-24, dmin = f16(1.397 * 2^-24) =
+    2^-24, m1 = 88 -> 63 (clamp), o1 = 63 * 2^-24; w1 = 88 / 15 * 2^-24 ->
+    sc1 = round(5.87) = 6, s1 = 6 * 2^-24: q = -25 / 6 -> -4 -> 0 (clamp),
+    zeros 63 / 6 = 10.5 -> 11 (even: 10)."""
+    u = np.float32(2.0 ** -24)
+    x = np.zeros(256, np.float32)
+    x[0], x[32] = np.float32(1323) * u, np.float32(-88) * u
+    q = np.zeros(256, np.int32)
+    q[0] = 15
+    q[33:64] = 11
+    return x, q, [63, 6, 0, 0, 0, 0, 0, 0], [0, 63, 0, 0, 0, 0, 0, 0], 2.0 ** -24, 2.0 ** -24
+
+
+def _kat_q6k_first_of_largest():
+    """Q6_K.  Sub-block 0: 0.5, -0.5, then zeros: the first value of largest
+    magnitude is 0.5, w0 = 0.5 / -32 = -2^-6; d = f16(2^-6 / 127) = 1032 *
+    2^-23; sc0 = round(-127.008) = -127, s0 = -131064 * 2^-23: q = 0.5 / s0
+    = -32.002 -> -32, -0.5 / s0 = 32.002 -> 31 (clamp).  The last value of
+    largest magnitude would give sc0 = 127, q = 31 and -32.  Other
+    sub-blocks: w = -0.0, sc = 0, s = 0, q = 0."""
+    x = np.zeros(256, np.float32)
+    x[0], x[1] = 0.5, -0.5
+    q = np.zeros(256, np.int32)
+    q[0], q[1] = -32, 31
+    return x, q, [-127] + [0] * 15, [], 1032 * 2.0 ** -23, 0.0
+
+
+KATS = [(O.Q4_K, _kat_q4k_ties_all_positive), (O.Q4_K, _kat_q4k_min_tie), (O.Q4_K, _kat_q4k_clamps),
+        (O.Q5_K, _kat_q4k_ties_all_positive), (O.Q6_K, _kat_q6k_first_of_largest)]
+
+
+@pytest.mark.parametrize("fmt,kat", KATS)
+def test_quantize_k_known_answers(fmt, kat):
+    x, q, sc, mn, d, dmin = kat()
+    if fmt == O.Q5_K:  # nmax 31: the same block's q doubles where exact (w / 31 instead of / 15)
+        pytest.skip("the known answers above are Q4_K's nmax 15")
+    gq, gsc, gmn, gd, gdmin = O.quantize_k(x, fmt)
+    assert gd == d and gdmin == dmin
+    assert list(gsc) == sc
+    if fmt != O.Q6_K:
+        assert list(gmn) == mn
+    assert np.array_equal(gq, q), np.nonzero(gq != q)[0][:8]
+
+
+@pytest.mark.parametrize("fmt,kat", KATS)
+def test_library_quantizer_bytes_on_known_answers(fmt, kat):
+    """rce_qmm_quantize (the product's encoder) writes the oracle's bytes
+    on the known-answer blocks (Q5_K too: same rule, nmax 31)."""
+    import rce_amd
+    x = kat()[0]
+    assert np.array_equal(rce_amd.quantize(x.reshape(1, 256), fmt), O.quantize(x, fmt))
