@@ -295,7 +295,9 @@ void rce_qmm_llama_destroy(rce_qmm_llama *m);
 
 /* TinyLlamaRuntime::new_state (L355): position 0, empty caches. */
 rce_qmm_status rce_qmm_llama_reset(rce_qmm_llama *m);
-/* TinyLlamaState::pos: positions decoded since the last reset. */
+/* TinyLlamaState::pos: positions decoded since the last reset (a step
+ * queued by rce_qmm_llama_forward_token_dev counts until
+ * rce_qmm_llama_check reports it skipped). */
 rce_qmm_status rce_qmm_llama_pos(const rce_qmm_llama *m, size_t *pos);
 
 /* forward_logits / forward_token (L356, L289-294): logits [vocab] (host)
@@ -308,13 +310,18 @@ rce_qmm_status rce_qmm_llama_forward_token(rce_qmm_llama *m, int32_t token_id, f
 rce_qmm_status rce_qmm_llama_forward_embedding(rce_qmm_llama *m, const float *embedding, float *logits);
 /* forward_token on device memory, asynchronous on `stream` (NULL = the
  * context's stream): token id read from token_dev, logits written to
- * logits_dev [vocab].  A full cache is RCE_QMM_BAD_SHAPE at the call; an
- * out-of-range token id found on the device is reported by
- * rce_qmm_llama_check (that step's logits are then undefined). */
+ * logits_dev [vocab].  A full cache is RCE_QMM_BAD_SHAPE at the call.  A
+ * token id out of range, found on the device, skips that step: no cache
+ * row is written and the position does not advance, so later steps decode
+ * as if it had not been given; its logits are undefined, and
+ * rce_qmm_llama_check reports it. */
 rce_qmm_status rce_qmm_llama_forward_token_dev(rce_qmm_llama *m, const int32_t *token_dev, float *logits_dev,
                                                void *stream);
-/* Wait for the decoder's work and report (then clear) an error found on the
- * device since the last check: RCE_QMM_BAD_SHAPE for a token id out of range. */
+/* Wait for the decoder's work -- on the context's stream and on the stream
+ * of the last rce_qmm_llama_forward_token_dev call -- and report (then
+ * clear) an error found on the device since the last check:
+ * RCE_QMM_BAD_SHAPE for token ids out of range (the position then counts
+ * only the steps that ran). */
 rce_qmm_status rce_qmm_llama_check(rce_qmm_llama *m);
 
 /* ---- the "hip:op-qmm" priced backend (rce-placement-adapter) ------------- */

@@ -40,9 +40,9 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
                                                       int *status) {
     __shared__ float part[NORM_NT / 64];
     const int t = threadIdx.x;
-    if (pos && t == 0) {  // the last norm of a decode step advances the position
+    if (pos && t == 0 && status[2] == 0) {  // the last norm of a decode step advances the position
         const int p = pos[0];
-        if (p >= ctx_len) status[0] = 2;
+        if (p >= ctx_len && status[0] == 0) status[0] = 2;
         pos[0] = p + 1;
     }
     float ss = 0.0f;
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
                                                            float *__restrict__ k_cache, float *__restrict__ v_cache,
                                                            const int *__restrict__ pos_p, int ctx_len, int n_q,
                                                            int n_kv, int rope_dim, float scale,
-                                                           float *__restrict__ att) {
+                                                           float *__restrict__ att, const int *__restrict__ skip) {
     constexpr int DPL = DH / 64;    // dimensions per lane
     constexpr int CH = 4096 / DH;   // keys per run (64 or 32)
     constexpr int R4 = DH / 4;      // float4 pieces of a row
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
         ks[i + half] = as + bc;
     }
     __syncthreads();
-    if (h % qpk == 0 && wave == 0) {  // append this position to the layer's caches
+    if (h % qpk == 0 && wave == 0 && !(skip && skip[0])) {  // append this position to the layer's caches
         float *kd = k_cache + (size_t)pos * kvd + (size_t)g * DH, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
 #pragma unroll
         for (int d = 0; d < DPL; d++) {
@@ -302,16 +302,16 @@ bool attention_supports(int d_head, int rope_dim) {
 
 hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache, const int *pos,
                             int ctx_len, int n_q, int n_kv, int d_head, int rope_dim, float scale, float *att,
-                            hipStream_t s) {
+                            const int *skip, hipStream_t s) {
     if (n_kv <= 0 || n_q % n_kv) return hipErrorInvalidValue;
     switch (d_head) {
     case 64:
         hipLaunchKernelGGL(k_attention<64>, dim3(n_q), dim3(64 * ATT_NW), 0, s, qkv, rope_cs, k_cache, v_cache, pos,
-                           ctx_len, n_q, n_kv, rope_dim, scale, att);
+                           ctx_len, n_q, n_kv, rope_dim, scale, att, skip);
         break;
     case 128:
         hipLaunchKernelGGL(k_attention<128>, dim3(n_q), dim3(64 * ATT_NW), 0, s, qkv, rope_cs, k_cache, v_cache, pos,
-                           ctx_len, n_q, n_kv, rope_dim, scale, att);
+                           ctx_len, n_q, n_kv, rope_dim, scale, att, skip);
         break;
     default:
         return hipErrorInvalidValue;

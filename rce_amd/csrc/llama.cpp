@@ -48,12 +48,14 @@ struct rce_qmm_llama {
     void *mem = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *g = nullptr, *u = nullptr,
           *o = nullptr, *logits = nullptr, *norms = nullptr, *rope_cs = nullptr, *kc = nullptr, *vc = nullptr;
-    int *pos_dev = nullptr, *status = nullptr, *token = nullptr;
+    int *pos_dev = nullptr, *status = nullptr, *token = nullptr;  // status: the three words of launch_embed_row
     // pinned host staging
     int32_t *h_token = nullptr;
     int *h_status = nullptr;
     float *h_logits = nullptr;
-    size_t pos = 0;  // host mirror of pos_dev
+    size_t pos = 0;  // host mirror of pos_dev (plus the skipped steps not yet checked)
+    hipEvent_t last_dev = nullptr;  // after the last forward_token_dev step, on the caller's stream
+    bool last_dev_pending = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     float *graph_logits = nullptr;  // where the captured graph writes logits
@@ -133,7 +135,7 @@ rce_qmm_status enqueue_body(rce_qmm_llama *m, float *logits, hipStream_t s) {
             HIP_TRY(launch_gemv(L.wv, m->xn, 1, m->qkv + qd + kvd, m->mode, s));
         }
         HIP_TRY(launch_attention(m->qkv, m->rope_cs, kc, vc, m->pos_dev, ctx_len, (int)c.n_q_heads, (int)c.n_kv_heads,
-                                 (int)c.d_head, (int)c.rope_dim, scale, m->att, s));
+                                 (int)c.d_head, (int)c.rope_dim, scale, m->att, m->status + 2, s));
         if (L.wo_res) {
             FxLaunch f;
             f.kind = FX_RESIDUAL;
@@ -230,15 +232,25 @@ rce_qmm_status run_step(rce_qmm_llama *m, float *logits, hipStream_t s) {
     return RCE_QMM_OK;
 }
 
-// Wait, read and clear the device status.
+// Wait for the decoder's work on `s` and on the stream of the last
+// forward_token_dev step, read the device status and clear it.  Steps
+// skipped for a bad token id did not advance the device position: the host
+// mirror gives them back.
 rce_qmm_status take_status(rce_qmm_llama *m, hipStream_t s) {
-    HIP_TRY(hipMemcpyAsync(m->h_status, m->status, sizeof(int), hipMemcpyDeviceToHost, s));
+    if (m->last_dev_pending) {
+        HIP_TRY(hipEventSynchronize(m->last_dev));
+        m->last_dev_pending = false;
+    }
+    HIP_TRY(hipMemcpyAsync(m->h_status, m->status, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
-    const int code = *m->h_status;
+    const int code = m->h_status[0], skipped = m->h_status[1];
     if (code == 0) return RCE_QMM_OK;
-    HIP_TRY(hipMemsetAsync(m->status, 0, sizeof(int), s));
+    HIP_TRY(hipMemsetAsync(m->status, 0, 2 * sizeof(int), s));
     HIP_TRY(hipStreamSynchronize(s));
-    if (code == 1) return fail(RCE_QMM_BAD_SHAPE, "token id out of range of token_embd");
+    m->pos -= std::min<size_t>(m->pos, (size_t)std::max(skipped, 0));
+    if (code == 1)
+        return fail(RCE_QMM_BAD_SHAPE, "token id out of range of token_embd (" + std::to_string(skipped) +
+                                           " step(s) skipped: no cache row, no position advance)");
     return fail(RCE_QMM_BAD_SHAPE, "decode position past the KV cache");
 }
 
@@ -346,8 +358,8 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     for (int i = 0; i < NF; i++) *fp[i] = reinterpret_cast<float *>(base + off[i]);
     int *ints = reinterpret_cast<int *>(base + off[NF]);
     m->pos_dev = ints;
-    m->status = ints + 1;
-    m->token = ints + 2;
+    m->token = ints + 1;
+    m->status = ints + 4;
     auto cleanup = [&](rce_qmm_status s2) {
         rce_qmm_llama_destroy(m);
         return s2;
@@ -357,6 +369,8 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
         hipHostMalloc(reinterpret_cast<void **>(&m->h_logits), c.vocab * sizeof(float), hipHostMallocDefault) !=
             hipSuccess)
         return cleanup(fail(RCE_QMM_OUT_OF_MEMORY, "decoder pinned staging"));
+    if ((e = hipEventCreateWithFlags(&m->last_dev, hipEventDisableTiming)) != hipSuccess)
+        return cleanup(hip_fail(e, "decoder event"));
 
     // norm weights [attn_norm, ffn_norm] per layer, then output_norm
     std::vector<float> norms((2 * c.n_layers + 1) * dm);
@@ -400,6 +414,7 @@ void rce_qmm_llama_destroy(rce_qmm_llama *m) {
     if (m->h_token) (void)hipHostFree(m->h_token);
     if (m->h_status) (void)hipHostFree(m->h_status);
     if (m->h_logits) (void)hipHostFree(m->h_logits);
+    if (m->last_dev) (void)hipEventDestroy(m->last_dev);
     rce_qmm_context *ctx = m->ctx;
     delete m;
     context_release(ctx);
@@ -410,8 +425,12 @@ rce_qmm_status rce_qmm_llama_reset(rce_qmm_llama *m) {
     rce_qmm_status st = set_device(m->ctx->device);
     if (st) return st;
     hipStream_t s = m->ctx->stream;
+    if (m->last_dev_pending) {
+        HIP_TRY(hipEventSynchronize(m->last_dev));
+        m->last_dev_pending = false;
+    }
     HIP_TRY(poison_caches(m, s));
-    HIP_TRY(hipMemsetAsync(m->pos_dev, 0, 2 * sizeof(int), s));  // pos, status
+    HIP_TRY(hipMemsetAsync(m->pos_dev, 0, 256, s));  // pos, token, status words
     HIP_TRY(hipStreamSynchronize(s));
     m->pos = 0;
     return RCE_QMM_OK;
@@ -446,6 +465,7 @@ rce_qmm_status rce_qmm_llama_forward_embedding(rce_qmm_llama *m, const float *em
     hipStream_t s = m->ctx->stream;
     if (m->pos >= m->cfg.context_length) return fail(RCE_QMM_BAD_SHAPE, "the KV cache is full");
     HIP_TRY(hipMemcpyAsync(m->x, embedding, m->cfg.d_model * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemsetAsync(m->status + 2, 0, sizeof(int), s));  // not a skipped step (outside the graph)
     if ((st = run_step(m, m->logits, s))) return st;
     return finish_host(m, logits, s);
 }
@@ -458,7 +478,10 @@ rce_qmm_status rce_qmm_llama_forward_token_dev(rce_qmm_llama *m, const int32_t *
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->ctx->stream;
     if (m->pos >= m->cfg.context_length) return fail(RCE_QMM_BAD_SHAPE, "the KV cache is full");
     HIP_TRY(launch_embed_row(m->embd, token_dev, m->x, m->status, s));
-    return run_step(m, logits_dev, s);
+    if ((st = run_step(m, logits_dev, s))) return st;
+    HIP_TRY(hipEventRecord(m->last_dev, s));  // rce_qmm_llama_check waits for it
+    m->last_dev_pending = true;
+    return RCE_QMM_OK;
 }
 
 rce_qmm_status rce_qmm_llama_check(rce_qmm_llama *m) {

@@ -279,7 +279,12 @@ rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, s
         return fail(RCE_QMM_BAD_SHAPE, "n_cols " + std::to_string(n_cols) + " is not a multiple of the block size " +
                                            std::to_string(qk));
     const size_t rowb = n_cols / qk * bb;
-    const size_t want_len = n_rows * rowb + (dtype == T_I2_S ? 4 : 0);  // I2_S: codes, then one f32 scale
+    size_t want_len = 0;
+    if (__builtin_mul_overflow(n_rows, rowb, &want_len) ||
+        __builtin_add_overflow(want_len, (size_t)(dtype == T_I2_S ? 4 : 0), &want_len))  // I2_S: codes, then one f32 scale
+        return fail(RCE_QMM_BAD_SHAPE, "n_rows * row_bytes overflows size_t");
+    if (want_len > ((size_t)1 << 48))  // the device layout adds padding per row: keep its size far from wrapping
+        return fail(RCE_QMM_BAD_SHAPE, "weights larger than 2^48 bytes");
     if (len != want_len)
         return fail(RCE_QMM_BAD_SHAPE, "len " + std::to_string(len) + " != " + std::to_string(want_len) +
                                            (dtype == T_I2_S ? " (n_rows*row_bytes + the f32 scale)" : " (n_rows*row_bytes)"));
@@ -327,12 +332,13 @@ rce_qmm_status rce_qmm_weight_sub_view(const rce_qmm_weight *w, size_t byte_offs
                                        size_t n_cols, rce_qmm_weight **out) {
     if (!w || !out) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
     *out = nullptr;
-    if (byte_offset + byte_len > w->len)
+    if (byte_offset > w->len || byte_len > w->len - byte_offset)
         return fail(RCE_QMM_BAD_SHAPE, "sub_view out of bounds: " + std::to_string(byte_offset) + "+" +
                                            std::to_string(byte_len) + " > " + std::to_string(w->len));
     if (n_cols != w->dw.n_cols) return fail(RCE_QMM_BAD_SHAPE, "sub_view must keep n_cols");
     const size_t rb = w->host_row_bytes;
-    if (rb == 0 || byte_offset % rb || byte_len != n_rows * rb)
+    size_t view_bytes = 0;
+    if (rb == 0 || byte_offset % rb || __builtin_mul_overflow(n_rows, rb, &view_bytes) || byte_len != view_bytes)
         return fail(RCE_QMM_BAD_SHAPE, "sub_view must cover whole rows of the parent");
     const size_t row0 = byte_offset / rb;
     if (w->dw.dtype == T_I2_S)  // one scale per tensor, after all rows

@@ -150,16 +150,21 @@ __global__ void k_dequant_row(DevWeight w, size_t row, float *__restrict__ out) 
 }
 
 // The row index comes from device memory (a token id of the decode step);
-// an id outside [0, n_rows) sets status[0] = 1 and leaves x unchanged.
+// an id outside [0, n_rows) leaves x unchanged and marks the step skipped
+// (the status words of launch_embed_row).
 __global__ void k_embed_row(DevWeight w, const int32_t *__restrict__ row_dev, float *__restrict__ x,
                             int *__restrict__ status) {
     const int32_t id = row_dev[0];
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id < 0 || (size_t)id >= w.n_rows) {
-        if (i == 0) status[0] = 1;
-        return;
+    const bool bad = id < 0 || (size_t)id >= w.n_rows;
+    if (i == 0) {
+        if (bad) {
+            if (status[0] == 0) status[0] = 1;
+            status[1] = status[1] + 1;
+        }
+        status[2] = bad ? 1 : 0;
     }
-    if (i < w.n_cols) x[i] = dequant_value(w, (size_t)id, i);
+    if (!bad && i < w.n_cols) x[i] = dequant_value(w, (size_t)id, i);
 }
 
 // The Q8 activations of `total` / (k / 8) tokens, quantized once into

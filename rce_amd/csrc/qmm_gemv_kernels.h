@@ -1145,9 +1145,9 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     const int RT = P * RPL;
     unsigned bx = blockIdx.x;
     if constexpr (KIND == FX_SEG) {  // block-uniform choice of the segment
-        if (fx.pos && bx == 0 && tid == 0) {  // the step's last kernel: advance the position
+        if (fx.pos && bx == 0 && tid == 0 && fx.status[2] == 0) {  // the step's last kernel: advance the position
             const int p = fx.pos[0];
-            if (p >= fx.ctx_len) fx.status[0] = 2;
+            if (p >= fx.ctx_len && fx.status[0] == 0) fx.status[0] = 2;
             fx.pos[0] = p + 1;
         }
         if (bx >= fx.blk3) { w = fx.w3; out = fx.out3; bx -= fx.blk3; }

@@ -175,8 +175,9 @@ struct FxLaunch {
     const float *norm_w = nullptr;
     float eps = 0.0f;
     // FX_SEG: when pos is given, one thread also ends a decode step, as
-    // launch_rms_norm does with pos (status[0] = 2 if pos[0] >= ctx_len,
-    // then pos[0] += 1); no other kernel of the step may follow that reads pos.
+    // launch_rms_norm does with pos (unless status[2] marks the step
+    // skipped: status[0] = 2 if pos[0] >= ctx_len, then pos[0] += 1); no
+    // other kernel of the step may follow that reads pos.
     int *pos = nullptr;
     int *status = nullptr;
     int ctx_len = 0;
@@ -201,13 +202,19 @@ hipError_t launch_gemv_fx_q4_1(const FxLaunch &f, const GemvGeom &g, const float
 hipError_t launch_gemv_fx_q3_k(const FxLaunch &f, const GemvGeom &g, const float *a, int mode, hipStream_t s);
 
 // ---- decode step (decoder.hip) ----
-// x = dequant_row(w, *row_dev) (QuantWeight::dequant_row); an id outside
-// [0, n_rows) sets status[0] = 1 and writes nothing.
+// The decode step's status words: status[0] the first error code since the
+// last check (1 a token id out of range, 2 a position past the cache),
+// status[1] the number of steps skipped for a bad token id since then,
+// status[2] 1 while the current step is such a skipped step (its cache row
+// and position advance are left out), else 0.
+// x = dequant_row(w, *row_dev) (QuantWeight::dequant_row), status[2] = 0;
+// an id outside [0, n_rows) writes nothing to x, sets status[0] = 1 (if
+// still 0) and status[2] = 1 and counts the step in status[1].
 hipError_t launch_embed_row(const DevWeight &w, const int32_t *row_dev, float *x, int *status, hipStream_t s);
 // out = rms_norm(x, w, eps) (rce-tinyllama L158-163) over n values.  When
-// pos is given, one thread also ends a decode step: status[0] = 2 if
-// pos[0] >= ctx_len, then pos[0] += 1 (no other kernel of the step may
-// follow that reads pos).
+// pos is given, one thread also ends a decode step unless status[2] marks
+// it skipped: status[0] = 2 if pos[0] >= ctx_len, then pos[0] += 1 (no
+// other kernel of the step may follow that reads pos).
 hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, float *out, int *pos, int ctx_len,
                            int *status, hipStream_t s);
 // RoPE of q (n_q heads) and k (n_kv heads) at position pos[0], append of k, v to
@@ -215,10 +222,11 @@ hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, 
 // attention over positions 0..pos (rce-op-attn L107-151, L185-251).
 // qkv: [q (n_q * d_head) | k (n_kv * d_head) | v (n_kv * d_head)];
 // rope_cs: [ctx_len][rope_dim / 2] (cos, sin) pairs; caches
-// [ctx_len][n_kv * d_head]; att: [n_q * d_head].
+// [ctx_len][n_kv * d_head]; att: [n_q * d_head].  skip (may be null): when
+// skip[0] != 0 the step is a skipped one and appends nothing to the caches.
 hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache,
                             const int *pos, int ctx_len, int n_q, int n_kv, int d_head, int rope_dim,
-                            float scale, float *att, hipStream_t s);
+                            float scale, float *att, const int *skip, hipStream_t s);
 bool attention_supports(int d_head, int rope_dim);
 // h = silu(g) * u, x = x + o: the unfused forms.
 hipError_t launch_swiglu(const float *g, const float *u, float *h, size_t n, hipStream_t s);

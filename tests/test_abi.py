@@ -93,3 +93,33 @@ def test_moe_router_matches_oracle_bit_for_bit():
 def test_moe_router_rejects_bad_top_k():
     with pytest.raises(rce_amd.QmmError):
         rce_amd.moe_router(np.zeros((1, 4), np.float32), 5)
+
+
+@pytest.mark.gpu
+def test_size_checks_do_not_wrap(ctx):
+    """Shape arguments whose products or sums overflow size_t are refused
+    before any copy (the reference's slices would panic): n_rows * row_bytes
+    wrapping to the buffer's length, and sub-views whose offset + length or
+    n_rows * row_bytes wrap."""
+    L = _lib.lib()
+    SMAX = (1 << 64) - 1
+    buf = np.zeros(64, np.uint8)
+    out = ctypes.c_void_p()
+    # Q4_0, 32 columns: 18 bytes per row; 2^64 / 18 + 1 rows wrap to 8 bytes
+    n = (1 << 64) // 18 + 1
+    wrapped = (n * 18) % (1 << 64)
+    assert wrapped < 64
+    st = L.rce_qmm_weight_from_bytes(ctx.handle, 2, n, 32, buf.ctypes.data, wrapped, ctypes.byref(out))
+    assert st == 2 and not out.value
+    rng = np.random.default_rng(3)
+    b = O.quantize((rng.standard_normal((8, 64)) * 0.02).astype(np.float32), O.Q4_0)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, 8, 64)
+    v = ctypes.c_void_p()
+    assert L.rce_qmm_weight_sub_view(w.handle, SMAX - 5, 36, 1, 64, ctypes.byref(v)) == 2  # offset + len wraps
+    assert L.rce_qmm_weight_sub_view(w.handle, 36, SMAX, 1, 64, ctypes.byref(v)) == 2
+    n = (1 << 64) // 36 + 1  # n_rows * 36 wraps to 20
+    assert L.rce_qmm_weight_sub_view(w.handle, 0, (n * 36) % (1 << 64), n, 64, ctypes.byref(v)) == 2
+    assert not v.value
+    assert L.rce_qmm_weight_sub_view(w.handle, 36, 72, 2, 64, ctypes.byref(v)) == 0  # a good view still works
+    L.rce_qmm_weight_destroy(v)
+    w.close()

@@ -189,6 +189,40 @@ def test_llama_errors(ctx):
         device_model(ctx, W, Mode.F16_MFMA)
 
 
+def test_llama_bad_token_on_caller_stream(ctx):
+    """Tokens queued with forward_token_dev on a stream the caller made: a
+    bad id in the middle is reported by check (which waits for that
+    stream), the position counts only the steps that ran, and the decoder
+    goes on as if the bad id had not been given (no cache row written)."""
+    note("llama bad token id on a caller stream")
+    W = make_weights(tiny_cfg(), seed=35)
+    vocab = W["cfg"]["vocab"]
+    dev = device_model(ctx, W, Mode.Q8)
+    ref = device_model(ctx, W, Mode.Q8)
+    hip = ctypes.CDLL("libamdhip64.so")
+    s = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    toks = rce_amd.DeviceBuffer.from_numpy(ctx, np.array([3, vocab + 7, 100], np.int32))
+    out = rce_amd.DeviceBuffer(ctx, 4 * vocab)
+    for i in range(3):
+        dev.forward_token_dev(toks.ptr + 4 * i, out.ptr, stream=s.value)
+    with pytest.raises(rce_amd.QmmError) as e:
+        dev.check()
+    assert e.value.status == 2 and "skipped" in str(e.value)
+    assert dev.pos == 2
+    dev.check()  # cleared
+    ref.forward_logits(3)
+    want = ref.forward_logits(100)
+    got = out.download(np.float32, vocab)  # the third step's logits (check waited for the stream)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for t in (7, 42):
+        a, b = dev.forward_logits(t), ref.forward_logits(t)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert dev.pos == ref.pos == 4
+    toks.free(); out.free(); dev.close(); ref.close()
+    assert hip.hipStreamDestroy(s) == 0
+
+
 def test_llama_dev_entry_matches_host_entry(ctx):
     note("llama forward_token_dev == forward_logits")
     W = make_weights(tiny_cfg(), seed=28)
