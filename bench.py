@@ -3,17 +3,21 @@
 Headline (BASELINE.json metric "GEMV HBM GB/s & GEMM TFLOPS per quant
 format, % of MI355X roofline", configs[1]): Q4_0 decode GEMV, weight
 11008x4096 N(0,0.02) quantized to Q4_0, activation batch 1 of 4096 f32
-N(0,1), Q8-activation mode.  A step is one GEMV launch over device-resident
+N(0,1), in the reference's own f32 order (EXACT mode, bit-identical to
+mm_1d; --mode q8 for the Q8-activation mode).  A step is one GEMV launch over device-resident
 inputs; weights rotate over enough copies (> 2 x 256 MB) that each step
 streams its weight from HBM rather than the Infinity Cache, and the steps
 are replayed from a HIP graph.  `value` is algorithmic bytes per launch
 (GGUF weight bytes + 4 k + 4 n per token) / time per launch, the time
-taken with HIP events on the stream the kernels run on.  Other formats
+taken with HIP events on the stream the kernels run on.  Next to the
+8 TB/s datasheet peak the line reports the measured read ceiling: the
+fastest single launch that only reads the same number of bytes
+(rce_qmm_read_ceiling_dev, weights rotated the same way).  Other formats
 and configs are reported under "per_format".  The CPU baseline is the
 oracle (a C restatement of the reference's mm_1d, one task per output row
 over the host cores) timed on a bounded sample of the same workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode q8|exact] [--no-cpu] [--quick]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode exact|q8] [--no-cpu] [--quick]
 python bench.py --copy-calibration   # device copies of known size (PMC scaling)
 """
 from __future__ import annotations
@@ -34,7 +38,12 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFS = 2500.0     # MI355X dense fp16 MFMA, TFLOP/s
 INFINITY_CACHE = 256 << 20
-HEADLINE_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_11008x4096_q8_traffic.md")
+# Committed HBM-traffic summaries of the headline kernel, per mode; each
+# records the SHA-256 of the kernel sources it was measured on.
+TRAFFIC_PROFILE = {"exact": os.path.join(ROOT, "profiles", "gemv_q4_0_11008x4096_exact_traffic.md"),
+                   "q8": os.path.join(ROOT, "profiles", "gemv_q4_0_11008x4096_q8_traffic.md")}
+KERNEL_SOURCES = ("rce_amd/csrc/qmm_gemv_kernels.h", "rce_amd/csrc/gemv_q4_0.hip", "rce_amd/csrc/qmm_gemv.hip",
+                  "rce_amd/csrc/qmm_internal.h")
 
 
 def log(msg: str) -> None:
@@ -382,15 +391,65 @@ def cpu_leg(line, head, rows, budget_s=10.0):
             log(f"  {key}: normwise vs oracle {row['normwise_err_vs_oracle']:.2e}")
 
 
-def headline_traffic():
+def kernel_sources_sha256() -> str:
+    """SHA-256 over the headline kernel's source files (the stamp a traffic
+    summary must carry to be used for this build)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def headline_traffic(mode_name: str):
     """HBM bytes per launch of the headline kernel from the committed PMC
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel), or None."""
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel), or None
+    when there is none for this mode or it was measured on other kernel
+    sources than the ones built here."""
     try:
-        text = open(HEADLINE_PROFILE).read()
-    except OSError:
+        text = open(TRAFFIC_PROFILE[mode_name]).read()
+    except (OSError, KeyError):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
-    return int(m.group(1)) if m else None
+    h = re.search(r"kernel_sources_sha256:\s*([0-9a-f]{64})", text)
+    if not m or not h or h.group(1) != kernel_sources_sha256():
+        log(f"  traffic summary for {mode_name} missing or measured on other kernel sources: traffic null")
+        return None
+    return int(m.group(1))
+
+
+def read_ceiling(hip, ctx, nbytes, steps):
+    """The fastest single launch that only reads nbytes (every variant of
+    rce_qmm_read_ceiling_dev), over the same rotation of HBM copies as the
+    GEMV: (us per launch, variant); also the empty-launch time."""
+    import rce_amd
+    from rce_amd import _lib
+    L = _lib.lib()
+    nb = (nbytes + 4095) // 4096 * 4096
+    copies = max(2, min(64, (2 * INFINITY_CACHE) // nb + 1))
+    buf = rce_amd.DeviceBuffer(ctx, nb * copies)
+    sink = rce_amd.DeviceBuffer(ctx, 256)
+    hip.ok(hip.L.hipMemset(ctypes.c_void_p(buf.ptr), 1, nb * copies), "hipMemset")
+    hip.ok(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    stream = ctx.stream
+
+    def run(variant, count, n):
+        for i in range(count):
+            _lib.check(L.rce_qmm_read_ceiling_dev(ctx.handle, ctypes.c_void_p(buf.ptr + (i % copies) * nb), n,
+                                                  ctypes.c_void_p(sink.ptr), variant, None))
+
+    best = None
+    for v in range(9):
+        run(v, 3, nbytes)
+        ms = hip.timed_graph(stream, lambda: run(v, steps, nbytes), steps)
+        if best is None or ms < best[0]:
+            best = (ms, v)
+    run(9, 3, 0)
+    empty_ms = hip.timed_graph(stream, lambda: run(9, steps, 0), steps)
+    buf.free()
+    sink.free()
+    return best[0] * 1e3, best[1], empty_ms * 1e3
 
 
 def copy_calibration(hip, nbytes=256 << 20, reps=8):
@@ -415,12 +474,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--mode", choices=["q8", "exact"], default="q8")
+    ap.add_argument("--mode", choices=["exact", "q8"], default="exact")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only, no per-format rows")
     ap.add_argument("--rows", default="sweep,gemm,moe,llama",
                     help="per-format rows: comma-separated subset of sweep,gemm,moe,llama")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the read-ceiling launches (profiling runs)")
     ap.add_argument("--sweep-only", default="",
                     help="run only the sweep rows whose name contains this text (e.g. 'b8'; profiling)")
     args = ap.parse_args()
@@ -449,8 +509,16 @@ def main():
     log(f"  {ms * 1e3:.2f} us/launch  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
     head = {"b": b, "x": x, "dt": int(dt), "n": n, "k": k, "res": res, "mode": int(mode)}
 
+    if args.no_ceiling:
+        ceil_us, ceil_var, empty_us = float("nan"), -1, float("nan")
+    else:
+        ceil_us, ceil_var, empty_us = read_ceiling(hip, ctx, nbytes, args.steps)
+    ceil_gbs = nbytes / (ceil_us * 1e-6) / 1e9
+    log(f"  read ceiling at {nbytes} B: {ceil_us:.2f} us ({ceil_gbs:.0f} GB/s, variant {ceil_var}); "
+        f"empty launch {empty_us:.2f} us")
     line = {
-        "metric": "GEMV HBM GB/s (Q4_0 decode 11008x4096, batch 1, Q8 activations)",
+        "metric": "GEMV HBM GB/s (Q4_0 decode 11008x4096, batch 1, "
+                  + ("Q8 activations)" if mode == Mode.Q8 else "f32 activations, reference order)"),
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -467,7 +535,9 @@ def main():
                    "bytes_per_launch": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": headline_traffic() if mode == Mode.Q8 else None},
+                     "traffic": headline_traffic(args.mode),
+                     "read_ceiling": {"GB/s": round(ceil_gbs, 1), "us": round(ceil_us, 3), "variant": ceil_var,
+                                      "frac": round(gbs / ceil_gbs, 4), "empty_launch_us": round(empty_us, 3)}},
     }
 
     # ---- per-format rows (the metric is per quant format) ------------------------
@@ -524,8 +594,8 @@ def main():
         log("  building the configs[4] decoder (22 layers, Q4_K + Q6_K head)")
         W = llama_weights(500)
         lsteps, lwarm = 128, 16
-        # the headline's mode, then (after Q8) the reference-order EXACT mode
-        for lmode in (mode,) + ((Mode.EXACT,) if mode == Mode.Q8 else ()):
+        # Q8, then the reference-order EXACT mode
+        for lmode in (Mode.Q8, Mode.EXACT):
             lms, lsample = time_llama(hip, ctx, W, lmode, lsteps, lwarm, 501)
             lgb = LLAMA_WEIGHT_BYTES / (lms * 1e-3) / 1e9
             key = f"TinyLlama-shape decode 22L Q4_K/Q6_K b1 {lmode.name.lower()}"

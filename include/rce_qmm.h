@@ -409,6 +409,19 @@ rce_qmm_status rce_qmm_weight_from_gguf(rce_qmm_context *ctx, const rce_qmm_gguf
  * weights): n must equal the element count. */
 rce_qmm_status rce_qmm_gguf_read_f32(const rce_qmm_gguf *g, const char *name, float *out, size_t n);
 
+/* ---- measurement ---------------------------------------------------------- */
+
+/* No counterpart in the reference: one launch on `stream` that reads
+ * `bytes` (a multiple of 16, 16-byte aligned) of buf_dev once and does
+ * nothing else, the HBM read rate a single decode-GEMV launch of that byte
+ * count could reach (launch cost and ramp included).  sink_dev: 4 writable
+ * bytes (written only if the buffer's XOR-fold hits one fixed word).  variant 0..8 picks a launch
+ * shape (one pass of 256 threads x 4 / 8 / 16 loads, 1024 x 8, 256 x 8
+ * non-temporal, grid-stride 1024 or 2048 blocks of 256 x 8, 512 blocks of
+ * 512 x 8, one pass of 512 x 4); 9 launches one empty block. */
+rce_qmm_status rce_qmm_read_ceiling_dev(rce_qmm_context *ctx, const void *buf_dev, size_t bytes, void *sink_dev,
+                                        int variant, void *stream);
+
 /* ---- device memory helpers (for callers without a HIP runtime) ---------- */
 
 rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out);

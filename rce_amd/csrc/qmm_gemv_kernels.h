@@ -17,8 +17,11 @@
 //
 // Exactness (EXACT): every + - * of the reference is one binary32 operation
 // in the same order.  Q4_0's product (n - 8) a is formed as fma(n, a, -8a)
-// when a thread has one token (-8a is exact, the fma rounds (n - 8) a once)
-// and as (float)(n) - 8 (exact) times a otherwise.  All other code is built
+// when a thread has one token (-8a is exact while |a| < 2^124, and the fma
+// rounds (n - 8) a once) and as (float)(n) - 8 (exact) times a otherwise;
+// Q5_0 and Q3_K likewise with -16a and -4a.  So EXACT is the reference's bit
+// for bit for activations of magnitude below 2^123; larger or non-finite
+// activations can give another overflow or NaN pattern.  All other code is built
 // with -ffp-contract=off.  The Q6_K row sum of the reference is one chain
 // over all positions of the row, so Q6_K EXACT runs one row per lane.
 //
@@ -36,12 +39,39 @@
 
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 namespace rce_qmm {
 namespace {
 
 
 constexpr uint32_t NIB = 0x0F0F0F0Fu;
+
+// Weight loads.  A launch reads each weight byte once, so the loads are
+// non-temporal: they stream through the caches instead of displacing what
+// is reused (measured on the headline shapes: 5-10 % faster per launch).
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
+typedef unsigned v2u32 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ldw16(const uint8_t *p) {
+    const v4u32 t = __builtin_nontemporal_load(reinterpret_cast<const v4u32 *>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint2 ldw8(const uint8_t *p) {
+    const v2u32 t = __builtin_nontemporal_load(reinterpret_cast<const v2u32 *>(p));
+    return make_uint2(t.x, t.y);
+}
+__device__ __forceinline__ uint32_t ldw4(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+}
+__device__ __forceinline__ uint32_t ldw2(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+}
+
+// Rows of weight loads a thread keeps in flight ahead of its arithmetic:
+// the next rows' loads go out before each row's addends, so a wave's data
+// arrives in the order it is used (measured: 2 beats issuing all rows at
+// once, 1 and 4).
+constexpr int PREFETCH_ROWS = 2;
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     _Float16 h;
@@ -137,63 +167,63 @@ struct RawQ3_K { uint2 q; uint32_t h; uint32_t sd; };  // sd: scales (bytes 0, 1
 __device__ __forceinline__ RawQ4_0 ld_q4_0(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ4_0 r;
-    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
-    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    r.q = ldw16(rp + w.plane1 + 16 * (size_t)col);
+    r.s = ldw2(rp + 2 * (size_t)col);
     return r;
 }
 
 __device__ __forceinline__ RawQ8_0 ld_q8_0(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ8_0 r;
-    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
-    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
-    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
+    r.q0 = ldw16(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = ldw16(rp + w.plane2 + 16 * (size_t)col);
+    r.s = ldw2(rp + 2 * (size_t)col);
     return r;
 }
 
 __device__ __forceinline__ RawQ4_K ld_q4_k(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ4_K r;
-    r.h = *reinterpret_cast<const uint4 *>(rp + 16 * (size_t)(col >> 2));
-    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
-    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
+    r.h = ldw16(rp + 16 * (size_t)(col >> 2));
+    r.q0 = ldw16(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = ldw16(rp + w.plane2 + 16 * (size_t)col);
     return r;
 }
 
 __device__ __forceinline__ RawQ5_K ld_q5_k(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ5_K r;
-    r.h = *reinterpret_cast<const uint4 *>(rp + 16 * (size_t)(col >> 2));
-    r.q0 = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
-    r.q1 = *reinterpret_cast<const uint4 *>(rp + w.plane2 + 16 * (size_t)col);
-    r.hb = *reinterpret_cast<const uint2 *>(rp + w.plane3 + 8 * (size_t)col);
+    r.h = ldw16(rp + 16 * (size_t)(col >> 2));
+    r.q0 = ldw16(rp + w.plane1 + 16 * (size_t)col);
+    r.q1 = ldw16(rp + w.plane2 + 16 * (size_t)col);
+    r.hb = ldw8(rp + w.plane3 + 8 * (size_t)col);
     return r;
 }
 
 __device__ __forceinline__ RawQ5_0 ld_q5_0(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ5_0 r;
-    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
-    r.s = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)col);
-    r.h = *reinterpret_cast<const uint32_t *>(rp + w.plane2 + 4 * (size_t)col);
+    r.q = ldw16(rp + w.plane1 + 16 * (size_t)col);
+    r.s = ldw2(rp + 2 * (size_t)col);
+    r.h = ldw4(rp + w.plane2 + 4 * (size_t)col);
     return r;
 }
 
 __device__ __forceinline__ RawQ4_1 ld_q4_1(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ4_1 r;
-    r.q = *reinterpret_cast<const uint4 *>(rp + w.plane1 + 16 * (size_t)col);
-    r.sm = *reinterpret_cast<const uint32_t *>(rp + 4 * (size_t)col);
+    r.q = ldw16(rp + w.plane1 + 16 * (size_t)col);
+    r.sm = ldw4(rp + 4 * (size_t)col);
     return r;
 }
 
 __device__ __forceinline__ RawQ3_K ld_q3_k(const DevWeight &w, size_t row, int col) {
     const uint8_t *rp = w.base + row * w.row_stride;
     RawQ3_K r;
-    r.q = *reinterpret_cast<const uint2 *>(rp + w.plane1 + 8 * (size_t)col);
-    r.h = *reinterpret_cast<const uint32_t *>(rp + w.plane2 + 4 * (size_t)col);
-    const uint32_t sc = *reinterpret_cast<const uint16_t *>(rp + w.plane3 + 2 * (size_t)col);
-    const uint32_t d = *reinterpret_cast<const uint16_t *>(rp + 2 * (size_t)(col >> 3));
+    r.q = ldw8(rp + w.plane1 + 8 * (size_t)col);
+    r.h = ldw4(rp + w.plane2 + 4 * (size_t)col);
+    const uint32_t sc = ldw2(rp + w.plane3 + 2 * (size_t)col);
+    const uint32_t d = ldw2(rp + 2 * (size_t)(col >> 3));
     r.sd = sc | (d << 16);
     return r;
 }
@@ -228,8 +258,8 @@ __device__ __forceinline__ void ld_q6_k(const DevWeight &w, size_t row, int sb, 
     const uint8_t *sp = w.base + (row >> 6) * w.group_stride + (size_t)sb * IL64_Q6K_SB;
     const size_t lane = row & 63;
 #pragma unroll
-    for (int j = 0; j < 13; j++) r.c[j] = *reinterpret_cast<const uint4 *>(sp + ((size_t)j * 64 + lane) * 16);
-    r.d = *reinterpret_cast<const uint16_t *>(sp + IL64_Q6K_D + lane * 2);
+    for (int j = 0; j < 13; j++) r.c[j] = ldw16(sp + ((size_t)j * 64 + lane) * 16);
+    r.d = ldw2(sp + IL64_Q6K_D + lane * 2);
 }
 
 // The four 6-bit value words (+32 offset, one byte per l) of positions
@@ -538,8 +568,8 @@ struct Q4_1Exact {
 #pragma unroll
         for (int t = 0; t < TB; t++)
             load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 32 * (size_t)col, av[t], 32);
-        sums();
     }
+    __device__ void prepare() { sums(); }  // after the weight loads are out
     __device__ void addends(const Raw &r, float *out) const {
         float va[TB];
 #pragma unroll
@@ -570,7 +600,6 @@ struct Q4_1Exact {
         load_f32x(gw + 32 * (size_t)col, g, 32);
 #pragma unroll
         for (int l = 0; l < 32; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
-        sums();
     }
 };
 
@@ -650,6 +679,9 @@ struct Q4_KExact {
             // are never folded or stored.
             load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 64 * (size_t)col, av[t], 64);
         }
+    }
+    // After the weight loads are out: the row-independent sums.
+    __device__ void prepare() {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             a_lo[t] = 0.0f;
@@ -690,16 +722,12 @@ struct Q4_KExact {
             out[t] = s;
         }
     }
-    // FX_NORM: the slice becomes (x * inv) * g and its sums are re-formed.
+    // FX_NORM: the slice becomes (x * inv) * g (prepare forms the sums after).
     __device__ void normalize(const float *gw, int col, float inv) {
         float g[64];
         load_f32x(gw + 64 * (size_t)col, g, 64);
 #pragma unroll
         for (int l = 0; l < 64; l++) { const float t = av[0][l] * inv; av[0][l] = t * g[l]; }
-        a_lo[0] = 0.0f;
-        a_hi[0] = 0.0f;
-#pragma unroll
-        for (int l = 0; l < 32; l++) { a_lo[0] = a_lo[0] + av[0][l]; a_hi[0] = a_hi[0] + av[0][32 + l]; }
     }
 };
 
@@ -718,6 +746,9 @@ struct Q5_KExact {
 #pragma unroll
         for (int t = 0; t < TB; t++)  // tokens past tv read token 0's slice (never folded)
             load_f32x(A + ((size_t)t0 + (t < tv ? t : 0)) * k + 64 * (size_t)col, av[t], 64);
+    }
+    // After the weight loads are out: the row-independent sums.
+    __device__ void prepare() {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             a_lo[t] = 0.0f;
@@ -763,10 +794,6 @@ struct Q5_KExact {
         load_f32x(gw + 64 * (size_t)col, gv, 64);
 #pragma unroll
         for (int l = 0; l < 64; l++) { const float t = av[0][l] * inv; av[0][l] = t * gv[l]; }
-        a_lo[0] = 0.0f;
-        a_hi[0] = 0.0f;
-#pragma unroll
-        for (int l = 0; l < 32; l++) { a_lo[0] = a_lo[0] + av[0][l]; a_hi[0] = a_hi[0] + av[0][32 + l]; }
     }
 };
 
@@ -1116,6 +1143,11 @@ struct Q6_KQ8 {
 
 __host__ __device__ constexpr int fold_ld(int U) { return ((U + 3) & ~3) + 4; }
 
+// Units with prepare(): work on the activations (row-independent sums) done
+// after the weight loads are issued, so it does not hold them back.
+template <class U, class = void> struct HasPrepare : std::false_type {};
+template <class U> struct HasPrepare<U, std::void_t<decltype(std::declval<U &>().prepare())>> : std::true_type {};
+
 // Dynamic LDS a block may use (the default per-block limit).
 constexpr size_t LDS_MAX = 64 * 1024;
 
@@ -1186,12 +1218,14 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weights'
     typename Unit::Raw raw[RPL];
     const int rs = active ? rsub : P - 1;
-#pragma unroll
-    for (int u = 0; u < RPL; u++) {
+    auto issue = [&](int u) {
         const bool up = KIND == FX_SWIGLU && u >= HALF;
         const size_t r = row0 + (size_t)((up ? u - HALF : u) * P + rs);
         raw[u] = Unit::load(up ? fx.w2 : w, r < w.n_rows ? r : w.n_rows - 1, col);
-    }
+    };
+    constexpr int PF = PREFETCH_ROWS < RPL ? PREFETCH_ROWS : RPL;  // rows loaded ahead of the arithmetic
+#pragma unroll
+    for (int u = 0; u < PF; u++) issue(u);
     // Keep every load above ahead of any arithmetic on loaded data.
     __builtin_amdgcn_sched_barrier(0);
     // FX_NORM: rms_norm's scale from the whole row, while the weights load.
@@ -1233,11 +1267,16 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
         if (active) unit.init_q8(L, k, tv, col);
         __syncthreads();  // the fold below reuses the LDS
     }
+    if constexpr (!Q8 && HasPrepare<Unit>::value) unit.prepare();
     // Phase 3: per-unit addends of every (token, row) to LDS.
     float *part = reinterpret_cast<float *>(lds);
     const int ld = fold_ld(U);
 #pragma unroll
     for (int u = 0; u < RPL; u++) {
+        if constexpr (PF < RPL) {  // the next rows' loads go out before this row's arithmetic
+            if (u + PF < RPL) issue(u + PF);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         // Every lane computes and stores (idle lanes into a dummy row past
         // the tile), so no load is sunk into a guarded branch.
         float ad[TB];
