@@ -517,6 +517,29 @@ GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
     while (g.tb * 2 <= tbmax && (size_t)g.tb * 2 <= t_rows) g.tb *= 2;
     if (w.dtype == T_Q6_K) {
         g.rpl = 4;
+    } else if (g.tb == 1 && !q8 && !is_ternary_block(w.dtype)) {
+        // One token, EXACT (bound by its f32 arithmetic, so the work of the
+        // busiest CU decides): the rows per lane that give the busiest of the 256 CUs
+        // the least work, counted as blocks per CU x (rows per block + 8):
+        // a block's own cost (activation loads, the fold, launch) is about
+        // eight rows' worth.  On a tie, the fewest blocks.  This picks the
+        // best of 2..16 rows per lane in a sweep of eight decode shapes
+        // (Q4_0 11008x4096: 12, 8.4 us against 9.7 at 8; Q4_K 4096x4096:
+        // 4; Q8_0 4096x4096: 8; Q4_0 4096x14336: 16).  Q8, lighter on
+        // arithmetic and better with more waves, keeps the rule below (its
+        // best in the same sweep).
+        static const int opts[] = {2, 4, 8, 12, 16};
+        size_t best_cost = ~(size_t)0, best_blocks = 0;
+        for (int o : opts) {
+            if (gemv_lds_bytes(U, g.nt, o, 1, q8, w.n_cols) > LDS_MAX) continue;
+            const size_t rt = (size_t)P * o, blocks = (w.n_rows + rt - 1) / rt;
+            const size_t cost = (blocks + 255) / 256 * (rt + 8);
+            if (cost < best_cost || (cost == best_cost && blocks < best_blocks)) {
+                best_cost = cost;
+                best_blocks = blocks;
+                g.rpl = o;
+            }
+        }
     } else {
         const double pass = (double)P * U * unit_bytes(w.dtype) * (256.0 / g.nt);
         const double want = 36864.0 / pass;
