@@ -308,12 +308,14 @@ rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, s
     relayout_host(bytes, dw, host.data());
     auto alloc = std::make_shared<DevAlloc>();
     alloc->device = ctx->device;
-    hipError_t e = hipMalloc(&alloc->p, std::max<size_t>(total, 256));
+    const size_t pad = layout_pad_bytes(dw);  // rows a decode tile may read past the end (never folded)
+    hipError_t e = hipMalloc(&alloc->p, std::max<size_t>(total + pad, 256));
     if (e != hipSuccess) {
         alloc->p = nullptr;
         return fail(RCE_QMM_OUT_OF_MEMORY, std::string("weight hipMalloc: ") + hipGetErrorString(e));
     }
     HIP_TRY(hipMemcpyAsync(alloc->p, host.data(), total, hipMemcpyHostToDevice, ctx->stream));
+    if (pad) HIP_TRY(hipMemsetAsync(static_cast<uint8_t *>(alloc->p) + total, 0, pad, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     dw.base = static_cast<const uint8_t *>(alloc->p);
     if (dtype == T_I2_S) dw.aux = dw.base + dw.plane1;

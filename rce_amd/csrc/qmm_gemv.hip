@@ -303,6 +303,13 @@ size_t plan_layout(DevWeight &dw) {
     }
 }
 
+size_t layout_pad_bytes(const DevWeight &dw) {
+    const int U = units_per_row(dw.dtype, dw.n_cols);
+    const size_t rows = 16 * (size_t)(U > 0 && U < 1024 ? 1024 / U : 1);  // the most rows a tile can add
+    if (dw.layout == LAYOUT_IL64_Q6_K || dw.layout == LAYOUT_IL64_ROWS) return ((rows + 63) / 64 + 1) * dw.group_stride;
+    return rows * dw.row_stride;
+}
+
 void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
     const size_t n = dw.n_rows, k = dw.n_cols;
     switch (dw.layout) {

@@ -1200,7 +1200,8 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     // the in-order load counter), then every weight load of the thread.
     // No load sits in a branch (the compiler waits for a load made inside
     // a branch before the branch joins, which would serialize the rows):
-    // rows past the end, and idle lanes, load a valid row and are dropped.
+    // rows past the end read the allocation's zero padding
+    // (layout_pad_bytes) and idle lanes a valid row; neither is folded.
     QuantTask qt0, qt1;
     const int kq = (int)(k / 8);
     // Q8: the block's quantization tasks; FX_NORM: the tasks of the sum of
@@ -1221,7 +1222,7 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     auto issue = [&](int u) {
         const bool up = KIND == FX_SWIGLU && u >= HALF;
         const size_t r = row0 + (size_t)((up ? u - HALF : u) * P + rs);
-        raw[u] = Unit::load(up ? fx.w2 : w, r < w.n_rows ? r : w.n_rows - 1, col);
+        raw[u] = Unit::load(up ? fx.w2 : w, r, col);
     };
     constexpr int PF = PREFETCH_ROWS < RPL ? PREFETCH_ROWS : RPL;  // rows loaded ahead of the arithmetic
 #pragma unroll
@@ -1278,14 +1279,13 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
             __builtin_amdgcn_sched_barrier(0);
         }
         // Every lane computes and stores (idle lanes into a dummy row past
-        // the tile), so no load is sunk into a guarded branch.
+        // the tile), so no load is sunk into a guarded branch; rows past
+        // n_rows store sums the fold below never reads.
         float ad[TB];
         unit.addends(raw[u], ad);
         const int r = u * P + rsub;
-        const bool up = KIND == FX_SWIGLU && u >= HALF;
-        const bool in = row0 + (up ? r - RTO : r) < w.n_rows;
 #pragma unroll
-        for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = in ? ad[t] : 0.0f;
+        for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = ad[t];
     }
     __syncthreads();
     // Phase 4: the reference's fold, one thread per (token, output row).

@@ -239,6 +239,12 @@ bool gpu_supports(uint32_t dtype, size_t n_cols, int mode);
 // group_stride of `dw` (dtype, n_rows, n_cols already set) and
 // returns the device bytes it needs.
 size_t plan_layout(DevWeight &dw);
+// Zero bytes the allocation holds past the layout: a decode launch's last
+// block reads whole tiles of rows, up to 16 x (1024 / units per row) rows
+// (64-row groups for the interleaved layouts) past n_rows, instead of
+// clamping each row; those rows' sums are never folded.  Sub-views end
+// inside their parent, so the parent's padding covers them.
+size_t layout_pad_bytes(const DevWeight &dw);
 // GGUF bytes (row-major rows of blocks) -> the device layout of `dw`.
 void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst);
 
