@@ -155,6 +155,8 @@ def make_weight(seed, dt, n, k):
             b[:, 108:110] = d
         else:
             b[:, 0:2] = d
+        if int(dt) == 3:  # Q4_1's f16 min: finite, of the size of the values
+            b[:, 2:4] = rng.uniform(-0.03, 0.03, b.shape[0]).astype(np.float16).view(np.uint8).reshape(-1, 2)
         return b.reshape(-1)
     w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
     if int(dt) == 0:

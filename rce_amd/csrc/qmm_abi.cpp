@@ -55,7 +55,7 @@ bool block_geometry(uint32_t t, size_t &qk, size_t &bb) {
 
 // Every kernel family: decode kernels (EXACT, Q8) and the MFMA GEMM.
 bool supports_mode(uint32_t dtype, size_t n_cols, int mode) {
-    if (mode == RCE_QMM_MODE_F16_MFMA) return gemm_supports(dtype, n_cols);
+    if (mode == RCE_QMM_MODE_F16_MFMA) return gemm_supports(dtype, n_cols) || gemm_gen_supports(dtype, n_cols);
     return gpu_supports(dtype, n_cols, mode);
 }
 
@@ -92,7 +92,13 @@ rce_qmm_status run_gemm(const void *a_dev, bool a_f16, size_t t_rows, const DevW
         HIP_TRY(launch_f32_to_f16(static_cast<const float *>(a_dev), sc.a_f16, t_rows * dw.n_cols, s));
         a = sc.a_f16;
     }
-    HIP_TRY(launch_gemm_f16(dw, a, t_rows, out_dev, s));
+    if (gemm_supports(dw.dtype, dw.n_cols)) {
+        HIP_TRY(launch_gemm_f16(dw, a, t_rows, out_dev, s));
+    } else {
+        if (reinterpret_cast<uintptr_t>(a) % 16)
+            return fail(RCE_QMM_BAD_SHAPE, "F16 activations of the F16_MFMA GEMM must be 16-byte aligned");
+        HIP_TRY(launch_gemm_gen(dw, a, t_rows, out_dev, s));
+    }
     return RCE_QMM_OK;
 }
 

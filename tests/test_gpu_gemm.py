@@ -1,7 +1,9 @@
 """GPU parity of the prefill GEMM on the matrix cores (RCE_QMM_MODE_F16_MFMA).
 
-The mode dequantizes Q4_K / Q4_0 weights to binary16 tiles and contracts
-them with f16 MFMA, f32 accumulation.  Two checks per case:
+The mode dequantizes the weights to binary16 (Q4_K / Q4_0 in registers,
+gemm_f16.hip; Q8_0, Q5_K, Q6_K, Q5_0, Q4_1, F16 into LDS tiles,
+gemm_gen.hip) and contracts them with f16 MFMA, f32 accumulation.  Two
+checks per case:
   * against a numpy restatement of the same f16 weights (f64 products):
     only accumulation order differs, so normwise error must be ~1e-6 --
     this catches a wrong fragment layout, K order or scale;
@@ -120,4 +122,77 @@ def test_gemm_supports_matrix():
     assert rce_amd.supports(G.Q4K, 4096, Mode.F16_MFMA)
     assert rce_amd.supports(G.Q4_0, 4096, Mode.F16_MFMA)
     assert not rce_amd.supports(G.Q4_0, 4096 + 64, Mode.F16_MFMA)  # whole groups of 8 blocks
-    assert not rce_amd.supports(G.Q6K, 4096, Mode.F16_MFMA)
+    for dt in (G.Q6K, G.Q5K, G.Q8_0, G.Q5_0, G.Q4_1, G.F16):
+        assert rce_amd.supports(dt, 4096, Mode.F16_MFMA), dt
+    assert rce_amd.supports(G.Q8_0, 4096 + 64, Mode.F16_MFMA)
+    assert not rce_amd.supports(G.Q8_0, 4096 + 32, Mode.F16_MFMA)  # whole chunks of 64
+    assert not rce_amd.supports(G.Q6K, 4096 + 64, Mode.F16_MFMA)   # whole super-blocks
+    for dt in (G.F32, G.BF16, G.Q3K, G.Q1_0, G.Q2_0, G.I2S):       # beyond binary16's range / no form
+        assert not rce_amd.supports(dt, 4096, Mode.F16_MFMA), dt
+
+
+# ---- the other formats (gemm_gen.hip): every weight is the reference's f32
+# dequantized value (rce-ingest-gguf dequant.rs) rounded once to binary16, so
+# the restatement is the oracle's dequantize() rounded by numpy.
+
+def gen_weight_bytes(rng, dt, n, k):
+    from rand_blocks import float_bytes, rand_blocks
+    if dt == O.F16:
+        return float_bytes(rng, dt, n, k, 0.02)
+    if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks
+        return rand_blocks(rng, dt, n, k, dmax=0.02 / 8)
+    return O.quantize((rng.standard_normal((n, k)) * 0.02).astype(F32), dt)
+
+
+GEN_CASES = [
+    # (dtype, n_rows, n_cols, tokens): configs[2]'s shape for the three
+    # formats a Q4_K_M / Q5_K model's prefill needs besides Q4_K, then
+    # ragged M and N (partial tiles, N not a multiple of the 64-row IL64
+    # groups), chunk counts that are not multiples of the 3-deep load ring
+    (O.Q6_K, 4096, 4096, 512),
+    (O.Q8_0, 4096, 4096, 512),
+    (O.Q5_K, 4096, 4096, 512),
+    (O.Q6_K, 200, 2048, 33),
+    (O.Q8_0, 300, 576, 7),
+    (O.Q8_0, 64, 64, 1),
+    (O.Q5_K, 130, 512, 129),
+    (O.Q5_0, 256, 1024, 100),
+    (O.Q4_1, 192, 1088, 65),
+    (O.F16, 100, 640, 17),
+]
+
+
+@pytest.mark.parametrize("dt,n,k,t", GEN_CASES)
+def test_gemm_other_formats_parity(ctx, dt, n, k, t):
+    note(f"gemm-gen f16-mfma dtype={dt} n={n} k={k} t={t}")
+    rng = np.random.default_rng(7100 + dt + n + k + t)
+    b = gen_weight_bytes(rng, dt, n, k)
+    x = rng.standard_normal((t, k)).astype(F16)
+    xv = x.astype(np.float64)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = run_gemm(ctx, w, x, G.F16)
+    wf = O.dequantize(b, dt, n * k).reshape(n, k).astype(F16).astype(np.float64)
+    assert np.all(np.isfinite(wf))
+    assert normwise(got, xv @ wf.T) < 1e-5, "kernel differs from the f16-weight restatement"
+    ref = O.mm_batched(x.astype(F32), b, dt, n, k)
+    assert normwise(got, ref) < 2e-3
+    again = run_gemm(ctx, w, x, G.F16)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not run-to-run deterministic"
+    w.close()
+
+
+@pytest.mark.parametrize("dt", [O.Q6_K, O.Q8_0])
+def test_gemm_other_formats_f32_activations(ctx, dt):
+    """F32 activations are rounded to binary16 first (the library's
+    conversion kernel); the result equals the F16 call on those values."""
+    n, k, t = 192, 1024, 40
+    note(f"gemm-gen f32 activations dtype={dt}")
+    rng = np.random.default_rng(7200 + dt)
+    b = gen_weight_bytes(rng, dt, n, k)
+    x = rng.standard_normal((t, k)).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got32 = run_gemm(ctx, w, x, G.F32)
+    got16 = run_gemm(ctx, w, x.astype(F16), G.F16)
+    assert np.array_equal(got32.view(np.uint32), got16.view(np.uint32))
+    assert normwise(got32, O.mm_batched(x, b, dt, n, k)) < 2e-3
+    w.close()
