@@ -371,8 +371,8 @@ def cpu_leg(line, head, rows, budget_s=10.0):
         return float(f"{np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(want)):.3g}")
 
     per = line["per_format"]
-    if "gemm" in rows:
-        g = rows["gemm"]
+    for gk in [r for r in rows if r.startswith("gemm")]:
+        g = rows[gk]
         per[g["key"]]["normwise_err_vs_oracle"] = normwise(g["got"], O.mm_batched(g["x"], g["b"], g["dt"], g["n"], g["k"]))
     if "moe" in rows:
         m = rows["moe"]
@@ -575,13 +575,14 @@ def main():
                 key = f"{name} {m.name.lower()}"
                 per[key] = {"us": round(sms * 1e3, 2), "GB/s": round(sg, 1), "hbm_frac": round(sg / HBM_PEAK_GBS, 4)}
                 log(f"  {key}: {sms * 1e3:.2f} us  {sg:.0f} GB/s ({sg / HBM_PEAK_GBS:.1%})")
-    if "gemm" in rows:  # configs[2]: Q4_K prefill GEMM 512x4096x4096 on f16 MFMA
-        gms, gs = time_gemm(hip, ctx, G.Q4K, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
-        gtf = 2.0 * 512 * 4096 * 4096 / (gms * 1e-3) / 1e12
-        key = "Q4_K GEMM 512x4096x4096 f16_mfma"
-        per[key] = {"us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4)}
-        kept["gemm"] = dict(gs, key=key)
-        log(f"  {key}: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of f16 MFMA peak)")
+    if "gemm" in rows:  # configs[2]: Q4_K prefill GEMM 512x4096x4096 on f16 MFMA, then the other formats
+        for gdt in (G.Q4K, G.Q6K, G.Q8_0, G.Q5K):
+            gms, gs = time_gemm(hip, ctx, gdt, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
+            gtf = 2.0 * 512 * 4096 * 4096 / (gms * 1e-3) / 1e12
+            key = f"{G(gdt).name.replace('Q4K', 'Q4_K').replace('Q5K', 'Q5_K').replace('Q6K', 'Q6_K')} GEMM 512x4096x4096 f16_mfma"
+            per[key] = {"us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4)}
+            kept[f"gemm {int(gdt)}"] = dict(gs, key=key)
+            log(f"  {key}: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of f16 MFMA peak)")
     if "moe" in rows:  # configs[3]: grouped MoE, 8 Q4_0 experts, 256 tokens, top-2
         mms, mbytes, msample = time_moe(hip, ctx, 5, 2, 400, Mode.F16_MFMA)
         mtf = 120259084288 / (mms * 1e-3) / 1e12

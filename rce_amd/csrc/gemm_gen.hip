@@ -37,9 +37,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128, BN = 64, KC = 64, NT = 512;
+#ifndef GEN_DEPTH
+#define GEN_DEPTH 6
+#endif
+#ifndef GEN_CPB
+#define GEN_CPB 2
+#endif
+constexpr int DEPTH = GEN_DEPTH;  // register sets of chunk loads in flight
+constexpr int CPB = GEN_CPB;      // chunks per barrier
+constexpr int NBUF = 2 * CPB;     // LDS chunk buffers
+static_assert(DEPTH % CPB == 0 && DEPTH >= 2 * CPB, "load ring");
 constexpr int A_TILE = BM * KC * 2;               // 16 KB
 constexpr int B_TILE = BN * KC * 2;               // 8 KB
-constexpr int LDS_BYTES = 2 * (A_TILE + B_TILE);  // double-buffered: 48 KB
+constexpr int LDS_BYTES = 2 * GEN_CPB * (A_TILE + B_TILE);  // NBUF chunk buffers
 static_assert(4 * 2 * 4 * 64 * 16 <= LDS_BYTES, "the k-half partial sums reuse the tiles' LDS");
 
 __host__ __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
@@ -276,7 +286,7 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w, const _Float16 *__
     const int wn = tid >> 3, wo = tid & 7;
     const size_t wrow = F::IL64 || n0 + wn < N ? n0 + wn : N - 1;
     const int a_st0 = ar * 128 + 16 * (ap ^ swz(ar)), a_st1 = a_st0 + 64 * 128;
-    const int b_st = 2 * A_TILE + wn * 128 + 16 * (wo ^ swz(wn));
+    const int b_st = NBUF * A_TILE + wn * 128 + 16 * (wo ^ swz(wn));
 
     auto load = [&](Stage<F> &s, int c) {
         s.a0 = ld<u32x4>(reinterpret_cast<const uint8_t *>(ag0 + (size_t)c * KC));
@@ -303,7 +313,7 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w, const _Float16 *__
             a_rd[b][j] = r * 128 + 16 * (g ^ swz(r));
         }
         const int r = 32 * ch + l32;
-        b_rd[j] = 2 * A_TILE + r * 128 + 16 * (g ^ swz(r));
+        b_rd[j] = NBUF * A_TILE + r * 128 + 16 * (g ^ swz(r));
     }
     f32x16 acc0 = {}, acc1 = {};
     auto mma = [&](int buf) {
@@ -318,25 +328,45 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w, const _Float16 *__
     };
 
     // At the top of iteration c, LDS buffer c % 2 holds chunk c (after the
-    // barrier) and registers hold chunks c + 1 and c + 2.  Iteration c loads
-    // chunk c + 3 into the register set chunk c used, multiplies chunk c and
-    // stores chunk c + 1 into the other buffer (read last in iteration c - 1,
-    // which every wave has left at this barrier).
-    Stage<F> s0, s1, s2;
-    load(s0, 0);
-    if (nchunks > 1) load(s1, 1);
-    if (nchunks > 2) load(s2, 2);
-    store(s0, 0, 0);
-    auto step = [&](Stage<F> &ld_set, const Stage<F> &st_set, int c) {
-        __syncthreads();
-        if (c + 3 < nchunks) load(ld_set, c + 3);
-        mma(c & 1);
-        if (c + 1 < nchunks) store(st_set, c + 1, (c + 1) & 1);
-    };
-    for (int c = 0; c < nchunks; c += 3) {
-        step(s0, s1, c);
-        if (c + 1 < nchunks) step(s1, s2, c + 1);
-        if (c + 2 < nchunks) step(s2, s0, c + 2);
+    // barrier) and registers hold chunks c + 1 .. c + DEPTH - 1.  Iteration c
+    // loads chunk c + DEPTH into the register set chunk c used, multiplies
+    // chunk c and stores chunk c + 1 into the other buffer (read last in
+    // iteration c - 1, which every wave has left at this barrier).
+    // The main loop runs whole trips of DEPTH chunks with no branch, so the
+    // compiler's wait for a register set's loads counts only the loads
+    // issued after it (a loop with conditional loads waits for all of them);
+    // loads past the last chunk reload it.  At most DEPTH chunks remain.
+    const int last = nchunks - 1;
+    Stage<F> st[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; u++) load(st[u], u < last ? u : last);
+#pragma unroll
+    for (int v = 0; v < CPB; v++)
+        if (v < nchunks) store(st[v], v, v);
+    int c = 0;
+    for (; c + DEPTH + CPB <= nchunks; c += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u += CPB) {
+            __syncthreads();
+#pragma unroll
+            for (int v = 0; v < CPB; v++) load(st[u + v], c + u + v + DEPTH < last ? c + u + v + DEPTH : last);
+#pragma unroll
+            for (int v = 0; v < CPB; v++) mma((c + u + v) % NBUF);
+#pragma unroll
+            for (int v = 0; v < CPB; v++) store(st[(u + v + CPB) % DEPTH], c + u + v + CPB, (c + u + v + CPB) % NBUF);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < DEPTH + CPB; u += CPB) {
+        if (c + u < nchunks) {
+            __syncthreads();
+#pragma unroll
+            for (int v = 0; v < CPB; v++)
+                if (c + u + v < nchunks) mma((c + u + v) % NBUF);
+#pragma unroll
+            for (int v = 0; v < CPB; v++)
+                if (c + u + v + CPB < nchunks) store(st[(u + v + CPB) % DEPTH], c + u + v + CPB, (c + u + v + CPB) % NBUF);
+        }
     }
     __syncthreads();  // every fragment read done: the partial sums reuse LDS
 
