@@ -14,7 +14,12 @@
  *                          order (one binary32 rounding per op, no fused
  *                          multiply-add in the reference's arithmetic).
  *                          Bit-identical to rce_op_qmm::mm_1d / mm_batched
- *                          for finite inputs.
+ *                          for activations of magnitude below 2^123 (the
+ *                          forms (q - c) * a of Q4_0 / Q5_0 / Q3_K are one
+ *                          fma of q, a and -c * a, which overflows before
+ *                          the reference's product does); larger or
+ *                          non-finite activations can give another
+ *                          overflow or NaN pattern.
  *   RCE_QMM_MODE_Q8        activations quantized once per row to Q8 blocks
  *                          of 32 (nn.rs quantize_block semantics), exact
  *                          int32 block dot products, then the reference's
@@ -22,7 +27,8 @@
  *                          differs from EXACT by the activation rounding.
  *   RCE_QMM_MODE_F16_MFMA  (matmul / grouped experts) weights dequantized to
  *                          binary16 tiles and contracted on the matrix cores
- *                          with f32 accumulation in a fixed order.
+ *                          with f32 accumulation in a fixed order; within
+ *                          2e-3 normwise of mm_batched.
  * Every mode is run-to-run bit-identical: no floating-point atomics, fixed
  * reduction trees.
  *
@@ -195,7 +201,10 @@ rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, size_t n_rows,
  * the reference's callers do), out_dev [t_rows, n_rows] f32.  No host
  * synchronization; the library's scratch is owned by the context, so calls
  * on one context must not overlap on different streams (one context per
- * stream). */
+ * stream).  RCE_QMM_MODE_F16_MFMA (the prefill form) takes Q4_K / Q4_0 /
+ * Q5_K / Q6_K with n_cols a multiple of 256 and Q8_0 / Q5_0 / Q4_1 / F16 with
+ * n_cols a multiple of 64 (rce_qmm_supports); its F16 activations must be
+ * 16-byte aligned. */
 rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype,
                                       size_t t_rows, const rce_qmm_weight *w, float *out_dev,
                                       rce_qmm_mode mode, void *stream);

@@ -92,11 +92,11 @@ rce_qmm_status run_gemm(const void *a_dev, bool a_f16, size_t t_rows, const DevW
         HIP_TRY(launch_f32_to_f16(static_cast<const float *>(a_dev), sc.a_f16, t_rows * dw.n_cols, s));
         a = sc.a_f16;
     }
+    if (reinterpret_cast<uintptr_t>(a) % 16)
+        return fail(RCE_QMM_BAD_SHAPE, "F16 activations of the F16_MFMA GEMM must be 16-byte aligned");
     if (gemm_supports(dw.dtype, dw.n_cols)) {
         HIP_TRY(launch_gemm_f16(dw, a, t_rows, out_dev, s));
     } else {
-        if (reinterpret_cast<uintptr_t>(a) % 16)
-            return fail(RCE_QMM_BAD_SHAPE, "F16 activations of the F16_MFMA GEMM must be 16-byte aligned");
         HIP_TRY(launch_gemm_gen(dw, a, t_rows, out_dev, s));
     }
     return RCE_QMM_OK;

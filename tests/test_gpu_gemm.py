@@ -196,3 +196,18 @@ def test_gemm_other_formats_f32_activations(ctx, dt):
     assert np.array_equal(got32.view(np.uint32), got16.view(np.uint32))
     assert normwise(got32, O.mm_batched(x, b, dt, n, k)) < 2e-3
     w.close()
+
+
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q8_0])
+def test_gemm_misaligned_f16_activations_rejected(ctx, dt):
+    """The GEMM reads activations 16 bytes per lane: an F16 pointer off a
+    16-byte boundary is refused on the host before any launch."""
+    n, k, t = 64, 256, 4
+    rng = np.random.default_rng(7300 + dt)
+    b = O.quantize((rng.standard_normal((n, k)) * 0.02).astype(F32), dt)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    xa = rce_amd.DeviceBuffer(ctx, 2 * t * k + 16)
+    out = rce_amd.DeviceBuffer(ctx, 4 * t * n)
+    with pytest.raises(rce_amd.QmmError, match="16-byte aligned"):
+        rce_amd.mm_batched_dev(ctx, xa.ptr + 2, G.F16, t, w, out.ptr, Mode.F16_MFMA)
+    xa.free(); out.free(); w.close()
