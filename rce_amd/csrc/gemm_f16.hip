@@ -3,11 +3,14 @@
 // Q4_K or Q4_0 blocks, dequantized to binary16 MFMA fragments in registers
 // and contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
 //
-// Tiling.  A block owns a BM x BN (M x N) output tile of 8192 outputs:
-// 128 x 64 or 64 x 128 (Tile<BM>), so a 512 x 4096 product is 256 tiles,
-// one per CU.  The 64 x 128 tile moves a third less data into LDS per flop
-// (8 KB of activations + 4.5 KB of weights per chunk instead of 16 + 2.25)
-// and has no empty rows when an expert of the grouped mode gets 64 tokens.
+// Tiling.  A block owns a BM x BN (M x N) output tile: 128 x 64 or 64 x 128
+// (8192 outputs), so a 512 x 4096 product is 256 tiles, one per CU; or
+// 96 x 128 for the grouped mode when experts get about 64 rows each (65-96
+// rows in one tile instead of a 64-row tile and a mostly empty second one:
+// the configs[3] MoE's W2 then needs one round of tiles over the CUs, not
+// two).  The 64 x 128 tile moves a third less data into LDS per flop than
+// 128 x 64 (8 KB of activations + 4.5 KB of weights per chunk instead of
+// 16 + 2.25).
 // K runs in chunks of 64 (four MFMA k-steps of 16).  The block has ten waves:
 //   * eight compute waves: wave w = 2*kq + t computes k-step kq of every
 //     chunk for the BM x BN/2 sub-tile of columns BN/2 * t.. (RB x CB MFMA
@@ -87,12 +90,13 @@ static_assert(4 * GA >= NS + 2, "W groups loaded too late for the stage depth");
 static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 static_assert(NS >= 3, "stage ring");
 
-// Output tile BM x BN with BM * BN = 8192: 128 x 64 or 64 x 128.  Compute
-// wave w = 2*kq + t holds RB x CB MFMA blocks of 32 x 32 (rows 32*rb,
-// columns BN/2 * t + 32*cb): four MFMAs per chunk either way.
+// Output tile BM x BN: 128 x 64, 64 x 128, or 96 x 128 (grouped experts of
+// 65-96 rows, in one row tile instead of a 64-row tile and a mostly empty
+// second one).  Compute wave w = 2*kq + t holds RB x CB MFMA blocks of
+// 32 x 32 (rows 32*rb, columns BN/2 * t + 32*cb).
 template <int BM_>
 struct Tile {
-    static constexpr int BM = BM_, BN = 8192 / BM_;
+    static constexpr int BM = BM_, BN = BM_ == 96 ? 128 : 8192 / BM_;
     static constexpr int RB = BM / 32, CB = BN / 64;
     static constexpr int A_STAGE = BM * KC * 2;           // 16 KB / 8 KB
     static constexpr int A_LOADS = BM / 16;               // per producer per chunk (1 KB each)
@@ -103,10 +107,13 @@ struct Tile {
     static constexpr int OFF_W = NS * A_STAGE;
     static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
     static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
-    static constexpr int RED_LDS = 8 * RB * CB * 16 * 64 * 4;  // partial sums of every wave
+    // the partial sums of every wave for one column block cb at a time
+    static constexpr int RED_LDS = 8 * RB * 16 * 64 * 4;
     static constexpr int LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
     static_assert(LDS + BM * 4 <= 160 * 1024, "LDS budget");
-    static_assert(RB * CB == 4, "four MFMA blocks per compute wave; eight output blocks, one finished per wave");
+    static_assert(RB >= 2 && RB <= 4 && CB >= 1 && CB <= 2 && 2 * RB <= 8,
+                  "2 to 4 row blocks (the dequantization is spread over the first two), 1 or 2 column blocks "
+                  "per compute wave; a column block's 2 RB output blocks finished by as many waves");
     // Producer loads of iteration `it`, in order: the W loads of position
     // it % 4 (row halves at position 0, headers at 1), then the A loads of
     // chunk it + NS - 1.
@@ -178,6 +185,13 @@ __device__ __forceinline__ u32x4 lds_read16(uint32_t a) {
     static_assert(OFF >= 0 && OFF < 65536, "ds offset");
     u32x4 v;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read4(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
 }
 template <int OFF>
@@ -463,7 +477,11 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         }
         __builtin_amdgcn_s_waitcnt(0);  // drain the padding loads before LDS is reused
         __syncthreads();                 // barrier E1
-        __syncthreads();                 // barrier E2
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {  // the compute waves' epilogue barriers, one by one
+            if (cb > 0) __syncthreads();
+            __syncthreads();  // barrier E2
+        }
         return;
     }
 
@@ -490,20 +508,20 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     auto read_a = [&](half8 *a, uint32_t addr) {
         a[0] = lds_read_frag<0>(addr);
         if constexpr (RB > 1) a[1] = lds_read_frag<4096>(addr);
-        if constexpr (RB > 2) {
-            a[2] = lds_read_frag<8192>(addr);
-            a[3] = lds_read_frag<12288>(addr);
-        }
+        if constexpr (RB > 2) a[2] = lds_read_frag<8192>(addr);
+        if constexpr (RB > 3) a[3] = lds_read_frag<12288>(addr);
     };
     auto read_w = [&](u32x2 *r, uint32_t addr) {
         r[0] = lds_read8<0>(addr);
         if constexpr (CB > 1) r[1] = lds_read8<2048>(addr);
     };
-    auto read_sc = [&](u32x4 *v, uint32_t addr) {
-        v[0] = lds_read16<0>(addr);
-        if constexpr (CB > 1) v[1] = lds_read16<1024>(addr);
+    // one chunk's {scale, bias} per column block (a register each, not the
+    // group's four: the 96-row tile's accumulators need the room)
+    auto read_sb = [&](uint32_t *v, uint32_t addr) {
+        v[0] = lds_read4<0>(addr);
+        if constexpr (CB > 1) v[1] = lds_read4<1024>(addr);
     };
-    auto wait_reads = [&](half8 *a, u32x2 *r, u32x4 *v) {
+    auto wait_reads = [&](half8 *a, u32x2 *r, uint32_t *v) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int i = 0; i < RB; i++) pin(a[i]);
@@ -518,21 +536,26 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     __builtin_amdgcn_s_barrier();  // barrier P2: chunk 0 dequantized, chunk 1's nibbles read
     half8 a_cur[RB], b_cur[CB];
     u32x2 raw_nxt[CB];
-    u32x4 sc_cur[CB];
+    uint32_t sb_nxt[CB];  // {scale, bias} of chunk c+1
     {
         u32x2 raw0[CB];
+        uint32_t sb0[CB];
         read_a(a_cur, a_rd);
         read_w(raw0, w_rd[0]);
         read_w(raw_nxt, w_rd[1]);
-        read_sc(sc_cur, sc_rd);
-        wait_reads(a_cur, raw0, sc_cur);
+        read_sb(sb0, sc_rd);
+        read_sb(sb_nxt, sc_rd + 4);
+        wait_reads(a_cur, raw0, sb0);
 #pragma unroll
-        for (int cb = 0; cb < CB; cb++) pin(raw_nxt[cb]);
+        for (int cb = 0; cb < CB; cb++) {
+            pin(raw_nxt[cb]);
+            pin(sb_nxt[cb]);
+        }
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
             half2v h0, h1, h2, h3;
-            dequant4(nib(raw0[cb].x), sc_cur[cb].x, h0, h1);
-            dequant4(nib(raw0[cb].y), sc_cur[cb].x, h2, h3);
+            dequant4(nib(raw0[cb].x), sb0[cb], h0, h1);
+            dequant4(nib(raw0[cb].y), sb0[cb], h2, h3);
             b_cur[cb] = join8(h0, h1, h2, h3);
         }
     }
@@ -544,33 +567,31 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         // nibble reads of chunk c+2 (steps 0, 1: this group; 2, 3: the next)
         const uint32_t wb_cur = (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
         const uint32_t wb_nxt = (uint32_t)(((g + 1) & (NWBUF - 1)) * W_GROUP);
+        const uint32_t sc_cur_rd = sc_rd + (uint32_t)((g & 1) * SC_BUF);
         const uint32_t sc_nxt_rd = sc_rd + (uint32_t)(((g + 1) & 1) * SC_BUF);
-        u32x4 sc_nxt[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) sc_nxt[cb] = sc_cur[cb];
         auto step = [&](auto uc) {
             constexpr int u = decltype(uc)::value;
             // chunk c+1's A and W are in LDS (the producers waited for them);
             // every wave is done with the reads of chunk c
             __builtin_amdgcn_s_barrier();
-            // LDS reads: A fragments of chunk c+1, nibbles of chunk c+2; at
-            // u = 2 the next group's scales (written by the producers at u = 1)
+            // LDS reads: A fragments of chunk c+1, nibbles and {scale,
+            // bias} of chunk c+2 (from u = 2 on: the next group's, whose
+            // scales the producers wrote at u = 1)
             const uint32_t sa = a_rd + (uint32_t)(st1 * A_STAGE);
             st1 = st1 == NS - 1 ? 0 : st1 + 1;
             half8 a_nxt[RB];
             u32x2 raw_nn[CB];
+            uint32_t sb_nn[CB];
             read_a(a_nxt, sa);
             read_w(raw_nn, w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
-            if constexpr (u == 2) read_sc(sc_nxt, sc_nxt_rd);
+            read_sb(sb_nn, (u >= 2 ? sc_nxt_rd : sc_cur_rd) + (uint32_t)(4 * ((u + 2) & 3)));
             __builtin_amdgcn_sched_barrier(0);
             // Chunk c's MFMAs and chunk c+1's dequantization (the next
             // group's first chunk for u = 3), independent of each other.
-            constexpr int q1 = (u + 1) & 3;
             half2v hq[CB][4];
 #pragma unroll
             for (int cb = 0; cb < CB; cb++) {
-                const u32x4 &sv = (u == 3) ? sc_nxt[cb] : sc_cur[cb];
-                const uint32_t sb = q1 == 0 ? sv.x : q1 == 1 ? sv.y : q1 == 2 ? sv.z : sv.w;
+                const uint32_t sb = sb_nxt[cb];
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++) {
                     acc[rb * CB + cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[rb], b_cur[cb], acc[rb * CB + cb], 0, 0, 0);
@@ -579,59 +600,64 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            wait_reads(a_nxt, raw_nn, sc_nxt);
+            wait_reads(a_nxt, raw_nn, sb_nn);
 #pragma unroll
             for (int i = 0; i < RB; i++) a_cur[i] = a_nxt[i];
 #pragma unroll
             for (int cb = 0; cb < CB; cb++) {
                 b_cur[cb] = join8(hq[cb][0], hq[cb][1], hq[cb][2], hq[cb][3]);
                 raw_nxt[cb] = raw_nn[cb];
+                sb_nxt[cb] = sb_nn[cb];
             }
         };
         step(ic<0>{});
         step(ic<1>{});
         step(ic<2>{});
         step(ic<3>{});
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) sc_cur[cb] = sc_nxt[cb];
     }
     __syncthreads();  // barrier E1: the producers have drained their loads
 
-    // Partial sums to LDS: element r of acc[i] in lane l is row
-    // 8(r/4) + 4(l/32) + r%4, column l%32 of that 32 x 32 block.  Layout
-    // [wave][block][r/4][lane][r%4] (conflict-free 16-byte accesses).
+    // Partial sums to LDS, one column block cb at a time: element r of
+    // acc[rb * CB + cb] in lane l is row 8(r/4) + 4(l/32) + r%4, column l%32
+    // of that 32 x 32 block.  Layout [wave][rb][r/4][lane][r%4]
+    // (conflict-free 16-byte accesses).  Wave w < 2 RB then finishes output
+    // block (row block w / 2, column half w % 2) of column block cb: the
+    // partials of the waves 2*kq + ot, k-steps 0, 1, 2, 3 added in order.
     f32x4 *red = reinterpret_cast<f32x4 *>(lds);
 #pragma unroll
-    for (int i = 0; i < RB * CB; i++)
+    for (int cb = 0; cb < CB; cb++) {
+        if (cb > 0) __syncthreads();  // the previous column block's partials are read
 #pragma unroll
-        for (int rq = 0; rq < 4; rq++) {
-            const f32x4 v = {acc[i][4 * rq], acc[i][4 * rq + 1], acc[i][4 * rq + 2], acc[i][4 * rq + 3]};
-            red[((wave * 4 + i) * 4 + rq) * 64 + lane] = v;
-        }
-    __syncthreads();  // barrier E2
-    // Wave w finishes output block w (row block w / 2CB, column block
-    // w % 2CB, i.e. column half ot, block ocb of that half): the partials of
-    // the waves 2*kq + ot, k-steps 0, 1, 2, 3 added in order.
-    const int orb = wave / (2 * CB), occ = wave % (2 * CB), ot = occ / CB, ocb = occ % CB;
-    const int oi = orb * CB + ocb;
-    const size_t col = n0 + (size_t)(BN / 2 * ot + 32 * ocb + l32);
+        for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-    for (int rq = 0; rq < 4; rq++) {
-        f32x4 sum = red[((ot * 4 + oi) * 4 + rq) * 64 + lane];
+            for (int rq = 0; rq < 4; rq++) {
+                const f32x16 &a = acc[rb * CB + cb];
+                const f32x4 v = {a[4 * rq], a[4 * rq + 1], a[4 * rq + 2], a[4 * rq + 3]};
+                red[((wave * RB + rb) * 4 + rq) * 64 + lane] = v;
+            }
+        __syncthreads();  // barrier E2
+        if (wave < 2 * RB) {
+            const int orb = wave >> 1, ot = wave & 1;
+            const size_t col = n0 + (size_t)(BN / 2 * ot + 32 * cb + l32);
 #pragma unroll
-        for (int k2 = 1; k2 < 4; k2++) sum += red[(((2 * k2 + ot) * 4 + oi) * 4 + rq) * 64 + lane];
+            for (int rq = 0; rq < 4; rq++) {
+                f32x4 sum = red[((ot * RB + orb) * 4 + rq) * 64 + lane];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int m = 32 * orb + 8 * rq + 4 * h + e;
-            if (m < rows && col < N) {
-                const size_t o = (m0 + m) * N + col;
-                if constexpr (EPI == GEPI_F32) {
-                    static_cast<float *>(out_v)[o] = sum[e];
-                } else if constexpr (EPI == GEPI_SILU_F16) {  // rce-qwen36-moe/src/lib.rs L459-461
-                    static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_ref(sum[e]);
-                } else {  // silu(g) * u, rce-qwen36-moe/src/lib.rs L667-676
-                    const float hv = silu_ref(aux[o]) * sum[e];
-                    static_cast<_Float16 *>(out_v)[o] = (_Float16)hv;
+                for (int k2 = 1; k2 < 4; k2++) sum += red[(((2 * k2 + ot) * RB + orb) * 4 + rq) * 64 + lane];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int m = 32 * orb + 8 * rq + 4 * h + e;
+                    if (m < rows && col < N) {
+                        const size_t o = (m0 + m) * N + col;
+                        if constexpr (EPI == GEPI_F32) {
+                            static_cast<float *>(out_v)[o] = sum[e];
+                        } else if constexpr (EPI == GEPI_SILU_F16) {  // rce-qwen36-moe/src/lib.rs L459-461
+                            static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_ref(sum[e]);
+                        } else {  // silu(g) * u, rce-qwen36-moe/src/lib.rs L667-676
+                            const float hv = silu_ref(aux[o]) * sum[e];
+                            static_cast<_Float16 *>(out_v)[o] = (_Float16)hv;
+                        }
+                    }
                 }
             }
         }
@@ -715,7 +741,14 @@ hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t 
     return hipGetLastError();
 }
 
-int gemm_tile_rows(size_t rows_hint) { return rows_hint <= 96 ? 64 : 128; }
+int gemm_tile_rows(size_t rows_hint, bool grouped) {
+    // plain: the fewest rows that hold M (96 for 65..96);
+    // grouped: experts' rows scatter around the mean (about +-8 for 64), so
+    // a mean of 49..80 takes 96-row tiles: one tile per expert, not a
+    // 64-row tile and a mostly empty second one
+    if (grouped) return rows_hint <= 48 ? 64 : (rows_hint <= 80 ? 96 : 128);
+    return rows_hint <= 64 ? 64 : (rows_hint <= 96 ? 96 : 128);
+}
 
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
@@ -729,6 +762,9 @@ hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, co
     if (bm == 64)
         return q4k ? launch_grouped_epi<Q4K, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
                    : launch_grouped_epi<Q40, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    if (bm == 96)
+        return q4k ? launch_grouped_epi<Q4K, 96>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
+                   : launch_grouped_epi<Q40, 96>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     if (bm == 128)
         return q4k ? launch_grouped_epi<Q4K, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
                    : launch_grouped_epi<Q40, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux,
@@ -744,8 +780,9 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
     const bool q4k = w.dtype == T_Q4_K;
     if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
-    if (bm == 0) bm = gemm_tile_rows(M);
+    if (bm == 0) bm = gemm_tile_rows(M, false);
     if (bm == 64) return q4k ? launch_fmt<Q4K, 64>(w, a, M, out, s) : launch_fmt<Q40, 64>(w, a, M, out, s);
+    if (bm == 96) return q4k ? launch_fmt<Q4K, 96>(w, a, M, out, s) : launch_fmt<Q40, 96>(w, a, M, out, s);
     if (bm == 128) return q4k ? launch_fmt<Q4K, 128>(w, a, M, out, s) : launch_fmt<Q40, 128>(w, a, M, out, s);
     return hipErrorInvalidValue;
 }

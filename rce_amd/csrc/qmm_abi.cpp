@@ -486,7 +486,11 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
                 return fail(RCE_QMM_BAD_SHAPE, "up matrices must match the gate matrices in dtype and shape");
         }
     }
-    if (!supports_mode(a1.dtype, d_model, (int)mode) || !supports_mode(a2.dtype, d_ff, (int)mode))
+    // the grouped GEMM (F16_MFMA) has the Q4_K / Q4_0 forms only
+    auto experts_ok = [&](uint32_t dt, size_t k) {
+        return mode == RCE_QMM_MODE_F16_MFMA ? gemm_supports(dt, k) : supports_mode(dt, k, (int)mode);
+    };
+    if (!experts_ok(a1.dtype, d_model) || !experts_ok(a2.dtype, d_ff))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "the experts' dtype/shape has no GPU kernel in mode " +
                                                    std::to_string((int)mode));
     if (t_rows == 0) return RCE_QMM_OK;
@@ -498,7 +502,7 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
     const size_t n_pairs = t_rows * top_k;
     if (n_pairs >= (size_t)1 << 30) return fail(RCE_QMM_BAD_SHAPE, "too many (token, decision) pairs");
     // tile rows of the grouped GEMM for the average rows per expert
-    const int bm = gemm_tile_rows((n_pairs + n_expert - 1) / n_expert);
+    const int bm = gemm_tile_rows((n_pairs + n_expert - 1) / n_expert, true);
     const int max_tiles = (int)(n_pairs / bm + n_expert);
     const size_t meta_ints = (n_expert + 1) + 2 * n_pairs + 2;
     const size_t meta_bytes = align_up(meta_ints * 4, 16) + (size_t)max_tiles * sizeof(MoeTile);

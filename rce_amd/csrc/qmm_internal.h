@@ -298,7 +298,8 @@ hipError_t launch_gemv_ternary(const DevWeight &w, const GemvGeom &g, const floa
 // Prefill GEMM on the matrix cores (gemm_f16.hip): out[M, n_rows] =
 // A[M, n_cols] . W^T, A binary16, W dequantized to binary16 tiles.
 bool gemm_supports(uint32_t dtype, size_t n_cols);
-// bm: output tile rows, 64 (tile 64 x 128) or 128 (128 x 64); 0 = by M.
+// bm: output tile rows, 64 (tile 64 x 128), 96 (96 x 128) or 128 (128 x 64);
+// 0 = by M.
 hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s, int bm = 0);
 // The other formats' prefill GEMM (gemm_gen.hip): Q8_0, Q5_0, Q4_1, F16 (K
 // a multiple of 64), Q5_K, Q6_K (K a multiple of 256); nibble_forms also
@@ -307,9 +308,9 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
 bool gemm_gen_supports(uint32_t dtype, size_t n_cols);
 hipError_t launch_gemm_gen(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s,
                            bool nibble_forms = false);
-// The tile rows the GEMM uses for about `rows_hint` rows per tile column
-// (the grouped mode: rows per expert).
-int gemm_tile_rows(size_t rows_hint);
+// The tile rows the GEMM uses for M = rows_hint (plain) or for a mean of
+// rows_hint rows per expert (grouped).
+int gemm_tile_rows(size_t rows_hint, bool grouped);
 // f32 activations -> binary16 (round to nearest even) for the GEMM.
 hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t s);
 

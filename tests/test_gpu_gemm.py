@@ -93,6 +93,9 @@ CASES = [
     (O.Q4_0, 1024, 4096, 64),
     (O.Q4_0, 300, 512, 7),
     (O.Q4_0, 64, 14336, 5),
+    # 65..96 rows: the 96 x 128 tile (RB = 3: three row blocks per wave)
+    (O.Q4_K, 300, 1024, 80),
+    (O.Q4_0, 256, 2048, 96),
 ]
 
 

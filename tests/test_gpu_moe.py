@@ -181,3 +181,20 @@ def test_moe_swiglu(ctx, mode, tol, E, dm, dff, t, k, dt):
     got = run_swiglu(ctx, gb, ub, db, dt, dm, dff, x, ids, gw, mode)
     ref = O.moe_swiglu_ffn(x, gb, ub, db, dt, dff, ids, gw)
     assert normwise(got, ref) < tol
+
+
+def test_moe_f16_mfma_declines_formats_without_a_grouped_form(ctx):
+    """The grouped GEMM has the Q4_K / Q4_0 forms only: Q8_0 experts in
+    F16_MFMA are refused on the host (no launch), while EXACT takes them."""
+    E, dm, dff, T, K = 2, 256, 512, 4, 1
+    rng = np.random.default_rng(77)
+    w1 = [O.quantize((rng.standard_normal((dff, dm)) * 0.05).astype(np.float32), O.Q8_0) for _ in range(E)]
+    w2 = [O.quantize((rng.standard_normal((dm, dff)) * 0.05).astype(np.float32), O.Q8_0) for _ in range(E)]
+    x = rng.standard_normal((T, dm)).astype(np.float32)
+    ids = np.zeros((T, K), np.int32)
+    gw = np.ones((T, K), np.float32)
+    with pytest.raises(rce_amd.QmmError, match="no GPU kernel"):
+        run_moe(ctx, w1, w2, O.Q8_0, dm, dff, x, ids, gw, Mode.F16_MFMA)
+    got = run_moe(ctx, w1, w2, O.Q8_0, dm, dff, x, ids, gw, Mode.EXACT)
+    want = O.moe_ffn(x, w1, w2, O.Q8_0, dff, ids, gw)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
