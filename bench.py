@@ -173,8 +173,11 @@ def gemv_bytes(dt, n, k, t=1):
     return n * rce_amd.row_bytes(dt, k) + 4 * k * t + 4 * n * t
 
 
-def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
-    """Time `steps` device-resident GEMVs rotating over weight copies."""
+def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed, settle_s=0.0):
+    """Time `steps` device-resident GEMVs rotating over weight copies.
+    settle_s: seconds of untimed launches first, so that an idle GPU's
+    clocks have ramped up before the warmup and the timed steps (the first
+    launches after idle measure 5-10 % slower)."""
     import rce_amd
     b = make_weight(seed, dt, n, k)
     copies = max(2, min(64, (2 * INFINITY_CACHE) // b.size + 1))
@@ -189,6 +192,10 @@ def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed):
         for i in range(count):
             rce_amd.mm_batched_dev(ctx, xa.ptr, rce_amd.GgufDtype.F32, t_rows, ws[i % copies], out.ptr, mode)
 
+    t_settle = time.time()
+    while time.time() - t_settle < settle_s:
+        run(64)
+        ctx.synchronize()
     run(max(1, warmup))  # untimed, eager (also sizes any scratch before capture)
     ctx.synchronize()
     ms = hip.timed_graph(stream, lambda: run(steps), steps)
@@ -505,7 +512,7 @@ def main():
     # ---- headline: configs[1], Q4_0 11008x4096, batch 1 -------------------------
     dt, n, k = G.Q4_0, 11008, 4096
     log(f"headline Q4_0 GEMV {n}x{k} batch 1 mode={args.mode} steps={args.steps} warmup={args.warmup}")
-    ms, b, x, res, copies = time_gemv(hip, ctx, dt, n, k, 1, mode, args.steps, args.warmup, 11)
+    ms, b, x, res, copies = time_gemv(hip, ctx, dt, n, k, 1, mode, args.steps, args.warmup, 11, settle_s=0.3)
     nbytes = gemv_bytes(dt, n, k, 1)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"  {ms * 1e3:.2f} us/launch  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")

@@ -67,6 +67,64 @@ __device__ __forceinline__ uint32_t ldw2(const uint8_t *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
 }
 
+// Buffer access to one weight's rows.  A row's byte offset splits into the
+// lane's part (its row within the block's row pass, times the row stride;
+// loop-invariant, one VGPR) and the row pass's part (block-uniform, an SGPR
+// soffset), so the weight loads of every row after the first cost no vector
+// address arithmetic.  Loads are non-temporal (aux bit 1 on gfx950) like
+// the pointer forms above.  num_records is the maximum: the layouts'
+// padding rows (layout_pad_bytes) back every offset a tile forms, as for the
+// pointer loads, and the host keeps the weight's span below 2^31 bytes.
+struct WBuf {
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t lane;
+};
+__device__ __forceinline__ WBuf make_wbuf(const uint8_t *base, uint32_t lane_off) {
+    WBuf b;
+    b.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short)0, (int)0x7FFFFFFF, 0x00020000);
+    b.lane = lane_off;
+    return b;
+}
+constexpr int BUF_NT = 2;
+__device__ __forceinline__ uint4 bld16(const WBuf &b, uint32_t off, uint32_t soff) {
+    const v4u32 t = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)(b.lane + off), (int)soff, BUF_NT);
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint2 bld8(const WBuf &b, uint32_t off, uint32_t soff) {
+    const v2u32 t = __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)(b.lane + off), (int)soff, BUF_NT);
+    return make_uint2(t.x, t.y);
+}
+__device__ __forceinline__ uint32_t bld4(const WBuf &b, uint32_t off, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)(b.lane + off), (int)soff, BUF_NT);
+}
+__device__ __forceinline__ uint32_t bld2(const WBuf &b, uint32_t off, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(b.r, (int)(b.lane + off), (int)soff, BUF_NT);
+}
+
+// Two nibbles (bytes 2h and 2h + 1 of x, each 0..15) as exact floats.  A
+// byte n < 16 read as an OCP FP8 E4M3 code is n * 2^-9 exactly (codes 0..7
+// are the subnormals m * 2^-9, codes 8..15 the binade (1 + m/8) * 2^-6 =
+// (8 + m) * 2^-9); the conversion's scale 2^9 makes it n.  One instruction
+// per two values instead of one per value (v_cvt_f32_ubyte).
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x2v nib2f(uint32_t x, bool h) {
+    return h ? __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)x, 512.0f, true)
+             : __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)x, 512.0f, false);
+}
+// The four byte values (each < 16) of x as floats: FP8 = two packed
+// conversions (half rate, so the same issue time as four v_cvt_f32_ubyte;
+// measured per format: Q4_K 2 % faster with them, Q4_0 2-3 % slower).
+template <bool FP8>
+__device__ __forceinline__ void nib4f(uint32_t x, float *v) {
+    if constexpr (FP8) {
+        const f32x2v a = nib2f(x, false), b = nib2f(x, true);
+        v[0] = a.x; v[1] = a.y; v[2] = b.x; v[3] = b.y;
+    } else {
+        v[0] = (float)(x & 0xFFu); v[1] = (float)((x >> 8) & 0xFFu); v[2] = (float)((x >> 16) & 0xFFu);
+        v[3] = (float)(x >> 24);
+    }
+}
+
 // Rows of weight loads a thread keeps in flight ahead of its arithmetic:
 // the next rows' loads go out before each row's addends, so a wave's data
 // arrives in the order it is used (measured: 2 beats issuing all rows at
@@ -224,6 +282,59 @@ __device__ __forceinline__ RawQ3_K ld_q3_k(const DevWeight &w, size_t row, int c
     r.h = ldw4(rp + w.plane2 + 4 * (size_t)col);
     const uint32_t sc = ldw2(rp + w.plane3 + 2 * (size_t)col);
     const uint32_t d = ldw2(rp + 2 * (size_t)(col >> 3));
+    r.sd = sc | (d << 16);
+    return r;
+}
+
+// The same unit loads through a WBuf: soff is the row pass's byte offset
+// (uniform), b.lane the lane's row offset within the pass.
+__device__ __forceinline__ RawQ4_0 bl_q4_0(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ4_0 r;
+    r.q = bld16(b, (uint32_t)w.plane1 + 16u * col, soff);
+    r.s = bld2(b, 2u * col, soff);
+    return r;
+}
+__device__ __forceinline__ RawQ8_0 bl_q8_0(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ8_0 r;
+    r.q0 = bld16(b, (uint32_t)w.plane1 + 16u * col, soff);
+    r.q1 = bld16(b, (uint32_t)w.plane2 + 16u * col, soff);
+    r.s = bld2(b, 2u * col, soff);
+    return r;
+}
+__device__ __forceinline__ RawQ4_K bl_q4_k(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ4_K r;
+    r.h = bld16(b, 16u * (col >> 2), soff);
+    r.q0 = bld16(b, (uint32_t)w.plane1 + 16u * col, soff);
+    r.q1 = bld16(b, (uint32_t)w.plane2 + 16u * col, soff);
+    return r;
+}
+__device__ __forceinline__ RawQ5_K bl_q5_k(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ5_K r;
+    r.h = bld16(b, 16u * (col >> 2), soff);
+    r.q0 = bld16(b, (uint32_t)w.plane1 + 16u * col, soff);
+    r.q1 = bld16(b, (uint32_t)w.plane2 + 16u * col, soff);
+    r.hb = bld8(b, (uint32_t)w.plane3 + 8u * col, soff);
+    return r;
+}
+__device__ __forceinline__ RawQ5_0 bl_q5_0(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ5_0 r;
+    r.q = bld16(b, (uint32_t)w.plane1 + 16u * col, soff);
+    r.s = bld2(b, 2u * col, soff);
+    r.h = bld4(b, (uint32_t)w.plane2 + 4u * col, soff);
+    return r;
+}
+__device__ __forceinline__ RawQ4_1 bl_q4_1(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ4_1 r;
+    r.q = bld16(b, (uint32_t)w.plane1 + 16u * col, soff);
+    r.sm = bld4(b, 4u * col, soff);
+    return r;
+}
+__device__ __forceinline__ RawQ3_K bl_q3_k(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+    RawQ3_K r;
+    r.q = bld8(b, (uint32_t)w.plane1 + 8u * col, soff);
+    r.h = bld4(b, (uint32_t)w.plane2 + 4u * col, soff);
+    const uint32_t sc = bld2(b, (uint32_t)w.plane3 + 2u * col, soff);
+    const uint32_t d = bld2(b, 2u * (col >> 3), soff);
     r.sd = sc | (d << 16);
     return r;
 }
@@ -405,6 +516,7 @@ struct Q4_0Exact {
     using Raw = RawQ4_0;
     float av[TB][32];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_0(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q4_0(w, b, soff, col); }
     __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -421,10 +533,12 @@ struct Q4_0Exact {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t x = wrd(r.q, i);
-            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+            float nls[4], nhs[4];
+            nib4f<false>(and_opaque(x, NIB), nls);
+            nib4f<false>(and_opaque(x >> 4, NIB), nhs);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float nl = (float)((lo >> (8 * j)) & 0xFFu), nh = (float)((hi >> (8 * j)) & 0xFFu);
+                const float nl = nls[j], nh = nhs[j];
                 if constexpr (TB == 1) {
                     sub[0] = sub[0] + __builtin_fmaf(nl, av[0][4 * i + j], -8.0f * av[0][4 * i + j]);
                     sub[0] = sub[0] + __builtin_fmaf(nh, av[0][4 * i + j + 16], -8.0f * av[0][4 * i + j + 16]);
@@ -458,6 +572,7 @@ struct Q8_0Exact {
     using Raw = RawQ8_0;
     float av[TB][32];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q8_0(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q8_0(w, b, soff, col); }
     __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -503,6 +618,7 @@ struct Q5_0Exact {
     using Raw = RawQ5_0;
     float av[TB][32];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q5_0(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q5_0(w, b, soff, col); }
     __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
 #pragma unroll
         for (int t = 0; t < TB; t++)
@@ -556,6 +672,7 @@ struct Q4_1Exact {
     float av[TB][32];
     float as[TB];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_1(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q4_1(w, b, soff, col); }
     __device__ void sums() {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -577,10 +694,12 @@ struct Q4_1Exact {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t x = wrd(r.q, i);
-            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+            float nls[4], nhs[4];
+            nib4f<false>(and_opaque(x, NIB), nls);
+            nib4f<false>(and_opaque(x >> 4, NIB), nhs);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float nl = (float)((lo >> (8 * j)) & 0xFFu), nh = (float)((hi >> (8 * j)) & 0xFFu);
+                const float nl = nls[j], nh = nhs[j];
 #pragma unroll
                 for (int t = 0; t < TB; t++) {
                     const float p = nl * av[t][4 * i + j], q = nh * av[t][4 * i + j + 16];
@@ -613,6 +732,7 @@ struct Q3_KExact {
     using Raw = RawQ3_K;
     float av[TB][32];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q3_k(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q3_k(w, b, soff, col); }
     __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
 #pragma unroll
         for (int t = 0; t < TB; t++)
@@ -624,10 +744,12 @@ struct Q3_KExact {
         for (int t = 0; t < TB; t++) { s1[t] = 0.0f; s2[t] = 0.0f; }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t v1 = q3_vals(r, 0, i), v2 = q3_vals(r, 1, i);
+            float n1s[4], n2s[4];
+            nib4f<false>(q3_vals(r, 0, i), n1s);  // values 0..7
+            nib4f<false>(q3_vals(r, 1, i), n2s);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float n1 = (float)((v1 >> (8 * j)) & 0xFFu), n2 = (float)((v2 >> (8 * j)) & 0xFFu);
+                const float n1 = n1s[j], n2 = n2s[j];
                 const int p = 4 * i + j;
                 if constexpr (TB == 1) {  // (n - 4) a as fma(n, a, -4a): one rounding, like the product
                     s1[0] = s1[0] + __builtin_fmaf(n1, av[0][p], -4.0f * av[0][p]);
@@ -670,6 +792,7 @@ struct Q4_KExact {
     float a_lo[TB], a_hi[TB];
     int g;
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_k(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q4_k(w, b, soff, col); }
     __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
         g = col & 3;
 #pragma unroll
@@ -702,10 +825,12 @@ struct Q4_KExact {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t x = i < 4 ? wrd(r.q0, i) : wrd(r.q1, i - 4);
-            const uint32_t lo = and_opaque(x, NIB), hi = and_opaque(x >> 4, NIB);
+            float vls[4], vhs[4];
+            nib4f<true>(and_opaque(x, NIB), vls);
+            nib4f<true>(and_opaque(x >> 4, NIB), vhs);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float vl = (float)((lo >> (8 * j)) & 0xFFu), vh = (float)((hi >> (8 * j)) & 0xFFu);
+                const float vl = vls[j], vh = vhs[j];
 #pragma unroll
                 for (int t = 0; t < TB; t++) {
                     va_lo[t] = va_lo[t] + vl * av[t][4 * i + j];
@@ -741,6 +866,7 @@ struct Q5_KExact {
     float a_lo[TB], a_hi[TB];
     int g;
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q5_k(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q5_k(w, b, soff, col); }
     __device__ void init(const float *A, size_t k, int t0, int tv, int col) {
         g = col & 3;
 #pragma unroll
@@ -821,6 +947,12 @@ struct Q32Q8 {
         else if constexpr (KIND == B32_Q5_0) return ld_q5_0(w, row, col);
         else if constexpr (KIND == B32_Q4_1) return ld_q4_1(w, row, col);
         else return ld_q8_0(w, row, col);
+    }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) {
+        if constexpr (KIND == B32_Q4_0) return bl_q4_0(w, b, soff, col);
+        else if constexpr (KIND == B32_Q5_0) return bl_q5_0(w, b, soff, col);
+        else if constexpr (KIND == B32_Q4_1) return bl_q4_1(w, b, soff, col);
+        else return bl_q8_0(w, b, soff, col);
     }
     __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
 #pragma unroll
@@ -906,6 +1038,7 @@ struct Q3_KQ8 {
     float dx[TB];
     int xs1[TB], xs2[TB];
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q3_k(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q3_k(w, b, soff, col); }
     __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -952,6 +1085,7 @@ struct Q4_KQ8 {
     int sl[TB], sh[TB];
     int g;
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q4_k(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q4_k(w, b, soff, col); }
     __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
         g = col & 3;
 #pragma unroll
@@ -1013,6 +1147,7 @@ struct Q5_KQ8 {
     int sl[TB], sh[TB];
     int g;
     __device__ static Raw load(const DevWeight &w, size_t row, int col) { return ld_q5_k(w, row, col); }
+    __device__ static Raw load_b(const DevWeight &w, const WBuf &b, uint32_t soff, int col) { return bl_q5_k(w, b, soff, col); }
     __device__ void init_q8(const ActLds &L, size_t k, int tv, int col) {
         g = col & 3;
 #pragma unroll
@@ -1147,13 +1282,21 @@ __host__ __device__ constexpr int fold_ld(int U) { return ((U + 3) & ~3) + 4; }
 // after the weight loads are issued, so it does not hold them back.
 template <class U, class = void> struct HasPrepare : std::false_type {};
 template <class U> struct HasPrepare<U, std::void_t<decltype(std::declval<U &>().prepare())>> : std::true_type {};
+// Units whose weights load through a WBuf (every layout with whole rows at
+// row_stride; LAYOUT_IL64_Q6_K interleaves 64 rows and keeps the pointer form).
+template <class U, class = void> struct HasLoadB : std::false_type {};
+template <class U>
+struct HasLoadB<U, std::void_t<decltype(U::load_b(std::declval<const DevWeight &>(), std::declval<const WBuf &>(),
+                                                   0u, 0))>> : std::true_type {};
 
 // Dynamic LDS a block may use (the default per-block limit).
 constexpr size_t LDS_MAX = 64 * 1024;
 
 inline size_t gemv_lds_bytes(int U, int nt, int rpl, int tb, bool q8, size_t k) {
-    // the tile's addends plus one dummy row written by idle lanes
-    const size_t fold = ((size_t)tb * (size_t)(nt / U) * rpl + 1) * fold_ld(U) * sizeof(float);
+    // the tile's addends, plus (when nt is not a multiple of U) one tile of
+    // dummy rows for the idle lanes' stores
+    const size_t rt = (size_t)(nt / U) * rpl;
+    const size_t fold = ((size_t)tb * rt + (nt % U ? rt : 0)) * fold_ld(U) * sizeof(float);
     const size_t act = q8 ? act_lds_bytes(k, tb) : 0;
     return fold > act ? fold : act;
 }
@@ -1219,10 +1362,24 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weights'
     typename Unit::Raw raw[RPL];
     const int rs = active ? rsub : P - 1;
+    // Buffer loads: the lane's row within a pass in a VGPR, the pass
+    // (row0 + u P rows) as a uniform soffset.
+    WBuf wb1, wb2;
+    if constexpr (HasLoadB<Unit>::value) {
+        wb1 = make_wbuf(w.base, (uint32_t)((size_t)rs * w.row_stride));
+        if constexpr (KIND == FX_SWIGLU) wb2 = make_wbuf(fx.w2.base, (uint32_t)((size_t)rs * fx.w2.row_stride));
+    }
     auto issue = [&](int u) {
         const bool up = KIND == FX_SWIGLU && u >= HALF;
-        const size_t r = row0 + (size_t)((up ? u - HALF : u) * P + rs);
-        raw[u] = Unit::load(up ? fx.w2 : w, r, col);
+        const int uu = up ? u - HALF : u;
+        if constexpr (HasLoadB<Unit>::value) {
+            const DevWeight &ww = up ? fx.w2 : w;
+            const uint32_t soff = (uint32_t)((row0 + (size_t)(uu * P)) * ww.row_stride);
+            raw[u] = Unit::load_b(ww, up ? wb2 : wb1, soff, col);
+        } else {
+            const size_t r = row0 + (size_t)(uu * P + rs);
+            raw[u] = Unit::load(up ? fx.w2 : w, r, col);
+        }
     };
     constexpr int PF = PREFETCH_ROWS < RPL ? PREFETCH_ROWS : RPL;  // rows loaded ahead of the arithmetic
 #pragma unroll
@@ -1272,20 +1429,26 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     // Phase 3: per-unit addends of every (token, row) to LDS.
     float *part = reinterpret_cast<float *>(lds);
     const int ld = fold_ld(U);
+    // Store address of (token t, pass u): lane part + u P ld (uniform) +
+    // t RT ld.  Idle lanes (rsub == P, only when NT % U != 0) store into
+    // the dummy tile past the TB tiles, the same slot for every token.
+    int lane_fold = (active ? rsub : TB * RT) * ld + col;
+    int tok_fold = active ? RT * ld : 0;
+    // opaque, so the optimizer cannot fold the uniform offsets back into a
+    // per-row multiply
+    asm volatile("" : "+v"(lane_fold), "+v"(tok_fold));
 #pragma unroll
     for (int u = 0; u < RPL; u++) {
         if constexpr (PF < RPL) {  // the next rows' loads go out before this row's arithmetic
             if (u + PF < RPL) issue(u + PF);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // Every lane computes and stores (idle lanes into a dummy row past
-        // the tile), so no load is sunk into a guarded branch; rows past
-        // n_rows store sums the fold below never reads.
+        // Every lane computes and stores, so no load is sunk into a guarded
+        // branch; rows past n_rows store sums the fold below never reads.
         float ad[TB];
         unit.addends(raw[u], ad);
-        const int r = u * P + rsub;
 #pragma unroll
-        for (int t = 0; t < TB; t++) part[(active ? t * RT + r : TB * RT) * ld + col] = ad[t];
+        for (int t = 0; t < TB; t++) part[lane_fold + u * (P * ld) + t * tok_fold] = ad[t];
     }
     __syncthreads();
     // Phase 4: the reference's fold, one thread per (token, output row).
@@ -1338,11 +1501,18 @@ inline int units_per_row(uint32_t dtype, size_t n_cols) {
 
 inline int nt_for(int U) { return U <= 256 ? 256 : (U <= 512 ? 512 : 1024); }
 
+// The buffer loads' offsets are 32-bit: a launch's weights, with the rows a
+// tile reads past the end, must span less than 2^31 bytes.
+inline bool wbuf_span_ok(const DevWeight &w, size_t tile_rows) {
+    return (w.n_rows + tile_rows) * w.row_stride < ((size_t)1 << 31);
+}
+
 template <class Unit, int NT, int RPL, bool Q8>
 hipError_t launch_as(const DevWeight &w, int U, const float *a, size_t t_rows, float *out, hipStream_t s) {
     constexpr int TB = Unit::NTOK;
     const int P = NT / U, RT = P * RPL;
     if (P < 1) return hipErrorInvalidConfiguration;
+    if (!wbuf_span_ok(w, RT)) return hipErrorInvalidValue;
     const size_t lds = gemv_lds_bytes(U, NT, RPL, TB, Q8, w.n_cols);
     if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)((w.n_rows + RT - 1) / RT), (unsigned)((t_rows + TB - 1) / TB)), block(NT);
@@ -1357,6 +1527,8 @@ hipError_t launch_as_fx(const FxLaunch &f, int U, const float *a, hipStream_t s)
     static_assert(Unit::NTOK == 1, "the fused forms are single-token");
     const int P = NT / U, RT = P * RPL;
     if (P < 1) return hipErrorInvalidConfiguration;
+    for (int i = 0; i < f.nw && i < 3; i++)
+        if (!wbuf_span_ok(f.w[i], RT)) return hipErrorInvalidValue;
     const size_t lds = gemv_lds_bytes(U, NT, RPL, 1, Q8, f.w[0].n_cols);
     if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
     auto nblk = [&](const DevWeight &w, int rows_per_block) {
@@ -1464,6 +1636,7 @@ hipError_t launch_as_preq(const DevWeight &w, int U, const float *a, size_t t_ro
     constexpr int NT = 256, TB = Unit::NTOK;
     const int P = NT / U, RT = P * RPL;
     if (P < 1) return hipErrorInvalidConfiguration;
+    if (!wbuf_span_ok(w, RT)) return hipErrorInvalidValue;
     const size_t lds = gemv_lds_bytes(U, NT, RPL, TB, false, w.n_cols);
     if (lds > LDS_MAX) return hipErrorInvalidConfiguration;
     GemvFx fx{};
