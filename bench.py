@@ -175,9 +175,7 @@ def gemv_bytes(dt, n, k, t=1):
 
 def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed, settle_s=0.0):
     """Time `steps` device-resident GEMVs rotating over weight copies.
-    settle_s: seconds of untimed launches first, so that an idle GPU's
-    clocks have ramped up before the warmup and the timed steps (the first
-    launches after idle measure 5-10 % slower)."""
+    settle_s: seconds of untimed launches first (see settle)."""
     import rce_amd
     b = make_weight(seed, dt, n, k)
     copies = max(2, min(64, (2 * INFINITY_CACHE) // b.size + 1))
@@ -192,10 +190,7 @@ def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed, settle_s=0.
         for i in range(count):
             rce_amd.mm_batched_dev(ctx, xa.ptr, rce_amd.GgufDtype.F32, t_rows, ws[i % copies], out.ptr, mode)
 
-    t_settle = time.time()
-    while time.time() - t_settle < settle_s:
-        run(64)
-        ctx.synchronize()
+    settle(ctx, run, settle_s)
     run(max(1, warmup))  # untimed, eager (also sizes any scratch before capture)
     ctx.synchronize()
     ms = hip.timed_graph(stream, lambda: run(steps), steps)
@@ -208,7 +203,17 @@ def time_gemv(hip, ctx, dt, n, k, t_rows, mode, steps, warmup, seed, settle_s=0.
     return ms, b, x, res, copies
 
 
-def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed):
+def settle(ctx, run, settle_s):
+    """settle_s seconds of untimed launches: an idle GPU's clocks ramp up
+    over the first tens of milliseconds of work (measured: the Q4_K GEMM
+    takes 32 us per launch on a freshly idle GPU, 27 us once warm)."""
+    t0 = time.time()
+    while time.time() - t0 < settle_s:
+        run(16)
+        ctx.synchronize()
+
+
+def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed, settle_s=0.2):
     """configs[2]-style prefill GEMM in F16_MFMA mode: A [m, k] f16 resident,
     weights rotated over HBM copies; returns ms per launch and the first 16
     output rows (checked in the CPU leg)."""
@@ -226,6 +231,7 @@ def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed):
             rce_amd.mm_batched_dev(ctx, xa.ptr, rce_amd.GgufDtype.F16, m, ws[i % copies], out.ptr,
                                    rce_amd.Mode.F16_MFMA)
 
+    settle(ctx, run, settle_s)
     run(max(1, warmup))
     ctx.synchronize()
     ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
@@ -239,7 +245,7 @@ def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed):
     return ms, {"b": b, "x": x[:16].astype(np.float32), "got": res, "dt": dt, "n": n, "k": k}
 
 
-def time_moe(hip, ctx, steps, warmup, seed, mode):
+def time_moe(hip, ctx, steps, warmup, seed, mode, settle_s=0.2):
     """8 Q4_0 experts (w1 14336x4096, w2 4096x14336), 256 tokens,
     top-2 of N(0,1) router logits; ms per grouped-FFN call (all 8 experts'
     528 MB stream from HBM each call), the touched weight bytes, and a
@@ -268,6 +274,7 @@ def time_moe(hip, ctx, steps, warmup, seed, mode):
 
     run(max(1, warmup))  # sizes scratch and uploads the expert tables before capture
     ctx.synchronize()
+    settle(ctx, run, settle_s)
     ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
     ctx.synchronize()
     got = bo.download(np.float32, T * dm).reshape(T, dm)[:8]

@@ -74,7 +74,9 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
 //     this position's k and v, so no block waits for another).
 //  2. Wave w takes the keys [w*seq/NW, (w+1)*seq/NW) in runs of CH (64 for
 //     d_head 64, 32 for 128), all of a run's loads in flight together: lane
-//     j scores key j (the reference's sequential dot, times scale); the
+//     j scores key j (the reference's sequential dot, times scale; the key
+//     cache is transposed, [kv head][dimension][position], so each dimension
+//     of a run is one coalesced load instead of one cache line per key); the
 //     run's maximum and the sum of p_j = exp(s_j - m) are wave reductions
 //     of fixed shape; out[d] = sum_j p_j v_j[d] (lane = d, four partial sums
 //     added in a fixed order).  A wave's runs merge by rescaling with
@@ -108,7 +110,6 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
                                                            float *__restrict__ att, const int *__restrict__ skip) {
     constexpr int DPL = DH / 64;    // dimensions per lane
     constexpr int CH = 4096 / DH;   // keys per run (64 or 32)
-    constexpr int R4 = DH / 4;      // float4 pieces of a row
     __shared__ float qs[DH], ks[DH], vs[DH], cs[DH];
     __shared__ float mo[ATT_NW][DH + 2];  // each wave's out[DH], m, l
     // the wave index in a scalar register: the run bounds below are then
@@ -126,9 +127,11 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
     const int seq = pos + 1, half = rope_dim / 2;
     for (int i = tid; i < 2 * half; i += 64 * ATT_NW) cs[i] = rope_cs[(size_t)pos * half * 2 + i];
     const int j0 = (int)((long)wave * seq / ATT_NW), j1 = (int)((long)(wave + 1) * seq / ATT_NW);
-    const float *kbase = k_cache + (size_t)g * DH, *vbase = v_cache + (size_t)g * DH;
+    // keys are stored transposed, [kv head][dimension][position], so that a
+    // lane per key reads each dimension of a run with one coalesced load
+    const float *kbase = k_cache + (size_t)g * DH * ctx_len, *vbase = v_cache + (size_t)g * DH;
 
-    float4 kv[R4];
+    float kt[DH];
     float vv[CH][DPL];
     float vcur[DPL];  // this position's value column (not in the cache yet)
 #pragma unroll
@@ -143,9 +146,9 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
     // longer be in flight together.
     auto load_run = [&](int c0) {
         const int r = c0 + lane;
-        const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)(r < pos ? r : 0) * kvd);
+        const float *kp = kbase + (r < pos ? r : 0);
 #pragma unroll
-        for (int i = 0; i < R4; i++) kv[i] = kp[i];
+        for (int d = 0; d < DH; d++) kt[d] = kp[(size_t)d * ctx_len];
 #pragma unroll
         for (int j = 0; j < CH; j++) {
             const int rj = c0 + j;
@@ -173,10 +176,10 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
     }
     __syncthreads();
     if (h % qpk == 0 && wave == 0 && !(skip && skip[0])) {  // append this position to the layer's caches
-        float *kd = k_cache + (size_t)pos * kvd + (size_t)g * DH, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
+        float *kd = k_cache + (size_t)g * DH * ctx_len + pos, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
 #pragma unroll
         for (int d = 0; d < DPL; d++) {
-            kd[lane + 64 * d] = ks[lane + 64 * d];
+            kd[(size_t)(lane + 64 * d) * ctx_len] = ks[lane + 64 * d];
             vd[lane + 64 * d] = vs[lane + 64 * d];
         }
     }
@@ -193,20 +196,14 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
             if (c0 > j0) load_run(c0);
             if (c0 + lane == pos) {  // this lane's key is the current position
 #pragma unroll
-                for (int i = 0; i < R4; i++) kv[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
+                for (int d = 0; d < DH; d++) kt[d] = ks[d];
             }
             float sc = -INFINITY;
             if (lane < n) {
                 float dot = 0.0f;
 #pragma unroll
-                for (int i = 0; i < R4; i++) {
-                    float pr = q[4 * i] * kv[i].x;
-                    dot = dot + pr;
-                    pr = q[4 * i + 1] * kv[i].y;
-                    dot = dot + pr;
-                    pr = q[4 * i + 2] * kv[i].z;
-                    dot = dot + pr;
-                    pr = q[4 * i + 3] * kv[i].w;
+                for (int d = 0; d < DH; d++) {
+                    const float pr = q[d] * kt[d];
                     dot = dot + pr;
                 }
                 sc = dot * scale;
