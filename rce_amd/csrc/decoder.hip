@@ -74,13 +74,11 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
 //     this position's k and v, so no block waits for another).
 //  2. Wave w takes the keys [w*seq/NW, (w+1)*seq/NW) in runs of CH (64 for
 //     d_head 64, 32 for 128), all of a run's loads in flight together: lane
-//     j scores key j (the reference's sequential dot, times scale; the key
-//     cache is transposed, [kv head][dimension][position], so each dimension
-//     of a run is one coalesced load instead of one cache line per key); the
+//     j scores key j (the reference's sequential dot, times scale); the
 //     run's maximum and the sum of p_j = exp(s_j - m) are wave reductions
-//     of fixed shape; out[d] = sum_j p_j v_j[d] (lane = d, four partial sums
-//     added in a fixed order).  A wave's runs merge by rescaling with
-//     exp(m_old - m_new).
+//     of fixed shape; out[d] = sum_j p_j v_j[d] as four partial sums over
+//     the keys j = 0, 1, 2, 3 (mod 4), added (a0 + a1) + (a2 + a3).  A
+//     wave's runs merge by rescaling with exp(m_old - m_new).
 //  3. The waves' (m, l, out) merge in wave order through LDS (M = max m_w;
 //     out = sum_w exp(m_w - M) out_w, l = sum_w exp(m_w - M) l_w), then
 //     out *= 1 / l.
@@ -88,17 +86,34 @@ __global__ __launch_bounds__(NORM_NT) void k_rms_norm(const float *__restrict__ 
 // (rce-op-attn L196-251) folds key by key with its online recurrence,
 // evaluated in parallel: every reduction has a fixed shape (run-to-run
 // bit-identical), and the result differs from the reference's by f32
-// reassociation only (one key: out = v exactly, as the reference's first
+// reassociation only (one key gives v exactly, as the reference's first
 // key gives).
-// Waves per head: one per SIMD.  A run keeps a key row, a value column and
-// q in registers (about 200 for d_head 64), so the kernel asks for one wave
-// per SIMD and the whole register file: a launch has n_q blocks at most.
+// Cache layouts (per layer): keys in tiles of 64 positions, [kv head]
+// [position / 64][dimension / 4][position % 64][dimension % 4], so that a
+// lane per key reads four dimensions of its key with one 16-byte load and
+// a wave's load is one contiguous kilobyte (d_head / 4 loads per run);
+// values [position][kv head][dimension], read as 16-byte quads by
+// 64 / (d_head / 4) keys per load.  The caches hold ceil(ctx / 64) * 64
+// positions.
+// Waves per head: one per SIMD.  A run keeps a key row, its value quads
+// and q in registers (about 200 for d_head 64), so the kernel asks for one
+// wave per SIMD and the whole register file: a launch has n_q blocks at
+// most.
 constexpr int ATT_NW = 4;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
+}
+
+__device__ __forceinline__ float f4e(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+__device__ __forceinline__ float &f4e(float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+// Float offset of (position p, dimension d) in one kv head's key tiles.
+template <int DH>
+__device__ __forceinline__ size_t key_off(int p, int d) {
+    return (size_t)(p >> 6) * (64 * DH) + (size_t)(d >> 2) * 256 + (size_t)(p & 63) * 4 + (d & 3);
 }
 
 template <int DH>
@@ -108,57 +123,53 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
                                                            const int *__restrict__ pos_p, int ctx_len, int n_q,
                                                            int n_kv, int rope_dim, float scale,
                                                            float *__restrict__ att, const int *__restrict__ skip) {
-    constexpr int DPL = DH / 64;    // dimensions per lane
-    constexpr int CH = 4096 / DH;   // keys per run (64 or 32)
+    constexpr int NQD = DH / 4;      // dimension quads of a key
+    constexpr int KPI = 64 / NQD;    // keys per value load (4 or 2)
+    constexpr int NA = 4 / KPI;      // partial sums a lane holds (1 or 2)
+    constexpr int CH = 4096 / DH;    // keys per run (64 or 32)
+    constexpr int VL = CH / KPI;     // value loads per run (16)
     __shared__ float qs[DH], ks[DH], vs[DH], cs[DH];
     __shared__ float mo[ATT_NW][DH + 2];  // each wave's out[DH], m, l
     // the wave index in a scalar register: the run bounds below are then
     // wave-uniform and their branches scalar
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = blockIdx.x;
     const int qpk = n_q / n_kv, g = h / qpk;
-    const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH;
+    const int kk = lane / NQD, dq = lane % NQD;  // value lanes: key kk of each KPI, dimensions 4 dq .. 4 dq + 3
+    const size_t qd = (size_t)n_q * DH, kvd = (size_t)n_kv * DH, ctxp = ((size_t)ctx_len + 63) & ~(size_t)63;
     for (int i = tid; i < DH; i += 64 * ATT_NW) {  // independent of the position
         qs[i] = qkv[(size_t)h * DH + i];
         ks[i] = qkv[qd + (size_t)g * DH + i];
         vs[i] = qkv[qd + kvd + (size_t)g * DH + i];
     }
+    // this position's value quad (not in the cache yet)
+    const float4 vcur = *reinterpret_cast<const float4 *>(qkv + qd + kvd + (size_t)g * DH + 4 * dq);
     const int pos = pos_p[0];
     if (pos < 0 || pos >= ctx_len) return;  // the whole block; the step's last kernel reports it
     const int seq = pos + 1, half = rope_dim / 2;
     for (int i = tid; i < 2 * half; i += 64 * ATT_NW) cs[i] = rope_cs[(size_t)pos * half * 2 + i];
     const int j0 = (int)((long)wave * seq / ATT_NW), j1 = (int)((long)(wave + 1) * seq / ATT_NW);
-    // keys are stored transposed, [kv head][dimension][position], so that a
-    // lane per key reads each dimension of a run with one coalesced load
-    const float *kbase = k_cache + (size_t)g * DH * ctx_len, *vbase = v_cache + (size_t)g * DH;
+    const float *kbase = k_cache + (size_t)g * DH * ctxp, *vbase = v_cache + (size_t)g * DH + 4 * dq;
 
-    float kt[DH];
-    float vv[CH][DPL];
-    float vcur[DPL];  // this position's value column (not in the cache yet)
-#pragma unroll
-    for (int d = 0; d < DPL; d++) vcur[d] = qkv[qd + kvd + (size_t)g * DH + lane + 64 * d];
+    float4 kq[NQD];   // this lane's key, four dimensions per load
+    float4 vv[VL];    // value quads of keys kk, kk + KPI, ... of the run
     // A run's cached keys / values, every load unconditional: rows at or
     // past pos read row 0 (always in range); key rows at or past pos are
     // unused (the current key comes from LDS).  The loaded value rows are
-    // replaced where they are consumed (value_at): row pos by this
+    // replaced where they are consumed: row pos by this
     // position's values, rows past pos by 0, so every value row used is
     // finite.  Doing that here instead would put a branch after each load
     // whose untaken side waits for the load, and the run's loads would no
     // longer be in flight together.
     auto load_run = [&](int c0) {
         const int r = c0 + lane;
-        const float *kp = kbase + (r < pos ? r : 0);
+        const float4 *kp = reinterpret_cast<const float4 *>(kbase + key_off<DH>(r < pos ? r : 0, 0));
 #pragma unroll
-        for (int d = 0; d < DH; d++) kt[d] = kp[(size_t)d * ctx_len];
+        for (int i = 0; i < NQD; i++) kq[i] = kp[64 * i];
 #pragma unroll
-        for (int j = 0; j < CH; j++) {
-            const int rj = c0 + j;
-            const float *vp = vbase + (size_t)(rj < pos ? rj : 0) * kvd;
-#pragma unroll
-            for (int d = 0; d < DPL; d++) vv[j][d] = vp[lane + 64 * d];
+        for (int i = 0; i < VL; i++) {
+            const int rj = c0 + i * KPI + kk;
+            vv[i] = *reinterpret_cast<const float4 *>(vbase + (size_t)(rj < pos ? rj : 0) * kvd);
         }
-    };
-    auto value_at = [&](int rj, int j, int d) {
-        return rj < pos ? vv[j][d] : (rj == pos ? vcur[d] : 0.0f);
     };
     if (j0 < j1) load_run(j0);
     __syncthreads();
@@ -176,16 +187,14 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
     }
     __syncthreads();
     if (h % qpk == 0 && wave == 0 && !(skip && skip[0])) {  // append this position to the layer's caches
-        float *kd = k_cache + (size_t)g * DH * ctx_len + pos, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
+        float *kd = k_cache + (size_t)g * DH * ctxp, *vd = v_cache + (size_t)pos * kvd + (size_t)g * DH;
 #pragma unroll
-        for (int d = 0; d < DPL; d++) {
-            kd[(size_t)(lane + 64 * d) * ctx_len] = ks[lane + 64 * d];
+        for (int d = 0; d < DH / 64; d++) {
+            kd[key_off<DH>(pos, lane + 64 * d)] = ks[lane + 64 * d];
             vd[lane + 64 * d] = vs[lane + 64 * d];
         }
     }
-    float o[DPL];
-#pragma unroll
-    for (int d = 0; d < DPL; d++) o[d] = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // out[4 dq .. 4 dq + 3]
     float m = -INFINITY, l = 0.0f;
     if (j0 < j1) {
         float q[DH];  // every lane needs all of q for its key's dot
@@ -196,14 +205,14 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
             if (c0 > j0) load_run(c0);
             if (c0 + lane == pos) {  // this lane's key is the current position
 #pragma unroll
-                for (int d = 0; d < DH; d++) kt[d] = ks[d];
+                for (int i = 0; i < NQD; i++) kq[i] = make_float4(ks[4 * i], ks[4 * i + 1], ks[4 * i + 2], ks[4 * i + 3]);
             }
             float sc = -INFINITY;
             if (lane < n) {
                 float dot = 0.0f;
 #pragma unroll
                 for (int d = 0; d < DH; d++) {
-                    const float pr = q[d] * kt[d];
+                    const float pr = q[d] * f4e(kq[d >> 2], d & 3);
                     dot = dot + pr;
                 }
                 sc = dot * scale;
@@ -213,45 +222,54 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
             const float p = lane < n ? rce_exp(sc - m_new) : 0.0f;
             const float lc = l * corr;
             l = lc + wave_sum(p);
-            float a[4][DPL];
+            // a[i % NA] sums the keys i KPI + kk: partial sum (i KPI + kk) % 4
+            float4 a[NA];
 #pragma unroll
-            for (int k = 0; k < 4; k++)
+            for (int s = 0; s < NA; s++) a[s] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            // p = 0 and finite value rows past the run's keys: whole loads of
+            // KPI keys.  A constant trip count with a uniform test per load
+            // (not a break), so the loop unrolls and vv stays in registers.
 #pragma unroll
-                for (int d = 0; d < DPL; d++) a[k][d] = 0.0f;
-            // p = 0 and finite value rows past the run's keys: whole groups of
-            // four.  A constant trip count with a uniform test per group (not
-            // a break), so the loop unrolls and vv stays in registers.
+            for (int i = 0; i < VL; i++) {
+                if (i * KPI >= n) continue;
+                const int rj = c0 + i * KPI + kk;
+                const float pj = __shfl(p, i * KPI + kk);
 #pragma unroll
-            for (int j = 0; j < CH; j += 4) {
-                if (j >= n) continue;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), j + k));
-#pragma unroll
-                    for (int d = 0; d < DPL; d++) {
-                        const float t = pj * value_at(c0 + j + k, j + k, d);
-                        a[k][d] = a[k][d] + t;
-                    }
+                for (int e = 0; e < 4; e++) {
+                    const float v = rj < pos ? f4e(vv[i], e) : (rj == pos ? f4e(vcur, e) : 0.0f);
+                    const float t = pj * v;
+                    f4e(a[i % NA], e) = f4e(a[i % NA], e) + t;
                 }
             }
+            // (a0 + a1) + (a2 + a3): with KPI 4 lane group kk holds a_kk; with
+            // KPI 2 group kk holds a_kk and a_(kk + 2)
 #pragma unroll
-            for (int d = 0; d < DPL; d++) {
-                const float s01 = a[0][d] + a[1][d], s23 = a[2][d] + a[3][d];
-                const float sv = s01 + s23, oc = o[d] * corr;
-                o[d] = oc + sv;
+            for (int e = 0; e < 4; e++) {
+                float sv;
+                if constexpr (NA == 1) {
+                    const float x = f4e(a[0], e);
+                    const float s = x + __shfl_xor(x, 16);
+                    sv = s + __shfl_xor(s, 32);
+                } else {
+                    const float x0 = f4e(a[0], e), x1 = f4e(a[1], e);
+                    const float s01 = x0 + __shfl_xor(x0, 32), s23 = x1 + __shfl_xor(x1, 32);
+                    sv = s01 + s23;
+                }
+                const float oc = f4e(o, e) * corr;
+                f4e(o, e) = oc + sv;
             }
             m = m_new;
         }
     }
     float *out = att + (size_t)h * DH;
-#pragma unroll
-    for (int d = 0; d < DPL; d++) mo[wave][lane + 64 * d] = o[d];
+    if (kk == 0) *reinterpret_cast<float4 *>(&mo[wave][4 * dq]) = o;
     if (lane == 0) {
         mo[wave][DH] = m;  // -inf: a wave without keys
         mo[wave][DH + 1] = l;
     }
     __syncthreads();
     if (wave != 0) return;
+    constexpr int DPL = DH / 64;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < ATT_NW; w++) M = fmaxf(M, mo[w][DH]);

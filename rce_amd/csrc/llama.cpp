@@ -67,7 +67,8 @@ struct rce_qmm_llama {
     float *attn_norm(size_t il) const { return norms + (2 * il) * cfg.d_model; }
     float *ffn_norm(size_t il) const { return norms + (2 * il + 1) * cfg.d_model; }
     float *out_norm() const { return norms + 2 * cfg.n_layers * cfg.d_model; }
-    size_t cache_layer() const { return cfg.context_length * kvd(); }
+    // positions rounded up to whole 64-position key tiles (decoder.hip)
+    size_t cache_layer() const { return ((cfg.context_length + 63) / 64 * 64) * kvd(); }
 };
 
 namespace {
@@ -335,7 +336,7 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     const size_t big = std::max(c.d_ff, qd);
     const size_t n_f[] = {dm, dm, qd + 2 * kvd, qd, c.d_ff, c.d_ff, c.d_ff, std::max(dm, big), c.vocab,
                           (2 * c.n_layers + 1) * dm, c.context_length * std::max<size_t>(half, 1) * 2,
-                          c.n_layers * c.context_length * kvd, c.n_layers * c.context_length * kvd};
+                          c.n_layers * m->cache_layer(), c.n_layers * m->cache_layer()};
     constexpr int NF = sizeof(n_f) / sizeof(n_f[0]);
     size_t off[NF + 1], total = 0;
     for (int i = 0; i < NF; i++) {
