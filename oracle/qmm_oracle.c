@@ -1440,10 +1440,11 @@ EXPORT float orc_silu_dev(float x) {
     return t / (1.0f + e);
 }
 
-/* The wave-wide butterfly sum of the device (lane i adds lane i ^ off for
- * off = 32, 16, ..., 1; every lane ends with the same value). */
+/* The wave-wide sum of the device: the balanced pairwise tree over lane
+ * order, as a butterfly in which lane i adds lane i ^ off for off = 1, 2,
+ * 4, ..., 32 (adjacent lanes first; every lane ends with the same value). */
 static float dev_wave_sum(float v[64]) {
-    for (int off = 32; off >= 1; off >>= 1) {
+    for (int off = 1; off <= 32; off <<= 1) {
         float t[64];
         for (int i = 0; i < 64; i++) t[i] = v[i] + v[i ^ off];
         memcpy(v, t, sizeof t);
@@ -1486,8 +1487,9 @@ EXPORT void orc_rms_norm_dev(const float *x, const float *w, size_t n, float eps
 }
 
 /* One query head's attention as the device evaluates it (seq_len keys of
- * the caches, this position's row included): four waves take the keys
- * [w seq / 4, (w + 1) seq / 4) in runs of 4096 / d_head; in a run, key j's
+ * the caches, this position's row included): the keys form runs of ch =
+ * 4096 / d_head from key 0, and wave w of four takes the runs w, w + 4,
+ * w + 8, ... in that order; in a run, key j's
  * score is the sequential dot q . k_j times scale, m_new = max(m, the
  * run's scores), p_j = exp(s_j - m_new), l = l exp(m - m_new) + (butterfly
  * sum of the p_j over 64 lanes), and per dimension four partial sums a_k
@@ -1502,11 +1504,10 @@ EXPORT void orc_attend_head_dev(const float *q, const float *k_cache, const floa
     float *wo = (float *)calloc(NW * d_head, sizeof(float));
     float *a = (float *)calloc(4 * d_head, sizeof(float));
     for (int wv = 0; wv < NW; wv++) {
-        const size_t j0 = (size_t)wv * seq_len / NW, j1 = (size_t)(wv + 1) * seq_len / NW;
         float m = -INFINITY, l = 0.0f;
         float *o = wo + wv * d_head;
-        for (size_t c0 = j0; c0 < j1; c0 += ch) {
-            const size_t n = j1 - c0 < ch ? j1 - c0 : ch;
+        for (size_t c0 = (size_t)wv * ch; c0 < seq_len; c0 += NW * ch) {
+            const size_t n = seq_len - c0 < ch ? seq_len - c0 : ch;
             float sc[64], p[64];
             float mx = -INFINITY;
             for (size_t j = 0; j < 64; j++) {

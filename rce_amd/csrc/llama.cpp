@@ -282,9 +282,10 @@ rce_qmm_status rce_qmm_llama_create(rce_qmm_context *ctx, const rce_qmm_llama_co
     if (c.d_model == 0 || c.vocab == 0 || c.n_q_heads == 0 || c.n_kv_heads == 0 || c.context_length == 0 ||
         c.n_q_heads % c.n_kv_heads)
         return fail(RCE_QMM_BAD_SHAPE, "config: zero size or n_q_heads not a multiple of n_kv_heads");
-    if (!attention_supports((int)c.d_head, (int)c.rope_dim))
-        return fail(RCE_QMM_BAD_SHAPE, "config: d_head must be 64 or 128 and rope_dim even and <= d_head");
     if (c.context_length > (size_t)1 << 30) return fail(RCE_QMM_BAD_SHAPE, "config: context_length too large");
+    if (!attention_supports((int)c.d_head, (int)c.rope_dim, c.context_length, c.n_kv_heads))
+        return fail(RCE_QMM_BAD_SHAPE, "config: d_head must be 64 or 128, rope_dim even and <= d_head, and one "
+                                       "layer's KV cache under 2 GiB");
     const size_t dm = c.d_model, qd = c.n_q_heads * c.d_head, kvd = c.n_kv_heads * c.d_head;
     rce_qmm_status st;
     if (token_embd->device != ctx->device) return fail(RCE_QMM_BAD_SHAPE, "token_embd lives on another device");

@@ -1392,8 +1392,7 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
         __shared__ float red[NT / 64];
         float ss = quant_task_ssq(qt0, tid < qtotal);
         ss = ss + quant_task_ssq(qt1, tid + NT < qtotal);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off);
+        ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         float tot = 0.0f;

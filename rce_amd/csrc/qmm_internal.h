@@ -121,6 +121,38 @@ __device__ __forceinline__ float rce_exp(float x) {
     return (p * s1) * s2;
 }
 
+// Reductions over the 64 lanes of a wave as the balanced pairwise tree in
+// lane order (the tree a butterfly over lane xor 1, 2, 4, ..., 32 forms):
+// levels 1-4 by DPP within rows of 16 lanes (quad permutes [1,0,3,2] and
+// [2,3,0,1], then the half-row and row mirrors, each of which pairs a lane
+// with one that holds the other half's partial), levels 5-6 from the four
+// rows' partials read as scalars: (r0 + r1) + (r2 + r3).  Every lane gets
+// the same value, with no trip through the LDS crossbar.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rdlane_f32(float x, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = v + dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    v = v + dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    v = v + dpp_f32<0x141>(v);  // row_half_mirror: the other quad of the 8
+    v = v + dpp_f32<0x140>(v);  // row_mirror: the other 8 of the row
+    const float r0 = rdlane_f32(v, 0), r1 = rdlane_f32(v, 16), r2 = rdlane_f32(v, 32), r3 = rdlane_f32(v, 48);
+    const float s01 = r0 + r1, s23 = r2 + r3;
+    return s01 + s23;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    const float r0 = rdlane_f32(v, 0), r1 = rdlane_f32(v, 16), r2 = rdlane_f32(v, 32), r3 = rdlane_f32(v, 48);
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // The reference's silu (rce-tinyllama/src/lib.rs L164-166, rce-qwen36-moe
 // L459-461): x * sigmoid(x) with exp's argument kept non-positive, exp
 // being rce_exp.
@@ -221,13 +253,17 @@ hipError_t launch_rms_norm(const float *x, const float *w, size_t n, float eps, 
 // the layer's caches, and per query head the reference's online-softmax
 // attention over positions 0..pos (rce-op-attn L107-151, L185-251).
 // qkv: [q (n_q * d_head) | k (n_kv * d_head) | v (n_kv * d_head)];
-// rope_cs: [ctx_len][rope_dim / 2] (cos, sin) pairs; caches
-// [ctx_len][n_kv * d_head]; att: [n_q * d_head].  skip (may be null): when
-// skip[0] != 0 the step is a skipped one and appends nothing to the caches.
+// rope_cs: [ctx_len][rope_dim / 2] (cos, sin) pairs; caches of
+// ceil(ctx_len / 64) * 64 positions, values [position][n_kv * d_head], keys
+// in 64-position tiles (decoder.hip); att: [n_q * d_head].  skip (may be
+// null): when skip[0] != 0 the step is a skipped one and appends nothing to
+// the caches.
 hipError_t launch_attention(const float *qkv, const float *rope_cs, float *k_cache, float *v_cache,
                             const int *pos, int ctx_len, int n_q, int n_kv, int d_head, int rope_dim,
                             float scale, float *att, const int *skip, hipStream_t s);
-bool attention_supports(int d_head, int rope_dim);
+// d_head 64 or 128, rope_dim even and <= d_head, and one layer's cache
+// under 2 GiB (the kernel addresses it with 32-bit offsets).
+bool attention_supports(int d_head, int rope_dim, size_t ctx_len, size_t n_kv);
 // h = silu(g) * u, x = x + o: the unfused forms.
 hipError_t launch_swiglu(const float *g, const float *u, float *h, size_t n, hipStream_t s);
 hipError_t launch_add_inplace(float *x, const float *o, size_t n, hipStream_t s);

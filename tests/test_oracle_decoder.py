@@ -255,8 +255,9 @@ def test_attend_head_dev_is_the_same_softmax(seq, d_head):
     the values exactly as the reference's recurrence does (a key dropped or
     counted twice, a wrong run bound or a lost wave fails).  Random inputs:
     within 1e-6 of the reference's order.  Seq lengths cover waves without
-    keys (seq < 4), one partial run, several runs per wave, and the
-    32-key runs of d_head 128."""
+    keys (fewer than four runs), one partial run, several runs per wave
+    (more than four runs: 257 and 300 keys), and the 32-key runs of
+    d_head 128."""
     rng = np.random.default_rng(seq * 7 + d_head)
     kvd = 2 * d_head
     q = np.zeros(d_head, F32)
