@@ -74,10 +74,11 @@ __device__ float dequant_value(const DevWeight &w, size_t row, size_t i) {
     } else if (w.dtype == T_I2_S) {  // dequant.rs L222-256: scale * map2bit[code]
         const size_t blk = i / 128;
         const int within = (int)(i % 128), slot = within / 32, gp = within % 32;
-        const size_t byte = 32 * blk + gp;
-        const uint8_t x = *(w.base + (row >> 6) * w.group_stride + ((byte / 16) * 64 + (row & 63)) * 16 + byte % 16);
-        const int code = (x >> (6 - 2 * slot)) & 3;
-        const float m = code == 0 ? -1.0f : (code == 2 ? 1.0f : 0.0f);
+        const size_t j = 128 * blk + 4 * (size_t)gp + (size_t)slot;  // chain order
+        const uint8_t *cp = w.base + (row >> 6) * w.group_stride + (j / 64) * 1024 + (row & 63) * 8 + (j % 64) / 8;
+        const int bit = (int)(j % 8);
+        const bool plus = (cp[0] >> bit) & 1, minus = (cp[512] >> bit) & 1;
+        const float m = minus ? -1.0f : (plus ? 1.0f : 0.0f);
         v = *reinterpret_cast<const float *>(w.aux) * m;
     } else if (is_whole_element(w.dtype)) {  // dequant.rs L343-356: the value itself
         const size_t es = w.dtype == T_F32 ? 4 : 2, o = i * es;
@@ -282,9 +283,9 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane1 = pad16(2 * (k / 256));
         dw.row_stride = dw.plane1 + 64 * (k / 256);
         return dw.row_stride * n;
-    case T_I2_S:  // the codes in the 64-row interleave, then the tensor's f32 scale
-        dw.layout = LAYOUT_IL64_ROWS;
-        dw.group_stride = ((k / 4 + 15) / 16) * 1024;
+    case T_I2_S:  // the codes as bit planes in the 64-row groups, then the tensor's f32 scale
+        dw.layout = LAYOUT_I2S_PLANES;
+        dw.group_stride = (k / 64) * 1024;
         dw.plane1 = dw.group_stride * ((n + 63) / 64);
         return dw.plane1 + 16;
     case T_F32:
@@ -306,7 +307,8 @@ size_t plan_layout(DevWeight &dw) {
 size_t layout_pad_bytes(const DevWeight &dw) {
     const int U = units_per_row(dw.dtype, dw.n_cols);
     const size_t rows = 16 * (size_t)(U > 0 && U < 1024 ? 1024 / U : 1);  // the most rows a tile can add
-    if (dw.layout == LAYOUT_IL64_Q6_K || dw.layout == LAYOUT_IL64_ROWS) return ((rows + 63) / 64 + 1) * dw.group_stride;
+    if (dw.layout == LAYOUT_IL64_Q6_K || dw.layout == LAYOUT_IL64_ROWS || dw.layout == LAYOUT_I2S_PLANES)
+        return ((rows + 63) / 64 + 1) * dw.group_stride;
     return rows * dw.row_stride;
 }
 
@@ -447,9 +449,24 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
         }
         break;
     }
+    case LAYOUT_I2S_PLANES: {  // lib.rs L1478-1537: code 2 (+1) and code 0 (-1) as bit planes
+        const size_t rb = k / 4;
+        std::memcpy(dst + dw.plane1, src + n * rb, 4);  // the tensor's scale
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t *s = src + r * rb;
+            uint8_t *g = dst + (r >> 6) * dw.group_stride + (r & 63) * 8;
+            for (size_t j = 0; j < k; j++) {  // chain order: block b, byte gp, slot s
+                const size_t b = j / 128, gp = (j % 128) / 4, slot = j % 4;
+                const int code = (s[32 * b + gp] >> (6 - 2 * slot)) & 3;
+                uint8_t *cp = g + (j / 64) * 1024 + (j % 64) / 8;
+                if (code == 2) cp[0] |= (uint8_t)(1u << (j % 8));
+                if (code == 0) cp[512] |= (uint8_t)(1u << (j % 8));
+            }
+        }
+        break;
+    }
     case LAYOUT_IL64_ROWS: {
-        const size_t rb = dw.dtype == T_I2_S ? k / 4 : k * (dw.dtype == T_F32 ? 4 : 2);
-        if (dw.dtype == T_I2_S) std::memcpy(dst + dw.plane1, src + n * rb, 4);  // the tensor's scale
+        const size_t rb = k * (dw.dtype == T_F32 ? 4 : 2);
         for (size_t r = 0; r < n; r++) {
             uint8_t *g = dst + (r >> 6) * dw.group_stride + (r & 63) * 16;
             const uint8_t *s = src + r * rb;

@@ -60,15 +60,20 @@ enum Layout : int {
     // F32 / F16 / BF16: rows in groups of 64, each row cut into 16-byte
     // chunks, zero-padded to a multiple of CHAIN_STAGE chunks; chunk c of
     // row r at (c * 64 + r % 64) * 16 within the group's group_stride bytes.
-    // (I2_S: the same without the stage padding.)
     LAYOUT_IL64_ROWS = 9,
     // STQ1_0: the super-blocks' f16 d, padded to 16, then per super-block
     // u the 256 lane codes its codebook gives (64 B at plane1 + 64 u:
     // position p at bits 2 (p % 4) of byte p / 4; 0 = -1, 1 = 0, 2 = +1).
     // Q1_0 uses LAYOUT_SPLIT_Q4_0 (2-byte d + 16 bytes per block of 128)
-    // and Q2_0 LAYOUT_SPLIT_Q8_0 (2-byte d + 32 bytes); I2_S uses
-    // LAYOUT_IL64_ROWS with its f32 scale at plane1 (pointed to by aux).
+    // and Q2_0 LAYOUT_SPLIT_Q8_0 (2-byte d + 32 bytes).
     LAYOUT_SPLIT_STQ1_0 = 10,
+    // I2_S: the codes as two bit planes in the reference's chain order
+    // (element j of a row is position 128 b + 32 s + gp for j = 128 b +
+    // 4 gp + s), rows in groups of 64: chunk c (elements 64 c .. 64 c + 63)
+    // of a group is 1 KB at c * 1024, the plane P (code 2, +1) of its 64 rows
+    // as 8 bytes each (bit e = element 64 c + e), then the plane N (code 0,
+    // -1) likewise at + 512; the tensor's f32 scale at plane1 (aux).
+    LAYOUT_I2S_PLANES = 11,
 };
 
 struct DevWeight {
