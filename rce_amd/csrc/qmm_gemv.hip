@@ -526,8 +526,8 @@ static size_t unit_bytes(uint32_t dtype) {
 // and keep at least one block per CU; Q6_K (one 210-byte super-block per
 // thread-row, heavy activation slice) is best at 4 rows per thread.  With
 // several tokens, Q8 keeps up to 8 per block (the weight tile is read once
-// per block) and EXACT up to 4 (2 for Q4_K: 64 f32 activations per token
-// per thread).
+// per block) and EXACT 2, with 16 rows per lane where the grid keeps 256
+// blocks (below).
 GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
     GemvGeom g;
     const int U = units_per_row(w.dtype, w.n_cols);
@@ -576,6 +576,20 @@ GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode) {
         const bool heavy = (q8 && g.tb >= 4) || (!q8 && (g.tb >= 4 || (k4 && g.tb >= 2)));
         if (heavy && g.rpl > 4) g.rpl = 4;
         if (is_ternary_block(w.dtype) && g.rpl > 4) g.rpl = 4;  // 128 activations or 256-lane codes per row
+        if (!q8 && g.tb >= 2 && !is_ternary_block(w.dtype)) {
+            // Several tokens, EXACT: two tokens per block and the most rows
+            // per lane that leave 256 blocks (a sweep over tokens per block x
+            // rows per lane at 2-64 tokens, Q4_0 11008x4096, Q4_K and Q8_0
+            // 4096x4096: 16 rows per lane against 4 takes Q4_0 at 8 tokens
+            // from 51 to 40 us, Q8_0 from 23 to 15; more tokens per block
+            // hold more activations per lane and fewer waves fit a SIMD).
+            g.tb = 2;
+            auto blocks = [&](int rpl) {
+                return (w.n_rows + (size_t)P * rpl - 1) / ((size_t)P * rpl) * ((t_rows + 1) / 2);
+            };
+            g.rpl = 16;
+            while (g.rpl > 2 && blocks(g.rpl) < 256) g.rpl = g.rpl == 16 ? 12 : (g.rpl == 12 ? 8 : g.rpl / 2);
+        }
     }
     // shrink rows, then tokens, until the block's LDS fits
     while (gemv_lds_bytes(U, g.nt, g.rpl, g.tb, q8, w.n_cols) > LDS_MAX) {
