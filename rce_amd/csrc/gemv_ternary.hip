@@ -102,22 +102,26 @@ struct STQ1_0Unit {
     __device__ void init(const float *A, size_t k, int t0, int, int col) { ap = A + (size_t)t0 * k + 256 * (size_t)col; }
     __device__ void addends(const Raw &r, float *out) const {
         float pos = 0.0f, neg = 0.0f;
+        // Positions 64 seg .. 64 seg + 63: 16 code bytes, 64 activations;
+        // the next segment's activations are loaded while this one is
+        // summed (two segments live at a time; no reuse across rows).
+        float a[2][64];
+        load_f32x(ap, a[0], 64);
 #pragma unroll
-        for (int seg = 0; seg < 4; seg++) {  // positions 64 seg .. 64 seg + 63: 16 code bytes, 64 activations
+        for (int seg = 0; seg < 4; seg++) {
             const uint4 cw = r.c[seg];
-            float a[64];
-            load_f32x(ap + 64 * seg, a, 64);
+            if (seg < 3) load_f32x(ap + 64 * (seg + 1), a[(seg + 1) & 1], 64);
+            const float *as = a[seg & 1];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t x = wrd(cw, i);
 #pragma unroll
                 for (int l = 0; l < 16; l++) {
                     const uint32_t c = (x >> (2 * l)) & 3u;
-                    pos = pos + keep(a[16 * i + l], c == 2 ? ~0u : 0u);
-                    neg = neg + keep(a[16 * i + l], c == 0 ? ~0u : 0u);
+                    pos = pos + keep(as[16 * i + l], c == 2 ? ~0u : 0u);
+                    neg = neg + keep(as[16 * i + l], c == 0 ? ~0u : 0u);
                 }
             }
-            asm volatile("" ::: "memory");  // one segment's 64 activations live at a time (no reuse across rows)
         }
         const float t = pos - neg;
         out[0] = h2f(r.d) * t;
