@@ -504,6 +504,117 @@ def issue_rates(ctx, iters=200):
     return out
 
 
+def cache_warmth(hip, ctx, steps=200):
+    """The decode step's GEMV shapes timed three ways: weights rotated over
+    copies beyond 2 x the Infinity Cache (every read from HBM), over copies
+    within about 96 MB (Infinity Cache), and one copy (L2 and Infinity
+    Cache warm).  Equal times mean a launch is bound by its own latency, not
+    by where its bytes come from."""
+    import rce_amd
+    from rce_amd import GgufDtype as G, Mode
+    shapes = ((G.Q4K, 2048, 2048, "Q4_K 2048x2048 (wq, wo)"), (G.Q4K, 2560, 2048, "Q4_K 2560x2048 (q|k|v)"),
+              (G.Q4K, 11264, 2048, "Q4_K 11264x2048 (gate|up)"), (G.Q4K, 2048, 5632, "Q4_K 2048x5632 (down)"),
+              (G.Q4_0, 11008, 4096, "Q4_0 11008x4096 (headline)"))
+    out = {}
+    for dt, n, k, name in shapes:
+        size = make_weight(3, dt, n, k).size
+        plan = (("hbm", max(2, min(64, (2 * INFINITY_CACHE) // size + 1))), ("infinity_cache", max(2, (96 << 20) // size + 1)),
+                ("one_copy", 1))
+        for mode, mname in ((Mode.Q8, "q8"), (Mode.EXACT, "exact")):
+            row = {}
+            for where, copies in plan:
+                b = make_weight(3, dt, n, k)
+                ws = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k) for _ in range(copies)]
+                x = np.random.default_rng(4).standard_normal((1, k)).astype(np.float32)
+                xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+                o = rce_amd.DeviceBuffer(ctx, 4 * n)
+
+                def run(c):
+                    for i in range(c):
+                        rce_amd.mm_batched_dev(ctx, xa.ptr, G.F32, 1, ws[i % copies], o.ptr, mode)
+                settle(ctx, run, 0.1)
+                run(10)
+                ctx.synchronize()
+                ms = hip.timed_graph(ctx.stream, lambda: run(steps), steps)
+                for w in ws:
+                    w.close()
+                xa.free()
+                o.free()
+                row[where] = {"us": round(ms * 1e3, 3), "copies": copies}
+            out[f"{name} {mname}"] = row
+            log(f"  cache warmth {name} {mname}: " + "  ".join(f"{k2} {v['us']:.2f} us" for k2, v in row.items()))
+    return out
+
+
+def vendor_gemm(steps=40):
+    """AMD's library on the prefill shapes, no dequantization: torch.matmul
+    (hipBLASLt) of f16 and bf16 operands in this path's layout, A [m, k]
+    times W^T with W [n, k] row-major (a transposed 2-D view, which the
+    library takes as its transpose flag), weights rotated over copies
+    beyond 2 x the Infinity Cache, timed with events on torch's stream."""
+    import torch
+    out = {}
+    for m, n, k in ((512, 4096, 4096), (2048, 4096, 4096), (4096, 4096, 4096), (64, 14336, 4096)):
+        for dt, dname in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+            g = torch.Generator(device="cuda").manual_seed(1)
+            a = torch.randn(m, k, device="cuda", dtype=dt, generator=g)
+            copies = max(2, min(32, (2 * INFINITY_CACHE) // (2 * n * k) + 1))
+            ws = [torch.randn(n, k, device="cuda", dtype=dt, generator=g) for _ in range(copies)]
+            for i in range(5):
+                torch.matmul(a, ws[i % copies].t())
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(steps):
+                torch.matmul(a, ws[i % copies].t())
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            tf = 2.0 * m * n * k / (us * 1e-6) / 1e12
+            out[f"{m}x{n}x{k} {dname}"] = {"us": round(us, 2), "tflops": round(tf, 1),
+                                            "frac_of_dense_peak": round(tf / MFMA_F16_PEAK_TFS, 4)}
+            log(f"  vendor GEMM {m}x{n}x{k} {dname}: {us:.2f} us  {tf:.0f} TFLOP/s")
+            del ws, a
+    return out
+
+
+def handoff(hip, ctx, steps=200):
+    """rce_qmm_handoff_probe_dev: microseconds per launch (graph replay) of n
+    blocks that each store 64 floats, without a hand-off (mode 0), with the
+    last-block-done hand-off through __threadfence and one device-scope
+    counter (mode 1), and with agent-scope atomic stores and loads instead
+    of the fence (mode 2)."""
+    import rce_amd
+    from rce_amd import _lib
+    L = _lib.lib()
+    data = rce_amd.DeviceBuffer(ctx, 4 * 64 * 512)
+    cnt = rce_amd.DeviceBuffer(ctx, 256)
+    res = rce_amd.DeviceBuffer(ctx, 4 * 256)
+    hip.ok(hip.L.hipMemset(ctypes.c_void_p(cnt.ptr), 0, 256), "hipMemset")
+    hip.ok(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    out = {}
+    for blocks in (32, 160, 512):
+        row = {}
+        for mode, mname in ((0, "stores_only"), (1, "threadfence_counter"), (2, "atomic_stores_counter")):
+            def run(c):
+                for _ in range(c):
+                    _lib.check(L.rce_qmm_handoff_probe_dev(ctx.handle, mode, blocks, ctypes.c_void_p(data.ptr),
+                                                           ctypes.c_void_p(cnt.ptr), ctypes.c_void_p(res.ptr),
+                                                           ctypes.c_void_p(ctx.stream)))
+            run(5)
+            ctx.synchronize()
+            row[mname] = round(hip.timed_graph(ctx.stream, lambda: run(steps), steps) * 1e3, 2)
+        left = int(cnt.download(np.uint32, 1)[0])
+        if left != 0:
+            raise RuntimeError(f"hand-off probe left its counter at {left}")
+        out[f"{blocks}_blocks_us"] = row
+        log(f"  hand-off {blocks} blocks: " + "  ".join(f"{k2} {v:.2f} us" for k2, v in row.items()))
+    data.free()
+    cnt.free()
+    res.free()
+    return out
+
+
 def copy_calibration(hip, nbytes=256 << 20, reps=8):
     """Device-to-device copies of a known size: the reference reading for the
     FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = nbytes)."""
@@ -535,6 +646,12 @@ def main():
     ap.add_argument("--no-ceiling", action="store_true", help="skip the read-ceiling launches (profiling runs)")
     ap.add_argument("--issue-rates", action="store_true",
                     help="also report the instruction issue-rate probes (shader cycles per instruction)")
+    ap.add_argument("--cache-warmth", action="store_true",
+                    help="also time the decode-step GEMV shapes with weights from HBM, the Infinity Cache and one copy")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time AMD's library (torch.matmul, f16 / bf16) on the prefill shapes")
+    ap.add_argument("--handoff", action="store_true",
+                    help="also measure the cost of a cross-block hand-off (rce_qmm_handoff_probe_dev)")
     ap.add_argument("--sweep-only", default="",
                     help="run only the sweep rows whose name contains this text (e.g. 'b8'; profiling)")
     args = ap.parse_args()
@@ -664,6 +781,12 @@ def main():
     if args.issue_rates:
         line["issue_rates"] = issue_rates(ctx)
         log(f"  issue rates: {json.dumps(line['issue_rates'])}")
+    if args.cache_warmth:
+        line["cache_warmth"] = cache_warmth(hip, ctx)
+    if args.vendor_gemm:
+        line["vendor_gemm"] = vendor_gemm()
+    if args.handoff:
+        line["handoff"] = handoff(hip, ctx)
 
     # ---- CPU baseline + parity checks (oracle) -------------------------------------
     if not args.no_cpu:

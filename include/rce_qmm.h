@@ -445,6 +445,18 @@ rce_qmm_status rce_qmm_read_ceiling_dev(rce_qmm_context *ctx, const void *buf_de
 rce_qmm_status rce_qmm_issue_rate_dev(rce_qmm_context *ctx, int kind, int threads, int blocks, int iters,
                                       void *cycles_dev, void *sink_dev, void *stream);
 
+/* No counterpart in the reference: the cost of a cross-block hand-off (for
+ * bench.py --handoff; a measurement, not part of the matmul path).  One
+ * launch of `blocks` blocks of 256 threads, each storing 64 floats into
+ * data_dev (4 * 64 * blocks bytes).  mode 0: nothing more; mode 1: each
+ * block then does __threadfence() and one device-scope increment of
+ * *counter_dev, and the block that completes the count reads all blocks'
+ * floats into result_dev (256 floats) and resets the counter; mode 2: the
+ * same with agent-scope atomic stores and loads instead of the fence.
+ * counter_dev (4 bytes) must be zero before the first call. */
+rce_qmm_status rce_qmm_handoff_probe_dev(rce_qmm_context *ctx, int mode, int blocks, void *data_dev,
+                                         void *counter_dev, void *result_dev, void *stream);
+
 /* ---- device memory helpers (for callers without a HIP runtime) ---------- */
 
 rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out);

@@ -166,7 +166,71 @@ __global__ __launch_bounds__(1024) void k_issue(unsigned long long *__restrict__
     }
 }
 
+// Cross-block hand-off cost: every block of the launch stores 64 floats;
+// MODE 0 ends there; MODE 1 then makes them visible device-wide the
+// memory model's way (__threadfence: L2 write-back and invalidate) and
+// counts itself in one device-scope counter, and the block that sees the
+// count complete reads every block's floats (the last-block-done pattern a
+// kernel would use to run a dependent stage without a second launch);
+// MODE 2 does the same with agent-scope atomic stores and loads instead of
+// the L2 write-back.  The counter is reset by that last block, so every
+// launch starts from zero.  No block waits for another (no spin).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_handoff(float *__restrict__ data, unsigned *__restrict__ cnt,
+                                                 float *__restrict__ res, int nblk) {
+    const int tid = threadIdx.x;
+    __shared__ int last;
+    float v = (float)(blockIdx.x * 256 + tid) * 0.001f;
+    if (tid < 64) {
+        if constexpr (MODE == 2)
+            __hip_atomic_store(data + blockIdx.x * 64 + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            data[blockIdx.x * 64 + tid] = v;
+    }
+    if constexpr (MODE == 0) return;
+    if constexpr (MODE == 1) __threadfence();
+    if constexpr (MODE == 2) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == (unsigned)nblk - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    if constexpr (MODE == 1) __threadfence();
+    float sum = 0.0f;
+    for (int i = tid; i < nblk * 64; i += 256) {
+        float x;
+        if constexpr (MODE == 2) x = __hip_atomic_load(data + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else x = data[i];
+        sum += x;
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    res[tid] = sum;
+}
+
 }  // namespace
+
+/* No counterpart in the reference: cross-block hand-off probe (see k_handoff). */
+extern "C" rce_qmm_status rce_qmm_handoff_probe_dev(rce_qmm_context *ctx, int mode, int blocks, void *data_dev,
+                                                    void *counter_dev, void *result_dev, void *stream) {
+    using namespace rce_qmm_abi;
+    if (!ctx || !data_dev || !counter_dev || !result_dev) return fail(RCE_QMM_NULL_ARGUMENT, "null argument");
+    if (blocks <= 0 || blocks > 65536) return fail(RCE_QMM_BAD_SHAPE, "blocks in 1..65536");
+    rce_qmm_status st = set_device(ctx->device);
+    if (st) return st;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    float *d = static_cast<float *>(data_dev), *r = static_cast<float *>(result_dev);
+    unsigned *c = static_cast<unsigned *>(counter_dev);
+    switch (mode) {
+    case 0: hipLaunchKernelGGL(k_handoff<0>, dim3(blocks), dim3(256), 0, s, d, c, r, blocks); break;
+    case 1: hipLaunchKernelGGL(k_handoff<1>, dim3(blocks), dim3(256), 0, s, d, c, r, blocks); break;
+    case 2: hipLaunchKernelGGL(k_handoff<2>, dim3(blocks), dim3(256), 0, s, d, c, r, blocks); break;
+    default: return fail(RCE_QMM_BAD_SHAPE, "hand-off mode must be 0..2");
+    }
+    HIP_TRY(hipGetLastError());
+    return RCE_QMM_OK;
+}
 
 /* No counterpart in the reference: instruction issue-rate probes (see k_issue). */
 extern "C" rce_qmm_status rce_qmm_issue_rate_dev(rce_qmm_context *ctx, int kind, int threads, int blocks, int iters,
