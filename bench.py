@@ -546,6 +546,21 @@ def cache_warmth(hip, ctx, steps=200):
     return out
 
 
+def read_ceilings(hip, ctx, steps=200):
+    """The read ceiling (read_ceiling) at the byte counts of the decode step's
+    weights and of the headline: what a single launch that only streams
+    that many bytes takes, launch cost included."""
+    out = {}
+    for name, nbytes in (("Q4_K 2048x2048", 2359296), ("Q4_K 2560x2048", 2949120), ("Q4_K 2048x5632", 6488064),
+                         ("Q4_K 11264x2048", 12976128), ("Q4_0 11008x4096 (headline)", 25422848),
+                         ("Q6_K 32000x2048", 53760000)):
+        us, var, empty = read_ceiling(hip, ctx, nbytes, steps)
+        out[name] = {"bytes": nbytes, "us": round(us, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "variant": var, "empty_launch_us": round(empty, 3)}
+        log(f"  read ceiling {name} ({nbytes} B): {us:.2f} us ({nbytes / (us * 1e-6) / 1e9:.0f} GB/s)")
+    return out
+
+
 def vendor_gemm(steps=40):
     """AMD's library on the prefill shapes, no dequantization: torch.matmul
     (hipBLASLt) of f16 and bf16 operands in this path's layout, A [m, k]
@@ -650,6 +665,8 @@ def main():
                     help="also time the decode-step GEMV shapes with weights from HBM, the Infinity Cache and one copy")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time AMD's library (torch.matmul, f16 / bf16) on the prefill shapes")
+    ap.add_argument("--read-ceilings", action="store_true",
+                    help="also measure the read ceiling at the decode step's weight sizes")
     ap.add_argument("--handoff", action="store_true",
                     help="also measure the cost of a cross-block hand-off (rce_qmm_handoff_probe_dev)")
     ap.add_argument("--sweep-only", default="",
@@ -783,6 +800,8 @@ def main():
         log(f"  issue rates: {json.dumps(line['issue_rates'])}")
     if args.cache_warmth:
         line["cache_warmth"] = cache_warmth(hip, ctx)
+    if args.read_ceilings:
+        line["read_ceilings"] = read_ceilings(hip, ctx)
     if args.vendor_gemm:
         line["vendor_gemm"] = vendor_gemm()
     if args.handoff:
