@@ -355,6 +355,20 @@ __global__ __launch_bounds__(64 * ATT_NW) __attribute__((amdgpu_waves_per_eu(1, 
         m = m_new;
     }
     float *out = att + (size_t)h * DH;
+    if (seq <= CH) {
+        // Wave 0 holds every key (the other waves have left): the merge
+        // below would weigh it by exp(m - m) = 1 and add it to +0.0, which
+        // gives its (o, l) back unchanged (o is never -0.0), so out = o / l
+        // directly, without the LDS round trip and the barrier.
+        if (kk == 0) {
+            const float inv = 1.0f / l;
+            float4 r;
+#pragma unroll
+            for (int e = 0; e < 4; e++) f4e(r, e) = f4e(o, e) * inv;
+            *reinterpret_cast<float4 *>(out + 4 * dq) = r;
+        }
+        return;
+    }
     if (kk == 0) *reinterpret_cast<float4 *>(&mo[wave][4 * dq]) = o;
     if (lane == 0) {
         mo[wave][DH] = m;
