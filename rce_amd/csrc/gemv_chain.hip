@@ -7,6 +7,7 @@
 // c (16 B) of the 64 rows of a group is one contiguous 1 KB read.  The
 // token's activations are first copied to LDS (k <= CHAIN_MAX_K), where
 // every lane reads the same address (a broadcast).
+#include "gemv_chain_pipe.h"
 #include "qmm_gemv_kernels.h"
 
 namespace rce_qmm {
@@ -39,49 +40,6 @@ __device__ __forceinline__ float chunk_value(const uint4 &v, int e) {
             asm volatile("v_lshlrev_b32 %0, 16, %1" : "=v"(r) : "v"(x));
         return __uint_as_float(r);
     }
-}
-
-// The chain wave's side of the stage pipeline shared by the kernels below:
-// s_tot barriers; after barrier s the stage s addends are in LDS slot s % 2
-// (float4 q of a stage at prod[(slot * SV / 4 + q) * LN], prod already at
-// the lane's chain).  Half stages rotate through two register sets: the
-// reads of one half are issued before the adds of the half before it, so
-// the LDS latency hides behind 4 * (SV / 8) adds, and the chain adds
-// every stage below ns in order.
-template <int SV, int LN>
-__device__ __forceinline__ float run_chain(const float4 *prod, int ns, int s_tot) {
-    constexpr int HQ = SV / 8;  // float4 per half stage
-    static_assert(HQ * 8 == SV, "half stages of whole float4");
-    float4 r1[HQ], r2[HQ];
-    float acc = 0.0f;
-    auto rd = [&](int s, int half, float4 *v) {
-        const float4 *p = prod + ((size_t)(s & 1) * (SV / 4) + half * HQ) * LN;
-#pragma unroll
-        for (int q = 0; q < HQ; q++) v[q] = p[q * LN];
-    };
-    auto add = [&](int s, const float4 *v) {
-        if (s >= ns) return;
-#pragma unroll
-        for (int q = 0; q < HQ; q++) {
-            acc = acc + v[q].x;
-            acc = acc + v[q].y;
-            acc = acc + v[q].z;
-            acc = acc + v[q].w;
-        }
-    };
-    __syncthreads();
-    rd(0, 0, r1);
-    rd(0, 1, r2);
-    add(0, r1);
-    for (int s = 1; s < s_tot; s++) {
-        __syncthreads();  // stage s written; stage s - 1's slot free for stage s + 1
-        rd(s, 0, r1);
-        add(s - 1, r2);
-        rd(s, 1, r2);
-        add(s, r1);
-    }
-    add(s_tot - 1, r2);
-    return acc;
 }
 
 // One block serves RB rows (16, 32 or 64) of a 64-row group.  Wave 0 holds
@@ -142,26 +100,8 @@ __global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_chain(DevWeight w, 
 #pragma unroll
         for (int j = 0; j < R; j++) ring[j] = bld16(wb, 0, soff_of(j));
     }
-    {  // the token's activations, zeros up to the padded row: all loads
-       // first; no branch (stores past the row go to the dump slot), so the
-       // loads are known complete after the stores
-        constexpr int U = 24;
-        const size_t kp = (size_t)nc * E;
-        const float *a = A + t * k;
-        for (size_t i0 = 0; i0 < kp; i0 += (size_t)NT * U) {
-            float v[U];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const size_t i = i0 + (size_t)u * NT + tid;
-                v[u] = a[i < k ? i : k - 1];
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const size_t i = i0 + (size_t)u * NT + tid;
-                act[i < kp ? i : kp] = i < k ? v[u] : 0.0f;
-            }
-        }
-    }
+    // the token's activations, zeros up to the padded row
+    stage_act<NT, 24>(A + t * k, k, (size_t)nc * E, act, [](size_t i) { return i; });
     __syncthreads();
     if (wv == 0) {
         const float acc = run_chain<SV, RB>(prod + r, ns, s_tot);
@@ -266,23 +206,8 @@ __global__ __launch_bounds__(320) void k_gemv_chain_i2s(DevWeight w, const float
 #pragma unroll
         for (int j = 0; j < I2S_DS; j++) ring[j] = bld4(wb, 0, soff_of(j));
     }
-    {  // activations in chain order: all loads first, stores past k to the dump slot
-        constexpr int U = 16;
-        const float *a = A + t * k;
-        for (size_t i0 = 0; i0 < k; i0 += (size_t)NT * U) {
-            float v[U];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const size_t i = i0 + (size_t)u * NT + tid;
-                v[u] = a[i < k ? i : k - 1];
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const size_t i = i0 + (size_t)u * NT + tid, r = i % 128;
-                act[i < k ? i - r + 4 * (r % 32) + r / 32 : k] = v[u];
-            }
-        }
-    }
+    // the activations in chain order
+    stage_act<NT, 16>(A + t * k, k, k, act, [](size_t i) { const size_t r = i % 128; return i - r + 4 * (r % 32) + r / 32; });
     __syncthreads();
     if (wv == 0) {
         const float acc = run_chain<SV, 64>(prod + lane, ns, s_tot);

@@ -1,11 +1,13 @@
-// gemv_q6_k.hip -- the Q6_K decode kernels (EXACT: one lane per row; Q8).
+// gemv_q6_k.hip -- the Q6_K decode kernels (EXACT: one chain lane per row; Q8).
+#include "gemv_chain_pipe.h"
 #include "qmm_gemv_kernels.h"
 
 namespace rce_qmm {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Q6_K EXACT: one lane per row (the row sum is a single chain).
+// Q6_K EXACT: one lane per row (the row sum is a single chain); this form,
+// which also forms its own products, serves rows longer than the LDS holds.
 // ---------------------------------------------------------------------------
 
 // rce-op-qmm/src/lib.rs L425-454, L1667-1705: per half o, l in 0..32, the
@@ -83,16 +85,151 @@ __global__ __launch_bounds__(256) void k_gemv_exact_q6k(DevWeight w, const float
     if (row < w.n_rows) out[(size_t)blockIdx.y * w.n_rows + row] = sumf;
 }
 
+// The same row chains with the products formed by helper waves (the
+// pipeline of gemv_chain_pipe.h), for k <= Q6_EXACT_LDS_K.  A block serves
+// RB rows (16, 32 or 64) of a 64-row group; wave 0 holds the chains, waves
+// 1..H (H = RB / 16) the products.  A stage is one half o of a super-block:
+// chain steps l = 0..31, m = 0..3 (position 128 o + l + 32 m), written as
+// float4 (m = 0..3) per l.  Helper lane (row r, pair p = 0..3) forms the
+// steps of l = 8 p .. 8 p + 7 (lq = 2 p, 2 p + 1) from 8-byte slices of the
+// ql, qh and scale chunks and the row's d.
+constexpr int Q6_DS = 8;  // stages of loads a helper keeps in flight
+
+template <int RB>
+__global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_exact_q6k_split(DevWeight w, const float *__restrict__ A,
+                                                                              float *__restrict__ out) {
+    constexpr int SV = 128;
+    constexpr int H = RB / 16;
+    constexpr int NT = 64 * (1 + H);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t t = blockIdx.y, row0 = (size_t)blockIdx.x * RB;
+    const size_t k = w.n_cols;
+    const int ns = (int)(k / SV);  // two stages per super-block
+    const int s_tot = (ns + Q6_DS - 1) / Q6_DS * Q6_DS;
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *act = reinterpret_cast<float *>(lds);  // k values, then a 16-byte dump slot
+    float4 *prod = reinterpret_cast<float4 *>(act + k + 4);  // [2][32][RB]
+    const int r = lane % RB, hw = wv - 1;
+    const int p = hw * (64 / RB) + lane / RB;  // this helper lane's pair of lq groups
+    const int c = p >> 1;                      // ql / qh chunk within the half, and is = l / 16
+    const uint32_t rl = (uint32_t)(row0 % 64 + r);
+    const uint8_t *gb = w.base + (row0 / 64) * w.group_stride;
+    const WBuf wq = make_wbuf(gb, rl * 16 + 8 * (p & 1));  // the pair's 8 bytes of a chunk
+    const WBuf ws = make_wbuf(gb, rl * 16);                // scale chunk
+    const WBuf wd = make_wbuf(gb, rl * 2);                 // d
+    struct Slice { uint2 qa, qb, qh, sc; uint32_t d; };
+    // stage s: super-block s / 2, half s % 2; stages past the row load the last one (not used)
+    auto load = [&](int s, Slice &v) {
+        const int sc = min(s, ns - 1), o = sc & 1;
+        const uint32_t so = (uint32_t)(sc >> 1) * (uint32_t)IL64_Q6K_SB;
+        v.qa = bld8(wq, (uint32_t)(4 * o + c) * 1024u, so);
+        v.qb = bld8(wq, (uint32_t)(4 * o + 2 + c) * 1024u, so);
+        v.qh = bld8(wq, (uint32_t)(8 + 2 * o + c) * 1024u, so);
+        v.sc = bld8(ws, 12u * 1024u + 8u * (uint32_t)o, so);
+        v.d = bld2(wd, (uint32_t)IL64_Q6K_D, so);
+    };
+    Slice ring[Q6_DS];
+    if (wv != 0) {
+#pragma unroll
+        for (int j = 0; j < Q6_DS; j++) load(j, ring[j]);
+    }
+    stage_act<NT, 16>(A + t * k, k, k, act, [](size_t i) { return i; });
+    __syncthreads();
+    if (wv == 0) {
+        const float acc = run_chain<SV, RB>(prod + r, ns, s_tot);
+        const size_t row = row0 + lane;
+        if (lane < RB && row < w.n_rows) out[t * w.n_rows + row] = acc;
+        return;
+    }
+    // a stage's activations (positions 4 lq + 32 m .. + 3 of the half, for
+    // this lane's two lq), read during the stage before
+    float4 an[2][2][4];
+    auto read_act = [&](int s, float4 (*dst)[4]) {
+        const float *ah = act + (size_t)min(s, ns - 1) * SV;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int m = 0; m < 4; m++) dst[h][m] = *reinterpret_cast<const float4 *>(ah + 4 * (2 * p + h) + 32 * m);
+    };
+    read_act(0, an[0]);
+    for (int s0 = 0; s0 < s_tot; s0 += Q6_DS) {
+#pragma unroll
+        for (int u = 0; u < Q6_DS; u++) {
+            const int s = s0 + u;
+            read_act(s + 1, an[(u + 1) & 1]);
+            const Slice v = ring[u];
+            // (d sc) per m as the reference forms it, and -32 (d sc) for the
+            // fma that rounds (q - 32) (d sc) once
+            const float d = h2f(v.d);
+            float ds[4], nn[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int bi = c + 2 * m;  // scale byte 8 o + is + 2 m within the half's 8 bytes
+                const uint32_t wsc = (bi >> 2) ? v.sc.y : v.sc.x;
+                ds[m] = d * (float)(int)(int8_t)((wsc >> (8 * (bi & 3))) & 0xFFu);
+                nn[m] = -32.0f * ds[m];
+            }
+            float4 pr[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t qa = h ? v.qa.y : v.qa.x, qb = h ? v.qb.y : v.qb.x, qh = h ? v.qh.y : v.qh.x;
+                const uint32_t uq[4] = {(qa & NIB) | ((qh & 0x03030303u) << 4), (qb & NIB) | ((qh & 0x0C0C0C0Cu) << 2),
+                                        ((qa >> 4) & NIB) | (qh & 0x30303030u),
+                                        ((qb >> 4) & NIB) | ((qh >> 2) & 0x30303030u)};
+                float pj[4][4];  // [J][m]
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const float4 x = an[u & 1][h][m];
+                    const float xa[4] = {x.x, x.y, x.z, x.w};
+                    pj[0][m] = __builtin_fmaf(ubyte<0>(uq[m]), ds[m], nn[m]) * xa[0];
+                    pj[1][m] = __builtin_fmaf(ubyte<1>(uq[m]), ds[m], nn[m]) * xa[1];
+                    pj[2][m] = __builtin_fmaf(ubyte<2>(uq[m]), ds[m], nn[m]) * xa[2];
+                    pj[3][m] = __builtin_fmaf(ubyte<3>(uq[m]), ds[m], nn[m]) * xa[3];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) pr[h][j] = make_float4(pj[j][0], pj[j][1], pj[j][2], pj[j][3]);
+            }
+            load(s + Q6_DS, ring[u]);  // the slot's next stage once this one is used
+            float4 *pp = prod + (size_t)(s & 1) * (SV / 4) * RB + r;
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) pp[(size_t)(4 * (2 * p + h) + j) * RB] = pr[h][j];
+            __syncthreads();
+        }
+    }
+}
+
+template <int RB>
+hipError_t launch_q6_split(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
+    static bool attr_set = false;  // per process; the attribute is per function
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_exact_q6k_split<RB>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const size_t lds = (w.n_cols + 4) * sizeof(float) + 2 * 128 * (size_t)RB * sizeof(float);
+    const dim3 grid((unsigned)((w.n_rows + RB - 1) / RB), (unsigned)t_rows);
+    hipLaunchKernelGGL(k_gemv_exact_q6k_split<RB>, grid, dim3(64 * (1 + RB / 16)), lds, s, w, a, out);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out, int mode,
                             hipStream_t s) {
     if (mode == 0) {
+        if (w.n_cols <= Q6_EXACT_LDS_K) {
+            // rows per block: 64 while that leaves a block per CU, else 32 or 16
+            const size_t groups = (w.n_rows + 63) / 64 * t_rows;
+            if (groups >= 256) return launch_q6_split<64>(w, a, t_rows, out, s);
+            if (2 * groups >= 256) return launch_q6_split<32>(w, a, t_rows, out, s);
+            return launch_q6_split<16>(w, a, t_rows, out, s);
+        }
         dim3 grid((unsigned)((w.n_rows + 255) / 256), (unsigned)t_rows);
-        if (w.n_cols <= Q6_EXACT_LDS_K)
-            hipLaunchKernelGGL(k_gemv_exact_q6k<true>, grid, dim3(256), w.n_cols * sizeof(float), s, w, a, out);
-        else
-            hipLaunchKernelGGL(k_gemv_exact_q6k<false>, grid, dim3(256), 0, s, w, a, out);
+        hipLaunchKernelGGL(k_gemv_exact_q6k<false>, grid, dim3(256), 0, s, w, a, out);
         return hipGetLastError();
     }
     return launch_as_tb<Q6_KQ8, true, 2>(w, g, a, t_rows, out, s);

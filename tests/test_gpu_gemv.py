@@ -88,6 +88,25 @@ def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
     assert np.array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("dt", [O.F16, O.BF16, O.F32, O.Q6_K])
+@pytest.mark.parametrize("n,t_rows", [(4100, 1), (4100, 3), (8200, 1), (8200, 3), (16448, 1)])
+def test_row_chain_block_shapes(ctx, dt, n, t_rows):
+    """The row-chain kernels (one chain lane per row, helper waves forming the
+    addends) take 16, 32 or 64 rows per block by the count of 64-row groups
+    times tokens (4100 x 1: 16; 4100 x 3 and 8200 x 1: 32; 8200 x 3 and
+    16448 x 1: 64), each with a ragged last group; all must equal the
+    reference order bit for bit."""
+    k = 256 if dt == O.Q6_K else 200
+    note(f"row chain dtype={dt} n={n} t={t_rows} k={k}")
+    rng = np.random.default_rng(2500 + dt + n + t_rows)
+    b = make(rng, dt, n, k)
+    x = rng.standard_normal((t_rows, k)).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = rce_amd.mm_batched(x, t_rows, w)
+    want = O.mm_batched(x, b, dt, n, k)
+    assert np.array_equal(bits(got), bits(want)), f"{np.sum(bits(got) != bits(want))} values differ"
+
+
 def run_dev(ctx, w, x, mode, a_dtype=G.F32):
     t_rows = x.shape[0]
     xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
