@@ -87,46 +87,43 @@ __global__ __launch_bounds__(256) void k_gemv_exact_q6k(DevWeight w, const float
 
 // The same row chains with the products formed by helper waves (the
 // pipeline of gemv_chain_pipe.h), for k <= Q6_EXACT_LDS_K.  A block serves
-// RB rows (16, 32 or 64) of a 64-row group; wave 0 holds the chains, waves
-// 1..H (H = RB / 16) the products.  A stage is one half o of a super-block:
-// chain steps l = 0..31, m = 0..3 (position 128 o + l + 32 m), written as
-// float4 (m = 0..3) per l.  Helper lane (row r, pair p = 0..3) forms the
-// steps of l = 8 p .. 8 p + 7 (lq = 2 p, 2 p + 1) from 8-byte slices of the
-// ql, qh and scale chunks and the row's d.
+// 64 rows of a group with four waves, one per SIMD: wave 0 holds the chains,
+// waves 1..3 form the products (a fifth wave would share the chain's SIMD
+// and the chain, which every barrier waits for, would get half its issue
+// slots).  The unit of work is a pair: steps l = 8 p .. 8 p + 7, m = 0..3
+// (positions 128 o + l + 32 m) of half o of a super-block, pairs numbered
+// g = 8 sb + 4 o + p in the chain's order.  Stage s is pairs 3 s .. 3 s + 2,
+// helper h forming pair 3 s + h - 1 from 8-byte slices of its ql, qh and
+// scale chunks and the rows' d; pairs past the row give +0.0 products, which
+// leave a chain (from +0.0, never -0.0) unchanged.
 constexpr int Q6_DS = 8;  // stages of loads a helper keeps in flight
 
-template <int RB>
-__global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_exact_q6k_split(DevWeight w, const float *__restrict__ A,
-                                                                              float *__restrict__ out) {
-    constexpr int SV = 128;
-    constexpr int H = RB / 16;
-    constexpr int NT = 64 * (1 + H);
+__global__ __launch_bounds__(256) void k_gemv_exact_q6k_split(DevWeight w, const float *__restrict__ A,
+                                                              float *__restrict__ out) {
+    constexpr int SV = 96;  // chain steps per stage: 3 pairs
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const size_t t = blockIdx.y, row0 = (size_t)blockIdx.x * RB;
+    const size_t t = blockIdx.y, row0 = (size_t)blockIdx.x * 64;
     const size_t k = w.n_cols;
-    const int ns = (int)(k / SV);  // two stages per super-block
+    const int np = (int)(k / 256) * 8;  // pairs in a row
+    const int ns = (np + 2) / 3;
     const int s_tot = (ns + Q6_DS - 1) / Q6_DS * Q6_DS;
     extern __shared__ __align__(16) unsigned char lds[];
     float *act = reinterpret_cast<float *>(lds);  // k values, then a 16-byte dump slot
-    float4 *prod = reinterpret_cast<float4 *>(act + k + 4);  // [2][32][RB]
-    const int r = lane % RB, hw = wv - 1;
-    const int p = hw * (64 / RB) + lane / RB;  // this helper lane's pair of lq groups
-    const int c = p >> 1;                      // ql / qh chunk within the half, and is = l / 16
-    const uint32_t rl = (uint32_t)(row0 % 64 + r);
+    float4 *prod = reinterpret_cast<float4 *>(act + k + 4);  // [2][24][64]
+    const int hw = wv - 1;
     const uint8_t *gb = w.base + (row0 / 64) * w.group_stride;
-    const WBuf wq = make_wbuf(gb, rl * 16 + 8 * (p & 1));  // the pair's 8 bytes of a chunk
-    const WBuf ws = make_wbuf(gb, rl * 16);                // scale chunk
-    const WBuf wd = make_wbuf(gb, rl * 2);                 // d
+    const WBuf wq = make_wbuf(gb, (uint32_t)lane * 16);  // chunk slices
+    const WBuf wd = make_wbuf(gb, (uint32_t)lane * 2);   // d
     struct Slice { uint2 qa, qb, qh, sc; uint32_t d; };
-    // stage s: super-block s / 2, half s % 2; stages past the row load the last one (not used)
+    // pair g's slices (g past the row: the last pair's, not used)
     auto load = [&](int s, Slice &v) {
-        const int sc = min(s, ns - 1), o = sc & 1;
-        const uint32_t so = (uint32_t)(sc >> 1) * (uint32_t)IL64_Q6K_SB;
-        v.qa = bld8(wq, (uint32_t)(4 * o + c) * 1024u, so);
-        v.qb = bld8(wq, (uint32_t)(4 * o + 2 + c) * 1024u, so);
-        v.qh = bld8(wq, (uint32_t)(8 + 2 * o + c) * 1024u, so);
-        v.sc = bld8(ws, 12u * 1024u + 8u * (uint32_t)o, so);
+        const int g = min(3 * s + hw, np - 1), o = (g >> 2) & 1, p = g & 3, c = p >> 1;
+        const uint32_t so = (uint32_t)(g >> 3) * (uint32_t)IL64_Q6K_SB, b8 = 8u * (uint32_t)(p & 1);
+        v.qa = bld8(wq, (uint32_t)(4 * o + c) * 1024u + b8, so);
+        v.qb = bld8(wq, (uint32_t)(4 * o + 2 + c) * 1024u + b8, so);
+        v.qh = bld8(wq, (uint32_t)(8 + 2 * o + c) * 1024u + b8, so);
+        v.sc = bld8(wq, 12u * 1024u + 8u * (uint32_t)o, so);
         v.d = bld2(wd, (uint32_t)IL64_Q6K_D, so);
     };
     Slice ring[Q6_DS];
@@ -134,23 +131,24 @@ __global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_exact_q6k_split(Dev
 #pragma unroll
         for (int j = 0; j < Q6_DS; j++) load(j, ring[j]);
     }
-    stage_act<NT, 16>(A + t * k, k, k, act, [](size_t i) { return i; });
+    stage_act<256, 16>(A + t * k, k, k, act, [](size_t i) { return i; });
     __syncthreads();
     if (wv == 0) {
-        const float acc = run_chain<SV, RB>(prod + r, ns, s_tot);
+        const float acc = run_chain<SV, 64>(prod + lane, ns, s_tot);
         const size_t row = row0 + lane;
-        if (lane < RB && row < w.n_rows) out[t * w.n_rows + row] = acc;
+        if (row < w.n_rows) out[t * w.n_rows + row] = acc;
         return;
     }
-    // a stage's activations (positions 4 lq + 32 m .. + 3 of the half, for
-    // this lane's two lq), read during the stage before
+    // the pair's 32 activations (positions 8 p + 4 h + 32 m .. + 3 of its
+    // half, h = 0, 1), read during the stage before
     float4 an[2][2][4];
     auto read_act = [&](int s, float4 (*dst)[4]) {
-        const float *ah = act + (size_t)min(s, ns - 1) * SV;
+        const int g = min(3 * s + hw, np - 1);
+        const float *ah = act + (size_t)(g >> 3) * 256 + 128 * ((g >> 2) & 1) + 8 * (g & 3);
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int m = 0; m < 4; m++) dst[h][m] = *reinterpret_cast<const float4 *>(ah + 4 * (2 * p + h) + 32 * m);
+            for (int m = 0; m < 4; m++) dst[h][m] = *reinterpret_cast<const float4 *>(ah + 4 * h + 32 * m);
     };
     read_act(0, an[0]);
     for (int s0 = 0; s0 < s_tot; s0 += Q6_DS) {
@@ -159,6 +157,7 @@ __global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_exact_q6k_split(Dev
             const int s = s0 + u;
             read_act(s + 1, an[(u + 1) & 1]);
             const Slice v = ring[u];
+            const int g = 3 * s + hw, c = (g & 3) >> 1;
             // (d sc) per m as the reference forms it, and -32 (d sc) for the
             // fma that rounds (q - 32) (d sc) once
             const float d = h2f(v.d);
@@ -191,28 +190,34 @@ __global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_exact_q6k_split(Dev
                 for (int j = 0; j < 4; j++) pr[h][j] = make_float4(pj[j][0], pj[j][1], pj[j][2], pj[j][3]);
             }
             load(s + Q6_DS, ring[u]);  // the slot's next stage once this one is used
-            float4 *pp = prod + (size_t)(s & 1) * (SV / 4) * RB + r;
+            float4 *pp = prod + ((size_t)(s & 1) * (SV / 4) + 8 * hw) * 64 + lane;
+            if (g < np) {
 #pragma unroll
-            for (int h = 0; h < 2; h++)
+                for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) pp[(size_t)(4 * (2 * p + h) + j) * RB] = pr[h][j];
+                    for (int j = 0; j < 4; j++) pp[(size_t)(4 * h + j) * 64] = pr[h][j];
+            } else {  // past the row: +0.0 steps
+#pragma unroll
+                for (int j = 0; j < 8; j++) pp[(size_t)j * 64] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
             __syncthreads();
         }
     }
 }
 
-template <int RB>
 hipError_t launch_q6_split(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
-    static bool attr_set = false;  // per process; the attribute is per function
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_exact_q6k_split<RB>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        attr_set = true;
+    const size_t lds = (w.n_cols + 4) * sizeof(float) + 2 * 96 * 64 * sizeof(float);
+    if (lds > 64 * 1024) {  // activations of a long row: more than the default 64 KB
+        static bool attr_set = false;  // per process; the attribute is per function
+        if (!attr_set) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_exact_q6k_split,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
     }
-    const size_t lds = (w.n_cols + 4) * sizeof(float) + 2 * 128 * (size_t)RB * sizeof(float);
-    const dim3 grid((unsigned)((w.n_rows + RB - 1) / RB), (unsigned)t_rows);
-    hipLaunchKernelGGL(k_gemv_exact_q6k_split<RB>, grid, dim3(64 * (1 + RB / 16)), lds, s, w, a, out);
+    const dim3 grid((unsigned)((w.n_rows + 63) / 64), (unsigned)t_rows);
+    hipLaunchKernelGGL(k_gemv_exact_q6k_split, grid, dim3(256), lds, s, w, a, out);
     return hipGetLastError();
 }
 
@@ -221,13 +226,7 @@ hipError_t launch_q6_split(const DevWeight &w, const float *a, size_t t_rows, fl
 hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out, int mode,
                             hipStream_t s) {
     if (mode == 0) {
-        if (w.n_cols <= Q6_EXACT_LDS_K) {
-            // rows per block: 64 while that leaves a block per CU, else 32 or 16
-            const size_t groups = (w.n_rows + 63) / 64 * t_rows;
-            if (groups >= 256) return launch_q6_split<64>(w, a, t_rows, out, s);
-            if (2 * groups >= 256) return launch_q6_split<32>(w, a, t_rows, out, s);
-            return launch_q6_split<16>(w, a, t_rows, out, s);
-        }
+        if (w.n_cols <= Q6_EXACT_LDS_K) return launch_q6_split(w, a, t_rows, out, s);
         dim3 grid((unsigned)((w.n_rows + 255) / 256), (unsigned)t_rows);
         hipLaunchKernelGGL(k_gemv_exact_q6k<false>, grid, dim3(256), 0, s, w, a, out);
         return hipGetLastError();
