@@ -44,7 +44,7 @@ __device__ __forceinline__ float chunk_value(const uint4 &v, int e) {
 
 // One block serves RB rows (16, 32 or 64) of a 64-row group.  Wave 0 holds
 // the chains (lane r < RB: row r; the other lanes repeat lane r % RB's
-// reads and store nothing); waves 1..H (H = RB / 16) form the products.  A
+// reads and store nothing); waves 1..H (chain_helpers) form the products.  A
 // stage is CHAIN_D chunks (the row padding unit), SV = CHAIN_D * E values.
 // The helpers write stage s's products to LDS slot s % 2 and meet the chain
 // at barrier s; after it the chain issues the reads of stage s and adds
@@ -54,16 +54,22 @@ __device__ __forceinline__ float chunk_value(const uint4 &v, int e) {
 // them; everything else (weight loads, widening, products) runs beside it.
 // Each helper keeps CHAIN_DS stages of its weight loads in flight, the
 // first ones issued before the activations are staged.
-constexpr int CHAIN_DS = 8;
 constexpr int CHAIN_SLOTS = 2;
+// Helper waves per block: one per row group of 16, but three for 64 rows
+// (four waves in all, one per SIMD: a fifth would share the chain's SIMD,
+// and the chain, which every barrier waits for, would get half its issue
+// slots); stages of loads each helper keeps in flight.
+constexpr int chain_helpers(int rb) { return rb == 64 ? 3 : rb / 16; }
+constexpr int chain_depth(int rb) { return rb == 64 ? 6 : 8; }
 
 template <int DT, int RB>
-__global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_chain(DevWeight w, const float *__restrict__ A,
-                                                                   float *__restrict__ out) {
+__global__ __launch_bounds__(64 * (1 + chain_helpers(RB))) void k_gemv_chain(DevWeight w, const float *__restrict__ A,
+                                                                             float *__restrict__ out) {
     constexpr int E = ChainFmt<DT>::E;
     constexpr int G = CHAIN_D;       // chunks per stage
     constexpr int SV = G * E;        // values per stage
-    constexpr int H = RB / 16;       // helper waves
+    constexpr int H = chain_helpers(RB);
+    constexpr int CHAIN_DS = chain_depth(RB);
     constexpr int NT = 64 * (1 + H);
     constexpr int CPL = 64 / RB;     // chunks per wave-wide load
     constexpr int WLH = G / (CPL * H);  // wave-wide loads per helper per stage
@@ -78,7 +84,7 @@ __global__ __launch_bounds__(64 * (1 + RB / 16)) void k_gemv_chain(DevWeight w, 
     // to the chain (exact: the chain starts at +0.0 and is never -0.0).
     const int nc = (int)(w.group_stride / 1024);
     const int ns = nc / G;
-    const int s_tot = (ns + CHAIN_DS - 1) / CHAIN_DS * CHAIN_DS;  // stages run (whole ring rounds, >= 8)
+    const int s_tot = (ns + CHAIN_DS - 1) / CHAIN_DS * CHAIN_DS;  // stages run (whole ring rounds)
     extern __shared__ float lds[];
     float *act = lds;  // nc * E values, then a 16-byte dump slot for the staging's overshoot
     float4 *prod = reinterpret_cast<float4 *>(lds + (size_t)nc * E + 4);  // [CHAIN_SLOTS][SV / 4][RB]
@@ -274,7 +280,7 @@ hipError_t launch_chain(const DevWeight &w, const float *a, size_t t_rows, float
         }
     }
     const dim3 grid((unsigned)((w.n_rows + RB - 1) / RB), (unsigned)t_rows);
-    hipLaunchKernelGGL((k_gemv_chain<DT, RB>), grid, dim3(64 * (1 + RB / 16)), lds, s, w, a, out);
+    hipLaunchKernelGGL((k_gemv_chain<DT, RB>), grid, dim3(64 * (1 + chain_helpers(RB))), lds, s, w, a, out);
     return hipGetLastError();
 }
 
