@@ -62,6 +62,7 @@
 // result differs from the reference's f32 order by the f16 rounding of the
 // weights (normwise about 7e-4 at the Q4_K prefill shape; the stated budget
 // is 2e-3) and is deterministic: each output's summation order is fixed.
+#include "lds_limit.h"
 #include "qmm_internal.h"
 
 #include <type_traits>
@@ -671,14 +672,7 @@ __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__
 
 template <class Fmt, int BM, int EPI>
 hipError_t set_lds_attr() {
-    static bool attr_set = false;  // per process; the attribute is per function
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm_f16<Fmt, BM, EPI>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, Tile<BM>::LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
-    return hipSuccess;
+    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI>, Tile<BM>::LDS);
 }
 
 template <class Fmt, int BM>

@@ -8,6 +8,7 @@
 // token's activations are first copied to LDS (k <= CHAIN_MAX_K), where
 // every lane reads the same address (a broadcast).
 #include "gemv_chain_pipe.h"
+#include "lds_limit.h"
 #include "qmm_gemv_kernels.h"
 
 namespace rce_qmm {
@@ -271,13 +272,8 @@ hipError_t launch_chain(const DevWeight &w, const float *a, size_t t_rows, float
     constexpr int E = ChainFmt<DT>::E;
     const size_t lds = ((w.group_stride / 1024) * E + 4) * sizeof(float) + (size_t)CHAIN_SLOTS * CHAIN_D * E * RB * sizeof(float);
     if (lds > 64 * 1024) {  // activations of a long row: more than the default 64 KB
-        static bool attr_set = false;  // per process; the attribute is per function
-        if (!attr_set) {
-            const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_chain<DT, RB>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
+        const hipError_t e = ensure_lds_limit((const void *)k_gemv_chain<DT, RB>, 160 * 1024);
+        if (e != hipSuccess) return e;
     }
     const dim3 grid((unsigned)((w.n_rows + RB - 1) / RB), (unsigned)t_rows);
     hipLaunchKernelGGL((k_gemv_chain<DT, RB>), grid, dim3(64 * (1 + chain_helpers(RB))), lds, s, w, a, out);
@@ -310,13 +306,8 @@ hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, 
     case T_I2_S: {
         // k activations, the dump slot, two stages of 128 addends of 64 chains
         const size_t lds = (w.n_cols + 4) * sizeof(float) + 2 * 128 * 64 * sizeof(float);
-        static bool attr_set = false;  // per process; the attribute is per function
-        if (!attr_set) {
-            const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_chain_i2s,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
+        const hipError_t e = ensure_lds_limit((const void *)k_gemv_chain_i2s, 160 * 1024);
+        if (e != hipSuccess) return e;
         const dim3 grid((unsigned)((w.n_rows + 31) / 32), (unsigned)t_rows);
         hipLaunchKernelGGL(k_gemv_chain_i2s, grid, dim3(320), lds, s, w, a, out);
         return hipGetLastError();

@@ -1,5 +1,6 @@
 // gemv_q6_k.hip -- the Q6_K decode kernels (EXACT: one chain lane per row; Q8).
 #include "gemv_chain_pipe.h"
+#include "lds_limit.h"
 #include "qmm_gemv_kernels.h"
 
 namespace rce_qmm {
@@ -208,13 +209,8 @@ __global__ __launch_bounds__(256) void k_gemv_exact_q6k_split(DevWeight w, const
 hipError_t launch_q6_split(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
     const size_t lds = (w.n_cols + 4) * sizeof(float) + 2 * 96 * 64 * sizeof(float);
     if (lds > 64 * 1024) {  // activations of a long row: more than the default 64 KB
-        static bool attr_set = false;  // per process; the attribute is per function
-        if (!attr_set) {
-            const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_exact_q6k_split,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
+        const hipError_t e = ensure_lds_limit((const void *)k_gemv_exact_q6k_split, 160 * 1024);
+        if (e != hipSuccess) return e;
     }
     const dim3 grid((unsigned)((w.n_rows + 63) / 64), (unsigned)t_rows);
     hipLaunchKernelGGL(k_gemv_exact_q6k_split, grid, dim3(256), lds, s, w, a, out);

@@ -1,0 +1,28 @@
+// lds_limit.h -- raising a kernel's dynamic LDS limit above HIP's default
+// 64 KB (gfx950 has 160 KB per CU).  The limit is an attribute of the
+// function on a device, so it is set once per (function, device); the
+// record is shared by every thread of the process.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <set>
+#include <utility>
+
+namespace rce_qmm {
+
+inline hipError_t ensure_lds_limit(const void *fn, int bytes) {
+    static std::mutex mu;
+    static std::set<std::pair<const void *, int>> done;  // (function, device)
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({fn, dev})) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) done.insert({fn, dev});
+    return e;
+}
+
+}  // namespace rce_qmm
