@@ -13,7 +13,6 @@ namespace {
 
 // rce-op-qmm/src/lib.rs L425-454, L1667-1705: per half o, l in 0..32, the
 // positions l, l+32, l+64, l+96 in order: sumf += ((d sc) q) a.
-template <bool LDS>
 __device__ __forceinline__ float q6_exact_superblock(const RawQ6_K &b, const float *as, float sumf) {
     const float d = h2f(b.d);
 #pragma unroll
@@ -29,18 +28,10 @@ __device__ __forceinline__ float q6_exact_superblock(const RawQ6_K &b, const flo
                 q6_words(b, o, lq, u1, u2, u3, u4);
                 const float *al = as + 128 * o + 4 * lq;
                 float x[4][4];  // activations of positions 4 lq + J + 32 m
-                if constexpr (LDS) {  // 16-byte broadcast reads
 #pragma unroll
-                    for (int m = 0; m < 4; m++) {
-                        const float4 v = *reinterpret_cast<const float4 *>(al + 32 * m);
-                        x[m][0] = v.x; x[m][1] = v.y; x[m][2] = v.z; x[m][3] = v.w;
-                    }
-                } else {
+                for (int m = 0; m < 4; m++)
 #pragma unroll
-                    for (int m = 0; m < 4; m++)
-#pragma unroll
-                        for (int j = 0; j < 4; j++) x[m][j] = al[j + 32 * m];
-                }
+                    for (int j = 0; j < 4; j++) x[m][j] = al[j + 32 * m];
 #define Q6_STEP(J)                                                                   \
     sumf = sumf + __builtin_fmaf(ubyte<J>(u1), ds1, n1) * x[0][J];                     \
     sumf = sumf + __builtin_fmaf(ubyte<J>(u2), ds2, n2) * x[1][J];                     \
@@ -54,11 +45,9 @@ __device__ __forceinline__ float q6_exact_superblock(const RawQ6_K &b, const flo
     return sumf;
 }
 
-// LDS: the block's four waves share the token's activations staged in LDS
-// (k <= Q6_EXACT_LDS_K), read as broadcasts; else they read them from
-// global memory.
+// Rows longer than Q6_EXACT_LDS_K: the activations are read from global
+// memory (each lane the same addresses) instead of LDS.
 constexpr size_t Q6_EXACT_LDS_K = 16384;
-template <bool LDS>
 __global__ __launch_bounds__(256) void k_gemv_exact_q6k(DevWeight w, const float *__restrict__ A,
                                                         float *__restrict__ out) {
     const size_t row = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -66,23 +55,17 @@ __global__ __launch_bounds__(256) void k_gemv_exact_q6k(DevWeight w, const float
     const size_t rr = row < w.n_rows ? row : w.n_rows - 1;
     const int nsb = (int)(w.n_cols / 256);
     const float *a = A + (size_t)blockIdx.y * w.n_cols;
-    extern __shared__ float act[];
-    if constexpr (LDS) {
-        for (size_t i = threadIdx.x; i < w.n_cols; i += 256) act[i] = a[i];
-        __syncthreads();
-        a = act;
-    }
     float sumf = 0.0f;
     RawQ6_K b0, b1;
     ld_q6_k(w, rr, 0, b0);
     int sb = 0;
     for (; sb + 1 < nsb; sb += 2) {
         ld_q6_k(w, rr, sb + 1, b1);
-        sumf = q6_exact_superblock<LDS>(b0, a + 256 * sb, sumf);
+        sumf = q6_exact_superblock(b0, a + 256 * sb, sumf);
         if (sb + 2 < nsb) ld_q6_k(w, rr, sb + 2, b0);
-        sumf = q6_exact_superblock<LDS>(b1, a + 256 * (sb + 1), sumf);
+        sumf = q6_exact_superblock(b1, a + 256 * (sb + 1), sumf);
     }
-    if (sb < nsb) sumf = q6_exact_superblock<LDS>(b0, a + 256 * sb, sumf);
+    if (sb < nsb) sumf = q6_exact_superblock(b0, a + 256 * sb, sumf);
     if (row < w.n_rows) out[(size_t)blockIdx.y * w.n_rows + row] = sumf;
 }
 
@@ -224,7 +207,7 @@ hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *
     if (mode == 0) {
         if (w.n_cols <= Q6_EXACT_LDS_K) return launch_q6_split(w, a, t_rows, out, s);
         dim3 grid((unsigned)((w.n_rows + 255) / 256), (unsigned)t_rows);
-        hipLaunchKernelGGL(k_gemv_exact_q6k<false>, grid, dim3(256), 0, s, w, a, out);
+        hipLaunchKernelGGL(k_gemv_exact_q6k, grid, dim3(256), 0, s, w, a, out);
         return hipGetLastError();
     }
     return launch_as_tb<Q6_KQ8, true, 2>(w, g, a, t_rows, out, s);

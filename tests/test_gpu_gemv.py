@@ -92,10 +92,10 @@ def test_mm_batched_exact_bit_identical(ctx, dt, t_rows):
 @pytest.mark.parametrize("n,t_rows", [(4100, 1), (4100, 3), (8200, 1), (8200, 3), (16448, 1)])
 def test_row_chain_block_shapes(ctx, dt, n, t_rows):
     """The row-chain kernels (one chain lane per row, helper waves forming the
-    addends) take 16, 32 or 64 rows per block by the count of 64-row groups
-    times tokens (4100 x 1: 16; 4100 x 3 and 8200 x 1: 32; 8200 x 3 and
-    16448 x 1: 64), each with a ragged last group; all must equal the
-    reference order bit for bit."""
+    addends): F32 / F16 / BF16 take 16, 32 or 64 rows per block by the count
+    of 64-row groups times tokens (4100 x 1: 16; 4100 x 3 and 8200 x 1: 32;
+    8200 x 3 and 16448 x 1: 64), Q6_K EXACT always 64; each case has a ragged
+    last group, and all must equal the reference order bit for bit."""
     k = 256 if dt == O.Q6_K else 200
     note(f"row chain dtype={dt} n={n} t={t_rows} k={k}")
     rng = np.random.default_rng(2500 + dt + n + t_rows)
@@ -219,10 +219,12 @@ def test_errors_and_empty_inputs(ctx):
 
 # The largest K each kernel family takes (rce_qmm_supports): 1024 column
 # units per row (blocks of 1024 threads), the ternary blocks' 256 units,
-# and the row chains' LDS staging (F16: 16 KB values padded to stages).
+# and the row chains' LDS staging (F16: 16 KB values padded to stages;
+# Q6_K EXACT: 16384 is the longest row the LDS-staged chains take, longer
+# rows read their activations from global memory).
 MAX_K = [(O.Q4_0, 48, 32768), (O.Q8_0, 40, 32768), (O.Q5_0, 24, 32768), (O.Q4_K, 24, 65536),
-         (O.Q6_K, 70, 65536), (O.Q3_K, 16, 32768), (O.F16, 80, 16320), (O.Q1_0, 24, 32768),
-         (O.STQ1_0, 16, 65536), (O.I2_S, 70, 16384)]
+         (O.Q6_K, 70, 65536), (O.Q6_K, 70, 16384), (O.Q3_K, 16, 32768), (O.F16, 80, 16320),
+         (O.Q1_0, 24, 32768), (O.STQ1_0, 16, 65536), (O.I2_S, 70, 16384)]
 
 
 @pytest.mark.parametrize("dt,n,k", MAX_K)
