@@ -292,6 +292,19 @@ hipError_t launch_chain_rb(const DevWeight &w, const float *a, size_t t_rows, fl
 
 }  // namespace
 
+hipError_t chain_prepare_lds() {
+    const void *fns[] = {(const void *)k_gemv_chain<T_F32, 16>,  (const void *)k_gemv_chain<T_F32, 32>,
+                         (const void *)k_gemv_chain<T_F32, 64>,  (const void *)k_gemv_chain<T_F16, 16>,
+                         (const void *)k_gemv_chain<T_F16, 32>,  (const void *)k_gemv_chain<T_F16, 64>,
+                         (const void *)k_gemv_chain<T_BF16, 16>, (const void *)k_gemv_chain<T_BF16, 32>,
+                         (const void *)k_gemv_chain<T_BF16, 64>, (const void *)k_gemv_chain_i2s};
+    for (const void *f : fns) {
+        const hipError_t e = ensure_lds_limit(f, 160 * 1024);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_gemv_chain(const DevWeight &w, const float *a, size_t t_rows, float *out, hipStream_t s) {
     if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
     const bool i2s = w.dtype == T_I2_S;

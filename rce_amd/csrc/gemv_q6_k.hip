@@ -202,6 +202,8 @@ hipError_t launch_q6_split(const DevWeight &w, const float *a, size_t t_rows, fl
 
 }  // namespace
 
+hipError_t q6_prepare_lds() { return ensure_lds_limit((const void *)k_gemv_exact_q6k_split, 160 * 1024); }
+
 hipError_t launch_gemv_q6_k(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out, int mode,
                             hipStream_t s) {
     if (mode == 0) {

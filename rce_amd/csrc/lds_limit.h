@@ -25,4 +25,11 @@ inline hipError_t ensure_lds_limit(const void *fn, int bytes) {
     return e;
 }
 
+// Raise the limit, on the current device, for every kernel of the row-chain
+// GEMVs that can need more than 64 KB (gemv_chain.hip, gemv_q6_k.hip).
+// Called when a context binds its device, so that no first launch sets an
+// attribute while a stream is being captured into a graph.
+hipError_t chain_prepare_lds();
+hipError_t q6_prepare_lds();
+
 }  // namespace rce_qmm

@@ -6,6 +6,7 @@
 // exception crosses the ABI; failures set a thread-local message
 // (rce_qmm_last_error), the convention of compute/crates/rce-c/include/rce.h.
 #include "abi_internal.h"
+#include "lds_limit.h"
 
 #include <algorithm>
 #include <cmath>
@@ -226,6 +227,8 @@ rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out) {
     HIP_TRY(hipSetDevice(device));
     rce_qmm_status st = noalloc_setup(device);
     if (st) return st;
+    HIP_TRY(rce_qmm::chain_prepare_lds());
+    HIP_TRY(rce_qmm::q6_prepare_lds());
     hipStream_t s = nullptr;
     HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     rce_qmm_context *c = new (std::nothrow) rce_qmm_context();
