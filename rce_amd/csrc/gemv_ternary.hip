@@ -36,9 +36,15 @@ struct Q1_0Unit {
             const uint32_t x = wrd(r.q, i);
 #pragma unroll
             for (int j = 0; j < 32; j++) {
-                const uint32_t m = (uint32_t)((int32_t)(x << (31 - j)) >> 31);  // bit j as a mask
-                pos = pos + keep(av[32 * i + j], m);
-                neg = neg + keep(av[32 * i + j], ~m);
+                // bit j as a mask (one v_bfe_i32), the activation kept where it
+                // is set (v_and_b32) and where it is clear (one v_bfi_b32:
+                // (m & 0) | (~m & a)); volatile keeps each step's masks in place
+                uint32_t m, nv;
+                asm volatile("v_bfe_i32 %0, %1, %2, 1" : "=v"(m) : "v"(x), "n"(j));
+                const uint32_t a = __float_as_uint(av[32 * i + j]);
+                asm volatile("v_bfi_b32 %0, %1, 0, %2" : "=v"(nv) : "v"(m), "v"(a));
+                pos = pos + __uint_as_float(a & m);
+                neg = neg + __uint_as_float(nv);
             }
         }
         const float t = pos - neg;
