@@ -190,7 +190,10 @@ rce_qmm_status rce_qmm_dequant_row(rce_qmm_context *ctx, const rce_qmm_weight *w
  * L541-563, packed as spec/checker/tests/support/toy_gpt2.rs L46-58), Q4_K /
  * Q5_K / Q6_K by quantize_k + pack (kquant.rs L193-346).  len must equal n_rows *
  * row_bytes(dtype, n_cols).  Host only (no device needed); bit-identical for
- * any thread count. */
+ * any thread count.  Every input value is accepted: infinities, NaNs and
+ * blocks whose 1/d overflows get the bytes of the reference's release build
+ * (saturating float -> i32, wrapping adds, low bits kept by `as u8` / `as i8`
+ * and by f16_bits, which writes an infinite scale as 0x3C00). */
 rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, size_t n_rows, size_t n_cols, uint8_t *dst,
                                 size_t len);
 

@@ -146,6 +146,25 @@ EXPORT size_t orc_tensor_byte_size(uint32_t t, size_t n) {
 /* Quantizers (produce the configs' weights)                           */
 /* ------------------------------------------------------------------ */
 
+/* Rust's `f as i32` (saturating): NaN -> 0, values beyond the range -> the
+ * nearest bound, else truncation toward zero.  A plain C cast of NaN or an
+ * out-of-range float is undefined (x86 gives INT_MIN for all of them). */
+static inline int32_t as_i32(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+/* Planted mistakes for the known-answer tests (tests/test_oracle_formats.py
+ * compiles copies with -DORC_PLANT=k; the shipped build has 0):
+ * 1 round half to even instead of away from zero; 2 lo = the least value
+ * instead of min(0, least); 3 no clamp of sc at 63; 4 no clamp of m at 63;
+ * 5 Q6_K's last instead of first value of largest magnitude. */
+#ifndef ORC_PLANT
+#define ORC_PLANT 0
+#endif
+
 /* nn.rs L541-563 `quantize_block`: GGUF reference quantizers of one block
  * of 32.  Q8_0: d = amax/127, q = round_half_away(x*id).  Q4_0: m = first
  * x of largest magnitude, d = m/-8, q = min(15, floor(x*id + 8.5)) - 8.
@@ -161,11 +180,12 @@ EXPORT void orc_quantize_block(const float *x, int q4, int32_t *q, float *d_out)
         if (q4) {
             float t = x[i] * id;
             t = t + 8.5f;
-            int v = (int)floorf(t);
-            q[i] = (v < 15 ? v : 15) - 8;
+            int32_t v = as_i32(floorf(t));
+            /* `.min(15) - 8` wraps in a release build (only -inf reaches it) */
+            q[i] = (int32_t)((uint32_t)(v < 15 ? v : 15) - 8u);
         } else {
             float t = x[i] * id;
-            q[i] = (int)roundf(t);
+            q[i] = as_i32(roundf(t));
         }
     }
     *d_out = orc_round_to_f16(d);
@@ -183,15 +203,16 @@ EXPORT void orc_quantize_q8_0_q4_0(const float *w, size_t n, int q4, uint8_t *ou
         uint16_t h = orc_f16_bits(d);
         o[0] = (uint8_t)(h & 0xff); o[1] = (uint8_t)(h >> 8);
         if (q4) {
-            for (int t = 0; t < 16; t++)
-                o[2 + t] = (uint8_t)((uint8_t)(q[t] + 8) | ((uint8_t)(q[t + 16] + 8) << 4));
+            for (int t = 0; t < 16; t++)  /* (q + 8) as u8, the add wrapping */
+                o[2 + t] = (uint8_t)((uint8_t)((uint32_t)q[t] + 8u) | (uint8_t)((uint8_t)((uint32_t)q[t + 16] + 8u) << 4));
         } else {
             for (int t = 0; t < 32; t++) o[2 + t] = (uint8_t)(int8_t)q[t];
         }
     }
 }
 
-static inline int rnd_i(float x) { return (int)roundf(x); }  /* f32::round as i32 */
+/* f32::round (half away from zero) as i32 */
+static inline int rnd_i(float x) { return ORC_PLANT == 1 ? as_i32(rintf(x)) : as_i32(roundf(x)); }
 static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 /* kquant.rs L193-245 `quantize_k` (GT-10): RCE's reference quantizer of
@@ -205,7 +226,7 @@ EXPORT void orc_quantize_k(const float *x, uint32_t fmt, int32_t *q, int32_t *sc
             float amax = 0.0f, m = 0.0f;
             for (int i = 0; i < 16; i++) {
                 float v = x[b * 16 + i];
-                if (amax < fabsf(v)) { amax = fabsf(v); m = v; }
+                if (ORC_PLANT == 5 ? amax <= fabsf(v) : amax < fabsf(v)) { amax = fabsf(v); m = v; }
             }
             w[b] = m / -32.0f;
         }
@@ -223,7 +244,7 @@ EXPORT void orc_quantize_k(const float *x, uint32_t fmt, int32_t *q, int32_t *sc
     float nmax = fmt == T_Q5_K ? 31.0f : 15.0f;
     float w[8], v[8];
     for (int b = 0; b < 8; b++) {
-        float lo = 0.0f, hi = -INFINITY;
+        float lo = ORC_PLANT == 2 ? INFINITY : 0.0f, hi = -INFINITY;
         for (int i = 0; i < 32; i++) {
             float t = x[b * 32 + i];
             if (t < lo) lo = t;
@@ -239,8 +260,8 @@ EXPORT void orc_quantize_k(const float *x, uint32_t fmt, int32_t *q, int32_t *sc
     for (int b = 0; b < 8; b++) {
         int s = d != 0.0f ? rnd_i(w[b] / d) : 0;
         int m = dmin != 0.0f ? rnd_i(v[b] / dmin) : 0;
-        sc[b] = d != 0.0f ? (s < 63 ? s : 63) : 0;
-        mn[b] = dmin != 0.0f ? (m < 63 ? m : 63) : 0;
+        sc[b] = d != 0.0f ? (s < 63 || ORC_PLANT == 3 ? s : 63) : 0;
+        mn[b] = dmin != 0.0f ? (m < 63 || ORC_PLANT == 4 ? m : 63) : 0;
     }
     for (int p = 0; p < 256; p++) {
         float s = d * (float)sc[p / 32], o = dmin * (float)mn[p / 32];

@@ -384,18 +384,20 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         //   W: half pw of the group; instruction i covers rows 16i .. +15,
         //      4 lanes per row, slot p holding piece p ^ ((row >> 2) & 3);
         //      headers: rows BN/2*pw + lane for lanes 0..BN/2-1
+        //      The buffer starts at the tile's first row, so its offsets
+        //      span the tile's rows only.
+        const size_t wtile = N - n0 < (size_t)BN ? N - n0 : (size_t)BN;  // rows of this tile
         uint32_t w_lane[T::W_LOADS];
 #pragma unroll
         for (int i = 0; i < T::W_LOADS; i++) {
             const int wr = 16 * i + (lane >> 2);
-            size_t wrow = n0 + wr;
-            wrow = wrow < N ? wrow : N - 1;  // rows past the end load the last row
+            const size_t wrow = (size_t)wr < wtile ? (size_t)wr : wtile - 1;  // rows past the end load the last row
             w_lane[i] = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
         }
-        size_t hrow = n0 + BN / 2 * pw + (lane & (BN / 2 - 1));
-        hrow = hrow < N ? hrow : N - 1;
+        size_t hrow = (size_t)(BN / 2 * pw + (lane & (BN / 2 - 1)));
+        hrow = hrow < wtile ? hrow : wtile - 1;
         const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
-        const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(w.base, (uint32_t)(N * w.row_stride));
+        const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(w.base + n0 * w.row_stride, (uint32_t)(wtile * w.row_stride));
         const uint32_t a_soff_max = (uint32_t)(nchunks - 1) * (KC * 2);
         // Loads of (virtual) iteration it: W position it % 4 of group
         // it/4 + GA (past the end: group 0), then A chunk it + NS - 1 into
@@ -721,6 +723,32 @@ hipError_t launch_grouped_epi(int epi, const DevWeight &w, const DevWeight *wtab
 
 }  // namespace
 
+// The kernel's per-lane load offsets are 32-bit: the activations (all of
+// them: a grouped tile gathers rows from anywhere) below 2^32 bytes, and a
+// tile's 128 weight rows.
+bool gemm_shape_ok(size_t a_rows, const DevWeight &w) {
+    return a_rows * w.n_cols * 2 < ((size_t)1 << 32) && 128 * w.row_stride < ((size_t)1 << 32);
+}
+
+hipError_t gemm_prepare_lds() {
+    hipError_t e = hipSuccess;
+    auto all_epi = [&](auto fmt, auto bm) {
+        using F = decltype(fmt);
+        constexpr int BM = decltype(bm)::value;
+        if (e == hipSuccess) e = set_lds_attr<F, BM, GEPI_F32>();
+        if (e == hipSuccess) e = set_lds_attr<F, BM, GEPI_SILU_F16>();
+        if (e == hipSuccess) e = set_lds_attr<F, BM, GEPI_SWIGLU_F16>();
+    };
+    auto all_bm = [&](auto fmt) {
+        all_epi(fmt, ic<64>{});
+        all_epi(fmt, ic<96>{});
+        all_epi(fmt, ic<128>{});
+    };
+    all_bm(Q4K{});
+    all_bm(Q40{});
+    return e;
+}
+
 bool gemm_supports(uint32_t dtype, size_t n_cols) {
     if (n_cols >= (size_t)1 << 31 || n_cols == 0) return false;
     if (dtype == T_Q4_K) return n_cols % 256 == 0;
@@ -748,8 +776,7 @@ hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, co
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
                                    int bm, int epi, void *out, const float *aux, hipStream_t s) {
     if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
-    if (a_rows * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
-        return hipErrorInvalidValue;
+    if (!gemm_shape_ok(a_rows, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
     const bool q4k = w.dtype == T_Q4_K;
     if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
@@ -768,9 +795,7 @@ hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, co
 
 hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s, int bm) {
     if (M == 0 || w.n_rows == 0) return hipSuccess;
-    // the kernel's per-lane load offsets are 32-bit
-    if (M * w.n_cols * 2 >= ((size_t)1 << 32) || w.n_rows * w.row_stride >= ((size_t)1 << 32))
-        return hipErrorInvalidValue;
+    if (!gemm_shape_ok(M, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
     const bool q4k = w.dtype == T_Q4_K;
     if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;

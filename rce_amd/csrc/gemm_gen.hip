@@ -11,8 +11,9 @@
 //   * Loads, per chunk and thread: 32 bytes of A (two 16-byte loads; one
 //     load instruction of a wave covers 8 rows x 128 bytes) and the raw
 //     bytes of 8 consecutive weights of one W row (tile row t / 8, weights
-//     8 (t % 8) .. +7 of the chunk), issued three chunks ahead into
-//     registers, so HBM latency overlaps two chunks of matrix work.
+//     8 (t % 8) .. +7 of the chunk), issued DEPTH (six) chunks ahead into
+//     registers, so HBM latency overlaps several chunks of matrix work
+//     (gen_pipeline below).
 //   * Stores: A as loaded; the 8 weights as binary16, each the reference's
 //     f32 dequantized value (rce-ingest-gguf/src/dequant.rs) rounded once
 //     to nearest-even.  Both tiles are double-buffered in LDS with 16-byte
@@ -22,7 +23,7 @@
 //     blocks) of columns 32 ch .. +31 for k-steps 2 kh and 2 kh + 1 of every
 //     chunk.  The two k-halves are added at the end through LDS, kh 0 plus
 //     kh 1: each output's summation order is fixed (run-to-run identical).
-// One barrier per chunk.  Values: f16 rounding of A and W (about 2^-12
+// One barrier per CPB (two) chunks.  Values: f16 rounding of A and W (about 2^-12
 // relative each) with f32 accumulation; weights whose dequantized magnitude
 // exceeds 65504 become infinite.
 #include "qmm_internal.h"
@@ -257,6 +258,65 @@ struct FF16 {
     }
 };
 
+// The chunk pipeline of k_gemm_gen, a host/device function so the test
+// harness can replay its schedule (tests/gemm_gen_host.hip).  Operations:
+// sync() a block barrier; load(slot, ch) chunk ch's global loads into
+// register set `slot`; mma(ch, buf) the matrix work of chunk ch from LDS
+// buffer buf; store(slot, ch, buf) register set `slot` (holding chunk ch)
+// into LDS buffer buf.
+//
+// At the top of a trip, LDS buffers hold chunks c .. c + CPB - 1 (stored
+// before the last barrier) and register set s holds chunk c + s
+// (s < DEPTH).  Group u of a trip loads chunks c + u + DEPTH .. into the
+// register sets chunks c + u .. used (already stored), multiplies chunks
+// c + u .., and stores chunks c + u + CPB .. into the buffers read last in
+// the previous group, which every wave has left at this barrier.
+// The main loop runs whole trips of DEPTH chunks with no branch, so the
+// compiler's wait for a register set's loads counts only the loads issued
+// after it (a loop with conditional loads waits for all of them); loads
+// past the last chunk reload it.  The tail takes the last 0 .. DEPTH + CPB
+// - 1 chunks: those past c + DEPTH - 1 are loaded there, into the sets the
+// tail's first group frees.
+template <int DEPTH, int CPB, class Sync, class Load, class Mma, class Store>
+__host__ __device__ __forceinline__ void gen_pipeline(const int nchunks, Sync &&sync, Load &&load, Mma &&mma,
+                                                      Store &&store) {
+    constexpr int NBUF = 2 * CPB;
+    const int last = nchunks - 1;
+#pragma unroll
+    for (int u = 0; u < DEPTH; u++) load(u, u < last ? u : last);
+#pragma unroll
+    for (int v = 0; v < CPB; v++)
+        if (v < nchunks) store(v, v, v);
+    int c = 0;
+    for (; c + DEPTH + CPB <= nchunks; c += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u += CPB) {
+            sync();
+#pragma unroll
+            for (int v = 0; v < CPB; v++) load(u + v, c + u + v + DEPTH < last ? c + u + v + DEPTH : last);
+#pragma unroll
+            for (int v = 0; v < CPB; v++) mma(c + u + v, (c + u + v) % NBUF);
+#pragma unroll
+            for (int v = 0; v < CPB; v++) store((u + v + CPB) % DEPTH, c + u + v + CPB, (c + u + v + CPB) % NBUF);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < DEPTH + CPB; u += CPB) {
+        if (c + u < nchunks) {
+            sync();
+#pragma unroll
+            for (int v = 0; v < CPB; v++)
+                if (u + v < DEPTH && c + u + v + DEPTH < nchunks) load(u + v, c + u + v + DEPTH);
+#pragma unroll
+            for (int v = 0; v < CPB; v++)
+                if (c + u + v < nchunks) mma(c + u + v, (c + u + v) % NBUF);
+#pragma unroll
+            for (int v = 0; v < CPB; v++)
+                if (c + u + v + CPB < nchunks) store((u + v + CPB) % DEPTH, c + u + v + CPB, (c + u + v + CPB) % NBUF);
+        }
+    }
+}
+
 template <class F>
 struct Stage {
     u32x4 a0, a1;
@@ -327,47 +387,10 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w, const _Float16 *__
         }
     };
 
-    // At the top of iteration c, LDS buffer c % 2 holds chunk c (after the
-    // barrier) and registers hold chunks c + 1 .. c + DEPTH - 1.  Iteration c
-    // loads chunk c + DEPTH into the register set chunk c used, multiplies
-    // chunk c and stores chunk c + 1 into the other buffer (read last in
-    // iteration c - 1, which every wave has left at this barrier).
-    // The main loop runs whole trips of DEPTH chunks with no branch, so the
-    // compiler's wait for a register set's loads counts only the loads
-    // issued after it (a loop with conditional loads waits for all of them);
-    // loads past the last chunk reload it.  At most DEPTH chunks remain.
-    const int last = nchunks - 1;
     Stage<F> st[DEPTH];
-#pragma unroll
-    for (int u = 0; u < DEPTH; u++) load(st[u], u < last ? u : last);
-#pragma unroll
-    for (int v = 0; v < CPB; v++)
-        if (v < nchunks) store(st[v], v, v);
-    int c = 0;
-    for (; c + DEPTH + CPB <= nchunks; c += DEPTH) {
-#pragma unroll
-        for (int u = 0; u < DEPTH; u += CPB) {
-            __syncthreads();
-#pragma unroll
-            for (int v = 0; v < CPB; v++) load(st[u + v], c + u + v + DEPTH < last ? c + u + v + DEPTH : last);
-#pragma unroll
-            for (int v = 0; v < CPB; v++) mma((c + u + v) % NBUF);
-#pragma unroll
-            for (int v = 0; v < CPB; v++) store(st[(u + v + CPB) % DEPTH], c + u + v + CPB, (c + u + v + CPB) % NBUF);
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < DEPTH + CPB; u += CPB) {
-        if (c + u < nchunks) {
-            __syncthreads();
-#pragma unroll
-            for (int v = 0; v < CPB; v++)
-                if (c + u + v < nchunks) mma((c + u + v) % NBUF);
-#pragma unroll
-            for (int v = 0; v < CPB; v++)
-                if (c + u + v + CPB < nchunks) store(st[(u + v + CPB) % DEPTH], c + u + v + CPB, (c + u + v + CPB) % NBUF);
-        }
-    }
+    gen_pipeline<DEPTH, CPB>(
+        nchunks, [&] { __syncthreads(); }, [&](int slot, int ch) { load(st[slot], ch); },
+        [&](int, int buf) { mma(buf); }, [&](int slot, int ch, int buf) { store(st[slot], ch, buf); });
     __syncthreads();  // every fragment read done: the partial sums reuse LDS
 
     // k-half 1 hands its sums to k-half 0 (element r of a block in lane l is

@@ -31,5 +31,7 @@ inline hipError_t ensure_lds_limit(const void *fn, int bytes) {
 // attribute while a stream is being captured into a graph.
 hipError_t chain_prepare_lds();
 hipError_t q6_prepare_lds();
+// The same for every instantiation of the prefill / grouped GEMM (gemm_f16.hip).
+hipError_t gemm_prepare_lds();
 
 }  // namespace rce_qmm

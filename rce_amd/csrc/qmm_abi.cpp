@@ -96,7 +96,17 @@ rce_qmm_status run_gemm(const void *a_dev, bool a_f16, size_t t_rows, const DevW
     if (reinterpret_cast<uintptr_t>(a) % 16)
         return fail(RCE_QMM_BAD_SHAPE, "F16 activations of the F16_MFMA GEMM must be 16-byte aligned");
     if (gemm_supports(dw.dtype, dw.n_cols)) {
-        HIP_TRY(launch_gemm_f16(dw, a, t_rows, out_dev, s));
+        // The kernel's activation offsets are 32-bit: slices of whole
+        // 128-row tiles below 2^32 bytes each (each output's sum does not
+        // depend on the slicing).
+        const size_t k = dw.n_cols, max_rows = ((((size_t)1 << 32) - 1) / (k * 2)) / 128 * 128;
+        if (max_rows == 0)
+            return fail(RCE_QMM_BAD_SHAPE, "n_cols " + std::to_string(k) + " is too long for the F16_MFMA GEMM");
+        const _Float16 *a16 = static_cast<const _Float16 *>(a);
+        for (size_t r0 = 0; r0 < t_rows; r0 += max_rows) {
+            const size_t rows = t_rows - r0 < max_rows ? t_rows - r0 : max_rows;
+            HIP_TRY(launch_gemm_f16(dw, a16 + r0 * k, rows, out_dev + r0 * dw.n_rows, s));
+        }
     } else {
         HIP_TRY(launch_gemm_gen(dw, a, t_rows, out_dev, s));
     }
@@ -229,6 +239,7 @@ rce_qmm_status rce_qmm_context_create(int device, rce_qmm_context **out) {
     if (st) return st;
     HIP_TRY(rce_qmm::chain_prepare_lds());
     HIP_TRY(rce_qmm::q6_prepare_lds());
+    HIP_TRY(rce_qmm::gemm_prepare_lds());
     hipStream_t s = nullptr;
     HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     rce_qmm_context *c = new (std::nothrow) rce_qmm_context();
@@ -498,6 +509,9 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
                                                    std::to_string((int)mode));
     if (t_rows == 0) return RCE_QMM_OK;
     if (!x_dev || !ids_dev || !weights_dev || !out_dev) return fail(RCE_QMM_NULL_ARGUMENT, "null device buffer");
+    if (mode == RCE_QMM_MODE_F16_MFMA && (!gemm_shape_ok(t_rows, a1) || !gemm_shape_ok(t_rows * top_k, a2)))
+        return fail(RCE_QMM_BAD_SHAPE, "the grouped GEMM takes below 2^32 bytes of f16 activations per call "
+                                       "(t_rows * d_model * 2 and t_rows * top_k * d_ff * 2)");
     if ((st = set_device(ctx->device))) return st;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 

@@ -74,7 +74,8 @@ __device__ __forceinline__ uint32_t ldw2(const uint8_t *p) {
 // address arithmetic.  Loads are non-temporal (aux bit 1 on gfx950) like
 // the pointer forms above.  num_records is the maximum: the layouts'
 // padding rows (layout_pad_bytes) back every offset a tile forms, as for the
-// pointer loads, and the host keeps the weight's span below 2^31 bytes.
+// pointer loads.  Each block's buffer starts at its own first row, so its
+// offsets span the block's rows only (far below 2^31 bytes).
 struct WBuf {
     __amdgpu_buffer_rsrc_t r;
     uint32_t lane;
@@ -1362,19 +1363,21 @@ __global__ __launch_bounds__(NT) void k_gemv_as(DevWeight w, const float *__rest
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weights'
     typename Unit::Raw raw[RPL];
     const int rs = active ? rsub : P - 1;
-    // Buffer loads: the lane's row within a pass in a VGPR, the pass
-    // (row0 + u P rows) as a uniform soffset.
+    // Buffer loads: the buffer starts at the block's first row, the lane's
+    // row within a pass is a VGPR, the pass (u P rows) a uniform soffset:
+    // offsets stay below the block's own span, whatever the weight's size.
     WBuf wb1, wb2;
     if constexpr (HasLoadB<Unit>::value) {
-        wb1 = make_wbuf(w.base, (uint32_t)((size_t)rs * w.row_stride));
-        if constexpr (KIND == FX_SWIGLU) wb2 = make_wbuf(fx.w2.base, (uint32_t)((size_t)rs * fx.w2.row_stride));
+        wb1 = make_wbuf(w.base + row0 * w.row_stride, (uint32_t)((size_t)rs * w.row_stride));
+        if constexpr (KIND == FX_SWIGLU)
+            wb2 = make_wbuf(fx.w2.base + row0 * fx.w2.row_stride, (uint32_t)((size_t)rs * fx.w2.row_stride));
     }
     auto issue = [&](int u) {
         const bool up = KIND == FX_SWIGLU && u >= HALF;
         const int uu = up ? u - HALF : u;
         if constexpr (HasLoadB<Unit>::value) {
             const DevWeight &ww = up ? fx.w2 : w;
-            const uint32_t soff = (uint32_t)((row0 + (size_t)(uu * P)) * ww.row_stride);
+            const uint32_t soff = (uint32_t)((size_t)(uu * P) * ww.row_stride);
             raw[u] = Unit::load_b(ww, up ? wb2 : wb1, soff, col);
         } else {
             const size_t r = row0 + (size_t)(uu * P + rs);
@@ -1500,10 +1503,10 @@ inline int units_per_row(uint32_t dtype, size_t n_cols) {
 
 inline int nt_for(int U) { return U <= 256 ? 256 : (U <= 512 ? 512 : 1024); }
 
-// The buffer loads' offsets are 32-bit: a launch's weights, with the rows a
-// tile reads past the end, must span less than 2^31 bytes.
+// The buffer loads' offsets are 32-bit and relative to the block's first
+// row: one block's rows must span less than 2^31 bytes.
 inline bool wbuf_span_ok(const DevWeight &w, size_t tile_rows) {
-    return (w.n_rows + tile_rows) * w.row_stride < ((size_t)1 << 31);
+    return tile_rows * w.row_stride < ((size_t)1 << 31);
 }
 
 template <class Unit, int NT, int RPL, bool Q8>

@@ -10,12 +10,22 @@
 //     and pack (L284-346).
 // Scales are rounded with round_to_f16 (nn.rs L521-533): IEEE binary16
 // round-to-nearest-even, overflow to infinity -- exactly the compiler's
-// float -> _Float16 conversion.  Every + - * / is one binary32 rounding
-// (built with -ffp-contract=off).  Blocks are independent, so the work is
-// split over host threads by row ranges with no effect on the bytes.
+// float -> _Float16 conversion -- and written with the reference's
+// f16_bits (kquant.rs L267-281), which equals IEEE's encoding on every
+// finite binary16 value.  Every + - * / is one binary32 rounding (built
+// with -ffp-contract=off).  Blocks are independent, so the work is split
+// over host threads by row ranges with no effect on the bytes.
+//
+// Non-finite inputs get the reference's bytes too: float -> int is Rust's
+// saturating `as i32` (NaN -> 0), integer adds wrap as in a release build,
+// narrowing keeps the low bits (`as u8`, `as i8`), and f16_bits of an
+// infinity or NaN keeps its exponent's low bits (0x3C00 for +inf).  Such
+// blocks arise from infinite or NaN weights and from blocks whose largest
+// magnitude is so small that 1/d overflows to infinity.
 #include "abi_internal.h"
 
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <thread>
 
@@ -23,18 +33,32 @@ using namespace rce_qmm_abi;
 
 namespace {
 
-inline uint16_t f16_of(float x) {  // x already a binary16 value, or rounded here
-    const _Float16 h = (_Float16)x;
-    uint16_t b;
-    std::memcpy(&b, &h, 2);
-    return b;
+// f16_bits (kquant.rs L267-281, spec/checker/tests/support/toy_gpt2.rs
+// L30-42): the binary16 bits of x, a binary16 value (round_f16 made it one).
+inline uint16_t f16_of(float x) {
+    uint32_t b;
+    std::memcpy(&b, &x, 4);
+    const uint32_t s = (b >> 16) & 0x8000u, ab = b & 0x7FFFFFFFu;
+    const float a = std::fabs(x);
+    if (a == 0.0f) return (uint16_t)s;
+    if (a < 0x1p-14f) return (uint16_t)(s | (uint32_t)(a / 0x1p-24f));  // subnormal: an exact integer
+    const uint32_t e = (ab >> 23) - 127 + 15;  // 143 for an infinity or NaN: only its low bits stay
+    return (uint16_t)(s | (e << 10) | ((ab >> 13) & 0x3FFu));
 }
 inline float round_f16(float x) { return (float)(_Float16)x; }
 inline void put16(uint8_t *p, uint16_t v) {
     p[0] = (uint8_t)(v & 0xFF);
     p[1] = (uint8_t)(v >> 8);
 }
-inline int round_i(float x) { return (int)std::round(x); }  // f32::round (half away from zero) as i32
+// Rust's `f as i32`: NaN -> 0, out of range -> the nearest bound (a C cast
+// of those is undefined).
+inline int32_t as_i32(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+inline int round_i(float x) { return as_i32(std::round(x)); }  // f32::round (half away from zero) as i32
 inline int clamp_i(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // One block of 32 -> 34 bytes (Q8_0) or 18 bytes (Q4_0).
@@ -51,14 +75,16 @@ void encode_q32(const float *x, bool q4, uint8_t *out) {
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     put16(out, f16_of(round_f16(d)));
     if (q4) {
-        int q[32];
+        // the reference's q = min(15, floor(t)) - 8 is stored as (q + 8) as
+        // u8, the adds wrapping: that is min(15, floor(t)) as u8
+        uint8_t q[32];
         for (int i = 0; i < 32; i++) {
             float t = x[i] * id;
             t = t + 8.5f;
-            const int v = (int)std::floor(t);
-            q[i] = (v < 15 ? v : 15);  // stored offset-8 value
+            const int32_t v = as_i32(std::floor(t));
+            q[i] = (uint8_t)(v < 15 ? v : 15);
         }
-        for (int t = 0; t < 16; t++) out[2 + t] = (uint8_t)((q[t] & 0x0F) | ((q[t + 16] & 0x0F) << 4));
+        for (int t = 0; t < 16; t++) out[2 + t] = (uint8_t)(q[t] | (uint8_t)(q[t + 16] << 4));
     } else {
         for (int i = 0; i < 32; i++) {
             const float t = x[i] * id;
@@ -97,10 +123,11 @@ void encode_q45_k(const float *x, uint8_t *out, bool q5) {
     put16(out, f16_of(d));
     put16(out + 2, f16_of(dmin));
     uint8_t *s = out + 4;  // 6-bit scale / min packing (kquant.rs L284-292)
-    for (int j = 0; j < 4; j++) {
-        s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
-        s[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
-        s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+    for (int j = 0; j < 4; j++) {  // each value `as u8` first
+        const uint8_t sj = (uint8_t)sc[j], sj4 = (uint8_t)sc[j + 4], mj = (uint8_t)mn[j], mj4 = (uint8_t)mn[j + 4];
+        s[j] = (uint8_t)((sj & 63) | ((sj4 >> 4) << 6));
+        s[j + 4] = (uint8_t)((mj & 63) | ((mj4 >> 4) << 6));
+        s[j + 8] = (uint8_t)((sj4 & 15) | ((mj4 & 15) << 4));
     }
     int q[256];
     for (int p = 0; p < 256; p++) {

@@ -1,8 +1,12 @@
-// Host harness for tests/test_gemm_gen_formats.py: runs gemm_gen.hip's
-// per-format load + dequant policies on the host, over a weight relaid out
-// exactly as the library uploads it, and writes the binary16 weights the
-// GEMM would put in its LDS tile (row-major [n][k]).
+// Host harness for tests/test_gemm_gen_formats.py.
 //   gemm_gen_host DTYPE N K IN_GGUF_BYTES OUT_F16
+// runs gemm_gen.hip's per-format load + dequant policies on the host, over
+// a weight relaid out exactly as the library uploads it, and writes the
+// binary16 weights the GEMM would put in its LDS tile (row-major [n][k]).
+//   gemm_gen_host sched NCHUNKS
+// runs the kernel's chunk pipeline (gen_pipeline, with the kernel's DEPTH
+// and CPB) and prints its operations, one per line: "S" (barrier),
+// "L slot chunk", "M chunk buf", "T slot chunk buf" (store).
 #include "../rce_amd/csrc/gemm_gen.hip"
 
 #include <cstdio>
@@ -24,7 +28,17 @@ static void run(const DevWeight &w, uint16_t *out) {
             }
 }
 
+static int sched(int nchunks) {
+    gen_pipeline<DEPTH, CPB>(
+        nchunks, [] { std::printf("S\n"); }, [](int slot, int ch) { std::printf("L %d %d\n", slot, ch); },
+        [](int ch, int buf) { std::printf("M %d %d\n", ch, buf); },
+        [](int slot, int ch, int buf) { std::printf("T %d %d %d\n", slot, ch, buf); });
+    std::printf("E %d %d\n", DEPTH, CPB);
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc == 3 && std::strcmp(argv[1], "sched") == 0) return sched(atoi(argv[2]));
     if (argc != 6) return 2;
     const uint32_t dt = (uint32_t)atoi(argv[1]);
     const size_t n = (size_t)atol(argv[2]), k = (size_t)atol(argv[3]);

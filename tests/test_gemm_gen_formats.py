@@ -67,3 +67,65 @@ def test_generic_gemm_weights_are_the_reference_values_in_binary16(harness, tmp_
     both_zero = ((got | want) & 0x7FFF) == 0
     assert np.array_equal(got[~both_zero], want[~both_zero])
     assert got.max() != 0  # not an all-zero output
+
+
+def replay(ops, nchunks):
+    """Check one printed schedule of gen_pipeline: every chunk is multiplied
+    once, in order, from an LDS buffer that holds it and was stored before
+    the last barrier; a store writes the register set that holds its chunk
+    into a buffer no wave reads after the last barrier; a load never
+    overwrites a register set whose chunk is not yet stored."""
+    regs = {}        # slot -> (chunk, stored?)
+    bufs = {}        # buf -> (chunk, epoch stored)
+    read_epoch = {}  # buf -> epoch of its last read
+    epoch, nxt, depth, cpb = 0, 0, None, None
+    for line in ops:
+        f = line.split()
+        if f[0] == "S":
+            epoch += 1
+        elif f[0] == "L":
+            slot, ch = int(f[1]), int(f[2])
+            assert 0 <= ch < nchunks, line
+            if slot in regs and regs[slot][0] >= nxt:
+                assert regs[slot][1], f"load over unstored chunk {regs[slot][0]}: {line}"
+            regs[slot] = (ch, False)
+        elif f[0] == "T":
+            slot, ch, buf = int(f[1]), int(f[2]), int(f[3])
+            assert regs.get(slot, (None,))[0] == ch, f"register set {slot} does not hold chunk {ch}"
+            assert read_epoch.get(buf, -1) < epoch, f"store into buffer {buf} read in this epoch: {line}"
+            regs[slot] = (ch, True)
+            bufs[buf] = (ch, epoch)
+        elif f[0] == "M":
+            ch, buf = int(f[1]), int(f[2])
+            assert ch == nxt, f"chunk {ch} multiplied, {nxt} expected"
+            held, when = bufs.get(buf, (None, None))
+            assert held == ch, f"buffer {buf} holds chunk {held}, not {ch}"
+            assert when < epoch, "multiplied before a barrier after its store"
+            read_epoch[buf] = epoch
+            nxt += 1
+        elif f[0] == "E":
+            depth, cpb = int(f[1]), int(f[2])
+    assert nxt == nchunks, f"{nxt} of {nchunks} chunks multiplied"
+    return depth, cpb
+
+
+def test_generic_gemm_chunk_schedule(harness):
+    """The kernel's own pipeline function, replayed for 1..64 chunks (K 64 ..
+    4096): every residue of the load ring and the barrier pairs, including
+    K/64 = 7, 13, 19, ... where DEPTH + 1 chunks are left for the tail."""
+    for nchunks in range(1, 65):
+        out = subprocess.run([harness, "sched", str(nchunks)], check=True, capture_output=True, text=True).stdout
+        depth, cpb = replay(out.split("\n")[:-1], nchunks)
+        assert depth and cpb
+
+
+def test_schedule_replay_catches_a_stale_tail():
+    """The replay itself fails the schedule the tail had before it loaded
+    the chunks past c + DEPTH - 1 (7 chunks, DEPTH 6, CPB 2): chunk 6 is
+    stored from the register set that still holds chunk 0."""
+    ops = ["L %d %d" % (u, u) for u in range(6)] + ["T 0 0 0", "T 1 1 1"]
+    ops += ["S", "M 0 0", "M 1 1", "T 2 2 2", "T 3 3 3",
+            "S", "M 2 2", "M 3 3", "T 4 4 0", "T 5 5 1",
+            "S", "M 4 0", "M 5 1", "T 0 6 2"]
+    with pytest.raises(AssertionError, match="does not hold chunk 6"):
+        replay(ops, 7)

@@ -151,7 +151,7 @@ GEN_CASES = [
     # (dtype, n_rows, n_cols, tokens): configs[2]'s shape for the three
     # formats a Q4_K_M / Q5_K model's prefill needs besides Q4_K, then
     # ragged M and N (partial tiles, N not a multiple of the 64-row IL64
-    # groups), chunk counts that are not multiples of the 3-deep load ring
+    # groups), chunk counts that are not multiples of the 6-deep load ring
     (O.Q6_K, 4096, 4096, 512),
     (O.Q8_0, 4096, 4096, 512),
     (O.Q5_K, 4096, 4096, 512),
@@ -162,6 +162,11 @@ GEN_CASES = [
     (O.Q5_0, 256, 1024, 100),
     (O.Q4_1, 192, 1088, 65),
     (O.F16, 100, 640, 17),
+    # K / 64 = 7 and 13 (= 1 mod 6): the pipeline's tail then holds DEPTH + 1
+    # chunks, the last of which it must load itself
+    (O.Q8_0, 128, 448, 40),
+    (O.F16, 96, 832, 20),
+    (O.Q4_1, 64, 1600, 9),
 ]
 
 

@@ -1,6 +1,8 @@
 """Pins the oracle's binary16 conversions, quantizers, packers and
 dequantizers against the reference's own known answers and against what the
 mathematics fixes (IEEE binary16, round trips).  CPU only."""
+import os
+
 import numpy as np
 import pytest
 
@@ -252,15 +254,51 @@ def _kat_q6k_first_of_largest():
     return x, q, [-127] + [0] * 15, [], 1032 * 2.0 ** -23, 0.0
 
 
+def _kat_q5k_ties_all_positive():
+    """Q5_K (nmax 31), no negative value.  Sub-block 0: 122.0625, 9.84375,
+    1.96875, then zeros: w0 = 122.0625 / 31 = 3.9375 exactly, d = f16(3.9375
+    / 63) = 0.0625, sc0 = 63, s0 = 3.9375: q = 31, 9.84375 / s0 = 2.5 -> 3,
+    1.96875 / s0 = 0.5 -> 1 (half to even: 2 and 0).  Sub-block 1: 20.34375
+    then zeros: w1 = 0.65625, w1 / d = 10.5 -> sc1 = 11 (even: 10), s1 =
+    0.6875, q = 29.59 -> 30 (sc1 = 10 would give 32.55 -> 31).  Sub-block 2:
+    32 times 1.9375: lo = min(0, 1.9375) = 0, w2 = 1.9375 / 31 = 0.0625,
+    sc2 = 1, q = 31 (lo = 1.9375 would give w2 = 0, sc2 = 0, q = 0).  Every
+    v_b = 0: dmin = 0, every m = 0."""
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[2], x[32] = 122.0625, 9.84375, 1.96875, 20.34375
+    x[64:96] = 1.9375
+    q = np.zeros(256, np.int32)
+    q[0], q[1], q[2], q[32] = 31, 3, 1, 30
+    q[64:96] = 31
+    return x, q, [63, 11, 1, 0, 0, 0, 0, 0], [0] * 8, 0.0625, 0.0
+
+
+def _kat_q5k_min_tie():
+    """Q5_K with mins.  Sub-block 0: -7.875, 22.640625, then zeros: lo =
+    -7.875, hi - lo = 30.515625, w0 = 0.984375 -> d = f16(0.984375 / 63) =
+    2^-6, sc0 = 63, s0 = 0.984375; v0 = 7.875 -> dmin = f16(7.875 / 63) =
+    0.125, m0 = 63, o0 = 7.875: q = 0, 30.515625 / s0 = 31, zeros 7.875 / s0
+    = 8.  Sub-block 1: -2.5625, then zeros: w1 = 2.5625 / 31, w1 / d = 5.29
+    -> sc1 = 5, s1 = 0.078125; v1 / dmin = 20.5 -> m1 = 21 (even: 20), o1 =
+    2.625: q = 0.0625 / s1 = 0.8 -> 1 (m1 = 20: -0.8 -> 0), zeros 2.625 / s1
+    = 33.6 -> 34 -> 31 (clamp)."""
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[32] = -7.875, 22.640625, -2.5625
+    q = np.zeros(256, np.int32)
+    q[1] = 31
+    q[2:32] = 8
+    q[32] = 1
+    q[33:64] = 31
+    return x, q, [63, 5, 0, 0, 0, 0, 0, 0], [63, 21, 0, 0, 0, 0, 0, 0], 2.0 ** -6, 0.125
+
+
 KATS = [(O.Q4_K, _kat_q4k_ties_all_positive), (O.Q4_K, _kat_q4k_min_tie), (O.Q4_K, _kat_q4k_clamps),
-        (O.Q5_K, _kat_q4k_ties_all_positive), (O.Q6_K, _kat_q6k_first_of_largest)]
+        (O.Q5_K, _kat_q5k_ties_all_positive), (O.Q5_K, _kat_q5k_min_tie), (O.Q6_K, _kat_q6k_first_of_largest)]
 
 
 @pytest.mark.parametrize("fmt,kat", KATS)
 def test_quantize_k_known_answers(fmt, kat):
     x, q, sc, mn, d, dmin = kat()
-    if fmt == O.Q5_K:  # nmax 31: the same block's q doubles where exact (w / 31 instead of / 15)
-        pytest.skip("the known answers above are Q4_K's nmax 15")
     gq, gsc, gmn, gd, gdmin = O.quantize_k(x, fmt)
     assert gd == d and gdmin == dmin
     assert list(gsc) == sc
@@ -276,3 +314,126 @@ def test_library_quantizer_bytes_on_known_answers(fmt, kat):
     import rce_amd
     x = kat()[0]
     assert np.array_equal(rce_amd.quantize(x.reshape(1, 256), fmt), O.quantize(x, fmt))
+
+
+# ---- planted mistakes: copies of the oracle built with one mistake each
+# (-DORC_PLANT=k in oracle/qmm_oracle.c) must each fail a known answer.
+
+PLANTS = {1: "round half to even", 2: "lo = the least value", 3: "no clamp of sc", 4: "no clamp of m",
+          5: "Q6_K: the last value of largest magnitude"}
+
+
+@pytest.fixture(scope="module")
+def planted_oracles(tmp_path_factory):
+    import ctypes
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not available")
+    src = os.path.join(os.path.dirname(O.__file__), "qmm_oracle.c")
+    libs = {}
+    for k in [0, *PLANTS]:  # 0: the shipped oracle, built the same way (the control)
+        so = str(tmp_path_factory.mktemp("plant") / f"lib{k}.so")
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fPIC", "-shared", "-std=c11", f"-DORC_PLANT={k}", src,
+                        "-o", so, "-lm"], check=True)
+        L = ctypes.CDLL(so)
+        L.orc_quantize_k.restype = None
+        L.orc_quantize_k.argtypes = [ctypes.c_void_p, ctypes.c_uint32] + [ctypes.c_void_p] * 5
+        libs[k] = L
+    return libs
+
+
+def _kat_holds(L, fmt, kat):
+    x, q, sc, mn, d, dmin = kat()
+    x = np.ascontiguousarray(x, np.float32)
+    gq = np.zeros(256, np.int32); gsc = np.zeros(16, np.int32); gmn = np.zeros(8, np.int32)
+    gd = np.zeros(1, np.float32); gdm = np.zeros(1, np.float32)
+    L.orc_quantize_k(x.ctypes.data, fmt, gq.ctypes.data, gsc.ctypes.data, gmn.ctypes.data, gd.ctypes.data,
+                     gdm.ctypes.data)
+    nsc = 16 if fmt == O.Q6_K else 8
+    ok = gd[0] == d and gdm[0] == dmin and list(gsc[:nsc]) == sc and np.array_equal(gq, q)
+    return ok and (fmt == O.Q6_K or list(gmn) == mn)
+
+
+def test_unplanted_copy_holds_every_known_answer(planted_oracles):
+    assert all(_kat_holds(planted_oracles[0], fmt, kat) for fmt, kat in KATS)
+
+
+@pytest.mark.parametrize("plant", sorted(PLANTS))
+def test_each_planted_mistake_fails_a_known_answer(planted_oracles, plant):
+    failed = [kat.__name__ for fmt, kat in KATS if not _kat_holds(planted_oracles[plant], fmt, kat)]
+    assert failed, f"no known answer catches: {PLANTS[plant]}"
+
+
+# ---- non-finite blocks: the reference's integer semantics (Rust `as i32`
+# saturates, NaN -> 0; adds wrap in a release build; `as u8` / `as i8` keep
+# the low bits; f16_bits (kquant.rs L267-281, toy_gpt2.rs L30-42) of an
+# infinity keeps its exponent's low bits: (143 << 10) mod 2^16 = 0x3C00).
+# Each byte string is derived by hand from nn.rs L541-563 / kquant.rs
+# L193-245 and the packers.
+
+def _nf_q8_inf():
+    """Q8_0 [+inf, 1, NaN, -2, 0...]: amax = +inf (NaN fails amax < |v|), d =
+    inf, id = 1/inf = 0; x * 0 is NaN (inf, NaN) or +-0: every q = 0.  The
+    scale round_to_f16(inf) = inf is written 0x3C00."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[2], x[3] = np.inf, 1.0, np.nan, -2.0
+    return O.Q8_0, x, bytes([0x00, 0x3C] + [0] * 32)
+
+
+def _nf_q8_tiny():
+    """Q8_0 [2^-130, -2^-131, 0...]: d = 2^-130 / 127 (subnormal), 1/d
+    overflows to inf: q0 = round(inf) as i32 = i32::MAX, as i8 = -1 (0xFF);
+    q1 = i32::MIN as i8 = 0; 0 * inf = NaN -> 0.  round_to_f16(d) = 0."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1] = 2.0 ** -130, -(2.0 ** -131)
+    return O.Q8_0, x, bytes([0, 0, 0xFF, 0x00] + [0] * 30)
+
+
+def _nf_q4_0_tiny():
+    """Q4_0 [-2^-130, 2^-131, 0...]: m = -2^-130, d = m / -8 = 2^-133, id =
+    2^133 = inf.  t0 = -inf: floor as i32 = i32::MIN, .min(15) - 8 and + 8
+    wrap back to i32::MIN, as u8 = 0; t1 = +inf: i32::MAX -> 15; zeros: NaN
+    -> 0 -> q = -8 -> 0.  Byte 1 = 15 | 0 << 4; round_to_f16(2^-133) = 0."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1] = -(2.0 ** -130), 2.0 ** -131
+    return O.Q4_0, x, bytes([0, 0, 0x00, 0x0F] + [0] * 14)
+
+
+def _nf_q4k_inf():
+    """Q4_K [+inf, 1.875, 0...]: w0 = inf, d = f16(inf) = inf (0x3C00), dmin
+    = 0; sc0 = round(inf / inf) = NaN -> 0, the others 0 / inf = 0; s = inf
+    * 0 = NaN != 0, so q = round(NaN) -> 0 everywhere."""
+    x = np.zeros(256, np.float32)
+    x[0], x[1] = np.inf, 1.875
+    return O.Q4_K, x, bytes([0x00, 0x3C] + [0] * 142)
+
+
+def _nf_q4k_nan_subblock():
+    """Q4_K: sub-block 0 [1.875, 0...], sub-block 4 all NaN: there lo = 0 and
+    hi = -inf (NaN fails both tests), w4 = -inf; w0 = 0.125, d = f16(0.125 /
+    63) = 1040 * 2^-19 (0x1810), sc0 = round(63.015) = 63; sc4 = -inf / d as
+    i32 = i32::MIN, .min(63) keeps it, and `as u8` packs 0: scale byte 0 =
+    63 | (0 >> 4) << 6.  q0 = 1.875 / (63 d) = 15.004 -> 15; sub-block 4: s =
+    d * -2^31, q = round(NaN) -> 0."""
+    x = np.zeros(256, np.float32)
+    x[0] = 1.875
+    x[128:160] = np.nan
+    b = [0x10, 0x18, 0, 0, 0x3F] + [0] * 11 + [0x0F] + [0] * 127
+    return O.Q4_K, x, bytes(b)
+
+
+NONFINITE = [_nf_q8_inf, _nf_q8_tiny, _nf_q4_0_tiny, _nf_q4k_inf, _nf_q4k_nan_subblock]
+
+
+@pytest.mark.parametrize("kat", NONFINITE)
+def test_quantize_nonfinite_known_answers(kat):
+    fmt, x, want = kat()
+    assert bytes(O.quantize(x, fmt)) == want
+
+
+@pytest.mark.parametrize("kat", NONFINITE)
+def test_library_quantizer_nonfinite_known_answers(kat):
+    import rce_amd
+    fmt, x, want = kat()
+    assert bytes(rce_amd.quantize(x.reshape(1, -1), fmt)) == want

@@ -32,6 +32,25 @@ def test_quantize_edge_blocks(dt):
     assert np.array_equal(rce_amd.quantize(w, dt), O.quantize(w, dt))
 
 
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K])
+def test_quantize_nonfinite_blocks_match_oracle(dt):
+    """Blocks holding +-inf, NaN, subnormal maxima (1/d overflows) and huge
+    values: the library writes the oracle's bytes (the reference's
+    saturating casts, wrapping adds and f16_bits; the known answers are in
+    test_oracle_formats.py)."""
+    rng = np.random.default_rng(40 + dt)
+    k, n = 256, 64
+    w = (rng.standard_normal((n, k)) * 0.02).astype(F32)
+    specials = np.array([np.inf, -np.inf, np.nan, 2.0 ** -130, -(2.0 ** -131), 1e-45, 3e38, -3e38, 7e4], F32)
+    for r in range(n):
+        m = rng.random(k) < (0.02 + 0.3 * (r % 4 == 0))
+        w[r, m] = rng.choice(specials, int(m.sum()))
+        if r % 8 == 1:
+            w[r] = w[r] * F32(1e-38)  # subnormal blocks
+    with np.errstate(all="ignore"):
+        assert np.array_equal(rce_amd.quantize(w, dt), O.quantize(w, dt))
+
+
 def test_quantize_threaded_rows_identical():
     """Large inputs are split over threads by row ranges; the bytes equal a
     row-by-row quantization."""
