@@ -468,42 +468,6 @@ def read_ceiling(hip, ctx, nbytes, steps):
     return best[0] * 1e3, best[1], empty_ms * 1e3
 
 
-ISSUE_KINDS = (("valu_fma_f32", 0, 8), ("valu_dependent_add_f32", 1, 8), ("mfma_f32_32x32x16_f16", 2, 4),
-               ("mfma_plus_32_pk_fma_f16", 3, 4), ("cvt_scalef32_pk_f32_fp8_8_values", 4, 8),
-               ("cvt_f32_ubyte_8_values", 5, 8))
-
-
-def issue_rates(ctx, iters=200):
-    """Shader cycles per instruction (rce_qmm_issue_rate_dev): for each
-    pattern, with 1, 2 and 4 waves per SIMD (one block per CU of 256, 512 or
-    1024 threads), the cycles one wave takes per instruction of the pattern
-    and the SIMD's cycles per instruction (the same divided by the waves
-    sharing it).  For the MFMA patterns an instruction is one MFMA; for the
-    conversion patterns one value (converted and added)."""
-    import rce_amd
-    from rce_amd import _lib
-    L = _lib.lib()
-    cyc = rce_amd.DeviceBuffer(ctx, 8 * 1024)
-    sink = rce_amd.DeviceBuffer(ctx, 256)
-    out = {}
-    for name, kind, per_iter in ISSUE_KINDS:
-        row = {}
-        for wps in (1, 2, 4):
-            blocks = 256
-            for _ in range(2):  # the first launch warms the clocks
-                _lib.check(L.rce_qmm_issue_rate_dev(ctx.handle, kind, 256 * wps, blocks, iters, ctypes.c_void_p(cyc.ptr),
-                                                    ctypes.c_void_p(sink.ptr), None))
-                ctx.synchronize()
-            c = cyc.download(np.uint64, blocks).astype(np.float64)
-            per_wave = float(np.median(c)) / (16 * iters * per_iter)
-            row[f"{wps}_waves_per_simd"] = {"cycles_per_instr_per_wave": round(per_wave, 2),
-                                             "cycles_per_instr_per_simd": round(per_wave / wps, 2)}
-        out[name] = row
-    cyc.free()
-    sink.free()
-    return out
-
-
 def cache_warmth(hip, ctx, steps=200):
     """The decode step's GEMV shapes timed three ways: weights rotated over
     copies beyond 2 x the Infinity Cache (every read from HBM), over copies
@@ -593,43 +557,6 @@ def vendor_gemm(steps=40):
     return out
 
 
-def handoff(hip, ctx, steps=200):
-    """rce_qmm_handoff_probe_dev: microseconds per launch (graph replay) of n
-    blocks that each store 64 floats, without a hand-off (mode 0), with the
-    last-block-done hand-off through __threadfence and one device-scope
-    counter (mode 1), and with agent-scope atomic stores and loads instead
-    of the fence (mode 2)."""
-    import rce_amd
-    from rce_amd import _lib
-    L = _lib.lib()
-    data = rce_amd.DeviceBuffer(ctx, 4 * 64 * 512)
-    cnt = rce_amd.DeviceBuffer(ctx, 256)
-    res = rce_amd.DeviceBuffer(ctx, 4 * 256)
-    hip.ok(hip.L.hipMemset(ctypes.c_void_p(cnt.ptr), 0, 256), "hipMemset")
-    hip.ok(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
-    out = {}
-    for blocks in (32, 160, 512):
-        row = {}
-        for mode, mname in ((0, "stores_only"), (1, "threadfence_counter"), (2, "atomic_stores_counter")):
-            def run(c):
-                for _ in range(c):
-                    _lib.check(L.rce_qmm_handoff_probe_dev(ctx.handle, mode, blocks, ctypes.c_void_p(data.ptr),
-                                                           ctypes.c_void_p(cnt.ptr), ctypes.c_void_p(res.ptr),
-                                                           ctypes.c_void_p(ctx.stream)))
-            run(5)
-            ctx.synchronize()
-            row[mname] = round(hip.timed_graph(ctx.stream, lambda: run(steps), steps) * 1e3, 2)
-        left = int(cnt.download(np.uint32, 1)[0])
-        if left != 0:
-            raise RuntimeError(f"hand-off probe left its counter at {left}")
-        out[f"{blocks}_blocks_us"] = row
-        log(f"  hand-off {blocks} blocks: " + "  ".join(f"{k2} {v:.2f} us" for k2, v in row.items()))
-    data.free()
-    cnt.free()
-    res.free()
-    return out
-
-
 def copy_calibration(hip, nbytes=256 << 20, reps=8):
     """Device-to-device copies of a known size: the reference reading for the
     FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = nbytes)."""
@@ -659,16 +586,12 @@ def main():
                     help="per-format rows: comma-separated subset of sweep,gemm,moe,llama")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the read-ceiling launches (profiling runs)")
-    ap.add_argument("--issue-rates", action="store_true",
-                    help="also report the instruction issue-rate probes (shader cycles per instruction)")
     ap.add_argument("--cache-warmth", action="store_true",
                     help="also time the decode-step GEMV shapes with weights from HBM, the Infinity Cache and one copy")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time AMD's library (torch.matmul, f16 / bf16) on the prefill shapes")
     ap.add_argument("--read-ceilings", action="store_true",
                     help="also measure the read ceiling at the decode step's weight sizes")
-    ap.add_argument("--handoff", action="store_true",
-                    help="also measure the cost of a cross-block hand-off (rce_qmm_handoff_probe_dev)")
     ap.add_argument("--sweep-only", default="",
                     help="run only the sweep rows whose name contains this text (e.g. 'b8'; profiling)")
     args = ap.parse_args()
@@ -795,17 +718,12 @@ def main():
             log(f"  {key}: {lms * 1e3:.1f} us/token  {1e3 / lms:.0f} tok/s  weights {lgb:.0f} GB/s "
                 f"({lgb / HBM_PEAK_GBS:.1%} of HBM peak; floor {LLAMA_WEIGHT_BYTES / 8e12 * 1e6:.1f} us)")
     line["per_format"] = per
-    if args.issue_rates:
-        line["issue_rates"] = issue_rates(ctx)
-        log(f"  issue rates: {json.dumps(line['issue_rates'])}")
     if args.cache_warmth:
         line["cache_warmth"] = cache_warmth(hip, ctx)
     if args.read_ceilings:
         line["read_ceilings"] = read_ceilings(hip, ctx)
     if args.vendor_gemm:
         line["vendor_gemm"] = vendor_gemm()
-    if args.handoff:
-        line["handoff"] = handoff(hip, ctx)
 
     # ---- CPU baseline + parity checks (oracle) -------------------------------------
     if not args.no_cpu:

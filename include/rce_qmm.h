@@ -434,32 +434,6 @@ rce_qmm_status rce_qmm_gguf_read_f32(const rce_qmm_gguf *g, const char *name, fl
 rce_qmm_status rce_qmm_read_ceiling_dev(rce_qmm_context *ctx, const void *buf_dev, size_t bytes, void *sink_dev,
                                         int variant, void *stream);
 
-/* No counterpart in the reference: instruction issue-rate probes, the
- * numbers the kernels' rooflines are explained with.  `blocks` blocks of
- * `threads` (256, 512 or 1024: 1, 2 or 4 waves on each SIMD of the block's
- * CU) each time 16 * `iters` repetitions of pattern `kind` with the shader
- * clock (s_memtime); cycles_dev[b] (8 bytes per block) receives block b's
- * slowest wave's cycle count, sink_dev 4 writable bytes.  kind (instructions
- * per repetition): 0 = eight independent v_fma_f32 chains (8), 1 = one
- * dependent v_add_f32 chain (8), 2 = v_mfma_f32_32x32x16_f16 on four
- * independent accumulators (4), 3 = kind 2 with 32 v_pk_fma_f16 between
- * them (4 MFMA + 32), 4 = four v_cvt_scalef32_pk_f32_fp8 + 8 adds (8
- * values), 5 = eight v_cvt_f32_ubyte + 8 adds (8 values). */
-rce_qmm_status rce_qmm_issue_rate_dev(rce_qmm_context *ctx, int kind, int threads, int blocks, int iters,
-                                      void *cycles_dev, void *sink_dev, void *stream);
-
-/* No counterpart in the reference: the cost of a cross-block hand-off (for
- * bench.py --handoff; a measurement, not part of the matmul path).  One
- * launch of `blocks` blocks of 256 threads, each storing 64 floats into
- * data_dev (4 * 64 * blocks bytes).  mode 0: nothing more; mode 1: each
- * block then does __threadfence() and one device-scope increment of
- * *counter_dev, and the block that completes the count reads all blocks'
- * floats into result_dev (256 floats) and resets the counter; mode 2: the
- * same with agent-scope atomic stores and loads instead of the fence.
- * counter_dev (4 bytes) must be zero before the first call. */
-rce_qmm_status rce_qmm_handoff_probe_dev(rce_qmm_context *ctx, int mode, int blocks, void *data_dev,
-                                         void *counter_dev, void *result_dev, void *stream);
-
 /* ---- device memory helpers (for callers without a HIP runtime) ---------- */
 
 rce_qmm_status rce_qmm_dev_alloc(rce_qmm_context *ctx, size_t bytes, void **out);

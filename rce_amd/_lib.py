@@ -60,8 +60,6 @@ SIGNATURES = {
     "rce_qmm_hip_cost": (STATUS, [P, S, P, S, ctypes.c_double, ctypes.c_double, ctypes.c_double, P]),
     "rce_qmm_energy_read": (STATUS, [I, P, P]),
     "rce_qmm_read_ceiling_dev": (STATUS, [P, P, S, P, I, P]),
-    "rce_qmm_issue_rate_dev": (STATUS, [P, I, I, I, I, P, P, P]),
-    "rce_qmm_handoff_probe_dev": (STATUS, [P, I, I, P, P, P, P]),
     "rce_qmm_dev_alloc": (STATUS, [P, S, P]),
     "rce_qmm_dev_free": (STATUS, [P, P]),
     "rce_qmm_memcpy_h2d": (STATUS, [P, P, P, S]),

@@ -154,13 +154,52 @@ def test_llama_head_dim_128(ctx):
 
 
 def test_llama_long_context(ctx):
-    """150 positions: each wave's keys span several 64-key runs (merged by
-    rescaling), and the four waves' results merge in LDS."""
+    """150 positions at d_head 64: up to three 64-key runs, one per wave
+    (waves 0, 1, 2), whose results merge in LDS by max-rescaling."""
     note("llama 150 positions")
     c = tiny_cfg(n_layers=1, context_length=160)
     W = make_weights(c, seed=26)
     toks = [int(t) for t in np.random.default_rng(0).integers(0, c["vocab"], 150)]
     run_pair(ctx, W, Mode.EXACT, toks, 1e-5).close()
+
+
+def test_llama_runs_past_one_per_wave(ctx):
+    """300 positions at d_head 64: wave w takes the 64-key runs w, w + 4, ...,
+    so from position 256 on wave 0 merges a second run into its first (the
+    reload of the run loop and the rescale by exp(m - m_new) with a finite
+    m), before the four waves merge."""
+    note("llama d_head 64, 300 positions (two runs on wave 0 past 256)")
+    c = tiny_cfg(n_layers=1, context_length=320)
+    W = make_weights(c, seed=36)
+    toks = [int(t) for t in np.random.default_rng(2).integers(0, c["vocab"], 300)]
+    run_pair(ctx, W, Mode.EXACT, toks, 1e-5).close()
+
+
+def test_llama_head_dim_128_runs_past_one_per_wave(ctx):
+    """d_head 128 (32-key runs): past 128 positions wave 0 merges a second
+    run; 150 positions."""
+    note("llama d_head 128, 150 positions (two runs on wave 0 past 128)")
+    c = tiny_cfg(d_model=512, n_q_heads=4, n_kv_heads=1, d_head=128, rope_dim=64, d_ff=768,
+                 rope_freq_base=500000.0, context_length=160, n_layers=1)
+    W = make_weights(c, seed=37)
+    toks = [int(t) for t in np.random.default_rng(3).integers(0, c["vocab"], 150)]
+    run_pair(ctx, W, Mode.EXACT, toks, 1e-5).close()
+
+
+@pytest.mark.parametrize("mode,tol", [(Mode.EXACT, 1e-5), (Mode.Q8, 1e-1)])
+def test_llama_tinyllama_width_long_context(ctx, mode, tol):
+    """configs[4] widths (d 2048, 32 q / 4 kv heads, d_head 64, ffn 5632, Q4_K
+    linears, Q6_K 32000-row head) on 2 layers over 300 positions: every
+    wave's second 64-key run from position 256 on.  Bit-identical to the
+    device-order oracle at every position; EXACT within 1e-5 of the
+    reference order (Q8's distance to it is the activation-rounding noise,
+    bounded as in the full-depth test)."""
+    note(f"llama TinyLlama width, 2 layers, 300 positions, {mode.name}")
+    c = dict(d_model=2048, vocab=32000, n_layers=2, n_q_heads=32, n_kv_heads=4, d_head=64, rope_dim=64,
+             rope_freq_base=10000.0, d_ff=5632, context_length=320, eps=1e-5)
+    W = make_weights(c, seed=38, sigma=0.02)
+    toks = [int(t) for t in np.random.default_rng(4).integers(0, c["vocab"], 300)]
+    run_pair(ctx, W, mode, toks, tol).close()
 
 
 def test_llama_errors(ctx):
