@@ -245,24 +245,25 @@ def time_gemm(hip, ctx, dt, n, k, m, steps, warmup, seed, settle_s=0.2):
     return ms, {"b": b, "x": x[:16].astype(np.float32), "got": res, "dt": dt, "n": n, "k": k}
 
 
-def time_moe(hip, ctx, steps, warmup, seed, mode, settle_s=0.2):
+def time_moe(hip, ctx, steps, warmup, seed, mode, settle_s=0.2, dtype=None):
     """8 Q4_0 experts (w1 14336x4096, w2 4096x14336), 256 tokens,
     top-2 of N(0,1) router logits; ms per grouped-FFN call (all 8 experts'
-    528 MB stream from HBM each call), the touched weight bytes, and a
-    sample of the first 8 tokens (checked in the CPU leg)."""
+    weights stream from HBM each call), the touched weight bytes, and a
+    sample of the first 8 tokens (checked in the CPU leg).  dtype: the same
+    workload with experts of another format (per-format rows)."""
     import rce_amd
-    Q4_0 = rce_amd.GgufDtype.Q4_0
+    dt = rce_amd.GgufDtype.Q4_0 if dtype is None else dtype
     E, dm, dff, T, K = 8, 4096, 14336, 256, 2
     rng = np.random.default_rng(seed)
     w1b, w2b = [], []
     for _ in range(E):
-        w1b.append(rce_amd.quantize(rng.standard_normal((dff, dm), dtype=np.float32) * np.float32(0.02), Q4_0))
-        w2b.append(rce_amd.quantize(rng.standard_normal((dm, dff), dtype=np.float32) * np.float32(0.02), Q4_0))
+        w1b.append(rce_amd.quantize(rng.standard_normal((dff, dm), dtype=np.float32) * np.float32(0.02), dt))
+        w2b.append(rce_amd.quantize(rng.standard_normal((dm, dff), dtype=np.float32) * np.float32(0.02), dt))
     x = rng.standard_normal((T, dm), dtype=np.float32)
     logits = rng.standard_normal((T, E), dtype=np.float32)
     ids, gw = rce_amd.moe_router(logits, K)
-    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, Q4_0, dff, dm) for b in w1b]
-    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, Q4_0, dm, dff) for b in w2b]
+    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, dff, dm) for b in w1b]
+    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, dm, dff) for b in w2b]
     bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
     bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids)
     bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw)
@@ -284,7 +285,7 @@ def time_moe(hip, ctx, steps, warmup, seed, mode, settle_s=0.2):
         w.close()
     for bb in (bx, bi, bw, bo):
         bb.free()
-    sample = {"x": x[:8], "w1": w1b, "w2": w2b, "dff": dff, "ids": ids[:8], "gw": gw[:8], "got": got}
+    sample = {"x": x[:8], "w1": w1b, "w2": w2b, "dff": dff, "ids": ids[:8], "gw": gw[:8], "got": got, "dtype": int(dt)}
     return ms, wbytes + 2 * T * dm * 4, sample
 
 
@@ -352,6 +353,18 @@ def time_llama(hip, ctx, W, mode, steps, warmup, seed):
     return ms, {"tokens": [int(t) for t in toks[:4]], "got": first}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu reports as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_leg(line, head, rows, budget_s=10.0):
     """The CPU baseline and the parity checks (the only part of the bench
     that uses the oracle, the C restatement of the reference path).
@@ -374,6 +387,7 @@ def cpu_leg(line, head, rows, budget_s=10.0):
     med = float(np.median(times))
     cpu_gbs = gemv_bytes(dt, n, k, 1) / med / 1e9
     line["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                            "cpu_model": cpu_model(),
                             "sample": f"{len(times)} calls of mm_1d (f32 activations, reference order) on the "
                                       f"headline Q4_0 11008x4096 batch-1 workload, median {med * 1e3:.2f} ms"}
     log(f"  cpu {cpu_gbs:.2f} GB/s on {threads} threads")
@@ -388,9 +402,9 @@ def cpu_leg(line, head, rows, budget_s=10.0):
     for gk in [r for r in rows if r.startswith("gemm")]:
         g = rows[gk]
         per[g["key"]]["normwise_err_vs_oracle"] = normwise(g["got"], O.mm_batched(g["x"], g["b"], g["dt"], g["n"], g["k"]))
-    if "moe" in rows:
-        m = rows["moe"]
-        ref = O.moe_ffn(m["x"], m["w1"], m["w2"], O.Q4_0, m["dff"], m["ids"], m["gw"])
+    for mk in [r for r in rows if r.startswith("moe")]:
+        m = rows[mk]
+        ref = O.moe_ffn(m["x"], m["w1"], m["w2"], m["dtype"], m["dff"], m["ids"], m["gw"])
         per[m["key"]]["normwise_err_vs_oracle"] = normwise(m["got"], ref)
     for lk in [r for r in rows if r.startswith("llama")]:
         L = rows[lk]
@@ -702,6 +716,18 @@ def main():
         kept["moe"] = dict(msample, key=key)
         log(f"  MoE configs[3]: {mms * 1e3:.1f} us  {mtf:.0f} TFLOP/s ({mtf / MFMA_F16_PEAK_TFS:.1%}), "
             f"{mgb:.0f} GB/s ({mgb / HBM_PEAK_GBS:.1%})")
+        # the same workload with the expert formats Q4_K_M / Q5_K_M / Q8_0 models ship
+        for mdt, mname in ((G.Q6K, "Q6_K"), (G.Q5K, "Q5_K"), (G.Q8_0, "Q8_0")):
+            mms, mbytes, msample = time_moe(hip, ctx, 5, 2, 410 + int(mdt), Mode.F16_MFMA, dtype=mdt)
+            mtf = 120259084288 / (mms * 1e-3) / 1e12
+            mgb = mbytes / (mms * 1e-3) / 1e9
+            key = f"MoE 8x(14336x4096, 4096x14336) {mname} T256 top2 f16_mfma"
+            per[key] = {"us": round(mms * 1e3, 2), "TFLOP/s": round(mtf, 1),
+                        "mfma_frac": round(mtf / MFMA_F16_PEAK_TFS, 4), "GB/s": round(mgb, 1),
+                        "hbm_frac": round(mgb / HBM_PEAK_GBS, 4)}
+            kept[f"moe {mname}"] = dict(msample, key=key)
+            log(f"  {key}: {mms * 1e3:.1f} us  {mtf:.0f} TFLOP/s ({mtf / MFMA_F16_PEAK_TFS:.1%}), "
+                f"{mgb:.0f} GB/s ({mgb / HBM_PEAK_GBS:.1%})")
     if "llama" in rows:  # configs[4]: TinyLlama-shaped decode, batch 1
         log("  building the configs[4] decoder (22 layers, Q4_K + Q6_K head)")
         W = llama_weights(500)

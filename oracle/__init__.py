@@ -77,6 +77,7 @@ def lib() -> ctypes.CDLL:
             "orc_moe_router": (None, [P, S, S, I, P, P]),
             "orc_moe_combine": (None, [P, P, S, S, P]),
             "orc_moe_ffn": (I, [P, S, S, S, P, P, U32, P, P, S, P, I, I]),
+            "orc_moe_ffn2": (I, [P, S, S, S, P, P, U32, U32, P, P, S, P, I, I]),
             "orc_max_threads": (I, []),
             "orc_moe_swiglu_ffn": (I, [P, S, S, S, P, P, P, U32, P, P, S, P, I]),
             "orc_rms_norm": (None, [P, P, S, F, P]),
@@ -272,10 +273,11 @@ def moe_combine(w, ys) -> np.ndarray:
 
 
 def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0, q8: bool = False,
-            silu_dev: bool = False) -> np.ndarray:
+            silu_dev: bool = False, dtype2: int | None = None) -> np.ndarray:
     """The grouped-expert FFN per (token, decision) in the reference's order;
     q8: the Q8-activation products; silu_dev: silu with exp_dev (the
-    device's order)."""
+    device's order); dtype2: the second matrices' dtype when it differs
+    (a Q4_K_M model's Q6_K ffn_down_exps)."""
     x = _c(x, np.float32)
     t_rows, d_model = x.shape
     ids = _c(ids, np.int32); gate_w = _c(gate_w, np.float32)
@@ -284,9 +286,9 @@ def moe_ffn(x, w1_list, w2_list, dtype, d_ff, ids, gate_w, threads: int = 0, q8:
     P1 = (ctypes.c_void_p * len(w1))(*[b.ctypes.data for b in w1])
     P2 = (ctypes.c_void_p * len(w2))(*[b.ctypes.data for b in w2])
     out = np.zeros((t_rows, d_model), np.float32)
-    rc = lib().orc_moe_ffn(_p(x), t_rows, d_model, d_ff, ctypes.cast(P1, ctypes.c_void_p),
-                           ctypes.cast(P2, ctypes.c_void_p), dtype, _p(ids), _p(gate_w), top_k,
-                           _p(out), threads or max_threads(), int(silu_dev) | (2 * int(q8)))
+    rc = lib().orc_moe_ffn2(_p(x), t_rows, d_model, d_ff, ctypes.cast(P1, ctypes.c_void_p),
+                            ctypes.cast(P2, ctypes.c_void_p), dtype, dtype if dtype2 is None else dtype2, _p(ids),
+                            _p(gate_w), top_k, _p(out), threads or max_threads(), int(silu_dev) | (2 * int(q8)))
     if rc:
         raise ValueError(f"orc_moe_ffn rc={rc}")
     return out

@@ -1272,10 +1272,10 @@ EXPORT float orc_silu_dev(float x);
 /* how: 0 = the reference (mm_1d products, silu with the platform exp);
  * bit 0: silu with orc_exp_dev (the device's order, test instrumentation);
  * bit 1: the Q8-activation products (orc_mm_batched_q8) instead of mm_1d. */
-EXPORT int orc_moe_ffn(const float *x, size_t t_rows, size_t d_model, size_t d_ff,
-                       const uint8_t *const *w1_bytes, const uint8_t *const *w2_bytes, uint32_t t,
-                       const int32_t *ids, const float *gate_w, size_t top_k, float *out,
-                       int threads, int how) {
+EXPORT int orc_moe_ffn2(const float *x, size_t t_rows, size_t d_model, size_t d_ff,
+                        const uint8_t *const *w1_bytes, const uint8_t *const *w2_bytes, uint32_t t, uint32_t t2,
+                        const int32_t *ids, const float *gate_w, size_t top_k, float *out,
+                        int threads, int how) {
     float *h = (float *)malloc(d_ff * sizeof(float));
     float *ys = (float *)malloc(top_k * d_model * sizeof(float));
     int rc = 0;
@@ -1287,13 +1287,21 @@ EXPORT int orc_moe_ffn(const float *x, size_t t_rows, size_t d_model, size_t d_f
                     : orc_mm_1d(x + tr * d_model, w1_bytes[e], t, d_ff, d_model, h, threads);
             for (size_t i = 0; i < d_ff; i++) h[i] = (how & 1) ? orc_silu_dev(h[i]) : orc_silu(h[i]);
             if (!rc)
-                rc = q8 ? orc_mm_batched_q8(h, 1, w2_bytes[e], t, d_model, d_ff, ys + j * d_model, threads)
-                        : orc_mm_1d(h, w2_bytes[e], t, d_model, d_ff, ys + j * d_model, threads);
+                rc = q8 ? orc_mm_batched_q8(h, 1, w2_bytes[e], t2, d_model, d_ff, ys + j * d_model, threads)
+                        : orc_mm_1d(h, w2_bytes[e], t2, d_model, d_ff, ys + j * d_model, threads);
         }
         orc_moe_combine(gate_w + tr * top_k, ys, top_k, d_model, out + tr * d_model);
     }
     free(h); free(ys);
     return rc;
+}
+
+/* orc_moe_ffn2 with one dtype for both matrices. */
+EXPORT int orc_moe_ffn(const float *x, size_t t_rows, size_t d_model, size_t d_ff,
+                       const uint8_t *const *w1_bytes, const uint8_t *const *w2_bytes, uint32_t t,
+                       const int32_t *ids, const float *gate_w, size_t top_k, float *out,
+                       int threads, int how) {
+    return orc_moe_ffn2(x, t_rows, d_model, d_ff, w1_bytes, w2_bytes, t, t, ids, gate_w, top_k, out, threads, how);
 }
 
 /* ------------------------------------------------------------------ */

@@ -104,7 +104,7 @@ struct Tile {
     static constexpr int W_HALF = BN * 64;                // rows x 4 chunks x 16 B
     static constexpr int W_LOADS = BN / 16;               // per producer per group (its half)
     static constexpr int W_GROUP = 2 * W_HALF + BN * 16;  // + the scale headers
-    static constexpr int SC_BUF = BN * 2 * 16;            // [column][set][chunk] of f16 {scale, bias}
+    static constexpr int SC_BUF = 2 * 4 * BN * 4;         // [set][chunk][column] of f16 {scale, bias}
     static constexpr int OFF_W = NS * A_STAGE;
     static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
     static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
@@ -201,6 +201,9 @@ __device__ __forceinline__ u32x2 lds_read8(uint32_t a) {
     u32x2 v;
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
+}
+__device__ __forceinline__ void lds_write4(uint32_t a, uint32_t v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(a), "v"(v) : "memory");
 }
 __device__ __forceinline__ void lds_write16(uint32_t a, u32x4 v) {
     asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
@@ -332,16 +335,12 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     constexpr int OFF_W = T::OFF_W, OFF_SC = T::OFF_SC;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int arow[BM];
-    // Blocks are dispatched round-robin over 8 XCDs; consecutive logical
-    // tiles (the m-tiles of one n-tile, sharing W rows) go to one XCD.
-    const int G = gridDim.x, L = blockIdx.x;
-    const int logical = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
-    const int mt = logical % m_tiles, nt = logical / m_tiles;
+    int mt, nt;
+    if (!tile_of_block<T::BN>(w_arg.n_rows, m_tiles, n_tiles, mt, nt)) return;  // before any barrier
     DevWeight w = w_arg;
     size_t m0 = (size_t)mt * BM;
     int rows = (int)(M - m0 < (size_t)BM ? M - m0 : BM);
     if (tiles) {
-        if (mt >= n_tiles[0]) return;  // the whole block, before any barrier
         const MoeTile tl = tiles[mt];
         w = wtab[tl.e];
         m0 = (size_t)tl.r0;
@@ -428,12 +427,16 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             for (int pr = pt; pr < 2 * BN; pr += 128) {
                 const int p_col = pr & (BN - 1), p_si = pr / BN;
                 const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
-                const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_col * 2 + p_si) * 16);
+                const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
                 u32x4 hdr = lds_read16<0>(hdr_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP));
                 wait_lgkm0(hdr);
                 const u32x4 v = {Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
                                  Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
-                lds_write16(sc_wr + (uint32_t)((g & 1) * SC_BUF), v);
+                const uint32_t wr = sc_wr + (uint32_t)((g & 1) * SC_BUF);
+                lds_write4(wr, v.x);
+                lds_write4(wr + 4 * BN, v.y);
+                lds_write4(wr + 8 * BN, v.z);
+                lds_write4(wr + 12 * BN, v.w);
             }
         };
 
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     const int t = wave & 1, kq = wave >> 1;
     // LDS read addresses of this lane; A row block rb is +32 rows (+4096
     // bytes), W column block cb +32 rows of nibbles (+2048 bytes) and +32
-    // columns of scales (+1024 bytes): immediates.
+    // columns of scales (+128 bytes): immediates.
     const int g0 = Fmt::acol(kq) + h;
     const uint32_t a_rd = lds0 + (uint32_t)(l32 * 128 + 16 * (g0 ^ ((l32 & 7) ^ ((l32 >> 3) & 1))));
     const int ncol = BN / 2 * t + l32;  // tile column of this lane in column block 0
@@ -501,7 +504,10 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     for (int q = 0; q < 4; q++)
         w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
                                             16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
-    const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((ncol * 2 + Fmt::sidx(kq)) * 16);
+    // {scale, bias} of chunk q: [set][q][column], consecutive columns in
+    // consecutive banks (a 32-column read is conflict-free; the
+    // [column][set][chunk] order cost ~14 bank-conflict cycles per read)
+    const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((Fmt::sidx(kq) * 4 * BN + ncol) * 4);
 
     f32x16 acc[RB * CB];
 #pragma unroll
@@ -522,7 +528,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // group's four: the 96-row tile's accumulators need the room)
     auto read_sb = [&](uint32_t *v, uint32_t addr) {
         v[0] = lds_read4<0>(addr);
-        if constexpr (CB > 1) v[1] = lds_read4<1024>(addr);
+        if constexpr (CB > 1) v[1] = lds_read4<128>(addr);  // +32 columns
     };
     auto wait_reads = [&](half8 *a, u32x2 *r, uint32_t *v) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -547,7 +553,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         read_w(raw0, w_rd[0]);
         read_w(raw_nxt, w_rd[1]);
         read_sb(sb0, sc_rd);
-        read_sb(sb_nxt, sc_rd + 4);
+        read_sb(sb_nxt, sc_rd + 4 * BN);
         wait_reads(a_cur, raw0, sb0);
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
@@ -587,7 +593,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             uint32_t sb_nn[CB];
             read_a(a_nxt, sa);
             read_w(raw_nn, w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
-            read_sb(sb_nn, (u >= 2 ? sc_nxt_rd : sc_cur_rd) + (uint32_t)(4 * ((u + 2) & 3)));
+            read_sb(sb_nn, (u >= 2 ? sc_nxt_rd : sc_cur_rd) + (uint32_t)(4 * BN * ((u + 2) & 3)));
             __builtin_amdgcn_sched_barrier(0);
             // Chunk c's MFMAs and chunk c+1's dequantization (the next
             // group's first chunk for u = 3), independent of each other.
@@ -697,8 +703,8 @@ hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _
     const int n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
     hipError_t e = set_lds_attr<Fmt, BM, EPI>();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM, EPI>), dim3(max_tiles * n_tiles), dim3(NT), T::LDS, s, w, a, gather, a_rows,
-                       (uint32_t)(a_rows * w.n_cols * 2), out, aux, max_tiles, tiles, n_tiles_dev, wtab);
+    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM, EPI>), dim3(grouped_grid(max_tiles, n_tiles)), dim3(NT), T::LDS, s, w, a,
+                       gather, a_rows, (uint32_t)(a_rows * w.n_cols * 2), out, aux, max_tiles, tiles, n_tiles_dev, wtab);
     return hipGetLastError();
 }
 

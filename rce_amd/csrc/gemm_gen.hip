@@ -37,7 +37,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 64, KC = 64, NT = 512;
+constexpr int KC = 64, NT = 512;
 #ifndef GEN_DEPTH
 #define GEN_DEPTH 6
 #endif
@@ -48,9 +48,15 @@ constexpr int DEPTH = GEN_DEPTH;  // register sets of chunk loads in flight
 constexpr int CPB = GEN_CPB;      // chunks per barrier
 constexpr int NBUF = 2 * CPB;     // LDS chunk buffers
 static_assert(DEPTH % CPB == 0 && DEPTH >= 2 * CPB, "load ring");
+// Output tile 128 x 64.  This kernel is bound by its dequantization into
+// LDS, done once per row tile and weight, so the tallest tile is the
+// cheapest: a 64 x 128 tile (built and measured) dequantizes every weight
+// once per 64 rows and took the configs[3] workload with Q6_K experts from
+// 668 to 829 us.
+constexpr int BM = 128, BN = 64;
 constexpr int A_TILE = BM * KC * 2;               // 16 KB
 constexpr int B_TILE = BN * KC * 2;               // 8 KB
-constexpr int LDS_BYTES = 2 * GEN_CPB * (A_TILE + B_TILE);  // NBUF chunk buffers
+constexpr int LDS_BYTES = NBUF * (A_TILE + B_TILE);  // NBUF chunk buffers
 static_assert(4 * 2 * 4 * 64 * 16 <= LDS_BYTES, "the k-half partial sums reuse the tiles' LDS");
 
 __host__ __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
@@ -323,25 +329,41 @@ struct Stage {
     typename F::Raw w;
 };
 
-template <class F>
-__global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w, const _Float16 *__restrict__ A, size_t M,
-                                                 float *__restrict__ out, int m_tiles) {
+// Plain GEMM: tiles == nullptr, row tile mt covers rows mt * BM .. of M.
+// Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows <=
+// BM), multiplied by wtab[e], its A rows gathered through `gather` (when not
+// null); tiles at or past n_tiles[0] do nothing.  EPI (GemmEpilogue) is what
+// the block stores for an output element o with f32 sum v: v (f32 out),
+// binary16 silu(v), or binary16 silu(aux[o]) * v.
+template <class F, int EPI>
+__global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w_arg, const _Float16 *__restrict__ A, size_t M,
+                                                 void *__restrict__ out_v, int m_tiles, const int *__restrict__ gather,
+                                                 const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
+                                                 const DevWeight *__restrict__ wtab, const float *__restrict__ aux) {
     __shared__ __align__(16) unsigned char lds[LDS_BYTES];
-    // Blocks are dispatched round-robin over 8 XCDs; consecutive logical
-    // tiles (the m-tiles of one n-tile, sharing W rows) go to one XCD.
-    const int G = gridDim.x, L = blockIdx.x;
-    const int logical = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
-    const int mt = logical % m_tiles, nt = logical / m_tiles;
+    int mt, nt;
+    if (!tile_of_block<BN>(w_arg.n_rows, m_tiles, n_tiles, mt, nt)) return;  // before any barrier
+    DevWeight w = w_arg;
+    size_t m0 = (size_t)mt * BM;
+    int rows = (int)(M - m0 < (size_t)BM ? M - m0 : BM);
+    if (tiles) {
+        const MoeTile tl = tiles[mt];
+        w = wtab[tl.e];
+        m0 = (size_t)tl.r0;
+        rows = tl.rows;
+    }
     const size_t N = w.n_rows, K = w.n_cols;
-    const size_t m0 = (size_t)mt * BM, n0 = (size_t)nt * BN;
+    const size_t n0 = (size_t)nt * BN;
     const int nchunks = (int)(K / KC);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     // Loads: A rows ar and ar + 64 of the tile, 16-byte piece ap of the
-    // chunk (rows past M load row M - 1); W tile row wn, octet wo (rows past
-    // N: the last row, or the 64-row group's padding for the IL64 layouts).
+    // chunk (rows past the tile's load its last row); W tile row wn, octet
+    // wo (rows past N: the last row, or the 64-row group's padding for the
+    // IL64 layouts).
     const int ar = tid >> 3, ap = tid & 7;
-    const size_t am0 = m0 + ar < M ? m0 + ar : M - 1, am1 = m0 + ar + 64 < M ? m0 + ar + 64 : M - 1;
+    const size_t r0a = m0 + (size_t)(ar < rows ? ar : rows - 1), r1a = m0 + (size_t)(ar + 64 < rows ? ar + 64 : rows - 1);
+    const size_t am0 = gather ? (size_t)gather[r0a] : r0a, am1 = gather ? (size_t)gather[r1a] : r1a;
     const _Float16 *ag0 = A + am0 * K + 8 * ap, *ag1 = A + am1 * K + 8 * ap;
     const int wn = tid >> 3, wo = tid & 7;
     const size_t wrow = F::IL64 || n0 + wn < N ? n0 + wn : N - 1;
@@ -415,8 +437,18 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w, const _Float16 *__
             const f32x4 other = red[((pw * 2 + b) * 4 + rq) * 64 + lane];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const size_t m = m0 + 64 * rh + 32 * b + 8 * rq + 4 * h + e;
-                if (m < M && col < N) out[m * N + col] = acc[4 * rq + e] + other[e];
+                const int m = 64 * rh + 32 * b + 8 * rq + 4 * h + e;
+                if (m < rows && col < N) {
+                    const size_t o = (m0 + m) * N + col;
+                    const float v = acc[4 * rq + e] + other[e];
+                    if constexpr (EPI == GEPI_F32) {
+                        static_cast<float *>(out_v)[o] = v;
+                    } else if constexpr (EPI == GEPI_SILU_F16) {  // rce-qwen36-moe/src/lib.rs L459-461
+                        static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_ref(v);
+                    } else {  // silu(g) * u, rce-qwen36-moe/src/lib.rs L667-676
+                        static_cast<_Float16 *>(out_v)[o] = (_Float16)(silu_ref(aux[o]) * v);
+                    }
+                }
             }
         }
     }
@@ -426,7 +458,36 @@ template <class F>
 hipError_t launch(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
     const size_t m_tiles = (M + BM - 1) / BM, n_tiles = (w.n_rows + BN - 1) / BN;
     if (m_tiles * n_tiles > 0x7fffffffu || m_tiles > 0x7fffffffu) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_gen<F>, dim3((unsigned)(m_tiles * n_tiles)), dim3(NT), 0, s, w, a, M, out, (int)m_tiles);
+    hipLaunchKernelGGL((k_gemm_gen<F, GEPI_F32>), dim3((unsigned)(m_tiles * n_tiles)), dim3(NT), 0, s, w, a, M,
+                       (void *)out, (int)m_tiles, (const int *)nullptr, (const MoeTile *)nullptr, (const int *)nullptr,
+                       (const DevWeight *)nullptr, (const float *)nullptr);
+    return hipGetLastError();
+}
+
+template <class F>
+hipError_t launch_grouped(int epi, const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
+                          const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, void *out,
+                          const float *aux, hipStream_t s) {
+    const size_t n_tiles = (w.n_rows + BN - 1) / BN;
+    if ((size_t)max_tiles * n_tiles > 0x7ffffff0u) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)grouped_grid(max_tiles, (int)n_tiles));
+    switch (epi) {
+    case GEPI_F32:
+        hipLaunchKernelGGL((k_gemm_gen<F, GEPI_F32>), grid, dim3(NT), 0, s, w, a, a_rows, out, max_tiles, gather, tiles,
+                           n_tiles_dev, wtab, aux);
+        break;
+    case GEPI_SILU_F16:
+        hipLaunchKernelGGL((k_gemm_gen<F, GEPI_SILU_F16>), grid, dim3(NT), 0, s, w, a, a_rows, out, max_tiles, gather,
+                           tiles, n_tiles_dev, wtab, aux);
+        break;
+    case GEPI_SWIGLU_F16:
+        if (!aux) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm_gen<F, GEPI_SWIGLU_F16>), grid, dim3(NT), 0, s, w, a, a_rows, out, max_tiles, gather,
+                           tiles, n_tiles_dev, wtab, aux);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -462,6 +523,23 @@ hipError_t launch_gemm_gen(const DevWeight &w, const void *a_f16, size_t M, floa
     case T_Q6_K: return k % 256 ? hipErrorInvalidValue : launch<FQ6_K>(w, a, M, out, s);
     case T_Q4_0: return nibble_forms ? launch<FQ32<0>>(w, a, M, out, s) : hipErrorInvalidValue;
     case T_Q4_K: return nibble_forms && k % 256 == 0 ? launch<FQK<false>>(w, a, M, out, s) : hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemm_gen_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
+                                   const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
+                                   int epi, void *out, const float *aux, hipStream_t s) {
+    if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
+    if (!gemm_gen_supports(w.dtype, w.n_cols)) return hipErrorInvalidValue;
+    const _Float16 *a = static_cast<const _Float16 *>(a_f16);
+    switch (w.dtype) {
+    case T_Q8_0: return launch_grouped<FQ8_0>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_Q5_0: return launch_grouped<FQ32<1>>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_Q4_1: return launch_grouped<FQ32<2>>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_F16: return launch_grouped<FF16>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_Q5_K: return launch_grouped<FQK<true>>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_Q6_K: return launch_grouped<FQ6_K>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -361,6 +361,41 @@ hipError_t launch_f32_to_f16(const float *src, void *dst, size_t n, hipStream_t 
 struct MoeTile {
     int e, r0, rows, pad;
 };
+
+// Which output tile (row tile mt, column tile nt) block blockIdx.x of a
+// prefill GEMM computes; false: none (the block returns before any barrier).
+// Blocks are dispatched round-robin over the 8 XCDs (block L to XCD L % 8),
+// each XCD with its own L2.
+//   Plain (n_tiles_dev == nullptr; grid = m_tiles * column tiles): XCD x
+//   takes a contiguous range of tiles in (nt, mt) order, so the m-tiles
+//   sharing W rows run on one XCD.
+//   Grouped (grid = grouped_grid(m_tiles, column tiles)): only the first
+//   n_tiles_dev[0] row tiles exist; their V = n_tiles_dev[0] * column tiles
+//   blocks are numbered in (mt, nt) order and XCD x takes the range
+//   [x P, (x + 1) P), P = ceil(V / 8): each expert's tiles run on one or two
+//   XCDs, whose L2 then holds that expert's activation rows (with the
+//   (nt, mt) order every XCD read every expert's rows: 1.4x the HBM bytes
+//   of the expert weights on configs[3], 1.1x with this one, at the same
+//   speed), and blocks past V return at once.
+__host__ __device__ inline int grouped_grid(int m_tiles, int col_tiles) { return (m_tiles * col_tiles + 7) / 8 * 8; }
+#ifdef __HIPCC__
+template <int BN>
+__device__ __forceinline__ bool tile_of_block(size_t n_rows, int m_tiles, const int *n_tiles_dev, int &mt, int &nt) {
+    const int G = gridDim.x, L = blockIdx.x;
+    if (!n_tiles_dev) {
+        const int logical = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
+        mt = logical % m_tiles;
+        nt = logical / m_tiles;
+        return true;
+    }
+    const int nn = (int)((n_rows + BN - 1) / BN), V = n_tiles_dev[0] * nn, P = (V + 7) / 8;
+    const int v = (L % 8) * P + L / 8;
+    if (L / 8 >= P || v >= V) return false;
+    mt = v / nn;
+    nt = v % nn;
+    return true;
+}
+#endif
 // Stable grouping of pairs p = token * top_k + j by expert ids[p]:
 // offs[n_expert + 1], slot_of_pair[n_pairs] (-1: id out of range),
 // tok_of_slot[n_pairs], tiles[n_pairs / bm + n_expert] (bm-row pieces of
@@ -393,5 +428,10 @@ enum GemmEpilogue { GEPI_F32 = 0, GEPI_SILU_F16 = 1, GEPI_SWIGLU_F16 = 2 };
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
                                    int bm, int epi, void *out, const float *aux, hipStream_t s);
+// The same for the other formats (gemm_gen.hip: gemm_gen_supports' dtypes),
+// 128 x 64 output tiles: any tile table whose tiles hold at most 128 rows.
+hipError_t launch_gemm_gen_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
+                                   const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
+                                   int epi, void *out, const float *aux, hipStream_t s);
 
 }  // namespace rce_qmm

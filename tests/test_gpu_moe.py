@@ -184,17 +184,128 @@ def test_moe_swiglu(ctx, mode, tol, E, dm, dff, t, k, dt):
 
 
 def test_moe_f16_mfma_declines_formats_without_a_grouped_form(ctx):
-    """The grouped GEMM has the Q4_K / Q4_0 forms only: Q8_0 experts in
-    F16_MFMA are refused on the host (no launch), while EXACT takes them."""
+    """Q3_K has no matrix-core form: Q3_K experts in F16_MFMA are refused on
+    the host (no launch), while EXACT takes them."""
+    from rand_blocks import rand_blocks
     E, dm, dff, T, K = 2, 256, 512, 4, 1
     rng = np.random.default_rng(77)
-    w1 = [O.quantize((rng.standard_normal((dff, dm)) * 0.05).astype(np.float32), O.Q8_0) for _ in range(E)]
-    w2 = [O.quantize((rng.standard_normal((dm, dff)) * 0.05).astype(np.float32), O.Q8_0) for _ in range(E)]
+    w1 = [rand_blocks(rng, O.Q3_K, dff, dm, dmax=0.05 / 32) for _ in range(E)]
+    w2 = [rand_blocks(rng, O.Q3_K, dm, dff, dmax=0.05 / 32) for _ in range(E)]
     x = rng.standard_normal((T, dm)).astype(np.float32)
     ids = np.zeros((T, K), np.int32)
     gw = np.ones((T, K), np.float32)
     with pytest.raises(rce_amd.QmmError, match="no GPU kernel"):
-        run_moe(ctx, w1, w2, O.Q8_0, dm, dff, x, ids, gw, Mode.F16_MFMA)
-    got = run_moe(ctx, w1, w2, O.Q8_0, dm, dff, x, ids, gw, Mode.EXACT)
-    want = O.moe_ffn(x, w1, w2, O.Q8_0, dff, ids, gw)
+        run_moe(ctx, w1, w2, O.Q3_K, dm, dff, x, ids, gw, Mode.F16_MFMA)
+    got = run_moe(ctx, w1, w2, O.Q3_K, dm, dff, x, ids, gw, Mode.EXACT)
+    want = O.moe_ffn(x, w1, w2, O.Q3_K, dff, ids, gw)
     assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+# ---- grouped experts of the other formats on the matrix cores (gemm_gen.hip
+# with tiles, gather and the silu epilogue) -----------------------------------
+
+def expert_bytes(rng, dt, n, k, sigma=0.02):
+    from rand_blocks import float_bytes, rand_blocks
+    if dt == O.F16:
+        return float_bytes(rng, dt, n, k, sigma)
+    if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks
+        return rand_blocks(rng, dt, n, k, dmax=sigma / 8)
+    return O.quantize((rng.standard_normal((n, k)) * sigma).astype(F32), dt)
+
+
+def run_moe2(ctx, w1b, w2b, dt1, dt2, d_model, d_ff, x, ids, gw, mode):
+    """run_moe with a dtype per matrix."""
+    t_rows, top_k = ids.shape
+    W1 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt1, d_ff, d_model) for b in w1b]
+    W2 = [rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt2, d_model, d_ff) for b in w2b]
+    bx = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    bi = rce_amd.DeviceBuffer.from_numpy(ctx, ids.astype(np.int32))
+    bw = rce_amd.DeviceBuffer.from_numpy(ctx, gw.astype(F32))
+    bo = rce_amd.DeviceBuffer(ctx, t_rows * d_model * 4)
+    outs = []
+    for _ in range(2):
+        rce_amd.moe_ffn_dev(ctx, W1, W2, bx.ptr, t_rows, bi.ptr, bw.ptr, top_k, bo.ptr, mode)
+        ctx.synchronize()
+        outs.append(bo.download(F32, t_rows * d_model).reshape(t_rows, d_model))
+    for b in (bx, bi, bw, bo):
+        b.free()
+    for w in W1 + W2:
+        w.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "not run-to-run deterministic"
+    return outs[0]
+
+
+def f16_weights(b, dt, n, k):
+    """The binary16 weights the F16_MFMA kernels form: the oracle's
+    dequantized value rounded once (gemm_gen.hip), or for Q4_K the nibble
+    kernel's f16(f16(d*sc)*q + f16(-dmin*m)) (gemm_f16.hip)."""
+    if dt == O.Q4_K:
+        from test_gpu_gemm import q4k_f16_weights
+        return q4k_f16_weights(b, n, k)
+    return O.dequantize(b, dt, n * k).reshape(n, k).astype(np.float16).astype(np.float64)
+
+
+def f16_restatement(x, w1b, w2b, dt1, dt2, d_model, d_ff, ids, gw):
+    """The grouped F16_MFMA path restated in numpy: x and every weight
+    rounded to binary16 as the kernels form them, products summed in
+    float64, h = binary16(silu(W1 x)), y = W2 h, combined in decision order."""
+    x16 = x.astype(np.float16).astype(np.float64)
+    out = np.zeros((x.shape[0], d_model))
+    cache = {}
+    for t in range(x.shape[0]):
+        for j in range(ids.shape[1]):
+            e = int(ids[t, j])
+            if e not in cache:
+                cache[e] = (f16_weights(w1b[e], dt1, d_ff, d_model), f16_weights(w2b[e], dt2, d_model, d_ff))
+            a1, a2 = cache[e]
+            h = a1 @ x16[t]
+            h = (h / (1.0 + np.exp(-h))).astype(np.float16).astype(np.float64)
+            out[t] += float(gw[t, j]) * (a2 @ h)
+    return out
+
+
+GEN_MOE_CASES = [
+    # (n_expert, d_model, d_ff, t_rows, top_k, dtype of W1, dtype of W2)
+    (4, 512, 1024, 40, 2, O.Q6_K, O.Q6_K),
+    (4, 512, 1024, 40, 2, O.Q5_K, O.Q5_K),
+    (4, 512, 1024, 40, 2, O.Q8_0, O.Q8_0),
+    (6, 256, 512, 100, 2, O.Q4_K, O.Q6_K),   # Q4_K_M: Q4_K gate/up, Q6_K down (both kernels in one call)
+    (3, 256, 768, 17, 1, O.Q5_0, O.Q4_1),
+    (5, 256, 512, 300, 3, O.F16, O.Q8_0),    # experts past 128 rows: two tiles each
+]
+
+
+@pytest.mark.parametrize("E,dm,dff,t,k,dt1,dt2", GEN_MOE_CASES)
+def test_moe_f16_mfma_other_formats(ctx, E, dm, dff, t, k, dt1, dt2):
+    note(f"moe f16-mfma other formats E={E} d={dm} ff={dff} t={t} k={k} dt={dt1}/{dt2}")
+    rng = np.random.default_rng(800 + E + t + dt1)
+    w1 = [expert_bytes(rng, dt1, dff, dm) for _ in range(E)]
+    w2 = [expert_bytes(rng, dt2, dm, dff) for _ in range(E)]
+    x = rng.standard_normal((t, dm)).astype(F32)
+    ids, gw = rce_amd.moe_router(rng.standard_normal((t, E)).astype(F32), k)
+    got = run_moe2(ctx, w1, w2, dt1, dt2, dm, dff, x, ids, gw, Mode.F16_MFMA)
+    assert normwise(got, f16_restatement(x, w1, w2, dt1, dt2, dm, dff, ids, gw)) < 1e-4, \
+        "differs from the binary16 restatement of the same path"
+    ref = O.moe_ffn(x, w1, w2, dt1, dff, ids, gw, dtype2=dt2)
+    assert normwise(got, ref) < 3e-3
+    if dt1 == dt2:  # EXACT takes the same experts, within 1e-5 of the reference
+        assert normwise(run_moe2(ctx, w1, w2, dt1, dt2, dm, dff, x, ids, gw, Mode.EXACT), ref) < 1e-5
+
+
+@pytest.mark.parametrize("dt", [O.Q6_K, O.Q5_K, O.Q8_0])
+def test_moe_f16_mfma_other_formats_mixtral_shapes(ctx, dt):
+    """Real expert shapes (w1 14336 x 4096, w2 4096 x 14336) in the formats
+    Q4_K_M / Q5_K_M / Q8_0 models ship, 4 experts, 64 tokens top-2: every
+    token against the reference order within the fp16-dequant budget."""
+    E, dm, dff, t, k = 4, 4096, 14336, 64, 2
+    note(f"moe f16-mfma mixtral-shaped dt={dt}")
+    rng = np.random.default_rng(900 + dt)
+    q = lambda n, kk: rce_amd.quantize(rng.standard_normal((n, kk), dtype=F32) * F32(0.02), dt)  # noqa: E731
+    w1 = [q(dff, dm) for _ in range(E)]
+    w2 = [q(dm, dff) for _ in range(E)]
+    x = rng.standard_normal((t, dm)).astype(F32)
+    ids, gw = rce_amd.moe_router(rng.standard_normal((t, E)).astype(F32), k)
+    got = run_moe2(ctx, w1, w2, dt, dt, dm, dff, x, ids, gw, Mode.F16_MFMA)
+    err = normwise(got, O.moe_ffn(x, w1, w2, dt, dff, ids, gw))
+    note(f"  normwise {err:.3e}")
+    assert err < 3e-3
