@@ -699,10 +699,11 @@ def main():
                 per[key] = {"us": round(sms * 1e3, 2), "GB/s": round(sg, 1), "hbm_frac": round(sg / HBM_PEAK_GBS, 4)}
                 log(f"  {key}: {sms * 1e3:.2f} us  {sg:.0f} GB/s ({sg / HBM_PEAK_GBS:.1%})")
     if "gemm" in rows:  # configs[2]: Q4_K prefill GEMM 512x4096x4096 on f16 MFMA, then the other formats
-        for gdt in (G.Q4K, G.Q6K, G.Q8_0, G.Q5K):
+        for gdt in (G.Q4K, G.Q6K, G.Q8_0, G.Q5K, G.BF16, G.F32):
             gms, gs = time_gemm(hip, ctx, gdt, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
             gtf = 2.0 * 512 * 4096 * 4096 / (gms * 1e-3) / 1e12
-            key = f"{G(gdt).name.replace('Q4K', 'Q4_K').replace('Q5K', 'Q5_K').replace('Q6K', 'Q6_K')} GEMM 512x4096x4096 f16_mfma"
+            mname = "bf16_mfma" if gdt in (G.BF16, G.F32) else "f16_mfma"
+            key = f"{G(gdt).name.replace('Q4K', 'Q4_K').replace('Q5K', 'Q5_K').replace('Q6K', 'Q6_K')} GEMM 512x4096x4096 {mname}"
             per[key] = {"us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4)}
             kept[f"gemm {int(gdt)}"] = dict(gs, key=key)
             log(f"  {key}: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of f16 MFMA peak)")

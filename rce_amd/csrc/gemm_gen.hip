@@ -28,6 +28,8 @@
 // exceeds 65504 become infinite.
 #include "qmm_internal.h"
 
+#include <type_traits>
+
 namespace rce_qmm {
 namespace {
 
@@ -323,6 +325,74 @@ __host__ __device__ __forceinline__ void gen_pipeline(const int nchunks, Sync &&
     }
 }
 
+// BF16 / F32, LAYOUT_IL64_ROWS (chunk c of a row: 16 bytes, at (c * 64 + row
+// % 64) * 16 in its 64-row group; 8 BF16 or 4 F32 values).  These take the
+// bf16 matrix cores: binary16 cannot hold every BF16 or F32 weight (their
+// exponent range is binary32's).  dequant gives the weights as WT bf16
+// terms: BF16 exactly (one term), F32 as hi = bf16(w) plus lo = bf16(w - hi)
+// (16 significant bits; the rest is below 2^-16 of |w|).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+struct FBF16 {
+    static constexpr bool IL64 = true, BF = true;
+    static constexpr int WT = 1;
+    struct Raw {
+        u32x4 v;
+    };
+    __host__ __device__ static void load(Raw &r, const DevWeight &w, size_t row, int c, int o) {
+        const uint8_t *gb = w.base + (row >> 6) * w.group_stride;
+        r.v = ld<u32x4>(gb + ((size_t)(8 * c + o) * 64 + (row & 63)) * 16);
+    }
+    __host__ __device__ static void dequant(const Raw &r, int, int, bf16x8 (&t)[1]) { __builtin_memcpy(&t[0], &r.v, 16); }
+};
+struct FF32 {
+    static constexpr bool IL64 = true, BF = true;
+    static constexpr int WT = 2;
+    struct Raw {
+        u32x4 v0, v1;
+    };
+    __host__ __device__ static void load(Raw &r, const DevWeight &w, size_t row, int c, int o) {
+        const uint8_t *gb = w.base + (row >> 6) * w.group_stride + (row & 63) * 16;
+        const size_t ch = 16 * (size_t)c + 2 * o;  // weights 64 c + 8 o .. +7: chunks ch, ch + 1
+        r.v0 = ld<u32x4>(gb + ch * 1024);
+        r.v1 = ld<u32x4>(gb + (ch + 1) * 1024);
+    }
+    __host__ __device__ static void dequant(const Raw &r, int, int, bf16x8 (&t)[2]) {
+        float v[8];
+        __builtin_memcpy(v, &r.v0, 16);
+        __builtin_memcpy(v + 4, &r.v1, 16);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const __bf16 hi = (__bf16)v[i];
+            t[0][i] = hi;
+            t[1][i] = (__bf16)(v[i] - (float)hi);
+        }
+    }
+};
+
+// BF and WT of a format (the binary16 formats define neither: false, 1).
+template <class F, class = void>
+struct IsBf : std::false_type {};
+template <class F>
+struct IsBf<F, std::void_t<decltype(F::BF)>> : std::bool_constant<F::BF> {};
+template <class F, class = void>
+struct WtOf : std::integral_constant<int, 1> {};
+template <class F>
+struct WtOf<F, std::void_t<decltype(F::WT)>> : std::integral_constant<int, F::WT> {};
+
+// Eight binary16 values as bf16 hi = bf16(a) and lo = bf16(a - hi), both
+// rounded to nearest even; a - hi has at most 4 significant bits, so lo is
+// exact and hi + lo = a.
+__device__ __forceinline__ void split_bf16(const u32x4 &a, bf16x8 &hi, bf16x8 &lo) {
+    half8 h;
+    __builtin_memcpy(&h, &a, 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float f = (float)h[i];
+        hi[i] = (__bf16)f;
+        lo[i] = (__bf16)(f - (float)hi[i]);
+    }
+}
+
 template <class F>
 struct Stage {
     u32x4 a0, a1;
@@ -367,8 +437,16 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w_arg, const _Float16
     const _Float16 *ag0 = A + am0 * K + 8 * ap, *ag1 = A + am1 * K + 8 * ap;
     const int wn = tid >> 3, wo = tid & 7;
     const size_t wrow = F::IL64 || n0 + wn < N ? n0 + wn : N - 1;
+    // The bf16 formats (BF): A as two bf16 tiles, hi = bf16(a) then lo =
+    // a - hi (exact: a binary16 value has 11 significant bits), and WT
+    // weight tiles; one chunk per barrier (a chunk is 40 or 48 KB of LDS).
+    constexpr bool BF = IsBf<F>::value;
+    constexpr int WT = WtOf<F>::value;
+    constexpr int KCPB = BF ? 1 : CPB, KNBUF = 2 * KCPB;
+    constexpr int KA_TILE = BF ? 2 * A_TILE : A_TILE, KB_TILE = WT * B_TILE;
+    static_assert(KNBUF * (KA_TILE + KB_TILE) <= LDS_BYTES, "LDS");
     const int a_st0 = ar * 128 + 16 * (ap ^ swz(ar)), a_st1 = a_st0 + 64 * 128;
-    const int b_st = NBUF * A_TILE + wn * 128 + 16 * (wo ^ swz(wn));
+    const int b_st = KNBUF * KA_TILE + wn * 128 + 16 * (wo ^ swz(wn));
 
     auto load = [&](Stage<F> &s, int c) {
         s.a0 = ld<u32x4>(reinterpret_cast<const uint8_t *>(ag0 + (size_t)c * KC));
@@ -376,9 +454,22 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w_arg, const _Float16
         F::load(s.w, w, wrow, c, wo);
     };
     auto store = [&](const Stage<F> &s, int c, int buf) {
-        *reinterpret_cast<u32x4 *>(lds + buf * A_TILE + a_st0) = s.a0;
-        *reinterpret_cast<u32x4 *>(lds + buf * A_TILE + a_st1) = s.a1;
-        *reinterpret_cast<half8 *>(lds + buf * B_TILE + b_st) = F::dequant(s.w, c, wo);
+        if constexpr (BF) {
+            bf16x8 hi0, lo0, hi1, lo1, t[WT];
+            split_bf16(s.a0, hi0, lo0);
+            split_bf16(s.a1, hi1, lo1);
+            *reinterpret_cast<bf16x8 *>(lds + buf * KA_TILE + a_st0) = hi0;
+            *reinterpret_cast<bf16x8 *>(lds + buf * KA_TILE + a_st1) = hi1;
+            *reinterpret_cast<bf16x8 *>(lds + buf * KA_TILE + A_TILE + a_st0) = lo0;
+            *reinterpret_cast<bf16x8 *>(lds + buf * KA_TILE + A_TILE + a_st1) = lo1;
+            F::dequant(s.w, c, wo, t);
+#pragma unroll
+            for (int i = 0; i < WT; i++) *reinterpret_cast<bf16x8 *>(lds + buf * KB_TILE + i * B_TILE + b_st) = t[i];
+        } else {
+            *reinterpret_cast<u32x4 *>(lds + buf * A_TILE + a_st0) = s.a0;
+            *reinterpret_cast<u32x4 *>(lds + buf * A_TILE + a_st1) = s.a1;
+            *reinterpret_cast<half8 *>(lds + buf * B_TILE + b_st) = F::dequant(s.w, c, wo);
+        }
     };
 
     // Fragment reads: A rows 64 rh + 32 b + l32, B rows 32 ch + l32, slot
@@ -395,22 +486,42 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w_arg, const _Float16
             a_rd[b][j] = r * 128 + 16 * (g ^ swz(r));
         }
         const int r = 32 * ch + l32;
-        b_rd[j] = NBUF * A_TILE + r * 128 + 16 * (g ^ swz(r));
+        b_rd[j] = KNBUF * KA_TILE + r * 128 + 16 * (g ^ swz(r));
     }
     f32x16 acc0 = {}, acc1 = {};
     auto mma = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const half8 a0 = *reinterpret_cast<const half8 *>(lds + buf * A_TILE + a_rd[0][j]);
-            const half8 a1 = *reinterpret_cast<const half8 *>(lds + buf * A_TILE + a_rd[1][j]);
-            const half8 bf = *reinterpret_cast<const half8 *>(lds + buf * B_TILE + b_rd[j]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf, acc1, 0, 0, 0);
+            if constexpr (BF) {
+                // sum a.w as a_hi.w_hi + a_lo.w_hi (+ a_hi.w_lo for F32):
+                // every product exact in f32, f32 accumulation
+                const unsigned char *at = lds + buf * KA_TILE, *bt = lds + buf * KB_TILE;
+                const bf16x8 a0h = *reinterpret_cast<const bf16x8 *>(at + a_rd[0][j]);
+                const bf16x8 a0l = *reinterpret_cast<const bf16x8 *>(at + A_TILE + a_rd[0][j]);
+                const bf16x8 a1h = *reinterpret_cast<const bf16x8 *>(at + a_rd[1][j]);
+                const bf16x8 a1l = *reinterpret_cast<const bf16x8 *>(at + A_TILE + a_rd[1][j]);
+                const bf16x8 bh = *reinterpret_cast<const bf16x8 *>(bt + b_rd[j]);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h, bh, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h, bh, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0l, bh, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1l, bh, acc1, 0, 0, 0);
+                if constexpr (WT == 2) {
+                    const bf16x8 bl = *reinterpret_cast<const bf16x8 *>(bt + B_TILE + b_rd[j]);
+                    acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h, bl, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h, bl, acc1, 0, 0, 0);
+                }
+            } else {
+                const half8 a0 = *reinterpret_cast<const half8 *>(lds + buf * A_TILE + a_rd[0][j]);
+                const half8 a1 = *reinterpret_cast<const half8 *>(lds + buf * A_TILE + a_rd[1][j]);
+                const half8 bf = *reinterpret_cast<const half8 *>(lds + buf * B_TILE + b_rd[j]);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf, acc1, 0, 0, 0);
+            }
         }
     };
 
     Stage<F> st[DEPTH];
-    gen_pipeline<DEPTH, CPB>(
+    gen_pipeline<DEPTH, KCPB>(
         nchunks, [&] { __syncthreads(); }, [&](int slot, int ch) { load(st[slot], ch); },
         [&](int, int buf) { mma(buf); }, [&](int slot, int ch, int buf) { store(st[slot], ch, buf); });
     __syncthreads();  // every fragment read done: the partial sums reuse LDS
@@ -500,6 +611,8 @@ bool gemm_gen_supports(uint32_t dtype, size_t n_cols) {
     case T_Q5_0:
     case T_Q4_1:
     case T_F16:
+    case T_BF16:
+    case T_F32:
         return true;
     case T_Q5_K:
     case T_Q6_K:
@@ -519,6 +632,8 @@ hipError_t launch_gemm_gen(const DevWeight &w, const void *a_f16, size_t M, floa
     case T_Q5_0: return launch<FQ32<1>>(w, a, M, out, s);
     case T_Q4_1: return launch<FQ32<2>>(w, a, M, out, s);
     case T_F16: return launch<FF16>(w, a, M, out, s);
+    case T_BF16: return launch<FBF16>(w, a, M, out, s);
+    case T_F32: return launch<FF32>(w, a, M, out, s);
     case T_Q5_K: return k % 256 ? hipErrorInvalidValue : launch<FQK<true>>(w, a, M, out, s);
     case T_Q6_K: return k % 256 ? hipErrorInvalidValue : launch<FQ6_K>(w, a, M, out, s);
     case T_Q4_0: return nibble_forms ? launch<FQ32<0>>(w, a, M, out, s) : hipErrorInvalidValue;
@@ -537,6 +652,8 @@ hipError_t launch_gemm_gen_grouped(const DevWeight &w, const DevWeight *wtab, co
     case T_Q8_0: return launch_grouped<FQ8_0>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     case T_Q5_0: return launch_grouped<FQ32<1>>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     case T_Q4_1: return launch_grouped<FQ32<2>>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_BF16: return launch_grouped<FBF16>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    case T_F32: return launch_grouped<FF32>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     case T_F16: return launch_grouped<FF16>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     case T_Q5_K: return launch_grouped<FQK<true>>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
     case T_Q6_K: return launch_grouped<FQ6_K>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);

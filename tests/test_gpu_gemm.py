@@ -130,7 +130,10 @@ def test_gemm_supports_matrix():
     assert rce_amd.supports(G.Q8_0, 4096 + 64, Mode.F16_MFMA)
     assert not rce_amd.supports(G.Q8_0, 4096 + 32, Mode.F16_MFMA)  # whole chunks of 64
     assert not rce_amd.supports(G.Q6K, 4096 + 64, Mode.F16_MFMA)   # whole super-blocks
-    for dt in (G.F32, G.BF16, G.Q3K, G.Q1_0, G.Q2_0, G.I2S):       # beyond binary16's range / no form
+    for dt in (G.F32, G.BF16):                                     # the bf16 matrix-core forms
+        assert rce_amd.supports(dt, 4096, Mode.F16_MFMA), dt
+        assert not rce_amd.supports(dt, 4096 + 32, Mode.F16_MFMA), dt
+    for dt in (G.Q3K, G.Q1_0, G.Q2_0, G.I2S):                      # no matrix-core form
         assert not rce_amd.supports(dt, 4096, Mode.F16_MFMA), dt
 
 
@@ -140,7 +143,7 @@ def test_gemm_supports_matrix():
 
 def gen_weight_bytes(rng, dt, n, k):
     from rand_blocks import float_bytes, rand_blocks
-    if dt == O.F16:
+    if dt in (O.F16, O.BF16, O.F32):
         return float_bytes(rng, dt, n, k, 0.02)
     if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks
         return rand_blocks(rng, dt, n, k, dmax=0.02 / 8)
@@ -167,7 +170,33 @@ GEN_CASES = [
     (O.Q8_0, 128, 448, 40),
     (O.F16, 96, 832, 20),
     (O.Q4_1, 64, 1600, 9),
+    # the bf16 forms (BF16 exact; F32 as two bf16 terms), configs[2]'s
+    # shape and ragged ones
+    (O.BF16, 4096, 4096, 512),
+    (O.F32, 4096, 4096, 512),
+    (O.BF16, 100, 640, 17),
+    (O.F32, 130, 832, 65),
 ]
+
+
+def bf16_round(v):
+    """float32 -> the nearest bfloat16 (ties to even), as float64."""
+    u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def mfma_weights(b, dt, n, k):
+    """The weights the F16_MFMA kernels contract: the reference's f32
+    dequantized value rounded once to binary16; BF16 exactly; F32 as
+    bf16(w) + bf16(w - bf16(w))."""
+    v = O.dequantize(b, dt, n * k).reshape(n, k)
+    if dt == O.BF16:
+        return v.astype(np.float64)
+    if dt == O.F32:
+        hi = bf16_round(v)
+        return hi + bf16_round((v.astype(np.float64) - hi).astype(np.float32))
+    return v.astype(F16).astype(np.float64)
 
 
 @pytest.mark.parametrize("dt,n,k,t", GEN_CASES)
@@ -179,13 +208,35 @@ def test_gemm_other_formats_parity(ctx, dt, n, k, t):
     xv = x.astype(np.float64)
     w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
     got = run_gemm(ctx, w, x, G.F16)
-    wf = O.dequantize(b, dt, n * k).reshape(n, k).astype(F16).astype(np.float64)
+    wf = mfma_weights(b, dt, n, k)
     assert np.all(np.isfinite(wf))
     assert normwise(got, xv @ wf.T) < 1e-5, "kernel differs from the f16-weight restatement"
     ref = O.mm_batched(x.astype(F32), b, dt, n, k)
     assert normwise(got, ref) < 2e-3
     again = run_gemm(ctx, w, x, G.F16)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not run-to-run deterministic"
+    w.close()
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F32])
+def test_gemm_bf16_forms_beyond_binary16_range(ctx, dt):
+    """BF16 / F32 weights whose magnitudes binary16 cannot hold (2^100 and
+    2^-100 scales on alternate rows) keep their values on the bf16 matrix
+    cores: the result equals the restatement of the same bf16 terms."""
+    n, k, t = 192, 1024, 40
+    note(f"gemm bf16 forms, range, dtype={dt}")
+    rng = np.random.default_rng(7500 + dt)
+    wv = rng.standard_normal((n, k)).astype(F32)
+    wv[0::2] *= F32(2.0 ** 100)
+    wv[1::2] *= F32(2.0 ** -100)
+    b = wv.view(np.uint8).reshape(-1) if dt == O.F32 else (wv.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
+    x = rng.standard_normal((t, k)).astype(F16)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = run_gemm(ctx, w, x, G.F16)
+    want = x.astype(np.float64) @ mfma_weights(b, dt, n, k).T
+    for rows in (slice(0, None, 2), slice(1, None, 2)):  # each scale against its own rows
+        assert np.all(np.isfinite(got[:, rows]))
+        assert normwise(got[:, rows], want[:, rows]) < 1e-5
     w.close()
 
 

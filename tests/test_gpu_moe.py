@@ -206,7 +206,7 @@ def test_moe_f16_mfma_declines_formats_without_a_grouped_form(ctx):
 
 def expert_bytes(rng, dt, n, k, sigma=0.02):
     from rand_blocks import float_bytes, rand_blocks
-    if dt == O.F16:
+    if dt in (O.F16, O.BF16, O.F32):
         return float_bytes(rng, dt, n, k, sigma)
     if dt in (O.Q5_0, O.Q4_1):  # no quantizer in the reference: random blocks
         return rand_blocks(rng, dt, n, k, dmax=sigma / 8)
@@ -242,7 +242,8 @@ def f16_weights(b, dt, n, k):
     if dt == O.Q4_K:
         from test_gpu_gemm import q4k_f16_weights
         return q4k_f16_weights(b, n, k)
-    return O.dequantize(b, dt, n * k).reshape(n, k).astype(np.float16).astype(np.float64)
+    from test_gpu_gemm import mfma_weights
+    return mfma_weights(b, dt, n, k)
 
 
 def f16_restatement(x, w1b, w2b, dt1, dt2, d_model, d_ff, ids, gw):
@@ -272,6 +273,7 @@ GEN_MOE_CASES = [
     (6, 256, 512, 100, 2, O.Q4_K, O.Q6_K),   # Q4_K_M: Q4_K gate/up, Q6_K down (both kernels in one call)
     (3, 256, 768, 17, 1, O.Q5_0, O.Q4_1),
     (5, 256, 512, 300, 3, O.F16, O.Q8_0),    # experts past 128 rows: two tiles each
+    (4, 256, 512, 40, 2, O.BF16, O.F32),     # the bf16 forms
 ]
 
 
