@@ -5,6 +5,7 @@
 #include "qmm_gemv_kernels.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 namespace rce_qmm {
@@ -666,7 +667,18 @@ hipError_t launch_gemv_fx(const FxLaunch &f, const float *a, int mode, hipStream
     }
 }
 
+// RCE_QMM_Q8_MFMA: 0 = never the matrix-core form, 2 = always where it
+// applies (tests of both forms on the same shapes), unset = where faster.
+// Read at every call, so a test can switch it.
+static int q8_mfma_env() {
+    const char *e = getenv("RCE_QMM_Q8_MFMA");
+    return e ? atoi(e) : 1;
+}
+bool gemv_q8_mfma_enabled() { return q8_mfma_env() != 0; }
+bool gemv_q8_mfma_forced() { return q8_mfma_env() == 2; }
+
 bool gemv_q8_pre_supports(uint32_t dtype, size_t n_cols, size_t t_rows) {
+    if (gemv_q8_mfma_supports(dtype, n_cols, t_rows)) return true;
     if (t_rows < 2 || t_rows > 65535 * 8 || !gpu_supports(dtype, n_cols, 1)) return false;
     if (dtype != T_Q4_0 && dtype != T_Q8_0 && dtype != T_Q4_K && dtype != T_Q5_K && dtype != T_Q6_K) return false;
     return nt_for(units_per_row(dtype, n_cols)) == 256;
@@ -675,6 +687,19 @@ bool gemv_q8_pre_supports(uint32_t dtype, size_t n_cols, size_t t_rows) {
 hipError_t launch_gemv_q8_pre(const DevWeight &w, const float *a, size_t t_rows, float *out, void *ws,
                               hipStream_t s) {
     if (t_rows == 0 || w.n_rows == 0) return hipSuccess;
+    if (gemv_q8_mfma_supports(w.dtype, w.n_cols, t_rows) && gemv_q8_mfma_enabled() &&
+        (gemv_q8_mfma_preferred(w.n_cols, t_rows) || gemv_q8_mfma_forced())) {
+        // Q4_0 / Q8_0: the int8 matrix-core form (gemv_q8_mfma.hip), every
+        // token of a 16-token tile in one pass over the weight
+        const size_t k = w.n_cols;
+        const int total = (int)(t_rows * (k / 8));
+        unsigned char *q = static_cast<unsigned char *>(ws);
+        hipLaunchKernelGGL(k_quantize_act, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, a, k, total, q,
+                           (int)t_rows);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_gemv_q8_mfma(w, q, t_rows, out, s);
+    }
     if (!gemv_q8_pre_supports(w.dtype, w.n_cols, t_rows)) return launch_gemv(w, a, t_rows, out, 1, s);
     GemvGeom g = pick_gemv_geom(w, t_rows, 1);
     if (g.nt != 256 || g.tb < 2) return launch_gemv(w, a, t_rows, out, 1, s);

@@ -301,6 +301,16 @@ hipError_t launch_gemv(const DevWeight &w, const float *a, size_t t_rows, float 
 hipError_t launch_gemv_q8_pre(const DevWeight &w, const float *a, size_t t_rows, float *out, void *ws,
                               hipStream_t s);
 bool gemv_q8_pre_supports(uint32_t dtype, size_t n_cols, size_t t_rows);
+// The int8 matrix-core form of the same (gemv_q8_mfma.hip): Q4_0 / Q8_0,
+// n_cols a multiple of 256, 2 or more tokens; preq as k_quantize_act writes
+// it (the ActLds layout of t_rows tokens).  Chosen where it is faster
+// (gemv_q8_mfma_preferred); RCE_QMM_Q8_MFMA=0 turns it off, =2 forces it
+// wherever it applies (same bits either way).
+bool gemv_q8_mfma_supports(uint32_t dtype, size_t n_cols, size_t t_rows);
+bool gemv_q8_mfma_preferred(size_t n_cols, size_t t_rows);
+bool gemv_q8_mfma_enabled();
+bool gemv_q8_mfma_forced();
+hipError_t launch_gemv_q8_mfma(const DevWeight &w, const unsigned char *preq, size_t t_rows, float *out, hipStream_t s);
 GemvGeom pick_gemv_geom(const DevWeight &w, size_t t_rows, int mode);
 // Per-format launchers (gemv_<format>.hip), shape already chosen.
 hipError_t launch_gemv_q4_0(const DevWeight &w, const GemvGeom &g, const float *a, size_t t_rows, float *out,

@@ -141,6 +141,35 @@ def test_q8_path_bit_identical_to_its_restatement(ctx, dt, n, k, t_rows):
     assert np.max(np.abs(got - ex)) <= 2e-2 * np.max(np.abs(ex))
 
 
+MFMA_Q8_CASES = [
+    # (dtype, n_rows, n_cols, tokens): the int8 matrix-core form of the Q8
+    # path (Q4_0 / Q8_0, K a multiple of 256, 2+ tokens): ragged row tiles
+    # (n % 16), one stage (K 256), stage counts around the 4-stage unroll and
+    # the 8-stage ring (K 768, 1280, 2304), the configs' K, token tiles of
+    # 2, 16, 17 and 40 tokens
+    (O.Q4_0, 77, 256, 2), (O.Q8_0, 300, 768, 16), (O.Q4_0, 130, 1280, 17), (O.Q8_0, 64, 2304, 3),
+    (O.Q4_0, 11008, 4096, 8), (O.Q8_0, 4096, 4096, 8), (O.Q4_0, 4096, 14336, 40), (O.Q8_0, 33, 4096, 16),
+]
+
+
+@pytest.mark.parametrize("dt,n,k,t_rows", MFMA_Q8_CASES)
+def test_q8_matrix_core_form_bit_identical(ctx, monkeypatch, dt, n, k, t_rows):
+    """Forced on every case (RCE_QMM_Q8_MFMA=2; by default it runs where it
+    is the faster form): the same bits as the Q8 restatement, which the
+    decode kernels' form matches above; rows and tokens past the tile ends
+    are not stored."""
+    monkeypatch.setenv("RCE_QMM_Q8_MFMA", "2")
+    note(f"q8 mfma dtype={dt} n={n} k={k} t={t_rows}")
+    rng = np.random.default_rng(3100 + dt + n + t_rows)
+    b = make(rng, dt, n, k)
+    x = rng.standard_normal((t_rows, k)).astype(F32)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    got = run_dev(ctx, w, x, Mode.Q8)
+    want = O.mm_batched_q8(x, b, dt, n, k)
+    assert np.array_equal(bits(got), bits(want)), f"{np.sum(bits(got) != bits(want))} values differ"
+    w.close()
+
+
 def test_f16_activations_are_widened_exactly(ctx):
     rng = np.random.default_rng(4000)
     n, k, t = 512, 4096, 4
