@@ -530,6 +530,7 @@ def read_ceilings(hip, ctx, steps=200):
     that many bytes takes, launch cost included."""
     out = {}
     for name, nbytes in (("Q4_K 2048x2048", 2359296), ("Q4_K 2560x2048", 2949120), ("Q4_K 2048x5632", 6488064),
+                         ("Q4_K 4096x4096", 9469952),
                          ("Q4_K 11264x2048", 12976128), ("Q4_0 11008x4096 (headline)", 25422848),
                          ("Q6_K 32000x2048", 53760000)):
         us, var, empty = read_ceiling(hip, ctx, nbytes, steps)
