@@ -26,9 +26,11 @@
  *                          per-block formula and fold order.  Deterministic;
  *                          differs from EXACT by the activation rounding.
  *   RCE_QMM_MODE_F16_MFMA  (matmul / grouped experts) weights dequantized to
- *                          binary16 tiles and contracted on the matrix cores
- *                          with f32 accumulation in a fixed order; within
- *                          2e-3 normwise of mm_batched.
+ *                          binary16 tiles (BF16 / F32 weights: bf16 terms,
+ *                          activations split into two bf16 terms) and
+ *                          contracted on the matrix cores with f32
+ *                          accumulation in a fixed order; within 2e-3
+ *                          normwise of mm_batched (grouped experts: 3e-3).
  * Every mode is run-to-run bit-identical: no floating-point atomics, fixed
  * reduction trees.
  *
@@ -205,9 +207,9 @@ rce_qmm_status rce_qmm_quantize(uint32_t dtype, const float *src, size_t n_rows,
  * synchronization; the library's scratch is owned by the context, so calls
  * on one context must not overlap on different streams (one context per
  * stream).  RCE_QMM_MODE_F16_MFMA (the prefill form) takes Q4_K / Q4_0 /
- * Q5_K / Q6_K with n_cols a multiple of 256 and Q8_0 / Q5_0 / Q4_1 / F16 with
- * n_cols a multiple of 64 (rce_qmm_supports); its F16 activations must be
- * 16-byte aligned. */
+ * Q5_K / Q6_K with n_cols a multiple of 256 and Q8_0 / Q5_0 / Q4_1 / F16 /
+ * BF16 / F32 with n_cols a multiple of 64 (rce_qmm_supports); its F16
+ * activations must be 16-byte aligned. */
 rce_qmm_status rce_qmm_mm_batched_dev(rce_qmm_context *ctx, const void *a_dev, uint32_t a_dtype,
                                       size_t t_rows, const rce_qmm_weight *w, float *out_dev,
                                       rce_qmm_mode mode, void *stream);
@@ -242,8 +244,9 @@ rce_qmm_status rce_qmm_moe_router(const float *logits, size_t n_tokens, size_t n
  * e = ids[t, j]: h = silu(W1[e] x_t), y_j = W2[e] h, and
  * out_t = sum_j weights[t, j] * y_j in decision order from +0.0
  * (rce-qwen36-moe/src/lib.rs L667-710 with the router of rce-op-moe;
- * moe_combine L98-110).  w1[e]: [d_ff, d_model], w2[e]: [d_model, d_ff],
- * all of one dtype.  x_dev [t_rows, d_model] f32, ids_dev [t_rows, top_k]
+ * moe_combine L98-110).  w1[e]: [d_ff, d_model], w2[e]: [d_model, d_ff];
+ * the w1 of one dtype, the w2 of one dtype (the two may differ, as a
+ * Q4_K_M file's Q4_K gate with its Q6_K down).  x_dev [t_rows, d_model] f32, ids_dev [t_rows, top_k]
  * i32, weights_dev [t_rows, top_k] f32, out_dev [t_rows, d_model] f32.
  * Tokens are grouped per expert on the device (stable by expert, then
  * token, then decision). */
@@ -258,7 +261,8 @@ rce_qmm_status rce_qmm_moe_ffn_dev(rce_qmm_context *ctx, const rce_qmm_weight *c
  * g = gate[e] x_t, u = up[e] x_t, h = silu(g) * u, y_j = down[e] h
  * (swiglu_expert_serial, L667-676), out_t = sum_j weights[t, j] * y_j in
  * decision order from +0.0 (L698-703).  gate[e], up[e]: [d_ff, d_model],
- * down[e]: [d_model, d_ff], all of one dtype; buffers and grouping as
+ * down[e]: [d_model, d_ff]; gate and up of one dtype, down of one dtype
+ * (it may differ from theirs); buffers and grouping as
  * rce_qmm_moe_ffn_dev.  The shared expert and its sigmoid gate (L704-709)
  * stay with the caller (for instance one more call with n_expert = 1 and
  * the per-token gate as the weight). */

@@ -1,8 +1,10 @@
 // gemm_gen.hip -- the prefill GEMM of the GGUF quantized-matmul path for the
 // formats without a nibble-specialised matrix-core kernel (Q8_0, Q5_K, Q6_K,
-// Q5_0, Q4_1, F16): out[M, N] = A[M, K] . W[N, K]^T, A binary16, every
-// weight dequantized once per output tile into a binary16 tile in LDS and
-// contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).  It replaces
+// Q5_0, Q4_1, F16; BF16 and F32 on the bf16 matrix cores, below):
+// out[M, N] = A[M, K] . W[N, K]^T, A binary16, every weight dequantized once
+// per output tile into a binary16 tile in LDS and contracted with
+// v_mfma_f32_32x32x16_f16 (f32 accumulation); plain, or grouped over the
+// MoE tile table (tiles, gather and the epilogues of gemm_f16.hip).  It replaces
 // the reference's batched paths (rce-op-qmm/src/lib.rs L967-1023: the Q8_0
 // tile path for M >= 16, the Q5_K weight-stationary loop L1025-1100, the
 // per-row fallback of every other dtype) for the F16_MFMA mode.

@@ -501,7 +501,7 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
         }
     }
     // the grouped GEMM (F16_MFMA): the nibble kernel for Q4_K / Q4_0, the
-    // generic one for Q8_0, Q5_K, Q6_K, Q5_0, Q4_1 and F16
+    // generic one for Q8_0, Q5_K, Q6_K, Q5_0, Q4_1, F16, BF16 and F32
     auto experts_ok = [&](uint32_t dt, size_t k) { return supports_mode(dt, k, (int)mode); };
     if (!experts_ok(a1.dtype, d_model) || !experts_ok(a2.dtype, d_ff))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "the experts' dtype/shape has no GPU kernel in mode " +

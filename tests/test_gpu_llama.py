@@ -189,8 +189,9 @@ def test_llama_head_dim_128_runs_past_one_per_wave(ctx):
 @pytest.mark.parametrize("mode,tol", [(Mode.EXACT, 1e-5), (Mode.Q8, 1e-1)])
 def test_llama_tinyllama_width_long_context(ctx, mode, tol):
     """configs[4] widths (d 2048, 32 q / 4 kv heads, d_head 64, ffn 5632, Q4_K
-    linears, Q6_K 32000-row head) on 2 layers over 300 positions: every
-    wave's second 64-key run from position 256 on.  Bit-identical to the
+    linears, Q6_K 32000-row head) on 2 layers over 300 positions: from
+    position 256 on, wave 0 merges its second 64-key run (run 4) into its
+    first, with a finite running max.  Bit-identical to the
     device-order oracle at every position; EXACT within 1e-5 of the
     reference order (Q8's distance to it is the activation-rounding noise,
     bounded as in the full-depth test)."""
