@@ -399,12 +399,14 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(w.base + n0 * w.row_stride, (uint32_t)(wtile * w.row_stride));
         const uint32_t a_soff_max = (uint32_t)(nchunks - 1) * (KC * 2);
         // Loads of (virtual) iteration it: W position it % 4 of group
-        // it/4 + GA (past the end: group 0), then A chunk it + NS - 1 into
-        // stage it % NS (past the end: the last chunk).
+        // it/4 + GA, then A chunk it + NS - 1 into stage it % NS.  Past the
+        // end both repeat the last group / chunk: those loads only keep the
+        // in-order counts of the waits uniform, and data the block has just
+        // read is still in its L2, so the drain before the epilogue is short.
         auto issue = [&](int it) {
             const int q = it & 3;
             if (q < 2) {
-                const int g = (it >> 2) + GA, gs = g < ngroups ? g : 0;
+                const int g = (it >> 2) + GA, gs = g < ngroups ? g : ngroups - 1;
                 unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
                 if (q == 0) {
                     const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
@@ -444,7 +446,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int it = -4 * GA; it < 0; it++) {
             if ((it & 3) < 2) {
-                const int q = it & 3, g = (it >> 2) + GA, gs = g < ngroups ? g : 0;
+                const int q = it & 3, g = (it >> 2) + GA, gs = g < ngroups ? g : ngroups - 1;
                 unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
                 if (q == 0) {
                     const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
