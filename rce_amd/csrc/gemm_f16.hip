@@ -63,6 +63,7 @@
 // weights (normwise about 7e-4 at the Q4_K prefill shape; the stated budget
 // is 2e-3) and is deterministic: each output's summation order is fixed.
 #include "lds_limit.h"
+#include "gemm_epilogue.h"
 #include "qmm_internal.h"
 
 #include <type_traits>
@@ -663,9 +664,9 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                         if constexpr (EPI == GEPI_F32) {
                             static_cast<float *>(out_v)[o] = sum[e];
                         } else if constexpr (EPI == GEPI_SILU_F16) {  // rce-qwen36-moe/src/lib.rs L459-461
-                            static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_ref(sum[e]);
+                            static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_mfma(sum[e]);
                         } else {  // silu(g) * u, rce-qwen36-moe/src/lib.rs L667-676
-                            const float hv = silu_ref(aux[o]) * sum[e];
+                            const float hv = silu_mfma(aux[o]) * sum[e];
                             static_cast<_Float16 *>(out_v)[o] = (_Float16)hv;
                         }
                     }

@@ -28,6 +28,7 @@
 // One barrier per CPB (two) chunks.  Values: f16 rounding of A and W (about 2^-12
 // relative each) with f32 accumulation; weights whose dequantized magnitude
 // exceeds 65504 become infinite.
+#include "gemm_epilogue.h"
 #include "qmm_internal.h"
 
 #include <type_traits>
@@ -557,9 +558,9 @@ __global__ __launch_bounds__(NT) void k_gemm_gen(DevWeight w_arg, const _Float16
                     if constexpr (EPI == GEPI_F32) {
                         static_cast<float *>(out_v)[o] = v;
                     } else if constexpr (EPI == GEPI_SILU_F16) {  // rce-qwen36-moe/src/lib.rs L459-461
-                        static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_ref(v);
+                        static_cast<_Float16 *>(out_v)[o] = (_Float16)silu_mfma(v);
                     } else {  // silu(g) * u, rce-qwen36-moe/src/lib.rs L667-676
-                        static_cast<_Float16 *>(out_v)[o] = (_Float16)(silu_ref(aux[o]) * v);
+                        static_cast<_Float16 *>(out_v)[o] = (_Float16)(silu_mfma(aux[o]) * v);
                     }
                 }
             }
