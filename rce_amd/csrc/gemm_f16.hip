@@ -1,7 +1,8 @@
 // gemm_f16.hip -- prefill-shaped GEMM of the GGUF quantized-matmul path on
 // the CDNA4 matrix cores: out[M, N] = A[M, K] . W[N, K]^T with W in GGUF
-// Q4_K or Q4_0 blocks, dequantized to binary16 MFMA fragments in registers
-// and contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
+// Q4_K or Q4_0 blocks (and Q8_0, plain GEMM, 128 x 64 tiles: the Q80 format
+// below), dequantized to binary16 MFMA fragments in registers and
+// contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
 //
 // Tiling.  A block owns a BM x BN (M x N) output tile: 128 x 64 or 64 x 128
 // (8192 outputs), so a 512 x 4096 product is 256 tiles, one per CU; or
@@ -81,30 +82,29 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int KC = 64;                           // K per chunk (four MFMA k-steps of 16)
 constexpr int NC = 512;                          // compute threads (8 waves)
 constexpr int NT = NC + 128;                     // + 2 producer waves
-constexpr int NS = 6;                            // A stages (chunks), loaded NS - 1 ahead
 constexpr int NWBUF = 4, GA = 2;                 // W groups loaded GA groups ahead
-// W group g must be complete at the barrier of chunk 4g-3 (its headers are
-// read there for the scales): its last load (iteration 4(g-GA)+1) precedes
-// the loads of A chunk 4g-2 (iteration 4g-2-(NS-1)).
-static_assert(4 * GA >= NS + 2, "W groups loaded too late for the stage depth");
 // W buffer (g+GA) % NWBUF, refilled from iteration 4g, was last read for
 // chunk 4(g+GA-NWBUF)+3 (iteration 4(g+GA-NWBUF)+1 < 4g).
 static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
-static_assert(NS >= 3, "stage ring");
 
 // Output tile BM x BN: 128 x 64, 64 x 128, or 96 x 128 (grouped experts of
 // 65-96 rows, in one row tile instead of a 64-row tile and a mostly empty
 // second one).  Compute wave w = 2*kq + t holds RB x CB MFMA blocks of
 // 32 x 32 (rows 32*rb, columns BN/2 * t + 32*cb).
-template <int BM_>
+// NH: 64-byte pieces per row and scale group (2 for 4-bit weights, 4 for
+// Q8_0); the 8-bit tile keeps five A stages so that its larger weight
+// groups fit LDS.
+template <int BM_, int NH = 2>
 struct Tile {
     static constexpr int BM = BM_, BN = BM_ == 96 ? 128 : 8192 / BM_;
+    static constexpr int NS = NH == 2 ? 6 : 5;            // A stages (chunks), loaded NS - 1 ahead
     static constexpr int RB = BM / 32, CB = BN / 64;
     static constexpr int A_STAGE = BM * KC * 2;           // 16 KB / 8 KB
     static constexpr int A_LOADS = BM / 16;               // per producer per chunk (1 KB each)
     static constexpr int W_HALF = BN * 64;                // rows x 4 chunks x 16 B
-    static constexpr int W_LOADS = BN / 16;               // per producer per group (its half)
-    static constexpr int W_GROUP = 2 * W_HALF + BN * 16;  // + the scale headers
+    static constexpr int W_ROW_LOADS = BN / 16;           // loads of one 64-byte piece of every row
+    static constexpr int W_LOADS = W_ROW_LOADS * NH / 2;  // per producer per group (its pieces)
+    static constexpr int W_GROUP = NH * W_HALF + BN * 16; // + the scale headers
     static constexpr int SC_BUF = 2 * 4 * BN * 4;         // [set][chunk][column] of f16 {scale, bias}
     static constexpr int OFF_W = NS * A_STAGE;
     static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
@@ -113,6 +113,11 @@ struct Tile {
     static constexpr int RED_LDS = 8 * RB * 16 * 64 * 4;
     static constexpr int LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
     static_assert(LDS + BM * 4 <= 160 * 1024, "LDS budget");
+    // W group g must be complete at the barrier of chunk 4g-3 (its headers
+    // are read there for the scales): its last load (iteration 4(g-GA)+1)
+    // precedes the loads of A chunk 4g-2 (iteration 4g-2-(NS-1)).
+    static_assert(4 * GA >= NS + 2, "W groups loaded too late for the stage depth");
+    static_assert(NS >= 3, "stage ring");
     static_assert(RB >= 2 && RB <= 4 && CB >= 1 && CB <= 2 && 2 * RB <= 8,
                   "2 to 4 row blocks (the dequantization is spread over the first two), 1 or 2 column blocks "
                   "per compute wave; a column block's 2 RB output blocks finished by as many waves");
@@ -231,12 +236,14 @@ __device__ __forceinline__ void wait_vm_barrier() {
     __builtin_amdgcn_s_barrier();
 }
 
-// Four nibbles (one per byte of x, already masked to 0..15) as two f16
-// pairs in byte order: value = s * n + b (packed f16 fma, one rounding),
-// with sb = f16 {s, b}.  Eight VALU ops; two calls make one MFMA fragment.
+// Four bytes of x (nibbles masked to 0..15, or Q8_0's int8 values offset to
+// 0..255) as two f16 pairs in byte order: value = s * (n - OFF + 1024) + b
+// (packed f16 fma, one rounding), with sb = f16 {s, b}.  Eight VALU ops;
+// two calls make one MFMA fragment.
+template <int OFF = 1024>
 __device__ __forceinline__ void dequant4(uint32_t x, uint32_t sb, half2v &lo, half2v &hi) {
     const uint32_t K64 = 0x64646464u;
-    const half2v m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v m1024 = {(_Float16)(-(float)OFF), (_Float16)(-(float)OFF)};
     const half2v p = as_h2(sb);
     const half2v sc = __builtin_shufflevector(p, p, 0, 0), bias = __builtin_shufflevector(p, p, 1, 1);
     // byte pairs (n, 0x64): f16 bits 0x64nn = 1024 + n
@@ -265,6 +272,8 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 // super-block's four 64-groups; header = d, dmin, 12 scale bytes; scale
 // set 0 / 1 = the low / high nibble sub-block of each 64-group.
 struct Q4K {
+    static constexpr int NH = 2, OFF = 1024;
+    __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return (hf ? w.plane2 : w.plane1) + 64 * (size_t)g;
     }
@@ -297,6 +306,8 @@ struct Q4K {
 // header = their eight f16 scales; scale set 0 / 1 = block 2q / 2q+1.
 // d * (n - 8) = d*n + (-8d) (-8d exact; the fma rounds once).
 struct Q40 {
+    static constexpr int NH = 2, OFF = 1024;
+    __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return w.plane1 + 128 * (size_t)g + 64 * hf;
     }
@@ -316,6 +327,34 @@ struct Q40 {
 };
 
 
+// Q8_0: four 64-byte pieces per row and group: bytes 0..15 (plane 1) and
+// 16..31 (plane 2) of blocks 8g..8g+3 and 8g+4..8g+7 (piece 2 plane +
+// half); header = the eight blocks' f16 scales, set 0 / 1 = block 2q /
+// 2q+1.  K-step kq of chunk q is plane kq & 1 of block 2q + kq / 2.  A
+// value q (int8) is read as u = q + 128 (the byte xor 0x80), f16(1024 + u)
+// - 1152 = q exactly, and d * q + 0 rounds once: the reference's f32 value
+// d * q rounded to binary16.
+struct Q80 {
+    static constexpr int NH = 4, OFF = 1152;
+    __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
+        return ((hf >> 1) ? w.plane2 : w.plane1) + 128 * (size_t)g + 64 * (hf & 1);
+    }
+    __device__ static size_t hdr_off(int g) { return 16 * (size_t)g; }
+    __device__ static int half_of(int q, int kq) { return 2 * (kq & 1) + (q >> 1); }
+    __device__ static int piece_of(int q, int kq) { return 2 * (q & 1) + (kq >> 1); }
+    __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
+    __device__ static int sidx(int kq) { return kq >> 1; }
+    __device__ static uint32_t vals(uint32_t x, int) { return x ^ 0x80808080u; }
+    template <int Q>
+    __device__ static uint32_t scale(const u32x4 &h, int si) {
+        const uint32_t wd = Q == 0 ? h.x : Q == 1 ? h.y : Q == 2 ? h.z : h.w;  // scales 2q, 2q+1
+        const uint16_t bits = (uint16_t)(wd >> (16 * si));
+        _Float16 d;
+        __builtin_memcpy(&d, &bits, 2);
+        return pack_h2(d, (_Float16)0.0f);
+    }
+};
+
 template <int U>
 using ic = std::integral_constant<int, U>;
 
@@ -330,8 +369,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                                                  void *__restrict__ out_v, const float *__restrict__ aux, int m_tiles,
                                                  const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
                                                  const DevWeight *__restrict__ wtab) {
-    using T = Tile<BM_>;
-    constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB;
+    using T = Tile<BM_, Fmt::NH>;
+    constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB, NS = T::NS, NH = Fmt::NH;
     constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP, SC_BUF = T::SC_BUF;
     constexpr int OFF_W = T::OFF_W, OFF_SC = T::OFF_SC;
     extern __shared__ __align__(16) unsigned char lds[];
@@ -387,9 +426,9 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         //      The buffer starts at the tile's first row, so its offsets
         //      span the tile's rows only.
         const size_t wtile = N - n0 < (size_t)BN ? N - n0 : (size_t)BN;  // rows of this tile
-        uint32_t w_lane[T::W_LOADS];
+        uint32_t w_lane[T::W_ROW_LOADS];
 #pragma unroll
-        for (int i = 0; i < T::W_LOADS; i++) {
+        for (int i = 0; i < T::W_ROW_LOADS; i++) {
             const int wr = 16 * i + (lane >> 2);
             const size_t wrow = (size_t)wr < wtile ? (size_t)wr : wtile - 1;  // rows past the end load the last row
             w_lane[i] = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
@@ -410,12 +449,15 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 const int g = (it >> 2) + GA, gs = g < ngroups ? g : ngroups - 1;
                 unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
                 if (q == 0) {
-                    const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
 #pragma unroll
-                    for (int i = 0; i < T::W_LOADS; i++)
-                        buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
+                    for (int hf = 0; hf < NH; hf += 2) {  // pieces pw, pw + 2, ...
+                        const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, hf + pw);
+#pragma unroll
+                        for (int i = 0; i < T::W_ROW_LOADS; i++)
+                            buf_load_lds16(wbuf, w_lane[i], soff, dst + (hf + pw) * W_HALF + i * 1024);
+                    }
                 } else if (lane < BN / 2) {
-                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * (BN / 2) * 16);
+                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
                 }
             }
             const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
@@ -429,7 +471,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
             for (int pr = pt; pr < 2 * BN; pr += 128) {
                 const int p_col = pr & (BN - 1), p_si = pr / BN;
-                const uint32_t hdr_rd = lds0 + OFF_W + 2 * W_HALF + (uint32_t)(p_col * 16);
+                const uint32_t hdr_rd = lds0 + OFF_W + NH * W_HALF + (uint32_t)(p_col * 16);
                 const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
                 u32x4 hdr = lds_read16<0>(hdr_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP));
                 wait_lgkm0(hdr);
@@ -450,12 +492,15 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 const int q = it & 3, g = (it >> 2) + GA, gs = g < ngroups ? g : ngroups - 1;
                 unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
                 if (q == 0) {
-                    const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, pw);
 #pragma unroll
-                    for (int i = 0; i < T::W_LOADS; i++)
-                        buf_load_lds16(wbuf, w_lane[i], soff, dst + pw * W_HALF + i * 1024);
+                    for (int hf = 0; hf < NH; hf += 2) {  // pieces pw, pw + 2, ...
+                        const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, hf + pw);
+#pragma unroll
+                        for (int i = 0; i < T::W_ROW_LOADS; i++)
+                            buf_load_lds16(wbuf, w_lane[i], soff, dst + (hf + pw) * W_HALF + i * 1024);
+                    }
                 } else if (lane < BN / 2) {
-                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + 2 * W_HALF + pw * (BN / 2) * 16);
+                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
                 }
             }
             if (it + NS - 1 >= 0) {
@@ -516,7 +561,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
     for (int i = 0; i < RB * CB; i++) acc[i] = f32x16{};
     const int nsh = 4 * (kq & 1);  // low or high nibbles
-    auto nib = [&](uint32_t x) { return (x >> nsh) & 0x0F0F0F0Fu; };
+    auto nib = [&](uint32_t x) { return Fmt::vals(x, nsh); };
     auto read_a = [&](half8 *a, uint32_t addr) {
         a[0] = lds_read_frag<0>(addr);
         if constexpr (RB > 1) a[1] = lds_read_frag<4096>(addr);
@@ -566,8 +611,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
             half2v h0, h1, h2, h3;
-            dequant4(nib(raw0[cb].x), sb0[cb], h0, h1);
-            dequant4(nib(raw0[cb].y), sb0[cb], h2, h3);
+            dequant4<Fmt::OFF>(nib(raw0[cb].x), sb0[cb], h0, h1);
+            dequant4<Fmt::OFF>(nib(raw0[cb].y), sb0[cb], h2, h3);
             b_cur[cb] = join8(h0, h1, h2, h3);
         }
     }
@@ -607,8 +652,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++) {
                     acc[rb * CB + cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[rb], b_cur[cb], acc[rb * CB + cb], 0, 0, 0);
-                    if (rb == 0) dequant4(nib(raw_nxt[cb].x), sb, hq[cb][0], hq[cb][1]);
-                    if (rb == 1) dequant4(nib(raw_nxt[cb].y), sb, hq[cb][2], hq[cb][3]);
+                    if (rb == 0) dequant4<Fmt::OFF>(nib(raw_nxt[cb].x), sb, hq[cb][0], hq[cb][1]);
+                    if (rb == 1) dequant4<Fmt::OFF>(nib(raw_nxt[cb].y), sb, hq[cb][2], hq[cb][3]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -683,12 +728,12 @@ __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__
 
 template <class Fmt, int BM, int EPI>
 hipError_t set_lds_attr() {
-    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI>, Tile<BM>::LDS);
+    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI>, Tile<BM, Fmt::NH>::LDS);
 }
 
 template <class Fmt, int BM>
 hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
-    using T = Tile<BM>;
+    using T = Tile<BM, Fmt::NH>;
     const int m_tiles = (int)((M + T::BM - 1) / T::BM), n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
     hipError_t e = set_lds_attr<Fmt, BM, GEPI_F32>();
     if (e != hipSuccess) return e;
@@ -702,7 +747,7 @@ template <class Fmt, int BM, int EPI>
 hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
                               const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, void *out,
                               const float *aux, hipStream_t s) {
-    using T = Tile<BM>;
+    using T = Tile<BM, Fmt::NH>;
     const int n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
     hipError_t e = set_lds_attr<Fmt, BM, EPI>();
     if (e != hipSuccess) return e;
@@ -755,7 +800,12 @@ hipError_t gemm_prepare_lds() {
     };
     all_bm(Q4K{});
     all_bm(Q40{});
+    if (e == hipSuccess) e = set_lds_attr<Q80, 128, GEPI_F32>();
     return e;
+}
+
+bool gemm_q8_supports(uint32_t dtype, size_t n_cols) {
+    return dtype == T_Q8_0 && n_cols % 256 == 0 && n_cols < ((size_t)1 << 31);
 }
 
 bool gemm_supports(uint32_t dtype, size_t n_cols) {
@@ -806,6 +856,7 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
     if (M == 0 || w.n_rows == 0) return hipSuccess;
     if (!gemm_shape_ok(M, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
+    if (gemm_q8_supports(w.dtype, w.n_cols)) return launch_fmt<Q80, 128>(w, a, M, out, s);  // the 128 x 64 tile only
     const bool q4k = w.dtype == T_Q4_K;
     if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
     if (bm == 0) bm = gemm_tile_rows(M, false);

@@ -95,7 +95,7 @@ rce_qmm_status run_gemm(const void *a_dev, bool a_f16, size_t t_rows, const DevW
     }
     if (reinterpret_cast<uintptr_t>(a) % 16)
         return fail(RCE_QMM_BAD_SHAPE, "F16 activations of the F16_MFMA GEMM must be 16-byte aligned");
-    if (gemm_supports(dw.dtype, dw.n_cols)) {
+    if (gemm_supports(dw.dtype, dw.n_cols) || gemm_q8_supports(dw.dtype, dw.n_cols)) {
         // The kernel's activation offsets are 32-bit: slices of whole
         // 128-row tiles below 2^32 bytes each (each output's sum does not
         // depend on the slicing).

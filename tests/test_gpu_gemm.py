@@ -176,6 +176,13 @@ GEN_CASES = [
     (O.F32, 4096, 4096, 512),
     (O.BF16, 100, 640, 17),
     (O.F32, 130, 832, 65),
+    # Q8_0 with K a multiple of 256 runs on the nibble kernel's 128 x 64 tile
+    # (four 64-byte pieces per row and scale group, five A stages): one, two,
+    # three and five groups, ragged M and N, one token, two row tiles
+    (O.Q8_0, 64, 256, 1),
+    (O.Q8_0, 300, 768, 37),
+    (O.Q8_0, 130, 1280, 129),
+    (O.Q8_0, 96, 512, 200),
 ]
 
 
