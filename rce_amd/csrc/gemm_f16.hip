@@ -1,7 +1,8 @@
 // gemm_f16.hip -- prefill-shaped GEMM of the GGUF quantized-matmul path on
 // the CDNA4 matrix cores: out[M, N] = A[M, K] . W[N, K]^T with W in GGUF
-// Q4_K or Q4_0 blocks (and Q8_0, plain GEMM, 128 x 64 tiles: the Q80 format
-// below), dequantized to binary16 MFMA fragments in registers and
+// Q4_K or Q4_0 blocks (and Q8_0 and Q6_K, plain GEMM, 128 x 64 tiles: the
+// Q80 and Q6K formats below), dequantized to binary16 MFMA fragments in
+// registers and
 // contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
 //
 // Tiling.  A block owns a BM x BN (M x N) output tile: 128 x 64 or 64 x 128
@@ -78,6 +79,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// A lane's weight bytes of one k-step: l = 8 bytes (nibbles, or Q8_0's
+// values, or Q6_K's ql); h = Q6_K's 8 qh bytes.
+struct WRaw {
+    u32x2 l, h;
+};
 
 constexpr int KC = 64;                           // K per chunk (four MFMA k-steps of 16)
 constexpr int NC = 512;                          // compute threads (8 waves)
@@ -91,21 +97,23 @@ static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 // 65-96 rows, in one row tile instead of a 64-row tile and a mostly empty
 // second one).  Compute wave w = 2*kq + t holds RB x CB MFMA blocks of
 // 32 x 32 (rows 32*rb, columns BN/2 * t + 32*cb).
-// NH: 64-byte pieces per row and scale group (2 for 4-bit weights, 4 for
-// Q8_0); the 8-bit tile keeps five A stages so that its larger weight
-// groups fit LDS.
-template <int BM_, int NH = 2>
+// The weight format (below) sets the bytes of one scale group of the tile's
+// columns in LDS (W_GROUP), the loads a producer issues for them at group
+// position 0 (W_LOADS; position 1 is one load: headers or scales), the
+// {scale, bias} sets per chunk (NSETS) and the A stages that leave room
+// for them (NS).
+template <int BM_, class Fmt>
 struct Tile {
     static constexpr int BM = BM_, BN = BM_ == 96 ? 128 : 8192 / BM_;
-    static constexpr int NS = NH == 2 ? 6 : 5;            // A stages (chunks), loaded NS - 1 ahead
+    static constexpr int NS = Fmt::NS;                    // A stages (chunks), loaded NS - 1 ahead
     static constexpr int RB = BM / 32, CB = BN / 64;
     static constexpr int A_STAGE = BM * KC * 2;           // 16 KB / 8 KB
     static constexpr int A_LOADS = BM / 16;               // per producer per chunk (1 KB each)
     static constexpr int W_HALF = BN * 64;                // rows x 4 chunks x 16 B
     static constexpr int W_ROW_LOADS = BN / 16;           // loads of one 64-byte piece of every row
-    static constexpr int W_LOADS = W_ROW_LOADS * NH / 2;  // per producer per group (its pieces)
-    static constexpr int W_GROUP = NH * W_HALF + BN * 16; // + the scale headers
-    static constexpr int SC_BUF = 2 * 4 * BN * 4;         // [set][chunk][column] of f16 {scale, bias}
+    static constexpr int W_LOADS = Fmt::w_loads(BN);      // per producer per group at position 0
+    static constexpr int W_GROUP = Fmt::w_group(BN);
+    static constexpr int SC_BUF = Fmt::NSETS * 4 * BN * 4;  // [set][chunk][column] of f16 {scale, bias}
     static constexpr int OFF_W = NS * A_STAGE;
     static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
     static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
@@ -195,6 +203,13 @@ __device__ __forceinline__ u32x4 lds_read16(uint32_t a) {
     return v;
 }
 template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
 __device__ __forceinline__ uint32_t lds_read4(uint32_t a) {
     static_assert(OFF >= 0 && OFF < 65536, "ds offset");
     uint32_t v;
@@ -273,6 +288,10 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 // set 0 / 1 = the low / high nibble sub-block of each 64-group.
 struct Q4K {
     static constexpr int NH = 2, OFF = 1024;
+    static constexpr bool IL64 = false;
+    static constexpr int NSETS = 2, NS = NH == 2 ? 6 : 5;
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
+    static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return (hf ? w.plane2 : w.plane1) + 64 * (size_t)g;
@@ -307,6 +326,10 @@ struct Q4K {
 // d * (n - 8) = d*n + (-8d) (-8d exact; the fma rounds once).
 struct Q40 {
     static constexpr int NH = 2, OFF = 1024;
+    static constexpr bool IL64 = false;
+    static constexpr int NSETS = 2, NS = NH == 2 ? 6 : 5;
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
+    static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return w.plane1 + 128 * (size_t)g + 64 * hf;
@@ -336,6 +359,10 @@ struct Q40 {
 // d * q rounded to binary16.
 struct Q80 {
     static constexpr int NH = 4, OFF = 1152;
+    static constexpr bool IL64 = false;
+    static constexpr int NSETS = 2, NS = NH == 2 ? 6 : 5;
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
+    static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return ((hf >> 1) ? w.plane2 : w.plane1) + 128 * (size_t)g + 64 * (hf & 1);
     }
@@ -355,6 +382,30 @@ struct Q80 {
     }
 };
 
+// Q6_K (LAYOUT_IL64_Q6_K, 64-row groups, so only the 64-column tile): a
+// scale group is one super-block, whose 13 16-byte chunks (ql 0..7, qh
+// 8..11, scales 12) of the tile's 64 rows lie as 13 contiguous KB, then the
+// rows' d values (rce-op-qmm/src/lib.rs L425-454, dequant.rs L658-701).
+// Chunk q of the super-block is positions 64q .. 64q+63: 128-half n = q/2,
+// quarters 2(q&1) and 2(q&1)+1; k-step kq takes quarter 2(q&1) + kq/2,
+// positions l = 16(kq&1) .. +15 of it, lane half h l + 8h .. +7: ql bytes
+// 64n + 32(kq/2) + 16(kq&1) + 8h (chunk 4n + 2(kq/2) + (kq&1)), nibble
+// 4(q&1); qh bytes 32n + 16(kq&1) + 8h (chunk 8 + 2n + (kq&1)), bits
+// 2(2(q&1) + kq/2); scale 4q + kq (set kq).  u = ql | qh << 4 is q + 32 in
+// 0..63, and s u - 32 s with s = f16(d sc) rounds once to f16(s (u - 32))
+// (the reference's f32 d sc q rounded to binary16, but for the rounding of
+// d sc to binary16, as Q4_K's d sc).
+struct Q6K {
+    static constexpr bool IL64 = true;
+    static constexpr int NH = 0, OFF = 1024, NSETS = 4, NS = 6;
+    static constexpr int w_group(int) { return (int)IL64_Q6K_SB; }
+    static constexpr int w_loads(int) { return 6; }  // chunks 6 pw .. 6 pw + 5
+    __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
+    __device__ static int sidx(int kq) { return kq; }
+    __device__ static int ql_chunk(int q, int kq) { return 4 * (q >> 1) + 2 * (kq >> 1) + (kq & 1); }
+    __device__ static int qh_chunk(int q, int kq) { return 8 + 2 * (q >> 1) + (kq & 1); }
+};
+
 template <int U>
 using ic = std::integral_constant<int, U>;
 
@@ -369,7 +420,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                                                  void *__restrict__ out_v, const float *__restrict__ aux, int m_tiles,
                                                  const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
                                                  const DevWeight *__restrict__ wtab) {
-    using T = Tile<BM_, Fmt::NH>;
+    using T = Tile<BM_, Fmt>;
     constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB, NS = T::NS, NH = Fmt::NH;
     constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP, SC_BUF = T::SC_BUF;
     constexpr int OFF_W = T::OFF_W, OFF_SC = T::OFF_SC;
@@ -436,8 +487,41 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         size_t hrow = (size_t)(BN / 2 * pw + (lane & (BN / 2 - 1)));
         hrow = hrow < wtile ? hrow : wtile - 1;
         const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
-        const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(w.base + n0 * w.row_stride, (uint32_t)(wtile * w.row_stride));
+        // IL64 (Q6_K): the tile's 64 columns are one 64-row group, and every
+        // load is one 1 KB chunk of it (lane l: bytes 16 l ..)
+        const __amdgpu_buffer_rsrc_t wbuf =
+            Fmt::IL64 ? byte_buffer(w.base + (n0 >> 6) * w.group_stride, (uint32_t)w.group_stride)
+                      : byte_buffer(w.base + n0 * w.row_stride, (uint32_t)(wtile * w.row_stride));
         const uint32_t a_soff_max = (uint32_t)(nchunks - 1) * (KC * 2);
+        // W position q of group gs into the group buffer dst: at 0 the
+        // weight bytes (split formats: the 64-byte pieces pw, pw + 2, ... of
+        // every row; IL64: chunks 6 pw .. 6 pw + 5), at 1 one load (the
+        // 16-byte headers of rows BN/2 pw ..; IL64: the scales chunk, or the
+        // d values).
+        auto load_w = [&](int q, int gs, unsigned char *dst) {
+            if constexpr (Fmt::IL64) {
+                const uint32_t sb = (uint32_t)gs * (uint32_t)IL64_Q6K_SB, lo = 16u * (uint32_t)lane;
+                if (q == 0) {
+#pragma unroll
+                    for (int j = 0; j < 6; j++)
+                        buf_load_lds16(wbuf, lo, sb + (uint32_t)(6 * pw + j) * 1024u, dst + (6 * pw + j) * 1024);
+                } else if (pw == 0) {
+                    buf_load_lds16(wbuf, lo, sb + 12u * 1024u, dst + 12 * 1024);
+                } else if (lane < 8) {
+                    buf_load_lds16(wbuf, lo, sb + (uint32_t)IL64_Q6K_D, dst + 13 * 1024);
+                }
+            } else if (q == 0) {
+#pragma unroll
+                for (int hf = 0; hf < NH; hf += 2) {  // pieces pw, pw + 2, ...
+                    const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, hf + pw);
+#pragma unroll
+                    for (int i = 0; i < T::W_ROW_LOADS; i++)
+                        buf_load_lds16(wbuf, w_lane[i], soff, dst + (hf + pw) * W_HALF + i * 1024);
+                }
+            } else if (lane < BN / 2) {
+                buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
+            }
+        };
         // Loads of (virtual) iteration it: W position it % 4 of group
         // it/4 + GA, then A chunk it + NS - 1 into stage it % NS.  Past the
         // end both repeat the last group / chunk: those loads only keep the
@@ -447,18 +531,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             const int q = it & 3;
             if (q < 2) {
                 const int g = (it >> 2) + GA, gs = g < ngroups ? g : ngroups - 1;
-                unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
-                if (q == 0) {
-#pragma unroll
-                    for (int hf = 0; hf < NH; hf += 2) {  // pieces pw, pw + 2, ...
-                        const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, hf + pw);
-#pragma unroll
-                        for (int i = 0; i < T::W_ROW_LOADS; i++)
-                            buf_load_lds16(wbuf, w_lane[i], soff, dst + (hf + pw) * W_HALF + i * 1024);
-                    }
-                } else if (lane < BN / 2) {
-                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
-                }
+                load_w(q, gs, lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP);
             }
             const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
             unsigned char *dst = lds + ((it + NS - 1) % NS) * A_STAGE + pw * (A_STAGE / 2);
@@ -469,14 +542,29 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         // pair / BN), chunks 0..3 each
         auto make_scales = [&](int g) {
 #pragma unroll
-            for (int pr = pt; pr < 2 * BN; pr += 128) {
+            for (int pr = pt; pr < Fmt::NSETS * BN; pr += 128) {
                 const int p_col = pr & (BN - 1), p_si = pr / BN;
-                const uint32_t hdr_rd = lds0 + OFF_W + NH * W_HALF + (uint32_t)(p_col * 16);
                 const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
-                u32x4 hdr = lds_read16<0>(hdr_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP));
-                wait_lgkm0(hdr);
-                const u32x4 v = {Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
-                                 Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
+                const uint32_t gb = lds0 + OFF_W + (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
+                u32x4 v;
+                if constexpr (Fmt::IL64) {
+                    // the column's 16 signed scales and d: set p_si of chunk q is scale 4q + p_si
+                    u32x4 scb = lds_read16<0>(gb + 12u * 1024u + (uint32_t)(p_col * 16));
+                    uint32_t db = lds_read_u16<0>(gb + 13u * 1024u + (uint32_t)(p_col * 2));
+                    wait_lgkm0(scb, db);
+                    const float d = h2f(db);
+                    auto one = [&](uint32_t word) {
+                        const float ds = d * (float)(int8_t)(word >> (8 * p_si));  // exact: 11 x 8 bits
+                        const _Float16 sh = (_Float16)ds;
+                        return pack_h2(sh, (_Float16)(-32.0f * (float)sh));  // -32 s exact
+                    };
+                    v = u32x4{one(scb.x), one(scb.y), one(scb.z), one(scb.w)};
+                } else {
+                    u32x4 hdr = lds_read16<0>(gb + (uint32_t)(NH * W_HALF + p_col * 16));
+                    wait_lgkm0(hdr);
+                    v = u32x4{Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
+                              Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
+                }
                 const uint32_t wr = sc_wr + (uint32_t)((g & 1) * SC_BUF);
                 lds_write4(wr, v.x);
                 lds_write4(wr + 4 * BN, v.y);
@@ -490,18 +578,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         for (int it = -4 * GA; it < 0; it++) {
             if ((it & 3) < 2) {
                 const int q = it & 3, g = (it >> 2) + GA, gs = g < ngroups ? g : ngroups - 1;
-                unsigned char *dst = lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP;
-                if (q == 0) {
-#pragma unroll
-                    for (int hf = 0; hf < NH; hf += 2) {  // pieces pw, pw + 2, ...
-                        const uint32_t soff = (uint32_t)Fmt::half_off(w, gs, hf + pw);
-#pragma unroll
-                        for (int i = 0; i < T::W_ROW_LOADS; i++)
-                            buf_load_lds16(wbuf, w_lane[i], soff, dst + (hf + pw) * W_HALF + i * 1024);
-                    }
-                } else if (lane < BN / 2) {
-                    buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
-                }
+                load_w(q, gs, lds + OFF_W + (g & (NWBUF - 1)) * W_GROUP);
             }
             if (it + NS - 1 >= 0) {
                 const uint32_t soff = __builtin_elementwise_min((uint32_t)(it + NS - 1) * (KC * 2), a_soff_max);
@@ -547,11 +624,18 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     const int g0 = Fmt::acol(kq) + h;
     const uint32_t a_rd = lds0 + (uint32_t)(l32 * 128 + 16 * (g0 ^ ((l32 & 7) ^ ((l32 >> 3) & 1))));
     const int ncol = BN / 2 * t + l32;  // tile column of this lane in column block 0
-    uint32_t w_rd[4];                   // nibbles of chunk position q, lane half h (group buffer 0)
+    uint32_t w_rd[4], wh_rd[4];         // weight bytes of chunk position q, lane half h (group buffer 0)
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-        w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
-                                            16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
+    for (int q = 0; q < 4; q++) {
+        if constexpr (Fmt::IL64) {  // ql and qh chunks: column c at c * 16
+            w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::ql_chunk(q, kq) * 1024 + ncol * 16 + 8 * h);
+            wh_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::qh_chunk(q, kq) * 1024 + ncol * 16 + 8 * h);
+        } else {
+            w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
+                                                16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
+            wh_rd[q] = w_rd[q];
+        }
+    }
     // {scale, bias} of chunk q: [set][q][column], consecutive columns in
     // consecutive banks (a 32-column read is conflict-free; the
     // [column][set][chunk] order cost ~14 bank-conflict cycles per read)
@@ -561,16 +645,33 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
     for (int i = 0; i < RB * CB; i++) acc[i] = f32x16{};
     const int nsh = 4 * (kq & 1);  // low or high nibbles
-    auto nib = [&](uint32_t x) { return Fmt::vals(x, nsh); };
+    // the four byte values of word i (0, 1) of a lane's eight weights of
+    // chunk position q
+    auto nib = [&](const WRaw &r, int i, int q) -> uint32_t {
+        const uint32_t x = i ? r.l.y : r.l.x;
+        if constexpr (Fmt::IL64) {  // ql nibble | qh 2 bits << 4
+            const uint32_t y = i ? r.h.y : r.h.x;
+            return ((x >> (4 * (q & 1))) & 0x0F0F0F0Fu) | (((y >> (2 * (2 * (q & 1) + (kq >> 1)))) & 0x03030303u) << 4);
+        } else {
+            return Fmt::vals(x, nsh);
+        }
+    };
     auto read_a = [&](half8 *a, uint32_t addr) {
         a[0] = lds_read_frag<0>(addr);
         if constexpr (RB > 1) a[1] = lds_read_frag<4096>(addr);
         if constexpr (RB > 2) a[2] = lds_read_frag<8192>(addr);
         if constexpr (RB > 3) a[3] = lds_read_frag<12288>(addr);
     };
-    auto read_w = [&](u32x2 *r, uint32_t addr) {
-        r[0] = lds_read8<0>(addr);
-        if constexpr (CB > 1) r[1] = lds_read8<2048>(addr);
+    // column block cb: +32 rows of 64-byte pieces (split formats) or +32
+    // columns of 16 bytes (IL64)
+    constexpr int CBW = Fmt::IL64 ? 512 : 2048;
+    auto read_w = [&](WRaw *r, uint32_t addr, uint32_t addr_h) {
+        r[0].l = lds_read8<0>(addr);
+        if constexpr (CB > 1) r[1].l = lds_read8<CBW>(addr);
+        if constexpr (Fmt::IL64) {
+            r[0].h = lds_read8<0>(addr_h);
+            if constexpr (CB > 1) r[1].h = lds_read8<CBW>(addr_h);
+        }
     };
     // one chunk's {scale, bias} per column block (a register each, not the
     // group's four: the 96-row tile's accumulators need the room)
@@ -578,13 +679,14 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         v[0] = lds_read4<0>(addr);
         if constexpr (CB > 1) v[1] = lds_read4<128>(addr);  // +32 columns
     };
-    auto wait_reads = [&](half8 *a, u32x2 *r, uint32_t *v) {
+    auto wait_reads = [&](half8 *a, WRaw *r, uint32_t *v) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int i = 0; i < RB; i++) pin(a[i]);
 #pragma unroll
         for (int i = 0; i < CB; i++) {
-            pin(r[i]);
+            pin(r[i].l);
+            if constexpr (Fmt::IL64) pin(r[i].h);
             pin(v[i]);
         }
     };
@@ -592,27 +694,28 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     __builtin_amdgcn_s_barrier();  // barrier P1
     __builtin_amdgcn_s_barrier();  // barrier P2: chunk 0 dequantized, chunk 1's nibbles read
     half8 a_cur[RB], b_cur[CB];
-    u32x2 raw_nxt[CB];
+    WRaw raw_nxt[CB];
     uint32_t sb_nxt[CB];  // {scale, bias} of chunk c+1
     {
-        u32x2 raw0[CB];
+        WRaw raw0[CB];
         uint32_t sb0[CB];
         read_a(a_cur, a_rd);
-        read_w(raw0, w_rd[0]);
-        read_w(raw_nxt, w_rd[1]);
+        read_w(raw0, w_rd[0], wh_rd[0]);
+        read_w(raw_nxt, w_rd[1], wh_rd[1]);
         read_sb(sb0, sc_rd);
         read_sb(sb_nxt, sc_rd + 4 * BN);
         wait_reads(a_cur, raw0, sb0);
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
-            pin(raw_nxt[cb]);
+            pin(raw_nxt[cb].l);
+            if constexpr (Fmt::IL64) pin(raw_nxt[cb].h);
             pin(sb_nxt[cb]);
         }
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
             half2v h0, h1, h2, h3;
-            dequant4<Fmt::OFF>(nib(raw0[cb].x), sb0[cb], h0, h1);
-            dequant4<Fmt::OFF>(nib(raw0[cb].y), sb0[cb], h2, h3);
+            dequant4<Fmt::OFF>(nib(raw0[cb], 0, 0), sb0[cb], h0, h1);
+            dequant4<Fmt::OFF>(nib(raw0[cb], 1, 0), sb0[cb], h2, h3);
             b_cur[cb] = join8(h0, h1, h2, h3);
         }
     }
@@ -637,10 +740,10 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             const uint32_t sa = a_rd + (uint32_t)(st1 * A_STAGE);
             st1 = st1 == NS - 1 ? 0 : st1 + 1;
             half8 a_nxt[RB];
-            u32x2 raw_nn[CB];
+            WRaw raw_nn[CB];
             uint32_t sb_nn[CB];
             read_a(a_nxt, sa);
-            read_w(raw_nn, w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
+            read_w(raw_nn, w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur), wh_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
             read_sb(sb_nn, (u >= 2 ? sc_nxt_rd : sc_cur_rd) + (uint32_t)(4 * BN * ((u + 2) & 3)));
             __builtin_amdgcn_sched_barrier(0);
             // Chunk c's MFMAs and chunk c+1's dequantization (the next
@@ -652,8 +755,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++) {
                     acc[rb * CB + cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[rb], b_cur[cb], acc[rb * CB + cb], 0, 0, 0);
-                    if (rb == 0) dequant4<Fmt::OFF>(nib(raw_nxt[cb].x), sb, hq[cb][0], hq[cb][1]);
-                    if (rb == 1) dequant4<Fmt::OFF>(nib(raw_nxt[cb].y), sb, hq[cb][2], hq[cb][3]);
+                    if (rb == 0) dequant4<Fmt::OFF>(nib(raw_nxt[cb], 0, (u + 1) & 3), sb, hq[cb][0], hq[cb][1]);
+                    if (rb == 1) dequant4<Fmt::OFF>(nib(raw_nxt[cb], 1, (u + 1) & 3), sb, hq[cb][2], hq[cb][3]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -728,12 +831,12 @@ __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__
 
 template <class Fmt, int BM, int EPI>
 hipError_t set_lds_attr() {
-    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI>, Tile<BM, Fmt::NH>::LDS);
+    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI>, Tile<BM, Fmt>::LDS);
 }
 
 template <class Fmt, int BM>
 hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
-    using T = Tile<BM, Fmt::NH>;
+    using T = Tile<BM, Fmt>;
     const int m_tiles = (int)((M + T::BM - 1) / T::BM), n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
     hipError_t e = set_lds_attr<Fmt, BM, GEPI_F32>();
     if (e != hipSuccess) return e;
@@ -747,7 +850,7 @@ template <class Fmt, int BM, int EPI>
 hipError_t launch_fmt_grouped(const DevWeight &w, const DevWeight *wtab, const _Float16 *a, size_t a_rows,
                               const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles, void *out,
                               const float *aux, hipStream_t s) {
-    using T = Tile<BM, Fmt::NH>;
+    using T = Tile<BM, Fmt>;
     const int n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
     hipError_t e = set_lds_attr<Fmt, BM, EPI>();
     if (e != hipSuccess) return e;
@@ -801,11 +904,12 @@ hipError_t gemm_prepare_lds() {
     all_bm(Q4K{});
     all_bm(Q40{});
     if (e == hipSuccess) e = set_lds_attr<Q80, 128, GEPI_F32>();
+    if (e == hipSuccess) e = set_lds_attr<Q6K, 128, GEPI_F32>();
     return e;
 }
 
 bool gemm_q8_supports(uint32_t dtype, size_t n_cols) {
-    return dtype == T_Q8_0 && n_cols % 256 == 0 && n_cols < ((size_t)1 << 31);
+    return (dtype == T_Q8_0 || dtype == T_Q6_K) && n_cols % 256 == 0 && n_cols < ((size_t)1 << 31);
 }
 
 bool gemm_supports(uint32_t dtype, size_t n_cols) {
@@ -856,7 +960,9 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
     if (M == 0 || w.n_rows == 0) return hipSuccess;
     if (!gemm_shape_ok(M, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
-    if (gemm_q8_supports(w.dtype, w.n_cols)) return launch_fmt<Q80, 128>(w, a, M, out, s);  // the 128 x 64 tile only
+    // the 128 x 64 tile only
+    if (gemm_q8_supports(w.dtype, w.n_cols)) return w.dtype == T_Q8_0 ? launch_fmt<Q80, 128>(w, a, M, out, s)
+                                                                      : launch_fmt<Q6K, 128>(w, a, M, out, s);
     const bool q4k = w.dtype == T_Q4_K;
     if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
     if (bm == 0) bm = gemm_tile_rows(M, false);

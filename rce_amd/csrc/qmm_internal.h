@@ -349,7 +349,8 @@ hipError_t launch_gemv_ternary(const DevWeight &w, const GemvGeom &g, const floa
 // Prefill GEMM on the matrix cores (gemm_f16.hip): out[M, n_rows] =
 // A[M, n_cols] . W^T, A binary16, W dequantized to binary16 tiles.
 bool gemm_supports(uint32_t dtype, size_t n_cols);
-// Q8_0 weights on the same kernel (plain GEMM, 128 x 64 tiles, K % 256 == 0).
+// Q8_0 and Q6_K weights on the same kernel (plain GEMM, 128 x 64 tiles,
+// K % 256 == 0).
 bool gemm_q8_supports(uint32_t dtype, size_t n_cols);
 bool gemm_shape_ok(size_t a_rows, const DevWeight &w);
 // bm: output tile rows, 64 (tile 64 x 128), 96 (96 x 128) or 128 (128 x 64);

@@ -183,6 +183,10 @@ GEN_CASES = [
     (O.Q8_0, 300, 768, 37),
     (O.Q8_0, 130, 1280, 129),
     (O.Q8_0, 96, 512, 200),
+    # Q6_K likewise (the 64-row groups of its interleaved layout, 13 chunks
+    # per super-block, four scale sets per chunk): one and three super-blocks
+    (O.Q6_K, 64, 256, 1),
+    (O.Q6_K, 130, 768, 129),
 ]
 
 
@@ -191,6 +195,27 @@ def bf16_round(v):
     u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
     return r.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def q6k_f16_weights(b, n, k):
+    """Q6_K bytes -> the f16 weights the nibble kernel forms:
+    f16(f16(d*sc) * q), the scale rounded to binary16 first (GGUF block:
+    ql 128, qh 64, 16 signed scales, f16 d; position P of a super-block: half
+    n = P // 128, quarter qd, l: ql byte 64n + l + 32(qd & 1), high nibble
+    for qd >= 2, qh byte 32n + l bits 2qd, scale 8n + l // 16 + 2qd)."""
+    nsb = k // 256
+    blk = np.frombuffer(bytes(b), np.uint8).reshape(n, nsb, 210)
+    ql, qh = blk[:, :, :128].astype(np.int32), blk[:, :, 128:192].astype(np.int32)
+    sc = blk[:, :, 192:208].view(np.int8).astype(np.float32)
+    d = blk[:, :, 208:210].copy().view(np.float16).astype(np.float32)[:, :, 0]
+    P = np.arange(256)
+    hn, qd, l = P // 128, (P % 128) // 32, P % 32
+    lo = ql[:, :, 64 * hn + l + 32 * (qd & 1)]
+    nib = np.where(qd >= 2, lo >> 4, lo & 15)
+    q = (nib | (((qh[:, :, 32 * hn + l] >> (2 * qd)) & 3) << 4)) - 32
+    s16 = (d[:, :, None] * sc).astype(np.float16).astype(np.float64)  # f32 product, one rounding
+    w = (s16[:, :, 8 * hn + l // 16 + 2 * qd] * q).astype(np.float16)
+    return w.reshape(n, k).astype(np.float64)
 
 
 def mfma_weights(b, dt, n, k):
@@ -215,7 +240,8 @@ def test_gemm_other_formats_parity(ctx, dt, n, k, t):
     xv = x.astype(np.float64)
     w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
     got = run_gemm(ctx, w, x, G.F16)
-    wf = mfma_weights(b, dt, n, k)
+    # Q6_K's plain GEMM runs the nibble kernel (scale rounded to binary16 first)
+    wf = q6k_f16_weights(b, n, k) if dt == O.Q6_K else mfma_weights(b, dt, n, k)
     assert np.all(np.isfinite(wf))
     assert normwise(got, xv @ wf.T) < 1e-5, "kernel differs from the f16-weight restatement"
     ref = O.mm_batched(x.astype(F32), b, dt, n, k)
