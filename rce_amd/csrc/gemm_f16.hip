@@ -1,9 +1,9 @@
 // gemm_f16.hip -- prefill-shaped GEMM of the GGUF quantized-matmul path on
 // the CDNA4 matrix cores: out[M, N] = A[M, K] . W[N, K]^T with W in GGUF
-// Q4_K or Q4_0 blocks (and Q8_0 and Q6_K, plain GEMM, 128 x 64 tiles: the
-// Q80 and Q6K formats below), dequantized to binary16 MFMA fragments in
-// registers and
-// contracted with v_mfma_f32_32x32x16_f16 (f32 accumulation).
+// Q4_K, Q5_K or Q4_0 blocks (and Q8_0 and Q6_K, plain GEMM, 128 x 64
+// tiles: the Q80 and Q6K formats below), dequantized to binary16 MFMA
+// fragments in registers and contracted with v_mfma_f32_32x32x16_f16 (f32
+// accumulation).
 //
 // Tiling.  A block owns a BM x BN (M x N) output tile: 128 x 64 or 64 x 128
 // (8192 outputs), so a 512 x 4096 product is 256 tiles, one per CU; or
@@ -105,7 +105,12 @@ static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 template <int BM_, class Fmt>
 struct Tile {
     static constexpr int BM = BM_, BN = BM_ == 96 ? 128 : 8192 / BM_;
-    static constexpr int NS = Fmt::NS;                    // A stages (chunks), loaded NS - 1 ahead
+    // A stages (chunks), loaded NS - 1 ahead: six where the tile's LDS holds
+    // them, else five
+    static constexpr int pipe_lds(int ns) {
+        return ns * BM * KC * 2 + NWBUF * Fmt::w_group(BN) + 2 * Fmt::NSETS * 4 * BN * 4;
+    }
+    static constexpr int NS = pipe_lds(6) + BM * 4 <= 160 * 1024 ? 6 : 5;
     static constexpr int RB = BM / 32, CB = BN / 64;
     static constexpr int A_STAGE = BM * KC * 2;           // 16 KB / 8 KB
     static constexpr int A_LOADS = BM / 16;               // per producer per chunk (1 KB each)
@@ -117,6 +122,7 @@ struct Tile {
     static constexpr int OFF_W = NS * A_STAGE;
     static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
     static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
+    static_assert(PIPE_LDS == pipe_lds(NS), "LDS layout");
     // the partial sums of every wave for one column block cb at a time
     static constexpr int RED_LDS = 8 * RB * 16 * 64 * 4;
     static constexpr int LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
@@ -200,6 +206,13 @@ __device__ __forceinline__ u32x4 lds_read16(uint32_t a) {
     static_assert(OFF >= 0 && OFF < 65536, "ds offset");
     u32x4 v;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_u8(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    uint32_t v;
+    asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
 }
 template <int OFF>
@@ -288,8 +301,8 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 // set 0 / 1 = the low / high nibble sub-block of each 64-group.
 struct Q4K {
     static constexpr int NH = 2, OFF = 1024;
-    static constexpr bool IL64 = false;
-    static constexpr int NSETS = 2, NS = NH == 2 ? 6 : 5;
+    static constexpr bool IL64 = false, HB = false;
+    static constexpr int NSETS = 2;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
@@ -321,13 +334,27 @@ struct Q4K {
     }
 };
 
+// Q5_K (LAYOUT_SPLIT_Q5_K): Q4_K's halves, header and scales, plus per row
+// and group the 32 bytes of fifth bits of its four 64-groups (plane 3: one
+// 8-byte word per 64-group, bit l / 32 + l = the fifth bit of position l /
+// 32 + l), loaded with the halves.  A lane's eight weights of k-step kq of
+// chunk q are positions 32(kq & 1) + 16(kq / 2) + 8h .. +7 of 64-group q:
+// their fifth bits are byte 4(kq & 1) + 2(kq / 2) + h of that word.
+// u = nibble | bit << 4 in 0..31, value d1 u - min1 as for Q4_K.
+struct Q5K : Q4K {
+    static constexpr bool HB = true;
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16 + bn * 32; }
+    static constexpr int w_loads(int bn) { return bn / 16 * NH / 2 + bn / 64; }
+    __device__ static int hb_byte(int kq) { return 4 * (kq & 1) + 2 * (kq >> 1); }
+};
+
 // Q4_0: halves = the 16-byte nibble runs of blocks 8g..8g+3 and 8g+4..8g+7;
 // header = their eight f16 scales; scale set 0 / 1 = block 2q / 2q+1.
 // d * (n - 8) = d*n + (-8d) (-8d exact; the fma rounds once).
 struct Q40 {
     static constexpr int NH = 2, OFF = 1024;
-    static constexpr bool IL64 = false;
-    static constexpr int NSETS = 2, NS = NH == 2 ? 6 : 5;
+    static constexpr bool IL64 = false, HB = false;
+    static constexpr int NSETS = 2;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
@@ -359,8 +386,8 @@ struct Q40 {
 // d * q rounded to binary16.
 struct Q80 {
     static constexpr int NH = 4, OFF = 1152;
-    static constexpr bool IL64 = false;
-    static constexpr int NSETS = 2, NS = NH == 2 ? 6 : 5;
+    static constexpr bool IL64 = false, HB = false;
+    static constexpr int NSETS = 2;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
@@ -396,8 +423,8 @@ struct Q80 {
 // (the reference's f32 d sc q rounded to binary16, but for the rounding of
 // d sc to binary16, as Q4_K's d sc).
 struct Q6K {
-    static constexpr bool IL64 = true;
-    static constexpr int NH = 0, OFF = 1024, NSETS = 4, NS = 6;
+    static constexpr bool IL64 = true, HB = false;
+    static constexpr int NH = 0, OFF = 1024, NSETS = 4;
     static constexpr int w_group(int) { return (int)IL64_Q6K_SB; }
     static constexpr int w_loads(int) { return 6; }  // chunks 6 pw .. 6 pw + 5
     __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
@@ -484,6 +511,16 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             const size_t wrow = (size_t)wr < wtile ? (size_t)wr : wtile - 1;  // rows past the end load the last row
             w_lane[i] = (uint32_t)(wrow * w.row_stride) + 16u * (uint32_t)((lane & 3) ^ ((wr >> 2) & 3));
         }
+        // HB (Q5_K): the fifth-bit bytes, 32 per row; instruction i of this
+        // producer covers rows 32 (BN/64 pw + i) .. +31, 2 lanes per row
+        constexpr int HB_LOADS = Fmt::HB ? BN / 64 : 0;
+        uint32_t hb_lane[HB_LOADS > 0 ? HB_LOADS : 1];
+#pragma unroll
+        for (int i = 0; i < HB_LOADS; i++) {
+            const int hr = 32 * (HB_LOADS * pw + i) + (lane >> 1);
+            const size_t hbrow = (size_t)hr < wtile ? (size_t)hr : wtile - 1;
+            hb_lane[i] = (uint32_t)(hbrow * w.row_stride) + 16u * (uint32_t)(lane & 1);
+        }
         size_t hrow = (size_t)(BN / 2 * pw + (lane & (BN / 2 - 1)));
         hrow = hrow < wtile ? hrow : wtile - 1;
         const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
@@ -517,6 +554,12 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
                     for (int i = 0; i < T::W_ROW_LOADS; i++)
                         buf_load_lds16(wbuf, w_lane[i], soff, dst + (hf + pw) * W_HALF + i * 1024);
+                }
+                if constexpr (Fmt::HB) {
+#pragma unroll
+                    for (int i = 0; i < HB_LOADS; i++)
+                        buf_load_lds16(wbuf, hb_lane[i], (uint32_t)(w.plane3 + 32 * (size_t)gs),
+                                       dst + NH * W_HALF + BN * 16 + (HB_LOADS * pw + i) * 1024);
                 }
             } else if (lane < BN / 2) {
                 buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
@@ -633,7 +676,10 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         } else {
             w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
                                                 16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
-            wh_rd[q] = w_rd[q];
+            if constexpr (Fmt::HB)  // the fifth-bit byte of the lane's eight weights
+                wh_rd[q] = lds0 + OFF_W + (uint32_t)(NH * W_HALF + BN * 16 + ncol * 32 + 8 * q + Fmt::hb_byte(kq) + h);
+            else
+                wh_rd[q] = w_rd[q];
         }
     }
     // {scale, bias} of chunk q: [set][q][column], consecutive columns in
@@ -652,6 +698,9 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         if constexpr (Fmt::IL64) {  // ql nibble | qh 2 bits << 4
             const uint32_t y = i ? r.h.y : r.h.x;
             return ((x >> (4 * (q & 1))) & 0x0F0F0F0Fu) | (((y >> (2 * (2 * (q & 1) + (kq >> 1)))) & 0x03030303u) << 4);
+        } else if constexpr (Fmt::HB) {  // nibble | fifth bit << 4: bit e of the byte's half to byte e
+            const uint32_t b4 = i ? (r.h.x >> 4) & 15u : r.h.x & 15u;
+            return Fmt::vals(x, nsh) | (((b4 * 0x00204081u) & 0x01010101u) << 4);
         } else {
             return Fmt::vals(x, nsh);
         }
@@ -671,6 +720,9 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         if constexpr (Fmt::IL64) {
             r[0].h = lds_read8<0>(addr_h);
             if constexpr (CB > 1) r[1].h = lds_read8<CBW>(addr_h);
+        } else if constexpr (Fmt::HB) {
+            r[0].h.x = lds_read_u8<0>(addr_h);
+            if constexpr (CB > 1) r[1].h.x = lds_read_u8<1024>(addr_h);  // +32 rows of 32 bytes
         }
     };
     // one chunk's {scale, bias} per column block (a register each, not the
@@ -686,7 +738,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             pin(r[i].l);
-            if constexpr (Fmt::IL64) pin(r[i].h);
+            if constexpr (Fmt::IL64 || Fmt::HB) pin(r[i].h);
             pin(v[i]);
         }
     };
@@ -708,7 +760,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
             pin(raw_nxt[cb].l);
-            if constexpr (Fmt::IL64) pin(raw_nxt[cb].h);
+            if constexpr (Fmt::IL64 || Fmt::HB) pin(raw_nxt[cb].h);
             pin(sb_nxt[cb]);
         }
 #pragma unroll
@@ -902,6 +954,7 @@ hipError_t gemm_prepare_lds() {
         all_epi(fmt, ic<128>{});
     };
     all_bm(Q4K{});
+    all_bm(Q5K{});
     all_bm(Q40{});
     if (e == hipSuccess) e = set_lds_attr<Q80, 128, GEPI_F32>();
     if (e == hipSuccess) e = set_lds_attr<Q6K, 128, GEPI_F32>();
@@ -914,7 +967,7 @@ bool gemm_q8_supports(uint32_t dtype, size_t n_cols) {
 
 bool gemm_supports(uint32_t dtype, size_t n_cols) {
     if (n_cols >= (size_t)1 << 31 || n_cols == 0) return false;
-    if (dtype == T_Q4_K) return n_cols % 256 == 0;
+    if (dtype == T_Q4_K || dtype == T_Q5_K) return n_cols % 256 == 0;
     if (dtype == T_Q4_0) return n_cols % 256 == 0;  // whole scale groups of 8 blocks
     return false;
 }
@@ -935,25 +988,33 @@ int gemm_tile_rows(size_t rows_hint, bool grouped) {
     return rows_hint <= 64 ? 64 : (rows_hint <= 96 ? 96 : 128);
 }
 
+// Call f with the format tag of a nibble-kernel weight type (false when the
+// type has no format here).
+template <class F>
+static bool with_fmt(uint32_t dtype, F &&f) {
+    switch (dtype) {
+    case T_Q4_K: f(Q4K{}); return true;
+    case T_Q5_K: f(Q5K{}); return true;
+    case T_Q4_0: f(Q40{}); return true;
+    default: return false;
+    }
+}
+
 hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, const void *a_f16, size_t a_rows,
                                    const int *gather, const MoeTile *tiles, const int *n_tiles_dev, int max_tiles,
                                    int bm, int epi, void *out, const float *aux, hipStream_t s) {
     if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
     if (!gemm_shape_ok(a_rows, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
-    const bool q4k = w.dtype == T_Q4_K;
-    if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
-    if (bm == 64)
-        return q4k ? launch_grouped_epi<Q4K, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
-                   : launch_grouped_epi<Q40, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
-    if (bm == 96)
-        return q4k ? launch_grouped_epi<Q4K, 96>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
-                   : launch_grouped_epi<Q40, 96>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
-    if (bm == 128)
-        return q4k ? launch_grouped_epi<Q4K, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
-                   : launch_grouped_epi<Q40, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux,
-                                                  s);
-    return hipErrorInvalidValue;
+    hipError_t e = hipErrorInvalidValue;
+    with_fmt(w.dtype, [&](auto fmt) {
+        using F = decltype(fmt);
+        if (bm == 64) e = launch_grouped_epi<F, 64>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+        if (bm == 96) e = launch_grouped_epi<F, 96>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+        if (bm == 128)
+            e = launch_grouped_epi<F, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    });
+    return e;
 }
 
 hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s, int bm) {
@@ -963,13 +1024,15 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
     // the 128 x 64 tile only
     if (gemm_q8_supports(w.dtype, w.n_cols)) return w.dtype == T_Q8_0 ? launch_fmt<Q80, 128>(w, a, M, out, s)
                                                                       : launch_fmt<Q6K, 128>(w, a, M, out, s);
-    const bool q4k = w.dtype == T_Q4_K;
-    if (!q4k && w.dtype != T_Q4_0) return hipErrorInvalidValue;
     if (bm == 0) bm = gemm_tile_rows(M, false);
-    if (bm == 64) return q4k ? launch_fmt<Q4K, 64>(w, a, M, out, s) : launch_fmt<Q40, 64>(w, a, M, out, s);
-    if (bm == 96) return q4k ? launch_fmt<Q4K, 96>(w, a, M, out, s) : launch_fmt<Q40, 96>(w, a, M, out, s);
-    if (bm == 128) return q4k ? launch_fmt<Q4K, 128>(w, a, M, out, s) : launch_fmt<Q40, 128>(w, a, M, out, s);
-    return hipErrorInvalidValue;
+    hipError_t e = hipErrorInvalidValue;
+    with_fmt(w.dtype, [&](auto fmt) {
+        using F = decltype(fmt);
+        if (bm == 64) e = launch_fmt<F, 64>(w, a, M, out, s);
+        if (bm == 96) e = launch_fmt<F, 96>(w, a, M, out, s);
+        if (bm == 128) e = launch_fmt<F, 128>(w, a, M, out, s);
+    });
+    return e;
 }
 
 }  // namespace rce_qmm

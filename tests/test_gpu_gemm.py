@@ -1,9 +1,9 @@
 """GPU parity of the prefill GEMM on the matrix cores (RCE_QMM_MODE_F16_MFMA).
 
-The mode dequantizes the weights to binary16 (Q4_K / Q4_0 in registers,
-gemm_f16.hip; Q8_0, Q5_K, Q6_K, Q5_0, Q4_1, F16 into LDS tiles,
-gemm_gen.hip) and contracts them with f16 MFMA, f32 accumulation.  Two
-checks per case:
+The mode dequantizes the weights to binary16 and contracts them with f16
+MFMA, f32 accumulation: Q4_K, Q5_K, Q4_0 (and Q8_0, Q6_K in a plain GEMM)
+in registers, gemm_f16.hip; the other formats into LDS tiles,
+gemm_gen.hip.  Two checks per case:
   * against a numpy restatement of the same f16 weights (f64 products):
     only accumulation order differs, so normwise error must be ~1e-6 --
     this catches a wrong fragment layout, K order or scale;
@@ -30,12 +30,14 @@ def note(msg):
     print(msg, flush=True)
 
 
-def q4k_f16_weights(b, n, k):
+def q4k_f16_weights(b, n, k, q5=False):
     """Q4_K bytes -> the f16 weights the kernel forms: f16(f16(d*sc)*q + f16(-dmin*m))
     (one rounding of the fma), decoded with numpy from the GGUF layout
-    (rce-ingest-gguf dequant.rs L546-589)."""
+    (rce-ingest-gguf dequant.rs L546-589).  q5: Q5_K's 176-byte blocks, the
+    32 qh bytes after the scales giving q's fifth bit (qh byte l, bit s =
+    position 32 s + l; dequant.rs L591-636)."""
     nsb = k // 256
-    blk = b.reshape(n, nsb, 144)
+    blk = np.frombuffer(bytes(b), np.uint8).reshape(n, nsb, 176 if q5 else 144)
     d = blk[:, :, 0:2].copy().view(F16)[:, :, 0].astype(F32)
     dmin = blk[:, :, 2:4].copy().view(F16)[:, :, 0].astype(F32)
     s = blk[:, :, 4:16].astype(np.int32)
@@ -48,10 +50,15 @@ def q4k_f16_weights(b, n, k):
         else:
             sc[:, :, j] = (s[:, :, j + 4] & 0x0F) | ((s[:, :, j - 4] >> 6) << 4)
             mn[:, :, j] = (s[:, :, j + 4] >> 4) | ((s[:, :, j] >> 6) << 4)
-    qs = blk[:, :, 16:144].astype(np.int32).reshape(n, nsb, 4, 32)
+    qs_at = 48 if q5 else 16
+    qs = blk[:, :, qs_at:qs_at + 128].astype(np.int32).reshape(n, nsb, 4, 32)
     q = np.zeros((n, nsb, 8, 32), np.int32)
     q[:, :, 0::2, :] = qs & 0x0F
     q[:, :, 1::2, :] = qs >> 4
+    if q5:
+        qh = blk[:, :, 16:48].astype(np.int32)
+        for sb in range(8):
+            q[:, :, sb, :] |= ((qh >> sb) & 1) << 4
     d1 = (d[:, :, None] * sc.astype(F32)).astype(F16).astype(np.float64)
     m1 = (-(dmin[:, :, None] * mn.astype(F32))).astype(F16).astype(np.float64)
     w = (q.astype(np.float64) * d1[:, :, :, None] + m1[:, :, :, None]).astype(F16)
@@ -187,6 +194,11 @@ GEN_CASES = [
     # per super-block, four scale sets per chunk): one and three super-blocks
     (O.Q6_K, 64, 256, 1),
     (O.Q6_K, 130, 768, 129),
+    # Q5_K: Q4_K's tiles plus 32 bytes of fifth bits per row and group; the
+    # 64-, 96- and 128-row tiles, ragged M and N
+    (O.Q5_K, 64, 256, 1),
+    (O.Q5_K, 200, 768, 80),
+    (O.Q5_K, 130, 1280, 50),
 ]
 
 
@@ -240,8 +252,13 @@ def test_gemm_other_formats_parity(ctx, dt, n, k, t):
     xv = x.astype(np.float64)
     w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
     got = run_gemm(ctx, w, x, G.F16)
-    # Q6_K's plain GEMM runs the nibble kernel (scale rounded to binary16 first)
-    wf = q6k_f16_weights(b, n, k) if dt == O.Q6_K else mfma_weights(b, dt, n, k)
+    # Q6_K and Q5_K run the nibble kernel (scale rounded to binary16 first)
+    if dt == O.Q6_K:
+        wf = q6k_f16_weights(b, n, k)
+    elif dt == O.Q5_K:
+        wf = q4k_f16_weights(b, n, k, q5=True)
+    else:
+        wf = mfma_weights(b, dt, n, k)
     assert np.all(np.isfinite(wf))
     assert normwise(got, xv @ wf.T) < 1e-5, "kernel differs from the f16-weight restatement"
     ref = O.mm_batched(x.astype(F32), b, dt, n, k)

@@ -238,10 +238,11 @@ def run_moe2(ctx, w1b, w2b, dt1, dt2, d_model, d_ff, x, ids, gw, mode):
 def f16_weights(b, dt, n, k):
     """The binary16 weights the F16_MFMA kernels form: the oracle's
     dequantized value rounded once (gemm_gen.hip), or for Q4_K the nibble
-    kernel's f16(f16(d*sc)*q + f16(-dmin*m)) (gemm_f16.hip)."""
-    if dt == O.Q4_K:
+    kernel's f16(f16(d*sc)*q + f16(-dmin*m)) (gemm_f16.hip), for Q4_K and
+    Q5_K."""
+    if dt in (O.Q4_K, O.Q5_K):
         from test_gpu_gemm import q4k_f16_weights
-        return q4k_f16_weights(b, n, k)
+        return q4k_f16_weights(b, n, k, q5=dt == O.Q5_K)
     from test_gpu_gemm import mfma_weights
     return mfma_weights(b, dt, n, k)
 
