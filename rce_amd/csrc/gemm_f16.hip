@@ -956,8 +956,8 @@ hipError_t gemm_prepare_lds() {
     all_bm(Q4K{});
     all_bm(Q5K{});
     all_bm(Q40{});
-    if (e == hipSuccess) e = set_lds_attr<Q80, 128, GEPI_F32>();
-    if (e == hipSuccess) e = set_lds_attr<Q6K, 128, GEPI_F32>();
+    all_epi(Q80{}, ic<128>{});
+    all_epi(Q6K{}, ic<128>{});
     return e;
 }
 
@@ -1006,6 +1006,13 @@ hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, co
     if (max_tiles <= 0 || w.n_rows == 0 || a_rows == 0) return hipSuccess;
     if (!gemm_shape_ok(a_rows, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
+    // Q8_0 and Q6_K: the 128 x 64 tile only
+    if (gemm_q8_supports(w.dtype, w.n_cols)) {
+        if (bm != 128) return hipErrorInvalidValue;
+        return w.dtype == T_Q8_0
+                   ? launch_grouped_epi<Q80, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s)
+                   : launch_grouped_epi<Q6K, 128>(epi, w, wtab, a, a_rows, gather, tiles, n_tiles_dev, max_tiles, out, aux, s);
+    }
     hipError_t e = hipErrorInvalidValue;
     with_fmt(w.dtype, [&](auto fmt) {
         using F = decltype(fmt);

@@ -500,16 +500,23 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
                 return fail(RCE_QMM_BAD_SHAPE, "up matrices must match the gate matrices in dtype and shape");
         }
     }
-    // the grouped GEMM (F16_MFMA): the nibble kernel for Q4_K / Q4_0, the
-    // generic one for Q8_0, Q5_K, Q6_K, Q5_0, Q4_1, F16, BF16 and F32
+    // the grouped GEMM (F16_MFMA): the nibble kernel for Q4_K / Q5_K / Q4_0
+    // (any tile) and Q8_0 / Q6_K with K a multiple of 256 (128-row tiles),
+    // the generic one for the rest (Q8_0 at other K, Q5_0, Q4_1, F16, BF16
+    // and F32)
     auto experts_ok = [&](uint32_t dt, size_t k) { return supports_mode(dt, k, (int)mode); };
     if (!experts_ok(a1.dtype, d_model) || !experts_ok(a2.dtype, d_ff))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "the experts' dtype/shape has no GPU kernel in mode " +
                                                    std::to_string((int)mode));
     if (t_rows == 0) return RCE_QMM_OK;
     if (!x_dev || !ids_dev || !weights_dev || !out_dev) return fail(RCE_QMM_NULL_ARGUMENT, "null device buffer");
-    if (mode == RCE_QMM_MODE_F16_MFMA && ((gemm_supports(a1.dtype, d_model) && !gemm_shape_ok(t_rows, a1)) ||
-                                          (gemm_supports(a2.dtype, d_ff) && !gemm_shape_ok(t_rows * top_k, a2))))
+    // the nibble kernel's offsets are 32-bit: past that the generic kernel,
+    // where it takes the format
+    const bool fit1 = gemm_shape_ok(t_rows, a1), fit2 = gemm_shape_ok(t_rows * top_k, a2);
+    const bool nib1 = fit1 && gemm_supports(a1.dtype, d_model), nib2 = fit2 && gemm_supports(a2.dtype, d_ff);
+    const bool q8n1 = fit1 && gemm_q8_supports(a1.dtype, d_model), q8n2 = fit2 && gemm_q8_supports(a2.dtype, d_ff);
+    if (mode == RCE_QMM_MODE_F16_MFMA && ((!nib1 && !q8n1 && !gemm_gen_supports(a1.dtype, d_model)) ||
+                                          (!nib2 && !q8n2 && !gemm_gen_supports(a2.dtype, d_ff))))
         return fail(RCE_QMM_BAD_SHAPE, "the grouped Q4_K / Q4_0 GEMM takes below 2^32 bytes of f16 activations per "
                                        "call (t_rows * d_model * 2 and t_rows * top_k * d_ff * 2)");
     if ((st = set_device(ctx->device))) return st;
@@ -519,9 +526,9 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
     const size_t n_pairs = t_rows * top_k;
     if (n_pairs >= (size_t)1 << 30) return fail(RCE_QMM_BAD_SHAPE, "too many (token, decision) pairs");
     // tile rows of the grouped GEMM for the average rows per expert (the
-    // generic kernel takes any tile of at most 128 rows)
-    const bool nib1 = gemm_supports(a1.dtype, d_model), nib2 = gemm_supports(a2.dtype, d_ff);
-    const int bm = nib1 || nib2 ? gemm_tile_rows((n_pairs + n_expert - 1) / n_expert, true) : 128;
+    // generic kernel takes any tile of at most 128 rows; Q8_0 / Q6_K on the
+    // nibble kernel only 128)
+    const int bm = (nib1 || nib2) && !q8n1 && !q8n2 ? gemm_tile_rows((n_pairs + n_expert - 1) / n_expert, true) : 128;
     const int max_tiles = (int)(n_pairs / bm + n_expert);
     const size_t meta_ints = (n_expert + 1) + 2 * n_pairs + 2;
     const size_t meta_bytes = align_up(meta_ints * 4, 16) + (size_t)max_tiles * sizeof(MoeTile);
@@ -562,22 +569,23 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
         if ((st = ensure(ctx, ctx->moe_h16, n_pairs * d_ff * 2, s))) return st;
         HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, bm, offs, slot_of_pair, tok_of_slot,
                                  tiles, n_tiles, status, x_dev, ctx->moe_x.p, t_rows * d_model, s));
-        auto grouped = [&](const DevWeight &w, const DevWeight *wtab, const void *a, size_t a_rows, const int *gather,
-                           int epi, void *out, const float *aux) {
-            return gemm_supports(w.dtype, w.n_cols)
+        auto grouped = [&](bool nibble, const DevWeight &w, const DevWeight *wtab, const void *a, size_t a_rows,
+                           const int *gather, int epi, void *out, const float *aux) {
+            return nibble
                        ? launch_gemm_f16_grouped(w, wtab, a, a_rows, gather, tiles, n_tiles, max_tiles, bm, epi, out, aux, s)
                        : launch_gemm_gen_grouped(w, wtab, a, a_rows, gather, tiles, n_tiles, max_tiles, epi, out, aux, s);
         };
         if (w3) {
             if ((st = ensure(ctx, ctx->moe_h, n_pairs * d_ff * sizeof(float), s))) return st;
             float *g = static_cast<float *>(ctx->moe_h.p);
-            HIP_TRY(grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, GEPI_F32, g, nullptr));
-            HIP_TRY(grouped(a1, wtab3, ctx->moe_x.p, t_rows, tok_of_slot, GEPI_SWIGLU_F16, ctx->moe_h16.p, g));
+            HIP_TRY(grouped(nib1 || q8n1, a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, GEPI_F32, g, nullptr));
+            HIP_TRY(grouped(nib1 || q8n1, a1, wtab3, ctx->moe_x.p, t_rows, tok_of_slot, GEPI_SWIGLU_F16, ctx->moe_h16.p, g));
         } else {
-            HIP_TRY(grouped(a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, GEPI_SILU_F16, ctx->moe_h16.p, nullptr));
+            HIP_TRY(grouped(nib1 || q8n1, a1, wtab1, ctx->moe_x.p, t_rows, tok_of_slot, GEPI_SILU_F16, ctx->moe_h16.p,
+                            nullptr));
         }
         // 4. W2 GEMM on the slots themselves
-        HIP_TRY(grouped(a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, GEPI_F32, y, nullptr));
+        HIP_TRY(grouped(nib2 || q8n2, a2, wtab2, ctx->moe_h16.p, n_pairs, nullptr, GEPI_F32, y, nullptr));
     } else {
         if (mode != RCE_QMM_MODE_EXACT && mode != RCE_QMM_MODE_Q8) return fail(RCE_QMM_BAD_SHAPE, "unknown mode");
         HIP_TRY(launch_moe_group(ids_dev, n_pairs, (int)top_k, (int)n_expert, bm, offs, slot_of_pair, tok_of_slot,

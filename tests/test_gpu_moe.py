@@ -166,7 +166,8 @@ def run_swiglu(ctx, gb, ub, db, dt, d_model, d_ff, x, ids, gw, mode):
 
 
 @pytest.mark.parametrize("mode,tol", [(Mode.EXACT, 1e-5), (Mode.F16_MFMA, 3e-3)])
-@pytest.mark.parametrize("E,dm,dff,t,k,dt", [(4, 512, 1024, 16, 2, O.Q4_0), (6, 256, 512, 9, 3, O.Q4_K)])
+@pytest.mark.parametrize("E,dm,dff,t,k,dt", [(4, 512, 1024, 16, 2, O.Q4_0), (6, 256, 512, 9, 3, O.Q4_K),
+                                              (4, 512, 1024, 40, 2, O.Q8_0), (3, 256, 768, 30, 2, O.Q6_K)])
 def test_moe_swiglu(ctx, mode, tol, E, dm, dff, t, k, dt):
     """rce_qmm_moe_swiglu_dev against the oracle's swiglu_expert_serial +
     combine (orc_moe_swiglu_ffn); tolerances as the two-matrix form."""
@@ -239,10 +240,13 @@ def f16_weights(b, dt, n, k):
     """The binary16 weights the F16_MFMA kernels form: the oracle's
     dequantized value rounded once (gemm_gen.hip), or for Q4_K the nibble
     kernel's f16(f16(d*sc)*q + f16(-dmin*m)) (gemm_f16.hip), for Q4_K and
-    Q5_K."""
+    Q5_K, and its f16(f16(d*sc)*q) for Q6_K."""
     if dt in (O.Q4_K, O.Q5_K):
         from test_gpu_gemm import q4k_f16_weights
         return q4k_f16_weights(b, n, k, q5=dt == O.Q5_K)
+    if dt == O.Q6_K:
+        from test_gpu_gemm import q6k_f16_weights
+        return q6k_f16_weights(b, n, k)
     from test_gpu_gemm import mfma_weights
     return mfma_weights(b, dt, n, k)
 
