@@ -108,7 +108,7 @@ struct Tile {
     // A stages (chunks), loaded NS - 1 ahead: six where the tile's LDS holds
     // them, else five
     static constexpr int pipe_lds(int ns) {
-        return ns * BM * KC * 2 + NWBUF * Fmt::w_group(BN) + 2 * Fmt::NSETS * 4 * BN * 4;
+        return ns * BM * KC * 2 + NWBUF * Fmt::w_group(BN) + 2 * (Fmt::DSC ? 0 : Fmt::NSETS * 4 * BN * 4);
     }
     static constexpr int NS = pipe_lds(6) + BM * 4 <= 160 * 1024 ? 6 : 5;
     static constexpr int RB = BM / 32, CB = BN / 64;
@@ -118,7 +118,9 @@ struct Tile {
     static constexpr int W_ROW_LOADS = BN / 16;           // loads of one 64-byte piece of every row
     static constexpr int W_LOADS = Fmt::w_loads(BN);      // per producer per group at position 0
     static constexpr int W_GROUP = Fmt::w_group(BN);
-    static constexpr int SC_BUF = Fmt::NSETS * 4 * BN * 4;  // [set][chunk][column] of f16 {scale, bias}
+    // [set][chunk][column] of f16 {scale, bias} (none where the compute
+    // waves read the scales from the weight headers)
+    static constexpr int SC_BUF = Fmt::DSC ? 0 : Fmt::NSETS * 4 * BN * 4;
     static constexpr int OFF_W = NS * A_STAGE;
     static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
     static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
@@ -301,7 +303,7 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 // set 0 / 1 = the low / high nibble sub-block of each 64-group.
 struct Q4K {
     static constexpr int NH = 2, OFF = 1024;
-    static constexpr bool IL64 = false, HB = false;
+    static constexpr bool IL64 = false, HB = false, DSC = false;
     static constexpr int NSETS = 2;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
@@ -350,10 +352,12 @@ struct Q5K : Q4K {
 
 // Q4_0: halves = the 16-byte nibble runs of blocks 8g..8g+3 and 8g+4..8g+7;
 // header = their eight f16 scales; scale set 0 / 1 = block 2q / 2q+1.
-// d * (n - 8) = d*n + (-8d) (-8d exact; the fma rounds once).
+// f16(1024 + n) - 1032 = n - 8 exactly, then (n - 8) d + 0 rounds once.
+// DSC: the {scale, bias} word of a chunk is the header's f16 d read
+// zero-extended, {d, +0}: no scale pass.
 struct Q40 {
-    static constexpr int NH = 2, OFF = 1024;
-    static constexpr bool IL64 = false, HB = false;
+    static constexpr int NH = 2, OFF = 1032;
+    static constexpr bool IL64 = false, HB = false, DSC = true;
     static constexpr int NSETS = 2;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
@@ -366,14 +370,8 @@ struct Q40 {
     __device__ static int piece_of(int q, int kq) { return 2 * (q & 1) + (kq >> 1); }
     __device__ static int acol(int kq) { return 2 * kq; }
     __device__ static int sidx(int kq) { return kq >> 1; }
-    template <int Q>
-    __device__ static uint32_t scale(const u32x4 &h, int si) {
-        const uint32_t wd = Q == 0 ? h.x : Q == 1 ? h.y : Q == 2 ? h.z : h.w;  // scales 2q, 2q+1
-        const uint16_t bits = (uint16_t)(wd >> (16 * si));
-        _Float16 d;
-        __builtin_memcpy(&d, &bits, 2);
-        return pack_h2(d, (_Float16)(-8.0f * (float)d));
-    }
+    // header byte of the f16 d of chunk q's block 2q + sidx(kq)
+    __device__ static int sbyte(int q, int kq) { return 4 * q + 2 * sidx(kq); }
 };
 
 
@@ -386,7 +384,7 @@ struct Q40 {
 // d * q rounded to binary16.
 struct Q80 {
     static constexpr int NH = 4, OFF = 1152;
-    static constexpr bool IL64 = false, HB = false;
+    static constexpr bool IL64 = false, HB = false, DSC = true;  // {d, +0} read from the header, as Q40
     static constexpr int NSETS = 2;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
@@ -398,15 +396,8 @@ struct Q80 {
     __device__ static int piece_of(int q, int kq) { return 2 * (q & 1) + (kq >> 1); }
     __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
     __device__ static int sidx(int kq) { return kq >> 1; }
+    __device__ static int sbyte(int q, int kq) { return 4 * q + 2 * sidx(kq); }
     __device__ static uint32_t vals(uint32_t x, int) { return x ^ 0x80808080u; }
-    template <int Q>
-    __device__ static uint32_t scale(const u32x4 &h, int si) {
-        const uint32_t wd = Q == 0 ? h.x : Q == 1 ? h.y : Q == 2 ? h.z : h.w;  // scales 2q, 2q+1
-        const uint16_t bits = (uint16_t)(wd >> (16 * si));
-        _Float16 d;
-        __builtin_memcpy(&d, &bits, 2);
-        return pack_h2(d, (_Float16)0.0f);
-    }
 };
 
 // Q6_K (LAYOUT_IL64_Q6_K, 64-row groups, so only the 64-column tile): a
@@ -423,7 +414,7 @@ struct Q80 {
 // (the reference's f32 d sc q rounded to binary16, but for the rounding of
 // d sc to binary16, as Q4_K's d sc).
 struct Q6K {
-    static constexpr bool IL64 = true, HB = false;
+    static constexpr bool IL64 = true, HB = false, DSC = false;
     static constexpr int NH = 0, OFF = 1024, NSETS = 4;
     static constexpr int w_group(int) { return (int)IL64_Q6K_SB; }
     static constexpr int w_loads(int) { return 6; }  // chunks 6 pw .. 6 pw + 5
@@ -584,35 +575,37 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         // scales of group g: the (column, set) pairs pt, pt + 128, ... (set =
         // pair / BN), chunks 0..3 each
         auto make_scales = [&](int g) {
+            if constexpr (!Fmt::DSC) {
 #pragma unroll
-            for (int pr = pt; pr < Fmt::NSETS * BN; pr += 128) {
-                const int p_col = pr & (BN - 1), p_si = pr / BN;
-                const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
-                const uint32_t gb = lds0 + OFF_W + (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
-                u32x4 v;
-                if constexpr (Fmt::IL64) {
-                    // the column's 16 signed scales and d: set p_si of chunk q is scale 4q + p_si
-                    u32x4 scb = lds_read16<0>(gb + 12u * 1024u + (uint32_t)(p_col * 16));
-                    uint32_t db = lds_read_u16<0>(gb + 13u * 1024u + (uint32_t)(p_col * 2));
-                    wait_lgkm0(scb, db);
-                    const float d = h2f(db);
-                    auto one = [&](uint32_t word) {
-                        const float ds = d * (float)(int8_t)(word >> (8 * p_si));  // exact: 11 x 8 bits
-                        const _Float16 sh = (_Float16)ds;
-                        return pack_h2(sh, (_Float16)(-32.0f * (float)sh));  // -32 s exact
-                    };
-                    v = u32x4{one(scb.x), one(scb.y), one(scb.z), one(scb.w)};
-                } else {
-                    u32x4 hdr = lds_read16<0>(gb + (uint32_t)(NH * W_HALF + p_col * 16));
-                    wait_lgkm0(hdr);
-                    v = u32x4{Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
-                              Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
+                for (int pr = pt; pr < Fmt::NSETS * BN; pr += 128) {
+                    const int p_col = pr & (BN - 1), p_si = pr / BN;
+                    const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
+                    const uint32_t gb = lds0 + OFF_W + (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
+                    u32x4 v;
+                    if constexpr (Fmt::IL64) {
+                        // the column's 16 signed scales and d: set p_si of chunk q is scale 4q + p_si
+                        u32x4 scb = lds_read16<0>(gb + 12u * 1024u + (uint32_t)(p_col * 16));
+                        uint32_t db = lds_read_u16<0>(gb + 13u * 1024u + (uint32_t)(p_col * 2));
+                        wait_lgkm0(scb, db);
+                        const float d = h2f(db);
+                        auto one = [&](uint32_t word) {
+                            const float ds = d * (float)(int8_t)(word >> (8 * p_si));  // exact: 11 x 8 bits
+                            const _Float16 sh = (_Float16)ds;
+                            return pack_h2(sh, (_Float16)(-32.0f * (float)sh));  // -32 s exact
+                        };
+                        v = u32x4{one(scb.x), one(scb.y), one(scb.z), one(scb.w)};
+                    } else {
+                        u32x4 hdr = lds_read16<0>(gb + (uint32_t)(NH * W_HALF + p_col * 16));
+                        wait_lgkm0(hdr);
+                        v = u32x4{Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
+                                  Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
+                    }
+                    const uint32_t wr = sc_wr + (uint32_t)((g & 1) * SC_BUF);
+                    lds_write4(wr, v.x);
+                    lds_write4(wr + 4 * BN, v.y);
+                    lds_write4(wr + 8 * BN, v.z);
+                    lds_write4(wr + 12 * BN, v.w);
                 }
-                const uint32_t wr = sc_wr + (uint32_t)((g & 1) * SC_BUF);
-                lds_write4(wr, v.x);
-                lds_write4(wr + 4 * BN, v.y);
-                lds_write4(wr + 8 * BN, v.z);
-                lds_write4(wr + 12 * BN, v.w);
             }
         };
 
@@ -686,6 +679,15 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // consecutive banks (a 32-column read is conflict-free; the
     // [column][set][chunk] order cost ~14 bank-conflict cycles per read)
     const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((Fmt::sidx(kq) * 4 * BN + ncol) * 4);
+    // DSC: the column's 16-byte header in W group buffer 0
+    const uint32_t hd_rd = lds0 + OFF_W + (uint32_t)(NH * W_HALF + ncol * 16);
+    // {scale, bias} address of chunk position q of group g
+    auto sb_addr = [&](int g, int q) -> uint32_t {
+        if constexpr (Fmt::DSC)
+            return hd_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP + Fmt::sbyte(q, kq));
+        else
+            return sc_rd + (uint32_t)((g & 1) * SC_BUF + 4 * BN * q);
+    };
 
     f32x16 acc[RB * CB];
 #pragma unroll
@@ -728,8 +730,13 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // one chunk's {scale, bias} per column block (a register each, not the
     // group's four: the 96-row tile's accumulators need the room)
     auto read_sb = [&](uint32_t *v, uint32_t addr) {
-        v[0] = lds_read4<0>(addr);
-        if constexpr (CB > 1) v[1] = lds_read4<128>(addr);  // +32 columns
+        if constexpr (Fmt::DSC) {  // f16 d zero-extended: {d, +0}
+            v[0] = lds_read_u16<0>(addr);
+            if constexpr (CB > 1) v[1] = lds_read_u16<512>(addr);  // +32 columns of 16-byte headers
+        } else {
+            v[0] = lds_read4<0>(addr);
+            if constexpr (CB > 1) v[1] = lds_read4<128>(addr);  // +32 columns
+        }
     };
     auto wait_reads = [&](half8 *a, WRaw *r, uint32_t *v) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -754,8 +761,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         read_a(a_cur, a_rd);
         read_w(raw0, w_rd[0], wh_rd[0]);
         read_w(raw_nxt, w_rd[1], wh_rd[1]);
-        read_sb(sb0, sc_rd);
-        read_sb(sb_nxt, sc_rd + 4 * BN);
+        read_sb(sb0, sb_addr(0, 0));
+        read_sb(sb_nxt, sb_addr(0, 1));
         wait_reads(a_cur, raw0, sb0);
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
@@ -779,8 +786,6 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         // nibble reads of chunk c+2 (steps 0, 1: this group; 2, 3: the next)
         const uint32_t wb_cur = (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
         const uint32_t wb_nxt = (uint32_t)(((g + 1) & (NWBUF - 1)) * W_GROUP);
-        const uint32_t sc_cur_rd = sc_rd + (uint32_t)((g & 1) * SC_BUF);
-        const uint32_t sc_nxt_rd = sc_rd + (uint32_t)(((g + 1) & 1) * SC_BUF);
         auto step = [&](auto uc) {
             constexpr int u = decltype(uc)::value;
             // chunk c+1's A and W are in LDS (the producers waited for them);
@@ -796,7 +801,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             uint32_t sb_nn[CB];
             read_a(a_nxt, sa);
             read_w(raw_nn, w_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur), wh_rd[(u + 2) & 3] + (u >= 2 ? wb_nxt : wb_cur));
-            read_sb(sb_nn, (u >= 2 ? sc_nxt_rd : sc_cur_rd) + (uint32_t)(4 * BN * ((u + 2) & 3)));
+            read_sb(sb_nn, sb_addr(u >= 2 ? g + 1 : g, (u + 2) & 3));
             __builtin_amdgcn_sched_barrier(0);
             // Chunk c's MFMAs and chunk c+1's dequantization (the next
             // group's first chunk for u = 3), independent of each other.
