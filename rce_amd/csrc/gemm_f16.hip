@@ -99,7 +99,7 @@ static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 // 32 x 32 (rows 32*rb, columns BN/2 * t + 32*cb).
 // The weight format (below) sets the bytes of one scale group of the tile's
 // columns in LDS (W_GROUP), the loads a producer issues for them at group
-// position 0 (W_LOADS; position 1 is one load: headers or scales), the
+// position 0 (W_LOADS; at position 1 h_loads: headers or scales), the
 // {scale, bias} sets per chunk (NSETS) and the A stages that leave room
 // for them (NS).
 template <int BM_, class Fmt>
@@ -140,7 +140,7 @@ struct Tile {
     // Producer loads of iteration `it`, in order: the W loads of position
     // it % 4 (row halves at position 0, headers at 1), then the A loads of
     // chunk it + NS - 1.
-    static constexpr int w_loads(int q) { return (q & 3) == 0 ? W_LOADS : (q & 3) == 1 ? 1 : 0; }
+    static constexpr int w_loads(int q) { return (q & 3) == 0 ? W_LOADS : (q & 3) == 1 ? Fmt::h_loads(BN) : 0; }
     // vmcnt immediate for a producer's barrier at chunk position q: the
     // loads it issued after chunk c+1's A loads (iterations c+3-NS .. c-1).
     static constexpr int vm_after(int q) {
@@ -250,6 +250,12 @@ template <class T>
 __device__ __forceinline__ void pin(T &r) {
     asm volatile("" : "+v"(r));
 }
+// pin the low word of a pair only (the high word never written)
+__device__ __forceinline__ void pin_lo(u32x2 &r) {
+    uint32_t x = r.x;
+    asm volatile("" : "+v"(x));
+    r.x = x;
+}
 template <class... R>
 __device__ __forceinline__ void wait_lgkm0(R &...r) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -288,52 +294,41 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 }
 
 // --- weight formats ----------------------------------------------------------
-// A scale group is four chunks.  Per row it is two 64-byte halves of
-// nibbles and a 16-byte header:
-//   half_off(w, g, hf): byte offset inside a row of half hf of group g;
-//   hdr_off(g): byte offset of group g's 16-byte header;
-//   half_of(q, kq), piece_of(q, kq): the half and 16-byte piece (0..3)
+// A scale group is four chunks.  Per row it is NH 64-byte pieces of weight
+// bytes and an HDR-byte header:
+//   half_off(w, g, hf): byte offset inside a row of piece hf of group g;
+//   hdr_off(w, g): byte offset of group g's header;
+//   half_of(q, kq), piece_of(q, kq): the piece and its 16-byte part (0..3)
 //     holding k-step kq of chunk q of the group;
 //   acol(kq): the 16-byte A column (0..7 within the chunk) of lane half 0;
 //   sidx(kq): which of a column's two scale sets k-step kq uses;
-//   scale<q>(hdr, si): f16 {scale, bias} of set si for chunk q.
+//   DSC: the compute waves read chunk q's {scale, bias} word straight from
+//     the header in LDS, at byte sbyte(q, kq), SBW bytes zero-extended (an
+//     f16 d read as {d, +0}, or a precomputed f16 pair).  Q6_K instead has
+//     its producer waves form the pairs into a scale buffer.
 
 // Q4_K: halves = qs bytes 0..15 (plane 1) and 16..31 (plane 2) of the
-// super-block's four 64-groups; header = d, dmin, 12 scale bytes; scale
-// set 0 / 1 = the low / high nibble sub-block of each 64-group.
+// super-block's four 64-groups; header = the super-block's eight f16
+// {d sc_j, -(dmin m_j)} pairs (plane 4, formed at upload from d, dmin and
+// the 12 scale bytes); scale set 0 / 1 = the low / high nibble sub-block
+// of each 64-group, so chunk q set si is pair 2q + si.
 struct Q4K {
-    static constexpr int NH = 2, OFF = 1024;
-    static constexpr bool IL64 = false, HB = false, DSC = false;
+    static constexpr int NH = 2, OFF = 1024, HDR = 32, SBW = 4;
+    static constexpr bool IL64 = false, HB = false, DSC = true;
     static constexpr int NSETS = 2;
-    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
+    static constexpr int h_loads(int bn) { return bn / 64; }  // 32 rows x 32 bytes per load
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return (hf ? w.plane2 : w.plane1) + 64 * (size_t)g;
     }
-    __device__ static size_t hdr_off(int g) { return 16 * (size_t)g; }
+    __device__ static size_t hdr_off(const DevWeight &w, int g) { return w.plane4 + 32 * (size_t)g; }
     __device__ static int half_of(int, int kq) { return kq >> 1; }
     __device__ static int piece_of(int q, int) { return q; }
     __device__ static int acol(int kq) { return (kq & 1) * 4 + (kq >> 1) * 2; }
     __device__ static int sidx(int kq) { return kq & 1; }
-    // q4_k_get_scale_min (rce-op-qmm/src/lib.rs L719-728) of sub-block
-    // j = 2q + si (q a constant, si = 0 or 1): the 12 scale bytes are header
-    // bytes 4..15 = words y, z, w
-    template <int Q>
-    __device__ static uint32_t scale(const u32x4 &h, int si) {
-        const int sh = 8 * (2 * (Q & 1) + si);  // byte (j & 3) of a word
-        uint32_t sc, m;
-        if constexpr (Q < 2) {  // j < 4
-            sc = (h.y >> sh) & 63;
-            m = (h.z >> sh) & 63;
-        } else {
-            const uint32_t hw = h.w >> sh;
-            sc = (hw & 0x0F) | (((h.y >> sh) >> 6 & 3) << 4);
-            m = (hw >> 4 & 0x0F) | (((h.z >> sh) >> 6 & 3) << 4);
-        }
-        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
-        return pack_h2((_Float16)(d * (float)sc), (_Float16)(-(dmin * (float)m)));
-    }
+    __device__ static int sbyte(int q, int kq) { return 4 * (2 * q + sidx(kq)); }
 };
 
 // Q5_K (LAYOUT_SPLIT_Q5_K): Q4_K's halves, header and scales, plus per row
@@ -345,7 +340,7 @@ struct Q4K {
 // u = nibble | bit << 4 in 0..31, value d1 u - min1 as for Q4_K.
 struct Q5K : Q4K {
     static constexpr bool HB = true;
-    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16 + bn * 32; }
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR + bn * 32; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2 + bn / 64; }
     __device__ static int hb_byte(int kq) { return 4 * (kq & 1) + 2 * (kq >> 1); }
 };
@@ -356,16 +351,17 @@ struct Q5K : Q4K {
 // DSC: the {scale, bias} word of a chunk is the header's f16 d read
 // zero-extended, {d, +0}: no scale pass.
 struct Q40 {
-    static constexpr int NH = 2, OFF = 1032;
+    static constexpr int NH = 2, OFF = 1032, HDR = 16, SBW = 2;
     static constexpr bool IL64 = false, HB = false, DSC = true;
     static constexpr int NSETS = 2;
-    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
+    static constexpr int h_loads(int) { return 1; }  // BN / 2 lanes of 16 bytes
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return w.plane1 + 128 * (size_t)g + 64 * hf;
     }
-    __device__ static size_t hdr_off(int g) { return 16 * (size_t)g; }
+    __device__ static size_t hdr_off(const DevWeight &, int g) { return 16 * (size_t)g; }
     __device__ static int half_of(int q, int) { return q >> 1; }
     __device__ static int piece_of(int q, int kq) { return 2 * (q & 1) + (kq >> 1); }
     __device__ static int acol(int kq) { return 2 * kq; }
@@ -383,15 +379,16 @@ struct Q40 {
 // - 1152 = q exactly, and d * q + 0 rounds once: the reference's f32 value
 // d * q rounded to binary16.
 struct Q80 {
-    static constexpr int NH = 4, OFF = 1152;
+    static constexpr int NH = 4, OFF = 1152, HDR = 16, SBW = 2;
     static constexpr bool IL64 = false, HB = false, DSC = true;  // {d, +0} read from the header, as Q40
     static constexpr int NSETS = 2;
-    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * 16; }
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
+    static constexpr int h_loads(int) { return 1; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return ((hf >> 1) ? w.plane2 : w.plane1) + 128 * (size_t)g + 64 * (hf & 1);
     }
-    __device__ static size_t hdr_off(int g) { return 16 * (size_t)g; }
+    __device__ static size_t hdr_off(const DevWeight &, int g) { return 16 * (size_t)g; }
     __device__ static int half_of(int q, int kq) { return 2 * (kq & 1) + (q >> 1); }
     __device__ static int piece_of(int q, int kq) { return 2 * (q & 1) + (kq >> 1); }
     __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
@@ -415,9 +412,10 @@ struct Q80 {
 // d sc to binary16, as Q4_K's d sc).
 struct Q6K {
     static constexpr bool IL64 = true, HB = false, DSC = false;
-    static constexpr int NH = 0, OFF = 1024, NSETS = 4;
+    static constexpr int NH = 0, OFF = 1024, NSETS = 4, HDR = 0, SBW = 4;
     static constexpr int w_group(int) { return (int)IL64_Q6K_SB; }
     static constexpr int w_loads(int) { return 6; }  // chunks 6 pw .. 6 pw + 5
+    static constexpr int h_loads(int) { return 1; }  // the scales chunk, or the d values
     __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
     __device__ static int sidx(int kq) { return kq; }
     __device__ static int ql_chunk(int q, int kq) { return 4 * (q >> 1) + 2 * (kq >> 1) + (kq & 1); }
@@ -512,9 +510,18 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             const size_t hbrow = (size_t)hr < wtile ? (size_t)hr : wtile - 1;
             hb_lane[i] = (uint32_t)(hbrow * w.row_stride) + 16u * (uint32_t)(lane & 1);
         }
-        size_t hrow = (size_t)(BN / 2 * pw + (lane & (BN / 2 - 1)));
-        hrow = hrow < wtile ? hrow : wtile - 1;
-        const uint32_t h_lane = (uint32_t)(hrow * w.row_stride);
+        // headers of rows BN/2 pw ..: 16-byte headers one lane per row
+        // (lanes 0..BN/2-1); 32-byte ones two lanes per row, instruction i
+        // covering rows BN/2 pw + 32 i .. +31
+        constexpr int H_LOADS = Fmt::IL64 ? 1 : Fmt::h_loads(BN);
+        uint32_t h_lane[H_LOADS];
+#pragma unroll
+        for (int i = 0; i < H_LOADS; i++) {
+            size_t hrow = Fmt::HDR == 16 ? (size_t)(BN / 2 * pw + (lane & (BN / 2 - 1)))
+                                         : (size_t)(BN / 2 * pw + 32 * i + (lane >> 1));
+            hrow = hrow < wtile ? hrow : wtile - 1;
+            h_lane[i] = (uint32_t)(hrow * w.row_stride) + (Fmt::HDR == 16 ? 0u : 16u * (uint32_t)(lane & 1));
+        }
         // IL64 (Q6_K): the tile's 64 columns are one 64-row group, and every
         // load is one 1 KB chunk of it (lane l: bytes 16 l ..)
         const __amdgpu_buffer_rsrc_t wbuf =
@@ -523,9 +530,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         const uint32_t a_soff_max = (uint32_t)(nchunks - 1) * (KC * 2);
         // W position q of group gs into the group buffer dst: at 0 the
         // weight bytes (split formats: the 64-byte pieces pw, pw + 2, ... of
-        // every row; IL64: chunks 6 pw .. 6 pw + 5), at 1 one load (the
-        // 16-byte headers of rows BN/2 pw ..; IL64: the scales chunk, or the
-        // d values).
+        // every row; IL64: chunks 6 pw .. 6 pw + 5), at 1 the headers of
+        // rows BN/2 pw .. (IL64: the scales chunk, or the d values).
         auto load_w = [&](int q, int gs, unsigned char *dst) {
             if constexpr (Fmt::IL64) {
                 const uint32_t sb = (uint32_t)gs * (uint32_t)IL64_Q6K_SB, lo = 16u * (uint32_t)lane;
@@ -550,10 +556,16 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
                     for (int i = 0; i < HB_LOADS; i++)
                         buf_load_lds16(wbuf, hb_lane[i], (uint32_t)(w.plane3 + 32 * (size_t)gs),
-                                       dst + NH * W_HALF + BN * 16 + (HB_LOADS * pw + i) * 1024);
+                                       dst + NH * W_HALF + BN * Fmt::HDR + (HB_LOADS * pw + i) * 1024);
                 }
-            } else if (lane < BN / 2) {
-                buf_load_lds16(wbuf, h_lane, (uint32_t)Fmt::hdr_off(gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
+            } else if constexpr (Fmt::HDR == 16) {
+                if (lane < BN / 2)
+                    buf_load_lds16(wbuf, h_lane[0], (uint32_t)Fmt::hdr_off(w, gs), dst + NH * W_HALF + pw * (BN / 2) * 16);
+            } else {
+#pragma unroll
+                for (int i = 0; i < H_LOADS; i++)
+                    buf_load_lds16(wbuf, h_lane[i], (uint32_t)Fmt::hdr_off(w, gs),
+                                   dst + NH * W_HALF + (BN / 2 * pw + 32 * i) * Fmt::HDR);
             }
         };
         // Loads of (virtual) iteration it: W position it % 4 of group
@@ -572,8 +584,10 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
             for (int i = 0; i < T::A_LOADS; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
         };
-        // scales of group g: the (column, set) pairs pt, pt + 128, ... (set =
-        // pair / BN), chunks 0..3 each
+        // Q6_K's scales of group g: the (column, set) pairs pt, pt + 128,
+        // ... (set = pair / BN), chunks 0..3 each (the other formats' come
+        // from their headers)
+        static_assert(Fmt::DSC || Fmt::IL64, "a scale pass for the IL64 layout only");
         auto make_scales = [&](int g) {
             if constexpr (!Fmt::DSC) {
 #pragma unroll
@@ -581,25 +595,17 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                     const int p_col = pr & (BN - 1), p_si = pr / BN;
                     const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
                     const uint32_t gb = lds0 + OFF_W + (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
-                    u32x4 v;
-                    if constexpr (Fmt::IL64) {
-                        // the column's 16 signed scales and d: set p_si of chunk q is scale 4q + p_si
-                        u32x4 scb = lds_read16<0>(gb + 12u * 1024u + (uint32_t)(p_col * 16));
-                        uint32_t db = lds_read_u16<0>(gb + 13u * 1024u + (uint32_t)(p_col * 2));
-                        wait_lgkm0(scb, db);
-                        const float d = h2f(db);
-                        auto one = [&](uint32_t word) {
-                            const float ds = d * (float)(int8_t)(word >> (8 * p_si));  // exact: 11 x 8 bits
-                            const _Float16 sh = (_Float16)ds;
-                            return pack_h2(sh, (_Float16)(-32.0f * (float)sh));  // -32 s exact
-                        };
-                        v = u32x4{one(scb.x), one(scb.y), one(scb.z), one(scb.w)};
-                    } else {
-                        u32x4 hdr = lds_read16<0>(gb + (uint32_t)(NH * W_HALF + p_col * 16));
-                        wait_lgkm0(hdr);
-                        v = u32x4{Fmt::template scale<0>(hdr, p_si), Fmt::template scale<1>(hdr, p_si),
-                                  Fmt::template scale<2>(hdr, p_si), Fmt::template scale<3>(hdr, p_si)};
-                    }
+                    // the column's 16 signed scales and d: set p_si of chunk q is scale 4q + p_si
+                    u32x4 scb = lds_read16<0>(gb + 12u * 1024u + (uint32_t)(p_col * 16));
+                    uint32_t db = lds_read_u16<0>(gb + 13u * 1024u + (uint32_t)(p_col * 2));
+                    wait_lgkm0(scb, db);
+                    const float d = h2f(db);
+                    auto one = [&](uint32_t word) {
+                        const float ds = d * (float)(int8_t)(word >> (8 * p_si));  // exact: 11 x 8 bits
+                        const _Float16 sh = (_Float16)ds;
+                        return pack_h2(sh, (_Float16)(-32.0f * (float)sh));  // -32 s exact
+                    };
+                    const u32x4 v = u32x4{one(scb.x), one(scb.y), one(scb.z), one(scb.w)};
                     const uint32_t wr = sc_wr + (uint32_t)((g & 1) * SC_BUF);
                     lds_write4(wr, v.x);
                     lds_write4(wr + 4 * BN, v.y);
@@ -670,7 +676,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
                                                 16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
             if constexpr (Fmt::HB)  // the fifth-bit byte of the lane's eight weights
-                wh_rd[q] = lds0 + OFF_W + (uint32_t)(NH * W_HALF + BN * 16 + ncol * 32 + 8 * q + Fmt::hb_byte(kq) + h);
+                wh_rd[q] = lds0 + OFF_W + (uint32_t)(NH * W_HALF + BN * Fmt::HDR + ncol * 32 + 8 * q + Fmt::hb_byte(kq) + h);
             else
                 wh_rd[q] = w_rd[q];
         }
@@ -679,8 +685,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // consecutive banks (a 32-column read is conflict-free; the
     // [column][set][chunk] order cost ~14 bank-conflict cycles per read)
     const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((Fmt::sidx(kq) * 4 * BN + ncol) * 4);
-    // DSC: the column's 16-byte header in W group buffer 0
-    const uint32_t hd_rd = lds0 + OFF_W + (uint32_t)(NH * W_HALF + ncol * 16);
+    // DSC: the column's header in W group buffer 0
+    const uint32_t hd_rd = lds0 + OFF_W + (uint32_t)(NH * W_HALF + ncol * Fmt::HDR);
     // {scale, bias} address of chunk position q of group g
     auto sb_addr = [&](int g, int q) -> uint32_t {
         if constexpr (Fmt::DSC)
@@ -730,9 +736,12 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // one chunk's {scale, bias} per column block (a register each, not the
     // group's four: the 96-row tile's accumulators need the room)
     auto read_sb = [&](uint32_t *v, uint32_t addr) {
-        if constexpr (Fmt::DSC) {  // f16 d zero-extended: {d, +0}
+        if constexpr (Fmt::DSC && Fmt::SBW == 2) {  // f16 d zero-extended: {d, +0}
             v[0] = lds_read_u16<0>(addr);
-            if constexpr (CB > 1) v[1] = lds_read_u16<512>(addr);  // +32 columns of 16-byte headers
+            if constexpr (CB > 1) v[1] = lds_read_u16<32 * Fmt::HDR>(addr);  // +32 columns of headers
+        } else if constexpr (Fmt::DSC) {  // a precomputed pair
+            v[0] = lds_read4<0>(addr);
+            if constexpr (CB > 1) v[1] = lds_read4<32 * Fmt::HDR>(addr);
         } else {
             v[0] = lds_read4<0>(addr);
             if constexpr (CB > 1) v[1] = lds_read4<128>(addr);  // +32 columns
@@ -745,7 +754,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             pin(r[i].l);
-            if constexpr (Fmt::IL64 || Fmt::HB) pin(r[i].h);
+            if constexpr (Fmt::IL64) pin(r[i].h);
+            if constexpr (Fmt::HB) pin_lo(r[i].h);  // one byte: only the low word is live
             pin(v[i]);
         }
     };
@@ -767,7 +777,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
             pin(raw_nxt[cb].l);
-            if constexpr (Fmt::IL64 || Fmt::HB) pin(raw_nxt[cb].h);
+            if constexpr (Fmt::IL64) pin(raw_nxt[cb].h);
+            if constexpr (Fmt::HB) pin_lo(raw_nxt[cb].h);
             pin(sb_nxt[cb]);
         }
 #pragma unroll

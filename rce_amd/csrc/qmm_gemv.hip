@@ -235,18 +235,20 @@ size_t plan_layout(DevWeight &dw) {
         dw.plane2 = dw.plane1 + 16 * (k / 32);
         dw.row_stride = dw.plane2 + 16 * (k / 32);
         return dw.row_stride * n;
-    case T_Q4_K:
+    case T_Q4_K:  // the file's 144 B per super-block, then 32 B of scale pairs
         dw.layout = LAYOUT_SPLIT_Q4_K;
         dw.plane1 = 16 * (k / 256);
         dw.plane2 = dw.plane1 + 16 * (k / 64);
-        dw.row_stride = 144 * (k / 256);
+        dw.plane4 = 144 * (k / 256);
+        dw.row_stride = 176 * (k / 256);
         return dw.row_stride * n;
-    case T_Q5_K:  // 16 + 4 * (16 + 16 + 8) = 176 B per super-block, as in the file
+    case T_Q5_K:  // 16 + 4 * (16 + 16 + 8) = 176 B per super-block, as in the file, then 32 B of scale pairs
         dw.layout = LAYOUT_SPLIT_Q5_K;
         dw.plane1 = 16 * (k / 256);
         dw.plane2 = dw.plane1 + 16 * (k / 64);
         dw.plane3 = dw.plane2 + 16 * (k / 64);
-        dw.row_stride = 176 * (k / 256);
+        dw.plane4 = 176 * (k / 256);
+        dw.row_stride = 208 * (k / 256);
         return dw.row_stride * n;
     case T_Q5_0:
         dw.layout = LAYOUT_SPLIT_Q5_0;
@@ -311,6 +313,33 @@ size_t layout_pad_bytes(const DevWeight &dw) {
     if (dw.layout == LAYOUT_IL64_Q6_K || dw.layout == LAYOUT_IL64_ROWS || dw.layout == LAYOUT_I2S_PLANES)
         return ((rows + 63) / 64 + 1) * dw.group_stride;
     return rows * dw.row_stride;
+}
+
+// The matrix-core GEMM's scale pairs of one Q4_K / Q5_K super-block (its
+// 12 scale bytes and f16 d, dmin): for sub-block j, get_scale_min's (sc, m)
+// (rce-op-qmm/src/lib.rs L719-728), then binary16 {d * sc, -(dmin * m)},
+// each product exact in f32 (11 x 6 bits) and rounded once.
+static void kquant_scale_pairs(const uint8_t *hdr, uint8_t *out) {
+    auto f16_to_f32 = [](const uint8_t *b) {
+        _Float16 h;
+        std::memcpy(&h, b, 2);
+        return (float)h;
+    };
+    const float d = f16_to_f32(hdr), dmin = f16_to_f32(hdr + 2);
+    const uint8_t *q = hdr + 4;
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        if (j < 4) {
+            sc = q[j] & 63;
+            m = q[j + 4] & 63;
+        } else {
+            sc = (q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4);
+            m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+        }
+        const _Float16 s = (_Float16)(d * (float)sc), b = (_Float16)(-(dmin * (float)m));
+        std::memcpy(out + 4 * j, &s, 2);
+        std::memcpy(out + 4 * j + 2, &b, 2);
+    }
 }
 
 void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
@@ -398,6 +427,7 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
             for (size_t sb = 0; sb < nsb; sb++) {
                 const uint8_t *blk = s + sb * 144;
                 for (int i = 0; i < 16; i++) d[16 * sb + i] = blk[i];
+                kquant_scale_pairs(blk, d + dw.plane4 + 32 * sb);
                 for (int g = 0; g < 4; g++) {
                     const size_t u = 4 * sb + g;
                     for (int l = 0; l < 16; l++) d[dw.plane1 + 16 * u + l] = blk[16 + 32 * g + l];
@@ -415,6 +445,7 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
             for (size_t sb = 0; sb < nsb; sb++) {
                 const uint8_t *blk = s + sb * 176, *qh = blk + 16, *qs = blk + 48;
                 for (int i = 0; i < 16; i++) d[16 * sb + i] = blk[i];
+                kquant_scale_pairs(blk, d + dw.plane4 + 32 * sb);
                 for (int g = 0; g < 4; g++) {
                     const size_t u = 4 * sb + g;
                     for (int l = 0; l < 16; l++) d[dw.plane1 + 16 * u + l] = qs[32 * g + l];

@@ -31,7 +31,10 @@ enum Layout : int {
     LAYOUT_SPLIT_Q8_0 = 2,
     // Row r: [16 B header (d, dmin, 12 scale bytes) per super-block]
     // [qs bytes l = 0..15 of 64-group u at plane1 + 16 u]
-    // [qs bytes l = 16..31 of group u at plane2 + 16 u].
+    // [qs bytes l = 16..31 of group u at plane2 + 16 u]
+    // [at plane4 + 32 sb the super-block's eight binary16 pairs
+    //  {f16(d sc_j), f16(-(dmin m_j))}, j = 0..7: the matrix-core GEMM's
+    //  scales, formed once here instead of in every GEMM tile].
     LAYOUT_SPLIT_Q4_K = 3,
     // Rows in groups of 64; per group and super-block sb (IL64_Q6K_SB
     // bytes at sb * IL64_Q6K_SB) the 13 16-byte chunks of the super-block's
@@ -41,7 +44,8 @@ enum Layout : int {
     // Q5_K: LAYOUT_SPLIT_Q4_K's header and two qs planes, plus at plane3 +
     // 8 u one 8-byte word per 64-group u: bit l (l < 32) = the 5th bit of
     // position l, bit 32 + l = that of position 32 + l (the two qh bits of
-    // the group, 2g and 2g + 1, of qh byte l).
+    // the group, 2g and 2g + 1, of qh byte l); then Q4_K's scale pairs at
+    // plane4.
     LAYOUT_SPLIT_Q5_K = 5,
     // Q5_0: LAYOUT_SPLIT_Q4_0's scales and nibble plane, plus the blocks'
     // 4-byte qh words at plane2 + 4 b; rows padded to 16 B.
@@ -85,6 +89,7 @@ struct DevWeight {
     size_t plane1;        // SPLIT: offset of the first 16-B plane in a row
     size_t plane2;        // SPLIT_Q8_0 / SPLIT_Q4_K / SPLIT_Q5_K / SPLIT_Q5_0: offset of the second plane
     size_t plane3;        // SPLIT_Q5_K: offset of the high-bit words; SPLIT_Q3_K: of the scales
+    size_t plane4;        // SPLIT_Q4_K / SPLIT_Q5_K: offset of the f16 scale pairs
     size_t group_stride;  // IL64: bytes between 64-row groups
     const uint8_t *aux;   // I2_S: device address of the tensor's f32 scale
 };
