@@ -99,17 +99,14 @@ static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 // 32 x 32 (rows 32*rb, columns BN/2 * t + 32*cb).
 // The weight format (below) sets the bytes of one scale group of the tile's
 // columns in LDS (W_GROUP), the loads a producer issues for them at group
-// position 0 (W_LOADS; at position 1 h_loads: headers or scales), the
-// {scale, bias} sets per chunk (NSETS) and the A stages that leave room
-// for them (NS).
+// position 0 (W_LOADS; at position 1 h_loads: the headers or scale pairs)
+// and so the A stages that leave room for them (NS).
 template <int BM_, class Fmt>
 struct Tile {
     static constexpr int BM = BM_, BN = BM_ == 96 ? 128 : 8192 / BM_;
     // A stages (chunks), loaded NS - 1 ahead: six where the tile's LDS holds
     // them, else five
-    static constexpr int pipe_lds(int ns) {
-        return ns * BM * KC * 2 + NWBUF * Fmt::w_group(BN) + 2 * (Fmt::DSC ? 0 : Fmt::NSETS * 4 * BN * 4);
-    }
+    static constexpr int pipe_lds(int ns) { return ns * BM * KC * 2 + NWBUF * Fmt::w_group(BN); }
     static constexpr int NS = pipe_lds(6) + BM * 4 <= 160 * 1024 ? 6 : 5;
     static constexpr int RB = BM / 32, CB = BN / 64;
     static constexpr int A_STAGE = BM * KC * 2;           // 16 KB / 8 KB
@@ -118,20 +115,17 @@ struct Tile {
     static constexpr int W_ROW_LOADS = BN / 16;           // loads of one 64-byte piece of every row
     static constexpr int W_LOADS = Fmt::w_loads(BN);      // per producer per group at position 0
     static constexpr int W_GROUP = Fmt::w_group(BN);
-    // [set][chunk][column] of f16 {scale, bias} (none where the compute
-    // waves read the scales from the weight headers)
-    static constexpr int SC_BUF = Fmt::DSC ? 0 : Fmt::NSETS * 4 * BN * 4;
     static constexpr int OFF_W = NS * A_STAGE;
-    static constexpr int OFF_SC = OFF_W + NWBUF * W_GROUP;
-    static constexpr int PIPE_LDS = OFF_SC + 2 * SC_BUF;
+    static constexpr int PIPE_LDS = OFF_W + NWBUF * W_GROUP;
     static_assert(PIPE_LDS == pipe_lds(NS), "LDS layout");
     // the partial sums of every wave for one column block cb at a time
     static constexpr int RED_LDS = 8 * RB * 16 * 64 * 4;
     static constexpr int LDS = PIPE_LDS > RED_LDS ? PIPE_LDS : RED_LDS;
     static_assert(LDS + BM * 4 <= 160 * 1024, "LDS budget");
-    // W group g must be complete at the barrier of chunk 4g-3 (its headers
-    // are read there for the scales): its last load (iteration 4(g-GA)+1)
-    // precedes the loads of A chunk 4g-2 (iteration 4g-2-(NS-1)).
+    // W group g must be complete at the barrier of chunk 4g-3 (the compute
+    // waves read its bytes and scale words from chunk 4g-2 on): its last
+    // load (iteration 4(g-GA)+1) precedes the loads of A chunk 4g-2
+    // (iteration 4g-2-(NS-1)).
     static_assert(4 * GA >= NS + 2, "W groups loaded too late for the stage depth");
     static_assert(NS >= 3, "stage ring");
     static_assert(RB >= 2 && RB <= 4 && CB >= 1 && CB <= 2 && 2 * RB <= 8,
@@ -150,24 +144,10 @@ struct Tile {
     }
 };
 
-__device__ __forceinline__ float h2f(uint32_t bits) {
-    _Float16 h;
-    uint16_t b = (uint16_t)bits;
-    __builtin_memcpy(&h, &b, 2);
-    return (float)h;
-}
-
 __device__ __forceinline__ half2v as_h2(uint32_t u) {
     half2v h;
     __builtin_memcpy(&h, &u, 4);
     return h;
-}
-
-__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
-    const half2v h = {lo, hi};
-    uint32_t u;
-    __builtin_memcpy(&u, &h, 4);
-    return u;
 }
 
 // One 16-byte load from global memory straight into LDS at
@@ -192,7 +172,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *base, 
 // compiler counts the global->LDS loads as writes to all of LDS and would
 // wait for every load in flight before each LDS access (the whole
 // pipeline).  Their completion is waited for explicitly instead
-// (wait_lgkm0 below).  OFF is the instruction's immediate byte offset.
+// (s_waitcnt lgkmcnt(0), then pin below).  OFF is the instruction's
+// immediate byte offset.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
@@ -200,13 +181,6 @@ template <int OFF>
 __device__ __forceinline__ half8 lds_read_frag(uint32_t a) {
     static_assert(OFF >= 0 && OFF < 65536, "ds offset");
     half8 v;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
-    return v;
-}
-template <int OFF>
-__device__ __forceinline__ u32x4 lds_read16(uint32_t a) {
-    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
-    u32x4 v;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
 }
@@ -238,14 +212,8 @@ __device__ __forceinline__ u32x2 lds_read8(uint32_t a) {
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
 }
-__device__ __forceinline__ void lds_write4(uint32_t a, uint32_t v) {
-    asm volatile("ds_write_b32 %0, %1" : : "v"(a), "v"(v) : "memory");
-}
-__device__ __forceinline__ void lds_write16(uint32_t a, u32x4 v) {
-    asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
-}
-// s_waitcnt lgkmcnt(0), then an empty asm that "redefines" each register
-// the reads above filled, so no use of them can move ahead of the wait.
+// After s_waitcnt lgkmcnt(0): an empty asm that "redefines" a register
+// the reads above filled, so no use of it can move ahead of the wait.
 template <class T>
 __device__ __forceinline__ void pin(T &r) {
     asm volatile("" : "+v"(r));
@@ -255,11 +223,6 @@ __device__ __forceinline__ void pin_lo(u32x2 &r) {
     uint32_t x = r.x;
     asm volatile("" : "+v"(x));
     r.x = x;
-}
-template <class... R>
-__device__ __forceinline__ void wait_lgkm0(R &...r) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    (pin(r), ...);
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt not waited for),
@@ -302,10 +265,11 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 //     holding k-step kq of chunk q of the group;
 //   acol(kq): the 16-byte A column (0..7 within the chunk) of lane half 0;
 //   sidx(kq): which of a column's two scale sets k-step kq uses;
-//   DSC: the compute waves read chunk q's {scale, bias} word straight from
-//     the header in LDS, at byte sbyte(q, kq), SBW bytes zero-extended (an
-//     f16 d read as {d, +0}, or a precomputed f16 pair).  Q6_K instead has
-//     its producer waves form the pairs into a scale buffer.
+//   the compute waves read chunk q's {scale, bias} word straight from the
+//     group's header in LDS (at hoff(BN) + column * CST + sbyte(q, kq)),
+//     SBW bytes zero-extended: an f16 d read as {d, +0}, or a pair the
+//     upload formed (the device layouts of Q4_K, Q5_K, Q6_K), so no wave
+//     spends a step forming scales.
 
 // Q4_K: halves = qs bytes 0..15 (plane 1) and 16..31 (plane 2) of the
 // super-block's four 64-groups; header = the super-block's eight f16
@@ -313,12 +277,12 @@ __device__ __forceinline__ half8 join8(half2v a, half2v b, half2v c, half2v d) {
 // the 12 scale bytes); scale set 0 / 1 = the low / high nibble sub-block
 // of each 64-group, so chunk q set si is pair 2q + si.
 struct Q4K {
-    static constexpr int NH = 2, OFF = 1024, HDR = 32, SBW = 4;
-    static constexpr bool IL64 = false, HB = false, DSC = true;
-    static constexpr int NSETS = 2;
+    static constexpr int NH = 2, OFF = 1024, HDR = 32, SBW = 4, CST = HDR;
+    static constexpr bool IL64 = false, HB = false;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     static constexpr int h_loads(int bn) { return bn / 64; }  // 32 rows x 32 bytes per load
+    static constexpr int hoff(int bn) { return NH * bn * 64; }
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return (hf ? w.plane2 : w.plane1) + 64 * (size_t)g;
@@ -347,16 +311,16 @@ struct Q5K : Q4K {
 
 // Q4_0: halves = the 16-byte nibble runs of blocks 8g..8g+3 and 8g+4..8g+7;
 // header = their eight f16 scales; scale set 0 / 1 = block 2q / 2q+1.
-// f16(1024 + n) - 1032 = n - 8 exactly, then (n - 8) d + 0 rounds once.
-// DSC: the {scale, bias} word of a chunk is the header's f16 d read
-// zero-extended, {d, +0}: no scale pass.
+// f16(1024 + n) - 1032 = n - 8 exactly, then (n - 8) d + 0 rounds once
+// (the chunk's {scale, bias} word is the header's f16 d read
+// zero-extended, {d, +0}).
 struct Q40 {
-    static constexpr int NH = 2, OFF = 1032, HDR = 16, SBW = 2;
-    static constexpr bool IL64 = false, HB = false, DSC = true;
-    static constexpr int NSETS = 2;
+    static constexpr int NH = 2, OFF = 1032, HDR = 16, SBW = 2, CST = HDR;
+    static constexpr bool IL64 = false, HB = false;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     static constexpr int h_loads(int) { return 1; }  // BN / 2 lanes of 16 bytes
+    static constexpr int hoff(int bn) { return NH * bn * 64; }
     __device__ static uint32_t vals(uint32_t x, int nsh) { return (x >> nsh) & 0x0F0F0F0Fu; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return w.plane1 + 128 * (size_t)g + 64 * hf;
@@ -379,12 +343,12 @@ struct Q40 {
 // - 1152 = q exactly, and d * q + 0 rounds once: the reference's f32 value
 // d * q rounded to binary16.
 struct Q80 {
-    static constexpr int NH = 4, OFF = 1152, HDR = 16, SBW = 2;
-    static constexpr bool IL64 = false, HB = false, DSC = true;  // {d, +0} read from the header, as Q40
-    static constexpr int NSETS = 2;
+    static constexpr int NH = 4, OFF = 1152, HDR = 16, SBW = 2, CST = HDR;  // {d, +0} read from the header, as Q40
+    static constexpr bool IL64 = false, HB = false;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2; }
     static constexpr int h_loads(int) { return 1; }
+    static constexpr int hoff(int bn) { return NH * bn * 64; }
     __device__ static size_t half_off(const DevWeight &w, int g, int hf) {
         return ((hf >> 1) ? w.plane2 : w.plane1) + 128 * (size_t)g + 64 * (hf & 1);
     }
@@ -398,9 +362,12 @@ struct Q80 {
 };
 
 // Q6_K (LAYOUT_IL64_Q6_K, 64-row groups, so only the 64-column tile): a
-// scale group is one super-block, whose 13 16-byte chunks (ql 0..7, qh
-// 8..11, scales 12) of the tile's 64 rows lie as 13 contiguous KB, then the
-// rows' d values (rce-op-qmm/src/lib.rs L425-454, dequant.rs L658-701).
+// scale group is one super-block, whose 16-byte ql (0..7) and qh (8..11)
+// chunks of the tile's 64 rows lie as 12 contiguous KB, then (after the
+// scales chunk and the d values, which the GEMM does not read) the rows'
+// 16 f16 {s, -32 s} pairs as [pair][row], 4 KB (rce-op-qmm/src/lib.rs
+// L425-454, dequant.rs L658-701); the group buffer holds the 12 KB and the
+// pairs.
 // Chunk q of the super-block is positions 64q .. 64q+63: 128-half n = q/2,
 // quarters 2(q&1) and 2(q&1)+1; k-step kq takes quarter 2(q&1) + kq/2,
 // positions l = 16(kq&1) .. +15 of it, lane half h l + 8h .. +7: ql bytes
@@ -411,13 +378,15 @@ struct Q80 {
 // (the reference's f32 d sc q rounded to binary16, but for the rounding of
 // d sc to binary16, as Q4_K's d sc).
 struct Q6K {
-    static constexpr bool IL64 = true, HB = false, DSC = false;
-    static constexpr int NH = 0, OFF = 1024, NSETS = 4, HDR = 0, SBW = 4;
-    static constexpr int w_group(int) { return (int)IL64_Q6K_SB; }
+    static constexpr bool IL64 = true, HB = false;
+    static constexpr int NH = 0, OFF = 1024, HDR = 0, SBW = 4, CST = 4;
+    static constexpr int w_group(int) { return 16 * 1024; }
     static constexpr int w_loads(int) { return 6; }  // chunks 6 pw .. 6 pw + 5
-    static constexpr int h_loads(int) { return 1; }  // the scales chunk, or the d values
+    static constexpr int h_loads(int) { return 2; }  // pair KB 2 pw, 2 pw + 1
+    static constexpr int hoff(int) { return 12 * 1024; }
     __device__ static int acol(int kq) { return (kq >> 1) * 4 + (kq & 1) * 2; }
     __device__ static int sidx(int kq) { return kq; }
+    __device__ static int sbyte(int q, int kq) { return (4 * q + kq) * 256; }  // pair 4q + kq
     __device__ static int ql_chunk(int q, int kq) { return 4 * (q >> 1) + 2 * (kq >> 1) + (kq & 1); }
     __device__ static int qh_chunk(int q, int kq) { return 8 + 2 * (q >> 1) + (kq & 1); }
 };
@@ -438,8 +407,8 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                                                  const DevWeight *__restrict__ wtab) {
     using T = Tile<BM_, Fmt>;
     constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB, NS = T::NS, NH = Fmt::NH;
-    constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP, SC_BUF = T::SC_BUF;
-    constexpr int OFF_W = T::OFF_W, OFF_SC = T::OFF_SC;
+    constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP;
+    constexpr int OFF_W = T::OFF_W;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int arow[BM];
     int mt, nt;
@@ -475,7 +444,6 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         // the ranges); issuing them may stall on the memory pipeline, which
         // holds up only these two waves.
         const int pw = wave - NC / 64;  // 0, 1
-        const int pt = tid - NC;        // 0 .. 127
         //   A: rows BM/2*pw .. +BM/2-1; instruction i covers rows
         //      BM/2*pw + 8i .. +7, 8 lanes per row; lane slot p holds
         //      column p ^ f(row)
@@ -539,10 +507,11 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
                     for (int j = 0; j < 6; j++)
                         buf_load_lds16(wbuf, lo, sb + (uint32_t)(6 * pw + j) * 1024u, dst + (6 * pw + j) * 1024);
-                } else if (pw == 0) {
-                    buf_load_lds16(wbuf, lo, sb + 12u * 1024u, dst + 12 * 1024);
-                } else if (lane < 8) {
-                    buf_load_lds16(wbuf, lo, sb + (uint32_t)IL64_Q6K_D, dst + 13 * 1024);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        buf_load_lds16(wbuf, lo, sb + (uint32_t)IL64_Q6K_P + (uint32_t)(2 * pw + j) * 1024u,
+                                       dst + (12 + 2 * pw + j) * 1024);
                 }
             } else if (q == 0) {
 #pragma unroll
@@ -584,38 +553,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
 #pragma unroll
             for (int i = 0; i < T::A_LOADS; i++) buf_load_lds16(abuf, a_lane[i], soff, dst + i * 1024);
         };
-        // Q6_K's scales of group g: the (column, set) pairs pt, pt + 128,
-        // ... (set = pair / BN), chunks 0..3 each (the other formats' come
-        // from their headers)
-        static_assert(Fmt::DSC || Fmt::IL64, "a scale pass for the IL64 layout only");
-        auto make_scales = [&](int g) {
-            if constexpr (!Fmt::DSC) {
-#pragma unroll
-                for (int pr = pt; pr < Fmt::NSETS * BN; pr += 128) {
-                    const int p_col = pr & (BN - 1), p_si = pr / BN;
-                    const uint32_t sc_wr = lds0 + OFF_SC + (uint32_t)((p_si * 4 * BN + p_col) * 4);
-                    const uint32_t gb = lds0 + OFF_W + (uint32_t)((g & (NWBUF - 1)) * W_GROUP);
-                    // the column's 16 signed scales and d: set p_si of chunk q is scale 4q + p_si
-                    u32x4 scb = lds_read16<0>(gb + 12u * 1024u + (uint32_t)(p_col * 16));
-                    uint32_t db = lds_read_u16<0>(gb + 13u * 1024u + (uint32_t)(p_col * 2));
-                    wait_lgkm0(scb, db);
-                    const float d = h2f(db);
-                    auto one = [&](uint32_t word) {
-                        const float ds = d * (float)(int8_t)(word >> (8 * p_si));  // exact: 11 x 8 bits
-                        const _Float16 sh = (_Float16)ds;
-                        return pack_h2(sh, (_Float16)(-32.0f * (float)sh));  // -32 s exact
-                    };
-                    const u32x4 v = u32x4{one(scb.x), one(scb.y), one(scb.z), one(scb.w)};
-                    const uint32_t wr = sc_wr + (uint32_t)((g & 1) * SC_BUF);
-                    lds_write4(wr, v.x);
-                    lds_write4(wr + 4 * BN, v.y);
-                    lds_write4(wr + 8 * BN, v.z);
-                    lds_write4(wr + 12 * BN, v.w);
-                }
-            }
-        };
-
-        // prologue: virtual iterations -4GA .. -1; group 0's scales
+        // prologue: virtual iterations -4GA .. -1
 #pragma unroll
         for (int it = -4 * GA; it < 0; it++) {
             if ((it & 3) < 2) {
@@ -630,18 +568,11 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             }
         }
         wait_vm_barrier<T::vm_after(3)>();  // barrier P1: A chunks 0, 1 and W groups 0, 1 done
-        make_scales(0);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();  // barrier P2: group 0's scales written
         for (int g = 0; g < ngroups; g++) {
             auto step = [&](auto uc) {
                 constexpr int u = decltype(uc)::value;
                 wait_vm_barrier<T::vm_after(u)>();
                 issue(4 * g + u);
-                if constexpr (u == 1) {
-                    make_scales(g + 1);  // read by the compute waves from step 2 on
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // written before the next barrier
-                }
             };
             step(ic<0>{});
             step(ic<1>{});
@@ -681,18 +612,11 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 wh_rd[q] = w_rd[q];
         }
     }
-    // {scale, bias} of chunk q: [set][q][column], consecutive columns in
-    // consecutive banks (a 32-column read is conflict-free; the
-    // [column][set][chunk] order cost ~14 bank-conflict cycles per read)
-    const uint32_t sc_rd = lds0 + OFF_SC + (uint32_t)((Fmt::sidx(kq) * 4 * BN + ncol) * 4);
-    // DSC: the column's header in W group buffer 0
-    const uint32_t hd_rd = lds0 + OFF_W + (uint32_t)(NH * W_HALF + ncol * Fmt::HDR);
-    // {scale, bias} address of chunk position q of group g
+    // {scale, bias} word of chunk position q of group g: the column's header
+    // (or, Q6_K, its pair in the [pair][column] block) in the group buffer
+    const uint32_t hd_rd = lds0 + OFF_W + (uint32_t)(Fmt::hoff(BN) + ncol * Fmt::CST);
     auto sb_addr = [&](int g, int q) -> uint32_t {
-        if constexpr (Fmt::DSC)
-            return hd_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP + Fmt::sbyte(q, kq));
-        else
-            return sc_rd + (uint32_t)((g & 1) * SC_BUF + 4 * BN * q);
+        return hd_rd + (uint32_t)((g & (NWBUF - 1)) * W_GROUP + Fmt::sbyte(q, kq));
     };
 
     f32x16 acc[RB * CB];
@@ -736,15 +660,12 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // one chunk's {scale, bias} per column block (a register each, not the
     // group's four: the 96-row tile's accumulators need the room)
     auto read_sb = [&](uint32_t *v, uint32_t addr) {
-        if constexpr (Fmt::DSC && Fmt::SBW == 2) {  // f16 d zero-extended: {d, +0}
+        if constexpr (Fmt::SBW == 2) {  // f16 d zero-extended: {d, +0}
             v[0] = lds_read_u16<0>(addr);
-            if constexpr (CB > 1) v[1] = lds_read_u16<32 * Fmt::HDR>(addr);  // +32 columns of headers
-        } else if constexpr (Fmt::DSC) {  // a precomputed pair
+            if constexpr (CB > 1) v[1] = lds_read_u16<32 * Fmt::CST>(addr);  // +32 columns
+        } else {  // a pair formed at upload
             v[0] = lds_read4<0>(addr);
-            if constexpr (CB > 1) v[1] = lds_read4<32 * Fmt::HDR>(addr);
-        } else {
-            v[0] = lds_read4<0>(addr);
-            if constexpr (CB > 1) v[1] = lds_read4<128>(addr);  // +32 columns
+            if constexpr (CB > 1) v[1] = lds_read4<32 * Fmt::CST>(addr);
         }
     };
     auto wait_reads = [&](half8 *a, WRaw *r, uint32_t *v) {
@@ -761,7 +682,6 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     };
 
     __builtin_amdgcn_s_barrier();  // barrier P1
-    __builtin_amdgcn_s_barrier();  // barrier P2: chunk 0 dequantized, chunk 1's nibbles read
     half8 a_cur[RB], b_cur[CB];
     WRaw raw_nxt[CB];
     uint32_t sb_nxt[CB];  // {scale, bias} of chunk c+1

@@ -519,6 +519,15 @@ void relayout_host(const uint8_t *src, const DevWeight &dw, uint8_t *dst) {
                     for (int i = 0; i < 16; i++) d[(j * 64 + lane) * 16 + i] = blk[16 * j + i];
                 d[IL64_Q6K_D + 2 * lane] = blk[208];
                 d[IL64_Q6K_D + 2 * lane + 1] = blk[209];
+                // the GEMM's pairs: s = f16(d sc) (the f32 product is exact: 11 x 8 bits), -32 s
+                _Float16 dh;
+                std::memcpy(&dh, blk + 208, 2);
+                for (int jj = 0; jj < 16; jj++) {
+                    const _Float16 sh = (_Float16)((float)dh * (float)(int8_t)blk[192 + jj]);
+                    const _Float16 bh = (_Float16)(-32.0f * (float)sh);
+                    std::memcpy(d + IL64_Q6K_P + (jj * 64 + lane) * 4, &sh, 2);
+                    std::memcpy(d + IL64_Q6K_P + (jj * 64 + lane) * 4 + 2, &bh, 2);
+                }
             }
         }
         break;

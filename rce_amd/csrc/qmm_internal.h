@@ -39,7 +39,9 @@ enum Layout : int {
     // Rows in groups of 64; per group and super-block sb (IL64_Q6K_SB
     // bytes at sb * IL64_Q6K_SB) the 13 16-byte chunks of the super-block's
     // ql (0..7), qh (8..11) and scales (12) for the 64 rows, chunk j of row
-    // r at (j * 64 + r % 64) * 16, then the rows' 2-byte d values.
+    // r at (j * 64 + r % 64) * 16, then the rows' 2-byte d values, then at
+    // IL64_Q6K_P the matrix-core GEMM's binary16 pairs {f16(d sc_j),
+    // -32 f16(d sc_j)} of the 16 scales, pair j of row r at (j * 64 + r % 64) * 4.
     LAYOUT_IL64_Q6_K = 4,
     // Q5_K: LAYOUT_SPLIT_Q4_K's header and two qs planes, plus at plane3 +
     // 8 u one 8-byte word per 64-group u: bit l (l < 32) = the 5th bit of
@@ -94,8 +96,9 @@ struct DevWeight {
     const uint8_t *aux;   // I2_S: device address of the tensor's f32 scale
 };
 
-constexpr size_t IL64_Q6K_D = 13 * 64 * 16;         // 13312: the d values
-constexpr size_t IL64_Q6K_SB = IL64_Q6K_D + 64 * 2;  // 13440 = 64 * 210
+constexpr size_t IL64_Q6K_D = 13 * 64 * 16;          // 13312: the d values
+constexpr size_t IL64_Q6K_P = IL64_Q6K_D + 64 * 2;   // 13440 = 64 * 210: the scale pairs
+constexpr size_t IL64_Q6K_SB = IL64_Q6K_P + 64 * 64;  // 17536
 
 // Launch shape of a decode kernel: threads per block, rows per lane, and
 // activation rows (tokens) per block.
