@@ -137,8 +137,9 @@ int rce_qmm_supports(uint32_t dtype, size_t n_cols, rce_qmm_mode mode);
 /* A device-resident QuantWeight made from GGUF bytes: the weight
  * [n_rows = N_out, n_cols = K_in], row-major, each row k/QK blocks
  * (rce-op-qmm/src/lib.rs L60-91 QuantWeight, L123-138 from_owned_bytes).
- * The bytes are copied to HBM once (the library may store them in a
- * device layout of the same byte count); the caller keeps its buffer.
+ * The bytes are copied to HBM once, in a device layout of about the same
+ * byte count (Q4_K / Q5_K / Q6_K add their matrix-core GEMM scales, 32 or
+ * 64 bytes per super-block); the caller keeps its buffer.
  * len must equal n_rows * row_bytes(dtype, n_cols) (I2_S: plus its 4-byte scale). */
 rce_qmm_status rce_qmm_weight_from_bytes(rce_qmm_context *ctx, uint32_t dtype, size_t n_rows,
                                          size_t n_cols, const uint8_t *bytes, size_t len,
