@@ -446,13 +446,19 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
         const int pw = wave - NC / 64;  // 0, 1
         //   A: rows BM/2*pw .. +BM/2-1; instruction i covers rows
         //      BM/2*pw + 8i .. +7, 8 lanes per row; lane slot p holds
-        //      column p ^ f(row)
+        //      column p ^ f(row).  Lanes of rows past the tile's own (a
+        //      grouped tile's expert has fewer) read past the buffer's end,
+        //      which moves no data and lands zeros; their sums are not
+        //      stored.  (Where that offset plus the chunk offsets could wrap
+        //      32 bits, they read the tile's last row instead.)
+        const bool pad_oob = (uint64_t)a_bytes + 2 * (uint64_t)K < ((uint64_t)1 << 32);
         uint32_t a_lane[T::A_LOADS];
 #pragma unroll
         for (int i = 0; i < T::A_LOADS; i++) {
             const int ar = BM / 2 * pw + 8 * i + (lane >> 3);
             const int aswz = (ar & 7) ^ ((ar >> 3) & 1);
-            a_lane[i] = (uint32_t)arow[ar] * (uint32_t)(2 * K) + 16u * (uint32_t)((lane & 7) ^ aswz);
+            a_lane[i] = ar >= rows && pad_oob ? a_bytes
+                                              : (uint32_t)arow[ar] * (uint32_t)(2 * K) + 16u * (uint32_t)((lane & 7) ^ aswz);
         }
         const __amdgpu_buffer_rsrc_t abuf = byte_buffer(A, a_bytes);
         //   W: half pw of the group; instruction i covers rows 16i .. +15,
