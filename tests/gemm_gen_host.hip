@@ -7,6 +7,10 @@
 // runs the kernel's chunk pipeline (gen_pipeline, with the kernel's DEPTH
 // and CPB) and prints its operations, one per line: "S" (barrier),
 // "L slot chunk", "M chunk buf", "T slot chunk buf" (store).
+//   gemm_gen_host pairs DTYPE N K IN_GGUF_BYTES OUT
+// writes the binary16 {scale, bias} pairs the upload forms for the nibble
+// GEMM (Q4_K / Q5_K: 8 per super-block, Q6_K: 16), [row][super-block][pair],
+// 4 bytes each, read from the relaid-out weight.
 #include "../rce_amd/csrc/gemm_gen.hip"
 
 #include <cstdio>
@@ -39,6 +43,11 @@ static int sched(int nchunks) {
 
 int main(int argc, char **argv) {
     if (argc == 3 && std::strcmp(argv[1], "sched") == 0) return sched(atoi(argv[2]));
+    const bool pairs = argc == 7 && std::strcmp(argv[1], "pairs") == 0;
+    if (pairs) {
+        argv++;
+        argc--;
+    }
     if (argc != 6) return 2;
     const uint32_t dt = (uint32_t)atoi(argv[1]);
     const size_t n = (size_t)atol(argv[2]), k = (size_t)atol(argv[3]);
@@ -58,6 +67,24 @@ int main(int argc, char **argv) {
     std::vector<uint8_t> dev(bytes + layout_pad_bytes(w), 0);
     relayout_host(src.data(), w, dev.data());
     w.base = dev.data();
+    if (pairs) {
+        const size_t nsb = k / 256, np = dt == T_Q6_K ? 16 : 8;
+        std::vector<uint8_t> pr(n * nsb * np * 4);
+        for (size_t r = 0; r < n; r++)
+            for (size_t sb = 0; sb < nsb; sb++)
+                for (size_t j = 0; j < np; j++) {
+                    const uint8_t *src_p =
+                        dt == T_Q6_K ? dev.data() + (r >> 6) * w.group_stride + sb * IL64_Q6K_SB + IL64_Q6K_P +
+                                           (j * 64 + (r & 63)) * 4
+                                     : dev.data() + r * w.row_stride + w.plane4 + 32 * sb + 4 * j;
+                    std::memcpy(pr.data() + ((r * nsb + sb) * np + j) * 4, src_p, 4);
+                }
+        f = fopen(argv[5], "wb");
+        if (!f) return 6;
+        fwrite(pr.data(), 1, pr.size(), f);
+        fclose(f);
+        return 0;
+    }
     std::vector<uint16_t> out(n * k);
     switch (dt) {
     case T_Q8_0: run<FQ8_0>(w, out.data()); break;

@@ -69,6 +69,55 @@ def test_generic_gemm_weights_are_the_reference_values_in_binary16(harness, tmp_
     assert got.max() != 0  # not an all-zero output
 
 
+def scale_pairs(b, dt, n, k):
+    """The nibble GEMM's binary16 {scale, bias} pairs restated from the GGUF
+    bytes (rce-op-qmm/src/lib.rs L719-728 get_scale_min; dequant.rs L658-701
+    for Q6_K): Q4_K / Q5_K sub-block j: {f16(d sc_j), f16(-(dmin m_j))};
+    Q6_K scale j: {s = f16(d sc_j), f16(-32 s)}; [row][super-block][pair]
+    as uint16 pairs."""
+    nsb = k // 256
+    bs = {O.Q4_K: 144, O.Q5_K: 176, O.Q6_K: 210}[dt]
+    blk = np.frombuffer(bytes(b), np.uint8).reshape(n, nsb, bs)
+    f16 = lambda a: a.copy().view(np.float16)[..., 0].astype(np.float32)  # noqa: E731
+    if dt == O.Q6_K:
+        d = f16(blk[:, :, 208:210])
+        sc = blk[:, :, 192:208].view(np.int8).astype(np.float32)
+        s = (d[:, :, None] * sc).astype(np.float16)
+        bias = (np.float32(-32.0) * s.astype(np.float32)).astype(np.float16)
+    else:
+        d, dmin = f16(blk[:, :, 0:2]), f16(blk[:, :, 2:4])
+        q = blk[:, :, 4:16].astype(np.int32)
+        sc = np.zeros((n, nsb, 8), np.int32)
+        m = np.zeros((n, nsb, 8), np.int32)
+        for j in range(8):
+            if j < 4:
+                sc[:, :, j], m[:, :, j] = q[:, :, j] & 63, q[:, :, j + 4] & 63
+            else:
+                sc[:, :, j] = (q[:, :, j + 4] & 0x0F) | ((q[:, :, j - 4] >> 6) << 4)
+                m[:, :, j] = (q[:, :, j + 4] >> 4) | ((q[:, :, j] >> 6) << 4)
+        s = (d[:, :, None] * sc.astype(np.float32)).astype(np.float16)
+        bias = (-(dmin[:, :, None] * m.astype(np.float32))).astype(np.float16)
+    return np.stack([s.view(np.uint16), bias.view(np.uint16)], axis=-1)
+
+
+@pytest.mark.parametrize("dt,n,k", [(O.Q4_K, 20, 1024), (O.Q5_K, 70, 512), (O.Q6_K, 130, 768)])
+def test_upload_scale_pairs(harness, tmp_path, dt, n, k):
+    """The pairs the upload adds to the Q4_K / Q5_K / Q6_K device layouts
+    for the matrix-core GEMM equal their restatement from the file's bytes,
+    bit for bit (a wrong sub-block index, a swapped scale / min or a
+    rounding of the product in binary16 steps fails here)."""
+    rng = np.random.default_rng(1300 + dt + n)
+    b = weight_bytes(rng, dt, n, k)
+    src, dst = tmp_path / "w.bin", tmp_path / "p.bin"
+    b.tofile(src)
+    subprocess.run([harness, "pairs", str(dt), str(n), str(k), str(src), str(dst)], check=True)
+    nsb, npr = k // 256, 16 if dt == O.Q6_K else 8
+    got = np.fromfile(dst, np.uint16).reshape(n, nsb, npr, 2)
+    want = scale_pairs(b, dt, n, k)
+    assert np.array_equal(got, want)
+    assert np.any(got[..., 1] != 0)  # the biases are not all zero
+
+
 def replay(ops, nchunks):
     """Check one printed schedule of gen_pipeline: every chunk is multiplied
     once, in order, from an LDS buffer that holds it and was stored before
