@@ -700,7 +700,7 @@ def main():
                 per[key] = {"us": round(sms * 1e3, 2), "GB/s": round(sg, 1), "hbm_frac": round(sg / HBM_PEAK_GBS, 4)}
                 log(f"  {key}: {sms * 1e3:.2f} us  {sg:.0f} GB/s ({sg / HBM_PEAK_GBS:.1%})")
     if "gemm" in rows:  # configs[2]: Q4_K prefill GEMM 512x4096x4096 on f16 MFMA, then the other formats
-        for gdt in (G.Q4K, G.Q6K, G.Q8_0, G.Q5K, G.BF16, G.F32):
+        for gdt in (G.Q4K, G.Q6K, G.Q8_0, G.Q5K, G.Q5_0, G.Q4_1, G.BF16, G.F32):
             gms, gs = time_gemm(hip, ctx, gdt, 4096, 4096, 512, max(20, args.steps // 4), 5, 300)
             gtf = 2.0 * 512 * 4096 * 4096 / (gms * 1e-3) / 1e12
             mname = "bf16_mfma" if gdt in (G.BF16, G.F32) else "f16_mfma"

@@ -1,7 +1,7 @@
 // gemm_f16.hip -- prefill-shaped GEMM of the GGUF quantized-matmul path on
 // the CDNA4 matrix cores: out[M, N] = A[M, K] . W[N, K]^T with W in GGUF
-// Q4_K, Q5_K or Q4_0 blocks (and Q8_0 and Q6_K, plain GEMM, 128 x 64
-// tiles: the Q80 and Q6K formats below), dequantized to binary16 MFMA
+// Q4_K, Q5_K, Q4_0, Q4_1, Q5_0, Q8_0 or Q6_K blocks (the last two in
+// 128 x 64 tiles only), dequantized to binary16 MFMA
 // fragments in registers and contracted with v_mfma_f32_32x32x16_f16 (f32
 // accumulation).
 //
@@ -306,7 +306,10 @@ struct Q5K : Q4K {
     static constexpr bool HB = true;
     static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR + bn * 32; }
     static constexpr int w_loads(int bn) { return bn / 16 * NH / 2 + bn / 64; }
-    __device__ static int hb_byte(int kq) { return 4 * (kq & 1) + 2 * (kq >> 1); }
+    // the row's 32 fifth-bit bytes of group g, and the byte (of lane half 0)
+    // of chunk q, k-step kq
+    __device__ static size_t hb_src(const DevWeight &w, int g) { return w.plane3 + 32 * (size_t)g; }
+    __device__ static int hb_off(int q, int kq) { return 8 * q + 4 * (kq & 1) + 2 * (kq >> 1); }
 };
 
 // Q4_0: halves = the 16-byte nibble runs of blocks 8g..8g+3 and 8g+4..8g+7;
@@ -334,6 +337,35 @@ struct Q40 {
     __device__ static int sbyte(int q, int kq) { return 4 * q + 2 * sidx(kq); }
 };
 
+
+// Q4_1 (LAYOUT_SPLIT_Q4_1): Q4_0's nibble halves; header = the eight
+// blocks' 4-byte {d, m} words (rce-op-qmm/src/lib.rs L615-645: value
+// d q + m), which are the {scale, bias} words as they stand: the weight is
+// d n + m rounded once to binary16.
+struct Q41 : Q40 {
+    static constexpr int OFF = 1024, HDR = 32, SBW = 4, CST = HDR;
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR; }
+    static constexpr int h_loads(int bn) { return bn / 64; }  // 32 rows x 32 bytes per load
+    __device__ static size_t hdr_off(const DevWeight &, int g) { return 32 * (size_t)g; }
+    __device__ static int sbyte(int q, int kq) { return 4 * (2 * q + sidx(kq)); }
+};
+
+// Q5_0 (LAYOUT_SPLIT_Q5_0): Q4_0's scales and nibble halves, plus the
+// eight blocks' 4-byte qh words of a group (plane 2), 32 bytes per row,
+// loaded with the halves: bit p of a block's word is the fifth bit of its
+// position p (rce-op-qmm/src/lib.rs L525-561).  A lane's eight weights of
+// k-step kq of chunk q are positions 16(kq & 1) + 8h .. +7 of block
+// 2q + kq / 2, so their fifth bits are byte 2(kq & 1) + h of that word.
+// u = nibble | bit << 4 in 0..31, f16(1024 + u) - 1040 = u - 16 exactly,
+// then (u - 16) d + 0 rounds once.
+struct Q50 : Q40 {
+    static constexpr int OFF = 1040;
+    static constexpr bool HB = true;
+    static constexpr int w_group(int bn) { return NH * bn * 64 + bn * HDR + bn * 32; }
+    static constexpr int w_loads(int bn) { return bn / 16 * NH / 2 + bn / 64; }
+    __device__ static size_t hb_src(const DevWeight &w, int g) { return w.plane2 + 32 * (size_t)g; }
+    __device__ static int hb_off(int q, int kq) { return 4 * (2 * q + (kq >> 1)) + 2 * (kq & 1); }
+};
 
 // Q8_0: four 64-byte pieces per row and group: bytes 0..15 (plane 1) and
 // 16..31 (plane 2) of blocks 8g..8g+3 and 8g+4..8g+7 (piece 2 plane +
@@ -530,7 +562,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
                 if constexpr (Fmt::HB) {
 #pragma unroll
                     for (int i = 0; i < HB_LOADS; i++)
-                        buf_load_lds16(wbuf, hb_lane[i], (uint32_t)(w.plane3 + 32 * (size_t)gs),
+                        buf_load_lds16(wbuf, hb_lane[i], (uint32_t)Fmt::hb_src(w, gs),
                                        dst + NH * W_HALF + BN * Fmt::HDR + (HB_LOADS * pw + i) * 1024);
                 }
             } else if constexpr (Fmt::HDR == 16) {
@@ -613,7 +645,7 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             w_rd[q] = lds0 + OFF_W + (uint32_t)(Fmt::half_of(q, kq) * W_HALF + ncol * 64 +
                                                 16 * (Fmt::piece_of(q, kq) ^ ((ncol >> 2) & 3)) + 8 * h);
             if constexpr (Fmt::HB)  // the fifth-bit byte of the lane's eight weights
-                wh_rd[q] = lds0 + OFF_W + (uint32_t)(NH * W_HALF + BN * Fmt::HDR + ncol * 32 + 8 * q + Fmt::hb_byte(kq) + h);
+                wh_rd[q] = lds0 + OFF_W + (uint32_t)(NH * W_HALF + BN * Fmt::HDR + ncol * 32 + Fmt::hb_off(q, kq) + h);
             else
                 wh_rd[q] = w_rd[q];
         }
@@ -898,6 +930,8 @@ hipError_t gemm_prepare_lds() {
     all_bm(Q4K{});
     all_bm(Q5K{});
     all_bm(Q40{});
+    all_bm(Q41{});
+    all_bm(Q50{});
     all_epi(Q80{}, ic<128>{});
     all_epi(Q6K{}, ic<128>{});
     return e;
@@ -910,7 +944,7 @@ bool gemm_q8_supports(uint32_t dtype, size_t n_cols) {
 bool gemm_supports(uint32_t dtype, size_t n_cols) {
     if (n_cols >= (size_t)1 << 31 || n_cols == 0) return false;
     if (dtype == T_Q4_K || dtype == T_Q5_K) return n_cols % 256 == 0;
-    if (dtype == T_Q4_0) return n_cols % 256 == 0;  // whole scale groups of 8 blocks
+    if (dtype == T_Q4_0 || dtype == T_Q4_1 || dtype == T_Q5_0) return n_cols % 256 == 0;  // whole groups of 8 blocks
     return false;
 }
 
@@ -938,6 +972,8 @@ static bool with_fmt(uint32_t dtype, F &&f) {
     case T_Q4_K: f(Q4K{}); return true;
     case T_Q5_K: f(Q5K{}); return true;
     case T_Q4_0: f(Q40{}); return true;
+    case T_Q4_1: f(Q41{}); return true;
+    case T_Q5_0: f(Q50{}); return true;
     default: return false;
     }
 }

@@ -75,6 +75,20 @@ def q40_f16_weights(b, n, k):
     return (q * d[:, :, None]).astype(F16).reshape(n, k).astype(np.float64)
 
 
+def q41_f16_weights(b, n, k):
+    """Q4_1 bytes (d, m, qs[16] per block) -> the nibble kernel's weight
+    f16(d * q + m), the product and sum exact, one rounding (the reference
+    rounds d * q and the sum in f32 first, dequant.rs Q4_1; they differ in
+    rare double-rounding cases only)."""
+    nb = k // 32
+    blk = np.frombuffer(bytes(b), np.uint8).reshape(n, nb, 20)
+    d = blk[:, :, 0:2].copy().view(F16)[:, :, 0].astype(np.float64)
+    m = blk[:, :, 2:4].copy().view(F16)[:, :, 0].astype(np.float64)
+    qs = blk[:, :, 4:20].astype(np.int32)
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=2).astype(np.float64)
+    return (q * d[:, :, None] + m[:, :, None]).astype(F16).reshape(n, k).astype(np.float64)
+
+
 def run_gemm(ctx, w, x, a_dtype):
     t = x.shape[0]
     xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
@@ -199,6 +213,14 @@ GEN_CASES = [
     (O.Q5_K, 64, 256, 1),
     (O.Q5_K, 200, 768, 80),
     (O.Q5_K, 130, 1280, 50),
+    # Q4_1 ({d, m} words as the scale words) and Q5_0 (Q4_0 plus fifth-bit
+    # words) with K a multiple of 256 on the same kernel, all three tiles
+    (O.Q4_1, 130, 512, 37),
+    (O.Q4_1, 200, 768, 80),
+    (O.Q4_1, 64, 2048, 129),
+    (O.Q5_0, 64, 256, 1),
+    (O.Q5_0, 200, 768, 80),
+    (O.Q5_0, 130, 1280, 129),
 ]
 
 
@@ -252,11 +274,14 @@ def test_gemm_other_formats_parity(ctx, dt, n, k, t):
     xv = x.astype(np.float64)
     w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
     got = run_gemm(ctx, w, x, G.F16)
-    # Q6_K and Q5_K run the nibble kernel (scale rounded to binary16 first)
+    # Q6_K and Q5_K run the nibble kernel (scale rounded to binary16 first),
+    # as does Q4_1 at K % 256 == 0 (d q + m rounded once)
     if dt == O.Q6_K:
         wf = q6k_f16_weights(b, n, k)
     elif dt == O.Q5_K:
         wf = q4k_f16_weights(b, n, k, q5=True)
+    elif dt == O.Q4_1 and k % 256 == 0:
+        wf = q41_f16_weights(b, n, k)
     else:
         wf = mfma_weights(b, dt, n, k)
     assert np.all(np.isfinite(wf))

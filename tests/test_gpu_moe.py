@@ -240,13 +240,17 @@ def f16_weights(b, dt, n, k):
     """The binary16 weights the F16_MFMA kernels form: the oracle's
     dequantized value rounded once (gemm_gen.hip), or for Q4_K the nibble
     kernel's f16(f16(d*sc)*q + f16(-dmin*m)) (gemm_f16.hip), for Q4_K and
-    Q5_K, and its f16(f16(d*sc)*q) for Q6_K."""
+    Q5_K, its f16(f16(d*sc)*q) for Q6_K, and f16(d*q + m) for Q4_1 at K % 256
+    == 0."""
     if dt in (O.Q4_K, O.Q5_K):
         from test_gpu_gemm import q4k_f16_weights
         return q4k_f16_weights(b, n, k, q5=dt == O.Q5_K)
     if dt == O.Q6_K:
         from test_gpu_gemm import q6k_f16_weights
         return q6k_f16_weights(b, n, k)
+    if dt == O.Q4_1 and k % 256 == 0:
+        from test_gpu_gemm import q41_f16_weights
+        return q41_f16_weights(b, n, k)
     from test_gpu_gemm import mfma_weights
     return mfma_weights(b, dt, n, k)
 
