@@ -500,10 +500,10 @@ rce_qmm_status moe_run(rce_qmm_context *ctx, const rce_qmm_weight *const *w1, co
                 return fail(RCE_QMM_BAD_SHAPE, "up matrices must match the gate matrices in dtype and shape");
         }
     }
-    // the grouped GEMM (F16_MFMA): the nibble kernel for Q4_K / Q5_K / Q4_0
-    // (any tile) and Q8_0 / Q6_K with K a multiple of 256 (128-row tiles),
-    // the generic one for the rest (Q8_0 at other K, Q5_0, Q4_1, F16, BF16
-    // and F32)
+    // the grouped GEMM (F16_MFMA): the nibble kernel for Q4_K / Q5_K / Q4_0 /
+    // Q4_1 / Q5_0 (any tile) and Q8_0 / Q6_K (128-row tiles) with K a
+    // multiple of 256, the generic one for the rest (Q8_0 / Q5_0 / Q4_1 at
+    // other K, F16, BF16 and F32)
     auto experts_ok = [&](uint32_t dt, size_t k) { return supports_mode(dt, k, (int)mode); };
     if (!experts_ok(a1.dtype, d_model) || !experts_ok(a2.dtype, d_ff))
         return fail(RCE_QMM_UNSUPPORTED_DTYPE, "the experts' dtype/shape has no GPU kernel in mode " +
