@@ -254,9 +254,12 @@ __global__ __launch_bounds__(64) void k_gemv_q8_mfma(DevWeight w, const unsigned
 
 }  // namespace
 
+// The token bound is the decode kernels' pre-quantized form's (this form's
+// callers fall back to it), and k_quantize_act counts its tasks,
+// t_rows * n_cols / 8, in an int.
 bool gemv_q8_mfma_supports(uint32_t dtype, size_t n_cols, size_t t_rows) {
-    return (dtype == T_Q4_0 || dtype == T_Q8_0) && n_cols % 256 == 0 && t_rows >= 2 && t_rows <= 65535 * 16 &&
-           n_cols * 16 < ((size_t)1 << 31);
+    return (dtype == T_Q4_0 || dtype == T_Q8_0) && n_cols % 256 == 0 && t_rows >= 2 && t_rows <= 65535 * 8 &&
+           n_cols * 16 < ((size_t)1 << 31) && t_rows * (n_cols / 8) < ((size_t)1 << 31);
 }
 
 // Where this form is the faster one.  A wave walks all of K for its 16 rows
