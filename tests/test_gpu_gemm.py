@@ -345,3 +345,32 @@ def test_gemm_misaligned_f16_activations_rejected(ctx, dt):
     with pytest.raises(rce_amd.QmmError, match="16-byte aligned"):
         rce_amd.mm_batched_dev(ctx, xa.ptr + 2, G.F16, t, w, out.ptr, Mode.F16_MFMA)
     xa.free(); out.free(); w.close()
+
+
+def test_gemm_activations_past_4gib_sliced(ctx):
+    """The nibble kernel's activation offsets are 32-bit, so a call whose
+    f16 activations pass 2^32 bytes runs in slices of whole 128-row tiles
+    (qmm_abi.cpp run_gemm).  Each output's sum does not depend on the
+    slicing: rows on both sides of the slice boundary and the last rows
+    equal, bit for bit, a separate call on just those rows, which in turn
+    is within the f16 budget of the oracle."""
+    n, k = 64, 256
+    max_rows = ((2 ** 32 - 1) // (2 * k)) // 128 * 128  # the host's slice
+    t = max_rows + 1000
+    note(f"gemm f16-mfma sliced activations t={t} k={k} ({2 * t * k / 2 ** 30:.2f} GiB)")
+    rng = np.random.default_rng(7400)
+    b = O.quantize((rng.standard_normal((n, k)) * 0.02).astype(F32), O.Q4_0)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, O.Q4_0, n, k)
+    base = rng.standard_normal((4099, k)).astype(F16)  # a period prime to the tile rows
+    x = np.resize(base, (t, k))
+    xa = rce_amd.DeviceBuffer.from_numpy(ctx, x)
+    out = rce_amd.DeviceBuffer(ctx, t * n * 4)
+    rce_amd.mm_batched_dev(ctx, xa.ptr, G.F16, t, w, out.ptr, Mode.F16_MFMA)
+    ctx.synchronize()
+    got = out.download(F32, t * n).reshape(t, n)
+    xa.free(); out.free()
+    rows = np.r_[0:200, max_rows - 300:max_rows + 300, t - 200:t]
+    want = run_gemm(ctx, w, np.ascontiguousarray(x[rows]), G.F16)
+    assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
+    assert normwise(want, O.mm_batched(x[rows].astype(F32), b, O.Q4_0, n, k)) < 2e-3
+    w.close()
