@@ -22,11 +22,12 @@
 //     B tile is written), and issues four MFMAs.  The four k-step partial
 //     sums of each output are added at the end through LDS in a fixed order
 //     (deterministic);
-//   * two producer waves issue every global -> LDS load and compute the
-//     per-sub-block fma scales from the GGUF headers.  A load instruction
-//     can hold its wave up while the CU's memory pipeline is busy (each
-//     1 KB load occupies it ~20 cycles), so the loads live in waves that do
-//     nothing else and the MFMA/dequantization waves never stall on them.
+//   * two producer waves issue every global -> LDS load (the compute waves
+//     read each chunk's {scale, bias} word from the weight group in LDS
+//     themselves).  A load instruction can hold its wave up while the CU's
+//     memory pipeline is busy (each 1 KB load occupies it ~20 cycles), so
+//     the loads live in waves that do nothing else and the
+//     MFMA/dequantization waves never stall on them.
 // One barrier per chunk.  The producers wait (s_waitcnt vmcnt, one
 // compile-time immediate per chunk position) for the data the compute
 // waves read next before joining it.
@@ -42,7 +43,9 @@
 //     per LDS cycle; NS - 1 chunks ahead;
 //   * W: per scale group (four chunks: one Q4_K super-block, eight Q4_0
 //     blocks) each row's 2 x 64 bytes of nibbles (16-byte pieces rotated by
-//     (row >> 2) & 3) and its 16-byte scale header, loaded GA groups ahead.
+//     (row >> 2) & 3) and its scale words (Q4_0: the 16-byte header of f16
+//     block scales; Q4_K: the 32 bytes of {d*sc, -dmin*m} pairs formed at
+//     upload; the other formats below), loaded GA groups ahead.
 // The compute waves read chunk c+1's A fragments and chunk c+2's nibbles
 // while chunk c's MFMAs and chunk c+1's dequantization run.
 //
@@ -908,9 +911,10 @@ hipError_t launch_grouped_epi(int epi, const DevWeight &w, const DevWeight *wtab
 
 // The kernel's per-lane load offsets are 32-bit: the activations (all of
 // them: a grouped tile gathers rows from anywhere) below 2^32 bytes, and a
-// tile's 128 weight rows.
+// tile's 128 weight rows; the tile counts are ints.
 bool gemm_shape_ok(size_t a_rows, const DevWeight &w) {
-    return a_rows * w.n_cols * 2 < ((size_t)1 << 32) && 128 * w.row_stride < ((size_t)1 << 32);
+    return a_rows * w.n_cols * 2 < ((size_t)1 << 32) && 128 * w.row_stride < ((size_t)1 << 32) &&
+           w.n_rows < ((size_t)1 << 31);
 }
 
 hipError_t gemm_prepare_lds() {
