@@ -103,10 +103,12 @@ static_assert(NWBUF >= GA + 1 && (NWBUF & (NWBUF - 1)) == 0, "W buffer ring");
 // The weight format (below) sets the bytes of one scale group of the tile's
 // columns in LDS (W_GROUP), the loads a producer issues for them at group
 // position 0 (W_LOADS; at position 1 h_loads: the headers or scale pairs)
-// and so the A stages that leave room for them (NS).
-template <int BM_, class Fmt>
+// and so the A stages that leave room for them (NS).  BN_ (0: the default
+// above) sets the columns of the 64-row tile that a wider tile's block runs
+// when it holds at most 64 rows (64 x 64 in a 128 x 64 launch).
+template <int BM_, class Fmt, int BN_ = 0>
 struct Tile {
-    static constexpr int BM = BM_, BN = BM_ == 96 ? 128 : 8192 / BM_;
+    static constexpr int BM = BM_, BN = BN_ ? BN_ : (BM_ == 96 ? 128 : 8192 / BM_);
     // A stages (chunks), loaded NS - 1 ahead: six where the tile's LDS holds
     // them, else five
     static constexpr int pipe_lds(int ns) { return ns * BM * KC * 2 + NWBUF * Fmt::w_group(BN); }
@@ -429,47 +431,23 @@ struct Q6K {
 template <int U>
 using ic = std::integral_constant<int, U>;
 
-// Plain GEMM: tiles == nullptr, row tile mt covers rows mt*BM .. of M.
-// Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows),
-// multiplied by wtab[e]; tiles at or past n_tiles[0] do nothing.
-// EPI (GemmEpilogue) is what the block stores for an output element o with
-// f32 sum v: v (f32 out); binary16 silu(v); binary16 silu(aux[o]) * v.
-template <class Fmt, int BM_, int EPI>
-__global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16 *__restrict__ A,
-                                                 const int *__restrict__ gather, size_t M, uint32_t a_bytes,
-                                                 void *__restrict__ out_v, const float *__restrict__ aux, int m_tiles,
-                                                 const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
-                                                 const DevWeight *__restrict__ wtab) {
-    using T = Tile<BM_, Fmt>;
+// One block's output tile in the T shape: rows m0 .. m0 + rows - 1 (arow:
+// the activation row of each, padded to T::BM), columns n0 .. n0 + BN - 1
+// of w.  EPI (GemmEpilogue) is what the block stores for an output element
+// o with f32 sum v: v (f32 out); binary16 silu(v); binary16 silu(aux[o]) * v.
+template <class T, class Fmt, int EPI>
+__device__ __forceinline__ void gemm_tile(const DevWeight &w, const _Float16 *__restrict__ A, uint32_t a_bytes,
+                                          void *__restrict__ out_v, const float *__restrict__ aux, size_t m0,
+                                          int rows, size_t n0, const int *arow, unsigned char *lds) {
     constexpr int BM = T::BM, BN = T::BN, RB = T::RB, CB = T::CB, NS = T::NS, NH = Fmt::NH;
     constexpr int A_STAGE = T::A_STAGE, W_HALF = T::W_HALF, W_GROUP = T::W_GROUP;
     constexpr int OFF_W = T::OFF_W;
-    extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ int arow[BM];
-    int mt, nt;
-    if (!tile_of_block<T::BN>(w_arg.n_rows, m_tiles, n_tiles, mt, nt)) return;  // before any barrier
-    DevWeight w = w_arg;
-    size_t m0 = (size_t)mt * BM;
-    int rows = (int)(M - m0 < (size_t)BM ? M - m0 : BM);
-    if (tiles) {
-        const MoeTile tl = tiles[mt];
-        w = wtab[tl.e];
-        m0 = (size_t)tl.r0;
-        rows = tl.rows;
-    }
     const size_t N = w.n_rows, K = w.n_cols;
-    const size_t n0 = (size_t)nt * BN;
     const int nchunks = (int)(K / KC), ngroups = nchunks / 4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool producer = wave >= NC / 64;
     const int l32 = lane & 31, h = lane >> 5;
-
-    if (tid < BM) {
-        const size_t m = m0 + (tid < rows ? tid : rows - 1);  // rows past the tile load its last row
-        arow[tid] = gather ? gather[m] : (int)m;
-    }
-    __syncthreads();
     const uint32_t lds0 = lds_addr(lds);
 
     if (producer) {
@@ -851,6 +829,69 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
             }
         }
     }
+}
+
+// Plain GEMM: tiles == nullptr, row tile mt covers rows mt*BM .. of M.
+// Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows),
+// multiplied by wtab[e]; tiles at or past n_tiles[0] do nothing.
+template <class Fmt, int BM_, int EPI>
+__global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16 *__restrict__ A,
+                                                 const int *__restrict__ gather, size_t M, uint32_t a_bytes,
+                                                 void *__restrict__ out_v, const float *__restrict__ aux, int m_tiles,
+                                                 const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
+                                                 const DevWeight *__restrict__ wtab) {
+    using T = Tile<BM_, Fmt>;
+    constexpr int BM = T::BM;
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int arow[BM];
+    // Which tile: plain launches as tile_of_block places them (the m-tiles
+    // sharing W rows on one XCD); grouped launches take the tiles in
+    // (row tile, column tile) order, block L tile L, so consecutive column
+    // tiles of an expert go to consecutive XCDs and every XCD gets an equal
+    // share of every expert's tiles.  The tiles differ in cost (below: a
+    // row tile of at most 64 rows runs the 64-row body), and placing whole
+    // experts on XCDs, as tile_of_block does, left the XCD of the largest
+    // expert to finish last (configs[3] 234 -> 221 us with both changes; the
+    // placement alone measured the same as expert-major).  Blocks past the
+    // tile count return before any barrier.
+    int mt, nt;
+    if (n_tiles) {
+        const int nn = (int)((w_arg.n_rows + T::BN - 1) / T::BN), L = blockIdx.x;
+        if (L >= n_tiles[0] * nn) return;
+        mt = L / nn;
+        nt = L % nn;
+    } else if (!tile_of_block<T::BN>(w_arg.n_rows, m_tiles, n_tiles, mt, nt)) {
+        return;
+    }
+    DevWeight w = w_arg;
+    size_t m0 = (size_t)mt * BM;
+    int rows = (int)(M - m0 < (size_t)BM ? M - m0 : BM);
+    if (tiles) {
+        const MoeTile tl = tiles[mt];
+        w = wtab[tl.e];
+        m0 = (size_t)tl.r0;
+        rows = tl.rows;
+    }
+    const int tid = threadIdx.x;
+    if (tid < BM) {
+        const size_t m = m0 + (tid < rows ? tid : rows - 1);  // rows past the tile load its last row
+        arow[tid] = gather ? gather[m] : (int)m;
+    }
+    __syncthreads();
+    const size_t n0 = (size_t)nt * T::BN;
+    // A 96- or 128-row tile that holds at most 64 rows (a grouped tile whose
+    // expert has that few, a plain GEMM's last row tile) runs the 64-row
+    // tile's body over the same columns: a third or half fewer activation
+    // copies and MFMAs, and each output's sum formed the same way.
+    if constexpr (BM_ > 64) {
+        using T64 = Tile<64, Fmt, T::BN>;
+        static_assert(T64::BN == T::BN && T64::LDS <= T::LDS, "the 64-row body in the wider tile's launch");
+        if (rows <= 64) {
+            gemm_tile<T64, Fmt, EPI>(w, A, a_bytes, out_v, aux, m0, rows, n0, arow, lds);
+            return;
+        }
+    }
+    gemm_tile<T, Fmt, EPI>(w, A, a_bytes, out_v, aux, m0, rows, n0, arow, lds);
 }
 
 __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__ d, size_t n) {
