@@ -882,12 +882,23 @@ __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16
     // A 96- or 128-row tile that holds at most 64 rows (a grouped tile whose
     // expert has that few, a plain GEMM's last row tile) runs the 64-row
     // tile's body over the same columns: a third or half fewer activation
-    // copies and MFMAs, and each output's sum formed the same way.
+    // copies and MFMAs, and each output's sum formed the same way (a wave's
+    // k-step partial over the tile's chunks in order, the four partials
+    // added in order).
     if constexpr (BM_ > 64) {
         using T64 = Tile<64, Fmt, T::BN>;
         static_assert(T64::BN == T::BN && T64::LDS <= T::LDS, "the 64-row body in the wider tile's launch");
         if (rows <= 64) {
             gemm_tile<T64, Fmt, EPI>(w, A, a_bytes, out_v, aux, m0, rows, n0, arow, lds);
+            return;
+        }
+    }
+    // likewise a 128-row tile holding at most 96 rows runs the 96 x BN body
+    if constexpr (BM_ > 96) {
+        using T96 = Tile<96, Fmt, T::BN>;
+        static_assert(T96::BN == T::BN && T96::LDS <= T::LDS, "the 96-row body in the wider tile's launch");
+        if (rows <= 96) {
+            gemm_tile<T96, Fmt, EPI>(w, A, a_bytes, out_v, aux, m0, rows, n0, arow, lds);
             return;
         }
     }

@@ -117,6 +117,9 @@ CASES = [
     # 65..96 rows: the 96 x 128 tile (RB = 3: three row blocks per wave)
     (O.Q4_K, 300, 1024, 80),
     (O.Q4_0, 256, 2048, 96),
+    # a last 128-row tile holding 72 / 22 rows: the 96 x 64 / 64 x 64 body
+    (O.Q4_K, 256, 1024, 200),
+    (O.Q4_0, 128, 512, 150),
 ]
 
 
@@ -186,6 +189,9 @@ GEN_CASES = [
     (O.Q5_0, 256, 1024, 100),
     (O.Q4_1, 192, 1088, 65),
     (O.F16, 100, 640, 17),
+    # a last 128-row tile holding 72 / 22 rows (the 96- / 64-row bodies)
+    (O.Q8_0, 320, 1024, 200),
+    (O.Q6_K, 256, 1024, 150),
     # K / 64 = 7 and 13 (= 1 mod 6): the pipeline's tail then holds DEPTH + 1
     # chunks, the last of which it must load itself
     (O.Q8_0, 128, 448, 40),
