@@ -282,6 +282,10 @@ GEN_MOE_CASES = [
     (6, 256, 512, 100, 2, O.Q4_K, O.Q6_K),   # Q4_K_M: Q4_K gate/up, Q6_K down (both kernels in one call)
     (3, 256, 768, 17, 1, O.Q5_0, O.Q4_1),
     (5, 256, 512, 300, 3, O.F16, O.Q8_0),    # experts past 128 rows: two tiles each
+    # 128-row tiles holding 65-96 rows and at most 64 (the 96- and 64-row
+    # bodies): Q8_0 / Q6_K experts at about 64 rows, Q4_K at about 100
+    (8, 256, 512, 256, 2, O.Q8_0, O.Q6_K),
+    (4, 256, 512, 200, 2, O.Q4_K, O.Q4_K),
     (4, 256, 512, 40, 2, O.BF16, O.F32),     # the bf16 forms
 ]
 
