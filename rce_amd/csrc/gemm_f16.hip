@@ -12,7 +12,8 @@
 // the configs[3] MoE's W2 then needs one round of tiles over the CUs, not
 // two).  The 64 x 128 tile moves a third less data into LDS per flop than
 // 128 x 64 (8 KB of activations + 4.5 KB of weights per chunk instead of
-// 16 + 2.25).
+// 16 + 2.25).  A block whose tile holds at most 64 (or 96) rows runs the
+// 64-row (96-row) body over the same columns (k_gemm_f16 below).
 // K runs in chunks of 64 (four MFMA k-steps of 16).  The block has ten waves:
 //   * eight compute waves: wave w = 2*kq + t computes k-step kq of every
 //     chunk for the BM x BN/2 sub-tile of columns BN/2 * t.. (RB x CB MFMA
