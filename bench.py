@@ -708,6 +708,12 @@ def main():
             per[key] = {"us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4)}
             kept[f"gemm {int(gdt)}"] = dict(gs, key=key)
             log(f"  {key}: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of f16 MFMA peak)")
+        # a short prompt: 64 tokens (one row tile; the 64-column tiles)
+        gms, _ = time_gemm(hip, ctx, G.Q4K, 4096, 4096, 64, max(20, args.steps // 4), 5, 310)
+        gtf = 2.0 * 64 * 4096 * 4096 / (gms * 1e-3) / 1e12
+        key = "Q4_K GEMM 64x4096x4096 f16_mfma"
+        per[key] = {"us": round(gms * 1e3, 2), "TFLOP/s": round(gtf, 1), "mfma_frac": round(gtf / MFMA_F16_PEAK_TFS, 4)}
+        log(f"  {key}: {gms * 1e3:.2f} us  {gtf:.0f} TFLOP/s ({gtf / MFMA_F16_PEAK_TFS:.1%} of f16 MFMA peak)")
     if "moe" in rows:  # configs[3]: grouped MoE, 8 Q4_0 experts, 256 tokens, top-2
         mms, mbytes, msample = time_moe(hip, ctx, 5, 2, 400, Mode.F16_MFMA)
         mtf = 120259084288 / (mms * 1e-3) / 1e12

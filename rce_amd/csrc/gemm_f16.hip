@@ -835,13 +835,13 @@ __device__ __forceinline__ void gemm_tile(const DevWeight &w, const _Float16 *__
 // Plain GEMM: tiles == nullptr, row tile mt covers rows mt*BM .. of M.
 // Grouped (MoE): row tile mt is tiles[mt] (expert e, first row r0, rows),
 // multiplied by wtab[e]; tiles at or past n_tiles[0] do nothing.
-template <class Fmt, int BM_, int EPI>
+template <class Fmt, int BM_, int EPI, int BN_ = 0>
 __global__ __launch_bounds__(NT) void k_gemm_f16(DevWeight w_arg, const _Float16 *__restrict__ A,
                                                  const int *__restrict__ gather, size_t M, uint32_t a_bytes,
                                                  void *__restrict__ out_v, const float *__restrict__ aux, int m_tiles,
                                                  const MoeTile *__restrict__ tiles, const int *__restrict__ n_tiles,
                                                  const DevWeight *__restrict__ wtab) {
-    using T = Tile<BM_, Fmt>;
+    using T = Tile<BM_, Fmt, BN_>;
     constexpr int BM = T::BM;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int arow[BM];
@@ -911,18 +911,18 @@ __global__ void k_f32_to_f16(const float *__restrict__ s, _Float16 *__restrict__
     if (i < n) d[i] = (_Float16)s[i];
 }
 
-template <class Fmt, int BM, int EPI>
+template <class Fmt, int BM, int EPI, int BN_ = 0>
 hipError_t set_lds_attr() {
-    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI>, Tile<BM, Fmt>::LDS);
+    return ensure_lds_limit((const void *)k_gemm_f16<Fmt, BM, EPI, BN_>, Tile<BM, Fmt, BN_>::LDS);
 }
 
-template <class Fmt, int BM>
+template <class Fmt, int BM, int BN_ = 0>
 hipError_t launch_fmt(const DevWeight &w, const _Float16 *a, size_t M, float *out, hipStream_t s) {
-    using T = Tile<BM, Fmt>;
+    using T = Tile<BM, Fmt, BN_>;
     const int m_tiles = (int)((M + T::BM - 1) / T::BM), n_tiles = (int)((w.n_rows + T::BN - 1) / T::BN);
-    hipError_t e = set_lds_attr<Fmt, BM, GEPI_F32>();
+    hipError_t e = set_lds_attr<Fmt, BM, GEPI_F32, BN_>();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM, GEPI_F32>), dim3(m_tiles * n_tiles), dim3(NT), T::LDS, s, w, a,
+    hipLaunchKernelGGL((k_gemm_f16<Fmt, BM, GEPI_F32, BN_>), dim3(m_tiles * n_tiles), dim3(NT), T::LDS, s, w, a,
                        (const int *)nullptr, M, (uint32_t)(M * w.n_cols * 2), (void *)out, (const float *)nullptr,
                        m_tiles, (const MoeTile *)nullptr, (const int *)nullptr, (const DevWeight *)nullptr);
     return hipGetLastError();
@@ -980,9 +980,13 @@ hipError_t gemm_prepare_lds() {
         if (e == hipSuccess) e = set_lds_attr<F, BM, GEPI_SWIGLU_F16>();
     };
     auto all_bm = [&](auto fmt) {
+        using F = decltype(fmt);
         all_epi(fmt, ic<64>{});
         all_epi(fmt, ic<96>{});
         all_epi(fmt, ic<128>{});
+        // the plain GEMM's 64-column forms of the 64- and 96-row tiles
+        if (e == hipSuccess) e = set_lds_attr<F, 64, GEPI_F32, 64>();
+        if (e == hipSuccess) e = set_lds_attr<F, 96, GEPI_F32, 64>();
     };
     all_bm(Q4K{});
     all_bm(Q5K{});
@@ -1067,11 +1071,18 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
     if (gemm_q8_supports(w.dtype, w.n_cols)) return w.dtype == T_Q8_0 ? launch_fmt<Q80, 128>(w, a, M, out, s)
                                                                       : launch_fmt<Q6K, 128>(w, a, M, out, s);
     if (bm == 0) bm = gemm_tile_rows(M, false);
+    // The 64- and 96-row tiles are 128 columns wide; where that leaves less
+    // than one tile per CU (short M: one row tile), 64-column tiles give
+    // twice the blocks.  Each output's sum is formed the same way in either
+    // (a wave's k-step partial over the chunks in order, the four partials
+    // added in order), so the bits do not depend on the choice.
+    const size_t m_tiles = (M + bm - 1) / bm, n128 = (w.n_rows + 127) / 128;
+    const bool narrow = bm < 128 && m_tiles * n128 < 256;
     hipError_t e = hipErrorInvalidValue;
     with_fmt(w.dtype, [&](auto fmt) {
         using F = decltype(fmt);
-        if (bm == 64) e = launch_fmt<F, 64>(w, a, M, out, s);
-        if (bm == 96) e = launch_fmt<F, 96>(w, a, M, out, s);
+        if (bm == 64) e = narrow ? launch_fmt<F, 64, 64>(w, a, M, out, s) : launch_fmt<F, 64>(w, a, M, out, s);
+        if (bm == 96) e = narrow ? launch_fmt<F, 96, 64>(w, a, M, out, s) : launch_fmt<F, 96>(w, a, M, out, s);
         if (bm == 128) e = launch_fmt<F, 128>(w, a, M, out, s);
     });
     return e;

@@ -380,3 +380,26 @@ def test_gemm_activations_past_4gib_sliced(ctx):
     assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
     assert normwise(want, O.mm_batched(x[rows].astype(F32), b, O.Q4_0, n, k)) < 2e-3
     w.close()
+
+
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q4_0, O.Q8_0])
+def test_gemm_rows_independent_of_tile_shape(ctx, dt):
+    """Each output's sum is formed the same way in every tile shape and body
+    (a wave's k-step partial over the chunks in order, the four partials
+    added in order), so a row's result does not depend on how many rows the
+    call has: M 40 and 64 (a 64-row tile, 64 columns wide), 80 (96 rows),
+    200 (128 rows, then a 72-row tile in the 96-row body) and 512 against
+    the same rows of one another, bit for bit."""
+    n, k = 512, 1024
+    note(f"gemm tile-shape independence dtype={dt}")
+    rng = np.random.default_rng(7500 + dt)
+    b = O.quantize((rng.standard_normal((n, k)) * 0.02).astype(F32), dt)
+    w = rce_amd.QuantWeight.from_owned_bytes(ctx, b, dt, n, k)
+    x = rng.standard_normal((512, k)).astype(F16)
+    full = run_gemm(ctx, w, x, G.F16)
+    for m in (40, 64, 80, 200):
+        got = run_gemm(ctx, w, np.ascontiguousarray(x[:m]), G.F16)
+        assert np.array_equal(got.view(np.uint32), full[:m].view(np.uint32)), f"M={m}"
+    tail = run_gemm(ctx, w, np.ascontiguousarray(x[440:]), G.F16)  # 72 rows
+    assert np.array_equal(tail.view(np.uint32), full[440:].view(np.uint32))
+    w.close()
