@@ -984,9 +984,8 @@ hipError_t gemm_prepare_lds() {
         all_epi(fmt, ic<64>{});
         all_epi(fmt, ic<96>{});
         all_epi(fmt, ic<128>{});
-        // the plain GEMM's 64-column forms of the 64- and 96-row tiles
+        // the plain GEMM's 64 x 64 tile (short M)
         if (e == hipSuccess) e = set_lds_attr<F, 64, GEPI_F32, 64>();
-        if (e == hipSuccess) e = set_lds_attr<F, 96, GEPI_F32, 64>();
     };
     all_bm(Q4K{});
     all_bm(Q5K{});
@@ -995,6 +994,8 @@ hipError_t gemm_prepare_lds() {
     all_bm(Q50{});
     all_epi(Q80{}, ic<128>{});
     all_epi(Q6K{}, ic<128>{});
+    if (e == hipSuccess) e = set_lds_attr<Q80, 64, GEPI_F32, 64>();
+    if (e == hipSuccess) e = set_lds_attr<Q6K, 64, GEPI_F32, 64>();
     return e;
 }
 
@@ -1067,23 +1068,37 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
     if (M == 0 || w.n_rows == 0) return hipSuccess;
     if (!gemm_shape_ok(M, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
-    // the 128 x 64 tile only
-    if (gemm_q8_supports(w.dtype, w.n_cols)) return w.dtype == T_Q8_0 ? launch_fmt<Q80, 128>(w, a, M, out, s)
-                                                                      : launch_fmt<Q6K, 128>(w, a, M, out, s);
-    if (bm == 0) bm = gemm_tile_rows(M, false);
-    // The 64- and 96-row tiles are 128 columns wide; where that leaves less
-    // than one tile per CU (short M: one row tile), 64-column tiles give
-    // twice the blocks.  Each output's sum is formed the same way in either
-    // (a wave's k-step partial over the chunks in order, the four partials
-    // added in order), so the bits do not depend on the choice.
-    const size_t m_tiles = (M + bm - 1) / bm, n128 = (w.n_rows + 127) / 128;
-    const bool narrow = bm < 128 && m_tiles * n128 < 256;
+    const size_t n64 = (w.n_rows + 63) / 64, m64 = (M + 63) / 64;
+    // Q8_0 / Q6_K: 64-column tiles only, 128 rows, or 64 where that makes
+    // more blocks in one round (below)
+    if (gemm_q8_supports(w.dtype, w.n_cols)) {
+        const bool q64 = bm == 0 && ((M + 127) / 128) * n64 < 256 && m64 * n64 <= 256;
+        if (w.dtype == T_Q8_0) return q64 ? launch_fmt<Q80, 64, 64>(w, a, M, out, s) : launch_fmt<Q80, 128>(w, a, M, out, s);
+        return q64 ? launch_fmt<Q6K, 64, 64>(w, a, M, out, s) : launch_fmt<Q6K, 128>(w, a, M, out, s);
+    }
+    bool sq64 = false;  // the 64 x 64 tile
+    if (bm == 0) {
+        bm = gemm_tile_rows(M, false);
+        // Where the default tile leaves less than one tile per CU (short M),
+        // 64 x 64 tiles, as long as they still take one round: more blocks,
+        // each with less of the work.  Each output's sum is formed the same
+        // way in every tile shape (a wave's k-step partial over the chunks in
+        // order, the four partials added in order), so the bits do not
+        // depend on the choice.
+        const size_t bn = bm == 128 ? 64 : 128;
+        sq64 = ((M + bm - 1) / bm) * ((w.n_rows + bn - 1) / bn) < 256 && m64 * n64 <= 256;
+    }
     hipError_t e = hipErrorInvalidValue;
     with_fmt(w.dtype, [&](auto fmt) {
         using F = decltype(fmt);
-        if (bm == 64) e = narrow ? launch_fmt<F, 64, 64>(w, a, M, out, s) : launch_fmt<F, 64>(w, a, M, out, s);
-        if (bm == 96) e = narrow ? launch_fmt<F, 96, 64>(w, a, M, out, s) : launch_fmt<F, 96>(w, a, M, out, s);
-        if (bm == 128) e = launch_fmt<F, 128>(w, a, M, out, s);
+        if (sq64)
+            e = launch_fmt<F, 64, 64>(w, a, M, out, s);
+        else if (bm == 64)
+            e = launch_fmt<F, 64>(w, a, M, out, s);
+        else if (bm == 96)
+            e = launch_fmt<F, 96>(w, a, M, out, s);
+        else if (bm == 128)
+            e = launch_fmt<F, 128>(w, a, M, out, s);
     });
     return e;
 }
