@@ -72,6 +72,7 @@
 #include "gemm_epilogue.h"
 #include "qmm_internal.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace rce_qmm {
@@ -1064,21 +1065,42 @@ hipError_t launch_gemm_f16_grouped(const DevWeight &w, const DevWeight *wtab, co
     return e;
 }
 
+// Compute units of the current device (0 if unknown), read once per device.
+static int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int c = cache[dev].load(std::memory_order_relaxed);
+    if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+        cache[dev].store(c, std::memory_order_relaxed);
+    return c > 0 ? c : 0;
+}
+
 hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, float *out, hipStream_t s, int bm) {
     if (M == 0 || w.n_rows == 0) return hipSuccess;
     if (!gemm_shape_ok(M, w)) return hipErrorInvalidValue;
     const _Float16 *a = static_cast<const _Float16 *>(a_f16);
-    const size_t n64 = (w.n_rows + 63) / 64, m64 = (M + 63) / 64;
+    const size_t n64 = (w.n_rows + 63) / 64, m64 = (M + 63) / 64, cus = cu_count() ? (size_t)cu_count() : 256;
     // Q8_0 / Q6_K: 64-column tiles only, 128 rows, or 64 where that makes
     // more blocks in one round (below)
     if (gemm_q8_supports(w.dtype, w.n_cols)) {
-        const bool q64 = bm == 0 && ((M + 127) / 128) * n64 < 256 && m64 * n64 <= 256;
+        const bool q64 = bm == 0 && ((M + 127) / 128) * n64 < cus && m64 * n64 <= cus;
         if (w.dtype == T_Q8_0) return q64 ? launch_fmt<Q80, 64, 64>(w, a, M, out, s) : launch_fmt<Q80, 128>(w, a, M, out, s);
         return q64 ? launch_fmt<Q6K, 64, 64>(w, a, M, out, s) : launch_fmt<Q6K, 128>(w, a, M, out, s);
     }
     bool sq64 = false;  // the 64 x 64 tile
     if (bm == 0) {
         bm = gemm_tile_rows(M, false);
+        // Past one row tile of 128, 96 x 128 tiles where they take fewer
+        // rounds over the CUs than 128 x 64 ones at less total tile work
+        // (tile work ~ rows x columns: a round of 96 x 128 tiles costs about
+        // 1.5 rounds of 128 x 64): M 640 and 768 at N 4096 are 320 and 384
+        // tiles of 128 x 64 (two rounds, the second part empty), 224 and 256
+        // of 96 x 128 (one).
+        if (bm == 128) {
+            const size_t t128 = ((M + 127) / 128) * ((w.n_rows + 63) / 64), t96 = ((M + 95) / 96) * ((w.n_rows + 127) / 128);
+            if (((t96 + cus - 1) / cus) * 3 < ((t128 + cus - 1) / cus) * 2) bm = 96;
+        }
         // Where the default tile leaves less than one tile per CU (short M),
         // 64 x 64 tiles, as long as they still take one round: more blocks,
         // each with less of the work.  Each output's sum is formed the same
@@ -1086,7 +1108,7 @@ hipError_t launch_gemm_f16(const DevWeight &w, const void *a_f16, size_t M, floa
         // order, the four partials added in order), so the bits do not
         // depend on the choice.
         const size_t bn = bm == 128 ? 64 : 128;
-        sq64 = ((M + bm - 1) / bm) * ((w.n_rows + bn - 1) / bn) < 256 && m64 * n64 <= 256;
+        sq64 = ((M + bm - 1) / bm) * ((w.n_rows + bn - 1) / bn) < cus && m64 * n64 <= cus;
     }
     hipError_t e = hipErrorInvalidValue;
     with_fmt(w.dtype, [&](auto fmt) {
