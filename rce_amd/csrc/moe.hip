@@ -209,14 +209,16 @@ __global__ void k_swiglu_slots(float *__restrict__ g, const float *__restrict__ 
 
 // moe_combine (rce-op-moe/src/lib.rs L98-110): out[t, :] = sum_j w[t, j] * y[slot(t, j), :],
 // j in decision order, from +0.0; a pair without a slot contributes nothing.
-// One block per token, four columns per thread (d a multiple of 4).
+// Block (t, c): token t, columns 1024 c .. 1024 c + 1023 (and every
+// gridDim.y-th such range after), four per thread (d a multiple of 4), so
+// a thread's loads of y are one float4 per decision, all in flight at once.
 __global__ __launch_bounds__(256) void k_moe_combine4(const float *__restrict__ y, const int *__restrict__ slot_of_pair,
                                                       const float *__restrict__ gate_w, int top_k, size_t d,
                                                       float *__restrict__ out) {
     const size_t t = blockIdx.x, d4 = d / 4;
     const float4 *y4 = reinterpret_cast<const float4 *>(y);
     float4 *o4 = reinterpret_cast<float4 *>(out) + t * d4;
-    for (size_t i = threadIdx.x; i < d4; i += 256) {
+    for (size_t i = (size_t)blockIdx.y * 256 + threadIdx.x; i < d4; i += (size_t)gridDim.y * 256) {
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int j = 0; j < top_k; j++) {
             const int s = slot_of_pair[t * top_k + j];
@@ -289,7 +291,9 @@ hipError_t launch_moe_combine(const float *y, const int *slot_of_pair, const flo
                               size_t d, float *out, hipStream_t s) {
     if (t_rows == 0) return hipSuccess;
     if (d % 4 == 0 && t_rows < 0x7fffffff) {
-        hipLaunchKernelGGL(k_moe_combine4, dim3((unsigned)t_rows), dim3(256), 0, s, y, slot_of_pair, gate_w, top_k, d, out);
+        const size_t cy = d >= 4 ? (d / 4 + 255) / 256 : 1;
+        hipLaunchKernelGGL(k_moe_combine4, dim3((unsigned)t_rows, (unsigned)(cy < 65535 ? cy : 65535)), dim3(256), 0, s, y,
+                           slot_of_pair, gate_w, top_k, d, out);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_moe_combine, dim3(grid_1d(t_rows * d, 256)), dim3(256), 0, s, y, slot_of_pair, gate_w, top_k,
