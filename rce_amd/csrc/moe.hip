@@ -290,7 +290,7 @@ hipError_t launch_swiglu_slots(float *g, const float *u, const int *n_slots_dev,
 hipError_t launch_moe_combine(const float *y, const int *slot_of_pair, const float *gate_w, size_t t_rows, int top_k,
                               size_t d, float *out, hipStream_t s) {
     if (t_rows == 0) return hipSuccess;
-    if (d % 4 == 0 && t_rows < 0x7fffffff) {
+    if (d % 4 == 0 && t_rows <= 0xFFFFFFFFu / 256) {  // grid.x * 256 threads within 32 bits
         const size_t cy = d >= 4 ? (d / 4 + 255) / 256 : 1;
         hipLaunchKernelGGL(k_moe_combine4, dim3((unsigned)t_rows, (unsigned)(cy < 65535 ? cy : 65535)), dim3(256), 0, s, y,
                            slot_of_pair, gate_w, top_k, d, out);
